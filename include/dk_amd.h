@@ -1,0 +1,126 @@
+/*
+ * dk_amd.h — C ABI of the MI355X (gfx950) batch-1 decode kernel library libdk_amd.so.
+ *
+ * Drop-in boundary for the six ops that the reference's pybind module `decode_kernels` exports
+ * (kernels/bindings.cpp:90-99) plus the INT4 format producer of runtime/quant.py. Every entry point:
+ *   - takes raw device pointers, integer sizes and a HIP stream handle (hipStream_t passed as void*; NULL = default
+ *     stream); no torch or C++ types cross the boundary;
+ *   - validates its arguments on the host before any HIP call, mirroring the TORCH_CHECKs of kernels/bindings.cpp,
+ *     and returns DK_OK (0) or a DK_ERR_* code; dk_last_error() then gives a thread-local message;
+ *   - allocates nothing, keeps no state between calls and launches only on `stream`, so calls are capturable into a
+ *     hipGraph (stream capture);
+ *   - reads device-resident `pos` (int32[1]) where the reference does, so one captured graph serves every step.
+ *
+ * Layouts (all row-major, contiguous, fp16 = IEEE binary16):
+ *   packed  int32 [N, K/8]     word j holds elements 8j..8j+7; element 8j+2i at bits [4i,4i+4), 8j+2i+1 at
+ *                              [16+4i, 20+4i)   (runtime/quant.py:9-12)
+ *   sz      fp16  [N, K/G, 2]  (scale, zero) per group, interleaved (runtime/quant.py:122-124)
+ *   kc, vc  fp16  [pages, n_kv, P, D]; token t of the sequence lives in page bt[t / P], slot t % P
+ *   o_part  fp32  [n_q, max_splits, D]; m_part, l_part fp32 [n_q, max_splits]
+ */
+#ifndef DK_AMD_H
+#define DK_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum dk_status {
+  DK_OK = 0,
+  DK_ERR_NULL = 1,    /* a required pointer is NULL                                   */
+  DK_ERR_ALIGN = 2,   /* a pointer that is read/written 16 bytes at a time is not 16 B aligned */
+  DK_ERR_SHAPE = 3,   /* sizes inconsistent or out of the supported range               */
+  DK_ERR_DOMAIN = 4,  /* a knob outside its domain (stage, R, version, group, page ...) */
+  DK_ERR_LAUNCH = 5   /* the HIP launch itself failed (message carries hipGetErrorString) */
+};
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* dk_last_error(void);
+
+/* hipRuntimeGetVersion() as seen by this library (lets a host check that it shares one HIP runtime). */
+int dk_runtime_version(void);
+
+/*
+ * W4A16 GEMV  y[N] = dequant(W)[N,K] . x[K]   (fp16 in/out, fp32 accumulation)
+ * Replaces gemv_w4a16 (kernels/bindings.cpp:27-38) -> gemv_w4a16_launch (kernels/gemv_w4a16.cu:248-267).
+ * stage 0: one wave per row, per-element dequant fp16((q-z)*s) then fp32 FMA (the reference's exact-dequant ladder
+ *          rung, kernels/gemv_w4a16.cu:16-36);
+ * stage 1..3: the streaming kernel: R rows per workgroup (R in {1,2,4,8}), `warps` = waves per workgroup splitting K
+ *          (1..16; 0 = one wave per 64 x 16-byte columns of a row), pf in {0,1} = software-prefetch the next column
+ *          step. stage 1 forces R = 1.
+ * Requires K % 32 == 0, group a power of two >= 32 with K % group == 0, packed and x 16-byte aligned.
+ */
+int dk_gemv_w4a16(int stage, int R, int warps, int pf, const void* packed, const void* sz, const void* x, void* y,
+                  int N, int K, int group, void* stream);
+
+/*
+ * Achievable-read-bandwidth microbenchmark: reads `bytes` (multiple of 16) from buf, XOR-folds them and writes sink
+ * (uint32[1]) only on a value it never takes. Replaces bw_read (kernels/bindings.cpp:40-43,
+ * kernels/gemv_w4a16.cu:133-153). unroll in {1, 4}; threads a multiple of 64 in [64, 1024]; blocks >= 1.
+ */
+int dk_bw_read(const void* buf, size_t bytes, void* sink, int blocks, int threads, int unroll, void* stream);
+
+/*
+ * Paged split-K GQA decode attention for one query token at ctx = *pos + 1 (device int32).
+ * Replaces paged_attention (kernels/bindings.cpp:45-62) -> paged_attention_launch (kernels/paged_attention.cu:429-461).
+ * Grid = n_kv x max_splits workgroups; split s covers tokens [s*part_size, (s+1)*part_size) of the live context;
+ * splits past ceil(ctx/part_size) exit; with one live split the output is written directly, otherwise each split
+ * writes unnormalized o and its (m, l) and a combine kernel merges them with the log-sum-exp rule.
+ * head_dim in {64, 128}; n_q / n_kv in {1, 2, 4, 8}; page a power of two; version in {1, 2, 3} (accepted for
+ * signature compatibility; every version runs the same kernel). Context is clamped to n_bt * page (tokens without a
+ * block-table entry do not exist); a block-table entry outside [0, n_pages) masks its tokens. softmax scale
+ * 1/sqrt(head_dim).
+ */
+int dk_paged_attention(int version, const void* q, const void* kc, const void* vc, const int32_t* bt,
+                       const int32_t* pos, int n_q, int n_kv, int head_dim, int page, int n_pages, int n_bt,
+                       int part_size, int max_splits, float* o_part, float* m_part, float* l_part, void* out,
+                       void* stream);
+
+/*
+ * Fused residual add + RMSNorm:  x <- x + delta (fp16 add, written back; skipped if delta == NULL);
+ * out = w * fp16(float(x) * rsqrt(mean(float(x)^2) + eps)).
+ * Replaces add_rmsnorm (kernels/bindings.cpp:64-72) -> add_rmsnorm_launch (kernels/fused_norm.cu:56-58).
+ * H % 8 == 0, 8 <= H <= 2^20; x, delta, w, out 16-byte aligned.
+ */
+int dk_add_rmsnorm(void* x, const void* delta, const void* w, void* out, int H, float eps, void* stream);
+
+/*
+ * Fused SwiGLU: out[i] = fp16(silu(float(gu[i]))) * gu[I + i] (fp16 product).
+ * Replaces swiglu (kernels/bindings.cpp:74-79) -> swiglu_launch (kernels/fused_swiglu.cu:23-26).
+ * I % 8 == 0; gu, out 16-byte aligned.
+ */
+int dk_swiglu(const void* gu, void* out, int I, void* stream);
+
+/*
+ * RoPE (rotate_half pairs (i, i + D/2), fp32 tables [max_pos, D/2]) on q and k of the fused qkv vector at position
+ * *pos (device int32); q rotated in place, k rotated and v copied into page bt[pos / page], slot pos % page.
+ * Replaces rope_append (kernels/bindings.cpp:81-88) -> rope_append_launch (kernels/rope_kv.cu:34-38).
+ * head_dim in {64, 128}; page a power of two. If *pos >= max_pos nothing is touched; if pos / page >= n_bt or the
+ * block-table entry is outside [0, n_pages) q is still rotated but nothing is written to the caches.
+ */
+int dk_rope_append(void* qkv, const float* cos_t, const float* sin_t, const int32_t* pos, const int32_t* bt,
+                   void* kc, void* vc, int n_q, int n_kv, int head_dim, int page, int max_pos, int n_pages,
+                   int n_bt, void* stream);
+
+/*
+ * Greedy token pick closing a decode step: *tok = argmax(logits[0..V)) (int64; lowest index among equal maxima, NaN
+ * ranks highest as in torch.argmax), then *pos += 1 if pos != NULL. Replaces the two torch ops
+ * `torch.argmax(self.logits, out=self.tok)` and `self.pos += 1` of runtime/model.py:232-233 with one launch.
+ */
+int dk_argmax_advance(const void* logits, int V, int64_t* tok, int32_t* pos, void* stream);
+
+/*
+ * INT4 format producer on the GPU: round-to-nearest asymmetric group quantization of fp16 W [N, K] and packing,
+ * bit-identical to runtime/quant.py quantize (:42-48, RTN branch of group_params :20-28) + pack (:100-109) +
+ * pack_scale_zero (:122-124). Writes packed int32 [N, K/8] and sz fp16 [N, K/G, 2].
+ * group a power of two in [32, 512] with K % group == 0.
+ */
+int dk_quantize_w4(const void* w, void* packed, void* sz, int N, int K, int group, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DK_AMD_H */

@@ -1,0 +1,177 @@
+// C ABI of libdk_amd.so (declared in include/dk_amd.h): host-side validation, then one launch on the caller's stream.
+// The checks mirror the TORCH_CHECKs of the reference binding layer (kernels/bindings.cpp:18-88) so a bad argument
+// is reported as an error code and a message instead of a fault inside a captured graph.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "dk_amd.h"
+#include "launch.hpp"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+bool pow2(long long v) { return v > 0 && (v & (v - 1)) == 0; }
+int ilog2(long long v) {
+  int r = 0;
+  while ((1LL << r) < v) ++r;
+  return r;
+}
+
+// Clear a stale error before launching so that the check after the launch reports this launch only.
+void clear_error() { (void)hipGetLastError(); }
+
+int launched(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(DK_ERR_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+  g_err[0] = '\0';
+  return DK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* dk_last_error(void) { return g_err; }
+
+int dk_runtime_version(void) {
+  int v = 0;
+  if (hipRuntimeGetVersion(&v) != hipSuccess) return -1;
+  return v;
+}
+
+int dk_gemv_w4a16(int stage, int R, int warps, int pf, const void* packed, const void* sz, const void* x, void* y,
+                  int N, int K, int group, void* stream) {
+  if (!packed || !sz || !x || !y) return fail(DK_ERR_NULL, "gemv_w4a16: null pointer argument");
+  if (stage < 0 || stage > 3) return fail(DK_ERR_DOMAIN, "gemv_w4a16: stage must be 0..3, got %d", stage);
+  if (R != 1 && R != 2 && R != 4 && R != 8) return fail(DK_ERR_DOMAIN, "gemv: R must be 1,2,4,8, got %d", R);
+  if (warps < 0 || warps > 16) return fail(DK_ERR_DOMAIN, "gemv_w4a16: warps must be 0..16, got %d", warps);
+  if (pf != 0 && pf != 1) return fail(DK_ERR_DOMAIN, "gemv_w4a16: pf must be 0 or 1, got %d", pf);
+  if (N <= 0 || K <= 0) return fail(DK_ERR_SHAPE, "gemv_w4a16: N and K must be positive (N=%d K=%d)", N, K);
+  if (K % 32 != 0 || K % group != 0)
+    return fail(DK_ERR_SHAPE, "K must be a multiple of 32 and of the group size (K=%d group=%d)", K, group);
+  if (group < 32) return fail(DK_ERR_DOMAIN, "group must be >= 32 (one uint4 never straddles a group), got %d", group);
+  if (!pow2(group)) return fail(DK_ERR_DOMAIN, "group must be a power of two, got %d", group);
+  if (!aligned16(packed)) return fail(DK_ERR_ALIGN, "packed must be 16B aligned");
+  if (!aligned16(x)) return fail(DK_ERR_ALIGN, "x must be 16B aligned");
+  if (!aligned4(sz)) return fail(DK_ERR_ALIGN, "sz must be 4B aligned");
+  if (stage == 1) R = 1;
+  clear_error();
+  dk::launch_gemv_w4a16(stage, R, warps, pf, packed, sz, x, y, N, K, ilog2(group), (hipStream_t)stream);
+  return launched("gemv_w4a16");
+}
+
+int dk_bw_read(const void* buf, size_t bytes, void* sink, int blocks, int threads, int unroll, void* stream) {
+  if (!buf || !sink) return fail(DK_ERR_NULL, "bw_read: null pointer argument");
+  if (!aligned16(buf)) return fail(DK_ERR_ALIGN, "buf must be 16B aligned");
+  if (blocks < 1 || blocks > (1 << 30)) return fail(DK_ERR_SHAPE, "bw_read: blocks must be >= 1, got %d", blocks);
+  if (threads < 1 || threads > 1024) return fail(DK_ERR_SHAPE, "bw_read: threads must be 1..1024, got %d", threads);
+  if (unroll != 1 && unroll != 4) return fail(DK_ERR_DOMAIN, "bw_read: unroll must be 1 or 4, got %d", unroll);
+  clear_error();
+  dk::launch_bw_read(buf, bytes, sink, blocks, threads, unroll, (hipStream_t)stream);
+  return launched("bw_read");
+}
+
+int dk_paged_attention(int version, const void* q, const void* kc, const void* vc, const int32_t* bt,
+                       const int32_t* pos, int n_q, int n_kv, int head_dim, int page, int n_pages, int n_bt,
+                       int part_size, int max_splits, float* o_part, float* m_part, float* l_part, void* out,
+                       void* stream) {
+  if (!q || !kc || !vc || !bt || !pos || !out || !o_part || !m_part || !l_part)
+    return fail(DK_ERR_NULL, "paged_attention: null pointer argument");
+  if (head_dim != 64 && head_dim != 128)
+    return fail(DK_ERR_SHAPE, "paged_attention: head_dim must be 64 or 128, got %d", head_dim);
+  if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0)
+    return fail(DK_ERR_SHAPE, "heads-per-group must be 1/2/4/8 (n_q=%d n_kv=%d)", n_q, n_kv);
+  const int hpg = n_q / n_kv;
+  if (hpg != 1 && hpg != 2 && hpg != 4 && hpg != 8)
+    return fail(DK_ERR_SHAPE, "heads-per-group must be 1/2/4/8, got %d", hpg);
+  if (!pow2(page)) return fail(DK_ERR_DOMAIN, "page size must be a power of two, got %d", page);
+  if (part_size <= 0) return fail(DK_ERR_DOMAIN, "part_size must be > 0");
+  if (version < 1 || version > 3) return fail(DK_ERR_DOMAIN, "attention version must be 1, 2 or 3");
+  if (max_splits < 1 || max_splits > 65535)
+    return fail(DK_ERR_SHAPE, "paged_attention: max_splits must be 1..65535, got %d", max_splits);
+  if (n_pages < 1 || n_bt < 1) return fail(DK_ERR_SHAPE, "paged_attention: empty cache or block table");
+  if (n_kv > 65535 || n_q > 65535) return fail(DK_ERR_SHAPE, "paged_attention: too many heads");
+  if (!aligned16(q) || !aligned16(kc) || !aligned16(vc))
+    return fail(DK_ERR_ALIGN, "q, kc and vc must be 16B aligned");
+  clear_error();
+  dk::launch_paged_attention(q, kc, vc, bt, pos, n_q, n_kv, head_dim, ilog2(page), n_pages, n_bt, part_size,
+                             max_splits, o_part, m_part, l_part, out, (hipStream_t)stream);
+  return launched("paged_attention");
+}
+
+int dk_add_rmsnorm(void* x, const void* delta, const void* w, void* out, int H, float eps, void* stream) {
+  if (!x || !w || !out) return fail(DK_ERR_NULL, "add_rmsnorm: null pointer argument");
+  if (H <= 0 || H % 8 != 0 || H > (1 << 20))
+    return fail(DK_ERR_SHAPE, "add_rmsnorm: H must be a positive multiple of 8 (<= 2^20), got %d", H);
+  if (!aligned16(x)) return fail(DK_ERR_ALIGN, "x must be 16B aligned");
+  if (!aligned16(w)) return fail(DK_ERR_ALIGN, "w must be 16B aligned");
+  if (!aligned16(out)) return fail(DK_ERR_ALIGN, "out must be 16B aligned");
+  if (delta && !aligned16(delta)) return fail(DK_ERR_ALIGN, "delta must be 16B aligned");
+  clear_error();
+  dk::launch_add_rmsnorm(x, delta, w, out, H, eps, (hipStream_t)stream);
+  return launched("add_rmsnorm");
+}
+
+int dk_swiglu(const void* gu, void* out, int I, void* stream) {
+  if (!gu || !out) return fail(DK_ERR_NULL, "swiglu: null pointer argument");
+  if (I <= 0 || I % 8 != 0) return fail(DK_ERR_SHAPE, "swiglu: I must be a positive multiple of 8, got %d", I);
+  if (!aligned16(gu)) return fail(DK_ERR_ALIGN, "gu must be 16B aligned");
+  if (!aligned16(out)) return fail(DK_ERR_ALIGN, "out must be 16B aligned");
+  clear_error();
+  dk::launch_swiglu(gu, out, I, (hipStream_t)stream);
+  return launched("swiglu");
+}
+
+int dk_rope_append(void* qkv, const float* cos_t, const float* sin_t, const int32_t* pos, const int32_t* bt,
+                   void* kc, void* vc, int n_q, int n_kv, int head_dim, int page, int max_pos, int n_pages,
+                   int n_bt, void* stream) {
+  if (!qkv || !cos_t || !sin_t || !pos || !bt || !kc || !vc)
+    return fail(DK_ERR_NULL, "rope_append: null pointer argument");
+  if (head_dim != 64 && head_dim != 128)
+    return fail(DK_ERR_SHAPE, "rope_append: head_dim must be 64 or 128, got %d", head_dim);
+  if (n_q <= 0 || n_kv <= 0 || n_q > 65535 || n_kv > 65535)
+    return fail(DK_ERR_SHAPE, "rope_append: bad head counts (n_q=%d n_kv=%d)", n_q, n_kv);
+  if (!pow2(page)) return fail(DK_ERR_DOMAIN, "page size must be a power of two, got %d", page);
+  if (max_pos < 1 || n_pages < 1 || n_bt < 1)
+    return fail(DK_ERR_SHAPE, "rope_append: empty rope table, cache or block table");
+  clear_error();
+  dk::launch_rope_append(qkv, cos_t, sin_t, pos, bt, kc, vc, n_q, n_kv, head_dim, ilog2(page), max_pos, n_pages,
+                         n_bt, (hipStream_t)stream);
+  return launched("rope_append");
+}
+
+int dk_argmax_advance(const void* logits, int V, int64_t* tok, int32_t* pos, void* stream) {
+  if (!logits || !tok) return fail(DK_ERR_NULL, "argmax_advance: null pointer argument");
+  if (V <= 0) return fail(DK_ERR_SHAPE, "argmax_advance: V must be positive, got %d", V);
+  if (!aligned4(tok) || (pos && !aligned4(pos))) return fail(DK_ERR_ALIGN, "tok and pos must be 4B aligned");
+  clear_error();
+  dk::launch_argmax_advance(logits, V, tok, pos, (hipStream_t)stream);
+  return launched("argmax_advance");
+}
+
+int dk_quantize_w4(const void* w, void* packed, void* sz, int N, int K, int group, void* stream) {
+  if (!w || !packed || !sz) return fail(DK_ERR_NULL, "quantize_w4: null pointer argument");
+  if (N <= 0 || K <= 0) return fail(DK_ERR_SHAPE, "quantize_w4: N and K must be positive");
+  if (!pow2(group) || group < 32 || group > 512)
+    return fail(DK_ERR_DOMAIN, "quantize_w4: group must be a power of two in [32, 512], got %d", group);
+  if (K % group != 0) return fail(DK_ERR_SHAPE, "quantize_w4: K=%d is not a multiple of group=%d", K, group);
+  if ((long long)N * (K / 8) > (1LL << 40)) return fail(DK_ERR_SHAPE, "quantize_w4: matrix too large");
+  if (!aligned16(w)) return fail(DK_ERR_ALIGN, "w must be 16B aligned");
+  if (!aligned4(packed) || !aligned4(sz)) return fail(DK_ERR_ALIGN, "packed and sz must be 4B aligned");
+  clear_error();
+  dk::launch_quantize_w4(w, packed, sz, N, K, ilog2(group), (hipStream_t)stream);
+  return launched("quantize_w4");
+}
+
+}  // extern "C"

@@ -1,0 +1,205 @@
+// Single-pass bandwidth kernels of the decode step on gfx950: fused residual + RMSNorm, fused SwiGLU, RoPE + paged
+// KV append. Each rounds to fp16 at exactly the points the reference's fp16 semantics do (reference/ref_ops.py).
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace dk {
+namespace {
+
+// ---------------------------------------------------------------------------------------------------------------
+// x <- x + delta (fp16 add, one rounding, written back; skipped when delta is null);
+// out = w * fp16(float(x) * r), r = 1 / sqrt(sum(float(x)^2) / H + eps)   (reference/ref_ops.py:15-20).
+// One workgroup; each thread owns 8-element (16 B) chunks. The residual is bit-exact; the product float(x) * r is
+// rounded to fp16 before the fp16 multiply by w, as the reference does.
+__global__ void __launch_bounds__(1024)
+add_rmsnorm_kernel(f16* __restrict__ x, const f16* __restrict__ delta, const f16* __restrict__ w,
+                   f16* __restrict__ out, int H, float eps) {
+  __shared__ float wsum[16];
+  const int tid = threadIdx.x, nt = blockDim.x;
+  float ss = 0.f;
+  for (int i = tid * 8; i < H; i += nt * 8) {
+    u32x4 xv = *reinterpret_cast<const u32x4*>(x + i);
+    if (delta != nullptr) {
+      const u32x4 dv = *reinterpret_cast<const u32x4*>(delta + i);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) xv[k] = as_u32(as_f16x2(xv[k]) + as_f16x2(dv[k]));
+      *reinterpret_cast<u32x4*>(x + i) = xv;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const f16x2 h = as_f16x2(xv[k]);
+      const float a = (float)h.x, b = (float)h.y;
+      ss = fmaf(a, a, ss);
+      ss = fmaf(b, b, ss);
+    }
+  }
+  ss = group_sum<kWave>(ss);
+  if ((tid & 63) == 0) wsum[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+  const int nw = nt >> 6;
+  for (int i = 0; i < nw; ++i) tot += wsum[i];
+  const float r = 1.0f / sqrtf(tot / (float)H + eps);
+  for (int i = tid * 8; i < H; i += nt * 8) {
+    const u32x4 xv = *reinterpret_cast<const u32x4*>(x + i);  // this thread's own write above
+    const u32x4 wv = *reinterpret_cast<const u32x4*>(w + i);
+    u32x4 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const f16x2 h = as_f16x2(xv[k]);
+      const f16x2 hn = {(f16)((float)h.x * r), (f16)((float)h.y * r)};
+      o[k] = as_u32(as_f16x2(wv[k]) * hn);
+    }
+    *reinterpret_cast<u32x4*>(out + i) = o;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// out[i] = fp16(silu(float(gate[i]))) * up[i] in fp16, gate = gu[0:I], up = gu[I:2I]   (reference/ref_ops.py:23-27).
+__global__ void __launch_bounds__(256)
+swiglu_kernel(const f16* __restrict__ gu, f16* __restrict__ out, int I) {
+  const int i = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (i >= I) return;
+  const u32x4 gv = *reinterpret_cast<const u32x4*>(gu + i);
+  const u32x4 uv = *reinterpret_cast<const u32x4*>(gu + I + i);
+  u32x4 o;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const f16x2 g2 = as_f16x2(gv[k]);
+    const float a = (float)g2.x, b = (float)g2.y;
+    const f16x2 s = {(f16)(a / (1.0f + expf(-a))), (f16)(b / (1.0f + expf(-b)))};
+    o[k] = as_u32(s * as_f16x2(uv[k]));
+  }
+  *reinterpret_cast<u32x4*>(out + i) = o;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// RoPE, rotate_half pairs (i, i + D/2), at position *pos, then paged K/V append   (reference/ref_ops.py:36-53).
+// One thread per (head, pair): q heads rotate in place, k heads rotate into the cache, v heads copy into the cache.
+// fp32 products are rounded separately (no contraction), exactly as the reference's elementwise fp32 ops, so the
+// rotated values are bit-identical to the reference's.
+template <int D>
+__global__ void __launch_bounds__(256)
+rope_append_kernel(f16* __restrict__ qkv, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                   const int32_t* __restrict__ pos_ptr, const int32_t* __restrict__ bt, f16* __restrict__ kc,
+                   f16* __restrict__ vc, int n_q, int n_kv, int log2P, int max_pos, int n_pages, int n_bt) {
+#pragma clang fp contract(off)
+  constexpr int HALF = D / 2;
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  const int head = idx / HALF, i = idx % HALF;
+  if (head >= n_q + 2 * n_kv) return;
+  const int pos = *pos_ptr;
+  if (pos < 0 || pos >= max_pos) return;
+  const int lp = pos >> log2P;
+  int page = -1;
+  if (lp < n_bt) {
+    page = bt[lp];
+    if (page < 0 || page >= n_pages) page = -1;
+  }
+  const int slot = pos & ((1 << log2P) - 1);
+  f16* xh = qkv + (size_t)head * D;
+  if (head < n_q + n_kv) {
+    const float c = cos_t[(size_t)pos * HALF + i], s = sin_t[(size_t)pos * HALF + i];
+    const float a = (float)xh[i], b = (float)xh[i + HALF];
+    const float ac = a * c, bs = b * s, bc = b * c, as = a * s;
+    const f16 lo = (f16)(ac - bs), hi = (f16)(bc + as);
+    if (head < n_q) {
+      xh[i] = lo;
+      xh[i + HALF] = hi;
+    } else if (page >= 0) {
+      f16* dst = kc + ((((size_t)page * n_kv + (head - n_q)) << log2P) + slot) * D;
+      dst[i] = lo;
+      dst[i + HALF] = hi;
+    }
+  } else if (page >= 0) {
+    f16* dst = vc + ((((size_t)page * n_kv + (head - n_q - n_kv)) << log2P) + slot) * D;
+    dst[i] = xh[i];
+    dst[i + HALF] = xh[i + HALF];
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Greedy token pick closing the decode step: tok = argmax(logits) (lowest index among equal maxima, NaN counts as
+// largest like torch.argmax), then *pos += 1 when pos is given (runtime/model.py:232-233 of the reference as one
+// launch). One workgroup of 1024 threads.
+__device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
+  const bool na = a != a, nb = b != b;
+  if (na != nb) return na;
+  if (!na && a != b) return a > b;
+  return ia < ib;
+}
+
+__global__ void __launch_bounds__(1024)
+argmax_advance_kernel(const f16* __restrict__ logits, int V, int64_t* __restrict__ tok, int32_t* __restrict__ pos) {
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  const int tid = threadIdx.x, nt = blockDim.x;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = tid; i < V; i += nt) {
+    const float v = (float)logits[i];
+    if (better(v, i, bv, bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, kWave);
+    const int oi = __shfl_xor(bi, o, kWave);
+    if (better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if ((tid & 63) == 0) {
+    sv[tid >> 6] = bv;
+    si[tid >> 6] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < (nt >> 6); ++w)
+      if (better(sv[w], si[w], bv, bi)) {
+        bv = sv[w];
+        bi = si[w];
+      }
+    tok[0] = (int64_t)bi;
+    if (pos != nullptr) pos[0] += 1;
+  }
+}
+
+}  // namespace
+
+void launch_add_rmsnorm(void* x, const void* delta, const void* w, void* out, int H, float eps, hipStream_t st) {
+  int threads = ((H / 8 + 63) / 64) * 64;
+  if (threads > 1024) threads = 1024;
+  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(1), dim3(threads), 0, st, (f16*)x, (const f16*)delta, (const f16*)w,
+                     (f16*)out, H, eps);
+}
+
+void launch_swiglu(const void* gu, void* out, int I, hipStream_t st) {
+  const int n = I / 8;
+  const int threads = 256;
+  hipLaunchKernelGGL(swiglu_kernel, dim3((n + threads - 1) / threads), dim3(threads), 0, st, (const f16*)gu,
+                     (f16*)out, I);
+}
+
+void launch_rope_append(void* qkv, const float* cos_t, const float* sin_t, const int32_t* pos, const int32_t* bt,
+                        void* kc, void* vc, int n_q, int n_kv, int head_dim, int log2P, int max_pos, int n_pages,
+                        int n_bt, hipStream_t st) {
+  const int pairs = (n_q + 2 * n_kv) * (head_dim / 2);
+  const int threads = 256;
+  const dim3 grid((pairs + threads - 1) / threads);
+  if (head_dim == 64)
+    hipLaunchKernelGGL((rope_append_kernel<64>), grid, dim3(threads), 0, st, (f16*)qkv, cos_t, sin_t, pos, bt,
+                       (f16*)kc, (f16*)vc, n_q, n_kv, log2P, max_pos, n_pages, n_bt);
+  else
+    hipLaunchKernelGGL((rope_append_kernel<128>), grid, dim3(threads), 0, st, (f16*)qkv, cos_t, sin_t, pos, bt,
+                       (f16*)kc, (f16*)vc, n_q, n_kv, log2P, max_pos, n_pages, n_bt);
+}
+
+void launch_argmax_advance(const void* logits, int V, int64_t* tok, int32_t* pos, hipStream_t st) {
+  hipLaunchKernelGGL(argmax_advance_kernel, dim3(1), dim3(1024), 0, st, (const f16*)logits, V, tok, pos);
+}
+
+}  // namespace dk

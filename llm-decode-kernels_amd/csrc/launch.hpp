@@ -1,0 +1,32 @@
+// Internal launchers (host side). Arguments are validated by the C ABI layer (dk_api.hip) before these run.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace dk {
+
+// W4A16 GEMV. stage 0: exact per-element dequant, `waves` rows per workgroup. stage >= 1: streaming kernel with
+// R rows per workgroup, `waves` waves splitting K, `pf` software prefetch.
+void launch_gemv_w4a16(int stage, int R, int waves, int pf, const void* packed, const void* sz, const void* x,
+                       void* y, int N, int K, int log2G, hipStream_t st);
+// Default streaming configuration for a shape: (R, waves, pf).
+void gemv_default_config(int N, int K, int* R, int* waves, int* pf);
+
+void launch_bw_read(const void* buf, size_t bytes, void* sink, int blocks, int threads, int unroll, hipStream_t st);
+
+void launch_paged_attention(const void* q, const void* kc, const void* vc, const int32_t* bt, const int32_t* pos,
+                            int n_q, int n_kv, int head_dim, int log2P, int n_pages, int n_bt, int part_size,
+                            int max_splits, float* o_part, float* m_part, float* l_part, void* out, hipStream_t st);
+
+void launch_add_rmsnorm(void* x, const void* delta, const void* w, void* out, int H, float eps, hipStream_t st);
+void launch_swiglu(const void* gu, void* out, int I, hipStream_t st);
+void launch_rope_append(void* qkv, const float* cos_t, const float* sin_t, const int32_t* pos, const int32_t* bt,
+                        void* kc, void* vc, int n_q, int n_kv, int head_dim, int log2P, int max_pos, int n_pages,
+                        int n_bt, hipStream_t st);
+
+void launch_argmax_advance(const void* logits, int V, int64_t* tok, int32_t* pos, hipStream_t st);
+
+void launch_quantize_w4(const void* w, void* packed, void* sz, int N, int K, int log2G, hipStream_t st);
+
+}  // namespace dk

@@ -1,0 +1,215 @@
+"""Loader of the MI355X decode-kernel library and the torch-facing op module.
+
+Drop-in for the reference's ``runtime/ext.py`` (:9-20): ``load()`` returns an object with the six ops of the pybind
+module ``decode_kernels`` (kernels/bindings.cpp:90-99) — same names, argument order, in-place/out-param conventions
+and error behaviour (``RuntimeError`` for every TORCH_CHECK of kernels/bindings.cpp:18-88). Instead of a JIT nvcc
+build it loads ``libdk_amd.so``, a hipcc-built C-ABI library (include/dk_amd.h), through ctypes; every op launches on
+torch's current HIP stream, so the ops are capturable with ``torch.cuda.graph`` (a hipGraph on ROCm).
+
+There is no CPU path: without the built library ``load()`` raises.
+"""
+import ctypes
+import pathlib
+
+import torch
+
+PKG_DIR = pathlib.Path(__file__).resolve().parents[1]
+LIB_PATH = PKG_DIR / "libdk_amd.so"
+HEADER = PKG_DIR.parent / "include" / "dk_amd.h"
+
+# Every exported entry point, with its ctypes signature (kept in the order of include/dk_amd.h).
+_P, _I, _F, _Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+SIGNATURES = {
+    "dk_last_error": ([], ctypes.c_char_p),
+    "dk_runtime_version": ([], _I),
+    "dk_gemv_w4a16": ([_I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P], _I),
+    "dk_bw_read": ([_P, _Z, _P, _I, _I, _I, _P], _I),
+    "dk_paged_attention": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
+    "dk_add_rmsnorm": ([_P, _P, _P, _P, _I, _F, _P], _I),
+    "dk_swiglu": ([_P, _P, _I, _P], _I),
+    "dk_rope_append": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
+    "dk_argmax_advance": ([_P, _I, _P, _P, _P], _I),
+    "dk_quantize_w4": ([_P, _P, _P, _I, _I, _I, _P], _I),
+}
+
+_EXT = None
+
+
+def open_library(path=LIB_PATH):
+    """dlopen the library and bind every entry point (no GPU needed). torch is imported first so the library resolves
+    libamdhip64 to the HIP runtime torch already loaded (one runtime per process)."""
+    if not pathlib.Path(path).exists():
+        raise RuntimeError(f"{path} is not built: run `make -C llm-decode-kernels_amd/csrc` "
+                           "(or __graft_entry__.build()); there is no CPU fallback")
+    lib = ctypes.CDLL(str(path))
+    for name, (argtypes, restype) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = restype
+    return lib
+
+
+def _check_cuda(t, name):
+    if not (t.is_cuda and t.is_contiguous()):
+        raise RuntimeError(f"{name} must be a contiguous CUDA tensor")
+
+
+def _check_dtype(t, dtype, name):
+    if t.dtype != dtype:
+        raise RuntimeError(f"{name} must be {dtype}, got {t.dtype}")
+
+
+def _stream(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+class DecodeKernels:
+    """The op module. Every method validates like the reference binding, then calls one C entry point."""
+
+    def __init__(self, lib):
+        self.lib = lib
+
+    def _call(self, fn, *args):
+        rc = fn(*args)
+        if rc != 0:
+            raise RuntimeError(self.lib.dk_last_error().decode() or f"decode kernel error {rc}")
+
+    # kernels/bindings.cpp:27-38
+    def gemv_w4a16(self, stage, R, warps, pf, packed, sz, x, y, group):
+        for t, n in ((packed, "packed"), (sz, "sz"), (x, "x"), (y, "y")):
+            _check_cuda(t, n)
+        N, K = packed.size(0), packed.size(1) * 8
+        if K % 32 != 0 or K % group != 0:
+            raise RuntimeError("K must be a multiple of 32 and of the group size")
+        if group < 32:
+            raise RuntimeError("group must be >= 32 (one uint4 never straddles a group)")
+        if not (x.numel() == K and y.numel() == N and sz.size(0) == N and sz.size(1) == K // group):
+            raise RuntimeError("gemv_w4a16: shape mismatch between packed, sz, x and y")
+        _check_dtype(packed, torch.int32, "packed")
+        for t, n in ((x, "x"), (y, "y"), (sz, "sz")):
+            _check_dtype(t, torch.float16, n)
+        self._call(self.lib.dk_gemv_w4a16, int(stage), int(R), int(warps), int(pf), packed.data_ptr(), sz.data_ptr(),
+                   x.data_ptr(), y.data_ptr(), N, K, int(group), _stream(x))
+
+    # kernels/bindings.cpp:40-43
+    def bw_read(self, buf, sink, blocks, threads, unroll):
+        _check_cuda(buf, "buf")
+        self._call(self.lib.dk_bw_read, buf.data_ptr(), buf.numel() * buf.element_size(), sink.data_ptr(),
+                   int(blocks), int(threads), int(unroll), _stream(buf))
+
+    # kernels/bindings.cpp:45-62 (head_dim generalised from 64 to {64, 128})
+    def paged_attention(self, q, kc, vc, bt, pos, part_size, o_part, m_part, l_part, out, version=2):
+        for t, n in ((q, "q"), (kc, "kc"), (vc, "vc"), (bt, "bt"), (pos, "pos"), (out, "out"),
+                     (o_part, "o_part"), (m_part, "m_part"), (l_part, "l_part")):
+            _check_cuda(t, n)
+        if kc.dim() != 4 or kc.size(3) not in (64, 128) or vc.shape != kc.shape:
+            raise RuntimeError("cache must be [pages, n_kv, P, 64|128]")
+        if bt.dtype != torch.int32 or pos.dtype != torch.int32:
+            raise RuntimeError("bt and pos must be int32")
+        for t, n in ((q, "q"), (kc, "kc"), (vc, "vc"), (out, "out")):
+            _check_dtype(t, torch.float16, n)
+        for t, n in ((o_part, "o_part"), (m_part, "m_part"), (l_part, "l_part")):
+            _check_dtype(t, torch.float32, n)
+        D = kc.size(3)
+        n_q, n_kv, P = q.numel() // D, kc.size(1), kc.size(2)
+        if n_q * D != q.numel() or n_q % n_kv != 0 or (n_q // n_kv) not in (1, 2, 4, 8):
+            raise RuntimeError("heads-per-group must be 1/2/4/8")
+        if part_size <= 0:
+            raise RuntimeError("part_size must be > 0")
+        if not 1 <= version <= 3:
+            raise RuntimeError("attention version must be 1, 2 or 3")
+        max_splits = o_part.size(1)
+        if not (o_part.size(0) == n_q and o_part.size(2) == D and m_part.size(0) == n_q and l_part.size(0) == n_q
+                and m_part.size(1) == max_splits and l_part.size(1) == max_splits and out.numel() == n_q * D):
+            raise RuntimeError("paged_attention: split buffers must be o [n_q, S, D], m/l [n_q, S], out [n_q, D]")
+        self._call(self.lib.dk_paged_attention, int(version), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                   bt.data_ptr(), pos.data_ptr(), n_q, n_kv, D, P, kc.size(0), bt.numel(), int(part_size),
+                   max_splits, o_part.data_ptr(), m_part.data_ptr(), l_part.data_ptr(), out.data_ptr(), _stream(q))
+
+    # kernels/bindings.cpp:64-72
+    def add_rmsnorm(self, x, delta, w, out, eps):
+        _check_cuda(x, "x")
+        _check_cuda(w, "w")
+        _check_cuda(out, "out")
+        if x.numel() % 8 != 0:
+            raise RuntimeError("add_rmsnorm: numel must be a multiple of 8")
+        if w.numel() != x.numel() or out.numel() != x.numel():
+            raise RuntimeError("add_rmsnorm: x, w and out must have the same size")
+        for t, n in ((x, "x"), (w, "w"), (out, "out")):
+            _check_dtype(t, torch.float16, n)
+        d = None
+        if delta is not None:
+            _check_cuda(delta, "delta")
+            _check_dtype(delta, torch.float16, "delta")
+            if delta.numel() != x.numel():
+                raise RuntimeError("add_rmsnorm: delta must have the size of x")
+            d = delta.data_ptr()
+        self._call(self.lib.dk_add_rmsnorm, x.data_ptr(), d, w.data_ptr(), out.data_ptr(), x.numel(), float(eps),
+                   _stream(x))
+
+    # kernels/bindings.cpp:74-79
+    def swiglu(self, gu, out):
+        _check_cuda(gu, "gu")
+        _check_cuda(out, "out")
+        if not (out.numel() % 8 == 0 and gu.numel() == 2 * out.numel()):
+            raise RuntimeError("swiglu: out.numel() % 8 == 0 and gu.numel() == 2 * out.numel() required")
+        _check_dtype(gu, torch.float16, "gu")
+        _check_dtype(out, torch.float16, "out")
+        self._call(self.lib.dk_swiglu, gu.data_ptr(), out.data_ptr(), out.numel(), _stream(gu))
+
+    # kernels/bindings.cpp:81-88 (head_dim generalised from 64 to {64, 128})
+    def rope_append(self, qkv, cos_t, sin_t, pos, bt, kc, vc, n_q, n_kv):
+        for t, n in ((qkv, "qkv"), (cos_t, "cos_t"), (sin_t, "sin_t"), (kc, "kc"), (vc, "vc"), (pos, "pos"),
+                     (bt, "bt")):
+            _check_cuda(t, n)
+        if kc.dim() != 4 or kc.size(3) not in (64, 128) or vc.shape != kc.shape or kc.size(1) != n_kv:
+            raise RuntimeError("cache must be [pages, n_kv, P, 64|128]")
+        D = kc.size(3)
+        if qkv.numel() != (n_q + 2 * n_kv) * D or cos_t.dim() != 2 or cos_t.size(1) != D // 2 \
+                or sin_t.shape != cos_t.shape:
+            raise RuntimeError("rope_append: qkv must hold (n_q + 2 n_kv) * D values and cos/sin [max_pos, D/2]")
+        _check_dtype(qkv, torch.float16, "qkv")
+        _check_dtype(cos_t, torch.float32, "cos_t")
+        _check_dtype(sin_t, torch.float32, "sin_t")
+        if bt.dtype != torch.int32 or pos.dtype != torch.int32:
+            raise RuntimeError("bt and pos must be int32")
+        self._call(self.lib.dk_rope_append, qkv.data_ptr(), cos_t.data_ptr(), sin_t.data_ptr(), pos.data_ptr(),
+                   bt.data_ptr(), kc.data_ptr(), vc.data_ptr(), int(n_q), int(n_kv), D, kc.size(2), cos_t.size(0),
+                   kc.size(0), bt.numel(), _stream(qkv))
+
+    # runtime/model.py:232-233 (torch.argmax into tok, then pos += 1) as one launch
+    def argmax_advance(self, logits, tok, pos=None):
+        _check_cuda(logits, "logits")
+        _check_cuda(tok, "tok")
+        _check_dtype(logits, torch.float16, "logits")
+        _check_dtype(tok, torch.int64, "tok")
+        p = None
+        if pos is not None:
+            _check_cuda(pos, "pos")
+            _check_dtype(pos, torch.int32, "pos")
+            p = pos.data_ptr()
+        self._call(self.lib.dk_argmax_advance, logits.data_ptr(), logits.numel(), tok.data_ptr(), p, _stream(logits))
+
+    # runtime/quant.py:42-48,100-124 on the GPU
+    def quantize_w4(self, w, packed, sz, group):
+        for t, n in ((w, "w"), (packed, "packed"), (sz, "sz")):
+            _check_cuda(t, n)
+        N, K = w.shape
+        if not (packed.shape == (N, K // 8) and sz.shape == (N, K // group, 2)):
+            raise RuntimeError("quantize_w4: packed must be [N, K/8] int32 and sz [N, K/G, 2] fp16")
+        _check_dtype(w, torch.float16, "w")
+        _check_dtype(packed, torch.int32, "packed")
+        _check_dtype(sz, torch.float16, "sz")
+        self._call(self.lib.dk_quantize_w4, w.data_ptr(), packed.data_ptr(), sz.data_ptr(), N, K, int(group),
+                   _stream(w))
+
+
+def load(verbose=False):
+    """Load (once) and return the op module. Raises RuntimeError if the library is missing or not loadable."""
+    global _EXT
+    if _EXT is None:
+        lib = open_library()
+        _EXT = DecodeKernels(lib)
+        if verbose:
+            print(f"loaded {LIB_PATH} (HIP runtime {lib.dk_runtime_version()})")
+    return _EXT

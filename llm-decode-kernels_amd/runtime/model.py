@@ -1,0 +1,322 @@
+"""Batch-1 decode runtime for Llama-family models on one MI355X, built on the HIP decode kernels.
+
+Mirrors the reference's ``runtime/model.py`` (DecodeConfig :32-50, Linear :56-72, Model :75-297): one decode step
+(per layer)
+
+    add_rmsnorm -> qkv GEMV -> RoPE + paged-KV append -> paged split-K attention (+ combine) -> o GEMV
+    -> add_rmsnorm -> gate|up GEMV -> SwiGLU -> down GEMV
+
+then the final add_rmsnorm -> LM head -> argmax into the device token slot -> pos += 1. State (token id, position)
+lives in device tensors, so ``step()`` is captured once as a hipGraph (``torch.cuda.CUDAGraph`` on ROCm) and replayed
+for every token. Prefill is teacher-forcing through the same graph, as in the reference.
+
+Differences from the reference, all on the device side of the same composition:
+  * head_dim 64 and 128 (TinyLlama and Llama-3-8B shapes);
+  * the argmax and the position increment run as one kernel (dk_argmax_advance) instead of two torch ops;
+  * weights are quantized on the GPU by the HIP RTN kernel;
+  * there is no ``backend="ref"``: the CPU reference composition is test infrastructure (``oracle.decode_ref``).
+
+Knobs (DecodeConfig): weights "int4" | "fp16"; group; lm_head "auto" | "fp16" | "int4"; fused (False runs the
+HF-style torch op sequences for norm and SwiGLU on the GPU, the reference's unfused comparison point); max_ctx, page,
+part_size (0 -> attention policy table), attn_version, gemv_stage ((stage, R, warps, pf) forced everywhere, or None for
+the tuning table), autotune_path, attn_policy_path, shuffle_pages, device.
+"""
+import json
+import math
+from dataclasses import dataclass, field
+from pathlib import Path
+
+import torch
+
+from . import ext
+from .quant import QuantLinear
+
+PKG = Path(__file__).resolve().parents[1]
+
+
+@dataclass
+class DecodeConfig:
+    weights: str = "int4"
+    group: int = 128
+    quant: str = "rtn"
+    qparams: dict = field(default=None, repr=False)
+    lm_head: str = "auto"
+    fused: bool = True
+    backend: str = "hip"
+    max_ctx: int = 2048
+    page: int = 16
+    part_size: int = 0
+    attn_version: int = 0
+    gemv_stage: tuple = None
+    autotune_path: str = str(PKG / "configs" / "autotune.json")
+    attn_policy_path: str = str(PKG / "configs" / "attn_policy.json")
+    shuffle_pages: bool = True
+    device: str = "cuda"
+    seed: int = 0            # block-table permutation seed
+
+
+def default_gemv_config(N, K):
+    """(stage, R, waves, pf) used when the tuning table has no entry for a shape: one wave per 64 sixteen-byte
+    columns of a row (so one column step per lane), and as many rows per workgroup as keep >= 2048 waves in flight."""
+    U = K // 32
+    waves = min(16, (U + 63) // 64)
+    R = 4
+    while R > 1 and ((N + R - 1) // R) * waves < 2048:
+        R //= 2
+    return (2, R, waves, 1 if U > 64 * waves else 0)
+
+
+class Linear:
+    """One projection in the format the config asks for (runtime/model.py:56-72)."""
+
+    def __init__(self, w, cfg: DecodeConfig, quant: bool):
+        self.N, self.K = w.shape
+        self.quant = quant
+        dev = cfg.device
+        if quant:
+            if cfg.quant != "rtn":
+                raise NotImplementedError("only RTN quantization is produced by this runtime")
+            ql = QuantLinear(w.to(dev), cfg.group)
+            self.packed, self.sz = ql.packed, ql.sz
+            self.nbytes = ql.nbytes()
+        else:
+            self.w = w.to(dev).half().contiguous()
+            self.nbytes = self.w.numel() * 2
+
+
+class Model:
+    def __init__(self, hf_state, hf_config, cfg: DecodeConfig):
+        self.cfg = cfg
+        c = hf_config
+        self.H, self.L = c.hidden_size, c.num_hidden_layers
+        self.n_q, self.n_kv = c.num_attention_heads, c.num_key_value_heads
+        self.D = self.H // self.n_q
+        self.I, self.V = c.intermediate_size, c.vocab_size
+        self.eps = c.rms_norm_eps
+        if cfg.backend not in ("hip", "cuda"):
+            raise ValueError(f"backend {cfg.backend!r}: this runtime runs the HIP kernels only; the CPU reference "
+                             "composition is oracle.decode_ref (test infrastructure)")
+        if self.D not in (64, 128):
+            raise ValueError(f"head_dim {self.D} not supported (64 or 128)")
+        dev = cfg.device
+        self.K = ext.load()
+        quant = cfg.weights == "int4"
+        sd = hf_state
+        g = lambda k: sd[k].half()
+        self.emb = g("model.embed_tokens.weight").to(dev).contiguous()
+        self.layers = []
+        for i in range(self.L):
+            p = f"model.layers.{i}."
+            wqkv = torch.cat([g(p + "self_attn.q_proj.weight"), g(p + "self_attn.k_proj.weight"),
+                              g(p + "self_attn.v_proj.weight")], 0)
+            qkv = Linear(wqkv, cfg, quant)
+            del wqkv
+            wgu = torch.cat([g(p + "mlp.gate_proj.weight"), g(p + "mlp.up_proj.weight")], 0)
+            gu = Linear(wgu, cfg, quant)
+            del wgu
+            self.layers.append({
+                "ln1": g(p + "input_layernorm.weight").to(dev).contiguous(),
+                "ln2": g(p + "post_attention_layernorm.weight").to(dev).contiguous(),
+                "qkv": qkv, "o": Linear(g(p + "self_attn.o_proj.weight"), cfg, quant),
+                "gu": gu, "down": Linear(g(p + "mlp.down_proj.weight"), cfg, quant)})
+        self.norm_f = g("model.norm.weight").to(dev).contiguous()
+        lm = sd["lm_head.weight"] if "lm_head.weight" in sd else sd["model.embed_tokens.weight"]
+        head_int4 = cfg.lm_head == "int4" or (cfg.lm_head == "auto" and quant)
+        self.lm_head = Linear(lm.half(), cfg, head_int4)
+
+        self.gemv_table = {}
+        if cfg.gemv_stage is None and Path(cfg.autotune_path).exists():
+            self.gemv_table = json.load(open(cfg.autotune_path)).get("best", {})
+
+        # paged KV cache [L, 2, pages, n_kv, P, D]; one block table shared by all layers (one sequence)
+        self.n_pages = (cfg.max_ctx + cfg.page - 1) // cfg.page + 1
+        self.kv = torch.zeros(self.L, 2, self.n_pages, self.n_kv, cfg.page, self.D, dtype=torch.half, device=dev)
+        gen = torch.Generator().manual_seed(cfg.seed)
+        perm = torch.randperm(self.n_pages, generator=gen) if cfg.shuffle_pages else torch.arange(self.n_pages)
+        self.bt = perm.int().to(dev)
+        theta = getattr(c, "rope_theta", 10000.0)
+        self.cos, self.sin = (t.to(dev) for t in rope_tables(cfg.max_ctx + 1, self.D, theta))
+
+        self.attn_version = cfg.attn_version or self._policy().get("version", 3)
+        self.set_attention_partition(cfg.max_ctx)
+
+        h16 = dict(dtype=torch.half, device=dev)
+        self.tok = torch.zeros(1, dtype=torch.long, device=dev)
+        self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.x = torch.empty(self.H, **h16)
+        self.normed = torch.empty(self.H, **h16)
+        self.qkv = torch.empty((self.n_q + 2 * self.n_kv) * self.D, **h16)
+        self.attn = torch.empty(self.n_q, self.D, **h16)
+        self.o = torch.empty(self.H, **h16)
+        self.gu = torch.empty(2 * self.I, **h16)
+        self.act = torch.empty(self.I, **h16)
+        self.down = torch.empty(self.H, **h16)
+        self.logits = torch.empty(self.V, **h16)
+        self.graph = None
+        self.host_pos = 0
+
+    # ------------------------------------------------------------------ helpers
+    def set_attention_partition(self, ctx_cap, part_size=None):
+        """Split size for contexts up to ctx_cap and the split buffers (runtime/model.py:140-151): the grid is fixed
+        at ceil(ctx_cap / part_size) splits, surplus ones exit."""
+        ps = part_size or self.cfg.part_size or self._policy_part_size(ctx_cap)
+        self.part_size = ps
+        self.max_splits = max(1, math.ceil(ctx_cap / ps))
+        self.ctx_cap = self.max_splits * ps
+        f32 = dict(dtype=torch.float32, device=self.cfg.device)
+        self.o_part = torch.empty(self.n_q, self.max_splits, self.D, **f32)
+        self.m_part = torch.empty(self.n_q, self.max_splits, **f32)
+        self.l_part = torch.empty(self.n_q, self.max_splits, **f32)
+        self.graph = None
+
+    def prepare(self, ctx_cap, use_graph=True, part_size=None):
+        """Configure attention for contexts <= ctx_cap and (re)capture the decode graph (runtime/model.py:153-158)."""
+        assert ctx_cap <= self.cfg.max_ctx
+        self.set_attention_partition(ctx_cap, part_size)
+        if use_graph:
+            self.capture()
+
+    def _policy(self):
+        p = Path(self.cfg.attn_policy_path)
+        return json.load(open(p)) if p.exists() else {}
+
+    def _policy_part_size(self, ctx_cap):
+        """Entry tuned at the largest context <= ctx_cap (runtime/model.py:164-172)."""
+        ents = [e for e in self._policy().get("policy", []) if e["max_ctx"] < (1 << 30)]
+        if not ents:
+            return 64
+        below = [e for e in ents if e["max_ctx"] <= ctx_cap]
+        return (below[-1] if below else ents[0])["part_size"]
+
+    def gemv_cfg(self, lin):
+        if self.cfg.gemv_stage is not None:
+            return self.cfg.gemv_stage
+        e = self.gemv_table.get(f"{lin.N}x{lin.K}_G{self.cfg.group}")
+        return (2, *e) if e else default_gemv_config(lin.N, lin.K)
+
+    def linear(self, lin: Linear, x, y):
+        if lin.quant:
+            s, r, w, pf = self.gemv_cfg(lin)
+            self.K.gemv_w4a16(s, r, w, pf, lin.packed, lin.sz, x, y, self.cfg.group)
+        else:
+            torch.mm(x.view(1, -1), lin.w.t(), out=y.view(1, -1))  # rocBLAS / hipBLASLt, the reference's cuBLAS call
+
+    def add_norm(self, delta, w):
+        if self.cfg.fused:
+            self.K.add_rmsnorm(self.x, delta, w, self.normed, self.eps)
+        else:  # HF op sequence on the GPU (the reference's unfused comparison point)
+            if delta is not None:
+                self.x.add_(delta)
+            xf = self.x.float()
+            self.normed.copy_(w * (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)).half())
+
+    def swiglu(self):
+        if self.cfg.fused:
+            self.K.swiglu(self.gu, self.act)
+        else:
+            self.act.copy_(torch.nn.functional.silu(self.gu[: self.I].float()).half() * self.gu[self.I:])
+
+    def attention(self, li):
+        kc, vc = self.kv[li, 0], self.kv[li, 1]
+        self.K.rope_append(self.qkv, self.cos, self.sin, self.pos, self.bt, kc, vc, self.n_q, self.n_kv)
+        self.K.paged_attention(self.qkv[: self.n_q * self.D], kc, vc, self.bt, self.pos, self.part_size,
+                               self.o_part, self.m_part, self.l_part, self.attn, self.attn_version)
+
+    # ------------------------------------------------------------------ decode step
+    def step(self):
+        """One token: reads tok/pos, writes logits, tok <- argmax, pos += 1 (runtime/model.py:216-233)."""
+        torch.index_select(self.emb, 0, self.tok, out=self.x.view(1, -1))
+        delta = None
+        for li, lw in enumerate(self.layers):
+            self.add_norm(delta, lw["ln1"])
+            self.linear(lw["qkv"], self.normed, self.qkv)
+            self.attention(li)
+            self.linear(lw["o"], self.attn.view(-1), self.o)
+            self.add_norm(self.o, lw["ln2"])
+            self.linear(lw["gu"], self.normed, self.gu)
+            self.swiglu()
+            self.linear(lw["down"], self.act, self.down)
+            delta = self.down
+        self.add_norm(delta, self.norm_f)
+        self.linear(self.lm_head, self.normed, self.logits)
+        self.K.argmax_advance(self.logits, self.tok, self.pos)
+
+    def capture(self):
+        """Capture step() into a hipGraph after warm-up on a side stream (runtime/model.py:235-251)."""
+        saved_tok, saved_pos = self.tok.clone(), self.pos.clone()
+        self.pos.zero_()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                self.step()
+        torch.cuda.current_stream().wait_stream(s)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.step()
+        self.tok.copy_(saved_tok)
+        self.pos.copy_(saved_pos)
+        torch.cuda.synchronize()
+
+    def run_step(self, use_graph=True):
+        self.host_pos += 1
+        if self.host_pos > self.ctx_cap:
+            raise RuntimeError(f"context {self.host_pos} exceeds the prepared attention cap {self.ctx_cap}; "
+                               "call prepare()")
+        if use_graph and self.graph is not None:
+            self.graph.replay()
+        else:
+            self.step()
+
+    # ------------------------------------------------------------------ high level
+    def reset(self, pos=0):
+        self.pos.fill_(pos)
+        self.host_pos = pos
+
+    def teacher_force(self, tokens, use_graph=True, collect_logits=False):
+        """Feed tokens[i] at positions pos..; returns logits [len, V] (fp16) if requested."""
+        tokens = torch.as_tensor(tokens, device=self.tok.device).long()
+        out = torch.empty(len(tokens), self.V, dtype=torch.half, device=self.tok.device) if collect_logits else None
+        for i in range(len(tokens)):
+            self.tok.copy_(tokens[i:i + 1])
+            self.run_step(use_graph)
+            if collect_logits:
+                out[i].copy_(self.logits)
+        return out
+
+    def generate(self, prompt, n_new, use_graph=True):
+        """Greedy: teacher-force the prompt, then free-run n_new tokens (runtime/model.py:278-286)."""
+        self.reset(0)
+        self.teacher_force(prompt, use_graph)
+        new = [int(self.tok)]
+        for _ in range(n_new - 1):
+            self.run_step(use_graph)
+            new.append(int(self.tok))
+        return new
+
+    # ------------------------------------------------------------------ byte accounting (roofline)
+    def weight_bytes(self):
+        b = sum(l[k].nbytes for l in self.layers for k in ("qkv", "o", "gu", "down"))
+        b += sum(l["ln1"].numel() * 2 + l["ln2"].numel() * 2 for l in self.layers)
+        return {"body": b, "lm_head": self.lm_head.nbytes, "embedding_row": self.H * 2}
+
+    def kv_bytes_per_token(self, ctx):
+        row = self.n_kv * self.D * 2
+        return self.L * (2 * row * ctx + 2 * row)
+
+    def activation_bytes(self):
+        """fp16 activation vectors read/written per token (bench/analyze.py:40 of the reference)."""
+        return 2 * (self.L * (self.H * 6 + self.I * 3 + (self.n_q + 2 * self.n_kv) * self.D) + self.V)
+
+    def bytes_per_token(self, ctx):
+        w = self.weight_bytes()
+        return w["body"] + w["lm_head"] + w["embedding_row"] + self.kv_bytes_per_token(ctx) + self.activation_bytes()
+
+
+def rope_tables(max_pos, head_dim, theta=10000.0, device="cpu"):
+    """fp32 (cos, sin) [max_pos, head_dim/2] of angles p * theta^(-2i/head_dim) computed in float64
+    (reference/ref_ops.py:30-33)."""
+    i2 = torch.arange(0, head_dim, 2, dtype=torch.float64, device=device)
+    inv_freq = 1.0 / torch.pow(torch.tensor(float(theta), dtype=torch.float64, device=device), i2 / head_dim)
+    ang = torch.arange(max_pos, dtype=torch.float64, device=device)[:, None] * inv_freq[None, :]
+    return ang.cos().float().contiguous(), ang.sin().float().contiguous()

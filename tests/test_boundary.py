@@ -1,0 +1,144 @@
+"""CPU checks of the drop-in boundary (no GPU, no compute): the C-ABI library loads, exports every entry point that
+include/dk_amd.h declares with the signature the ctypes shim binds, and every argument-validation path of the C layer
+(kernels/bindings.cpp:18-88 TORCH_CHECKs) returns its error code and message before any HIP call. The torch-facing
+shim rejects non-CUDA tensors with the reference's message."""
+import ctypes
+import re
+
+import pytest
+import torch
+
+from runtime import ext
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return ext.open_library()
+
+
+def declared_entry_points():
+    txt = re.sub(r"/\*.*?\*/", "", ext.HEADER.read_text(), flags=re.S)
+    return re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(dk_\w+)\s*\(", txt, flags=re.M)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = declared_entry_points()
+    assert len(names) >= 10 and "dk_gemv_w4a16" in names and "dk_paged_attention" in names
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(ext.SIGNATURES), "ctypes signatures must cover exactly the header's entry points"
+
+
+def test_header_arities_match_shim(lib):
+    txt = re.sub(r"/\*.*?\*/", "", ext.HEADER.read_text(), flags=re.S)
+    for name, (argtypes, _) in ext.SIGNATURES.items():
+        m = re.search(rf"{name}\s*\(([^)]*)\)", txt)
+        params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
+        assert len(params) == len(argtypes), name
+
+
+def test_runtime_is_torch_runtime(lib):
+    """The library resolves libamdhip64 to the HIP runtime torch loaded: one runtime per process."""
+    v = lib.dk_runtime_version()
+    if torch.version.hip:
+        major, minor = (int(t) for t in torch.version.hip.split(".")[:2])
+        assert v // 10_000_000 == major and (v // 100_000) % 100 == minor, (v, torch.version.hip)
+
+
+A16 = 0x10000          # a 16-byte aligned fake address: validation fails before it is ever dereferenced
+
+
+def _err(lib, rc):
+    return rc, lib.dk_last_error().decode()
+
+
+@pytest.mark.parametrize("args,code,msg", [
+    ((0, 3, 0, 0, A16, A16, A16, A16, 4, 128, 128), 4, "R must be 1,2,4,8"),
+    ((4, 1, 0, 0, A16, A16, A16, A16, 4, 128, 128), 4, "stage"),
+    ((2, 1, 17, 0, A16, A16, A16, A16, 4, 128, 128), 4, "warps"),
+    ((2, 1, 0, 2, A16, A16, A16, A16, 4, 128, 128), 4, "pf"),
+    ((2, 1, 0, 0, A16, A16, A16, A16, 4, 100, 128), 3, "multiple of 32"),
+    ((2, 1, 0, 0, A16, A16, A16, A16, 4, 128, 256), 3, "multiple of 32 and of the group size"),
+    ((2, 1, 0, 0, A16, A16, A16, A16, 4, 192, 96), 4, "group must be a power of two"),
+    ((2, 1, 0, 0, A16, A16, A16, A16, 4, 256, 16), 4, "group must be >= 32"),
+    ((2, 1, 0, 0, A16 + 4, A16, A16, A16, 4, 128, 128), 2, "packed must be 16B aligned"),
+    ((2, 1, 0, 0, A16, A16, A16 + 8, A16, 4, 128, 128), 2, "x must be 16B aligned"),
+    ((2, 1, 0, 0, None, A16, A16, A16, 4, 128, 128), 1, "null"),
+    ((2, 1, 0, 0, A16, A16, A16, A16, 0, 128, 128), 3, "positive"),
+])
+def test_gemv_validation(lib, args, code, msg):
+    rc, m = _err(lib, lib.dk_gemv_w4a16(*args, None))
+    assert rc == code and msg in m, (rc, m)
+
+
+def _attn(lib, **kw):
+    a = dict(version=2, q=A16, kc=A16, vc=A16, bt=A16, pos=A16, n_q=32, n_kv=4, head_dim=64, page=16, n_pages=8,
+             n_bt=8, part_size=64, max_splits=4, o=A16, m=A16, l=A16, out=A16)
+    a.update(kw)
+    return _err(lib, lib.dk_paged_attention(*a.values(), None))
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(n_q=24), 3, "heads-per-group must be 1/2/4/8"),
+    (dict(n_q=30), 3, "heads-per-group"),
+    (dict(head_dim=96), 3, "head_dim"),
+    (dict(page=12), 4, "page size must be a power of two"),
+    (dict(part_size=0), 4, "part_size must be > 0"),
+    (dict(version=4), 4, "version must be 1, 2 or 3"),
+    (dict(version=0), 4, "version must be 1, 2 or 3"),
+    (dict(max_splits=0), 3, "max_splits"),
+    (dict(kc=A16 + 2), 2, "16B aligned"),
+    (dict(bt=None), 1, "null"),
+    (dict(n_bt=0), 3, "empty"),
+])
+def test_attention_validation(lib, kw, code, msg):
+    rc, m = _attn(lib, **kw)
+    assert rc == code and msg in m, (rc, m)
+
+
+def test_small_op_validation(lib):
+    assert _err(lib, lib.dk_add_rmsnorm(A16, None, A16, A16, 2047, 1e-5, None))[0] == 3
+    assert _err(lib, lib.dk_add_rmsnorm(A16 + 2, None, A16, A16, 2048, 1e-5, None))[0] == 2
+    assert _err(lib, lib.dk_add_rmsnorm(A16, A16 + 8, A16, A16, 2048, 1e-5, None))[0] == 2
+    assert _err(lib, lib.dk_add_rmsnorm(None, None, A16, A16, 2048, 1e-5, None))[0] == 1
+    assert _err(lib, lib.dk_swiglu(A16, A16, 5630, None))[0] == 3
+    assert _err(lib, lib.dk_swiglu(A16, A16 + 4, 5632, None))[0] == 2
+    rope = lambda **kw: _err(lib, lib.dk_rope_append(*dict(
+        dict(qkv=A16, c=A16, s=A16, pos=A16, bt=A16, kc=A16, vc=A16, n_q=32, n_kv=4, D=64, page=16, max_pos=100,
+             n_pages=8, n_bt=8), **kw).values(), None))
+    assert rope(D=80)[0] == 3 and rope(page=10)[0] == 4 and rope(max_pos=0)[0] == 3 and rope(bt=None)[0] == 1
+    assert _err(lib, lib.dk_argmax_advance(A16, 0, A16, A16, None))[0] == 3
+    assert _err(lib, lib.dk_argmax_advance(None, 10, A16, A16, None))[0] == 1
+    q = lambda **kw: _err(lib, lib.dk_quantize_w4(*dict(dict(w=A16, p=A16, sz=A16, N=4, K=256, G=128), **kw).values(),
+                                                  None))
+    assert q(G=1024)[0] == 4 and q(G=48)[0] == 4 and q(K=192)[0] == 3 and q(w=A16 + 2)[0] == 2
+    assert _err(lib, lib.dk_bw_read(A16, 1024, A16, 4, 256, 2, None))[0] == 4
+    assert _err(lib, lib.dk_bw_read(A16 + 1, 1024, A16, 4, 256, 1, None))[0] == 2
+
+
+def test_error_message_is_cleared_per_thread(lib):
+    lib.dk_swiglu(A16, A16, 3, None)
+    assert "multiple of 8" in lib.dk_last_error().decode()
+
+
+def test_shim_rejects_cpu_tensors(lib):
+    K = ext.DecodeKernels(lib)
+    packed = torch.zeros(4, 16, dtype=torch.int32)
+    sz = torch.zeros(4, 1, 2, dtype=torch.half)
+    with pytest.raises(RuntimeError, match="must be a contiguous CUDA tensor"):
+        K.gemv_w4a16(2, 4, 0, 0, packed, sz, torch.zeros(128, dtype=torch.half), torch.zeros(4, dtype=torch.half),
+                     128)
+    with pytest.raises(RuntimeError, match="must be a contiguous CUDA tensor"):
+        K.swiglu(torch.zeros(16, dtype=torch.half), torch.zeros(8, dtype=torch.half))
+
+
+def test_load_without_library_fails_loudly(tmp_path):
+    with pytest.raises(RuntimeError, match="not built"):
+        ext.open_library(tmp_path / "missing.so")
+
+
+def test_model_rejects_ref_backend():
+    from runtime.model import DecodeConfig, Model
+    from runtime.synth import LlamaShape
+    with pytest.raises(ValueError, match="oracle.decode_ref"):
+        Model({}, LlamaShape(128, 1, 2, 1, 256, 64), DecodeConfig(backend="ref", device="cpu"))

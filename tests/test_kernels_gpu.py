@@ -1,0 +1,333 @@
+"""GPU parity gate for every kernel, through the C ABI (ctypes op module), against the CPU oracle on identical seeded
+inputs. Mirrors the reference's tests/test_kernels.py order and tolerances:
+  1. 4-row GEMV, closed-form answer, every stage/config, exact                       (test_kernels.py:47-57)
+  2. one-hot x sweep over all 128 columns, exact                                    (test_kernels.py:58-68)
+  3. real GEMV shapes x group sizes vs fp32 matvec of the dequantized weight, 5e-3  (test_kernels.py:71-86)
+  4. paged attention at ctx 128 / odd contexts / 512..16K flat+peaky / spare splits, 2e-3  (test_kernels.py:89-147)
+  5. fused norm / swiglu / rope+append (residual and v-copy exact)                   (test_kernels.py:150-176)
+plus what the reference does not test: the GPU quantizer bit-exact against the oracle, head_dim 128, the argmax step
+kernel and graph replay of the ops. Error metric: normwise max_rel = max|out - ref| / max|ref|.
+"""
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import DEV, assert_close, dequant_from_gpu, err, gen, make_cache
+from oracle import quant_ref as Q
+from oracle import ref_ops as R
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def K():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from runtime import ext
+    return ext.load()
+
+
+# (stage, R, warps, pf): the exact-dequant rung, the R=1 rung, and the streaming kernel over rows x waves x prefetch
+GEMV_CFGS = [(0, 1, 4, 0), (0, 1, 1, 0), (1, 1, 0, 0)] + \
+            [(2, r, w, pf) for r in (1, 2, 4, 8) for w in (0, 1, 2, 4) for pf in (0, 1)]
+
+
+def gemv(K, cfg, packed, sz, x, N, group):
+    y = torch.empty(N, dtype=torch.half, device=DEV)
+    K.gemv_w4a16(cfg[0], cfg[1], cfg[2], cfg[3], packed, sz, x, y, group)
+    return y
+
+
+def _shape1():
+    N, Kd = 4, 128
+    q = np.array([[(k + r) % 16 for k in range(Kd)] for r in range(N)], np.uint8)
+    s = np.array([[(r + 1) * 0.5] for r in range(N)], np.float16)
+    z = np.full((N, 1), 8.0, np.float16)
+    return q, s, z
+
+
+@pytest.mark.parametrize("cfg", GEMV_CFGS)
+def test_gemv_shape1_and_onehot(K, cfg):
+    q, s, z = _shape1()
+    packed = torch.from_numpy(Q.pack(q)).to(DEV)
+    sz = torch.from_numpy(Q.pack_scale_zero(s, z)).to(DEV)
+    y = gemv(K, cfg, packed, sz, torch.ones(128, dtype=torch.half, device=DEV), 4, 128)
+    assert y.float().cpu().tolist() == [-32.0, -64.0, -96.0, -128.0], cfg
+    xs = torch.eye(128, dtype=torch.half, device=DEV)
+    ys = torch.stack([gemv(K, cfg, packed, sz, xs[k].contiguous(), 4, 128) for k in range(128)])  # [k, r]
+    want = (torch.from_numpy(q.astype(np.float32)).t() - 8) * torch.from_numpy(s[:, 0].astype(np.float32))
+    bad = int((ys.float().cpu() != want).any(dim=1).sum())
+    assert bad == 0, f"{cfg}: {bad} wrong columns"
+
+
+SHAPES = {"qkv": (2560, 2048), "o": (2048, 2048), "gate_up": (11264, 2048), "down": (2048, 5632),
+          "lm_head": (32000, 2048)}
+SHAPES_8B = {"qkv8b": (6144, 4096), "o8b": (4096, 4096), "down8b": (4096, 14336), "up8b": (14336, 4096)}
+
+
+def _quantized(K, N, Kd, G, seed):
+    w = (torch.randn(N, Kd, generator=gen(seed)) * 0.02).half()
+    packed = torch.empty(N, Kd // 8, dtype=torch.int32, device=DEV)
+    sz = torch.empty(N, Kd // G, 2, dtype=torch.half, device=DEV)
+    K.quantize_w4(w.to(DEV), packed, sz, G)
+    return w, packed, sz
+
+
+@pytest.mark.parametrize("name", list(SHAPES) + list(SHAPES_8B))
+@pytest.mark.parametrize("G", (64, 128, 256))
+def test_gemv_real_shapes(K, name, G):
+    N, Kd = {**SHAPES, **SHAPES_8B}[name]
+    if name in SHAPES_8B and G != 128:
+        pytest.skip("8B shapes are gated at the model's group size only")
+    w, packed, sz = _quantized(K, N, Kd, G, seed=zlib.crc32(name.encode()) % 1000)
+    wref = dequant_from_gpu(packed, sz, G)
+    x = torch.randn(Kd, generator=gen(1)).half()
+    ref = R.gemv_ref(wref, x)
+    xd = x.to(DEV)
+    cfgs = GEMV_CFGS if (G == 128 and name in SHAPES) else [(0, 1, 4, 0), (1, 1, 0, 0), (2, 4, 0, 0), (2, 8, 2, 1),
+                                                           (2, 2, 1, 1)]
+    from runtime.model import default_gemv_config
+    cfgs = cfgs + [default_gemv_config(N, Kd)]
+    for cfg in cfgs:
+        assert_close(gemv(K, cfg, packed, sz, xd, N, G), ref, 5e-3, f"gemv {name} {N}x{Kd} G{G} {cfg}")
+
+
+@pytest.mark.parametrize("N,Kd,G", [(64, 256, 32), (96, 1024, 64), (5632, 2048, 128), (2560, 2048, 256),
+                                    (33, 4096, 512), (4096, 14336, 128)])
+def test_quantize_bit_exact(K, N, Kd, G):
+    """GPU RTN quantize + pack == oracle quantize + pack, bit for bit (codes, scale, zero)."""
+    g = gen(N * 7 + Kd)
+    w = (torch.randn(N, Kd, generator=g) * 0.02).half()
+    w[0, :G] = 0.0                      # all-zero group: scale floor
+    if Kd >= 2 * G:
+        w[1 % N, G:2 * G] = 0.7         # constant group: zero clamps
+    packed = torch.empty(N, Kd // 8, dtype=torch.int32, device=DEV)
+    sz = torch.empty(N, Kd // G, 2, dtype=torch.half, device=DEV)
+    K.quantize_w4(w.to(DEV), packed, sz, G)
+    rows = np.arange(N) if N * Kd <= 16 << 20 else np.random.default_rng(0).choice(N, 256, replace=False)
+    wn = w.numpy()[rows]
+    q, s, z = Q.quantize(wn, G)
+    assert np.array_equal(packed.cpu().numpy()[rows], Q.pack(q))
+    assert np.array_equal(sz.cpu().numpy()[rows].view(np.uint16), Q.pack_scale_zero(s, z).view(np.uint16))
+
+
+def test_quantize_ties(K):
+    """Round-half-even ties (scale 0.5, w/scale in {0.5, 1.5, 2.5}; zero-point tie) reproduce the oracle's codes."""
+    w = torch.tensor([[-0.5, 7.0, 0.25, 0.75, 1.25, 0.0, 0.0, 0.0] * 4,
+                      [-0.25, 7.25, 0, 0, 0, 0, 0, 0] * 4], dtype=torch.half)
+    packed = torch.empty(2, 4, dtype=torch.int32, device=DEV)
+    sz = torch.empty(2, 1, 2, dtype=torch.half, device=DEV)
+    K.quantize_w4(w.to(DEV), packed, sz, 32)
+    q, s, z = Q.quantize(w.numpy(), 32)
+    assert np.array_equal(packed.cpu().numpy(), Q.pack(q))
+    assert Q.unpack(packed.cpu().numpy())[0, :8].tolist() == [0, 15, 1, 3, 3, 1, 1, 1]
+    assert sz.cpu().float().tolist() == [[[0.5, 1.0]], [[0.5, 0.0]]]
+
+
+# ---------------------------------------------------------------------------------------------------- attention
+def run_attn(K, q, kc, vc, bt, ctx, PS, version=3, spare=0):
+    """spare > 0 sizes the split buffers for more splits than ctx needs, as the runtime does."""
+    D = kc.shape[-1]
+    n_q = q.numel() // D
+    max_splits = max(1, (ctx + PS - 1) // PS) + spare
+    o_part = torch.empty(n_q, max_splits, D, device=DEV)
+    m_part = torch.empty(n_q, max_splits, device=DEV)
+    l_part = torch.empty_like(m_part)
+    out = torch.empty(n_q, D, dtype=torch.half, device=DEV)
+    pos = torch.tensor([ctx - 1], dtype=torch.int32, device=DEV)
+    K.paged_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), bt.to(DEV), pos, PS, o_part, m_part, l_part, out, version)
+    return out
+
+
+@pytest.mark.parametrize("n_q,n_kv", [(32, 4), (8, 8), (16, 4), (8, 4)])
+@pytest.mark.parametrize("page", (16, 32))
+def test_attention_ctx128(K, n_q, n_kv, page):
+    kc, vc, bt = make_cache(128, n_kv, page, seed=n_q + page)
+    q = torch.randn(n_q, 64, generator=gen(5)).half()
+    k, v = R.gather_kv(kc, vc, bt, 128, page)
+    ref = R.attention_contiguous_ref(q, k, v)
+    for PS in (4096, 64, 32, 48, 16):
+        for ver in (1, 2, 3):
+            assert_close(run_attn(K, q, kc, vc, bt, 128, PS, ver), ref, 2e-3, f"ctx128 {n_q}/{n_kv} P{page} PS{PS}")
+
+
+@pytest.mark.parametrize("ctx", (1, 2, 17, 63, 65, 129, 1000))
+def test_attention_odd_ctx(K, ctx):
+    kc, vc, bt = make_cache(ctx, 4, 16, seed=ctx)
+    q = torch.randn(32, 64, generator=gen(ctx + 1)).half()
+    ref = R.paged_attention_ref(q, kc, vc, bt, ctx, 16)
+    for PS in (8192, 64, 256):
+        assert_close(run_attn(K, q, kc, vc, bt, ctx, PS), ref, 2e-3, f"ctx{ctx} PS{PS}")
+
+
+@pytest.mark.parametrize("ctx", (512, 1024, 2048, 4096, 8192, 16384))
+@pytest.mark.parametrize("peaky", (1.0, 6.0))
+def test_attention_real_ctx(K, ctx, peaky):
+    kc, vc, bt = make_cache(ctx, 4, 16, peaky=peaky, seed=ctx)
+    q = torch.randn(32, 64, generator=gen(ctx + 2)).half()
+    ref = R.paged_attention_ref(q, kc, vc, bt, ctx, 16)
+    for PS in sorted({ctx, 1024, 256, 128, 64, 32}):
+        assert_close(run_attn(K, q, kc, vc, bt, ctx, PS), ref, 2e-3, f"ctx{ctx} peaky{peaky} PS{PS}")
+
+
+@pytest.mark.parametrize("ctx", (1, 40, 64, 100, 700, 2048, 5000))
+def test_attention_runtime_spare_splits(K, ctx):
+    kc, vc, bt = make_cache(ctx, 4, 16, peaky=6.0, seed=ctx + 3)
+    q = torch.randn(32, 64, generator=gen(ctx + 4)).half()
+    ref = R.paged_attention_ref(q, kc, vc, bt, ctx, 16)
+    for PS in (32, 64, 128, 256):
+        assert_close(run_attn(K, q, kc, vc, bt, ctx, PS, spare=8), ref, 2e-3, f"runtime ctx{ctx} PS{PS}")
+
+
+@pytest.mark.parametrize("n_q,n_kv", [(32, 8), (8, 8), (16, 8), (64, 8)])
+@pytest.mark.parametrize("ctx", (1, 100, 777, 4096))
+def test_attention_head_dim_128(K, n_q, n_kv, ctx):
+    kc, vc, bt = make_cache(ctx, n_kv, 16, D=128, peaky=2.0, seed=ctx + n_q)
+    q = torch.randn(n_q, 128, generator=gen(ctx)).half()
+    ref = R.paged_attention_ref(q, kc, vc, bt, ctx, 16)
+    for PS in (ctx, 64, 256):
+        assert_close(run_attn(K, q, kc, vc, bt, ctx, PS), ref, 2e-3, f"D128 {n_q}/{n_kv} ctx{ctx} PS{PS}")
+
+
+def test_attention_ctx1_is_v0(K):
+    """Softmax over one token returns that token's V exactly (fp16 in, fp16 out)."""
+    kc, vc, bt = make_cache(1, 4, 16, seed=9)
+    q = torch.randn(32, 64, generator=gen(9)).half()
+    out = run_attn(K, q, kc, vc, bt, 1, 64).cpu()
+    v0 = vc[bt[0], :, 0]                          # [n_kv, D]
+    assert torch.equal(out, v0.repeat_interleave(8, dim=0))
+
+
+def test_attention_split_buffers_ignored_past_live(K):
+    """Splits beyond ceil(ctx/PS) must not touch the buffers (grid sized for the cap, surplus splits exit)."""
+    ctx, PS, spare = 100, 32, 6
+    kc, vc, bt = make_cache(ctx, 4, 16, seed=11)
+    q = torch.randn(32, 64, generator=gen(11)).half()
+    ms = (ctx + PS - 1) // PS + spare
+    o_part = torch.full((32, ms, 64), 7.0, device=DEV)
+    m_part = torch.full((32, ms), 7.0, device=DEV)
+    l_part = torch.full((32, ms), 7.0, device=DEV)
+    out = torch.empty(32, 64, dtype=torch.half, device=DEV)
+    pos = torch.tensor([ctx - 1], dtype=torch.int32, device=DEV)
+    K.paged_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), bt.to(DEV), pos, PS, o_part, m_part, l_part, out, 3)
+    live = (ctx + PS - 1) // PS
+    assert torch.all(o_part[:, live:] == 7.0) and torch.all(m_part[:, live:] == 7.0)
+    assert_close(out, R.paged_attention_ref(q, kc, vc, bt, ctx, 16), 2e-3, "spare")
+
+
+# ----------------------------------------------------------------------------------------------- fused elementwise
+@pytest.mark.parametrize("H", (2048, 4096, 64))
+def test_add_rmsnorm(K, H):
+    g = gen(H)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).half()
+    x = (torch.randn(H, generator=g) * 3).half()
+    d = torch.randn(H, generator=g).half()
+    xr, outr = R.add_rmsnorm_ref(x.clone(), d, w, 1e-5)
+    xk, out = x.to(DEV), torch.empty(H, dtype=torch.half, device=DEV)
+    K.add_rmsnorm(xk, d.to(DEV), w.to(DEV), out, 1e-5)
+    assert torch.equal(xk.cpu(), xr), "residual must be bit-exact"
+    assert_close(out, outr, 2e-3, "add_rmsnorm out")
+    xk = x.to(DEV)
+    K.add_rmsnorm(xk, None, w.to(DEV), out, 1e-5)
+    assert torch.equal(xk.cpu(), x), "no-residual norm must not modify x"
+    assert_close(out, R.add_rmsnorm_ref(x, None, w, 1e-5)[1], 2e-3, "rmsnorm (no residual)")
+
+
+@pytest.mark.parametrize("I", (5632, 14336, 8))
+def test_swiglu(K, I):
+    gu = (torch.randn(2 * I, generator=gen(I)) * 2).half()
+    out = torch.empty(I, dtype=torch.half, device=DEV)
+    K.swiglu(gu.to(DEV), out)
+    assert_close(out, R.swiglu_ref(gu), 2e-3, "swiglu")
+
+
+@pytest.mark.parametrize("D,n_q,n_kv,theta", [(64, 32, 4, 1e4), (128, 32, 8, 5e5)])
+@pytest.mark.parametrize("pos", (0, 1, 37, 2047, 4095))
+def test_rope_append(K, D, n_q, n_kv, theta, pos):
+    """q and k are bit-exact (fp32 products rounded separately, as the reference's elementwise ops); v copy exact."""
+    page = 16
+    cos, sin = R.rope_tables(4096, D, theta)
+    kc, vc, bt = make_cache(4096, n_kv, page, D=D, seed=pos)
+    kr_c, vr_c = kc.clone(), vc.clone()
+    qkv = torch.randn((n_q + 2 * n_kv) * D, generator=gen(pos + D)).half()
+    qref = R.rope_append_ref(qkv.clone(), cos, sin, pos, kr_c, vr_c, bt, n_q, n_kv, D, page)
+    qk, kcd, vcd = qkv.to(DEV), kc.to(DEV), vc.to(DEV)
+    K.rope_append(qk, cos.to(DEV), sin.to(DEV), torch.tensor([pos], dtype=torch.int32, device=DEV), bt.to(DEV),
+                  kcd, vcd, n_q, n_kv)
+    assert torch.equal(qk[: n_q * D].view(n_q, D).cpu(), qref), f"rope q pos{pos}: {err(qk[:n_q * D].view(n_q, D), qref)}"
+    assert torch.equal(kcd.cpu(), kr_c), f"rope k-cache pos{pos}: {err(kcd, kr_c)}"
+    assert torch.equal(vcd.cpu(), vr_c), f"rope v-cache pos{pos}"
+    assert torch.equal(qk[n_q * D:].cpu(), qkv[n_q * D:]), "k and v slots of qkv must be untouched"
+
+
+def test_rope_out_of_table_position_is_noop(K):
+    """*pos beyond the rope table: nothing is touched (no out-of-bounds table read)."""
+    cos, sin = R.rope_tables(64, 64)
+    kc, vc, bt = make_cache(64, 4, 16, seed=3)
+    qkv = torch.randn(40 * 64, generator=gen(3)).half()
+    qk, kcd = qkv.to(DEV), kc.to(DEV)
+    K.rope_append(qk, cos.to(DEV), sin.to(DEV), torch.tensor([64], dtype=torch.int32, device=DEV), bt.to(DEV),
+                  kcd, vc.to(DEV), 32, 4)
+    assert torch.equal(qk.cpu(), qkv) and torch.equal(kcd.cpu(), kc)
+
+
+@pytest.mark.parametrize("V", (32000, 128256, 7))
+def test_argmax_advance(K, V):
+    logits = torch.randn(V, generator=gen(V)).half()
+    logits[V // 3] = 50.0
+    logits[V // 2] = 50.0                      # tie: the lower index wins, as torch.argmax on the CPU
+    tok = torch.zeros(1, dtype=torch.long, device=DEV)
+    pos = torch.tensor([41], dtype=torch.int32, device=DEV)
+    K.argmax_advance(logits.to(DEV), tok, pos)
+    assert int(tok) == int(torch.argmax(logits.float())) == V // 3 and int(pos) == 42
+    K.argmax_advance(logits.to(DEV), tok, None)
+    assert int(pos) == 42
+
+
+def test_graph_replay_of_ops(K):
+    """rope -> attention -> GEMV captured into one hipGraph; each replay (with eager work between replays) equals the
+    eager result, and the graph reads the device-resident position anew on every replay."""
+    n_q, n_kv, D, page, ctx_cap, PS = 32, 4, 64, 16, 256, 32
+    cos, sin = (t.to(DEV) for t in R.rope_tables(ctx_cap + 1, D))
+    kc, vc, bt = (t.to(DEV) for t in make_cache(ctx_cap, n_kv, page, seed=21))
+    w, packed, sz = _quantized(K, 512, n_q * D, 128, seed=21)
+    qkv0 = torch.randn((n_q + 2 * n_kv) * D, generator=gen(22)).half().to(DEV)
+    qkv = qkv0.clone()
+    pos = torch.tensor([100], dtype=torch.int32, device=DEV)
+    ms = ctx_cap // PS
+    o_part = torch.empty(n_q, ms, D, device=DEV)
+    m_part = torch.empty(n_q, ms, device=DEV)
+    l_part = torch.empty_like(m_part)
+    attn = torch.empty(n_q, D, dtype=torch.half, device=DEV)
+    y = torch.empty(512, dtype=torch.half, device=DEV)
+
+    def body():
+        K.rope_append(qkv, cos, sin, pos, bt, kc, vc, n_q, n_kv)
+        K.paged_attention(qkv[: n_q * D], kc, vc, bt, pos, PS, o_part, m_part, l_part, attn, 3)
+        K.gemv_w4a16(2, 4, 0, 0, packed, sz, attn.view(-1), y, 128)
+
+    expected = {}
+    for p in (100, 101, 150):
+        qkv.copy_(qkv0)
+        pos.fill_(p)
+        body()
+        torch.cuda.synchronize()
+        expected[p] = y.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        body()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        body()
+    for rep in range(3):
+        for p in (100, 101, 150):
+            qkv.copy_(qkv0)
+            pos.fill_(p)
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y, expected[p]), (rep, p)
+            _ = (qkv0.float() * 2).sum().item()     # eager work between replays
