@@ -47,10 +47,12 @@ int dk_runtime_version(void);
  * W4A16 GEMV  y[N] = dequant(W)[N,K] . x[K]   (fp16 in/out, fp32 accumulation)
  * Replaces gemv_w4a16 (kernels/bindings.cpp:27-38) -> gemv_w4a16_launch (kernels/gemv_w4a16.cu:248-267).
  * stage 0: one wave per row, per-element dequant fp16((q-z)*s) then fp32 FMA (the reference's exact-dequant ladder
- *          rung, kernels/gemv_w4a16.cu:16-36);
- * stage 1..3: the streaming kernel: R rows per workgroup (R in {1,2,4,8}), `warps` = waves per workgroup splitting K
- *          (1..16; 0 = one wave per 64 x 16-byte columns of a row), pf in {0,1} = software-prefetch the next column
- *          step. stage 1 forces R = 1.
+ *          rung, kernels/gemv_w4a16.cu:16-36); `warps` = rows (waves) per workgroup (0 = 4).
+ * stage 1, 2: every wave streams R whole rows (R in {1,2,4,8}; stage 1 forces R = 1), `warps` waves per workgroup
+ *          (1..16, 0 = 4), pf in 0..3 = 2^pf column steps of 16-byte loads in flight per lane (capped at 16 / R);
+ *          x is staged in LDS, so K <= 32768 (as the reference's gemv_rb<R,PF>, kernels/gemv_w4a16.cu:39-100).
+ * stage 3: split-K: the workgroup's `warps` waves (1..16, 0 = one per 64 columns of 32 weights) share R rows,
+ *          pf in {0,1} = one-step prefetch (for narrow N).
  * Requires K % 32 == 0, group a power of two >= 32 with K % group == 0, packed and x 16-byte aligned.
  */
 int dk_gemv_w4a16(int stage, int R, int warps, int pf, const void* packed, const void* sz, const void* x, void* y,

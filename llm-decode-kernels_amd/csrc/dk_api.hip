@@ -56,7 +56,12 @@ int dk_gemv_w4a16(int stage, int R, int warps, int pf, const void* packed, const
   if (stage < 0 || stage > 3) return fail(DK_ERR_DOMAIN, "gemv_w4a16: stage must be 0..3, got %d", stage);
   if (R != 1 && R != 2 && R != 4 && R != 8) return fail(DK_ERR_DOMAIN, "gemv: R must be 1,2,4,8, got %d", R);
   if (warps < 0 || warps > 16) return fail(DK_ERR_DOMAIN, "gemv_w4a16: warps must be 0..16, got %d", warps);
-  if (pf != 0 && pf != 1) return fail(DK_ERR_DOMAIN, "gemv_w4a16: pf must be 0 or 1, got %d", pf);
+  if (stage == 3 ? (pf != 0 && pf != 1) : (pf < 0 || pf > 3))
+    return fail(DK_ERR_DOMAIN, "gemv_w4a16: pf must be %s for stage %d, got %d", stage == 3 ? "0 or 1" : "0..3",
+                stage, pf);
+  if ((stage == 1 || stage == 2) && K > dk::kGemvRowsMaxK)
+    return fail(DK_ERR_SHAPE, "gemv_w4a16: stage %d stages x in LDS and needs K <= %d, got %d", stage,
+                dk::kGemvRowsMaxK, K);
   if (N <= 0 || K <= 0) return fail(DK_ERR_SHAPE, "gemv_w4a16: N and K must be positive (N=%d K=%d)", N, K);
   if (K % 32 != 0 || K % group != 0)
     return fail(DK_ERR_SHAPE, "K must be a multiple of 32 and of the group size (K=%d group=%d)", K, group);

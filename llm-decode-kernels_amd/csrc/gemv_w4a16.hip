@@ -2,11 +2,8 @@
 //
 // Weight format (runtime/quant.py:9-12 of the reference): packed int32 [N, K/8], word j = elements 8j..8j+7 with
 // element 8j+2i at bits [4i, 4i+4) and 8j+2i+1 at [16+4i, 20+4i); per (row, group of G) an fp16 (scale, zero) pair.
-// Dequantized weight w = (q - zero) * scale.
-//
-// Streaming kernel. A workgroup owns R consecutive rows; its W waves split the row's K/32 sixteen-byte columns
-// (column u = 32 weights), thread t taking columns t, t + 64W, ... For each column a lane loads R x 16 B of nibbles
-// (non-temporal), the matching 64 B of x (L2-resident, shared by all rows) and R (scale, zero) words.
+// Dequantized weight w = (q - zero) * scale. A "column" u of a row is one 16-byte chunk = 32 weights = 8 words; a row
+// has U = K / 32 columns.
 //
 // Dequant without a per-weight subtract or multiply: OR-ing a nibble into the mantissa of 0x6400 (fp16 1024) gives
 // the fp16 value 1024 + q exactly, and masking the nibble one position higher (bits 4..7) gives 1024 + 16 q. One
@@ -18,8 +15,18 @@
 // and the column adds scale * that to the row's fp32 accumulator. All products and the per-column sums are exact or
 // fp32-rounded, so the result agrees with the fp32 matvec of the fp16-dequantized weight far inside fp16 output
 // precision, and the exact cases (integer x, one-hot x) are reproduced bit for bit.
+// Per 8 weights: 1 shift + 4 v_and_or + 4 v_dot2 (no dequant multiply).
 //
-// Per 8 weights: 1 shift + 4 v_and_or + 4 v_dot2 (no dequant multiply), which keeps the ALU well under the HBM time.
+// Kernel family (the reference's ladder, kernels/gemv_w4a16.cu:16-130, re-cut for wave64):
+//   stage 0  gemv_w4a16_exact   one wave per row, per-element fp16 dequant, fp32 FMA (correctness rung).
+//   stage 1  = stage 2 with R = 1.
+//   stage 2  gemv_w4a16_rows    each wave owns R consecutive rows and streams all of K: lane l takes columns l,
+//                               l + 64, ... (1 KB contiguous per row per wave load), 2^pf column steps of loads in
+//                               flight per lane; x is staged once per workgroup in LDS, transposed so that the 64
+//                               lanes of a step read consecutive 16-byte words (no bank conflicts). No barrier after
+//                               the staging and no LDS reduction: each wave reduces its rows with lane shuffles.
+//   stage 3  gemv_w4a16_splitk  the workgroup's waves split K for R rows (x read through the cache), partial sums
+//                               reduced through LDS: for narrow N, where whole-row waves would leave CUs idle.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -57,11 +64,10 @@ gemv_w4a16_exact(const uint32_t* __restrict__ W, const uint32_t* __restrict__ SZ
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Streaming kernel, R rows per workgroup, blockDim.x = 64 * waves (waves <= 16).
+// One column (32 weights) of R rows against the column's 32 x values (xc[0..3], 8 fp16 each).
 template <int R>
-__device__ __forceinline__ void column_fma(const u32x4 (&w)[R], const uint32_t (&szw)[R], const u32x4* __restrict__ xp,
+__device__ __forceinline__ void column_fma(const u32x4 (&w)[R], const uint32_t (&szw)[R], const u32x4 (&xc)[4],
                                            float (&acc)[R]) {
-  const u32x4 xc[4] = {xp[0], xp[1], xp[2], xp[3]};
   const f16x2 one = {(f16)1.0f, (f16)1.0f};
   float SA = 0.f, SB = 0.f;
 #pragma unroll
@@ -91,13 +97,16 @@ __device__ __forceinline__ void column_fma(const u32x4 (&w)[R], const uint32_t (
   }
 }
 
-template <int R, bool PF>
+// ---------------------------------------------------------------------------------------------------------------
+// Stage 2: wave-owns-rows streaming kernel. blockDim.x = 64 * waves; dynamic LDS = ceil(U / 64) * 4 KB (x,
+// transposed: column u's k-th 16-byte word sits at xs[((u >> 6) * 4 + k) * 64 + (u & 63)]).
+template <int R, int P>
 __global__ void __launch_bounds__(1024)
-gemv_w4a16_stream(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, const u32x4* __restrict__ X,
-                  f16* __restrict__ y, int N, int U, int gsh) {
-  __shared__ float red[16][R];
-  const int t = threadIdx.x, nt = blockDim.x;
-  const int row0 = blockIdx.x * R;
+gemv_w4a16_rows(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, const u32x4* __restrict__ X,
+                f16* __restrict__ y, int N, int U, int gsh) {
+  extern __shared__ u32x4 xs[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+  const int row0 = (blockIdx.x * nw + wave) * R;
   const int NG = U >> gsh;
   const u32x4* wrow[R];
   const uint32_t* srow[R];
@@ -107,32 +116,94 @@ gemv_w4a16_stream(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, 
     wrow[r] = W + (size_t)rr * U;
     srow[r] = SZ + (size_t)rr * NG;
   }
+
+  // Weight loads of the first P steps go out before x is staged: they do not depend on it.
+  u32x4 w[P][R];
+  uint32_t s[P][R];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int u = p * kWave + lane;
+    if (u < U) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) w[p][r] = load_stream(wrow[r] + u);
+#pragma unroll
+      for (int r = 0; r < R; ++r) s[p][r] = srow[r][u >> gsh];
+    }
+  }
+  for (int i = tid; i < 4 * U; i += blockDim.x) {
+    const int u = i >> 2, k = i & 3;
+    xs[(((u >> 6) << 2) + k) * kWave + (u & 63)] = X[i];
+  }
+  __syncthreads();
+
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+  const int steps = (U + kWave - 1) / kWave;
+  for (int base = 0; base < steps; base += P) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int st = base + p;
+      const int u = st * kWave + lane;
+      if (u < U) {
+        const u32x4* xp = xs + (st << 2) * kWave + lane;
+        const u32x4 xc[4] = {xp[0], xp[kWave], xp[2 * kWave], xp[3 * kWave]};
+        column_fma<R>(w[p], s[p], xc, acc);
+      }
+      const int un = u + P * kWave;
+      if (un < U) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) w[p][r] = load_stream(wrow[r] + un);
+#pragma unroll
+        for (int r = 0; r < R; ++r) s[p][r] = srow[r][un >> gsh];
+      }
+    }
+  }
+
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = group_sum<kWave>(acc[r]);
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (lane == r && row0 + r < N) y[row0 + r] = (f16)acc[r];
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Stage 3: split-K kernel, R rows per workgroup, blockDim.x = 64 * waves (waves <= 16); thread t takes columns
+// t, t + 64 * waves, ...; one prefetch step when PF.
+template <int R, bool PF>
+__global__ void __launch_bounds__(1024)
+gemv_w4a16_splitk(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, const u32x4* __restrict__ X,
+                  f16* __restrict__ y, int N, int U, int gsh) {
+  __shared__ float red[16][R];
+  const int t = threadIdx.x, nt = blockDim.x;
+  const int row0 = blockIdx.x * R;
+  const int NG = U >> gsh;
+  const u32x4* wrow[R];
+  const uint32_t* srow[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int rr = min(row0 + r, N - 1);
+    wrow[r] = W + (size_t)rr * U;
+    srow[r] = SZ + (size_t)rr * NG;
+  }
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
 
-  if constexpr (!PF) {
-    for (int u = t; u < U; u += nt) {
-      u32x4 w[R];
-      uint32_t szw[R];
+  int u = t;
+  u32x4 w[R];
+  uint32_t szw[R];
+  if (u < U) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) w[r] = load_stream(wrow[r] + u);
+    for (int r = 0; r < R; ++r) w[r] = load_stream(wrow[r] + u);
 #pragma unroll
-      for (int r = 0; r < R; ++r) szw[r] = srow[r][u >> gsh];
-      column_fma<R>(w, szw, X + 4 * u, acc);
-    }
-  } else {
-    int u = t;
-    u32x4 w[R];
-    uint32_t szw[R];
-    if (u < U) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) w[r] = load_stream(wrow[r] + u);
-#pragma unroll
-      for (int r = 0; r < R; ++r) szw[r] = srow[r][u >> gsh];
-    }
-    while (u < U) {
-      const int un = u + nt;
+    for (int r = 0; r < R; ++r) szw[r] = srow[r][u >> gsh];
+  }
+  while (u < U) {
+    const u32x4* xp = X + 4 * u;
+    const u32x4 xc[4] = {xp[0], xp[1], xp[2], xp[3]};
+    const int un = u + nt;
+    if constexpr (PF) {
       u32x4 wn[R];
       uint32_t szn[R];
       if (un < U) {
@@ -141,14 +212,22 @@ gemv_w4a16_stream(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, 
 #pragma unroll
         for (int r = 0; r < R; ++r) szn[r] = srow[r][un >> gsh];
       }
-      column_fma<R>(w, szw, X + 4 * u, acc);
+      column_fma<R>(w, szw, xc, acc);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         w[r] = wn[r];
         szw[r] = szn[r];
       }
-      u = un;
+    } else {
+      column_fma<R>(w, szw, xc, acc);
+      if (un < U) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) w[r] = load_stream(wrow[r] + un);
+#pragma unroll
+        for (int r = 0; r < R; ++r) szw[r] = srow[r][un >> gsh];
+      }
     }
+    u = un;
   }
 
 #pragma unroll
@@ -172,28 +251,65 @@ gemv_w4a16_stream(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, 
   }
 }
 
+template <int R, int P>
+void launch_rows(int waves, const void* packed, const void* sz, const void* x, void* y, int N, int K, int log2G,
+                 hipStream_t st) {
+  const int U = K >> 5;
+  const int rows_per_block = R * waves;
+  const int blocks = (N + rows_per_block - 1) / rows_per_block;
+  // The transposed x layout pads the last step to 64 columns: ceil(U / 64) steps x 4 words x 64 lanes x 16 B.
+  const size_t lds = (size_t)((U + 63) / 64) * 4 * 64 * 16;
+  hipLaunchKernelGGL((gemv_w4a16_rows<R, P>), dim3(blocks), dim3(64 * waves), lds, st,
+                     (const u32x4*)packed, (const uint32_t*)sz, (const u32x4*)x, (f16*)y, N, U, log2G - 5);
+}
+
 template <int R>
-void launch_stream(int waves, int pf, const void* packed, const void* sz, const void* x, void* y, int N, int K,
+void launch_rows_p(int waves, int pf, const void* packed, const void* sz, const void* x, void* y, int N, int K,
+                   int log2G, hipStream_t st) {
+  // prefetch depth 2^pf column steps, capped so that at most 16 loads of 16 B per lane are in flight (R * depth <= 16)
+  const int P = min(1 << pf, 16 / R);
+  if constexpr (R <= 2) {
+    if (P >= 8) return launch_rows<R, 8>(waves, packed, sz, x, y, N, K, log2G, st);
+  }
+  if constexpr (R <= 4) {
+    if (P >= 4) return launch_rows<R, 4>(waves, packed, sz, x, y, N, K, log2G, st);
+  }
+  if (P >= 2) return launch_rows<R, 2>(waves, packed, sz, x, y, N, K, log2G, st);
+  launch_rows<R, 1>(waves, packed, sz, x, y, N, K, log2G, st);
+}
+
+template <int R>
+void launch_splitk(int waves, int pf, const void* packed, const void* sz, const void* x, void* y, int N, int K,
                    int log2G, hipStream_t st) {
   const int U = K >> 5;
   const int blocks = (N + R - 1) / R;
   const int gsh = log2G - 5;
   if (pf)
-    hipLaunchKernelGGL((gemv_w4a16_stream<R, true>), dim3(blocks), dim3(64 * waves), 0, st, (const u32x4*)packed,
+    hipLaunchKernelGGL((gemv_w4a16_splitk<R, true>), dim3(blocks), dim3(64 * waves), 0, st, (const u32x4*)packed,
                        (const uint32_t*)sz, (const u32x4*)x, (f16*)y, N, U, gsh);
   else
-    hipLaunchKernelGGL((gemv_w4a16_stream<R, false>), dim3(blocks), dim3(64 * waves), 0, st, (const u32x4*)packed,
+    hipLaunchKernelGGL((gemv_w4a16_splitk<R, false>), dim3(blocks), dim3(64 * waves), 0, st, (const u32x4*)packed,
                        (const uint32_t*)sz, (const u32x4*)x, (f16*)y, N, U, gsh);
 }
 
 }  // namespace
 
-void gemv_default_config(int N, int K, int* R, int* waves, int* pf) {
+void gemv_default_config(int N, int K, int* stage, int* R, int* waves, int* pf) {
+  // Whole-row waves (stage 2) while they give at least ~8 waves per CU (2048 waves on 256 CUs) and x fits the LDS
+  // budget; split-K (stage 3) below that, so that narrow outputs still fill the chip.
   const int U = K >> 5;
+  if (N >= 4096 && K <= kGemvRowsMaxK) {
+    *stage = 2;
+    *R = 2;
+    *waves = 4;
+    *pf = U > 64 ? 2 : 0;
+    return;
+  }
   int w = (U + 63) / 64;
   if (w > 16) w = 16;
   int r = 4;
   while (r > 1 && (long long)((N + r - 1) / r) * w < 2048) r >>= 1;
+  *stage = 3;
   *R = r;
   *waves = w;
   *pf = (U > 64 * w) ? 1 : 0;
@@ -207,16 +323,22 @@ void launch_gemv_w4a16(int stage, int R, int waves, int pf, const void* packed, 
                        (const uint32_t*)sz, (const f16*)x, (f16*)y, N, K, log2G);
     return;
   }
-  if (waves <= 0) {
-    int r, w, p;
-    gemv_default_config(N, K, &r, &w, &p);
-    waves = w;
+  if (waves <= 0) waves = stage == 3 ? min(16, ((K >> 5) + 63) / 64) : 4;
+  if (stage == 1) R = 1;
+  if (stage == 1 || stage == 2) {
+    switch (R) {
+      case 1: launch_rows_p<1>(waves, pf, packed, sz, x, y, N, K, log2G, st); break;
+      case 2: launch_rows_p<2>(waves, pf, packed, sz, x, y, N, K, log2G, st); break;
+      case 4: launch_rows_p<4>(waves, pf, packed, sz, x, y, N, K, log2G, st); break;
+      default: launch_rows_p<8>(waves, pf, packed, sz, x, y, N, K, log2G, st); break;
+    }
+    return;
   }
   switch (R) {
-    case 1: launch_stream<1>(waves, pf, packed, sz, x, y, N, K, log2G, st); break;
-    case 2: launch_stream<2>(waves, pf, packed, sz, x, y, N, K, log2G, st); break;
-    case 4: launch_stream<4>(waves, pf, packed, sz, x, y, N, K, log2G, st); break;
-    default: launch_stream<8>(waves, pf, packed, sz, x, y, N, K, log2G, st); break;
+    case 1: launch_splitk<1>(waves, pf, packed, sz, x, y, N, K, log2G, st); break;
+    case 2: launch_splitk<2>(waves, pf, packed, sz, x, y, N, K, log2G, st); break;
+    case 4: launch_splitk<4>(waves, pf, packed, sz, x, y, N, K, log2G, st); break;
+    default: launch_splitk<8>(waves, pf, packed, sz, x, y, N, K, log2G, st); break;
   }
 }
 

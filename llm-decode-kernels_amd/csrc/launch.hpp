@@ -6,12 +6,14 @@
 
 namespace dk {
 
-// W4A16 GEMV. stage 0: exact per-element dequant, `waves` rows per workgroup. stage >= 1: streaming kernel with
-// R rows per workgroup, `waves` waves splitting K, `pf` software prefetch.
+// W4A16 GEMV. stage 0: exact per-element dequant, `waves` rows per workgroup. stage 1/2: each wave streams R whole
+// rows, `waves` waves per workgroup, 2^pf column steps in flight, x staged in LDS (K <= kGemvRowsMaxK). stage 3: the
+// workgroup's `waves` waves split K for R rows, pf = one-step prefetch.
+constexpr int kGemvRowsMaxK = 32768;  // x in LDS: K * 2 bytes <= 64 KB per workgroup
 void launch_gemv_w4a16(int stage, int R, int waves, int pf, const void* packed, const void* sz, const void* x,
                        void* y, int N, int K, int log2G, hipStream_t st);
-// Default streaming configuration for a shape: (R, waves, pf).
-void gemv_default_config(int N, int K, int* R, int* waves, int* pf);
+// Default configuration for a shape: (stage, R, waves, pf).
+void gemv_default_config(int N, int K, int* stage, int* R, int* waves, int* pf);
 
 void launch_bw_read(const void* buf, size_t bytes, void* sink, int blocks, int threads, int unroll, hipStream_t st);
 

@@ -14,6 +14,12 @@
 namespace dk {
 namespace {
 
+// torch.clamp semantics: a value equal to a bound (in particular -0.0 against a bound of +0.0) and NaN pass through
+// unchanged. fminf / fmaxf would return +0.0 for (-0.0, +0.0) and drop NaN.
+__device__ __forceinline__ float clamp_keep_sign(float v, float lo, float hi) {
+  return v < lo ? lo : (v > hi ? hi : v);
+}
+
 template <int WPG>  // words (threads) per group
 __global__ void __launch_bounds__(256)
 quantize_w4_kernel(const f16* __restrict__ w, uint32_t* __restrict__ packed, uint32_t* __restrict__ sz, int N,
@@ -38,14 +44,16 @@ quantize_w4_kernel(const f16* __restrict__ w, uint32_t* __restrict__ packed, uin
     lo = fminf(lo, __shfl_xor(lo, o, kWave));
     hi = fmaxf(hi, __shfl_xor(hi, o, kWave));
   }
-  const float step = fmaxf((hi - lo) / 15.0f, 1e-6f);
+  const float step = clamp_keep_sign((hi - lo) / 15.0f, 1e-6f, INFINITY);
   const f16 scale16 = (f16)step;
   const float scale = (float)scale16;
-  const float zero = fminf(fmaxf(rintf(-lo / scale), 0.0f), 15.0f);
+  // A group whose minimum is 0 (or a tiny positive value) gives rint(-min / scale) = -0.0, which the reference's
+  // clamp keeps: the stored zero point is then fp16 -0.0 (0x8000), reproduced bit for bit here.
+  const float zero = clamp_keep_sign(rintf(-lo / scale), 0.0f, 15.0f);
   uint32_t word = 0;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float qf = fminf(fmaxf(rintf(v[e] / scale) + zero, 0.0f), 15.0f);
+    const float qf = clamp_keep_sign(rintf(v[e] / scale) + zero, 0.0f, 15.0f);
     word |= (uint32_t)qf << (4 * (e >> 1) + 16 * (e & 1));
   }
   if (!live) return;

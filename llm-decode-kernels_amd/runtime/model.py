@@ -56,14 +56,18 @@ class DecodeConfig:
 
 
 def default_gemv_config(N, K):
-    """(stage, R, waves, pf) used when the tuning table has no entry for a shape: one wave per 64 sixteen-byte
-    columns of a row (so one column step per lane), and as many rows per workgroup as keep >= 2048 waves in flight."""
+    """(stage, R, waves, pf) used when the tuning table has no entry for a shape (mirrors gemv_default_config in
+    csrc/gemv_w4a16.hip): whole-row waves (stage 2, 2 rows per wave, 4 waves per workgroup, 4 steps in flight) while
+    N >= 4096 and x fits the LDS budget; otherwise split-K (stage 3) with one wave per 64 columns of 32 weights and as
+    many rows per workgroup as keep >= 2048 waves in flight."""
     U = K // 32
+    if N >= 4096 and K <= 32768:
+        return (2, 2, 4, 2 if U > 64 else 0)
     waves = min(16, (U + 63) // 64)
     R = 4
     while R > 1 and ((N + R - 1) // R) * waves < 2048:
         R //= 2
-    return (2, R, waves, 1 if U > 64 * waves else 0)
+    return (3, R, waves, 1 if U > 64 * waves else 0)
 
 
 class Linear:
@@ -192,7 +196,9 @@ class Model:
         if self.cfg.gemv_stage is not None:
             return self.cfg.gemv_stage
         e = self.gemv_table.get(f"{lin.N}x{lin.K}_G{self.cfg.group}")
-        return (2, *e) if e else default_gemv_config(lin.N, lin.K)
+        if e is None:
+            return default_gemv_config(lin.N, lin.K)
+        return tuple(e) if len(e) == 4 else (2, *e)      # [R, warps, pf] is the reference's stage-2 schema
 
     def linear(self, lin: Linear, x, y):
         if lin.quant:

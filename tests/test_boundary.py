@@ -56,7 +56,9 @@ def _err(lib, rc):
     ((0, 3, 0, 0, A16, A16, A16, A16, 4, 128, 128), 4, "R must be 1,2,4,8"),
     ((4, 1, 0, 0, A16, A16, A16, A16, 4, 128, 128), 4, "stage"),
     ((2, 1, 17, 0, A16, A16, A16, A16, 4, 128, 128), 4, "warps"),
-    ((2, 1, 0, 2, A16, A16, A16, A16, 4, 128, 128), 4, "pf"),
+    ((2, 1, 0, 4, A16, A16, A16, A16, 4, 128, 128), 4, "pf must be 0..3"),
+    ((3, 1, 0, 2, A16, A16, A16, A16, 4, 128, 128), 4, "pf must be 0 or 1"),
+    ((2, 1, 0, 0, A16, A16, A16, A16, 4, 32800, 32), 3, "K <= 32768"),
     ((2, 1, 0, 0, A16, A16, A16, A16, 4, 100, 128), 3, "multiple of 32"),
     ((2, 1, 0, 0, A16, A16, A16, A16, 4, 128, 256), 3, "multiple of 32 and of the group size"),
     ((2, 1, 0, 0, A16, A16, A16, A16, 4, 192, 96), 4, "group must be a power of two"),
