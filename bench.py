@@ -1,18 +1,28 @@
 #!/usr/bin/env python3
-"""Benchmark of the batch-1 W4A16 decode hot path on one MI355X; prints ONE JSON line.
+"""Benchmark of the batch-1 W4A16 decode hot path on one MI355X; prints ONE JSON line on stdout.
 
-Workload: TinyLlama-1.1B-architecture decode step, random init W ~ N(0, 0.02) quantized W4A16
-group 128 on the GPU, 22 layers, hidden 2048, 32 q / 4 kv heads, head_dim 64, SwiGLU 5632, vocab 32000 fp16 LM head,
-batch 1, paged KV (page 16), the whole step captured as one hipGraph and replayed per token. A "step" is one token.
-`value` = tokens/s over the K timed replays starting at context --ctx (default 512), bracketed by device syncs.
+value: BASELINE config 4, the TinyLlama-1.1B-architecture decode step (random init W ~ N(0, 0.02) quantized W4A16
+group 128 on the GPU; 22 layers, hidden 2048, 32 q / 4 kv heads, head_dim 64, SwiGLU 5632, vocab 32000, fp16 LM
+head; batch 1; paged KV, page 16), the whole step captured as one hipGraph and replayed once per token. A "step" is
+one token. Timed: K replays starting at context --ctx (default 512) after W warm-up replays, bracketed by device
+syncs; value = K / elapsed (tokens/s).
 
-Also measured in the same run:
-  * roofline of the dominant kernel, the W4A16 GEMV, at the BASELINE target shape 4096 x 14336 (G128): algorithmic
-    bytes per launch (packed + scale/zero + x + y = 31,232,000 B) / mean launch duration from HIP events on the launch
-    stream, weights rotated over enough copies (> 1 GiB) that every launch reads from HBM, not L2 or the MALL;
-  * the 14336 x 4096 GEMV the same way, and the decode step against its bytes-per-token roofline;
-  * cpu_baseline: the CPU oracle's decode step (oracle.decode_ref, the reference's backend="ref" composition on the
-    host cores, torch fp32 matvec) on the same weights, a bounded sample of tokens.
+Also measured in the same run (extra keys of the JSON line):
+  roofline      the dominant kernel, the W4A16 GEMV, at BASELINE's target shape 4096 x 14336 G128 with its tuned
+                configuration: algorithmic bytes per launch (packed + scale/zero + x + y = 31,232,000 B) / mean launch
+                duration. The duration comes from HIP events around a hipGraph of back-to-back launches on the
+                capture stream, each launch reading a different cold copy of the weights (> 2.5 x the 256 MB MALL),
+                so every byte comes from HBM. `traffic` is the HBM bytes per launch measured by rocprofv3 PMC
+                (FETCH_SIZE + WRITE_SIZE, scaled by a plain read / copy of known size) when that summary is present
+                in profiles/, else null.
+  gemv_14336x4096, gemv_cfg1   the other BASELINE GEMV shapes the same way;
+  read_ceiling  the library's bw_read streaming the same number of bytes: what a kernel that only reads gets;
+  decode        per-token statistics, the bytes-per-token roofline of the step, ctx 2048 as well;
+  cpu_baseline  the CPU oracle's decode step (oracle.decode_ref: the reference backend="ref" composition, torch fp32
+                matvec) on the host cores, a bounded sample of tokens on the same weights.
+
+--gpus N > 1 exits with a message: the path is single-GPU by design (one GPU per box here).
+--leg gemv runs only the GEMV roofline leg (used under rocprofv3 for the kernel trace and counter passes).
 """
 import argparse
 import json
@@ -29,43 +39,78 @@ for _p in (str(ROOT), str(ROOT / "llm-decode-kernels_amd")):
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "W4A16 GEMV HBM GB/s (% of peak) + batch-1 decode tokens/s, TinyLlama shape"
+PMC_SUMMARY = ROOT / "profiles" / "gemv_w4a16_4096x14336_pmc.json"
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def gemv_leg(K, N, Kd, G=128, iters=60, copies=None):
-    """Mean / median per-launch duration (us) of the configured W4A16 GEMV with cold weights."""
-    import torch
-    from oracle import quant_ref as Q
-    from runtime.model import default_gemv_config
-    from runtime.quant import quantize_pack
+def tuned_config(N, K, G=128):
+    from runtime.model import DecodeConfig, default_gemv_config
+    p = pathlib.Path(DecodeConfig().autotune_path)
+    best = json.load(open(p)).get("best", {}) if p.exists() else {}
+    e = best.get(f"{N}x{K}_G{G}")
+    if e is None:
+        return default_gemv_config(N, K)
+    return tuple(e) if len(e) == 4 else (2, *e)
 
-    nbytes = Q.gemv_bytes(N, Kd, G)
-    copies = copies or max(4, int((1.25 * 2 ** 30) // nbytes) + 1)
-    g = torch.Generator(device="cuda").manual_seed(N + Kd)
-    w = torch.randn(N, Kd, generator=g, device="cuda") * 0.02
-    packed, sz = quantize_pack(w.half(), G)
-    del w
-    ws = [(packed.clone(), sz.clone()) for _ in range(copies)]
+
+def gemv_leg(Kx, N, Kd, G=128, reps=7):
+    """Mean per-launch duration of the tuned W4A16 GEMV with cold weights (hipGraph of back-to-back launches)."""
+    import torch
+    from runtime.autotune import gemv_bytes
+    from runtime.quant import quantize_pack
+    from runtime.timing import ColdCopies, graph_time, n_copies
+
+    nbytes = gemv_bytes(N, Kd, G)
+    g = torch.Generator(device="cuda").manual_seed(N * 7 + Kd)
+    packed, sz = quantize_pack((torch.randn(N, Kd, generator=g, device="cuda") * 0.02).half(), G)
     x = torch.randn(Kd, generator=g, device="cuda").half()
     y = torch.empty(N, dtype=torch.half, device="cuda")
-    cfg = default_gemv_config(N, Kd)
-    for i in range(copies):
-        K.gemv_w4a16(*cfg, ws[i][0], ws[i][1], x, y, G)
+    cfg = tuned_config(N, Kd, G)
+    cold = ColdCopies([packed, sz], n_copies(nbytes))
+    mn, med = graph_time(lambda i: Kx.gemv_w4a16(*cfg, *cold[i], x, y, G), cold.copies, reps)
+    launches = cold.copies * (reps + 2)
+    del cold
+    return {"N": N, "K": Kd, "group": G, "cfg": list(cfg), "bytes": nbytes, "mean_us": round(med, 3),
+            "min_us": round(mn, 3), "gbps": round(nbytes / med / 1e3, 1), "frac": round(nbytes / med / 1e3 / HBM_PEAK_GBS, 4),
+            "launches": launches}
+
+
+def read_ceiling_leg(Kx, nbytes, reps=5):
+    """Best bw_read time for the same byte count, cold (what a read-only kernel achieves at this size)."""
+    import torch
+    from runtime.timing import ColdCopies, graph_time, n_copies
+    src = torch.empty(nbytes // 16 * 16, dtype=torch.uint8, device="cuda")
+    cold = ColdCopies([src], n_copies(nbytes))
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    best = None
+    for blocks, threads in ((nbytes // 16 // 512, 512), (nbytes // 16 // 256, 256)):
+        mn, med = graph_time(lambda i: Kx.bw_read(cold[i][0], sink, blocks, threads, 1), cold.copies, reps)
+        if best is None or med < best[0]:
+            best = (med, blocks, threads)
+    del cold
+    return {"bytes": nbytes, "mean_us": round(best[0], 3), "gbps": round(nbytes / best[0] / 1e3, 1),
+            "frac": round(nbytes / best[0] / 1e3 / HBM_PEAK_GBS, 4), "grid": [best[1], best[2]]}
+
+
+def calibration_leg(Kx, nbytes, n=16):
+    """Known-size kernels for scaling hardware byte counters: n bw_read launches that each read `nbytes` once
+    (cold copies) and n device copies of `nbytes` (read + write once). Their FETCH_SIZE / WRITE_SIZE per dispatch,
+    divided by nbytes, are the counter-to-HBM-bytes factors (runtime.rocprof_summary)."""
+    import torch
+    from runtime.timing import ColdCopies
+    src = torch.empty(nbytes // 16 * 16, dtype=torch.uint8, device="cuda")
+    cold = ColdCopies([src], n + 1)
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    for i in range(n):
+        Kx.bw_read(cold[i][0], sink, nbytes // 16 // 512, 512, 1)
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
-    for i, (s, e) in enumerate(ev):
-        p, z = ws[i % copies]
-        s.record()
-        K.gemv_w4a16(*cfg, p, z, x, y, G)
-        e.record()
+    for i in range(n):
+        cold[i + 1][0].copy_(cold[i][0])
     torch.cuda.synchronize()
-    t = [s.elapsed_time(e) * 1e3 for s, e in ev]
-    return {"N": N, "K": Kd, "group": G, "cfg": list(cfg), "bytes": nbytes, "mean_us": statistics.mean(t),
-            "median_us": statistics.median(t), "min_us": min(t), "copies": copies,
-            "gbps_mean": nbytes / statistics.mean(t) / 1e3, "gbps_median": nbytes / statistics.median(t) / 1e3}
+    del cold
 
 
 def decode_leg(model, ctx, steps, warmup):
@@ -76,22 +121,25 @@ def decode_leg(model, ctx, steps, warmup):
     torch.cuda.synchronize()
     model.reset(ctx)
     per = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    start.record()
     for s, e in per:
         s.record()
         model.run_step()
         e.record()
+    end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    total_ms = start.elapsed_time(end)
     tok_us = sorted(s.elapsed_time(e) * 1e3 for s, e in per)
-    total_us = sum(tok_us)
-    return {"ctx_start": ctx, "steps": steps, "ms_per_step": total_us / steps / 1e3, "tok_s": steps / (total_us / 1e6),
+    return {"ctx_start": ctx, "steps": steps, "ms_per_step": total_ms / steps, "tok_s": steps / (total_ms / 1e3),
             "median_us": statistics.median(tok_us), "p10_us": tok_us[len(tok_us) // 10],
             "p90_us": tok_us[(9 * len(tok_us)) // 10], "wall_tok_s": steps / wall}
 
 
-def cpu_baseline_leg(model, shape, ctx, budget_s=20.0, max_tokens=8):
+def cpu_baseline_leg(model, shape, ctx, budget_s=15.0, max_tokens=64):
     """Tokens/s of the CPU oracle decode step on the host cores (a bounded sample)."""
     import torch
     from __graft_entry__ import _ref_weights
@@ -99,17 +147,18 @@ def cpu_baseline_leg(model, shape, ctx, budget_s=20.0, max_tokens=8):
 
     cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     torch.set_num_threads(cores)
-    dec = RefDecoder(_ref_weights(model, shape), shape, max_ctx=ctx + max_tokens + 2, page=model.cfg.page,
-                     block_table=torch.arange((ctx + max_tokens + 2) // model.cfg.page + 2, dtype=torch.int32))
-    dec.step(1, ctx)                                   # warm-up (first-touch of the weights)
+    cap = ctx + max_tokens + 2
+    dec = RefDecoder(_ref_weights(model, shape), shape, max_ctx=cap, page=model.cfg.page,
+                     block_table=torch.arange(cap // model.cfg.page + 2, dtype=torch.int32))
+    dec.step(1, ctx)                                   # warm-up (first touch of the weights)
     n, t0 = 0, time.perf_counter()
     while n < max_tokens and (time.perf_counter() - t0) < budget_s:
         dec.step(1 + n, ctx + 1 + n)
         n += 1
     dt = time.perf_counter() - t0
-    return {"value": n / dt, "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"{n} TinyLlama decode steps of oracle.decode_ref (torch fp32 CPU, reference backend='ref' "
-                      f"composition) at ctx {ctx}, after 1 warm-up step, {dt:.1f} s"}
+    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"{n} TinyLlama decode steps of oracle.decode_ref (torch fp32 CPU restatement of the reference "
+                      f"backend='ref' composition) at ctx {ctx}, after 1 warm-up step, {dt:.1f} s"}
 
 
 def main():
@@ -118,60 +167,80 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--ctx", type=int, default=512)
+    ap.add_argument("--leg", choices=("all", "gemv"), default="all")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline leg")
-    ap.add_argument("--gemv-iters", type=int, default=60)
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print(f"bench.py measures one GPU only (the batch-1 decode path is single-GPU by design); got --gpus {a.gpus}",
-              file=sys.stderr)
+        print(f"bench.py measures one GPU only: the batch-1 decode path is single-GPU by design and every box here "
+              f"has one GPU (got --gpus {a.gpus}); see DESIGN.md for how the path would shard", file=sys.stderr)
         sys.exit(2)
 
     import torch
     from runtime import ext
+
+    Kx = ext.load()
+    dev_name = torch.cuda.get_device_properties(0).name
+    if a.leg == "gemv":
+        g1 = gemv_leg(Kx, 4096, 14336)
+        log(f"gemv 4096x14336 {g1['cfg']}: {g1['mean_us']:.3f} us/launch -> {g1['gbps']:.0f} GB/s ({g1['frac']:.1%})")
+        calibration_leg(Kx, g1["bytes"])
+        print(json.dumps({"leg": "gemv", "gemv_4096x14336": g1}), flush=True)
+        return
+
     from runtime.model import DecodeConfig, Model
     from runtime.synth import TINYLLAMA, SyntheticLlama
 
-    K = ext.load()
-    dev_name = torch.cuda.get_device_properties(0).name
     log(f"device {dev_name}; building TinyLlama-shape W4A16 model")
     t0 = time.perf_counter()
-    cap = a.ctx + a.steps + a.warmup + 16
-    cfg = DecodeConfig(lm_head="fp16", max_ctx=cap)
-    model = Model(SyntheticLlama(TINYLLAMA, seed=0), TINYLLAMA, cfg)
-    model.prepare(cap)
+    cap = max(2048, a.ctx) + a.steps + a.warmup + 16
+    model = Model(SyntheticLlama(TINYLLAMA, seed=0), TINYLLAMA, DecodeConfig(lm_head="fp16", max_ctx=cap))
+    model.prepare(a.ctx + a.steps + a.warmup + 16)
     log(f"model built + graph captured in {time.perf_counter() - t0:.1f}s (part_size {model.part_size}, "
         f"max_splits {model.max_splits})")
-
     dec = decode_leg(model, a.ctx, a.steps, a.warmup)
-    log(f"decode: {dec['tok_s']:.1f} tok/s, median {dec['median_us']:.1f} us/token")
+    log(f"decode ctx {a.ctx}: {dec['tok_s']:.1f} tok/s, median {dec['median_us']:.1f} us/token")
     bpt = model.bytes_per_token(a.ctx + a.steps // 2)
-    g1 = gemv_leg(K, 4096, 14336, iters=a.gemv_iters)
-    log(f"gemv 4096x14336: mean {g1['mean_us']:.2f} us -> {g1['gbps_mean']:.0f} GB/s")
-    g2 = gemv_leg(K, 14336, 4096, iters=a.gemv_iters)
-    log(f"gemv 14336x4096: mean {g2['mean_us']:.2f} us -> {g2['gbps_mean']:.0f} GB/s")
+    model.prepare(2048 + 64 + 16)
+    dec2k = decode_leg(model, 2048, 64, 8)
+    log(f"decode ctx 2048: {dec2k['tok_s']:.1f} tok/s")
+    bpt2k = model.bytes_per_token(2048 + 32)
+
+    g1 = gemv_leg(Kx, 4096, 14336)
+    log(f"gemv 4096x14336 {g1['cfg']}: {g1['mean_us']:.3f} us/launch -> {g1['gbps']:.0f} GB/s ({g1['frac']:.1%})")
+    g2 = gemv_leg(Kx, 14336, 4096)
+    log(f"gemv 14336x4096 {g2['cfg']}: {g2['mean_us']:.3f} us/launch -> {g2['gbps']:.0f} GB/s ({g2['frac']:.1%})")
+    g3 = gemv_leg(Kx, 5632, 2048)
+    log(f"gemv 5632x2048 {g3['cfg']}: {g3['mean_us']:.3f} us/launch -> {g3['gbps']:.0f} GB/s ({g3['frac']:.1%})")
+    rc = read_ceiling_leg(Kx, g1["bytes"])
+    log(f"bw_read of {rc['bytes']} B: {rc['mean_us']:.3f} us -> {rc['gbps']:.0f} GB/s ({rc['frac']:.1%})")
+
     cpu = None
     if not a.no_cpu:
         cpu = cpu_baseline_leg(model, TINYLLAMA, a.ctx)
         log(f"cpu baseline: {cpu['value']:.3f} tok/s on {cpu['cores']} cores")
 
+    traffic = None
+    if PMC_SUMMARY.exists():
+        traffic = json.load(open(PMC_SUMMARY)).get("hbm_bytes_per_launch")
+
     out = {
         "metric": METRIC, "value": round(dec["tok_s"], 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(dec["ms_per_step"], 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "w4a16 (fp16 activations, fp32 accumulate)",
+        "scaling": "weak", "vs_baseline": None, "dtype": "w4a16 (int4 weights, fp16 activations, fp32 accumulate)",
         "data": "synthetic (random-init weights N(0,0.02), random token ids)",
-        "config": {"workload": "TinyLlama-1.1B-shape W4A16 G128 decode step, fp16 LM head, hipGraph replay",
-                   "model": "TinyLlama-1.1B architecture", "global_batch": 1, "seq_len": a.ctx,
+        "config": {"workload": "TinyLlama-1.1B-architecture W4A16 G128 decode step (BASELINE config 4), fp16 LM head, "
+                               "hipGraph replay, batch 1", "context_start": a.ctx, "global_batch": 1,
                    "parallelism": "single GPU", "device": dev_name},
-        "roofline": {"bound": "hbm", "kernel": f"W4A16 GEMV 4096x14336 G128 cfg {g1['cfg']}",
-                     "achieved": round(g1["gbps_mean"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(g1["gbps_mean"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_launch": g1["bytes"], "mean_us": round(g1["mean_us"], 3),
-                     "median_us": round(g1["median_us"], 3)},
-        "gemv_14336x4096": {"mean_us": round(g2["mean_us"], 3), "gbps": round(g2["gbps_mean"], 1),
-                            "frac": round(g2["gbps_mean"] / HBM_PEAK_GBS, 4), "cfg": g2["cfg"]},
+        "roofline": {"bound": "hbm", "kernel": f"gemv_w4a16 4096x14336 G128 cfg {g1['cfg']}",
+                     "achieved": g1["gbps"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": g1["frac"],
+                     "traffic": traffic, "bytes_per_launch": g1["bytes"], "mean_us": g1["mean_us"],
+                     "read_ceiling_frac": rc["frac"]},
+        "gemv_14336x4096": g2, "gemv_cfg1_5632x2048": g3, "read_ceiling": rc,
         "decode": {**{k: round(v, 3) if isinstance(v, float) else v for k, v in dec.items()},
                    "bytes_per_token": bpt, "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / bpt, 1),
                    "frac_of_roofline": round(dec["tok_s"] / (HBM_PEAK_GBS * 1e9 / bpt), 4)},
+        "decode_ctx2048": {"tok_s": round(dec2k["tok_s"], 2), "median_us": round(dec2k["median_us"], 2),
+                           "bytes_per_token": bpt2k, "frac_of_roofline": round(dec2k["tok_s"] / (HBM_PEAK_GBS * 1e9 / bpt2k), 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

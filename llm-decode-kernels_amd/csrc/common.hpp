@@ -45,6 +45,26 @@ __device__ __forceinline__ float strided_max(float v) {
   return v;
 }
 
+// Full-wave sum through DPP (no LDS traffic, a few cycles per step): quad_perm [1,0,3,2] and [2,3,0,1] sum the quad,
+// row_half_mirror and row_mirror the 16-lane row, row_bcast15 into rows 1 and 3 and row_bcast31 into rows 2 and 3
+// carry the row sums upward. The total is valid in lane 63 only. Must be called with every lane of the wave active
+// (the DPP source of an inactive lane is not defined); select 0 for dead lanes before calling.
+#define DK_DPP_F32(v, ctrl, row_mask) \
+  __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), (ctrl), (row_mask), 0xF, false))
+__device__ __forceinline__ float wave_sum_lane63(float v) {
+  v += DK_DPP_F32(v, 0xB1, 0xF);   // quad_perm [1,0,3,2]
+  v += DK_DPP_F32(v, 0x4E, 0xF);   // quad_perm [2,3,0,1]
+  v += DK_DPP_F32(v, 0x141, 0xF);  // row_half_mirror
+  v += DK_DPP_F32(v, 0x140, 0xF);  // row_mirror
+  v += DK_DPP_F32(v, 0x142, 0xA);  // row_bcast15, rows 1 and 3
+  v += DK_DPP_F32(v, 0x143, 0xC);  // row_bcast31, rows 2 and 3
+  return v;
+}
+// Same sum, broadcast to every lane (v_readlane of lane 63 into a scalar register).
+__device__ __forceinline__ float wave_sum_all(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_lane63(v)), 63));
+}
+
 // fp32 dot of two fp16 pairs plus an fp32 accumulator (v_dot2_f32_f16).
 __device__ __forceinline__ float dot2(f16x2 a, f16x2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
 

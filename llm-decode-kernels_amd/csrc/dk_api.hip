@@ -53,13 +53,16 @@ int dk_runtime_version(void) {
 int dk_gemv_w4a16(int stage, int R, int warps, int pf, const void* packed, const void* sz, const void* x, void* y,
                   int N, int K, int group, void* stream) {
   if (!packed || !sz || !x || !y) return fail(DK_ERR_NULL, "gemv_w4a16: null pointer argument");
-  if (stage < 0 || stage > 3) return fail(DK_ERR_DOMAIN, "gemv_w4a16: stage must be 0..3, got %d", stage);
+  if (stage < 0 || stage > 4) return fail(DK_ERR_DOMAIN, "gemv_w4a16: stage must be 0..4, got %d", stage);
   if (R != 1 && R != 2 && R != 4 && R != 8) return fail(DK_ERR_DOMAIN, "gemv: R must be 1,2,4,8, got %d", R);
   if (warps < 0 || warps > 16) return fail(DK_ERR_DOMAIN, "gemv_w4a16: warps must be 0..16, got %d", warps);
   if (stage == 3 ? (pf != 0 && pf != 1) : (pf < 0 || pf > 3))
     return fail(DK_ERR_DOMAIN, "gemv_w4a16: pf must be %s for stage %d, got %d", stage == 3 ? "0 or 1" : "0..3",
                 stage, pf);
-  if ((stage == 1 || stage == 2) && K > dk::kGemvRowsMaxK)
+  if (stage == 4 && K > 0 && warps != 0 && warps * 2048 < K)
+    return fail(DK_ERR_SHAPE, "gemv_w4a16: stage 4 needs warps * 2048 >= K (one column per lane), got warps=%d K=%d",
+                warps, K);
+  if ((stage == 1 || stage == 2 || stage == 4) && K > dk::kGemvRowsMaxK)
     return fail(DK_ERR_SHAPE, "gemv_w4a16: stage %d stages x in LDS and needs K <= %d, got %d", stage,
                 dk::kGemvRowsMaxK, K);
   if (N <= 0 || K <= 0) return fail(DK_ERR_SHAPE, "gemv_w4a16: N and K must be positive (N=%d K=%d)", N, K);

@@ -27,6 +27,11 @@
 //                               the staging and no LDS reduction: each wave reduces its rows with lane shuffles.
 //   stage 3  gemv_w4a16_splitk  the workgroup's waves split K for R rows (x read through the cache), partial sums
 //                               reduced through LDS: for narrow N, where whole-row waves would leave CUs idle.
+//   stage 4  gemv_w4a16_tile    the workgroup's waves cover K once with a register-resident x slice per lane and
+//                               walk 2^pf tiles of R rows, the next tile's loads in flight while the current one is
+//                               computed; x is read once per workgroup, row sums by DPP within waves, LDS across.
+// The compiler's scheduler, left alone, issues only two of a tile's weight loads before it starts computing (it keeps
+// register pressure low); __builtin_amdgcn_sched_barrier pins every load of a step ahead of its arithmetic.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -161,28 +166,32 @@ gemv_w4a16_rows(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
   }
 
 #pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = group_sum<kWave>(acc[r]);
+  for (int r = 0; r < R; ++r) acc[r] = wave_sum_lane63(acc[r]);
+  if (lane == 63) {
 #pragma unroll
-  for (int r = 0; r < R; ++r)
-    if (lane == r && row0 + r < N) y[row0 + r] = (f16)acc[r];
+    for (int r = 0; r < R; ++r)
+      if (row0 + r < N) y[row0 + r] = (f16)acc[r];
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
 // Stage 3: split-K kernel, R rows per workgroup, blockDim.x = 64 * waves (waves <= 16); thread t takes columns
-// t, t + 64 * waves, ...; one prefetch step when PF.
+// t, t + 64 * waves, ... Per column the x words, the R weight words and the R (scale, zero) words are all requested
+// before any arithmetic (a scheduling barrier keeps the compiler from interleaving them), PF adds one more column of
+// loads in flight. Rows are reduced with DPP within each wave, then across waves through LDS.
 template <int R, bool PF>
 __global__ void __launch_bounds__(1024)
 gemv_w4a16_splitk(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, const u32x4* __restrict__ X,
                   f16* __restrict__ y, int N, int U, int gsh) {
   __shared__ float red[16][R];
-  const int t = threadIdx.x, nt = blockDim.x;
+  const int t = threadIdx.x, nt = blockDim.x, lane = t & 63, wave = t >> 6, nw = nt >> 6;
   const int row0 = blockIdx.x * R;
   const int NG = U >> gsh;
   const u32x4* wrow[R];
   const uint32_t* srow[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int rr = min(row0 + r, N - 1);
+    const int rr = min(row0 + r, N - 1);  // tail rows: clamp the loads, skip the store
     wrow[r] = W + (size_t)rr * U;
     srow[r] = SZ + (size_t)rr * NG;
   }
@@ -190,56 +199,67 @@ gemv_w4a16_splitk(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, 
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
 
-  int u = t;
-  u32x4 w[R];
-  uint32_t szw[R];
-  if (u < U) {
+  if constexpr (!PF) {
+    for (int u = t; u < U; u += nt) {
+      u32x4 xc[4], w[R];
+      uint32_t szw[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) w[r] = load_stream(wrow[r] + u);
+      for (int k = 0; k < 4; ++k) xc[k] = X[4 * u + k];
 #pragma unroll
-    for (int r = 0; r < R; ++r) szw[r] = srow[r][u >> gsh];
-  }
-  while (u < U) {
-    const u32x4* xp = X + 4 * u;
-    const u32x4 xc[4] = {xp[0], xp[1], xp[2], xp[3]};
-    const int un = u + nt;
-    if constexpr (PF) {
-      u32x4 wn[R];
+      for (int r = 0; r < R; ++r) w[r] = load_stream(wrow[r] + u);
+#pragma unroll
+      for (int r = 0; r < R; ++r) szw[r] = srow[r][u >> gsh];
+      __builtin_amdgcn_sched_barrier(0);
+      column_fma<R>(w, szw, xc, acc);
+    }
+  } else {
+    int u = t;
+    u32x4 xc[4], w[R];
+    uint32_t szw[R];
+    if (u < U) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) xc[k] = X[4 * u + k];
+#pragma unroll
+      for (int r = 0; r < R; ++r) w[r] = load_stream(wrow[r] + u);
+#pragma unroll
+      for (int r = 0; r < R; ++r) szw[r] = srow[r][u >> gsh];
+    }
+    while (u < U) {
+      const int un = u + nt;
+      u32x4 xn[4], wn[R];
       uint32_t szn[R];
       if (un < U) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) xn[k] = X[4 * un + k];
 #pragma unroll
         for (int r = 0; r < R; ++r) wn[r] = load_stream(wrow[r] + un);
 #pragma unroll
         for (int r = 0; r < R; ++r) szn[r] = srow[r][un >> gsh];
       }
+      __builtin_amdgcn_sched_barrier(0);
       column_fma<R>(w, szw, xc, acc);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) xc[k] = xn[k];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         w[r] = wn[r];
         szw[r] = szn[r];
       }
-    } else {
-      column_fma<R>(w, szw, xc, acc);
-      if (un < U) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) w[r] = load_stream(wrow[r] + un);
-#pragma unroll
-        for (int r = 0; r < R; ++r) szw[r] = srow[r][un >> gsh];
-      }
+      u = un;
     }
-    u = un;
   }
 
 #pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = group_sum<kWave>(acc[r]);
-  const int wave = t >> 6, lane = t & 63, nw = nt >> 6;
+  for (int r = 0; r < R; ++r) acc[r] = wave_sum_lane63(acc[r]);
   if (nw == 1) {
+    if (lane == 63) {
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-      if (lane == r && row0 + r < N) y[row0 + r] = (f16)acc[r];
+      for (int r = 0; r < R; ++r)
+        if (row0 + r < N) y[row0 + r] = (f16)acc[r];
+    }
     return;
   }
-  if (lane == 0) {
+  if (lane == 63) {
 #pragma unroll
     for (int r = 0; r < R; ++r) red[wave][r] = acc[r];
   }
@@ -248,6 +268,99 @@ gemv_w4a16_splitk(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, 
     float v = 0.f;
     for (int i = 0; i < nw; ++i) v += red[i][t];
     y[row0 + t] = (f16)v;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Stage 4: row tiles with a stationary x slice. The workgroup's waves cover K once: lane l of wave v owns column
+// u = 64 v + l (so U <= 64 * waves) and loads its 32 x values once into registers. The workgroup walks NT tiles of T
+// consecutive rows; for each tile every lane requests its column of all T rows at once (T 16-byte loads + T scale /
+// zero words), and the loads of tile t + 1 are issued before tile t is computed (double buffering, pinned by
+// scheduling barriers so the compiler cannot serialise them). Each row partial is summed over the wave with DPP and
+// the waves meet in LDS; T * NT threads finish the rows and store them.
+template <int T>
+__device__ __forceinline__ void tile_issue(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, int row0,
+                                           int N, int U, int NG, int uc, int gsh, u32x4 (&w)[T], uint32_t (&s)[T]) {
+#pragma unroll
+  for (int r = 0; r < T; ++r) w[r] = load_stream(W + (size_t)min(row0 + r, N - 1) * U + uc);
+#pragma unroll
+  for (int r = 0; r < T; ++r) s[r] = SZ[(size_t)min(row0 + r, N - 1) * NG + (uc >> gsh)];
+}
+
+template <int T>
+__device__ __forceinline__ void tile_rows(const u32x4 (&w)[T], const uint32_t (&s)[T], const u32x4 (&xc)[4], float SA,
+                                          float SB, bool live, float (&v)[T]) {
+#pragma unroll
+  for (int r = 0; r < T; ++r) {
+    float dA = 0.f, dB = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t lo = w[r][k], hi = lo >> 8;
+      dA = dot2(as_f16x2((lo & kLoMask) | kMagic), as_f16x2(xc[k].x), dA);
+      dB = dot2(as_f16x2((lo & kHiMask) | kMagic), as_f16x2(xc[k].y), dB);
+      dA = dot2(as_f16x2((hi & kLoMask) | kMagic), as_f16x2(xc[k].z), dA);
+      dB = dot2(as_f16x2((hi & kHiMask) | kMagic), as_f16x2(xc[k].w), dB);
+    }
+    const f16x2 sz = as_f16x2(s[r]);
+    const float sc = (float)sz.x, z = (float)sz.y;
+    float c = fmaf(dB, 0.0625f, dA);
+    c = fmaf(-(1024.f + z), SA, c);
+    c = fmaf(-(64.f + z), SB, c);
+    const float part = live ? sc * c : 0.f;  // dead lanes (u >= U) contribute 0; the DPP sum runs on all lanes
+    v[r] = wave_sum_lane63(part);
+  }
+}
+
+template <int T, int NT>
+__global__ void __launch_bounds__(1024)
+gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, const u32x4* __restrict__ X,
+                f16* __restrict__ y, int N, int U, int gsh) {
+  __shared__ float red[16][T * NT];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+  const int u = wave * kWave + lane;
+  const bool live = u < U;
+  const int uc = live ? u : U - 1;  // dead lanes load a valid column and contribute 0
+  const int base = blockIdx.x * T * NT;
+  const int NG = U >> gsh;
+
+  u32x4 xc[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) xc[k] = X[4 * uc + k];
+  u32x4 wa[T], wb[T];
+  uint32_t sa[T], sb[T];
+  tile_issue<T>(W, SZ, base, N, U, NG, uc, gsh, wa, sa);
+  __builtin_amdgcn_sched_barrier(0);
+  const f16x2 one = {(f16)1.0f, (f16)1.0f};
+  float SA = 0.f, SB = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    SA = dot2(as_f16x2(xc[k].x), one, SA);
+    SA = dot2(as_f16x2(xc[k].z), one, SA);
+    SB = dot2(as_f16x2(xc[k].y), one, SB);
+    SB = dot2(as_f16x2(xc[k].w), one, SB);
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    float v[T];
+    if ((t & 1) == 0) {
+      if (t + 1 < NT) tile_issue<T>(W, SZ, base + (t + 1) * T, N, U, NG, uc, gsh, wb, sb);
+      __builtin_amdgcn_sched_barrier(0);
+      tile_rows<T>(wa, sa, xc, SA, SB, live, v);
+    } else {
+      if (t + 1 < NT) tile_issue<T>(W, SZ, base + (t + 1) * T, N, U, NG, uc, gsh, wa, sa);
+      __builtin_amdgcn_sched_barrier(0);
+      tile_rows<T>(wb, sb, xc, SA, SB, live, v);
+    }
+    if (lane == 63) {
+#pragma unroll
+      for (int r = 0; r < T; ++r) red[wave][t * T + r] = v[r];
+    }
+  }
+  __syncthreads();
+  if (tid < T * NT && base + tid < N) {
+    float acc = 0.f;
+    for (int i = 0; i < nw; ++i) acc += red[i][tid];
+    y[base + tid] = (f16)acc;
   }
 }
 
@@ -278,6 +391,26 @@ void launch_rows_p(int waves, int pf, const void* packed, const void* sz, const 
   launch_rows<R, 1>(waves, packed, sz, x, y, N, K, log2G, st);
 }
 
+template <int T, int NT>
+void launch_tile_nt(const void* packed, const void* sz, const void* x, void* y, int N, int K, int log2G,
+                    hipStream_t st) {
+  const int U = K >> 5;
+  const int waves = (U + 63) / 64;
+  hipLaunchKernelGGL((gemv_w4a16_tile<T, NT>), dim3((N + T * NT - 1) / (T * NT)), dim3(64 * waves), 0, st,
+                     (const u32x4*)packed, (const uint32_t*)sz, (const u32x4*)x, (f16*)y, N, U, log2G - 5);
+}
+
+template <int T>
+void launch_tile(int pf, const void* packed, const void* sz, const void* x, void* y, int N, int K, int log2G,
+                 hipStream_t st) {
+  switch (pf) {
+    case 0: launch_tile_nt<T, 1>(packed, sz, x, y, N, K, log2G, st); break;
+    case 1: launch_tile_nt<T, 2>(packed, sz, x, y, N, K, log2G, st); break;
+    case 2: launch_tile_nt<T, 4>(packed, sz, x, y, N, K, log2G, st); break;
+    default: launch_tile_nt<T, 8>(packed, sz, x, y, N, K, log2G, st); break;
+  }
+}
+
 template <int R>
 void launch_splitk(int waves, int pf, const void* packed, const void* sz, const void* x, void* y, int N, int K,
                    int log2G, hipStream_t st) {
@@ -295,24 +428,19 @@ void launch_splitk(int waves, int pf, const void* packed, const void* sz, const 
 }  // namespace
 
 void gemv_default_config(int N, int K, int* stage, int* R, int* waves, int* pf) {
-  // Whole-row waves (stage 2) while they give at least ~8 waves per CU (2048 waves on 256 CUs) and x fits the LDS
-  // budget; split-K (stage 3) below that, so that narrow outputs still fill the chip.
-  const int U = K >> 5;
-  if (N >= 4096 && K <= kGemvRowsMaxK) {
-    *stage = 2;
+  // Row tiles of 2 rows, one tile per workgroup, while the workgroup can cover K (K <= 32768); split-K beyond.
+  (void)N;
+  if (K <= kGemvRowsMaxK) {
+    *stage = 4;
     *R = 2;
-    *waves = 4;
-    *pf = U > 64 ? 2 : 0;
+    *waves = 0;
+    *pf = 0;
     return;
   }
-  int w = (U + 63) / 64;
-  if (w > 16) w = 16;
-  int r = 4;
-  while (r > 1 && (long long)((N + r - 1) / r) * w < 2048) r >>= 1;
   *stage = 3;
-  *R = r;
-  *waves = w;
-  *pf = (U > 64 * w) ? 1 : 0;
+  *R = 2;
+  *waves = 16;
+  *pf = 1;
 }
 
 void launch_gemv_w4a16(int stage, int R, int waves, int pf, const void* packed, const void* sz, const void* x,
@@ -324,6 +452,15 @@ void launch_gemv_w4a16(int stage, int R, int waves, int pf, const void* packed, 
     return;
   }
   if (waves <= 0) waves = stage == 3 ? min(16, ((K >> 5) + 63) / 64) : 4;
+  if (stage == 4) {
+    switch (R) {
+      case 1: launch_tile<1>(pf, packed, sz, x, y, N, K, log2G, st); break;
+      case 2: launch_tile<2>(pf, packed, sz, x, y, N, K, log2G, st); break;
+      case 4: launch_tile<4>(pf, packed, sz, x, y, N, K, log2G, st); break;
+      default: launch_tile<8>(pf, packed, sz, x, y, N, K, log2G, st); break;
+    }
+    return;
+  }
   if (stage == 1) R = 1;
   if (stage == 1 || stage == 2) {
     switch (R) {

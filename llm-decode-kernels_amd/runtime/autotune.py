@@ -1,7 +1,8 @@
 """Per-shape W4A16 GEMV tuner for MI355X (the role of the reference's scripts/autotune.py:27-54).
 
 For every (N, K, group) shape, sweeps the kernel family of libdk_amd (stage 2: whole-row waves, R rows per wave x
-waves per workgroup x 2^pf steps in flight; stage 3: split-K, R rows per workgroup x waves x one-step prefetch) with
+waves per workgroup x 2^pf steps in flight; stage 3: split-K, R rows per workgroup x waves x one-step prefetch;
+stage 4: 2^pf row tiles of R rows over a workgroup that covers K once) with
 cold weights (runtime.timing), and writes
 
     configs/autotune.json   {"device": ..., "best": {"NxK_G": [stage, R, warps, pf]}, "us": {"NxK_G": us},
@@ -52,6 +53,8 @@ def candidates(N, K):
                 if pf and U <= 64 * w:
                     continue
                 out.append((3, R, w, pf))
+    if K <= 32768:
+        out += [(4, R, 0, pf) for R in (1, 2, 4, 8) for pf in range(4)]
     return [c for c in out if not (c[0] == 2 and K > 32768)]
 
 

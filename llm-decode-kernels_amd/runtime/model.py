@@ -57,17 +57,11 @@ class DecodeConfig:
 
 def default_gemv_config(N, K):
     """(stage, R, waves, pf) used when the tuning table has no entry for a shape (mirrors gemv_default_config in
-    csrc/gemv_w4a16.hip): whole-row waves (stage 2, 2 rows per wave, 4 waves per workgroup, 4 steps in flight) while
-    N >= 4096 and x fits the LDS budget; otherwise split-K (stage 3) with one wave per 64 columns of 32 weights and as
-    many rows per workgroup as keep >= 2048 waves in flight."""
-    U = K // 32
-    if N >= 4096 and K <= 32768:
-        return (2, 2, 4, 2 if U > 64 else 0)
-    waves = min(16, (U + 63) // 64)
-    R = 4
-    while R > 1 and ((N + R - 1) // R) * waves < 2048:
-        R //= 2
-    return (3, R, waves, 1 if U > 64 * waves else 0)
+    csrc/gemv_w4a16.hip): row tiles of 2 rows, one tile per workgroup (stage 4) while a workgroup can cover K
+    (K <= 32768), split-K (stage 3) beyond."""
+    if K <= 32768:
+        return (4, 2, 0, 0)
+    return (3, 2, 16, 1)
 
 
 class Linear:

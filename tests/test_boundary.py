@@ -54,7 +54,10 @@ def _err(lib, rc):
 
 @pytest.mark.parametrize("args,code,msg", [
     ((0, 3, 0, 0, A16, A16, A16, A16, 4, 128, 128), 4, "R must be 1,2,4,8"),
-    ((4, 1, 0, 0, A16, A16, A16, A16, 4, 128, 128), 4, "stage"),
+    ((5, 1, 0, 0, A16, A16, A16, A16, 4, 128, 128), 4, "stage"),
+    ((4, 16, 0, 0, A16, A16, A16, A16, 4, 128, 128), 4, "R must be 1,2,4,8"),
+    ((4, 4, 0, 4, A16, A16, A16, A16, 4, 128, 128), 4, "pf must be 0..3"),
+    ((4, 4, 2, 0, A16, A16, A16, A16, 4, 8192, 128), 3, "warps * 2048 >= K"),
     ((2, 1, 17, 0, A16, A16, A16, A16, 4, 128, 128), 4, "warps"),
     ((2, 1, 0, 4, A16, A16, A16, A16, 4, 128, 128), 4, "pf must be 0..3"),
     ((3, 1, 0, 2, A16, A16, A16, A16, 4, 128, 128), 4, "pf must be 0 or 1"),

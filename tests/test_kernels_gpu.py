@@ -33,7 +33,8 @@ def K():
 # prefetch depth, and the split-K kernel over rows x waves x prefetch
 GEMV_CFGS = [(0, 1, 4, 0), (0, 1, 1, 0), (1, 1, 0, 0), (1, 1, 4, 3)] + \
             [(2, r, w, pf) for r in (1, 2, 4, 8) for w in (1, 4) for pf in (0, 1, 2, 3)] + \
-            [(3, r, w, pf) for r in (1, 2, 4, 8) for w in (0, 1, 4) for pf in (0, 1)]
+            [(3, r, w, pf) for r in (1, 2, 4, 8) for w in (0, 1, 4) for pf in (0, 1)] + \
+            [(4, r, 0, pf) for r in (1, 2, 4, 8) for pf in (0, 1, 2, 3)] + [(4, 4, 16, 1)]
 
 
 def gemv(K, cfg, packed, sz, x, N, group):
@@ -89,7 +90,8 @@ def test_gemv_real_shapes(K, name, G):
     ref = R.gemv_ref(wref, x)
     xd = x.to(DEV)
     cfgs = GEMV_CFGS if (G == 128 and name in SHAPES) else [(0, 1, 4, 0), (1, 1, 0, 0), (2, 4, 0, 0), (2, 8, 2, 1),
-                                                           (2, 2, 1, 3), (3, 4, 0, 0), (3, 2, 1, 1)]
+                                                           (2, 2, 1, 3), (3, 4, 0, 0), (3, 2, 1, 1), (4, 2, 0, 0),
+                                                           (4, 8, 0, 3)]
     from runtime.model import default_gemv_config
     cfgs = cfgs + [default_gemv_config(N, Kd)]
     for cfg in cfgs:
