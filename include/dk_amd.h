@@ -77,13 +77,29 @@ int dk_bw_read(const void* buf, size_t bytes, void* sink, int blocks, int thread
  * writes unnormalized o and its (m, l) and a combine kernel merges them with the log-sum-exp rule.
  * head_dim in {64, 128}; n_q / n_kv in {1, 2, 4, 8}; page a power of two; version in {1, 2, 3} (accepted for
  * signature compatibility; every version runs the same kernel). Context is clamped to n_bt * page (tokens without a
- * block-table entry do not exist); a block-table entry outside [0, n_pages) masks its tokens. softmax scale
- * 1/sqrt(head_dim).
+ * block-table entry do not exist); a block-table entry outside [0, n_pages) masks its tokens; tokens past
+ * max_splits * part_size are not attended (as in the reference). softmax scale 1/sqrt(head_dim). q, kc, vc and
+ * o_part 16-byte aligned.
  */
 int dk_paged_attention(int version, const void* q, const void* kc, const void* vc, const int32_t* bt,
                        const int32_t* pos, int n_q, int n_kv, int head_dim, int page, int n_pages, int n_bt,
                        int part_size, int max_splits, float* o_part, float* m_part, float* l_part, void* out,
                        void* stream);
+
+/*
+ * Fused decode attention: rope_append followed by paged_attention with one fewer launch, for callers that own the
+ * whole decode step (no counterpart in the reference's binding: it fuses rope_append, kernels/bindings.cpp:81-88,
+ * and the split kernel of paged_attention, kernels/bindings.cpp:45-62, as runtime/model.py:205-213 calls them back to
+ * back). qkv: the fused [q | k | v] vector, fp16 [(n_q + 2 n_kv) * head_dim], read only (q is rotated in registers,
+ * not written back). k (rotated) and v of position *pos are written into page bt[pos / page], slot pos % page exactly
+ * as dk_rope_append writes them, and the attention over ctx = *pos + 1 tokens uses them. Split partials go to
+ * o_part / m_part / l_part and a combine kernel merges them, as for dk_paged_attention. If *pos is outside
+ * [0, max_pos) nothing is touched. Other arguments and limits as dk_rope_append / dk_paged_attention.
+ */
+int dk_attention_decode(const void* qkv, const float* cos_t, const float* sin_t, int max_pos, const int32_t* pos,
+                        const int32_t* bt, int n_bt, void* kc, void* vc, int n_pages, int page, int n_q, int n_kv,
+                        int head_dim, int part_size, int max_splits, float* o_part, float* m_part, float* l_part,
+                        void* out, void* stream);
 
 /*
  * Fused residual add + RMSNorm:  x <- x + delta (fp16 add, written back; skipped if delta == NULL);

@@ -60,6 +60,17 @@ __device__ __forceinline__ float wave_sum_lane63(float v) {
   v += DK_DPP_F32(v, 0x143, 0xC);  // row_bcast31, rows 2 and 3
   return v;
 }
+// Sum over aligned groups of CPL = 8 or 16 consecutive lanes, every lane of the group ends with the group sum
+// (quad_perm x2, row_half_mirror, and row_mirror for 16).
+template <int CPL>
+__device__ __forceinline__ float group_sum_dpp(float v) {
+  static_assert(CPL == 8 || CPL == 16, "group of 8 or 16 lanes");
+  v += DK_DPP_F32(v, 0xB1, 0xF);
+  v += DK_DPP_F32(v, 0x4E, 0xF);
+  v += DK_DPP_F32(v, 0x141, 0xF);
+  if constexpr (CPL == 16) v += DK_DPP_F32(v, 0x140, 0xF);
+  return v;
+}
 // Same sum, broadcast to every lane (v_readlane of lane 63 into a scalar register).
 __device__ __forceinline__ float wave_sum_all(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_lane63(v)), 63));

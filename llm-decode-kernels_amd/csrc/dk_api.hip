@@ -112,10 +112,42 @@ int dk_paged_attention(int version, const void* q, const void* kc, const void* v
   if (n_kv > 65535 || n_q > 65535) return fail(DK_ERR_SHAPE, "paged_attention: too many heads");
   if (!aligned16(q) || !aligned16(kc) || !aligned16(vc))
     return fail(DK_ERR_ALIGN, "q, kc and vc must be 16B aligned");
+  if (!aligned16(o_part)) return fail(DK_ERR_ALIGN, "o_part must be 16B aligned");
   clear_error();
-  dk::launch_paged_attention(q, kc, vc, bt, pos, n_q, n_kv, head_dim, ilog2(page), n_pages, n_bt, part_size,
-                             max_splits, o_part, m_part, l_part, out, (hipStream_t)stream);
+  const dk::AttnLaunch a{q, nullptr, nullptr, 0, pos, bt, n_bt, const_cast<void*>(kc), const_cast<void*>(vc), n_pages,
+                         ilog2(page), n_q, n_kv, head_dim, part_size, max_splits, o_part, m_part, l_part, out};
+  dk::launch_paged_attention(a, (hipStream_t)stream);
   return launched("paged_attention");
+}
+
+int dk_attention_decode(const void* qkv, const float* cos_t, const float* sin_t, int max_pos, const int32_t* pos,
+                        const int32_t* bt, int n_bt, void* kc, void* vc, int n_pages, int page, int n_q, int n_kv,
+                        int head_dim, int part_size, int max_splits, float* o_part, float* m_part, float* l_part,
+                        void* out, void* stream) {
+  if (!qkv || !cos_t || !sin_t || !pos || !bt || !kc || !vc || !o_part || !m_part || !l_part || !out)
+    return fail(DK_ERR_NULL, "attention_decode: null pointer argument");
+  if (head_dim != 64 && head_dim != 128)
+    return fail(DK_ERR_SHAPE, "attention_decode: head_dim must be 64 or 128, got %d", head_dim);
+  if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0)
+    return fail(DK_ERR_SHAPE, "heads-per-group must be 1/2/4/8 (n_q=%d n_kv=%d)", n_q, n_kv);
+  const int hpg = n_q / n_kv;
+  if (hpg != 1 && hpg != 2 && hpg != 4 && hpg != 8)
+    return fail(DK_ERR_SHAPE, "heads-per-group must be 1/2/4/8, got %d", hpg);
+  if (!pow2(page)) return fail(DK_ERR_DOMAIN, "page size must be a power of two, got %d", page);
+  if (part_size <= 0) return fail(DK_ERR_DOMAIN, "part_size must be > 0");
+  if (max_splits < 1 || max_splits > 65535)
+    return fail(DK_ERR_SHAPE, "attention_decode: max_splits must be 1..65535, got %d", max_splits);
+  if (n_pages < 1 || n_bt < 1 || max_pos < 1)
+    return fail(DK_ERR_SHAPE, "attention_decode: empty cache, block table or rope table");
+  if (n_kv > 65535 || n_q > 65535) return fail(DK_ERR_SHAPE, "attention_decode: too many heads");
+  if (!aligned16(qkv) || !aligned16(kc) || !aligned16(vc))
+    return fail(DK_ERR_ALIGN, "qkv, kc and vc must be 16B aligned");
+  if (!aligned16(o_part)) return fail(DK_ERR_ALIGN, "o_part must be 16B aligned");
+  clear_error();
+  const dk::AttnLaunch a{qkv, cos_t, sin_t, max_pos, pos, bt, n_bt, kc, vc, n_pages, ilog2(page), n_q, n_kv,
+                         head_dim, part_size, max_splits, o_part, m_part, l_part, out};
+  dk::launch_attention_decode(a, (hipStream_t)stream);
+  return launched("attention_decode");
 }
 
 int dk_add_rmsnorm(void* x, const void* delta, const void* w, void* out, int H, float eps, void* stream) {

@@ -17,9 +17,29 @@ void gemv_default_config(int N, int K, int* stage, int* R, int* waves, int* pf);
 
 void launch_bw_read(const void* buf, size_t bytes, void* sink, int blocks, int threads, int unroll, hipStream_t st);
 
-void launch_paged_attention(const void* q, const void* kc, const void* vc, const int32_t* bt, const int32_t* pos,
-                            int n_q, int n_kv, int head_dim, int log2P, int n_pages, int n_bt, int part_size,
-                            int max_splits, float* o_part, float* m_part, float* l_part, void* out, hipStream_t st);
+// Paged attention arguments. q: the query heads [n_q * D] (reference op) or the fused qkv vector (decode op).
+struct AttnLaunch {
+  const void* q;
+  const float* cos_t;  // RoPE tables [max_pos, D/2] (decode op only)
+  const float* sin_t;
+  int max_pos;
+  const int32_t* pos;
+  const int32_t* bt;
+  int n_bt;
+  void* kc;
+  void* vc;
+  int n_pages;
+  int log2P;
+  int n_q, n_kv, head_dim, part_size, max_splits;
+  float* o_part;
+  float* m_part;
+  float* l_part;
+  void* out;
+};
+// Reference-compatible op: split kernel + combine kernel.
+void launch_paged_attention(const AttnLaunch& a, hipStream_t st);
+// Fused decode op: RoPE + KV append + split-K attention, then the combine kernel.
+void launch_attention_decode(const AttnLaunch& a, hipStream_t st);
 
 void launch_add_rmsnorm(void* x, const void* delta, const void* w, void* out, int H, float eps, hipStream_t st);
 void launch_swiglu(const void* gu, void* out, int I, hipStream_t st);

@@ -1,279 +1,412 @@
-// Paged split-K GQA decode attention (one query token) on gfx950.
+// Paged split-K GQA decode attention (one query token) on gfx950, with an optional fused RoPE + KV append and an
+// optional in-kernel combine.
 //
 // Cache layout (runtime/model.py:117-120 of the reference): kc / vc fp16 [pages, n_kv, P, D]; token t of the
 // sequence lives in physical page bt[t / P], slot t % P, so one (page, kv head) holds P contiguous D-vectors.
-// Context = *pos + 1 read from device memory, so one captured graph serves every decode step.
+// Context = min(*pos + 1, n_bt * P) read from device memory, so one captured graph serves every decode step.
 //
-// Grid (n_kv, max_splits); workgroup (kvh, s) = 4 waves owns tokens [s*PS, min(ctx, (s+1)*PS)) for all HPG query
-// heads of kv head kvh, so every K/V byte is read from HBM once. Splits past the live count exit.
+// Grid (n_kv, max_splits), 256 threads. Workgroup (kvh, s) owns tokens [s*PS, min(ctx, (s+1)*PS)) for all HPG query
+// heads of kv head kvh, so every K/V byte is read from HBM once. Splits past ceil(ctx / PS) exit at once.
+// The split is processed in blocks of TB tokens, three phases per block:
+//   1. token-major: lane (g, c) of a wave holds the 16-byte slice c (dims 8c..8c+7) of token slot g; CPL = D/8 lanes
+//      cover one token, so one wave load reads TPL = 64/CPL consecutive tokens (1 KB contiguous inside a page).
+//      Scores q.k per head: v_dot2_f32_f16 on the fp16 pairs (exact products, fp32 sums), summed over the CPL lanes
+//      with DPP, times 1/sqrt(D) in fp32. Scores go to LDS s_s[h][t], the V slices to LDS s_v[t][.].
+//   2. head-major: the 256/HPG threads of head h each read all TB scores of the block (LDS broadcast), update the
+//      running maximum M, compute p = exp(s - M) for their share of tokens into s_p[h][t].
+//   3. head-major: thread (h, j) owns dims [j*DPT, (j+1)*DPT) of head h: acc = a*acc + sum_t p[h][t] V[t][dims],
+//      l = a*l + sum_t p[h][t] with a = exp(M_old - M_new) (the online-softmax rescale between blocks).
+// No cross-lane reduction of the output is ever needed: every output element is accumulated by one thread.
+// With one live split the normalised output acc / l is written directly. Otherwise each split writes unnormalized
+// o, m = M, l, and the combine
+//     M* = max_s m_s;  L = sum_s e^(m_s - M*) l_s;  O = sum_s e^(m_s - M*) o_s / L
+// runs in a second kernel, one workgroup per query head: split lanes x 4-dim groups issue all their partial loads at
+// once, keep an online maximum, and merge through LDS. (Combining in the last split workgroup to finish instead
+// needs an agent-scope release by every workgroup and an acquire by the last, which on gfx950 are L2 writeback /
+// invalidate operations; measured slower than the second launch at every context length.)
 //
-// Lane map (wave64): CPL = D/8 lanes hold one token row (16 B each), so a wave load covers TPL = 64/CPL consecutive
-// tokens (8 at D = 64, 4 at D = 128) = 1 KB contiguous inside a page. Each wave walks its own chunks of
-// CH = 2*TPL tokens (chunks interleaved across the 4 waves) and keeps its own online-softmax state:
-//     m' = max(m, chunk max);  a = e^(m - m');  l' = a l + sum e^(s - m');  o' = a o + sum e^(s - m') v
-// Scores reduce over the CPL lanes of a row; the chunk max reduces over the token lanes. l and o stay per-lane
-// partials over the lane's tokens (all CPL lanes of a token see the same p) until one cross-lane reduction at the
-// end; the 4 waves then merge through LDS with the same max-rescale rule. With one live split the normalised output
-// is written directly; otherwise each split writes unnormalized o and its (m, l), and the combine kernel computes
-//     M = max_s m_s;  L = sum_s e^(m_s - M) l_s;  O = sum_s e^(m_s - M) o_s / L.
-// Scores are fp32 with q pre-scaled by 1/sqrt(D) in fp32.
+// ROPE mode (fused decode step): q and the new k come from the fused qkv vector, rotated with the rotate_half
+// convention (pairs (i, i + D/2), fp32 tables), each product rounded separately as the reference's elementwise fp32
+// ops do; rotated values are rounded to fp16 (reference/ref_ops.py:36-53). The workgroup that owns token pos
+// (split pos / PS, or the last live split if the cap is smaller) writes k and v into page bt[pos / P], slot pos % P,
+// and uses the fresh values for token pos itself instead of the cache. If *pos is outside [0, max_pos) nothing is
+// touched.
 #include "common.hpp"
 #include "launch.hpp"
 
 namespace dk {
 namespace {
 
-constexpr int kAttnWaves = 4;
+constexpr int kAttnThreads = 256;
+constexpr int kAttnWaves = kAttnThreads / kWave;
+constexpr int kNL = 2;  // token loads (of K and of V) per lane per block
 
-__device__ __forceinline__ int live_context(const int32_t* pos_ptr, int n_bt, int log2P) {
+template <int D, int HPG>
+struct AttnShape {
+  static constexpr int CPL = D / 8;                      // lanes per token row
+  static constexpr int TPL = kWave / CPL;                // tokens per wave load
+  static constexpr int TB = kAttnWaves * kNL * TPL;      // tokens per block (64 at D=64, 32 at D=128)
+  static constexpr int NTH = kAttnThreads / HPG;         // threads per head in phases 2-3
+  static constexpr int DPT = (HPG * D >= kAttnThreads) ? HPG * D / kAttnThreads : 1;  // dims per thread
+};
+
+__device__ __forceinline__ int attn_context(const int32_t* pos_ptr, int n_bt, int log2P) {
   const long long cap = (long long)n_bt << log2P;
   const long long ctx = (long long)(*pos_ptr) + 1;
   return (int)(ctx < cap ? ctx : cap);
 }
 
-__device__ __forceinline__ int live_splits(int ctx, int PS, int max_splits) {
+__device__ __forceinline__ int attn_splits(int ctx, int PS, int max_splits) {
   if (ctx <= 0) return 0;
   const int n = (ctx + PS - 1) / PS;
   return n < max_splits ? n : max_splits;
 }
 
-template <int D, int HPG>
-__global__ void __launch_bounds__(256)
-attn_split_kernel(const f16* __restrict__ q, const f16* __restrict__ kc, const f16* __restrict__ vc,
-                  const int32_t* __restrict__ bt, const int32_t* __restrict__ pos_ptr, int n_kv, int log2P,
-                  int n_pages, int n_bt, int PS, int max_splits, float scale, float* __restrict__ o_part,
-                  float* __restrict__ m_part, float* __restrict__ l_part, f16* __restrict__ out) {
-  constexpr int NW = kAttnWaves;
-  constexpr int CPL = D / 8;
-  constexpr int TPL = kWave / CPL;
-  constexpr int SL = 2;
-  constexpr int CH = TPL * SL;
-  __shared__ float red[NW][HPG][D];
-  __shared__ float wm[NW][HPG], wl[NW][HPG];
+// RoPE of one 8-dim slice c of a head vector x (fp16, D dims): own = x[8c..8c+8), partner = the slice D/2 away.
+// out_i = own_i * cos_i + sign * (partner_i * sin_i), sign = -1 in the first half, +1 in the second half; products
+// and sums rounded separately (no contraction), result rounded to fp16.
+template <int D>
+__device__ __forceinline__ u32x4 rope_slice(u32x4 own, u32x4 partner, const float* cs, const float* sn, bool first) {
+  // hipcc contracts a*c - b*s into one fma by default (one rounding instead of two), which changes the rotated value
+  // in the last bit now and then; the reference rounds both products. The pragma covers the operators written here
+  // (not those inside library helpers such as __fmul_rn, whose bodies carry their own contraction flag).
+#pragma clang fp contract(off)
+  float a[8], b[8];
+  unpack8(own, a);
+  unpack8(partner, b);
+  u32x4 r;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    f16 o2[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int i = 2 * k + e;
+      const float p1 = a[i] * cs[i];
+      const float p2 = b[i] * sn[i];
+      o2[e] = (f16)(first ? p1 - p2 : p1 + p2);
+    }
+    r[k] = as_u32(f16x2{o2[0], o2[1]});
+  }
+  return r;
+}
+
+template <int D, int HPG, bool ROPE>
+__global__ void __launch_bounds__(kAttnThreads)
+attn_decode_kernel(const f16* __restrict__ qsrc, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                   int max_pos, const int32_t* __restrict__ pos_ptr, const int32_t* __restrict__ bt, int n_bt,
+                   f16* __restrict__ kc, f16* __restrict__ vc, int n_pages, int log2P, int n_q, int n_kv, int PS,
+                   int max_splits, float scale, float* __restrict__ o_part, float* __restrict__ m_part,
+                   float* __restrict__ l_part, f16* __restrict__ out) {
+  using S = AttnShape<D, HPG>;
+  constexpr int CPL = S::CPL, TPL = S::TPL, TB = S::TB, NTH = S::NTH, DPT = S::DPT;
+  __shared__ float s_s[HPG][TB];
+  __shared__ float s_p[HPG][TB];
+  __shared__ u32x4 s_v[TB][CPL];
 
   const int kvh = blockIdx.x, split = blockIdx.y;
-  const int ctx = live_context(pos_ptr, n_bt, log2P);
-  const int nsplit = live_splits(ctx, PS, max_splits);
-  if (split >= nsplit) return;
-  const int t0 = split * PS;
-  const int t1 = min(ctx, t0 + PS);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane / CPL, c = lane % CPL;
   const int P = 1 << log2P;
+  // A split that starts past the last block-table token can hold no token (and split * PS may not fit an int).
+  const long long t0l = (long long)split * PS;
+  const bool reachable = t0l < ((long long)n_bt << log2P);
+  const int t0 = reachable ? (int)t0l : 0;
 
-  float qv[HPG][8];
+  // Independent loads first: block-table entries of this lane's tokens in blocks 0 and 1, the q slices, the new k / v.
+  // (Tokens past the split or the table get page -1; the live bound t1 is applied once pos is known.)
+  int pg[kNL], pgn[kNL];
+#pragma unroll
+  for (int jn = 0; jn < kNL; ++jn) {
+    const int tl = (wave * kNL + jn) * TPL + g;
+    const int lp = (t0 + tl) >> log2P, lpn = (t0 + TB + tl) >> log2P;
+    pg[jn] = (reachable && tl < PS && lp < n_bt) ? bt[lp] : -1;
+    pgn[jn] = (reachable && TB + tl < PS && lpn < n_bt) ? bt[lpn] : -1;
+  }
+  const int pos = *pos_ptr;
+  const int cp = (c + CPL / 2) % CPL;  // partner slice for RoPE
+  const bool first_half = c < CPL / 2;
+  u32x4 qraw[HPG], qpart[HPG];
 #pragma unroll
   for (int h = 0; h < HPG; ++h) {
-    const u32x4 raw = *reinterpret_cast<const u32x4*>(q + (size_t)(kvh * HPG + h) * D + c * 8);
-    unpack8(raw, qv[h]);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) qv[h][e] *= scale;
+    const f16* qh = qsrc + (size_t)(kvh * HPG + h) * D;
+    qraw[h] = *reinterpret_cast<const u32x4*>(qh + 8 * c);
+    if constexpr (ROPE) qpart[h] = *reinterpret_cast<const u32x4*>(qh + 8 * cp);
   }
-
-  float m[HPG], l[HPG], acc[HPG][8];
+  u32x4 knew = {0u, 0u, 0u, 0u}, vnew = {0u, 0u, 0u, 0u};
+  if constexpr (ROPE) {
+    const f16* kh = qsrc + (size_t)(n_q + kvh) * D;
+    const f16* vh = qsrc + (size_t)(n_q + n_kv + kvh) * D;
+    const u32x4 kown = *reinterpret_cast<const u32x4*>(kh + 8 * c);
+    const u32x4 kpar = *reinterpret_cast<const u32x4*>(kh + 8 * cp);
+    vnew = *reinterpret_cast<const u32x4*>(vh + 8 * c);
+    if (pos < 0 || pos >= max_pos) return;  // uniform: nothing is touched
+    const int ti = (8 * c) % (D / 2);
+    float cs[8], sn[8];
 #pragma unroll
-  for (int h = 0; h < HPG; ++h) {
-    m[h] = -INFINITY;
-    l[h] = 0.f;
+    for (int e = 0; e < 8; ++e) {
+      cs[e] = cos_t[(size_t)pos * (D / 2) + ti + e];
+      sn[e] = sin_t[(size_t)pos * (D / 2) + ti + e];
+    }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+    for (int h = 0; h < HPG; ++h) qraw[h] = rope_slice<D>(qraw[h], qpart[h], cs, sn, first_half);
+    knew = rope_slice<D>(kown, kpar, cs, sn, first_half);
   }
-
-  for (int cs = t0 + wave * CH; cs < t1; cs += NW * CH) {
-    u32x4 kr[SL], vr[SL];
-    bool ok[SL];
-#pragma unroll
-    for (int j = 0; j < SL; ++j) {
-      const int t = cs + j * TPL + g;
-      bool live = t < t1;
-      int page = 0;
-      if (live) {
-        page = bt[t >> log2P];
-        live = page >= 0 && page < n_pages;
-      }
-      ok[j] = live;
-      if (live) {
-        const size_t base = ((((size_t)page * n_kv + kvh) << log2P) + (t & (P - 1))) * D + c * 8;
-        kr[j] = load_stream(reinterpret_cast<const u32x4*>(kc + base));
-        vr[j] = load_stream(reinterpret_cast<const u32x4*>(vc + base));
-      } else {
-        kr[j] = u32x4{0u, 0u, 0u, 0u};
-        vr[j] = kr[j];
+  const int ctx = attn_context(pos_ptr, n_bt, log2P);
+  const int nsplit = attn_splits(ctx, PS, max_splits);
+  if (ROPE) {
+    // the workgroup owning token pos (or the last live split when the cap is below pos) appends k, v
+    const int owner = min(pos / PS, nsplit - 1);
+    if (split == owner && wave == 0 && lane < CPL) {
+      const int lp = pos >> log2P;
+      const int page = lp < n_bt ? bt[lp] : -1;
+      if (page >= 0 && page < n_pages) {
+        const size_t off = ((((size_t)page * n_kv + kvh) << log2P) + (pos & (P - 1))) * D + 8 * c;
+        *reinterpret_cast<u32x4*>(kc + off) = knew;
+        *reinterpret_cast<u32x4*>(vc + off) = vnew;
       }
     }
-    float s[SL][HPG];
+  }
+  if (split >= nsplit || !reachable) return;
+  const int t1 = (int)min((long long)ctx, t0l + PS);
+  const int nblk = (t1 - t0 + TB - 1) / TB;
+
+  // K / V of this lane's tokens in block b: pages pgb[], -1 = no token
+  auto issue_kv = [&](int tb, const int (&pgb)[kNL], u32x4 (&kk)[kNL], u32x4 (&vv)[kNL]) {
 #pragma unroll
-    for (int j = 0; j < SL; ++j) {
-      float kf[8];
-      unpack8(kr[j], kf);
+    for (int jn = 0; jn < kNL; ++jn) {
+      const int t = tb + (wave * kNL + jn) * TPL + g;
+      if (t < t1 && pgb[jn] >= 0 && pgb[jn] < n_pages) {
+        const size_t off = ((((size_t)pgb[jn] * n_kv + kvh) << log2P) + (t & (P - 1))) * D + 8 * c;
+        kk[jn] = load_stream(reinterpret_cast<const u32x4*>(kc + off));
+        vv[jn] = load_stream(reinterpret_cast<const u32x4*>(vc + off));
+      } else {
+        kk[jn] = u32x4{0u, 0u, 0u, 0u};
+        vv[jn] = kk[jn];
+      }
+    }
+  };
+  u32x4 kr[kNL], vr[kNL], kn[kNL], vn[kNL];
+  issue_kv(t0, pg, kr, vr);
+
+  const int h3 = tid / NTH, j3 = tid % NTH, d0 = j3 * DPT;
+  float M = -INFINITY, l = 0.f, acc[DPT];
+#pragma unroll
+  for (int e = 0; e < DPT; ++e) acc[e] = 0.f;
+
+  for (int b = 0; b < nblk; ++b) {
+    const int tb = t0 + b * TB;
+    // ---- pipeline: K / V of block b + 1 (pages loaded one block ahead) and pages of block b + 2 go out now, so
+    // their latency overlaps the three phases of block b
+    int pg2[kNL];
+    if (b + 1 < nblk) issue_kv(tb + TB, pgn, kn, vn);
+#pragma unroll
+    for (int jn = 0; jn < kNL; ++jn) {
+      const int t = tb + 2 * TB + (wave * kNL + jn) * TPL + g;
+      const int lp = t >> log2P;
+      pg2[jn] = (b + 2 < nblk && t < t1 && lp < n_bt) ? bt[lp] : -1;
+    }
+    // ---- phase 1: scores and V slices of this block (token-major)
+#pragma unroll
+    for (int jn = 0; jn < kNL; ++jn) {
+      const int tl = (wave * kNL + jn) * TPL + g;
+      const int t = tb + tl;
+      const bool ok = t < t1 && pg[jn] >= 0 && pg[jn] < n_pages;
+      u32x4 kk = kr[jn], vv = vr[jn];
+      if (ROPE && t == pos && ok) {  // the cache slot of pos is being written by this launch: use the fresh k, v
+        kk = knew;
+        vv = vnew;
+      }
+      float sc[HPG];
 #pragma unroll
       for (int h = 0; h < HPG; ++h) {
         float a = 0.f;
+        a = dot2(as_f16x2(qraw[h].x), as_f16x2(kk.x), a);
+        a = dot2(as_f16x2(qraw[h].y), as_f16x2(kk.y), a);
+        a = dot2(as_f16x2(qraw[h].z), as_f16x2(kk.z), a);
+        a = dot2(as_f16x2(qraw[h].w), as_f16x2(kk.w), a);
+        sc[h] = group_sum_dpp<CPL>(a) * scale;
+      }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) a = fmaf(kf[e], qv[h][e], a);
-        a = group_sum<CPL>(a);
-        s[j][h] = ok[j] ? a : -INFINITY;
+      for (int h = 0; h < HPG; ++h)
+        if (c == h) s_s[h][tl] = ok ? sc[h] : -INFINITY;
+      s_v[tl][c] = ok ? vv : u32x4{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();
+    // ---- phase 2: block maximum and probabilities (head-major)
+    float bm = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < TB; t += 4) {
+      const float4 v4 = *reinterpret_cast<const float4*>(&s_s[h3][t]);
+      bm = fmaxf(bm, fmaxf(fmaxf(v4.x, v4.y), fmaxf(v4.z, v4.w)));
+    }
+    const float Mn = fmaxf(M, bm);
+    const float alpha = (M == -INFINITY) ? 0.f : __expf(M - Mn);
+    for (int t = j3; t < TB; t += NTH) {
+      const float sv = s_s[h3][t];
+      s_p[h3][t] = (sv == -INFINITY) ? 0.f : __expf(sv - Mn);
+    }
+    M = Mn;
+    __syncthreads();
+    // ---- phase 3: rescale and accumulate p . V (head-major)
+    l *= alpha;
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) acc[e] *= alpha;
+    if (d0 < D) {
+      const f16* vbase = reinterpret_cast<const f16*>(&s_v[0][0]) + d0;
+#pragma unroll 4
+      for (int t = 0; t < TB; ++t) {
+        const float p = s_p[h3][t];
+        l += p;
+        const f16* vt = vbase + (size_t)t * D;
+#pragma unroll
+        for (int e = 0; e < DPT; ++e) acc[e] = fmaf(p, (float)vt[e], acc[e]);
       }
     }
+    __syncthreads();
+    // ---- rotate the pipeline registers
 #pragma unroll
-    for (int h = 0; h < HPG; ++h) {
-      float cm = s[0][h];
-#pragma unroll
-      for (int j = 1; j < SL; ++j) cm = fmaxf(cm, s[j][h]);
-      cm = strided_max<CPL>(cm);
-      const float mn = fmaxf(m[h], cm);
-      const float al = (mn == -INFINITY) ? 1.f : __expf(m[h] - mn);
-      m[h] = mn;
-      l[h] *= al;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[h][e] *= al;
-    }
-#pragma unroll
-    for (int j = 0; j < SL; ++j) {
-      float vf[8];
-      unpack8(vr[j], vf);
-#pragma unroll
-      for (int h = 0; h < HPG; ++h) {
-        const float p = ok[j] ? __expf(s[j][h] - m[h]) : 0.f;
-        l[h] += p;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(p, vf[e], acc[h][e]);
-      }
+    for (int jn = 0; jn < kNL; ++jn) {
+      kr[jn] = kn[jn];
+      vr[jn] = vn[jn];
+      pg[jn] = pgn[jn];
+      pgn[jn] = pg2[jn];
     }
   }
 
-  // per-lane partials -> per-wave totals (reduce over the TPL token lanes that share c)
+  const int head = kvh * HPG + h3;
+  if (d0 >= D) return;
+  if (nsplit == 1) {
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
 #pragma unroll
-  for (int h = 0; h < HPG; ++h) {
-    l[h] = strided_sum<CPL>(l[h]);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[h][e] = strided_sum<CPL>(acc[h][e]);
+    for (int e = 0; e < DPT; ++e) out[(size_t)head * D + d0 + e] = (f16)(acc[e] * inv);
+    return;
   }
-  if (g == 0) {
 #pragma unroll
-    for (int h = 0; h < HPG; ++h)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) red[wave][h][c * 8 + e] = acc[h][e];
-  }
-  if (lane == 0) {
-#pragma unroll
-    for (int h = 0; h < HPG; ++h) {
-      wm[wave][h] = m[h];
-      wl[wave][h] = l[h];
-    }
-  }
-  __syncthreads();
-  for (int i = tid; i < HPG * D; i += NW * kWave) {
-    const int h = i / D, d = i % D, head = kvh * HPG + h;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, wm[w][h]);
-    float o = 0.f, L = 0.f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const float a = (wm[w][h] == -INFINITY) ? 0.f : __expf(wm[w][h] - M);
-      o = fmaf(a, red[w][h][d], o);
-      L = fmaf(a, wl[w][h], L);
-    }
-    if (nsplit == 1) {
-      out[(size_t)head * D + d] = (f16)(L > 0.f ? o / L : 0.f);
-    } else {
-      o_part[((size_t)head * max_splits + split) * D + d] = o;
-      if (d == 0) {
-        m_part[(size_t)head * max_splits + split] = M;
-        l_part[(size_t)head * max_splits + split] = L;
-      }
-    }
+  for (int e = 0; e < DPT; ++e) o_part[((size_t)head * max_splits + split) * D + d0 + e] = acc[e];
+  if (j3 == 0) {
+    m_part[(size_t)head * max_splits + split] = M;
+    l_part[(size_t)head * max_splits + split] = l;
   }
 }
 
-// One workgroup per query head; 256 threads = 256/D split lanes x D dims.
+// Combine of the split partials of one query head per workgroup: thread (sl, d4) takes splits sl, sl + SLN, ... and
+// dims [4 d4, 4 d4 + 4); every lane keeps an online maximum over its splits (loads of 4 splits in flight), then the
+// SLN split lanes merge through LDS with the same max-rescale rule.
 template <int D>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kAttnThreads)
 attn_combine_kernel(const float* __restrict__ o_part, const float* __restrict__ m_part,
-                    const float* __restrict__ l_part, const int32_t* __restrict__ pos_ptr, int n_bt, int log2P,
-                    int PS, int max_splits, f16* __restrict__ out) {
-  constexpr int NT = 256, NWV = NT / kWave, SLN = NT / D;
-  __shared__ float sred[NWV];
-  __shared__ float osum[SLN][D];
-  const int head = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nsplit = live_splits(live_context(pos_ptr, n_bt, log2P), PS, max_splits);
+                    const float* __restrict__ l_part, const int32_t* __restrict__ pos_ptr, int max_pos, int n_bt,
+                    int log2P, int PS, int max_splits, f16* __restrict__ out) {
+  constexpr int NG = D / 4;                 // 4-dim groups per head
+  constexpr int SLN = kAttnThreads / NG;    // split lanes
+  __shared__ float s_m[SLN], s_l[SLN];
+  __shared__ float4 s_a[SLN][NG];
+  if (max_pos > 0 && (*pos_ptr < 0 || *pos_ptr >= max_pos)) return;  // decode op: the split kernel did nothing
+  const int nsplit = attn_splits(attn_context(pos_ptr, n_bt, log2P), PS, max_splits);
   if (nsplit <= 1) return;
+  const int head = blockIdx.x, tid = threadIdx.x, sl = tid / NG, d4 = tid % NG;
   const float* m = m_part + (size_t)head * max_splits;
   const float* l = l_part + (size_t)head * max_splits;
-
-  float mx = -INFINITY;
-  for (int s = tid; s < nsplit; s += NT) mx = fmaxf(mx, m[s]);
-  mx = group_max<kWave>(mx);
-  if (lane == 0) sred[wave] = mx;
-  __syncthreads();
-  float M = sred[0];
+  const float* op = o_part + (size_t)head * max_splits * D + 4 * d4;
+  float M = -INFINITY, L = 0.f;
+  float4 a = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = sl; s0 < nsplit; s0 += 4 * SLN) {
+    float ms[4], ls[4];
+    float4 os[4];
 #pragma unroll
-  for (int w = 1; w < NWV; ++w) M = fmaxf(M, sred[w]);
-  __syncthreads();
-
-  float L = 0.f;
-  for (int s = tid; s < nsplit; s += NT)
-    if (m[s] != -INFINITY) L = fmaf(__expf(m[s] - M), l[s], L);
-  L = group_sum<kWave>(L);
-  if (lane == 0) sred[wave] = L;
-  __syncthreads();
-  L = 0.f;
+    for (int k = 0; k < 4; ++k) {
+      const int s = s0 + k * SLN;
+      const bool v = s < nsplit;
+      ms[k] = v ? m[s] : -INFINITY;
+      ls[k] = v ? l[s] : 0.f;
+      os[k] = v ? *reinterpret_cast<const float4*>(op + (size_t)s * D) : float4{0.f, 0.f, 0.f, 0.f};
+    }
+    const float Mn = fmaxf(fmaxf(M, fmaxf(ms[0], ms[1])), fmaxf(ms[2], ms[3]));
+    if (Mn == -INFINITY) continue;
+    const float r = (M == -INFINITY) ? 0.f : __expf(M - Mn);
+    L *= r;
+    a.x *= r;
+    a.y *= r;
+    a.z *= r;
+    a.w *= r;
 #pragma unroll
-  for (int w = 0; w < NWV; ++w) L += sred[w];
-
-  const int d = tid % D, sl = tid / D;
-  const float* op = o_part + (size_t)head * max_splits * D + d;
-  float o = 0.f;
-  for (int s = sl; s < nsplit; s += SLN)
-    if (m[s] != -INFINITY) o = fmaf(__expf(m[s] - M), op[(size_t)s * D], o);
-  osum[sl][d] = o;
+    for (int k = 0; k < 4; ++k) {
+      const float w = (ms[k] == -INFINITY) ? 0.f : __expf(ms[k] - Mn);
+      L = fmaf(w, ls[k], L);
+      a.x = fmaf(w, os[k].x, a.x);
+      a.y = fmaf(w, os[k].y, a.y);
+      a.z = fmaf(w, os[k].z, a.z);
+      a.w = fmaf(w, os[k].w, a.w);
+    }
+    M = Mn;
+  }
+  if (d4 == 0) {
+    s_m[sl] = M;
+    s_l[sl] = L;
+  }
+  s_a[sl][d4] = a;
   __syncthreads();
-  if (tid < D) {
-    float v = 0.f;
+  if (tid < NG) {
+    float Mx = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < SLN; ++i) v += osum[i][tid];
-    out[(size_t)head * D + tid] = (f16)(L > 0.f ? v / L : 0.f);
+    for (int i = 0; i < SLN; ++i) Mx = fmaxf(Mx, s_m[i]);
+    float Lt = 0.f;
+    float4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < SLN; ++i) {
+      const float w = (s_m[i] == -INFINITY) ? 0.f : __expf(s_m[i] - Mx);
+      Lt = fmaf(w, s_l[i], Lt);
+      o.x = fmaf(w, s_a[i][tid].x, o.x);
+      o.y = fmaf(w, s_a[i][tid].y, o.y);
+      o.z = fmaf(w, s_a[i][tid].z, o.z);
+      o.w = fmaf(w, s_a[i][tid].w, o.w);
+    }
+    const float inv = Lt > 0.f ? 1.0f / Lt : 0.f;
+    f16* dst = out + (size_t)head * D + 4 * tid;
+    dst[0] = (f16)(o.x * inv);
+    dst[1] = (f16)(o.y * inv);
+    dst[2] = (f16)(o.z * inv);
+    dst[3] = (f16)(o.w * inv);
   }
 }
 
-template <int D, int HPG>
-void launch_split(const void* q, const void* kc, const void* vc, const int32_t* bt, const int32_t* pos, int n_kv,
-                  int log2P, int n_pages, int n_bt, int PS, int max_splits, float* o_part, float* m_part,
-                  float* l_part, void* out, hipStream_t st) {
+template <int D, int HPG, bool ROPE>
+void launch_attn(const AttnLaunch& a, hipStream_t st) {
   const float scale = 1.0f / sqrtf((float)D);
-  hipLaunchKernelGGL((attn_split_kernel<D, HPG>), dim3(n_kv, max_splits), dim3(kAttnWaves * kWave), 0, st,
-                     (const f16*)q, (const f16*)kc, (const f16*)vc, bt, pos, n_kv, log2P, n_pages, n_bt, PS,
-                     max_splits, scale, o_part, m_part, l_part, (f16*)out);
+  hipLaunchKernelGGL((attn_decode_kernel<D, HPG, ROPE>), dim3(a.n_kv, a.max_splits), dim3(kAttnThreads), 0, st,
+                     (const f16*)a.q, a.cos_t, a.sin_t, a.max_pos, a.pos, a.bt, a.n_bt, (f16*)a.kc, (f16*)a.vc,
+                     a.n_pages, a.log2P, a.n_q, a.n_kv, a.part_size, a.max_splits, scale, a.o_part, a.m_part,
+                     a.l_part, (f16*)a.out);
+  if (a.max_splits > 1)
+    hipLaunchKernelGGL((attn_combine_kernel<D>), dim3(a.n_q), dim3(kAttnThreads), 0, st, a.o_part, a.m_part,
+                       a.l_part, a.pos, ROPE ? a.max_pos : 0, a.n_bt, a.log2P, a.part_size, a.max_splits,
+                       (f16*)a.out);
 }
 
-template <int D>
-void launch_d(int hpg, const void* q, const void* kc, const void* vc, const int32_t* bt, const int32_t* pos, int n_q,
-              int n_kv, int log2P, int n_pages, int n_bt, int PS, int max_splits, float* o_part, float* m_part,
-              float* l_part, void* out, hipStream_t st) {
-  switch (hpg) {
-    case 1: launch_split<D, 1>(q, kc, vc, bt, pos, n_kv, log2P, n_pages, n_bt, PS, max_splits, o_part, m_part, l_part, out, st); break;
-    case 2: launch_split<D, 2>(q, kc, vc, bt, pos, n_kv, log2P, n_pages, n_bt, PS, max_splits, o_part, m_part, l_part, out, st); break;
-    case 4: launch_split<D, 4>(q, kc, vc, bt, pos, n_kv, log2P, n_pages, n_bt, PS, max_splits, o_part, m_part, l_part, out, st); break;
-    default: launch_split<D, 8>(q, kc, vc, bt, pos, n_kv, log2P, n_pages, n_bt, PS, max_splits, o_part, m_part, l_part, out, st); break;
+template <int D, bool ROPE>
+void launch_attn_hpg(const AttnLaunch& a, hipStream_t st) {
+  switch (a.n_q / a.n_kv) {
+    case 1: launch_attn<D, 1, ROPE>(a, st); break;
+    case 2: launch_attn<D, 2, ROPE>(a, st); break;
+    case 4: launch_attn<D, 4, ROPE>(a, st); break;
+    default: launch_attn<D, 8, ROPE>(a, st); break;
   }
-  if (max_splits > 1)
-    hipLaunchKernelGGL((attn_combine_kernel<D>), dim3(n_q), dim3(256), 0, st, o_part, m_part, l_part, pos, n_bt,
-                       log2P, PS, max_splits, (f16*)out);
 }
 
 }  // namespace
 
-void launch_paged_attention(const void* q, const void* kc, const void* vc, const int32_t* bt, const int32_t* pos,
-                            int n_q, int n_kv, int head_dim, int log2P, int n_pages, int n_bt, int part_size,
-                            int max_splits, float* o_part, float* m_part, float* l_part, void* out, hipStream_t st) {
-  const int hpg = n_q / n_kv;
-  if (head_dim == 64)
-    launch_d<64>(hpg, q, kc, vc, bt, pos, n_q, n_kv, log2P, n_pages, n_bt, part_size, max_splits, o_part, m_part,
-                 l_part, out, st);
+void launch_paged_attention(const AttnLaunch& a, hipStream_t st) {
+  if (a.head_dim == 64)
+    launch_attn_hpg<64, false>(a, st);
   else
-    launch_d<128>(hpg, q, kc, vc, bt, pos, n_q, n_kv, log2P, n_pages, n_bt, part_size, max_splits, o_part, m_part,
-                  l_part, out, st);
+    launch_attn_hpg<128, false>(a, st);
+}
+
+void launch_attention_decode(const AttnLaunch& a, hipStream_t st) {
+  if (a.head_dim == 64)
+    launch_attn_hpg<64, true>(a, st);
+  else
+    launch_attn_hpg<128, true>(a, st);
 }
 
 }  // namespace dk

@@ -25,6 +25,7 @@ SIGNATURES = {
     "dk_gemv_w4a16": ([_I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P], _I),
     "dk_bw_read": ([_P, _Z, _P, _I, _I, _I, _P], _I),
     "dk_paged_attention": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
+    "dk_attention_decode": ([_P, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
     "dk_add_rmsnorm": ([_P, _P, _P, _P, _I, _F, _P], _I),
     "dk_swiglu": ([_P, _P, _I, _P], _I),
     "dk_rope_append": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
@@ -125,6 +126,35 @@ class DecodeKernels:
         self._call(self.lib.dk_paged_attention, int(version), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
                    bt.data_ptr(), pos.data_ptr(), n_q, n_kv, D, P, kc.size(0), bt.numel(), int(part_size),
                    max_splits, o_part.data_ptr(), m_part.data_ptr(), l_part.data_ptr(), out.data_ptr(), _stream(q))
+
+    # rope_append (kernels/bindings.cpp:81-88) + paged_attention (kernels/bindings.cpp:45-62) fused into one launch
+    def attention_decode(self, qkv, cos_t, sin_t, pos, bt, kc, vc, n_q, n_kv, part_size, o_part, m_part, l_part,
+                         out):
+        for t, n in ((qkv, "qkv"), (cos_t, "cos_t"), (sin_t, "sin_t"), (pos, "pos"), (bt, "bt"), (kc, "kc"),
+                     (vc, "vc"), (o_part, "o_part"), (m_part, "m_part"), (l_part, "l_part"), (out, "out")):
+            _check_cuda(t, n)
+        if kc.dim() != 4 or kc.size(3) not in (64, 128) or vc.shape != kc.shape or kc.size(1) != n_kv:
+            raise RuntimeError("cache must be [pages, n_kv, P, 64|128]")
+        D = kc.size(3)
+        if qkv.numel() != (n_q + 2 * n_kv) * D or cos_t.dim() != 2 or cos_t.size(1) != D // 2 \
+                or sin_t.shape != cos_t.shape:
+            raise RuntimeError("attention_decode: qkv must hold (n_q + 2 n_kv) * D values and cos/sin [max_pos, D/2]")
+        for t, n in ((qkv, "qkv"), (kc, "kc"), (vc, "vc"), (out, "out")):
+            _check_dtype(t, torch.float16, n)
+        for t, n in ((cos_t, "cos_t"), (sin_t, "sin_t"), (o_part, "o_part"), (m_part, "m_part"), (l_part, "l_part")):
+            _check_dtype(t, torch.float32, n)
+        for t, n in ((pos, "pos"), (bt, "bt")):
+            _check_dtype(t, torch.int32, n)
+        if n_q % n_kv != 0 or (n_q // n_kv) not in (1, 2, 4, 8):
+            raise RuntimeError("heads-per-group must be 1/2/4/8")
+        max_splits = o_part.size(1)
+        if not (o_part.size(0) == n_q and o_part.size(2) == D and m_part.shape == (n_q, max_splits)
+                and l_part.shape == (n_q, max_splits) and out.numel() == n_q * D):
+            raise RuntimeError("attention_decode: buffers must be o [n_q, S, D], m/l [n_q, S], out [n_q, D]")
+        self._call(self.lib.dk_attention_decode, qkv.data_ptr(), cos_t.data_ptr(), sin_t.data_ptr(), cos_t.size(0),
+                   pos.data_ptr(), bt.data_ptr(), bt.numel(), kc.data_ptr(), vc.data_ptr(), kc.size(0), kc.size(2),
+                   int(n_q), int(n_kv), D, int(part_size), max_splits, o_part.data_ptr(), m_part.data_ptr(),
+                   l_part.data_ptr(), out.data_ptr(), _stream(qkv))
 
     # kernels/bindings.cpp:64-72
     def add_rmsnorm(self, x, delta, w, out, eps):

@@ -53,6 +53,8 @@ class DecodeConfig:
     shuffle_pages: bool = True
     device: str = "cuda"
     seed: int = 0            # block-table permutation seed
+    fused_attention: bool = True   # dk_attention_decode (RoPE + append inside the split kernel) instead of
+                                   # rope_append + paged_attention
 
 
 def default_gemv_config(N, K):
@@ -179,8 +181,10 @@ class Model:
         return json.load(open(p)) if p.exists() else {}
 
     def _policy_part_size(self, ctx_cap):
-        """Entry tuned at the largest context <= ctx_cap (runtime/model.py:164-172)."""
-        ents = [e for e in self._policy().get("policy", []) if e["max_ctx"] < (1 << 30)]
+        """Entry tuned at the largest context <= ctx_cap (runtime/model.py:164-172), from the head-dim-specific table
+        ("policy_d128") when there is one."""
+        pol = self._policy()
+        ents = [e for e in pol.get(f"policy_d{self.D}", pol.get("policy", [])) if e["max_ctx"] < (1 << 30)]
         if not ents:
             return 64
         below = [e for e in ents if e["max_ctx"] <= ctx_cap]
@@ -218,6 +222,10 @@ class Model:
 
     def attention(self, li):
         kc, vc = self.kv[li, 0], self.kv[li, 1]
+        if self.cfg.fused_attention:
+            self.K.attention_decode(self.qkv, self.cos, self.sin, self.pos, self.bt, kc, vc, self.n_q, self.n_kv,
+                                    self.part_size, self.o_part, self.m_part, self.l_part, self.attn)
+            return
         self.K.rope_append(self.qkv, self.cos, self.sin, self.pos, self.bt, kc, vc, self.n_q, self.n_kv)
         self.K.paged_attention(self.qkv[: self.n_q * self.D], kc, vc, self.bt, self.pos, self.part_size,
                                self.o_part, self.m_part, self.l_part, self.attn, self.attn_version)

@@ -101,6 +101,28 @@ def test_attention_validation(lib, kw, code, msg):
     assert rc == code and msg in m, (rc, m)
 
 
+def _dec(lib, **kw):
+    a = dict(qkv=A16, c=A16, s=A16, max_pos=100, pos=A16, bt=A16, n_bt=8, kc=A16, vc=A16, n_pages=8, page=16, n_q=32,
+             n_kv=4, D=64, part_size=64, max_splits=4, o=A16, m=A16, l=A16, out=A16)
+    a.update(kw)
+    return _err(lib, lib.dk_attention_decode(*a.values(), None))
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(n_q=24), 3, "heads-per-group must be 1/2/4/8"),
+    (dict(D=96), 3, "head_dim"),
+    (dict(page=12), 4, "page size must be a power of two"),
+    (dict(part_size=0), 4, "part_size must be > 0"),
+    (dict(max_splits=0), 3, "max_splits"),
+    (dict(max_pos=0), 3, "empty"),
+    (dict(c=None), 1, "null"),
+    (dict(qkv=A16 + 2), 2, "16B aligned"),
+])
+def test_attention_decode_validation(lib, kw, code, msg):
+    rc, m = _dec(lib, **kw)
+    assert rc == code and msg in m, (rc, m)
+
+
 def test_small_op_validation(lib):
     assert _err(lib, lib.dk_add_rmsnorm(A16, None, A16, A16, 2047, 1e-5, None))[0] == 3
     assert _err(lib, lib.dk_add_rmsnorm(A16 + 2, None, A16, A16, 2048, 1e-5, None))[0] == 2
