@@ -63,6 +63,28 @@ int dk_gemv_w4a16(int stage, int R, int warps, int pf, const void* packed, const
                   int N, int K, int group, void* stream);
 
 /*
+ * W4A16 GEMV whose input is the residual + RMSNorm of the reference's add_rmsnorm, computed inside the GEMV
+ * (no counterpart in the reference's binding: it fuses add_rmsnorm, kernels/bindings.cpp:64-72, with the gemv_w4a16
+ * that runtime/model.py:189-196,219-228 calls right after it):
+ *   xn = x + delta (fp16 add; delta may be NULL), or xn = the row *row of x when row != NULL (x is then an embedding
+ *        table [*, K] and delta must be NULL: the decode step's embedding gather);
+ *   y  = dequant(W) . (norm_w * fp16(float(xn) * rsqrt(mean(float(xn)^2) + eps)))
+ *   x_out (if not NULL) receives xn; it must not alias x or delta (the residual stream is double-buffered).
+ * Rounding points as dk_add_rmsnorm and dk_gemv_w4a16. stage must be 4; R and pf as for stage 4; K <= 32768.
+ */
+int dk_gemv_w4a16_rmsnorm(int stage, int R, int warps, int pf, const void* packed, const void* sz, const void* x,
+                          const int64_t* row, const void* delta, const void* norm_w, float eps, void* x_out, void* y,
+                          int N, int K, int group, void* stream);
+
+/*
+ * W4A16 GEMV whose input is SwiGLU of gu = [gate | up] (fp16 [2K]): x[i] = fp16(silu(float(gate[i]))) * up[i],
+ * computed inside the GEMV (fuses swiglu, kernels/bindings.cpp:74-79, with the down-projection gemv_w4a16 of
+ * runtime/model.py:227-228; no counterpart in the reference's binding). Rounding as dk_swiglu; stage must be 4.
+ */
+int dk_gemv_w4a16_swiglu(int stage, int R, int warps, int pf, const void* packed, const void* sz, const void* gu,
+                         void* y, int N, int K, int group, void* stream);
+
+/*
  * Achievable-read-bandwidth microbenchmark: reads `bytes` (multiple of 16) from buf, XOR-folds them and writes sink
  * (uint32[1]) only on a value it never takes. Replaces bw_read (kernels/bindings.cpp:40-43,
  * kernels/gemv_w4a16.cu:133-153). unroll in {1, 4}; threads a multiple of 64 in [64, 1024]; blocks >= 1.

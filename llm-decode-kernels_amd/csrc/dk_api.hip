@@ -79,6 +79,54 @@ int dk_gemv_w4a16(int stage, int R, int warps, int pf, const void* packed, const
   return launched("gemv_w4a16");
 }
 
+// Checks shared by the fused row-tile GEMVs (stage 4 only).
+static int check_fused_gemv(const char* what, int stage, int R, int warps, int pf, const void* packed, const void* sz,
+                            int N, int K, int group) {
+  if (!packed || !sz) return fail(DK_ERR_NULL, "%s: null pointer argument", what);
+  if (stage != 4) return fail(DK_ERR_DOMAIN, "%s: the fused prologue exists for stage 4 only, got %d", what, stage);
+  if (R != 1 && R != 2 && R != 4 && R != 8) return fail(DK_ERR_DOMAIN, "gemv: R must be 1,2,4,8, got %d", R);
+  if (warps < 0 || warps > 16) return fail(DK_ERR_DOMAIN, "%s: warps must be 0..16, got %d", what, warps);
+  if (pf < 0 || pf > 3) return fail(DK_ERR_DOMAIN, "%s: pf must be 0..3 for stage 4, got %d", what, pf);
+  if (N <= 0 || K <= 0) return fail(DK_ERR_SHAPE, "%s: N and K must be positive (N=%d K=%d)", what, N, K);
+  if (K > dk::kGemvRowsMaxK) return fail(DK_ERR_SHAPE, "%s: K <= %d required, got %d", what, dk::kGemvRowsMaxK, K);
+  if (K % 32 != 0 || K % group != 0)
+    return fail(DK_ERR_SHAPE, "K must be a multiple of 32 and of the group size (K=%d group=%d)", K, group);
+  if (group < 32) return fail(DK_ERR_DOMAIN, "group must be >= 32 (one uint4 never straddles a group), got %d", group);
+  if (!pow2(group)) return fail(DK_ERR_DOMAIN, "group must be a power of two, got %d", group);
+  if (!aligned16(packed)) return fail(DK_ERR_ALIGN, "packed must be 16B aligned");
+  if (!aligned4(sz)) return fail(DK_ERR_ALIGN, "sz must be 4B aligned");
+  return DK_OK;
+}
+
+int dk_gemv_w4a16_rmsnorm(int stage, int R, int warps, int pf, const void* packed, const void* sz, const void* x,
+                          const int64_t* row, const void* delta, const void* norm_w, float eps, void* x_out, void* y,
+                          int N, int K, int group, void* stream) {
+  const int rc = check_fused_gemv("gemv_w4a16_rmsnorm", stage, R, warps, pf, packed, sz, N, K, group);
+  if (rc != DK_OK) return rc;
+  if (!x || !norm_w || !y) return fail(DK_ERR_NULL, "gemv_w4a16_rmsnorm: null pointer argument");
+  if (!aligned16(x) || !aligned16(norm_w) || (delta && !aligned16(delta)) || (x_out && !aligned16(x_out)))
+    return fail(DK_ERR_ALIGN, "x, delta, norm_w and x_out must be 16B aligned");
+  if (row && (reinterpret_cast<uintptr_t>(row) & 7u)) return fail(DK_ERR_ALIGN, "row must be 8B aligned");
+  if (x_out && (x_out == x || (delta && x_out == delta)))
+    return fail(DK_ERR_DOMAIN, "gemv_w4a16_rmsnorm: x_out must not alias x or delta (other workgroups still read them)");
+  clear_error();
+  dk::GemvInput in{x, row, delta, norm_w, eps, x_out};
+  dk::launch_gemv_w4a16_fused(1, R, pf, packed, sz, in, y, N, K, ilog2(group), (hipStream_t)stream);
+  return launched("gemv_w4a16_rmsnorm");
+}
+
+int dk_gemv_w4a16_swiglu(int stage, int R, int warps, int pf, const void* packed, const void* sz, const void* gu,
+                         void* y, int N, int K, int group, void* stream) {
+  const int rc = check_fused_gemv("gemv_w4a16_swiglu", stage, R, warps, pf, packed, sz, N, K, group);
+  if (rc != DK_OK) return rc;
+  if (!gu || !y) return fail(DK_ERR_NULL, "gemv_w4a16_swiglu: null pointer argument");
+  if (!aligned16(gu)) return fail(DK_ERR_ALIGN, "gu must be 16B aligned");
+  clear_error();
+  dk::GemvInput in{gu, nullptr, nullptr, nullptr, 0.f, nullptr};
+  dk::launch_gemv_w4a16_fused(2, R, pf, packed, sz, in, y, N, K, ilog2(group), (hipStream_t)stream);
+  return launched("gemv_w4a16_swiglu");
+}
+
 int dk_bw_read(const void* buf, size_t bytes, void* sink, int blocks, int threads, int unroll, void* stream) {
   if (!buf || !sink) return fail(DK_ERR_NULL, "bw_read: null pointer argument");
   if (!aligned16(buf)) return fail(DK_ERR_ALIGN, "buf must be 16B aligned");

@@ -311,11 +311,105 @@ __device__ __forceinline__ void tile_rows(const u32x4 (&w)[T], const uint32_t (&
   }
 }
 
-template <int T, int NT>
+// The x operand of the row-tile kernel, produced per lane for its column u (32 values = 4 x 16 B):
+//   kInPlain    x[32u .. 32u+32)
+//   kInRmsNorm  the residual + RMSNorm of the reference's add_rmsnorm (kernels/fused_norm.cu:8-54) recomputed by every
+//               workgroup: xn = fp16(xi + delta) (xi = x or the row *row of x, the embedding gather), the sum of
+//               squares over the workgroup's K values (DPP within waves, LDS across), r = 1 / sqrt(ss / K + eps),
+//               value = norm_w * fp16(float(xn) * r). Workgroup 0 writes xn to x_out (a different buffer: every other
+//               workgroup still reads xi).
+//   kInSwiglu   fp16(silu(float(gate))) * up with gate = x[0..I), up = x[I..2I), K == I (kernels/fused_swiglu.cu:7-21).
+enum { kInPlain = 0, kInRmsNorm = 1, kInSwiglu = 2 };
+
+template <int PRO>
+__device__ __forceinline__ void tile_input(const GemvInput& in, int uc, bool live, int K, float* s_ss, int wave,
+                                           int nw, u32x4 (&xc)[4]) {
+  if constexpr (PRO == kInPlain) {
+    const u32x4* X = reinterpret_cast<const u32x4*>(in.x);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xc[k] = X[4 * uc + k];
+  } else if constexpr (PRO == kInSwiglu) {
+    const u32x4* G = reinterpret_cast<const u32x4*>(in.x);
+    const u32x4* Up = G + (K >> 3);
+    u32x4 g[4], up[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      g[k] = G[4 * uc + k];
+      up[k] = Up[4 * uc + k];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const f16x2 g2 = as_f16x2(g[k][e]);
+        const float a = (float)g2.x, b = (float)g2.y;
+        const f16x2 sl = {(f16)(a / (1.0f + expf(-a))), (f16)(b / (1.0f + expf(-b)))};
+        xc[k][e] = as_u32(sl * as_f16x2(up[k][e]));
+      }
+    }
+  } else {
+    const long long off = in.row != nullptr ? (long long)(*in.row) * (K >> 3) : 0;
+    const u32x4* X = reinterpret_cast<const u32x4*>(in.x) + off;
+    const u32x4* Dl = reinterpret_cast<const u32x4*>(in.delta);
+    const u32x4* Wn = reinterpret_cast<const u32x4*>(in.norm_w);
+    u32x4 xr[4], wn[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      xr[k] = X[4 * uc + k];
+      wn[k] = Wn[4 * uc + k];
+    }
+    if (Dl != nullptr) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const u32x4 d = Dl[4 * uc + k];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xr[k][e] = as_u32(as_f16x2(xr[k][e]) + as_f16x2(d[e]));
+      }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const f16x2 h = as_f16x2(xr[k][e]);
+        const float a = (float)h.x, b = (float)h.y;
+        ss = fmaf(a, a, ss);
+        ss = fmaf(b, b, ss);
+      }
+    }
+    ss = wave_sum_all(live ? ss : 0.f);
+    if ((threadIdx.x & 63) == 0) s_ss[wave] = ss;
+    __syncthreads();
+    float tot = 0.f;
+    for (int i = 0; i < nw; ++i) tot += s_ss[i];
+    const float r = 1.0f / sqrtf(tot / (float)K + in.eps);
+    if (blockIdx.x == 0 && in.x_out != nullptr && live) {
+      u32x4* Xo = reinterpret_cast<u32x4*>(in.x_out);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) Xo[4 * uc + k] = xr[k];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const f16x2 h = as_f16x2(xr[k][e]);
+        const f16x2 hn = {(f16)((float)h.x * r), (f16)((float)h.y * r)};
+        xc[k][e] = as_u32(as_f16x2(wn[k][e]) * hn);
+      }
+    }
+  }
+  if (!live) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xc[k] = u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+template <int T, int NT, int PRO>
 __global__ void __launch_bounds__(1024)
-gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, const u32x4* __restrict__ X,
+gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, const GemvInput in,
                 f16* __restrict__ y, int N, int U, int gsh) {
   __shared__ float red[16][T * NT];
+  __shared__ float s_ss[16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
   const int u = wave * kWave + lane;
   const bool live = u < U;
@@ -323,13 +417,12 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
   const int base = blockIdx.x * T * NT;
   const int NG = U >> gsh;
 
-  u32x4 xc[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) xc[k] = X[4 * uc + k];
   u32x4 wa[T], wb[T];
   uint32_t sa[T], sb[T];
   tile_issue<T>(W, SZ, base, N, U, NG, uc, gsh, wa, sa);
   __builtin_amdgcn_sched_barrier(0);
+  u32x4 xc[4];
+  tile_input<PRO>(in, uc, live, U << 5, s_ss, wave, nw, xc);
   const f16x2 one = {(f16)1.0f, (f16)1.0f};
   float SA = 0.f, SB = 0.f;
 #pragma unroll
@@ -391,23 +484,34 @@ void launch_rows_p(int waves, int pf, const void* packed, const void* sz, const 
   launch_rows<R, 1>(waves, packed, sz, x, y, N, K, log2G, st);
 }
 
-template <int T, int NT>
-void launch_tile_nt(const void* packed, const void* sz, const void* x, void* y, int N, int K, int log2G,
+template <int T, int NT, int PRO>
+void launch_tile_nt(const void* packed, const void* sz, const GemvInput& in, void* y, int N, int K, int log2G,
                     hipStream_t st) {
   const int U = K >> 5;
   const int waves = (U + 63) / 64;
-  hipLaunchKernelGGL((gemv_w4a16_tile<T, NT>), dim3((N + T * NT - 1) / (T * NT)), dim3(64 * waves), 0, st,
-                     (const u32x4*)packed, (const uint32_t*)sz, (const u32x4*)x, (f16*)y, N, U, log2G - 5);
+  hipLaunchKernelGGL((gemv_w4a16_tile<T, NT, PRO>), dim3((N + T * NT - 1) / (T * NT)), dim3(64 * waves), 0, st,
+                     (const u32x4*)packed, (const uint32_t*)sz, in, (f16*)y, N, U, log2G - 5);
 }
 
-template <int T>
-void launch_tile(int pf, const void* packed, const void* sz, const void* x, void* y, int N, int K, int log2G,
+template <int T, int PRO>
+void launch_tile(int pf, const void* packed, const void* sz, const GemvInput& in, void* y, int N, int K, int log2G,
                  hipStream_t st) {
   switch (pf) {
-    case 0: launch_tile_nt<T, 1>(packed, sz, x, y, N, K, log2G, st); break;
-    case 1: launch_tile_nt<T, 2>(packed, sz, x, y, N, K, log2G, st); break;
-    case 2: launch_tile_nt<T, 4>(packed, sz, x, y, N, K, log2G, st); break;
-    default: launch_tile_nt<T, 8>(packed, sz, x, y, N, K, log2G, st); break;
+    case 0: launch_tile_nt<T, 1, PRO>(packed, sz, in, y, N, K, log2G, st); break;
+    case 1: launch_tile_nt<T, 2, PRO>(packed, sz, in, y, N, K, log2G, st); break;
+    case 2: launch_tile_nt<T, 4, PRO>(packed, sz, in, y, N, K, log2G, st); break;
+    default: launch_tile_nt<T, 8, PRO>(packed, sz, in, y, N, K, log2G, st); break;
+  }
+}
+
+template <int PRO>
+void launch_tile_r(int R, int pf, const void* packed, const void* sz, const GemvInput& in, void* y, int N, int K,
+                   int log2G, hipStream_t st) {
+  switch (R) {
+    case 1: launch_tile<1, PRO>(pf, packed, sz, in, y, N, K, log2G, st); break;
+    case 2: launch_tile<2, PRO>(pf, packed, sz, in, y, N, K, log2G, st); break;
+    case 4: launch_tile<4, PRO>(pf, packed, sz, in, y, N, K, log2G, st); break;
+    default: launch_tile<8, PRO>(pf, packed, sz, in, y, N, K, log2G, st); break;
   }
 }
 
@@ -453,12 +557,9 @@ void launch_gemv_w4a16(int stage, int R, int waves, int pf, const void* packed, 
   }
   if (waves <= 0) waves = stage == 3 ? min(16, ((K >> 5) + 63) / 64) : 4;
   if (stage == 4) {
-    switch (R) {
-      case 1: launch_tile<1>(pf, packed, sz, x, y, N, K, log2G, st); break;
-      case 2: launch_tile<2>(pf, packed, sz, x, y, N, K, log2G, st); break;
-      case 4: launch_tile<4>(pf, packed, sz, x, y, N, K, log2G, st); break;
-      default: launch_tile<8>(pf, packed, sz, x, y, N, K, log2G, st); break;
-    }
+    GemvInput in{};
+    in.x = x;
+    launch_tile_r<kInPlain>(R, pf, packed, sz, in, y, N, K, log2G, st);
     return;
   }
   if (stage == 1) R = 1;
@@ -477,6 +578,14 @@ void launch_gemv_w4a16(int stage, int R, int waves, int pf, const void* packed, 
     case 4: launch_splitk<4>(waves, pf, packed, sz, x, y, N, K, log2G, st); break;
     default: launch_splitk<8>(waves, pf, packed, sz, x, y, N, K, log2G, st); break;
   }
+}
+
+void launch_gemv_w4a16_fused(int prologue, int R, int pf, const void* packed, const void* sz, const GemvInput& in,
+                             void* y, int N, int K, int log2G, hipStream_t st) {
+  if (prologue == kInRmsNorm)
+    launch_tile_r<kInRmsNorm>(R, pf, packed, sz, in, y, N, K, log2G, st);
+  else
+    launch_tile_r<kInSwiglu>(R, pf, packed, sz, in, y, N, K, log2G, st);
 }
 
 }  // namespace dk

@@ -5,8 +5,9 @@ waves per workgroup x 2^pf steps in flight; stage 3: split-K, R rows per workgro
 stage 4: 2^pf row tiles of R rows over a workgroup that covers K once) with
 cold weights (runtime.timing), and writes
 
-    configs/autotune.json   {"device": ..., "best": {"NxK_G": [stage, R, warps, pf]}, "us": {"NxK_G": us},
-                             "grid": [every measurement]}
+    configs/autotune.json   {"device": ..., "best": {"NxK_G": [stage, R, warps, pf]}, "best_tile": {the best stage-4
+                             entry}, "us": {"NxK_G": us}, "best_norm": {the fused residual + RMSNorm GEMV},
+                             "us_norm": {...}, "grid": [every measurement]}
 
 The runtime (runtime.model.Model.gemv_cfg) reads "best"; 3-element entries [R, warps, pf] of the reference's schema
 are read as stage 2. Run:  python -m runtime.autotune [--shapes tinyllama,llama3_8b,baseline] [--groups 128]
@@ -58,6 +59,33 @@ def candidates(N, K):
     return [c for c in out if not (c[0] == 2 and K > 32768)]
 
 
+def norm_candidates():
+    """stage-4 configurations of the fused residual + RMSNorm GEMV (dk_gemv_w4a16_rmsnorm)."""
+    return [(4, R, 0, pf) for R in (1, 2, 4, 8) for pf in range(4)]
+
+
+def tune_norm_shape(Kx, N, K, G, reps=5, log=print):
+    """Best configuration of the fused-norm GEMV for one shape, cold weights; also returns the time of the separate
+    add_rmsnorm + best plain GEMV pair so the runtime can tell whether fusing pays at this shape."""
+    g = torch.Generator(device="cuda").manual_seed(N * 17 + K)
+    packed, sz = quantize_pack((torch.randn(N, K, generator=g, device="cuda") * 0.02).half(), G)
+    x = torch.randn(K, generator=g, device="cuda").half()
+    d = torch.randn(K, generator=g, device="cuda").half()
+    w = torch.ones(K, dtype=torch.half, device="cuda")
+    xo, nrm = torch.empty_like(x), torch.empty_like(x)
+    y = torch.empty(N, dtype=torch.half, device="cuda")
+    cold = ColdCopies([packed, sz], n_copies(gemv_bytes(N, K, G)))
+    recs = []
+    for cfg in norm_candidates():
+        _, med = graph_time(lambda i: Kx.gemv_w4a16_rmsnorm(*cfg, *cold[i], x, None, d, w, 1e-5, xo, y, G),
+                            cold.copies, reps)
+        recs.append({"N": N, "K": K, "G": G, "cfg": list(cfg), "median_us": med, "variant": "rmsnorm"})
+    best = min(recs, key=lambda r: r["median_us"])
+    log(f"  norm {N}x{K} G{G}: best {best['cfg']} {best['median_us']:.2f} us; {len(recs)} configs")
+    del cold
+    return best, recs
+
+
 def gemv_bytes(N, K, G):
     return N * K // 2 + N * (K // G) * 4 + 2 * K + 2 * N
 
@@ -81,18 +109,36 @@ def tune_shape(Kx, N, K, G, reps=5, log=print):
     return best, recs
 
 
+# GEMVs that consume a residual + RMSNorm in the decode step (qkv, gate|up, INT4 LM head)
+NORM_SHAPES = {"tinyllama": ((2560, 2048), (11264, 2048), (32000, 2048)),
+               "llama3_8b": ((6144, 4096), (28672, 4096), (128256, 4096)), "baseline": ()}
+
+
 def tune(shape_sets=("tinyllama", "llama3_8b", "baseline"), groups=(128,), reps=5, path=CONFIG, log=print):
     Kx = ext.load()
     old = json.load(open(path)) if pathlib.Path(path).exists() else {}
     best, us, grid = dict(old.get("best", {})), dict(old.get("us", {})), []
+    best_tile = dict(old.get("best_tile", {}))
+    best_norm, us_norm = dict(old.get("best_norm", {})), dict(old.get("us_norm", {}))
+    for ss in shape_sets:
+        for (N, K) in NORM_SHAPES.get(ss, ()):
+            for G in groups:
+                b, recs = tune_norm_shape(Kx, N, K, G, reps, log)
+                key = f"{N}x{K}_G{G}"
+                best_norm[key], us_norm[key] = b["cfg"], round(b["median_us"], 3)
+                grid += recs
     for ss in shape_sets:
         for name, (N, K) in SHAPE_SETS[ss].items():
             for G in groups:
                 b, recs = tune_shape(Kx, N, K, G, reps, log)
                 key = f"{N}x{K}_G{G}"
                 best[key], us[key] = b["cfg"], round(b["median_us"], 3)
+                tiles = [r for r in recs if r["cfg"][0] == 4]
+                if tiles:
+                    best_tile[key] = min(tiles, key=lambda r: r["median_us"])["cfg"]
                 grid += [dict(r, shape=name) for r in recs]
-    out = {"device": torch.cuda.get_device_properties(0).name, "best": best, "us": us, "grid": grid}
+    out = {"device": torch.cuda.get_device_properties(0).name, "best": best, "best_tile": best_tile, "us": us,
+           "best_norm": best_norm, "us_norm": us_norm, "grid": grid}
     pathlib.Path(path).parent.mkdir(exist_ok=True)
     json.dump(out, open(path, "w"), indent=1)
     return out

@@ -23,6 +23,8 @@ SIGNATURES = {
     "dk_last_error": ([], ctypes.c_char_p),
     "dk_runtime_version": ([], _I),
     "dk_gemv_w4a16": ([_I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P], _I),
+    "dk_gemv_w4a16_rmsnorm": ([_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _I, _I, _P], _I),
+    "dk_gemv_w4a16_swiglu": ([_I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P], _I),
     "dk_bw_read": ([_P, _Z, _P, _I, _I, _I, _P], _I),
     "dk_paged_attention": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
     "dk_attention_decode": ([_P, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
@@ -91,6 +93,50 @@ class DecodeKernels:
             _check_dtype(t, torch.float16, n)
         self._call(self.lib.dk_gemv_w4a16, int(stage), int(R), int(warps), int(pf), packed.data_ptr(), sz.data_ptr(),
                    x.data_ptr(), y.data_ptr(), N, K, int(group), _stream(x))
+
+    def _gemv_shape(self, packed, sz, y, K, group):
+        N = packed.size(0)
+        if packed.size(1) * 8 != K or y.numel() != N or sz.size(0) != N or sz.size(1) != K // group:
+            raise RuntimeError("gemv: shape mismatch between packed, sz, x and y")
+        _check_dtype(packed, torch.int32, "packed")
+        _check_dtype(sz, torch.float16, "sz")
+        _check_dtype(y, torch.float16, "y")
+        return N
+
+    # add_rmsnorm (kernels/bindings.cpp:64-72) fused into the gemv_w4a16 that follows it
+    def gemv_w4a16_rmsnorm(self, stage, R, warps, pf, packed, sz, x, row, delta, norm_w, eps, x_out, y, group):
+        for t, n in ((packed, "packed"), (sz, "sz"), (x, "x"), (norm_w, "norm_w"), (y, "y")):
+            _check_cuda(t, n)
+        K = norm_w.numel()
+        N = self._gemv_shape(packed, sz, y, K, group)
+        if row is None and x.numel() != K:
+            raise RuntimeError("gemv_w4a16_rmsnorm: x must hold K values (or be a [*, K] table with row)")
+        if row is not None and (x.dim() != 2 or x.size(1) != K or row.dtype != torch.int64 or delta is not None):
+            raise RuntimeError("gemv_w4a16_rmsnorm: row needs an int64 index into a [*, K] x and no delta")
+        for t, n in ((x, "x"), (norm_w, "norm_w")):
+            _check_dtype(t, torch.float16, n)
+        ptr = lambda t: None if t is None else t.data_ptr()
+        for t, n in ((delta, "delta"), (x_out, "x_out"), (row, "row")):
+            if t is not None:
+                _check_cuda(t, n)
+        for t, n in ((delta, "delta"), (x_out, "x_out")):
+            if t is not None and (t.numel() != K or t.dtype != torch.float16):
+                raise RuntimeError(f"gemv_w4a16_rmsnorm: {n} must be fp16 [K]")
+        self._call(self.lib.dk_gemv_w4a16_rmsnorm, int(stage), int(R), int(warps), int(pf), packed.data_ptr(),
+                   sz.data_ptr(), x.data_ptr(), ptr(row), ptr(delta), norm_w.data_ptr(), float(eps), ptr(x_out),
+                   y.data_ptr(), N, K, int(group), _stream(x))
+
+    # swiglu (kernels/bindings.cpp:74-79) fused into the down-projection gemv_w4a16
+    def gemv_w4a16_swiglu(self, stage, R, warps, pf, packed, sz, gu, y, group):
+        for t, n in ((packed, "packed"), (sz, "sz"), (gu, "gu"), (y, "y")):
+            _check_cuda(t, n)
+        K = packed.size(1) * 8
+        N = self._gemv_shape(packed, sz, y, K, group)
+        if gu.numel() != 2 * K:
+            raise RuntimeError("gemv_w4a16_swiglu: gu must hold 2 K values ([gate | up])")
+        _check_dtype(gu, torch.float16, "gu")
+        self._call(self.lib.dk_gemv_w4a16_swiglu, int(stage), int(R), int(warps), int(pf), packed.data_ptr(),
+                   sz.data_ptr(), gu.data_ptr(), y.data_ptr(), N, K, int(group), _stream(gu))
 
     # kernels/bindings.cpp:40-43
     def bw_read(self, buf, sink, blocks, threads, unroll):

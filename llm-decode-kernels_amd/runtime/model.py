@@ -55,6 +55,10 @@ class DecodeConfig:
     seed: int = 0            # block-table permutation seed
     fused_attention: bool = True   # dk_attention_decode (RoPE + append inside the split kernel) instead of
                                    # rope_append + paged_attention
+    fused_gemv: bool = True        # residual + RMSNorm (and the embedding gather) computed inside the INT4 GEMV that
+                                   # consumes it (dk_gemv_w4a16_rmsnorm) instead of a separate add_rmsnorm kernel
+    fused_swiglu: bool = False     # SwiGLU inside the down GEMV (dk_gemv_w4a16_swiglu): every workgroup re-evaluates
+                                   # silu for its columns, measured slower than the separate kernel on MI355X
 
 
 def default_gemv_config(N, K):
@@ -124,9 +128,12 @@ class Model:
         head_int4 = cfg.lm_head == "int4" or (cfg.lm_head == "auto" and quant)
         self.lm_head = Linear(lm.half(), cfg, head_int4)
 
-        self.gemv_table = {}
+        self.gemv_table, self.gemv_tile_table, self.gemv_norm_table = {}, {}, {}
         if cfg.gemv_stage is None and Path(cfg.autotune_path).exists():
-            self.gemv_table = json.load(open(cfg.autotune_path)).get("best", {})
+            tab = json.load(open(cfg.autotune_path))
+            self.gemv_table, self.gemv_tile_table = tab.get("best", {}), tab.get("best_tile", {})
+            self.gemv_norm_table = tab.get("best_norm", {})
+        self.use_fused_gemv = (cfg.fused and cfg.fused_gemv and quant and self.H <= 32768 and self.I <= 32768)
 
         # paged KV cache [L, 2, pages, n_kv, P, D]; one block table shared by all layers (one sequence)
         self.n_pages = (cfg.max_ctx + cfg.page - 1) // cfg.page + 1
@@ -144,6 +151,7 @@ class Model:
         self.tok = torch.zeros(1, dtype=torch.long, device=dev)
         self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
         self.x = torch.empty(self.H, **h16)
+        self.x_alt = torch.empty(self.H, **h16)    # second residual buffer of the fused-prologue step
         self.normed = torch.empty(self.H, **h16)
         self.qkv = torch.empty((self.n_q + 2 * self.n_kv) * self.D, **h16)
         self.attn = torch.empty(self.n_q, self.D, **h16)
@@ -198,6 +206,30 @@ class Model:
             return default_gemv_config(lin.N, lin.K)
         return tuple(e) if len(e) == 4 else (2, *e)      # [R, warps, pf] is the reference's stage-2 schema
 
+    def gemv_tile_cfg(self, lin):
+        """Stage-4 (row tile) configuration for the fused-prologue GEMVs: the tuned stage-4 entry, else R=2, 1 tile."""
+        e = self.gemv_tile_table.get(f"{lin.N}x{lin.K}_G{self.cfg.group}")
+        if e is None:
+            e = self.gemv_table.get(f"{lin.N}x{lin.K}_G{self.cfg.group}")
+            e = tuple(e) if e is not None and len(e) == 4 and e[0] == 4 else None
+        return tuple(e) if e is not None else (4, 2, 0, 0)
+
+    def gemv_norm_cfg(self, lin):
+        """Configuration of the fused-norm GEMV: its own tuned entry (every workgroup recomputes the norm, so larger
+        row tiles pay off), else 4-row tiles."""
+        e = self.gemv_norm_table.get(f"{lin.N}x{lin.K}_G{self.cfg.group}")
+        return tuple(e) if e is not None else (4, 4, 0, 1)
+
+    def linear_norm(self, lin: Linear, x_in, delta, w, x_out, y, row=None):
+        """y = W . rmsnorm(x_in + delta) with x_out <- x_in + delta, one launch (dk_gemv_w4a16_rmsnorm)."""
+        s, r, wv, pf = self.gemv_norm_cfg(lin)
+        self.K.gemv_w4a16_rmsnorm(s, r, wv, pf, lin.packed, lin.sz, x_in, row, delta, w, self.eps, x_out, y,
+                                  self.cfg.group)
+
+    def linear_swiglu(self, lin: Linear, gu, y):
+        s, r, wv, pf = self.gemv_tile_cfg(lin)
+        self.K.gemv_w4a16_swiglu(s, r, wv, pf, lin.packed, lin.sz, gu, y, self.cfg.group)
+
     def linear(self, lin: Linear, x, y):
         if lin.quant:
             s, r, w, pf = self.gemv_cfg(lin)
@@ -233,6 +265,9 @@ class Model:
     # ------------------------------------------------------------------ decode step
     def step(self):
         """One token: reads tok/pos, writes logits, tok <- argmax, pos += 1 (runtime/model.py:216-233)."""
+        if self.use_fused_gemv:
+            self.step_fused()
+            return
         torch.index_select(self.emb, 0, self.tok, out=self.x.view(1, -1))
         delta = None
         for li, lw in enumerate(self.layers):
@@ -247,6 +282,36 @@ class Model:
             delta = self.down
         self.add_norm(delta, self.norm_f)
         self.linear(self.lm_head, self.normed, self.logits)
+        self.K.argmax_advance(self.logits, self.tok, self.pos)
+
+    def step_fused(self):
+        """The same composition with every residual + RMSNorm inside the GEMV that consumes it (the layer-0 one also
+        gathers the embedding row of the device token): per layer qkv, attention (split + combine), o, gate|up,
+        SwiGLU, down = 7 launches. The residual stream alternates between two buffers because a fused GEMV's
+        workgroups all read x_in while workgroup 0 writes x_in + delta."""
+        cur, nxt = self.x, self.x_alt
+        delta = None
+        for li, lw in enumerate(self.layers):
+            if li == 0:
+                self.linear_norm(lw["qkv"], self.emb, None, lw["ln1"], cur, self.qkv, row=self.tok)
+            else:
+                self.linear_norm(lw["qkv"], cur, delta, lw["ln1"], nxt, self.qkv)
+                cur, nxt = nxt, cur
+            self.attention(li)
+            self.linear(lw["o"], self.attn.view(-1), self.o)
+            self.linear_norm(lw["gu"], cur, self.o, lw["ln2"], nxt, self.gu)
+            cur, nxt = nxt, cur
+            if self.cfg.fused_swiglu:
+                self.linear_swiglu(lw["down"], self.gu, self.down)
+            else:
+                self.K.swiglu(self.gu, self.act)
+                self.linear(lw["down"], self.act, self.down)
+            delta = self.down
+        if self.lm_head.quant:
+            self.linear_norm(self.lm_head, cur, delta, self.norm_f, None, self.logits)
+        else:
+            self.K.add_rmsnorm(cur, delta, self.norm_f, self.normed, self.eps)
+            self.linear(self.lm_head, self.normed, self.logits)
         self.K.argmax_advance(self.logits, self.tok, self.pos)
 
     def capture(self):

@@ -335,3 +335,63 @@ def test_graph_replay_of_ops(K):
             torch.cuda.synchronize()
             assert torch.equal(y, expected[p]), (rep, p)
             _ = (qkv0.float() * 2).sum().item()     # eager work between replays
+
+
+# --------------------------------------------------------------------------------- fused-prologue GEMVs (stage 4)
+@pytest.mark.parametrize("N,Kd", [(2560, 2048), (11264, 2048), (6144, 4096), (1000, 5632), (4096, 14336)])
+@pytest.mark.parametrize("mode", ("delta", "no_delta", "row"))
+def test_gemv_rmsnorm_fused(K, N, Kd, mode):
+    """y = W . add_rmsnorm(x, delta, w) in one launch vs the oracle's add_rmsnorm_ref then gemv_ref; the residual
+    written to x_out is bit-exact (fp16 add); the embedding-row gather reads row *tok of a table."""
+    G = 128
+    w, packed, sz = _quantized(K, N, Kd, G, seed=N % 97 + Kd)
+    wref = dequant_from_gpu(packed, sz, G)
+    g = gen(N + Kd)
+    table = (torch.randn(7, Kd, generator=g) * 2).half()
+    x = table[3].clone()
+    d = torch.randn(Kd, generator=g).half() if mode == "delta" else None
+    nw = (1 + 0.1 * torch.randn(Kd, generator=g)).half()
+    xr, normed = R.add_rmsnorm_ref(x, d, nw, 1e-5)
+    ref = R.gemv_ref(wref, normed)
+    y = torch.empty(N, dtype=torch.half, device=DEV)
+    x_out = torch.zeros(Kd, dtype=torch.half, device=DEV)
+    for cfg in ((4, 2, 0, 0), (4, 1, 0, 1), (4, 4, 0, 3), (4, 8, 0, 2)):
+        if mode == "row":
+            K.gemv_w4a16_rmsnorm(*cfg, packed, sz, table.to(DEV), torch.tensor([3], device=DEV), None, nw.to(DEV),
+                                 1e-5, x_out, y, G)
+        else:
+            K.gemv_w4a16_rmsnorm(*cfg, packed, sz, x.to(DEV), None, None if d is None else d.to(DEV), nw.to(DEV),
+                                 1e-5, x_out, y, G)
+        assert_close(y, ref, 5e-3, f"gemv_rmsnorm {mode} {N}x{Kd} {cfg}")
+        assert torch.equal(x_out.cpu(), xr), f"residual {mode} {cfg}"
+
+
+@pytest.mark.parametrize("N,Kd", [(2048, 5632), (4096, 14336), (512, 2048)])
+def test_gemv_swiglu_fused(K, N, Kd):
+    G = 128
+    w, packed, sz = _quantized(K, N, Kd, G, seed=N + 3)
+    wref = dequant_from_gpu(packed, sz, G)
+    gu = (torch.randn(2 * Kd, generator=gen(Kd)) * 2).half()
+    ref = R.gemv_ref(wref, R.swiglu_ref(gu))
+    y = torch.empty(N, dtype=torch.half, device=DEV)
+    for cfg in ((4, 2, 0, 0), (4, 1, 0, 1), (4, 4, 0, 3)):
+        K.gemv_w4a16_swiglu(*cfg, packed, sz, gu.to(DEV), y, G)
+        assert_close(y, ref, 5e-3, f"gemv_swiglu {N}x{Kd} {cfg}")
+
+
+def test_fused_step_equals_unfused_step(K):
+    """The decode step with fused prologues and the one with separate norm / SwiGLU kernels give the same logits
+    (same rounding points; only the sum-of-squares order may differ) and the same tokens."""
+    from runtime.model import DecodeConfig, Model
+    from runtime.synth import LlamaShape, SyntheticLlama
+    shape = LlamaShape(512, 3, 8, 2, 1024, 700)
+    out = []
+    for fused, swiglu in ((False, False), (True, False), (True, True)):
+        m = Model(SyntheticLlama(shape, seed=4, device=DEV, std=0.05), shape,
+                  DecodeConfig(max_ctx=64, device=DEV, fused_gemv=fused, fused_swiglu=swiglu))
+        m.prepare(64)
+        m.reset(0)
+        out.append(m.teacher_force([1, 5, 99, 400, 12], collect_logits=True).float().cpu())
+    for o in out[1:]:
+        err = ((o - out[0]).abs().max() / out[0].abs().max()).item()
+        assert err <= 5e-3, err
