@@ -167,7 +167,8 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--ctx", type=int, default=512)
-    ap.add_argument("--leg", choices=("all", "gemv"), default="all")
+    ap.add_argument("--leg", choices=("all", "gemv", "decode"), default="all",
+                    help="gemv: the 4096x14336 GEMV and its calibration copies only; decode: the decode step only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline leg")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -199,6 +200,9 @@ def main():
         f"max_splits {model.max_splits})")
     dec = decode_leg(model, a.ctx, a.steps, a.warmup)
     log(f"decode ctx {a.ctx}: {dec['tok_s']:.1f} tok/s, median {dec['median_us']:.1f} us/token")
+    if a.leg == "decode":
+        print(json.dumps({"leg": "decode", "decode": dec}), flush=True)
+        return
     bpt = model.bytes_per_token(a.ctx + a.steps // 2)
     model.prepare(2048 + 64 + 16)
     dec2k = decode_leg(model, 2048, 64, 8)

@@ -85,6 +85,20 @@ int dk_gemv_w4a16_swiglu(int stage, int R, int warps, int pf, const void* packed
                          void* y, int N, int K, int group, void* stream);
 
 /*
+ * The gate|up W4A16 GEMV with SwiGLU applied to its output: fuses gemv_w4a16 of the MLP's gate|up projection with
+ * swiglu (kernels/bindings.cpp:27-38 then :74-79, as runtime/model.py:226-227 calls them; no single counterpart in
+ * the reference's binding). The N = 2I weight rows are stored interleaved, row 2i = gate row i and row 2i + 1 = up
+ * row i (a row permutation of the reference's [gate; up] stack, quantized per row exactly as before); writes
+ * act[i] = fp16(silu(float(g_i))) * u_i for i < I, where g_i and u_i are the fp16 GEMV outputs of the two rows, so
+ * the result equals gemv_w4a16 followed by swiglu bit for bit. Input: x as dk_gemv_w4a16 when norm_w is NULL (row,
+ * delta and x_out must then be NULL), else the residual + RMSNorm input of dk_gemv_w4a16_rmsnorm. stage must be 4,
+ * N even and R * 2^pf >= 2.
+ */
+int dk_gemv_w4a16_gate_up(int stage, int R, int warps, int pf, const void* packed, const void* sz, const void* x,
+                          const int64_t* row, const void* delta, const void* norm_w, float eps, void* x_out, void* act,
+                          int N, int K, int group, void* stream);
+
+/*
  * Achievable-read-bandwidth microbenchmark: reads `bytes` (multiple of 16) from buf, XOR-folds them and writes sink
  * (uint32[1]) only on a value it never takes. Replaces bw_read (kernels/bindings.cpp:40-43,
  * kernels/gemv_w4a16.cu:133-153). unroll in {1, 4}; threads a multiple of 64 in [64, 1024]; blocks >= 1.

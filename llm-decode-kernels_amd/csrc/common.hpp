@@ -76,6 +76,13 @@ __device__ __forceinline__ float wave_sum_all(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_lane63(v)), 63));
 }
 
+// SwiGLU of one fp16 (gate, up) pair with the reference's rounding points (kernels/fused_swiglu.cu:2,
+// reference/ref_ops.py:23-27): silu in fp32 of the fp16 gate, rounded to fp16, then an fp16 product with up.
+__device__ __forceinline__ f16 silu_mul(f16 g, f16 u) {
+  const float a = (float)g;
+  return (f16)(a / (1.0f + expf(-a))) * u;
+}
+
 // fp32 dot of two fp16 pairs plus an fp32 accumulator (v_dot2_f32_f16).
 __device__ __forceinline__ float dot2(f16x2 a, f16x2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
 

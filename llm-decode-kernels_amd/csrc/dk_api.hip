@@ -83,7 +83,7 @@ int dk_gemv_w4a16(int stage, int R, int warps, int pf, const void* packed, const
 static int check_fused_gemv(const char* what, int stage, int R, int warps, int pf, const void* packed, const void* sz,
                             int N, int K, int group) {
   if (!packed || !sz) return fail(DK_ERR_NULL, "%s: null pointer argument", what);
-  if (stage != 4) return fail(DK_ERR_DOMAIN, "%s: the fused prologue exists for stage 4 only, got %d", what, stage);
+  if (stage != 4) return fail(DK_ERR_DOMAIN, "%s: the fused variants exist for stage 4 only, got %d", what, stage);
   if (R != 1 && R != 2 && R != 4 && R != 8) return fail(DK_ERR_DOMAIN, "gemv: R must be 1,2,4,8, got %d", R);
   if (warps < 0 || warps > 16) return fail(DK_ERR_DOMAIN, "%s: warps must be 0..16, got %d", what, warps);
   if (pf < 0 || pf > 3) return fail(DK_ERR_DOMAIN, "%s: pf must be 0..3 for stage 4, got %d", what, pf);
@@ -111,7 +111,7 @@ int dk_gemv_w4a16_rmsnorm(int stage, int R, int warps, int pf, const void* packe
     return fail(DK_ERR_DOMAIN, "gemv_w4a16_rmsnorm: x_out must not alias x or delta (other workgroups still read them)");
   clear_error();
   dk::GemvInput in{x, row, delta, norm_w, eps, x_out};
-  dk::launch_gemv_w4a16_fused(1, R, pf, packed, sz, in, y, N, K, ilog2(group), (hipStream_t)stream);
+  dk::launch_gemv_w4a16_fused(1, 0, R, pf, packed, sz, in, y, N, K, ilog2(group), (hipStream_t)stream);
   return launched("gemv_w4a16_rmsnorm");
 }
 
@@ -123,8 +123,33 @@ int dk_gemv_w4a16_swiglu(int stage, int R, int warps, int pf, const void* packed
   if (!aligned16(gu)) return fail(DK_ERR_ALIGN, "gu must be 16B aligned");
   clear_error();
   dk::GemvInput in{gu, nullptr, nullptr, nullptr, 0.f, nullptr};
-  dk::launch_gemv_w4a16_fused(2, R, pf, packed, sz, in, y, N, K, ilog2(group), (hipStream_t)stream);
+  dk::launch_gemv_w4a16_fused(2, 0, R, pf, packed, sz, in, y, N, K, ilog2(group), (hipStream_t)stream);
   return launched("gemv_w4a16_swiglu");
+}
+
+int dk_gemv_w4a16_gate_up(int stage, int R, int warps, int pf, const void* packed, const void* sz, const void* x,
+                          const int64_t* row, const void* delta, const void* norm_w, float eps, void* x_out, void* act,
+                          int N, int K, int group, void* stream) {
+  const int rc = check_fused_gemv("gemv_w4a16_gate_up", stage, R, warps, pf, packed, sz, N, K, group);
+  if (rc != DK_OK) return rc;
+  if (N % 2 != 0) return fail(DK_ERR_SHAPE, "gemv_w4a16_gate_up: N (interleaved gate/up rows) must be even, got %d", N);
+  if ((R << pf) < 2)
+    return fail(DK_ERR_DOMAIN, "gemv_w4a16_gate_up: the row tile R * 2^pf must hold a gate/up pair (>= 2), got R=%d "
+                "pf=%d", R, pf);
+  if (!x || !act) return fail(DK_ERR_NULL, "gemv_w4a16_gate_up: null pointer argument");
+  if (!norm_w && (row || delta || x_out))
+    return fail(DK_ERR_DOMAIN, "gemv_w4a16_gate_up: row, delta and x_out belong to the RMSNorm input (norm_w)");
+  if (!aligned16(x) || (norm_w && !aligned16(norm_w)) || (delta && !aligned16(delta)) || (x_out && !aligned16(x_out)))
+    return fail(DK_ERR_ALIGN, "x, delta, norm_w and x_out must be 16B aligned");
+  if (row && (reinterpret_cast<uintptr_t>(row) & 7u)) return fail(DK_ERR_ALIGN, "row must be 8B aligned");
+  if (x_out && (x_out == x || (delta && x_out == delta)))
+    return fail(DK_ERR_DOMAIN, "gemv_w4a16_gate_up: x_out must not alias x or delta (other workgroups still read them)");
+  if (act == x || (delta && act == delta))
+    return fail(DK_ERR_DOMAIN, "gemv_w4a16_gate_up: act must not alias x or delta");
+  clear_error();
+  dk::GemvInput in{x, row, delta, norm_w, eps, x_out};
+  dk::launch_gemv_w4a16_fused(norm_w ? 1 : 0, 1, R, pf, packed, sz, in, act, N, K, ilog2(group), (hipStream_t)stream);
+  return launched("gemv_w4a16_gate_up");
 }
 
 int dk_bw_read(const void* buf, size_t bytes, void* sink, int blocks, int threads, int unroll, void* stream) {

@@ -65,10 +65,9 @@ swiglu_kernel(const f16* __restrict__ gu, f16* __restrict__ out, int I) {
   u32x4 o;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const f16x2 g2 = as_f16x2(gv[k]);
-    const float a = (float)g2.x, b = (float)g2.y;
-    const f16x2 s = {(f16)(a / (1.0f + expf(-a))), (f16)(b / (1.0f + expf(-b)))};
-    o[k] = as_u32(s * as_f16x2(uv[k]));
+    const f16x2 g2 = as_f16x2(gv[k]), u2 = as_f16x2(uv[k]);
+    const f16x2 r = {silu_mul(g2.x, u2.x), silu_mul(g2.y, u2.y)};
+    o[k] = as_u32(r);
   }
   *reinterpret_cast<u32x4*>(out + i) = o;
 }

@@ -341,10 +341,9 @@ __device__ __forceinline__ void tile_input(const GemvInput& in, int uc, bool liv
     for (int k = 0; k < 4; ++k) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const f16x2 g2 = as_f16x2(g[k][e]);
-        const float a = (float)g2.x, b = (float)g2.y;
-        const f16x2 sl = {(f16)(a / (1.0f + expf(-a))), (f16)(b / (1.0f + expf(-b)))};
-        xc[k][e] = as_u32(sl * as_f16x2(up[k][e]));
+        const f16x2 g2 = as_f16x2(g[k][e]), u2 = as_f16x2(up[k][e]);
+        const f16x2 r = {silu_mul(g2.x, u2.x), silu_mul(g2.y, u2.y)};
+        xc[k][e] = as_u32(r);
       }
     }
   } else {
@@ -404,10 +403,19 @@ __device__ __forceinline__ void tile_input(const GemvInput& in, int uc, bool liv
   }
 }
 
-template <int T, int NT, int PRO>
+// The output of the row-tile kernel:
+//   kOutRows    y[n] = fp16(row sum n)                                      (y has N entries)
+//   kOutSwiglu  the rows are interleaved gate / up pairs (row 2i = gate_i, row 2i + 1 = up_i) and
+//               y[i] = silu_mul(fp16(row 2i), fp16(row 2i + 1))              (y has N / 2 entries)
+//               = swiglu (kernels/fused_swiglu.cu:7-21) of the gate|up GEMV's output, rounded exactly as the two
+//               separate ops round it. Needs an even tile (T * NT) so that a pair never straddles two workgroups.
+enum { kOutRows = 0, kOutSwiglu = 1 };
+
+template <int T, int NT, int PRO, int EPI>
 __global__ void __launch_bounds__(1024)
 gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, const GemvInput in,
                 f16* __restrict__ y, int N, int U, int gsh) {
+  static_assert(EPI == kOutRows || (T * NT) % 2 == 0, "gate/up pairs need an even row tile");
   __shared__ float red[16][T * NT];
   __shared__ float s_ss[16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
@@ -450,10 +458,21 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
     }
   }
   __syncthreads();
-  if (tid < T * NT && base + tid < N) {
-    float acc = 0.f;
-    for (int i = 0; i < nw; ++i) acc += red[i][tid];
-    y[base + tid] = (f16)acc;
+  if constexpr (EPI == kOutRows) {
+    if (tid < T * NT && base + tid < N) {
+      float acc = 0.f;
+      for (int i = 0; i < nw; ++i) acc += red[i][tid];
+      y[base + tid] = (f16)acc;
+    }
+  } else {
+    if (tid < T * NT / 2 && base + 2 * tid + 1 < N) {
+      float g = 0.f, up = 0.f;
+      for (int i = 0; i < nw; ++i) {
+        g += red[i][2 * tid];
+        up += red[i][2 * tid + 1];
+      }
+      y[(base >> 1) + tid] = silu_mul((f16)g, (f16)up);
+    }
   }
 }
 
@@ -484,34 +503,38 @@ void launch_rows_p(int waves, int pf, const void* packed, const void* sz, const 
   launch_rows<R, 1>(waves, packed, sz, x, y, N, K, log2G, st);
 }
 
-template <int T, int NT, int PRO>
+template <int T, int NT, int PRO, int EPI>
 void launch_tile_nt(const void* packed, const void* sz, const GemvInput& in, void* y, int N, int K, int log2G,
                     hipStream_t st) {
-  const int U = K >> 5;
-  const int waves = (U + 63) / 64;
-  hipLaunchKernelGGL((gemv_w4a16_tile<T, NT, PRO>), dim3((N + T * NT - 1) / (T * NT)), dim3(64 * waves), 0, st,
-                     (const u32x4*)packed, (const uint32_t*)sz, in, (f16*)y, N, U, log2G - 5);
-}
-
-template <int T, int PRO>
-void launch_tile(int pf, const void* packed, const void* sz, const GemvInput& in, void* y, int N, int K, int log2G,
-                 hipStream_t st) {
-  switch (pf) {
-    case 0: launch_tile_nt<T, 1, PRO>(packed, sz, in, y, N, K, log2G, st); break;
-    case 1: launch_tile_nt<T, 2, PRO>(packed, sz, in, y, N, K, log2G, st); break;
-    case 2: launch_tile_nt<T, 4, PRO>(packed, sz, in, y, N, K, log2G, st); break;
-    default: launch_tile_nt<T, 8, PRO>(packed, sz, in, y, N, K, log2G, st); break;
+  if constexpr (EPI == kOutSwiglu && (T * NT) % 2 != 0) {
+    return;  // rejected by the host checks (R * 2^pf >= 2); never instantiated as a kernel
+  } else {
+    const int U = K >> 5;
+    const int waves = (U + 63) / 64;
+    hipLaunchKernelGGL((gemv_w4a16_tile<T, NT, PRO, EPI>), dim3((N + T * NT - 1) / (T * NT)), dim3(64 * waves), 0,
+                       st, (const u32x4*)packed, (const uint32_t*)sz, in, (f16*)y, N, U, log2G - 5);
   }
 }
 
-template <int PRO>
+template <int T, int PRO, int EPI>
+void launch_tile(int pf, const void* packed, const void* sz, const GemvInput& in, void* y, int N, int K, int log2G,
+                 hipStream_t st) {
+  switch (pf) {
+    case 0: launch_tile_nt<T, 1, PRO, EPI>(packed, sz, in, y, N, K, log2G, st); break;
+    case 1: launch_tile_nt<T, 2, PRO, EPI>(packed, sz, in, y, N, K, log2G, st); break;
+    case 2: launch_tile_nt<T, 4, PRO, EPI>(packed, sz, in, y, N, K, log2G, st); break;
+    default: launch_tile_nt<T, 8, PRO, EPI>(packed, sz, in, y, N, K, log2G, st); break;
+  }
+}
+
+template <int PRO, int EPI = kOutRows>
 void launch_tile_r(int R, int pf, const void* packed, const void* sz, const GemvInput& in, void* y, int N, int K,
                    int log2G, hipStream_t st) {
   switch (R) {
-    case 1: launch_tile<1, PRO>(pf, packed, sz, in, y, N, K, log2G, st); break;
-    case 2: launch_tile<2, PRO>(pf, packed, sz, in, y, N, K, log2G, st); break;
-    case 4: launch_tile<4, PRO>(pf, packed, sz, in, y, N, K, log2G, st); break;
-    default: launch_tile<8, PRO>(pf, packed, sz, in, y, N, K, log2G, st); break;
+    case 1: launch_tile<1, PRO, EPI>(pf, packed, sz, in, y, N, K, log2G, st); break;
+    case 2: launch_tile<2, PRO, EPI>(pf, packed, sz, in, y, N, K, log2G, st); break;
+    case 4: launch_tile<4, PRO, EPI>(pf, packed, sz, in, y, N, K, log2G, st); break;
+    default: launch_tile<8, PRO, EPI>(pf, packed, sz, in, y, N, K, log2G, st); break;
   }
 }
 
@@ -580,8 +603,15 @@ void launch_gemv_w4a16(int stage, int R, int waves, int pf, const void* packed, 
   }
 }
 
-void launch_gemv_w4a16_fused(int prologue, int R, int pf, const void* packed, const void* sz, const GemvInput& in,
-                             void* y, int N, int K, int log2G, hipStream_t st) {
+void launch_gemv_w4a16_fused(int prologue, int epilogue, int R, int pf, const void* packed, const void* sz,
+                             const GemvInput& in, void* y, int N, int K, int log2G, hipStream_t st) {
+  if (epilogue == kOutSwiglu) {
+    if (prologue == kInRmsNorm)
+      launch_tile_r<kInRmsNorm, kOutSwiglu>(R, pf, packed, sz, in, y, N, K, log2G, st);
+    else
+      launch_tile_r<kInPlain, kOutSwiglu>(R, pf, packed, sz, in, y, N, K, log2G, st);
+    return;
+  }
   if (prologue == kInRmsNorm)
     launch_tile_r<kInRmsNorm>(R, pf, packed, sz, in, y, N, K, log2G, st);
   else

@@ -12,7 +12,8 @@ namespace dk {
 constexpr int kGemvRowsMaxK = 32768;  // x in LDS: K * 2 bytes <= 64 KB per workgroup
 void launch_gemv_w4a16(int stage, int R, int waves, int pf, const void* packed, const void* sz, const void* x,
                        void* y, int N, int K, int log2G, hipStream_t st);
-// x operand of the fused row-tile GEMVs (prologue 1 = residual + RMSNorm, 2 = SwiGLU; see gemv_w4a16.hip).
+// x operand of the fused row-tile GEMVs (prologue 0 = plain x, 1 = residual + RMSNorm, 2 = SwiGLU; see
+// gemv_w4a16.hip).
 struct GemvInput {
   const void* x;          // plain / swiglu: the input vector; rmsnorm: the residual stream (or the embedding table)
   const int64_t* row;     // rmsnorm: device row index into x (embedding gather) or null
@@ -21,8 +22,9 @@ struct GemvInput {
   float eps;
   void* x_out;            // rmsnorm: receives x + delta (written by workgroup 0) or null
 };
-void launch_gemv_w4a16_fused(int prologue, int R, int pf, const void* packed, const void* sz, const GemvInput& in,
-                             void* y, int N, int K, int log2G, hipStream_t st);
+// epilogue 0 = one fp16 output per row, 1 = SwiGLU of interleaved gate / up row pairs (N / 2 outputs).
+void launch_gemv_w4a16_fused(int prologue, int epilogue, int R, int pf, const void* packed, const void* sz,
+                             const GemvInput& in, void* y, int N, int K, int log2G, hipStream_t st);
 // Default configuration for a shape: (stage, R, waves, pf).
 void gemv_default_config(int N, int K, int* stage, int* R, int* waves, int* pf);
 

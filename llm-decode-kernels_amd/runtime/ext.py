@@ -25,6 +25,7 @@ SIGNATURES = {
     "dk_gemv_w4a16": ([_I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P], _I),
     "dk_gemv_w4a16_rmsnorm": ([_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _I, _I, _P], _I),
     "dk_gemv_w4a16_swiglu": ([_I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P], _I),
+    "dk_gemv_w4a16_gate_up": ([_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _I, _I, _P], _I),
     "dk_bw_read": ([_P, _Z, _P, _I, _I, _I, _P], _I),
     "dk_paged_attention": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
     "dk_attention_decode": ([_P, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
@@ -137,6 +138,42 @@ class DecodeKernels:
         _check_dtype(gu, torch.float16, "gu")
         self._call(self.lib.dk_gemv_w4a16_swiglu, int(stage), int(R), int(warps), int(pf), packed.data_ptr(),
                    sz.data_ptr(), gu.data_ptr(), y.data_ptr(), N, K, int(group), _stream(gu))
+
+    # gemv_w4a16 of the interleaved gate|up rows followed by swiglu (kernels/bindings.cpp:27-38, 74-79), one launch;
+    # the input is x itself (norm_w None) or the residual + RMSNorm of gemv_w4a16_rmsnorm
+    def gemv_w4a16_gate_up(self, stage, R, warps, pf, packed, sz, x, row, delta, norm_w, eps, x_out, act, group):
+        for t, n in ((packed, "packed"), (sz, "sz"), (x, "x"), (act, "act")):
+            _check_cuda(t, n)
+        K = packed.size(1) * 8
+        N = packed.size(0)
+        if N % 2 != 0 or act.numel() * 2 != N or sz.size(0) != N or sz.size(1) != K // group:
+            raise RuntimeError("gemv_w4a16_gate_up: packed/sz need 2I interleaved rows and act I entries")
+        _check_dtype(packed, torch.int32, "packed")
+        _check_dtype(sz, torch.float16, "sz")
+        _check_dtype(act, torch.float16, "act")
+        _check_dtype(x, torch.float16, "x")
+        if norm_w is None:
+            if row is not None or delta is not None or x_out is not None or x.numel() != K:
+                raise RuntimeError("gemv_w4a16_gate_up: without norm_w, x must hold K values and row/delta/x_out be None")
+        else:
+            _check_cuda(norm_w, "norm_w")
+            _check_dtype(norm_w, torch.float16, "norm_w")
+            if norm_w.numel() != K:
+                raise RuntimeError("gemv_w4a16_gate_up: norm_w must hold K values")
+            if row is None and x.numel() != K:
+                raise RuntimeError("gemv_w4a16_gate_up: x must hold K values (or be a [*, K] table with row)")
+            if row is not None and (x.dim() != 2 or x.size(1) != K or row.dtype != torch.int64 or delta is not None):
+                raise RuntimeError("gemv_w4a16_gate_up: row needs an int64 index into a [*, K] x and no delta")
+            for t, n in ((delta, "delta"), (x_out, "x_out"), (row, "row")):
+                if t is not None:
+                    _check_cuda(t, n)
+            for t, n in ((delta, "delta"), (x_out, "x_out")):
+                if t is not None and (t.numel() != K or t.dtype != torch.float16):
+                    raise RuntimeError(f"gemv_w4a16_gate_up: {n} must be fp16 [K]")
+        ptr = lambda t: None if t is None else t.data_ptr()
+        self._call(self.lib.dk_gemv_w4a16_gate_up, int(stage), int(R), int(warps), int(pf), packed.data_ptr(),
+                   sz.data_ptr(), x.data_ptr(), ptr(row), ptr(delta), ptr(norm_w), float(eps), ptr(x_out),
+                   act.data_ptr(), N, K, int(group), _stream(x))
 
     # kernels/bindings.cpp:40-43
     def bw_read(self, buf, sink, blocks, threads, unroll):

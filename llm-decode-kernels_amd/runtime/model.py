@@ -19,7 +19,8 @@ Differences from the reference, all on the device side of the same composition:
 Knobs (DecodeConfig): weights "int4" | "fp16"; group; lm_head "auto" | "fp16" | "int4"; fused (False runs the
 HF-style torch op sequences for norm and SwiGLU on the GPU, the reference's unfused comparison point); max_ctx, page,
 part_size (0 -> attention policy table), attn_version, gemv_stage ((stage, R, warps, pf) forced everywhere, or None for
-the tuning table), autotune_path, attn_policy_path, shuffle_pages, device.
+the tuning table), autotune_path, attn_policy_path, shuffle_pages, device; fused_attention, fused_gemv and swiglu
+select the MI355X launch fusions (each one is checked against the unfused composition by the GPU tests).
 """
 import json
 import math
@@ -57,8 +58,10 @@ class DecodeConfig:
                                    # rope_append + paged_attention
     fused_gemv: bool = True        # residual + RMSNorm (and the embedding gather) computed inside the INT4 GEMV that
                                    # consumes it (dk_gemv_w4a16_rmsnorm) instead of a separate add_rmsnorm kernel
-    fused_swiglu: bool = False     # SwiGLU inside the down GEMV (dk_gemv_w4a16_swiglu): every workgroup re-evaluates
-                                   # silu for its columns, measured slower than the separate kernel on MI355X
+    swiglu: str = "epilogue"       # where SwiGLU runs when fused_gemv is on: "epilogue" = inside the gate|up GEMV
+                                   # (dk_gemv_w4a16_gate_up, gate/up rows stored interleaved); "prologue" = inside the
+                                   # down GEMV (dk_gemv_w4a16_swiglu: every workgroup re-evaluates silu for its columns,
+                                   # slower on MI355X); "kernel" = the separate dk_swiglu launch
 
 
 def default_gemv_config(N, K):
@@ -71,11 +74,16 @@ def default_gemv_config(N, K):
 
 
 class Linear:
-    """One projection in the format the config asks for (runtime/model.py:56-72)."""
+    """One projection in the format the config asks for (runtime/model.py:56-72).
 
-    def __init__(self, w, cfg: DecodeConfig, quant: bool):
+    ``pairs_interleaved``: the rows of a [gate; up] stack are stored as gate_0, up_0, gate_1, up_1, ... (the layout
+    dk_gemv_w4a16_gate_up reads); quantization is per row, so this is a pure row permutation of the stacked
+    quantization. ``rows_reference_order`` undoes it for anything that needs the reference's row order."""
+
+    def __init__(self, w, cfg: DecodeConfig, quant: bool, interleave_pairs: bool = False):
         self.N, self.K = w.shape
         self.quant = quant
+        self.pairs_interleaved = interleave_pairs and quant
         dev = cfg.device
         if quant:
             if cfg.quant != "rtn":
@@ -83,9 +91,27 @@ class Linear:
             ql = QuantLinear(w.to(dev), cfg.group)
             self.packed, self.sz = ql.packed, ql.sz
             self.nbytes = ql.nbytes()
+            if self.pairs_interleaved:
+                self.packed = interleave_halves(self.packed)
+                self.sz = interleave_halves(self.sz)
         else:
             self.w = w.to(dev).half().contiguous()
             self.nbytes = self.w.numel() * 2
+
+    def rows_reference_order(self, t):
+        """A per-row tensor of this projection (dequantized weight, packed, sz) in the reference's [gate; up] order."""
+        return deinterleave_halves(t) if self.pairs_interleaved else t
+
+
+def interleave_halves(t):
+    """[a_0 .. a_{n-1}, b_0 .. b_{n-1}] rows -> [a_0, b_0, a_1, b_1, ...]."""
+    n = t.size(0) // 2
+    return t.view(2, n, *t.shape[1:]).transpose(0, 1).contiguous().view(t.shape)
+
+
+def deinterleave_halves(t):
+    n = t.size(0) // 2
+    return t.view(n, 2, *t.shape[1:]).transpose(0, 1).contiguous().view(t.shape)
 
 
 class Model:
@@ -105,6 +131,10 @@ class Model:
         dev = cfg.device
         self.K = ext.load()
         quant = cfg.weights == "int4"
+        if cfg.swiglu not in ("epilogue", "prologue", "kernel"):
+            raise ValueError(f"swiglu {cfg.swiglu!r}: 'epilogue', 'prologue' or 'kernel'")
+        self.use_fused_gemv = (cfg.fused and cfg.fused_gemv and quant and self.H <= 32768 and self.I <= 32768)
+        self.gate_up_epilogue = self.use_fused_gemv and cfg.swiglu == "epilogue"
         sd = hf_state
         g = lambda k: sd[k].half()
         self.emb = g("model.embed_tokens.weight").to(dev).contiguous()
@@ -116,7 +146,7 @@ class Model:
             qkv = Linear(wqkv, cfg, quant)
             del wqkv
             wgu = torch.cat([g(p + "mlp.gate_proj.weight"), g(p + "mlp.up_proj.weight")], 0)
-            gu = Linear(wgu, cfg, quant)
+            gu = Linear(wgu, cfg, quant, interleave_pairs=self.gate_up_epilogue)
             del wgu
             self.layers.append({
                 "ln1": g(p + "input_layernorm.weight").to(dev).contiguous(),
@@ -128,12 +158,12 @@ class Model:
         head_int4 = cfg.lm_head == "int4" or (cfg.lm_head == "auto" and quant)
         self.lm_head = Linear(lm.half(), cfg, head_int4)
 
-        self.gemv_table, self.gemv_tile_table, self.gemv_norm_table = {}, {}, {}
+        self.gemv_table, self.gemv_tile_table, self.gemv_norm_table, self.gemv_gate_up_table = {}, {}, {}, {}
         if cfg.gemv_stage is None and Path(cfg.autotune_path).exists():
             tab = json.load(open(cfg.autotune_path))
             self.gemv_table, self.gemv_tile_table = tab.get("best", {}), tab.get("best_tile", {})
             self.gemv_norm_table = tab.get("best_norm", {})
-        self.use_fused_gemv = (cfg.fused and cfg.fused_gemv and quant and self.H <= 32768 and self.I <= 32768)
+            self.gemv_gate_up_table = tab.get("best_gate_up", {})
 
         # paged KV cache [L, 2, pages, n_kv, P, D]; one block table shared by all layers (one sequence)
         self.n_pages = (cfg.max_ctx + cfg.page - 1) // cfg.page + 1
@@ -226,6 +256,23 @@ class Model:
         self.K.gemv_w4a16_rmsnorm(s, r, wv, pf, lin.packed, lin.sz, x_in, row, delta, w, self.eps, x_out, y,
                                   self.cfg.group)
 
+    def gemv_gate_up_cfg(self, lin):
+        """Configuration of the gate|up GEMV with the SwiGLU epilogue: its tuned entry, else the fused-norm one; the
+        row tile R * 2^pf must hold a gate/up pair."""
+        key = f"{lin.N}x{lin.K}_G{self.cfg.group}"
+        e = self.gemv_gate_up_table.get(key) or self.gemv_norm_table.get(key) or (4, 4, 0, 1)
+        s, r, wv, pf = e
+        if (r << pf) < 2:
+            r = 2
+        return s, r, wv, pf
+
+    def linear_gate_up(self, lin: Linear, x_in, delta, w, x_out, act):
+        """act = swiglu(W_gu . rmsnorm(x_in + delta)) with x_out <- x_in + delta, one launch (dk_gemv_w4a16_gate_up
+        over the interleaved gate/up rows)."""
+        s, r, wv, pf = self.gemv_gate_up_cfg(lin)
+        self.K.gemv_w4a16_gate_up(s, r, wv, pf, lin.packed, lin.sz, x_in, None, delta, w, self.eps, x_out, act,
+                                  self.cfg.group)
+
     def linear_swiglu(self, lin: Linear, gu, y):
         s, r, wv, pf = self.gemv_tile_cfg(lin)
         self.K.gemv_w4a16_swiglu(s, r, wv, pf, lin.packed, lin.sz, gu, y, self.cfg.group)
@@ -286,9 +333,9 @@ class Model:
 
     def step_fused(self):
         """The same composition with every residual + RMSNorm inside the GEMV that consumes it (the layer-0 one also
-        gathers the embedding row of the device token): per layer qkv, attention (split + combine), o, gate|up,
-        SwiGLU, down = 7 launches. The residual stream alternates between two buffers because a fused GEMV's
-        workgroups all read x_in while workgroup 0 writes x_in + delta."""
+        gathers the embedding row of the device token) and, by default, SwiGLU in the gate|up GEMV's epilogue: per
+        layer qkv, attention (split + combine), o, gate|up, down = 6 launches. The residual stream alternates between
+        two buffers because a fused GEMV's workgroups all read x_in while workgroup 0 writes x_in + delta."""
         cur, nxt = self.x, self.x_alt
         delta = None
         for li, lw in enumerate(self.layers):
@@ -299,13 +346,18 @@ class Model:
                 cur, nxt = nxt, cur
             self.attention(li)
             self.linear(lw["o"], self.attn.view(-1), self.o)
-            self.linear_norm(lw["gu"], cur, self.o, lw["ln2"], nxt, self.gu)
-            cur, nxt = nxt, cur
-            if self.cfg.fused_swiglu:
-                self.linear_swiglu(lw["down"], self.gu, self.down)
-            else:
-                self.K.swiglu(self.gu, self.act)
+            if self.gate_up_epilogue:
+                self.linear_gate_up(lw["gu"], cur, self.o, lw["ln2"], nxt, self.act)
+                cur, nxt = nxt, cur
                 self.linear(lw["down"], self.act, self.down)
+            else:
+                self.linear_norm(lw["gu"], cur, self.o, lw["ln2"], nxt, self.gu)
+                cur, nxt = nxt, cur
+                if self.cfg.swiglu == "prologue":
+                    self.linear_swiglu(lw["down"], self.gu, self.down)
+                else:
+                    self.K.swiglu(self.gu, self.act)
+                    self.linear(lw["down"], self.act, self.down)
             delta = self.down
         if self.lm_head.quant:
             self.linear_norm(self.lm_head, cur, delta, self.norm_f, None, self.logits)

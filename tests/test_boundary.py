@@ -123,6 +123,45 @@ def test_attention_decode_validation(lib, kw, code, msg):
     assert rc == code and msg in m, (rc, m)
 
 
+B16 = 0x20000
+
+
+def _fused(lib, fn, **kw):
+    a = dict(stage=4, R=2, warps=0, pf=0, packed=A16, sz=A16, x=A16, row=None, delta=None, norm_w=A16, eps=1e-5,
+             x_out=None, y=B16, N=64, K=256, group=128)
+    a.update(kw)
+    return _err(lib, fn(*a.values(), None))
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(stage=2), 4, "stage 4 only"),
+    (dict(N=63), 3, "must be even"),
+    (dict(R=1, pf=0), 4, "gate/up pair"),
+    (dict(norm_w=None, delta=A16), 4, "belong to the RMSNorm input"),
+    (dict(norm_w=None, x_out=B16 + 0x1000), 4, "belong to the RMSNorm input"),
+    (dict(x_out=A16), 4, "x_out must not alias"),
+    (dict(y=A16), 4, "act must not alias"),
+    (dict(norm_w=A16 + 8), 2, "16B aligned"),
+    (dict(row=A16 + 4), 2, "row must be 8B aligned"),
+    (dict(K=32800, group=32), 3, "K <= 32768"),
+    (dict(y=None), 1, "null"),
+])
+def test_gate_up_validation(lib, kw, code, msg):
+    rc, m = _fused(lib, lib.dk_gemv_w4a16_gate_up, **kw)
+    assert rc == code and msg in m, (rc, m)
+
+
+def test_fused_gemv_validation(lib):
+    assert _fused(lib, lib.dk_gemv_w4a16_rmsnorm, stage=3)[0] == 4
+    assert _fused(lib, lib.dk_gemv_w4a16_rmsnorm, norm_w=None)[0] == 1
+    assert _fused(lib, lib.dk_gemv_w4a16_rmsnorm, x_out=A16)[0] == 4
+    assert _fused(lib, lib.dk_gemv_w4a16_rmsnorm, pf=4)[0] == 4
+    sw = lambda **kw: _err(lib, lib.dk_gemv_w4a16_swiglu(*dict(dict(stage=4, R=2, warps=0, pf=0, packed=A16, sz=A16,
+                                                                    gu=A16, y=B16, N=64, K=256, group=128),
+                                                               **kw).values(), None))
+    assert sw(gu=A16 + 2)[0] == 2 and sw(R=3)[0] == 4 and sw(N=0)[0] == 3
+
+
 def test_small_op_validation(lib):
     assert _err(lib, lib.dk_add_rmsnorm(A16, None, A16, A16, 2047, 1e-5, None))[0] == 3
     assert _err(lib, lib.dk_add_rmsnorm(A16 + 2, None, A16, A16, 2048, 1e-5, None))[0] == 2

@@ -379,19 +379,61 @@ def test_gemv_swiglu_fused(K, N, Kd):
         assert_close(y, ref, 5e-3, f"gemv_swiglu {N}x{Kd} {cfg}")
 
 
+@pytest.mark.parametrize("I,Kd", [(5632, 2048), (14336, 4096), (40, 256), (1000, 5632)])
+@pytest.mark.parametrize("norm", (False, True))
+def test_gemv_gate_up_swiglu_epilogue(K, I, Kd, norm):
+    """act = swiglu(W_gu . x) in one launch over interleaved gate/up rows. Against the oracle (gemv_ref then
+    swiglu_ref on the [gate; up] stack) within the GEMV tolerance, and bit-exact against the two separate HIP ops
+    (gemv_w4a16 / gemv_w4a16_rmsnorm on the stacked rows, then swiglu): the epilogue rounds exactly where they do.
+    I = 40 and 1000 leave a partial last tile."""
+    from runtime.model import interleave_halves
+    G = 128
+    w, packed, sz = _quantized(K, 2 * I, Kd, G, seed=I + Kd)
+    wref = dequant_from_gpu(packed, sz, G)
+    pk_il, sz_il = interleave_halves(packed), interleave_halves(sz)
+    g = gen(I * 5 + Kd)
+    x = (torch.randn(Kd, generator=g) * (1 if norm else 0.5)).half()
+    d = torch.randn(Kd, generator=g).half() if norm else None
+    nw = (1 + 0.1 * torch.randn(Kd, generator=g)).half() if norm else None
+    if norm:
+        xr, xin = R.add_rmsnorm_ref(x, d, nw, 1e-5)
+    else:
+        xin = x
+    ref = R.swiglu_ref(R.gemv_ref(wref, xin))
+    act = torch.empty(I, dtype=torch.half, device=DEV)
+    gu = torch.empty(2 * I, dtype=torch.half, device=DEV)
+    sep = torch.empty(I, dtype=torch.half, device=DEV)
+    x_out = torch.zeros(Kd, dtype=torch.half, device=DEV) if norm else None
+    xd = x.to(DEV)
+    for cfg in ((4, 2, 0, 0), (4, 1, 0, 1), (4, 4, 0, 2), (4, 8, 0, 3)):
+        if norm:
+            K.gemv_w4a16_gate_up(*cfg, pk_il, sz_il, xd, None, d.to(DEV), nw.to(DEV), 1e-5, x_out, act, G)
+            K.gemv_w4a16_rmsnorm(*cfg, packed, sz, xd, None, d.to(DEV), nw.to(DEV), 1e-5,
+                                 torch.empty_like(xd), gu, G)
+            assert torch.equal(x_out.cpu(), xr), f"residual {cfg}"
+        else:
+            K.gemv_w4a16_gate_up(*cfg, pk_il, sz_il, xd, None, None, None, 0.0, None, act, G)
+            K.gemv_w4a16(*cfg, packed, sz, xd, gu, G)
+        K.swiglu(gu, sep)
+        assert_close(act, ref, 5e-3, f"gate_up I{I} K{Kd} norm={norm} {cfg}")
+        assert torch.equal(act, sep), f"gate_up vs gemv + swiglu I{I} K{Kd} norm={norm} {cfg}"
+
+
 def test_fused_step_equals_unfused_step(K):
-    """The decode step with fused prologues and the one with separate norm / SwiGLU kernels give the same logits
-    (same rounding points; only the sum-of-squares order may differ) and the same tokens."""
+    """The decode step with fused prologues / epilogue and the one with separate norm / SwiGLU kernels give the same
+    logits (same rounding points; only the sum-of-squares order may differ)."""
     from runtime.model import DecodeConfig, Model
     from runtime.synth import LlamaShape, SyntheticLlama
     shape = LlamaShape(512, 3, 8, 2, 1024, 700)
     out = []
-    for fused, swiglu in ((False, False), (True, False), (True, True)):
+    for fused, swiglu in ((False, "kernel"), (True, "kernel"), (True, "prologue"), (True, "epilogue")):
         m = Model(SyntheticLlama(shape, seed=4, device=DEV, std=0.05), shape,
-                  DecodeConfig(max_ctx=64, device=DEV, fused_gemv=fused, fused_swiglu=swiglu))
+                  DecodeConfig(max_ctx=64, device=DEV, fused_gemv=fused, swiglu=swiglu))
         m.prepare(64)
         m.reset(0)
         out.append(m.teacher_force([1, 5, 99, 400, 12], collect_logits=True).float().cpu())
     for o in out[1:]:
         err = ((o - out[0]).abs().max() / out[0].abs().max()).item()
         assert err <= 5e-3, err
+    # the gate|up SwiGLU epilogue rounds exactly where the separate swiglu kernel does
+    assert torch.equal(out[1], out[3])
