@@ -120,12 +120,23 @@ rope_append_kernel(f16* __restrict__ qkv, const float* __restrict__ cos_t, const
 // ---------------------------------------------------------------------------------------------------------------
 // Greedy token pick closing the decode step: tok = argmax(logits) (lowest index among equal maxima, NaN counts as
 // largest like torch.argmax), then *pos += 1 when pos is given (runtime/model.py:232-233 of the reference as one
-// launch). One workgroup of 1024 threads.
+// launch). One workgroup of 1024 threads: each thread issues all of its 16-byte chunks of a batch (kArgmaxBatch per
+// thread) before comparing, so the whole vector is in flight at once instead of one 2-byte load per step; a scalar
+// head and tail cover a logits pointer that is not 16-byte aligned and V % 8.
+constexpr int kArgmaxBatch = 4;
+
 __device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
   const bool na = a != a, nb = b != b;
   if (na != nb) return na;
   if (!na && a != b) return a > b;
   return ia < ib;
+}
+
+__device__ __forceinline__ void take(float v, int i, float& bv, int& bi) {
+  if (better(v, i, bv, bi)) {
+    bv = v;
+    bi = i;
+  }
 }
 
 __global__ void __launch_bounds__(1024)
@@ -135,21 +146,39 @@ argmax_advance_kernel(const f16* __restrict__ logits, int V, int64_t* __restrict
   const int tid = threadIdx.x, nt = blockDim.x;
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int i = tid; i < V; i += nt) {
-    const float v = (float)logits[i];
-    if (better(v, i, bv, bi)) {
-      bv = v;
-      bi = i;
+  // elements [0, h) before the first 16-byte boundary, chunks of 8 over [h, h + 8 * nc), scalar tail after
+  const int h = min(V, (int)(((16u - ((uint32_t)(uintptr_t)logits & 15u)) & 15u) >> 1));
+  const int nc = (V - h) >> 3;
+  if (tid < h) take((float)logits[tid], tid, bv, bi);
+  const u32x4* C = reinterpret_cast<const u32x4*>(logits + h);
+  for (int c0 = tid; c0 < nc; c0 += kArgmaxBatch * nt) {
+    u32x4 v[kArgmaxBatch];
+#pragma unroll
+    for (int b = 0; b < kArgmaxBatch; ++b) {
+      const int c = c0 + b * nt;
+      v[b] = c < nc ? C[c] : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int b = 0; b < kArgmaxBatch; ++b) {
+      const int c = c0 + b * nt;
+      if (c < nc) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const f16x2 p = as_f16x2(v[b][e]);
+          const int i = h + 8 * c + 2 * e;
+          take((float)p.x, i, bv, bi);
+          take((float)p.y, i + 1, bv, bi);
+        }
+      }
     }
   }
+  const int t0 = h + 8 * nc;
+  if (t0 + tid < V) take((float)logits[t0 + tid], t0 + tid, bv, bi);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float ov = __shfl_xor(bv, o, kWave);
     const int oi = __shfl_xor(bi, o, kWave);
-    if (better(ov, oi, bv, bi)) {
-      bv = ov;
-      bi = oi;
-    }
+    take(ov, oi, bv, bi);
   }
   if ((tid & 63) == 0) {
     sv[tid >> 6] = bv;
@@ -157,11 +186,7 @@ argmax_advance_kernel(const f16* __restrict__ logits, int V, int64_t* __restrict
   }
   __syncthreads();
   if (tid == 0) {
-    for (int w = 1; w < (nt >> 6); ++w)
-      if (better(sv[w], si[w], bv, bi)) {
-        bv = sv[w];
-        bi = si[w];
-      }
+    for (int w = 1; w < (nt >> 6); ++w) take(sv[w], si[w], bv, bi);
     tok[0] = (int64_t)bi;
     if (pos != nullptr) pos[0] += 1;
   }

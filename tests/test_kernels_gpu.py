@@ -290,6 +290,29 @@ def test_argmax_advance(K, V):
     assert int(pos) == 42
 
 
+@pytest.mark.parametrize("V", (1, 5, 8, 9, 31999, 32000, 128256))
+@pytest.mark.parametrize("offset", (0, 1, 3, 7))
+def test_argmax_edges(K, V, offset):
+    """Unaligned starts (scalar head), V % 8 tails, maxima in the head / tail / across batches, NaN (ranks highest,
+    first NaN wins) and an all -inf vector (index 0), each against torch.argmax on the CPU."""
+    base = torch.randn(V + offset, generator=gen(V * 8 + offset)).half()
+    cases = [base.clone()]
+    for where in (0, V - 1, V // 2, min(V - 1, 9000)):
+        t = base.clone()
+        t[offset + where] = 60.0
+        cases.append(t)
+    t = base.clone()
+    t[offset + V - 1] = float("nan")
+    t[offset + V // 3] = float("nan")
+    cases.append(t)
+    cases.append(torch.full((V + offset,), float("-inf"), dtype=torch.half))
+    tok = torch.zeros(1, dtype=torch.long, device=DEV)
+    for c in cases:
+        dev = c.to(DEV)[offset:]
+        K.argmax_advance(dev, tok, None)
+        assert int(tok) == int(torch.argmax(c[offset:].float())), (V, offset)
+
+
 def test_graph_replay_of_ops(K):
     """rope -> attention -> GEMV captured into one hipGraph; each replay (with eager work between replays) equals the
     eager result, and the graph reads the device-resident position anew on every replay."""
