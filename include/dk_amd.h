@@ -99,6 +99,23 @@ int dk_gemv_w4a16_gate_up(int stage, int R, int warps, int pf, const void* packe
                           int N, int K, int group, void* stream);
 
 /*
+ * fp16-weight GEMV y[N] = W[N, K] . x[K] (W row-major fp16, fp32 accumulation, fp16 out). Replaces the fp16 LM head's
+ * torch.mm(x, W^T) (runtime/model.py:187 of the reference; cuBLAS there, no custom kernel). R rows per tile (1, 2, 4),
+ * warps waves per workgroup (0 = 4; 1, 2, 4, 8), 2^pf tiles per wave (pf 0..3). K % 8 == 0, K <= 4096 and
+ * R * ceil(K / 512) rounded up to a power of two <= 16. w and x 16-byte aligned.
+ */
+int dk_gemv_f16(int R, int warps, int pf, const void* w, const void* x, void* y, int N, int K, void* stream);
+
+/*
+ * dk_gemv_f16 whose input is the residual + RMSNorm of dk_add_rmsnorm: x_out (optional, must not alias x or delta)
+ * receives x + delta (fp16 add; delta may be NULL) and y = W . (norm_w * fp16(float(x + delta) * r)),
+ * r = 1 / sqrt(sum / K + eps). Fuses the decode step's final add_rmsnorm with the fp16 LM head
+ * (kernels/bindings.cpp:64-72 then runtime/model.py:187; no counterpart in the reference's binding).
+ */
+int dk_gemv_f16_rmsnorm(int R, int warps, int pf, const void* w, const void* x, const void* delta, const void* norm_w,
+                        float eps, void* x_out, void* y, int N, int K, void* stream);
+
+/*
  * Achievable-read-bandwidth microbenchmark: reads `bytes` (multiple of 16) from buf, XOR-folds them and writes sink
  * (uint32[1]) only on a value it never takes. Replaces bw_read (kernels/bindings.cpp:40-43,
  * kernels/gemv_w4a16.cu:133-153). unroll in {1, 4}; threads a multiple of 64 in [64, 1024]; blocks >= 1.

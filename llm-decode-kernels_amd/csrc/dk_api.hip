@@ -152,6 +152,51 @@ int dk_gemv_w4a16_gate_up(int stage, int R, int warps, int pf, const void* packe
   return launched("gemv_w4a16_gate_up");
 }
 
+// Checks shared by the fp16 GEMVs.
+static int check_gemv_f16(const char* what, int R, int warps, int pf, const void* w, const void* x, const void* y,
+                          int N, int K) {
+  if (!w || !x || !y) return fail(DK_ERR_NULL, "%s: null pointer argument", what);
+  if (R != 1 && R != 2 && R != 4) return fail(DK_ERR_DOMAIN, "%s: R must be 1, 2 or 4, got %d", what, R);
+  if (warps != 0 && warps != 1 && warps != 2 && warps != 4 && warps != 8)
+    return fail(DK_ERR_DOMAIN, "%s: warps must be 0 (default), 1, 2, 4 or 8, got %d", what, warps);
+  if (pf < 0 || pf > 3) return fail(DK_ERR_DOMAIN, "%s: pf must be 0..3, got %d", what, pf);
+  if (N <= 0 || K <= 0) return fail(DK_ERR_SHAPE, "%s: N and K must be positive (N=%d K=%d)", what, N, K);
+  if (K % 8 != 0 || K > dk::kGemvF16MaxK)
+    return fail(DK_ERR_SHAPE, "%s: K must be a multiple of 8 and <= %d, got %d", what, dk::kGemvF16MaxK, K);
+  const int chunks = ((K >> 3) + 63) / 64;
+  const int c_pow2 = chunks <= 1 ? 1 : chunks <= 2 ? 2 : chunks <= 4 ? 4 : 8;
+  if (R * c_pow2 > dk::kGemvF16MaxLoads)
+    return fail(DK_ERR_DOMAIN, "%s: R * %d chunks per lane exceeds %d loads per tile (K=%d: R <= %d)", what, c_pow2,
+                dk::kGemvF16MaxLoads, K, dk::kGemvF16MaxLoads / c_pow2);
+  if (!aligned16(w) || !aligned16(x)) return fail(DK_ERR_ALIGN, "%s: w and x must be 16B aligned", what);
+  if (reinterpret_cast<uintptr_t>(y) & 1u) return fail(DK_ERR_ALIGN, "%s: y must be 2B aligned", what);
+  return DK_OK;
+}
+
+int dk_gemv_f16(int R, int warps, int pf, const void* w, const void* x, void* y, int N, int K, void* stream) {
+  const int rc = check_gemv_f16("gemv_f16", R, warps, pf, w, x, y, N, K);
+  if (rc != DK_OK) return rc;
+  clear_error();
+  dk::GemvInput in{x, nullptr, nullptr, nullptr, 0.f, nullptr};
+  dk::launch_gemv_f16(0, R, warps, pf, w, in, y, N, K, (hipStream_t)stream);
+  return launched("gemv_f16");
+}
+
+int dk_gemv_f16_rmsnorm(int R, int warps, int pf, const void* w, const void* x, const void* delta, const void* norm_w,
+                        float eps, void* x_out, void* y, int N, int K, void* stream) {
+  const int rc = check_gemv_f16("gemv_f16_rmsnorm", R, warps, pf, w, x, y, N, K);
+  if (rc != DK_OK) return rc;
+  if (!norm_w) return fail(DK_ERR_NULL, "gemv_f16_rmsnorm: null pointer argument");
+  if (!aligned16(norm_w) || (delta && !aligned16(delta)) || (x_out && !aligned16(x_out)))
+    return fail(DK_ERR_ALIGN, "gemv_f16_rmsnorm: delta, norm_w and x_out must be 16B aligned");
+  if (x_out && (x_out == x || (delta && x_out == delta)))
+    return fail(DK_ERR_DOMAIN, "gemv_f16_rmsnorm: x_out must not alias x or delta (other waves still read them)");
+  clear_error();
+  dk::GemvInput in{x, nullptr, delta, norm_w, eps, x_out};
+  dk::launch_gemv_f16(1, R, warps, pf, w, in, y, N, K, (hipStream_t)stream);
+  return launched("gemv_f16_rmsnorm");
+}
+
 int dk_bw_read(const void* buf, size_t bytes, void* sink, int blocks, int threads, int unroll, void* stream) {
   if (!buf || !sink) return fail(DK_ERR_NULL, "bw_read: null pointer argument");
   if (!aligned16(buf)) return fail(DK_ERR_ALIGN, "buf must be 16B aligned");

@@ -319,50 +319,71 @@ __device__ __forceinline__ void tile_rows(const u32x4 (&w)[T], const uint32_t (&
 //               value = norm_w * fp16(float(xn) * r). Workgroup 0 writes xn to x_out (a different buffer: every other
 //               workgroup still reads xi).
 //   kInSwiglu   fp16(silu(float(gate))) * up with gate = x[0..I), up = x[I..2I), K == I (kernels/fused_swiglu.cu:7-21).
+// Split in two: tile_input_load issues the operand loads and tile_input_finish computes the operand. The loads are
+// issued before any weight load of the workgroup: a wave's vector loads return in issue order, so operand loads
+// issued after the weights would wait behind an HBM round trip and hold back the prologue and the next tile's loads.
 enum { kInPlain = 0, kInRmsNorm = 1, kInSwiglu = 2 };
 
+struct TileRaw {
+  u32x4 a[4];  // x / gate / residual
+  u32x4 b[4];  // up / delta
+  u32x4 c[4];  // norm weight
+};
+
 template <int PRO>
-__device__ __forceinline__ void tile_input(const GemvInput& in, int uc, bool live, int K, float* s_ss, int wave,
-                                           int nw, u32x4 (&xc)[4]) {
+__device__ __forceinline__ void tile_input_load(const GemvInput& in, int uc, int K, TileRaw& raw) {
   if constexpr (PRO == kInPlain) {
     const u32x4* X = reinterpret_cast<const u32x4*>(in.x);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) xc[k] = X[4 * uc + k];
+    for (int k = 0; k < 4; ++k) raw.a[k] = X[4 * uc + k];
   } else if constexpr (PRO == kInSwiglu) {
     const u32x4* G = reinterpret_cast<const u32x4*>(in.x);
     const u32x4* Up = G + (K >> 3);
-    u32x4 g[4], up[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      g[k] = G[4 * uc + k];
-      up[k] = Up[4 * uc + k];
+      raw.a[k] = G[4 * uc + k];
+      raw.b[k] = Up[4 * uc + k];
     }
+  } else {
+    const long long off = in.row != nullptr ? (long long)(*in.row) * (K >> 3) : 0;
+    const u32x4* X = reinterpret_cast<const u32x4*>(in.x) + off;
+    const u32x4* Wn = reinterpret_cast<const u32x4*>(in.norm_w);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      raw.a[k] = X[4 * uc + k];
+      raw.c[k] = Wn[4 * uc + k];
+    }
+    if (in.delta != nullptr) {
+      const u32x4* Dl = reinterpret_cast<const u32x4*>(in.delta);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) raw.b[k] = Dl[4 * uc + k];
+    }
+  }
+}
+
+template <int PRO>
+__device__ __forceinline__ void tile_input_finish(const GemvInput& in, TileRaw& raw, int uc, bool live, int K,
+                                                  float* s_ss, int wave, int nw, u32x4 (&xc)[4]) {
+  if constexpr (PRO == kInPlain) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xc[k] = raw.a[k];
+  } else if constexpr (PRO == kInSwiglu) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const f16x2 g2 = as_f16x2(g[k][e]), u2 = as_f16x2(up[k][e]);
+        const f16x2 g2 = as_f16x2(raw.a[k][e]), u2 = as_f16x2(raw.b[k][e]);
         const f16x2 r = {silu_mul(g2.x, u2.x), silu_mul(g2.y, u2.y)};
         xc[k][e] = as_u32(r);
       }
     }
   } else {
-    const long long off = in.row != nullptr ? (long long)(*in.row) * (K >> 3) : 0;
-    const u32x4* X = reinterpret_cast<const u32x4*>(in.x) + off;
-    const u32x4* Dl = reinterpret_cast<const u32x4*>(in.delta);
-    const u32x4* Wn = reinterpret_cast<const u32x4*>(in.norm_w);
-    u32x4 xr[4], wn[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      xr[k] = X[4 * uc + k];
-      wn[k] = Wn[4 * uc + k];
-    }
-    if (Dl != nullptr) {
+    u32x4 (&xr)[4] = raw.a;
+    if (in.delta != nullptr) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const u32x4 d = Dl[4 * uc + k];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) xr[k][e] = as_u32(as_f16x2(xr[k][e]) + as_f16x2(d[e]));
+        for (int e = 0; e < 4; ++e) xr[k][e] = as_u32(as_f16x2(xr[k][e]) + as_f16x2(raw.b[k][e]));
       }
     }
     float ss = 0.f;
@@ -393,7 +414,7 @@ __device__ __forceinline__ void tile_input(const GemvInput& in, int uc, bool liv
       for (int e = 0; e < 4; ++e) {
         const f16x2 h = as_f16x2(xr[k][e]);
         const f16x2 hn = {(f16)((float)h.x * r), (f16)((float)h.y * r)};
-        xc[k][e] = as_u32(as_f16x2(wn[k][e]) * hn);
+        xc[k][e] = as_u32(as_f16x2(raw.c[k][e]) * hn);
       }
     }
   }
@@ -411,6 +432,9 @@ __device__ __forceinline__ void tile_input(const GemvInput& in, int uc, bool liv
 //               separate ops round it. Needs an even tile (T * NT) so that a pair never straddles two workgroups.
 enum { kOutRows = 0, kOutSwiglu = 1 };
 
+// Pipeline: operand loads, then the weight loads of tiles 0 and 1, then the operand (waits for the operand loads
+// only), then for each tile t: compute it from its buffer and refill that buffer with tile t + 2. Two tiles are in
+// flight from the first instruction on.
 template <int T, int NT, int PRO, int EPI>
 __global__ void __launch_bounds__(1024)
 gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, const GemvInput in,
@@ -425,12 +449,15 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
   const int base = blockIdx.x * T * NT;
   const int NG = U >> gsh;
 
-  u32x4 wa[T], wb[T];
-  uint32_t sa[T], sb[T];
-  tile_issue<T>(W, SZ, base, N, U, NG, uc, gsh, wa, sa);
+  TileRaw raw;
+  tile_input_load<PRO>(in, uc, U << 5, raw);
+  u32x4 w[2][T];
+  uint32_t sz[2][T];
+  tile_issue<T>(W, SZ, base, N, U, NG, uc, gsh, w[0], sz[0]);
+  if constexpr (NT > 1) tile_issue<T>(W, SZ, base + T, N, U, NG, uc, gsh, w[1], sz[1]);
   __builtin_amdgcn_sched_barrier(0);
   u32x4 xc[4];
-  tile_input<PRO>(in, uc, live, U << 5, s_ss, wave, nw, xc);
+  tile_input_finish<PRO>(in, raw, uc, live, U << 5, s_ss, wave, nw, xc);
   const f16x2 one = {(f16)1.0f, (f16)1.0f};
   float SA = 0.f, SB = 0.f;
 #pragma unroll
@@ -443,15 +470,9 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     float v[T];
-    if ((t & 1) == 0) {
-      if (t + 1 < NT) tile_issue<T>(W, SZ, base + (t + 1) * T, N, U, NG, uc, gsh, wb, sb);
-      __builtin_amdgcn_sched_barrier(0);
-      tile_rows<T>(wa, sa, xc, SA, SB, live, v);
-    } else {
-      if (t + 1 < NT) tile_issue<T>(W, SZ, base + (t + 1) * T, N, U, NG, uc, gsh, wa, sa);
-      __builtin_amdgcn_sched_barrier(0);
-      tile_rows<T>(wb, sb, xc, SA, SB, live, v);
-    }
+    tile_rows<T>(w[t & 1], sz[t & 1], xc, SA, SB, live, v);
+    if (t + 2 < NT) tile_issue<T>(W, SZ, base + (t + 2) * T, N, U, NG, uc, gsh, w[t & 1], sz[t & 1]);
+    __builtin_amdgcn_sched_barrier(0);
     if (lane == 63) {
 #pragma unroll
       for (int r = 0; r < T; ++r) red[wave][t * T + r] = v[r];

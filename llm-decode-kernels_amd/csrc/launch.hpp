@@ -28,6 +28,14 @@ void launch_gemv_w4a16_fused(int prologue, int epilogue, int R, int pf, const vo
 // Default configuration for a shape: (stage, R, waves, pf).
 void gemv_default_config(int N, int K, int* stage, int* R, int* waves, int* pf);
 
+// fp16-weight GEMV (the fp16 LM head): each wave owns R-row tiles of whole rows, 2^pf tiles per wave, `waves` waves
+// per workgroup (0 = 4); prologue 0 = plain x, 1 = residual + RMSNorm (GemvInput without row). K <= kGemvF16MaxK and
+// R * ceil(K / 512) <= kGemvF16MaxLoads (16-byte loads per lane per tile).
+constexpr int kGemvF16MaxK = 4096;
+constexpr int kGemvF16MaxLoads = 16;
+void launch_gemv_f16(int prologue, int R, int waves, int pf, const void* w, const GemvInput& in, void* y, int N,
+                     int K, hipStream_t st);
+
 void launch_bw_read(const void* buf, size_t bytes, void* sink, int blocks, int threads, int unroll, hipStream_t st);
 
 // Paged attention arguments. q: the query heads [n_q * D] (reference op) or the fused qkv vector (decode op).

@@ -7,7 +7,9 @@ cold weights (runtime.timing), and writes
 
     configs/autotune.json   {"device": ..., "best": {"NxK_G": [stage, R, warps, pf]}, "best_tile": {the best stage-4
                              entry}, "us": {"NxK_G": us}, "best_norm": {the fused residual + RMSNorm GEMV},
-                             "us_norm": {...}, "grid": [every measurement]}
+                             "best_gate_up": {the gate|up GEMV with the SwiGLU epilogue}, "best_f16" /
+                             "best_f16_norm": {"NxK": [R, waves, pf]} of the fp16 GEMV, "us_*": times,
+                             "grid": [every measurement]}
 
 The runtime (runtime.model.Model.gemv_cfg) reads "best"; 3-element entries [R, warps, pf] of the reference's schema
 are read as stage 2. Run:  python -m runtime.autotune [--shapes tinyllama,llama3_8b,baseline] [--groups 128]
@@ -59,29 +61,51 @@ def candidates(N, K):
     return [c for c in out if not (c[0] == 2 and K > 32768)]
 
 
-def norm_candidates():
-    """stage-4 configurations of the fused residual + RMSNorm GEMV (dk_gemv_w4a16_rmsnorm)."""
-    return [(4, R, 0, pf) for R in (1, 2, 4, 8) for pf in range(4)]
+def fused_candidates(kind):
+    """stage-4 configurations of the fused INT4 GEMVs (the gate|up SwiGLU epilogue needs an even row tile)."""
+    return [(4, R, 0, pf) for R in (1, 2, 4, 8) for pf in range(4) if kind != "gate_up" or (R << pf) >= 2]
 
 
-def tune_norm_shape(Kx, N, K, G, reps=5, log=print):
-    """Best configuration of the fused-norm GEMV for one shape, cold weights; also returns the time of the separate
-    add_rmsnorm + best plain GEMV pair so the runtime can tell whether fusing pays at this shape."""
+def f16_candidates(K):
+    """(R, waves, pf) of the fp16 GEMV: R * 2^ceil(log2(ceil(K / 512))) <= 16 loads per lane per tile."""
+    c = 1 << max(0, (-(-K // 512) - 1).bit_length())
+    return [(R, w, pf) for R in (1, 2, 4) if R * c <= 16 for w in (1, 2, 4, 8) for pf in range(4)]
+
+
+def tune_fused_shape(Kx, kind, N, K, G, reps=5, log=print):
+    """Best configuration of one fused variant for one shape, cold weights:
+       rmsnorm   dk_gemv_w4a16_rmsnorm (qkv, gate|up, INT4 LM head behind a residual + RMSNorm)
+       gate_up   dk_gemv_w4a16_gate_up with the RMSNorm input (the MLP's gate|up + SwiGLU; N = 2I rows)
+       f16       dk_gemv_f16 (fp16 LM head, G unused)
+       f16_norm  dk_gemv_f16_rmsnorm (the fp16 LM head behind the final residual + RMSNorm)"""
     g = torch.Generator(device="cuda").manual_seed(N * 17 + K)
-    packed, sz = quantize_pack((torch.randn(N, K, generator=g, device="cuda") * 0.02).half(), G)
+    w = (torch.randn(N, K, generator=g, device="cuda") * 0.02).half()
     x = torch.randn(K, generator=g, device="cuda").half()
     d = torch.randn(K, generator=g, device="cuda").half()
-    w = torch.ones(K, dtype=torch.half, device="cuda")
-    xo, nrm = torch.empty_like(x), torch.empty_like(x)
+    nw = torch.ones(K, dtype=torch.half, device="cuda")
+    xo = torch.empty_like(x)
     y = torch.empty(N, dtype=torch.half, device="cuda")
-    cold = ColdCopies([packed, sz], n_copies(gemv_bytes(N, K, G)))
+    act = torch.empty(N // 2, dtype=torch.half, device="cuda")
+    if kind in ("f16", "f16_norm"):
+        ops, nb, cands = [w], N * K * 2, f16_candidates(K)
+    else:
+        ops, nb, cands = list(quantize_pack(w, G)), gemv_bytes(N, K, G), fused_candidates(kind)
+    del w
+    cold = ColdCopies(ops, n_copies(nb))
+    call = {
+        "rmsnorm": lambda c, i: Kx.gemv_w4a16_rmsnorm(*c, *cold[i], x, None, d, nw, 1e-5, xo, y, G),
+        "gate_up": lambda c, i: Kx.gemv_w4a16_gate_up(*c, *cold[i], x, None, d, nw, 1e-5, xo, act, G),
+        "f16": lambda c, i: Kx.gemv_f16(*c, cold[i][0], x, y),
+        "f16_norm": lambda c, i: Kx.gemv_f16_rmsnorm(*c, cold[i][0], x, d, nw, 1e-5, None, y),
+    }[kind]
     recs = []
-    for cfg in norm_candidates():
-        _, med = graph_time(lambda i: Kx.gemv_w4a16_rmsnorm(*cfg, *cold[i], x, None, d, w, 1e-5, xo, y, G),
-                            cold.copies, reps)
-        recs.append({"N": N, "K": K, "G": G, "cfg": list(cfg), "median_us": med, "variant": "rmsnorm"})
+    for cfg in cands:
+        _, med = graph_time(lambda i: call(cfg, i), cold.copies, reps)
+        recs.append({"N": N, "K": K, "G": G, "cfg": list(cfg), "median_us": med, "variant": kind,
+                     "gbps": nb / med / 1e3})
     best = min(recs, key=lambda r: r["median_us"])
-    log(f"  norm {N}x{K} G{G}: best {best['cfg']} {best['median_us']:.2f} us; {len(recs)} configs")
+    log(f"  {kind} {N}x{K}: best {best['cfg']} {best['median_us']:.2f} us {best['gbps']:.0f} GB/s; "
+        f"{len(recs)} configs")
     del cold
     return best, recs
 
@@ -109,9 +133,18 @@ def tune_shape(Kx, N, K, G, reps=5, log=print):
     return best, recs
 
 
-# GEMVs that consume a residual + RMSNorm in the decode step (qkv, gate|up, INT4 LM head)
-NORM_SHAPES = {"tinyllama": ((2560, 2048), (11264, 2048), (32000, 2048)),
-               "llama3_8b": ((6144, 4096), (28672, 4096), (128256, 4096)), "baseline": ()}
+# Shapes of the fused variants in the decode step: INT4 GEMVs behind a residual + RMSNorm (qkv, INT4 LM head), the
+# gate|up GEMV with the SwiGLU epilogue, and the fp16 LM head (plain and behind the final norm)
+FUSED_SHAPES = {
+    "tinyllama": {"rmsnorm": ((2560, 2048), (11264, 2048), (32000, 2048)), "gate_up": ((11264, 2048),),
+                  "f16": ((32000, 2048),), "f16_norm": ((32000, 2048),)},
+    "llama3_8b": {"rmsnorm": ((6144, 4096), (28672, 4096), (128256, 4096)), "gate_up": ((28672, 4096),),
+                  "f16": ((128256, 4096),), "f16_norm": ((128256, 4096),)},
+    "baseline": {},
+}
+# table name in configs/autotune.json per variant, and whether its key carries the group size
+TABLES = {"rmsnorm": ("best_norm", True), "gate_up": ("best_gate_up", True), "f16": ("best_f16", False),
+          "f16_norm": ("best_f16_norm", False)}
 
 
 def tune(shape_sets=("tinyllama", "llama3_8b", "baseline"), groups=(128,), reps=5, path=CONFIG, log=print):
@@ -119,14 +152,17 @@ def tune(shape_sets=("tinyllama", "llama3_8b", "baseline"), groups=(128,), reps=
     old = json.load(open(path)) if pathlib.Path(path).exists() else {}
     best, us, grid = dict(old.get("best", {})), dict(old.get("us", {})), []
     best_tile = dict(old.get("best_tile", {}))
-    best_norm, us_norm = dict(old.get("best_norm", {})), dict(old.get("us_norm", {}))
+    tables = {t: dict(old.get(t, {})) for t, _ in TABLES.values()}
+    times = {t: dict(old.get("us_" + t[5:], {})) for t, _ in TABLES.values()}
     for ss in shape_sets:
-        for (N, K) in NORM_SHAPES.get(ss, ()):
-            for G in groups:
-                b, recs = tune_norm_shape(Kx, N, K, G, reps, log)
-                key = f"{N}x{K}_G{G}"
-                best_norm[key], us_norm[key] = b["cfg"], round(b["median_us"], 3)
-                grid += recs
+        for kind, shapes in FUSED_SHAPES.get(ss, {}).items():
+            table, grouped = TABLES[kind]
+            for (N, K) in shapes:
+                for G in (groups if grouped else (128,)):
+                    b, recs = tune_fused_shape(Kx, kind, N, K, G, reps, log)
+                    key = f"{N}x{K}_G{G}" if grouped else f"{N}x{K}"
+                    tables[table][key], times[table][key] = b["cfg"], round(b["median_us"], 3)
+                    grid += recs
     for ss in shape_sets:
         for name, (N, K) in SHAPE_SETS[ss].items():
             for G in groups:
@@ -137,11 +173,37 @@ def tune(shape_sets=("tinyllama", "llama3_8b", "baseline"), groups=(128,), reps=
                 if tiles:
                     best_tile[key] = min(tiles, key=lambda r: r["median_us"])["cfg"]
                 grid += [dict(r, shape=name) for r in recs]
-    out = {"device": torch.cuda.get_device_properties(0).name, "best": best, "best_tile": best_tile, "us": us,
-           "best_norm": best_norm, "us_norm": us_norm, "grid": grid}
+    out = {"device": torch.cuda.get_device_properties(0).name, "best": best, "best_tile": best_tile, "us": us}
+    for t, _ in TABLES.values():
+        out[t], out["us_" + t[5:]] = tables[t], times[t]
+    out["grid"] = grid
     pathlib.Path(path).parent.mkdir(exist_ok=True)
-    json.dump(out, open(path, "w"), indent=1)
+    write_table(out, path)
     return out
+
+
+def write_table(out, path):
+    """One line per table entry and per grid record (times rounded to ns)."""
+    def compact(v):
+        if isinstance(v, float):
+            return round(v, 3)
+        if isinstance(v, dict):
+            return {k: compact(x) for k, x in v.items()}
+        return v
+
+    parts = []
+    for k, v in out.items():
+        if isinstance(v, dict):
+            body = ",\n".join(f"  {json.dumps(kk)}: {json.dumps(compact(vv))}" for kk, vv in v.items())
+            parts.append(f" {json.dumps(k)}: {{\n{body}\n }}" if v else f" {json.dumps(k)}: {{}}")
+        elif isinstance(v, list):
+            body = ",\n".join("  " + json.dumps(compact(r), separators=(",", ":")) for r in v)
+            parts.append(f" {json.dumps(k)}: [\n{body}\n ]" if v else f" {json.dumps(k)}: []")
+        else:
+            parts.append(f" {json.dumps(k)}: {json.dumps(v)}")
+    txt = "{\n" + ",\n".join(parts) + "\n}\n"
+    assert json.loads(txt).keys() == out.keys()
+    pathlib.Path(path).write_text(txt)
 
 
 def main(argv=None):

@@ -26,6 +26,8 @@ SIGNATURES = {
     "dk_gemv_w4a16_rmsnorm": ([_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _I, _I, _P], _I),
     "dk_gemv_w4a16_swiglu": ([_I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P], _I),
     "dk_gemv_w4a16_gate_up": ([_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _I, _I, _P], _I),
+    "dk_gemv_f16": ([_I, _I, _I, _P, _P, _P, _I, _I, _P], _I),
+    "dk_gemv_f16_rmsnorm": ([_I, _I, _I, _P, _P, _P, _P, _F, _P, _P, _I, _I, _P], _I),
     "dk_bw_read": ([_P, _Z, _P, _I, _I, _I, _P], _I),
     "dk_paged_attention": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
     "dk_attention_decode": ([_P, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
@@ -174,6 +176,33 @@ class DecodeKernels:
         self._call(self.lib.dk_gemv_w4a16_gate_up, int(stage), int(R), int(warps), int(pf), packed.data_ptr(),
                    sz.data_ptr(), x.data_ptr(), ptr(row), ptr(delta), ptr(norm_w), float(eps), ptr(x_out),
                    act.data_ptr(), N, K, int(group), _stream(x))
+
+    def _f16_shape(self, w, x, y, what):
+        for t, n in ((w, "w"), (x, "x"), (y, "y")):
+            _check_cuda(t, n)
+            _check_dtype(t, torch.float16, n)
+        if w.dim() != 2 or x.numel() != w.size(1) or y.numel() != w.size(0):
+            raise RuntimeError(f"{what}: w must be [N, K], x [K] and y [N]")
+        return w.size(0), w.size(1)
+
+    # the fp16 LM head's torch.mm(x, W^T) (runtime/model.py:187) as a HIP GEMV
+    def gemv_f16(self, R, warps, pf, w, x, y):
+        N, Kd = self._f16_shape(w, x, y, "gemv_f16")
+        self._call(self.lib.dk_gemv_f16, int(R), int(warps), int(pf), w.data_ptr(), x.data_ptr(), y.data_ptr(), N, Kd,
+                   _stream(x))
+
+    # add_rmsnorm (kernels/bindings.cpp:64-72) fused into the fp16 GEMV that follows it
+    def gemv_f16_rmsnorm(self, R, warps, pf, w, x, delta, norm_w, eps, x_out, y):
+        N, Kd = self._f16_shape(w, x, y, "gemv_f16_rmsnorm")
+        _check_cuda(norm_w, "norm_w")
+        for t, n in ((delta, "delta"), (norm_w, "norm_w"), (x_out, "x_out")):
+            if t is not None:
+                _check_cuda(t, n)
+                if t.numel() != Kd or t.dtype != torch.float16:
+                    raise RuntimeError(f"gemv_f16_rmsnorm: {n} must be fp16 [K]")
+        ptr = lambda t: None if t is None else t.data_ptr()
+        self._call(self.lib.dk_gemv_f16_rmsnorm, int(R), int(warps), int(pf), w.data_ptr(), x.data_ptr(), ptr(delta),
+                   norm_w.data_ptr(), float(eps), ptr(x_out), y.data_ptr(), N, Kd, _stream(x))
 
     # kernels/bindings.cpp:40-43
     def bw_read(self, buf, sink, blocks, threads, unroll):

@@ -58,6 +58,8 @@ class DecodeConfig:
                                    # rope_append + paged_attention
     fused_gemv: bool = True        # residual + RMSNorm (and the embedding gather) computed inside the INT4 GEMV that
                                    # consumes it (dk_gemv_w4a16_rmsnorm) instead of a separate add_rmsnorm kernel
+    f16_gemv: bool = True          # fp16-weight projections with K <= 4096 (the fp16 LM head) on the HIP fp16 GEMV
+                                   # (dk_gemv_f16 / dk_gemv_f16_rmsnorm) instead of torch.mm
     swiglu: str = "epilogue"       # where SwiGLU runs when fused_gemv is on: "epilogue" = inside the gate|up GEMV
                                    # (dk_gemv_w4a16_gate_up, gate/up rows stored interleaved); "prologue" = inside the
                                    # down GEMV (dk_gemv_w4a16_swiglu: every workgroup re-evaluates silu for its columns,
@@ -159,11 +161,16 @@ class Model:
         self.lm_head = Linear(lm.half(), cfg, head_int4)
 
         self.gemv_table, self.gemv_tile_table, self.gemv_norm_table, self.gemv_gate_up_table = {}, {}, {}, {}
+        self.gemv_f16_table, self.gemv_f16_norm_table = {}, {}
+        self.gemv_us, self.gemv_norm_us = {}, {}
         if cfg.gemv_stage is None and Path(cfg.autotune_path).exists():
             tab = json.load(open(cfg.autotune_path))
             self.gemv_table, self.gemv_tile_table = tab.get("best", {}), tab.get("best_tile", {})
             self.gemv_norm_table = tab.get("best_norm", {})
+            self.gemv_us, self.gemv_norm_us = tab.get("us", {}), tab.get("us_norm", {})
             self.gemv_gate_up_table = tab.get("best_gate_up", {})
+            self.gemv_f16_table = tab.get("best_f16", {})
+            self.gemv_f16_norm_table = tab.get("best_f16_norm", {})
 
         # paged KV cache [L, 2, pages, n_kv, P, D]; one block table shared by all layers (one sequence)
         self.n_pages = (cfg.max_ctx + cfg.page - 1) // cfg.page + 1
@@ -250,6 +257,17 @@ class Model:
         e = self.gemv_norm_table.get(f"{lin.N}x{lin.K}_G{self.cfg.group}")
         return tuple(e) if e is not None else (4, 4, 0, 1)
 
+    # in-graph time of the separate add_rmsnorm launch at hidden 2048-4096 on MI355X (decode-step kernel trace)
+    ADD_RMSNORM_US = 2.5
+
+    def norm_fusion_pays(self, lin):
+        """Whether the residual + RMSNorm should run inside this INT4 GEMV: the tuned fused time against the tuned
+        plain GEMV plus a separate add_rmsnorm. Every workgroup of the fused kernel recomputes the norm over K, which
+        loses on the widest shapes (e.g. the 128256 x 4096 INT4 head, where split-K wins)."""
+        key = f"{lin.N}x{lin.K}_G{self.cfg.group}"
+        fused, plain = self.gemv_norm_us.get(key), self.gemv_us.get(key)
+        return fused is None or plain is None or fused <= plain + self.ADD_RMSNORM_US
+
     def linear_norm(self, lin: Linear, x_in, delta, w, x_out, y, row=None):
         """y = W . rmsnorm(x_in + delta) with x_out <- x_in + delta, one launch (dk_gemv_w4a16_rmsnorm)."""
         s, r, wv, pf = self.gemv_norm_cfg(lin)
@@ -277,10 +295,21 @@ class Model:
         s, r, wv, pf = self.gemv_tile_cfg(lin)
         self.K.gemv_w4a16_swiglu(s, r, wv, pf, lin.packed, lin.sz, gu, y, self.cfg.group)
 
+    def use_f16_gemv(self, lin):
+        return self.cfg.fused and self.cfg.f16_gemv and not lin.quant and lin.K <= 4096 and lin.K % 8 == 0
+
+    def gemv_f16_cfg(self, lin, norm=False):
+        """(R, waves, pf) of the fp16 GEMV (norm: the variant behind the final RMSNorm): tuned entry, else 2-row tiles
+        (1 for K > 2048), 1 wave per workgroup, 4 tiles per wave."""
+        e = (self.gemv_f16_norm_table if norm else self.gemv_f16_table).get(f"{lin.N}x{lin.K}")
+        return tuple(e) if e is not None else ((2 if lin.K <= 2048 else 1), 1, 2)
+
     def linear(self, lin: Linear, x, y):
         if lin.quant:
             s, r, w, pf = self.gemv_cfg(lin)
             self.K.gemv_w4a16(s, r, w, pf, lin.packed, lin.sz, x, y, self.cfg.group)
+        elif self.use_f16_gemv(lin):
+            self.K.gemv_f16(*self.gemv_f16_cfg(lin), lin.w, x, y)
         else:
             torch.mm(x.view(1, -1), lin.w.t(), out=y.view(1, -1))  # rocBLAS / hipBLASLt, the reference's cuBLAS call
 
@@ -341,9 +370,12 @@ class Model:
         for li, lw in enumerate(self.layers):
             if li == 0:
                 self.linear_norm(lw["qkv"], self.emb, None, lw["ln1"], cur, self.qkv, row=self.tok)
-            else:
+            elif self.norm_fusion_pays(lw["qkv"]):
                 self.linear_norm(lw["qkv"], cur, delta, lw["ln1"], nxt, self.qkv)
                 cur, nxt = nxt, cur
+            else:
+                self.K.add_rmsnorm(cur, delta, lw["ln1"], self.normed, self.eps)
+                self.linear(lw["qkv"], self.normed, self.qkv)
             self.attention(li)
             self.linear(lw["o"], self.attn.view(-1), self.o)
             if self.gate_up_epilogue:
@@ -359,8 +391,11 @@ class Model:
                     self.K.swiglu(self.gu, self.act)
                     self.linear(lw["down"], self.act, self.down)
             delta = self.down
-        if self.lm_head.quant:
+        if self.lm_head.quant and self.norm_fusion_pays(self.lm_head):
             self.linear_norm(self.lm_head, cur, delta, self.norm_f, None, self.logits)
+        elif self.use_f16_gemv(self.lm_head):
+            self.K.gemv_f16_rmsnorm(*self.gemv_f16_cfg(self.lm_head, norm=True), self.lm_head.w, cur, delta,
+                                    self.norm_f, self.eps, None, self.logits)
         else:
             self.K.add_rmsnorm(cur, delta, self.norm_f, self.normed, self.eps)
             self.linear(self.lm_head, self.normed, self.logits)

@@ -162,6 +162,19 @@ def test_fused_gemv_validation(lib):
     assert sw(gu=A16 + 2)[0] == 2 and sw(R=3)[0] == 4 and sw(N=0)[0] == 3
 
 
+def test_gemv_f16_validation(lib):
+    f = lambda **kw: _err(lib, lib.dk_gemv_f16(*dict(dict(R=2, warps=4, pf=2, w=A16, x=A16, y=B16, N=64, K=2048),
+                                                      **kw).values(), None))
+    assert f(R=3)[0] == 4 and f(warps=3)[0] == 4 and f(pf=4)[0] == 4 and f(N=0)[0] == 3
+    assert f(K=2044)[0] == 3 and f(K=4104)[0] == 3 and f(w=A16 + 8)[0] == 2 and f(y=B16 + 1)[0] == 2
+    assert f(K=4096, R=4)[0] == 4 and "R <= 2" in f(K=4096, R=4)[1]
+    assert f(x=None)[0] == 1
+    n = lambda **kw: _err(lib, lib.dk_gemv_f16_rmsnorm(*dict(dict(R=2, warps=4, pf=2, w=A16, x=A16, d=None, nw=A16,
+                                                                  eps=1e-5, xo=None, y=B16, N=64, K=2048),
+                                                             **kw).values(), None))
+    assert n(nw=None)[0] == 1 and n(xo=A16)[0] == 4 and n(d=A16 + 4)[0] == 2 and n(R=8)[0] == 4
+
+
 def test_small_op_validation(lib):
     assert _err(lib, lib.dk_add_rmsnorm(A16, None, A16, A16, 2047, 1e-5, None))[0] == 3
     assert _err(lib, lib.dk_add_rmsnorm(A16 + 2, None, A16, A16, 2048, 1e-5, None))[0] == 2

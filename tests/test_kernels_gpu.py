@@ -442,6 +442,66 @@ def test_gemv_gate_up_swiglu_epilogue(K, I, Kd, norm):
         assert torch.equal(act, sep), f"gate_up vs gemv + swiglu I{I} K{Kd} norm={norm} {cfg}"
 
 
+# ------------------------------------------------------------------------------------------ fp16-weight GEMV (LM head)
+F16_CFGS = [(1, 0, 0), (2, 4, 2), (4, 1, 1), (1, 8, 3), (2, 2, 0), (4, 4, 3)]
+
+
+@pytest.mark.parametrize("N,Kd", [(32000, 2048), (37, 8), (100, 520), (1000, 4096), (513, 1024), (64, 3000)])
+def test_gemv_f16(K, N, Kd):
+    """y = W . x for fp16 W against the oracle's fp32 matvec (reference/ref_ops.py:10-12 with W as stored), the
+    reference's GEMV tolerance 5e-3 normwise. K = 520 / 3000 leave dead chunks in the last lane pass; N = 37 / 513 a
+    partial last tile."""
+    g = gen(N + 3 * Kd)
+    w = (torch.randn(N, Kd, generator=g) * 0.02).half()
+    x = torch.randn(Kd, generator=g).half()
+    ref = R.gemv_ref(w, x)
+    wd, xd = w.to(DEV), x.to(DEV)
+    y = torch.empty(N, dtype=torch.half, device=DEV)
+    for cfg in F16_CFGS:
+        if cfg[0] * (1 << max(0, (-(-Kd // 512) - 1).bit_length())) > 16:
+            continue
+        y.fill_(7.0)
+        K.gemv_f16(*cfg, wd, xd, y)
+        assert_close(y, ref, 5e-3, f"gemv_f16 {N}x{Kd} {cfg}")
+
+
+def test_gemv_f16_onehot_exact(K):
+    """One-hot x picks a column of W exactly (every other product is an exact zero)."""
+    N, Kd = 300, 1040
+    w = (torch.randn(N, Kd, generator=gen(9)) * 3).half()
+    wd = w.to(DEV)
+    y = torch.empty(N, dtype=torch.half, device=DEV)
+    for k in (0, 1, 7, 8, 511, 512, 1039):
+        x = torch.zeros(Kd, dtype=torch.half, device=DEV)
+        x[k] = 1.0
+        for cfg in ((1, 0, 0), (2, 4, 2), (4, 2, 3)):
+            K.gemv_f16(*cfg, wd, x, y)
+            assert torch.equal(y.cpu(), w[:, k]), (k, cfg)
+
+
+@pytest.mark.parametrize("N,Kd", [(32000, 2048), (1000, 4096), (77, 520)])
+@pytest.mark.parametrize("with_delta", (True, False))
+def test_gemv_f16_rmsnorm(K, N, Kd, with_delta):
+    """The final add_rmsnorm fused in front of the fp16 GEMV: y against add_rmsnorm_ref then gemv_ref (5e-3), x_out
+    bit-exact (fp16 add)."""
+    g = gen(N * 3 + Kd)
+    w = (torch.randn(N, Kd, generator=g) * 0.02).half()
+    x = (torch.randn(Kd, generator=g) * 2).half()
+    d = torch.randn(Kd, generator=g).half() if with_delta else None
+    nw = (1 + 0.1 * torch.randn(Kd, generator=g)).half()
+    xr, normed = R.add_rmsnorm_ref(x, d, nw, 1e-5)
+    ref = R.gemv_ref(w, normed)
+    wd = w.to(DEV)
+    y = torch.empty(N, dtype=torch.half, device=DEV)
+    for cfg in ((2, 4, 2), (1, 8, 0), (1, 1, 3)):
+        x_out = torch.zeros(Kd, dtype=torch.half, device=DEV)
+        K.gemv_f16_rmsnorm(*cfg, wd, x.to(DEV), None if d is None else d.to(DEV), nw.to(DEV), 1e-5, x_out, y)
+        assert_close(y, ref, 5e-3, f"gemv_f16_rmsnorm {N}x{Kd} {cfg}")
+        assert torch.equal(x_out.cpu(), xr), cfg
+    K.gemv_f16_rmsnorm(2, 4, 2, wd, x.to(DEV), None if d is None else d.to(DEV), nw.to(DEV), 1e-5, None, y)
+    assert_close(y, ref, 5e-3, "no x_out")
+
+
 def test_fused_step_equals_unfused_step(K):
     """The decode step with fused prologues / epilogue and the one with separate norm / SwiGLU kernels give the same
     logits (same rounding points; only the sum-of-squares order may differ)."""
