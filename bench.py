@@ -139,6 +139,34 @@ def decode_leg(model, ctx, steps, warmup):
             "p90_us": tok_us[(9 * len(tok_us)) // 10], "wall_tok_s": steps / wall}
 
 
+def decode_8b_leg(ctx=4096, steps=64, warmup=8):
+    """Llama-3-8B-architecture W4A16 decode at context `ctx`, hipGraph replay, once with the INT4
+    LM head and once with the fp16 one (the config leaves the head format open)."""
+    import torch
+    from runtime.model import DecodeConfig, Model
+    from runtime.synth import LLAMA3_8B, SyntheticLlama
+
+    out = {}
+    for head in ("int4", "fp16"):
+        t0 = time.perf_counter()
+        m = Model(SyntheticLlama(LLAMA3_8B, seed=0), LLAMA3_8B,
+                  DecodeConfig(lm_head=head, max_ctx=ctx + steps + warmup + 16))
+        m.prepare(ctx + steps + warmup + 16)
+        built = time.perf_counter() - t0
+        d = decode_leg(m, ctx, steps, warmup)
+        bpt = m.bytes_per_token(ctx + steps // 2)
+        roof = HBM_PEAK_GBS * 1e9 / bpt
+        out[f"{head}_head"] = {"tok_s": round(d["tok_s"], 2), "median_us": round(d["median_us"], 2),
+                               "bytes_per_token": bpt, "roofline_tok_s": round(roof, 1),
+                               "frac_of_roofline": round(d["tok_s"] / roof, 4), "part_size": m.part_size,
+                               "build_s": round(built, 1)}
+        log(f"llama3-8b ctx {ctx} {head} head: {d['tok_s']:.1f} tok/s, median {d['median_us']:.1f} us "
+            f"({d['tok_s'] / roof:.1%} of the {roof:.0f} tok/s roofline)")
+        del m
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline_leg(model, shape, ctx, budget_s=15.0, max_tokens=64):
     """Tokens/s of the CPU oracle decode step on the host cores (a bounded sample)."""
     import torch
@@ -167,8 +195,9 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--ctx", type=int, default=512)
-    ap.add_argument("--leg", choices=("all", "gemv", "decode"), default="all",
-                    help="gemv: the 4096x14336 GEMV and its calibration copies only; decode: the decode step only")
+    ap.add_argument("--leg", choices=("all", "gemv", "decode", "decode8b"), default="all",
+                    help="gemv: the 4096x14336 GEMV and its calibration copies only; decode: the TinyLlama decode "
+                         "step only; decode8b: the Llama-3-8B decode legs only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline leg")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -186,6 +215,10 @@ def main():
         log(f"gemv 4096x14336 {g1['cfg']}: {g1['mean_us']:.3f} us/launch -> {g1['gbps']:.0f} GB/s ({g1['frac']:.1%})")
         calibration_leg(Kx, g1["bytes"])
         print(json.dumps({"leg": "gemv", "gemv_4096x14336": g1}), flush=True)
+        return
+
+    if a.leg == "decode8b":
+        print(json.dumps({"leg": "decode8b", "decode_llama3_8b_ctx4096": decode_8b_leg()}), flush=True)
         return
 
     from runtime.model import DecodeConfig, Model
@@ -218,6 +251,8 @@ def main():
     rc = read_ceiling_leg(Kx, g1["bytes"])
     log(f"bw_read of {rc['bytes']} B: {rc['mean_us']:.3f} us -> {rc['gbps']:.0f} GB/s ({rc['frac']:.1%})")
 
+    d8b = decode_8b_leg()
+
     cpu = None
     if not a.no_cpu:
         cpu = cpu_baseline_leg(model, TINYLLAMA, a.ctx)
@@ -245,6 +280,7 @@ def main():
                    "frac_of_roofline": round(dec["tok_s"] / (HBM_PEAK_GBS * 1e9 / bpt), 4)},
         "decode_ctx2048": {"tok_s": round(dec2k["tok_s"], 2), "median_us": round(dec2k["median_us"], 2),
                            "bytes_per_token": bpt2k, "frac_of_roofline": round(dec2k["tok_s"] / (HBM_PEAK_GBS * 1e9 / bpt2k), 4)},
+        "decode_llama3_8b_ctx4096": d8b,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -146,13 +146,16 @@ int dk_paged_attention(int version, const void* q, const void* kc, const void* v
  * back). qkv: the fused [q | k | v] vector, fp16 [(n_q + 2 n_kv) * head_dim], read only (q is rotated in registers,
  * not written back). k (rotated) and v of position *pos are written into page bt[pos / page], slot pos % page exactly
  * as dk_rope_append writes them, and the attention over ctx = *pos + 1 tokens uses them. Split partials go to
- * o_part / m_part / l_part and a combine kernel merges them, as for dk_paged_attention. If *pos is outside
- * [0, max_pos) nothing is touched. Other arguments and limits as dk_rope_append / dk_paged_attention.
+ * o_part / m_part / l_part. counters == NULL: a combine kernel merges them, as for dk_paged_attention. counters =
+ * uint32 [n_kv], zero before the first call (every call leaves them zero): when 1 < max_splits <= 64 the split
+ * workgroup of each kv head that finishes last merges its partials (one launch in all); calls that share counters
+ * must not run concurrently. If *pos is outside [0, max_pos) nothing is touched. Other arguments and limits as
+ * dk_rope_append / dk_paged_attention.
  */
 int dk_attention_decode(const void* qkv, const float* cos_t, const float* sin_t, int max_pos, const int32_t* pos,
                         const int32_t* bt, int n_bt, void* kc, void* vc, int n_pages, int page, int n_q, int n_kv,
                         int head_dim, int part_size, int max_splits, float* o_part, float* m_part, float* l_part,
-                        void* out, void* stream);
+                        uint32_t* counters, void* out, void* stream);
 
 /*
  * Fused residual add + RMSNorm:  x <- x + delta (fp16 add, written back; skipped if delta == NULL);

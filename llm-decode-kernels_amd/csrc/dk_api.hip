@@ -233,7 +233,8 @@ int dk_paged_attention(int version, const void* q, const void* kc, const void* v
   if (!aligned16(o_part)) return fail(DK_ERR_ALIGN, "o_part must be 16B aligned");
   clear_error();
   const dk::AttnLaunch a{q, nullptr, nullptr, 0, pos, bt, n_bt, const_cast<void*>(kc), const_cast<void*>(vc), n_pages,
-                         ilog2(page), n_q, n_kv, head_dim, part_size, max_splits, o_part, m_part, l_part, out};
+                         ilog2(page), n_q, n_kv, head_dim, part_size, max_splits, o_part, m_part, l_part, out,
+                         nullptr};
   dk::launch_paged_attention(a, (hipStream_t)stream);
   return launched("paged_attention");
 }
@@ -241,9 +242,11 @@ int dk_paged_attention(int version, const void* q, const void* kc, const void* v
 int dk_attention_decode(const void* qkv, const float* cos_t, const float* sin_t, int max_pos, const int32_t* pos,
                         const int32_t* bt, int n_bt, void* kc, void* vc, int n_pages, int page, int n_q, int n_kv,
                         int head_dim, int part_size, int max_splits, float* o_part, float* m_part, float* l_part,
-                        void* out, void* stream) {
+                        uint32_t* counters, void* out, void* stream) {
   if (!qkv || !cos_t || !sin_t || !pos || !bt || !kc || !vc || !o_part || !m_part || !l_part || !out)
     return fail(DK_ERR_NULL, "attention_decode: null pointer argument");
+  if (counters && (reinterpret_cast<uintptr_t>(counters) & 3u))
+    return fail(DK_ERR_ALIGN, "attention_decode: counters must be 4B aligned");
   if (head_dim != 64 && head_dim != 128)
     return fail(DK_ERR_SHAPE, "attention_decode: head_dim must be 64 or 128, got %d", head_dim);
   if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0)
@@ -263,7 +266,7 @@ int dk_attention_decode(const void* qkv, const float* cos_t, const float* sin_t,
   if (!aligned16(o_part)) return fail(DK_ERR_ALIGN, "o_part must be 16B aligned");
   clear_error();
   const dk::AttnLaunch a{qkv, cos_t, sin_t, max_pos, pos, bt, n_bt, kc, vc, n_pages, ilog2(page), n_q, n_kv,
-                         head_dim, part_size, max_splits, o_part, m_part, l_part, out};
+                         head_dim, part_size, max_splits, o_part, m_part, l_part, out, counters};
   dk::launch_attention_decode(a, (hipStream_t)stream);
   return launched("attention_decode");
 }

@@ -56,10 +56,12 @@ struct AttnLaunch {
   float* m_part;
   float* l_part;
   void* out;
+  uint32_t* counters;  // decode op: one per kv head (zero, left zero) -> combine in the last split workgroup; or null
 };
 // Reference-compatible op: split kernel + combine kernel.
 void launch_paged_attention(const AttnLaunch& a, hipStream_t st);
-// Fused decode op: RoPE + KV append + split-K attention, then the combine kernel.
+// Fused decode op: RoPE + KV append + split-K attention, then the combine (in the last split workgroup when
+// counters are given and max_splits <= 64, else the combine kernel).
 void launch_attention_decode(const AttnLaunch& a, hipStream_t st);
 
 void launch_add_rmsnorm(void* x, const void* delta, const void* w, void* out, int H, float eps, hipStream_t st);

@@ -30,7 +30,8 @@ SIGNATURES = {
     "dk_gemv_f16_rmsnorm": ([_I, _I, _I, _P, _P, _P, _P, _F, _P, _P, _I, _I, _P], _I),
     "dk_bw_read": ([_P, _Z, _P, _I, _I, _I, _P], _I),
     "dk_paged_attention": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
-    "dk_attention_decode": ([_P, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
+    "dk_attention_decode": ([_P, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P],
+                            _I),
     "dk_add_rmsnorm": ([_P, _P, _P, _P, _I, _F, _P], _I),
     "dk_swiglu": ([_P, _P, _I, _P], _I),
     "dk_rope_append": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
@@ -241,7 +242,9 @@ class DecodeKernels:
 
     # rope_append (kernels/bindings.cpp:81-88) + paged_attention (kernels/bindings.cpp:45-62) fused into one launch
     def attention_decode(self, qkv, cos_t, sin_t, pos, bt, kc, vc, n_q, n_kv, part_size, o_part, m_part, l_part,
-                         out):
+                         out, counters=None):
+        """counters: None (split kernel + combine kernel) or int32 [n_kv] zeros, left zero by every call (the last
+        split workgroup of each kv head combines; one launch)."""
         for t, n in ((qkv, "qkv"), (cos_t, "cos_t"), (sin_t, "sin_t"), (pos, "pos"), (bt, "bt"), (kc, "kc"),
                      (vc, "vc"), (o_part, "o_part"), (m_part, "m_part"), (l_part, "l_part"), (out, "out")):
             _check_cuda(t, n)
@@ -263,10 +266,16 @@ class DecodeKernels:
         if not (o_part.size(0) == n_q and o_part.size(2) == D and m_part.shape == (n_q, max_splits)
                 and l_part.shape == (n_q, max_splits) and out.numel() == n_q * D):
             raise RuntimeError("attention_decode: buffers must be o [n_q, S, D], m/l [n_q, S], out [n_q, D]")
+        if counters is not None:
+            _check_cuda(counters, "counters")
+            _check_dtype(counters, torch.int32, "counters")
+            if counters.numel() != n_kv:
+                raise RuntimeError("attention_decode: counters must be int32 [n_kv]")
         self._call(self.lib.dk_attention_decode, qkv.data_ptr(), cos_t.data_ptr(), sin_t.data_ptr(), cos_t.size(0),
                    pos.data_ptr(), bt.data_ptr(), bt.numel(), kc.data_ptr(), vc.data_ptr(), kc.size(0), kc.size(2),
                    int(n_q), int(n_kv), D, int(part_size), max_splits, o_part.data_ptr(), m_part.data_ptr(),
-                   l_part.data_ptr(), out.data_ptr(), _stream(qkv))
+                   l_part.data_ptr(), None if counters is None else counters.data_ptr(), out.data_ptr(),
+                   _stream(qkv))
 
     # kernels/bindings.cpp:64-72
     def add_rmsnorm(self, x, delta, w, out, eps):

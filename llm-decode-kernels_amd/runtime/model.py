@@ -56,6 +56,9 @@ class DecodeConfig:
     seed: int = 0            # block-table permutation seed
     fused_attention: bool = True   # dk_attention_decode (RoPE + append inside the split kernel) instead of
                                    # rope_append + paged_attention
+    combine_in_split: bool = False # with fused_attention: the last split workgroup of each kv head merges the
+                                   # partials (per-kv-head counters) instead of a second combine launch; its three
+                                   # device-coherent round trips cost what the second launch costs on MI355X
     fused_gemv: bool = True        # residual + RMSNorm (and the embedding gather) computed inside the INT4 GEMV that
                                    # consumes it (dk_gemv_w4a16_rmsnorm) instead of a separate add_rmsnorm kernel
     f16_gemv: bool = True          # fp16-weight projections with K <= 4096 (the fp16 LM head) on the HIP fp16 GEMV
@@ -212,6 +215,8 @@ class Model:
         self.o_part = torch.empty(self.n_q, self.max_splits, self.D, **f32)
         self.m_part = torch.empty(self.n_q, self.max_splits, **f32)
         self.l_part = torch.empty(self.n_q, self.max_splits, **f32)
+        # per-kv-head arrival counters of the in-split combine: zero here, left zero by every launch
+        self.attn_counters = torch.zeros(self.n_kv, dtype=torch.int32, device=self.cfg.device)
         self.graph = None
 
     def prepare(self, ctx_cap, use_graph=True, part_size=None):
@@ -332,7 +337,8 @@ class Model:
         kc, vc = self.kv[li, 0], self.kv[li, 1]
         if self.cfg.fused_attention:
             self.K.attention_decode(self.qkv, self.cos, self.sin, self.pos, self.bt, kc, vc, self.n_q, self.n_kv,
-                                    self.part_size, self.o_part, self.m_part, self.l_part, self.attn)
+                                    self.part_size, self.o_part, self.m_part, self.l_part, self.attn,
+                                    self.attn_counters if self.cfg.combine_in_split else None)
             return
         self.K.rope_append(self.qkv, self.cos, self.sin, self.pos, self.bt, kc, vc, self.n_q, self.n_kv)
         self.K.paged_attention(self.qkv[: self.n_q * self.D], kc, vc, self.bt, self.pos, self.part_size,

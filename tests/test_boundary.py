@@ -103,7 +103,7 @@ def test_attention_validation(lib, kw, code, msg):
 
 def _dec(lib, **kw):
     a = dict(qkv=A16, c=A16, s=A16, max_pos=100, pos=A16, bt=A16, n_bt=8, kc=A16, vc=A16, n_pages=8, page=16, n_q=32,
-             n_kv=4, D=64, part_size=64, max_splits=4, o=A16, m=A16, l=A16, out=A16)
+             n_kv=4, D=64, part_size=64, max_splits=4, o=A16, m=A16, l=A16, counters=None, out=A16)
     a.update(kw)
     return _err(lib, lib.dk_attention_decode(*a.values(), None))
 
@@ -114,6 +114,7 @@ def _dec(lib, **kw):
     (dict(page=12), 4, "page size must be a power of two"),
     (dict(part_size=0), 4, "part_size must be > 0"),
     (dict(max_splits=0), 3, "max_splits"),
+    (dict(counters=A16 + 2), 2, "counters must be 4B aligned"),
     (dict(max_pos=0), 3, "empty"),
     (dict(c=None), 1, "null"),
     (dict(qkv=A16 + 2), 2, "16B aligned"),
