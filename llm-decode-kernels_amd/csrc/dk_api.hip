@@ -223,7 +223,10 @@ int dk_paged_attention(int version, const void* q, const void* kc, const void* v
     return fail(DK_ERR_SHAPE, "heads-per-group must be 1/2/4/8, got %d", hpg);
   if (!pow2(page)) return fail(DK_ERR_DOMAIN, "page size must be a power of two, got %d", page);
   if (part_size <= 0) return fail(DK_ERR_DOMAIN, "part_size must be > 0");
-  if (version < 1 || version > 3) return fail(DK_ERR_DOMAIN, "attention version must be 1, 2 or 3");
+  if (version < 1 || version > 4) return fail(DK_ERR_DOMAIN, "attention version must be 1, 2, 3 or 4");
+  if (version == 4 && !dk::attn_mfma_fits(part_size, ilog2(page)))
+    return fail(DK_ERR_DOMAIN, "paged_attention: version 4 stages at most %d block-table pages per split "
+                "(part_size %d, page %d)", dk::kAttnMaxSplitPages, part_size, page);
   if (max_splits < 1 || max_splits > 65535)
     return fail(DK_ERR_SHAPE, "paged_attention: max_splits must be 1..65535, got %d", max_splits);
   if (n_pages < 1 || n_bt < 1) return fail(DK_ERR_SHAPE, "paged_attention: empty cache or block table");
@@ -234,19 +237,22 @@ int dk_paged_attention(int version, const void* q, const void* kc, const void* v
   clear_error();
   const dk::AttnLaunch a{q, nullptr, nullptr, 0, pos, bt, n_bt, const_cast<void*>(kc), const_cast<void*>(vc), n_pages,
                          ilog2(page), n_q, n_kv, head_dim, part_size, max_splits, o_part, m_part, l_part, out,
-                         nullptr};
+                         nullptr, version == 4 ? 2 : 1};
   dk::launch_paged_attention(a, (hipStream_t)stream);
   return launched("paged_attention");
 }
 
 int dk_attention_decode(const void* qkv, const float* cos_t, const float* sin_t, int max_pos, const int32_t* pos,
                         const int32_t* bt, int n_bt, void* kc, void* vc, int n_pages, int page, int n_q, int n_kv,
-                        int head_dim, int part_size, int max_splits, float* o_part, float* m_part, float* l_part,
-                        uint32_t* counters, void* out, void* stream) {
+                        int head_dim, int part_size, int max_splits, int impl, float* o_part, float* m_part,
+                        float* l_part, uint32_t* counters, void* out, void* stream) {
   if (!qkv || !cos_t || !sin_t || !pos || !bt || !kc || !vc || !o_part || !m_part || !l_part || !out)
     return fail(DK_ERR_NULL, "attention_decode: null pointer argument");
   if (counters && (reinterpret_cast<uintptr_t>(counters) & 3u))
     return fail(DK_ERR_ALIGN, "attention_decode: counters must be 4B aligned");
+  if (impl < 0 || impl > 2) return fail(DK_ERR_DOMAIN, "attention_decode: impl must be 0, 1 or 2, got %d", impl);
+  if (impl == 2 && counters)
+    return fail(DK_ERR_DOMAIN, "attention_decode: the in-split combine (counters) belongs to impl 1");
   if (head_dim != 64 && head_dim != 128)
     return fail(DK_ERR_SHAPE, "attention_decode: head_dim must be 64 or 128, got %d", head_dim);
   if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0)
@@ -265,8 +271,11 @@ int dk_attention_decode(const void* qkv, const float* cos_t, const float* sin_t,
     return fail(DK_ERR_ALIGN, "qkv, kc and vc must be 16B aligned");
   if (!aligned16(o_part)) return fail(DK_ERR_ALIGN, "o_part must be 16B aligned");
   clear_error();
+  if (impl == 2 && !dk::attn_mfma_fits(part_size, ilog2(page)))
+    return fail(DK_ERR_DOMAIN, "attention_decode: impl 2 stages at most %d block-table pages per split "
+                "(part_size %d, page %d)", dk::kAttnMaxSplitPages, part_size, page);
   const dk::AttnLaunch a{qkv, cos_t, sin_t, max_pos, pos, bt, n_bt, kc, vc, n_pages, ilog2(page), n_q, n_kv,
-                         head_dim, part_size, max_splits, o_part, m_part, l_part, out, counters};
+                         head_dim, part_size, max_splits, o_part, m_part, l_part, out, counters, impl};
   dk::launch_attention_decode(a, (hipStream_t)stream);
   return launched("attention_decode");
 }

@@ -57,7 +57,12 @@ struct AttnLaunch {
   float* l_part;
   void* out;
   uint32_t* counters;  // decode op: one per kv head (zero, left zero) -> combine in the last split workgroup; or null
+  int impl;            // 0 or 1 = block kernel; 2 = MFMA kernel
 };
+// The MFMA attention kernel stages a split's block-table pages in LDS: ((part_size - 1) >> log2P) + 2 of them at most.
+constexpr int kAttnMaxSplitPages = 1024;
+inline bool attn_mfma_fits(int part_size, int log2P) { return ((part_size - 1) >> log2P) + 2 <= kAttnMaxSplitPages; }
+inline bool attn_use_mfma(const AttnLaunch& a) { return a.impl == 2 && attn_mfma_fits(a.part_size, a.log2P); }
 // Reference-compatible op: split kernel + combine kernel.
 void launch_paged_attention(const AttnLaunch& a, hipStream_t st);
 // Fused decode op: RoPE + KV append + split-K attention, then the combine (in the last split workgroup when

@@ -13,6 +13,8 @@ cold weights (runtime.timing), and writes
 
 The runtime (runtime.model.Model.gemv_cfg) reads "best"; 3-element entries [R, warps, pf] of the reference's schema
 are read as stage 2. Run:  python -m runtime.autotune [--shapes tinyllama,llama3_8b,baseline] [--groups 128]
+With --attention it tunes the decode attention instead (kernel and split size per head dim and context) and writes
+configs/attn_policy.json.
 """
 import argparse
 import json
@@ -206,15 +208,84 @@ def write_table(out, path):
     pathlib.Path(path).write_text(txt)
 
 
+# ------------------------------------------------------------------------------------------ attention policy
+ATTN_MODELS = {64: "TINYLLAMA", 128: "LLAMA3_8B"}   # head_dim -> the model whose decode step the policy is tuned in
+ATTN_CONTEXTS = (512, 1024, 2048, 4096, 16384)
+ATTN_PATH = PKG / "configs" / "attn_policy.json"
+
+
+def step_time_us(model, ctx, steps=24, warmup=8):
+    """Mean graph-replayed decode step time starting at context ctx."""
+    model.reset(ctx)
+    for _ in range(warmup):
+        model.run_step()
+    torch.cuda.synchronize()
+    model.reset(ctx)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        model.run_step()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / steps
+
+
+def tune_attention(dims=(64, 128), contexts=ATTN_CONTEXTS, path=ATTN_PATH, log=print):
+    """Writes configs/attn_policy.json: per head dim, entries {max_ctx, part_size, impl} (the reference's schema,
+    runtime/model.py:160-178, plus the kernel choice), the last one open-ended. Every candidate (impl 1 block kernel or
+    2 MFMA kernel, split size) is timed inside the decode step of the model that has this head dim (graph replay at
+    context ctx): an attention kernel costs more inside the step, interleaved with the GEMVs, than back to back, and
+    by different amounts per kernel, so isolated launches would choose wrongly."""
+    from . import synth
+    from .model import DecodeConfig, Model
+    old = json.load(open(path)) if pathlib.Path(path).exists() else {}
+    out = {"version": old.get("version", 3),
+           "note": "part_size (tokens per split) and impl (1 block kernel, 2 MFMA kernel) by the largest tuned context "
+                   "<= the prepared cap; chosen by the decode step time of the TinyLlama (head_dim 64) and Llama-3-8B "
+                   "(head_dim 128) shapes on MI355X (runtime.autotune.tune_attention). 'policy' is head_dim 64, "
+                   "'policy_d128' head_dim 128."}
+    grid = []
+    for D in dims:
+        shape = getattr(synth, ATTN_MODELS[D])
+        cap_max = max(contexts) + 64
+        model = Model(synth.SyntheticLlama(shape, seed=0), shape,
+                      DecodeConfig(lm_head="int4" if D == 128 else "fp16", max_ctx=cap_max))
+        ents = []
+        for ctx in contexts:
+            best = None
+            for impl in (1, 2):
+                for ps in (32, 64, 128, 256, 512):
+                    if impl == 1 and ps > 128:
+                        continue                       # the block kernel costs about 3 us per extra 64-token block
+                    model.prepare(ctx + 48, part_size=ps, impl=impl)
+                    us = step_time_us(model, ctx)
+                    grid.append({"D": D, "ctx": ctx, "impl": impl, "part_size": ps, "step_us": round(us, 2)})
+                    if best is None or us < best[0]:
+                        best = (us, impl, ps)
+            log(f"  attention D{D} ctx {ctx}: best impl {best[1]} part_size {best[2]} ({best[0]:.1f} us per step)")
+            ents.append({"max_ctx": ctx, "part_size": best[2], "impl": best[1]})
+        ents[-1] = dict(ents[-1], max_ctx=1 << 30)
+        out["policy" if D == 64 else f"policy_d{D}"] = ents
+        del model
+        torch.cuda.empty_cache()
+    out["grid"] = grid
+    write_table(out, path)
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--shapes", default="tinyllama,llama3_8b,baseline")
     ap.add_argument("--groups", default="128")
     ap.add_argument("--reps", type=int, default=5)
-    ap.add_argument("--out", default=str(CONFIG))
+    ap.add_argument("--out", default=None)
+    ap.add_argument("--attention", action="store_true", help="tune the attention policy instead of the GEMVs")
     a = ap.parse_args(argv)
-    tune(a.shapes.split(","), tuple(int(g) for g in a.groups.split(",")), a.reps, a.out,
-         log=lambda *s: print(*s, flush=True))
+    log = lambda *s: print(*s, flush=True)
+    if a.attention:
+        tune_attention(path=a.out or ATTN_PATH, log=log)
+        return
+    tune(a.shapes.split(","), tuple(int(g) for g in a.groups.split(",")), a.reps, a.out or CONFIG, log=log)
 
 
 if __name__ == "__main__":

@@ -30,8 +30,8 @@ SIGNATURES = {
     "dk_gemv_f16_rmsnorm": ([_I, _I, _I, _P, _P, _P, _P, _F, _P, _P, _I, _I, _P], _I),
     "dk_bw_read": ([_P, _Z, _P, _I, _I, _I, _P], _I),
     "dk_paged_attention": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
-    "dk_attention_decode": ([_P, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P],
-                            _I),
+    "dk_attention_decode": ([_P, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P,
+                             _P], _I),
     "dk_add_rmsnorm": ([_P, _P, _P, _P, _I, _F, _P], _I),
     "dk_swiglu": ([_P, _P, _I, _P], _I),
     "dk_rope_append": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
@@ -230,8 +230,8 @@ class DecodeKernels:
             raise RuntimeError("heads-per-group must be 1/2/4/8")
         if part_size <= 0:
             raise RuntimeError("part_size must be > 0")
-        if not 1 <= version <= 3:
-            raise RuntimeError("attention version must be 1, 2 or 3")
+        if not 1 <= version <= 4:
+            raise RuntimeError("attention version must be 1, 2, 3 or 4")
         max_splits = o_part.size(1)
         if not (o_part.size(0) == n_q and o_part.size(2) == D and m_part.size(0) == n_q and l_part.size(0) == n_q
                 and m_part.size(1) == max_splits and l_part.size(1) == max_splits and out.numel() == n_q * D):
@@ -242,9 +242,10 @@ class DecodeKernels:
 
     # rope_append (kernels/bindings.cpp:81-88) + paged_attention (kernels/bindings.cpp:45-62) fused into one launch
     def attention_decode(self, qkv, cos_t, sin_t, pos, bt, kc, vc, n_q, n_kv, part_size, o_part, m_part, l_part,
-                         out, counters=None):
+                         out, counters=None, impl=0):
         """counters: None (split kernel + combine kernel) or int32 [n_kv] zeros, left zero by every call (the last
-        split workgroup of each kv head combines; one launch)."""
+        split workgroup of each kv head combines; one launch; block kernel only). impl: 0 or 1 = block kernel,
+        2 = MFMA kernel."""
         for t, n in ((qkv, "qkv"), (cos_t, "cos_t"), (sin_t, "sin_t"), (pos, "pos"), (bt, "bt"), (kc, "kc"),
                      (vc, "vc"), (o_part, "o_part"), (m_part, "m_part"), (l_part, "l_part"), (out, "out")):
             _check_cuda(t, n)
@@ -273,9 +274,9 @@ class DecodeKernels:
                 raise RuntimeError("attention_decode: counters must be int32 [n_kv]")
         self._call(self.lib.dk_attention_decode, qkv.data_ptr(), cos_t.data_ptr(), sin_t.data_ptr(), cos_t.size(0),
                    pos.data_ptr(), bt.data_ptr(), bt.numel(), kc.data_ptr(), vc.data_ptr(), kc.size(0), kc.size(2),
-                   int(n_q), int(n_kv), D, int(part_size), max_splits, o_part.data_ptr(), m_part.data_ptr(),
-                   l_part.data_ptr(), None if counters is None else counters.data_ptr(), out.data_ptr(),
-                   _stream(qkv))
+                   int(n_q), int(n_kv), D, int(part_size), max_splits, int(impl), o_part.data_ptr(),
+                   m_part.data_ptr(), l_part.data_ptr(), None if counters is None else counters.data_ptr(),
+                   out.data_ptr(), _stream(qkv))
 
     # kernels/bindings.cpp:64-72
     def add_rmsnorm(self, x, delta, w, out, eps):

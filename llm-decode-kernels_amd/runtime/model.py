@@ -48,6 +48,7 @@ class DecodeConfig:
     page: int = 16
     part_size: int = 0
     attn_version: int = 0
+    attn_impl: int = 0             # decode attention kernel: 0 = policy table, 1 = block kernel, 2 = MFMA kernel
     gemv_stage: tuple = None
     autotune_path: str = str(PKG / "configs" / "autotune.json")
     attn_policy_path: str = str(PKG / "configs" / "attn_policy.json")
@@ -204,10 +205,14 @@ class Model:
         self.host_pos = 0
 
     # ------------------------------------------------------------------ helpers
-    def set_attention_partition(self, ctx_cap, part_size=None):
-        """Split size for contexts up to ctx_cap and the split buffers (runtime/model.py:140-151): the grid is fixed
-        at ceil(ctx_cap / part_size) splits, surplus ones exit."""
-        ps = part_size or self.cfg.part_size or self._policy_part_size(ctx_cap)
+    def set_attention_partition(self, ctx_cap, part_size=None, impl=None):
+        """Split size (and attention kernel) for contexts up to ctx_cap and the split buffers (runtime/model.py:140-151):
+        the grid is fixed at ceil(ctx_cap / part_size) splits, surplus ones exit."""
+        ent = self._policy_entry(ctx_cap)
+        ps = part_size or self.cfg.part_size or ent.get("part_size", 64)
+        self.attn_impl = impl or self.cfg.attn_impl or ent.get("impl", 1)
+        if self.attn_impl == 2 and ((ps - 1) >> (self.cfg.page.bit_length() - 1)) + 2 > 1024:
+            self.attn_impl = 1                      # the MFMA kernel stages at most 1024 pages per split
         self.part_size = ps
         self.max_splits = max(1, math.ceil(ctx_cap / ps))
         self.ctx_cap = self.max_splits * ps
@@ -219,10 +224,10 @@ class Model:
         self.attn_counters = torch.zeros(self.n_kv, dtype=torch.int32, device=self.cfg.device)
         self.graph = None
 
-    def prepare(self, ctx_cap, use_graph=True, part_size=None):
+    def prepare(self, ctx_cap, use_graph=True, part_size=None, impl=None):
         """Configure attention for contexts <= ctx_cap and (re)capture the decode graph (runtime/model.py:153-158)."""
         assert ctx_cap <= self.cfg.max_ctx
-        self.set_attention_partition(ctx_cap, part_size)
+        self.set_attention_partition(ctx_cap, part_size, impl)
         if use_graph:
             self.capture()
 
@@ -230,15 +235,15 @@ class Model:
         p = Path(self.cfg.attn_policy_path)
         return json.load(open(p)) if p.exists() else {}
 
-    def _policy_part_size(self, ctx_cap):
+    def _policy_entry(self, ctx_cap):
         """Entry tuned at the largest context <= ctx_cap (runtime/model.py:164-172), from the head-dim-specific table
-        ("policy_d128") when there is one."""
+        ("policy_d128") when there is one: {"part_size", "impl"}."""
         pol = self._policy()
         ents = [e for e in pol.get(f"policy_d{self.D}", pol.get("policy", [])) if e["max_ctx"] < (1 << 30)]
         if not ents:
-            return 64
+            return {"part_size": 64, "impl": 1}
         below = [e for e in ents if e["max_ctx"] <= ctx_cap]
-        return (below[-1] if below else ents[0])["part_size"]
+        return below[-1] if below else ents[0]
 
     def gemv_cfg(self, lin):
         if self.cfg.gemv_stage is not None:
@@ -338,7 +343,8 @@ class Model:
         if self.cfg.fused_attention:
             self.K.attention_decode(self.qkv, self.cos, self.sin, self.pos, self.bt, kc, vc, self.n_q, self.n_kv,
                                     self.part_size, self.o_part, self.m_part, self.l_part, self.attn,
-                                    self.attn_counters if self.cfg.combine_in_split else None)
+                                    self.attn_counters if self.cfg.combine_in_split else None,
+                                    1 if self.cfg.combine_in_split else self.attn_impl)
             return
         self.K.rope_append(self.qkv, self.cos, self.sin, self.pos, self.bt, kc, vc, self.n_q, self.n_kv)
         self.K.paged_attention(self.qkv[: self.n_q * self.D], kc, vc, self.bt, self.pos, self.part_size,

@@ -20,8 +20,12 @@ def K():
     return ext.load()
 
 
-def run_fused(K, qkv, cos, sin, kc, vc, bt, pos, n_q, n_kv, PS, max_splits, counters=False):
-    """counters=True: the in-split combine (per-kv-head arrival counters, which every launch must leave at zero)."""
+MODES = ("block", "counters", "mfma")   # impl 1, impl 1 with the in-split combine, impl 2
+
+
+def run_fused(K, qkv, cos, sin, kc, vc, bt, pos, n_q, n_kv, PS, max_splits, mode="block"):
+    """mode "counters": the in-split combine (per-kv-head arrival counters, which every launch must leave at zero)."""
+    counters = mode == "counters"
     D = kc.shape[-1]
     o_part = torch.full((n_q, max_splits, D), 7.0, device=DEV)
     m_part = torch.full((n_q, max_splits), 7.0, device=DEV)
@@ -29,7 +33,7 @@ def run_fused(K, qkv, cos, sin, kc, vc, bt, pos, n_q, n_kv, PS, max_splits, coun
     out = torch.zeros(n_q, D, dtype=torch.half, device=DEV)
     cnt = torch.zeros(n_kv, dtype=torch.int32, device=DEV) if counters else None
     K.attention_decode(qkv, cos, sin, torch.tensor([pos], dtype=torch.int32, device=DEV), bt, kc, vc, n_q, n_kv, PS,
-                       o_part, m_part, l_part, out, cnt)
+                       o_part, m_part, l_part, out, cnt, impl=2 if mode == "mfma" else 1)
     if counters:
         assert torch.all(cnt == 0), "arrival counters must be left at zero"
     return out, o_part, m_part
@@ -47,8 +51,8 @@ CASES = [(64, 32, 4), (64, 8, 8), (64, 16, 4), (64, 8, 4), (128, 32, 8), (128, 6
 
 @pytest.mark.parametrize("D,n_q,n_kv", CASES)
 @pytest.mark.parametrize("ctx", (1, 2, 17, 64, 65, 500, 2048))
-@pytest.mark.parametrize("counters", (False, True))
-def test_fused_attention_matches_rope_then_attention(K, D, n_q, n_kv, ctx, counters):
+@pytest.mark.parametrize("mode", MODES)
+def test_fused_attention_matches_rope_then_attention(K, D, n_q, n_kv, ctx, mode):
     page = 16
     theta = 1e4 if D == 64 else 5e5
     cos, sin = R.rope_tables(ctx + 8, D, theta)
@@ -59,15 +63,15 @@ def test_fused_attention_matches_rope_then_attention(K, D, n_q, n_kv, ctx, count
         ms = -(-ctx // PS)
         kd, vd, qd = kc.to(DEV), vc.to(DEV), qkv.to(DEV)
         out, _, _ = run_fused(K, qd, cos.to(DEV), sin.to(DEV), kd, vd, bt.to(DEV), ctx - 1, n_q, n_kv, PS, ms,
-                              counters)
-        assert_close(out, ref, 2e-3, f"fused D{D} {n_q}/{n_kv} ctx{ctx} PS{PS} counters={counters}")
+                              mode)
+        assert_close(out, ref, 2e-3, f"fused D{D} {n_q}/{n_kv} ctx{ctx} PS{PS} {mode}")
         assert torch.equal(kd.cpu(), kr) and torch.equal(vd.cpu(), vr), f"cache append D{D} ctx{ctx} PS{PS}"
         assert torch.equal(qd.cpu(), qkv), "qkv must not be modified"
 
 
 @pytest.mark.parametrize("ctx", (100, 1000, 4096))
-@pytest.mark.parametrize("counters", (False, True))
-def test_fused_attention_spare_splits_untouched(K, ctx, counters):
+@pytest.mark.parametrize("mode", MODES)
+def test_fused_attention_spare_splits_untouched(K, ctx, mode):
     """Grid sized for more splits than ctx needs (the runtime's cap): partials past the live splits stay untouched."""
     D, n_q, n_kv, page, PS, spare = 64, 32, 4, 16, 64, 7
     cos, sin = R.rope_tables(ctx + 8, D)
@@ -76,13 +80,13 @@ def test_fused_attention_spare_splits_untouched(K, ctx, counters):
     ref, _, _ = reference(qkv, cos, sin, kc, vc, bt, ctx - 1, n_q, n_kv, D, page)
     live = -(-ctx // PS)
     out, o_part, m_part = run_fused(K, qkv.to(DEV), cos.to(DEV), sin.to(DEV), kc.to(DEV), vc.to(DEV), bt.to(DEV),
-                                       ctx - 1, n_q, n_kv, PS, live + spare, counters)
+                                       ctx - 1, n_q, n_kv, PS, live + spare, mode)
     assert_close(out, ref, 2e-3, f"spare ctx{ctx}")
     assert torch.all(o_part[:, live:] == 7.0) and torch.all(m_part[:, live:] == 7.0)
 
 
-@pytest.mark.parametrize("counters", (False, True))
-def test_fused_attention_cap_below_position(K, counters):
+@pytest.mark.parametrize("mode", MODES)
+def test_fused_attention_cap_below_position(K, mode):
     """pos beyond max_splits * PS: the new k / v are still appended (by the last live split) and attention covers the
     first max_splits * PS tokens, as rope_append + paged_attention with the same split buffers do."""
     D, n_q, n_kv, page, PS, ms, pos = 64, 32, 4, 16, 32, 4, 200
@@ -92,25 +96,25 @@ def test_fused_attention_cap_below_position(K, counters):
     ref, kr, vr = reference(qkv, cos, sin, kc, vc, bt, pos, n_q, n_kv, D, page, attend=ms * PS)
     kd, vd = kc.to(DEV), vc.to(DEV)
     out, _, _ = run_fused(K, qkv.to(DEV), cos.to(DEV), sin.to(DEV), kd, vd, bt.to(DEV), pos, n_q, n_kv, PS, ms,
-                          counters)
+                          mode)
     assert_close(out, ref, 2e-3, "cap")
     assert torch.equal(kd.cpu(), kr) and torch.equal(vd.cpu(), vr)
 
 
-@pytest.mark.parametrize("counters", (False, True))
-def test_fused_attention_position_outside_table_is_noop(K, counters):
+@pytest.mark.parametrize("mode", MODES)
+def test_fused_attention_position_outside_table_is_noop(K, mode):
     D, n_q, n_kv = 64, 32, 4
     cos, sin = R.rope_tables(64, D)
     kc, vc, bt = make_cache(80, n_kv, 16, D=D, seed=8)
     qkv = torch.randn((n_q + 2 * n_kv) * D, generator=gen(8)).half()
     kd = kc.to(DEV)
     out, o_part, _ = run_fused(K, qkv.to(DEV), cos.to(DEV), sin.to(DEV), kd, vc.to(DEV), bt.to(DEV), 64, n_q,
-                               n_kv, 16, 5, counters)
+                               n_kv, 16, 5, mode)
     assert torch.equal(kd.cpu(), kc) and torch.all(out == 0) and torch.all(o_part == 7.0)
 
 
-@pytest.mark.parametrize("counters", (False, True))
-def test_fused_attention_graph_replays(K, counters):
+@pytest.mark.parametrize("mode", MODES)
+def test_fused_attention_graph_replays(K, mode):
     """One captured launch replayed at several positions (the graph reads *pos anew), eager work between replays;
     every replay equals the eager result; the in-split combine's counters are back at zero after every replay."""
     D, n_q, n_kv, page, PS, ms = 64, 32, 4, 16, 32, 10
@@ -124,10 +128,11 @@ def test_fused_attention_graph_replays(K, counters):
     m_part = torch.empty(n_q, ms, device=DEV)
     l_part = torch.empty_like(m_part)
     out = torch.empty(n_q, D, dtype=torch.half, device=DEV)
-    cnt = torch.zeros(n_kv, dtype=torch.int32, device=DEV) if counters else None
+    cnt = torch.zeros(n_kv, dtype=torch.int32, device=DEV) if mode == "counters" else None
 
     def body():
-        K.attention_decode(qkv, cos, sin, pos, bt, kc, vc, n_q, n_kv, PS, o_part, m_part, l_part, out, cnt)
+        K.attention_decode(qkv, cos, sin, pos, bt, kc, vc, n_q, n_kv, PS, o_part, m_part, l_part, out, cnt,
+                           impl=2 if mode == "mfma" else 1)
 
     expected = {}
     for p in (0, 31, 32, 150, 319):

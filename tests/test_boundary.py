@@ -89,8 +89,9 @@ def _attn(lib, **kw):
     (dict(head_dim=96), 3, "head_dim"),
     (dict(page=12), 4, "page size must be a power of two"),
     (dict(part_size=0), 4, "part_size must be > 0"),
-    (dict(version=4), 4, "version must be 1, 2 or 3"),
-    (dict(version=0), 4, "version must be 1, 2 or 3"),
+    (dict(version=5), 4, "version must be 1, 2, 3 or 4"),
+    (dict(version=0), 4, "version must be 1, 2, 3 or 4"),
+    (dict(version=4, part_size=32768), 4, "block-table pages per split"),
     (dict(max_splits=0), 3, "max_splits"),
     (dict(kc=A16 + 2), 2, "16B aligned"),
     (dict(bt=None), 1, "null"),
@@ -103,7 +104,7 @@ def test_attention_validation(lib, kw, code, msg):
 
 def _dec(lib, **kw):
     a = dict(qkv=A16, c=A16, s=A16, max_pos=100, pos=A16, bt=A16, n_bt=8, kc=A16, vc=A16, n_pages=8, page=16, n_q=32,
-             n_kv=4, D=64, part_size=64, max_splits=4, o=A16, m=A16, l=A16, counters=None, out=A16)
+             n_kv=4, D=64, part_size=64, max_splits=4, impl=0, o=A16, m=A16, l=A16, counters=None, out=A16)
     a.update(kw)
     return _err(lib, lib.dk_attention_decode(*a.values(), None))
 
@@ -115,6 +116,9 @@ def _dec(lib, **kw):
     (dict(part_size=0), 4, "part_size must be > 0"),
     (dict(max_splits=0), 3, "max_splits"),
     (dict(counters=A16 + 2), 2, "counters must be 4B aligned"),
+    (dict(impl=3), 4, "impl must be 0, 1 or 2"),
+    (dict(impl=2, counters=A16), 4, "belongs to impl 1"),
+    (dict(impl=2, part_size=32768, page=16), 4, "block-table pages per split"),
     (dict(max_pos=0), 3, "empty"),
     (dict(c=None), 1, "null"),
     (dict(qkv=A16 + 2), 2, "16B aligned"),

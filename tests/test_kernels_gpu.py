@@ -131,8 +131,27 @@ def test_quantize_ties(K):
 
 
 # ---------------------------------------------------------------------------------------------------- attention
+def close_or_rejected(out, ref, tol, what):
+    if out is not None:
+        assert_close(out, ref, tol, what)
+
+
+def mfma_fits(PS, page):
+    """version 4 / impl 2 stage a split's block-table pages in LDS (at most 1024 of them)."""
+    return ((PS - 1) >> (page.bit_length() - 1)) + 2 <= 1024
+
+
 def run_attn(K, q, kc, vc, bt, ctx, PS, version=3, spare=0):
-    """spare > 0 sizes the split buffers for more splits than ctx needs, as the runtime does."""
+    """spare > 0 sizes the split buffers for more splits than ctx needs, as the runtime does. A part size the MFMA
+    kernel (version 4) cannot stage must be rejected: then the call is checked to raise and None is returned."""
+    if version == 4 and not mfma_fits(PS, kc.shape[2]):
+        with pytest.raises(RuntimeError, match="block-table pages per split"):
+            _run_attn(K, q, kc, vc, bt, ctx, PS, version, spare)
+        return None
+    return _run_attn(K, q, kc, vc, bt, ctx, PS, version, spare)
+
+
+def _run_attn(K, q, kc, vc, bt, ctx, PS, version, spare):
     D = kc.shape[-1]
     n_q = q.numel() // D
     max_splits = max(1, (ctx + PS - 1) // PS) + spare
@@ -153,58 +172,65 @@ def test_attention_ctx128(K, n_q, n_kv, page):
     k, v = R.gather_kv(kc, vc, bt, 128, page)
     ref = R.attention_contiguous_ref(q, k, v)
     for PS in (4096, 64, 32, 48, 16):
-        for ver in (1, 2, 3):
-            assert_close(run_attn(K, q, kc, vc, bt, 128, PS, ver), ref, 2e-3, f"ctx128 {n_q}/{n_kv} P{page} PS{PS}")
+        for ver in (1, 2, 3, 4):
+            close_or_rejected(run_attn(K, q, kc, vc, bt, 128, PS, ver), ref, 2e-3,
+                         f"ctx128 {n_q}/{n_kv} P{page} PS{PS} v{ver}")
 
 
 @pytest.mark.parametrize("ctx", (1, 2, 17, 63, 65, 129, 1000))
-def test_attention_odd_ctx(K, ctx):
+@pytest.mark.parametrize("ver", (3, 4))
+def test_attention_odd_ctx(K, ver, ctx):
     kc, vc, bt = make_cache(ctx, 4, 16, seed=ctx)
     q = torch.randn(32, 64, generator=gen(ctx + 1)).half()
     ref = R.paged_attention_ref(q, kc, vc, bt, ctx, 16)
     for PS in (8192, 64, 256):
-        assert_close(run_attn(K, q, kc, vc, bt, ctx, PS), ref, 2e-3, f"ctx{ctx} PS{PS}")
+        close_or_rejected(run_attn(K, q, kc, vc, bt, ctx, PS, ver), ref, 2e-3, f"ctx{ctx} PS{PS} v{ver}")
 
 
 @pytest.mark.parametrize("ctx", (512, 1024, 2048, 4096, 8192, 16384))
 @pytest.mark.parametrize("peaky", (1.0, 6.0))
-def test_attention_real_ctx(K, ctx, peaky):
+@pytest.mark.parametrize("ver", (3, 4))
+def test_attention_real_ctx(K, ver, ctx, peaky):
     kc, vc, bt = make_cache(ctx, 4, 16, peaky=peaky, seed=ctx)
     q = torch.randn(32, 64, generator=gen(ctx + 2)).half()
     ref = R.paged_attention_ref(q, kc, vc, bt, ctx, 16)
     for PS in sorted({ctx, 1024, 256, 128, 64, 32}):
-        assert_close(run_attn(K, q, kc, vc, bt, ctx, PS), ref, 2e-3, f"ctx{ctx} peaky{peaky} PS{PS}")
+        close_or_rejected(run_attn(K, q, kc, vc, bt, ctx, PS, ver), ref, 2e-3, f"ctx{ctx} peaky{peaky} PS{PS} v{ver}")
 
 
 @pytest.mark.parametrize("ctx", (1, 40, 64, 100, 700, 2048, 5000))
-def test_attention_runtime_spare_splits(K, ctx):
+@pytest.mark.parametrize("ver", (3, 4))
+def test_attention_runtime_spare_splits(K, ver, ctx):
     kc, vc, bt = make_cache(ctx, 4, 16, peaky=6.0, seed=ctx + 3)
     q = torch.randn(32, 64, generator=gen(ctx + 4)).half()
     ref = R.paged_attention_ref(q, kc, vc, bt, ctx, 16)
     for PS in (32, 64, 128, 256):
-        assert_close(run_attn(K, q, kc, vc, bt, ctx, PS, spare=8), ref, 2e-3, f"runtime ctx{ctx} PS{PS}")
+        close_or_rejected(run_attn(K, q, kc, vc, bt, ctx, PS, ver, spare=8), ref, 2e-3, f"runtime ctx{ctx} PS{PS} v{ver}")
 
 
 @pytest.mark.parametrize("n_q,n_kv", [(32, 8), (8, 8), (16, 8), (64, 8)])
 @pytest.mark.parametrize("ctx", (1, 100, 777, 4096))
-def test_attention_head_dim_128(K, n_q, n_kv, ctx):
+@pytest.mark.parametrize("ver", (3, 4))
+def test_attention_head_dim_128(K, ver, n_q, n_kv, ctx):
     kc, vc, bt = make_cache(ctx, n_kv, 16, D=128, peaky=2.0, seed=ctx + n_q)
     q = torch.randn(n_q, 128, generator=gen(ctx)).half()
     ref = R.paged_attention_ref(q, kc, vc, bt, ctx, 16)
     for PS in (ctx, 64, 256):
-        assert_close(run_attn(K, q, kc, vc, bt, ctx, PS), ref, 2e-3, f"D128 {n_q}/{n_kv} ctx{ctx} PS{PS}")
+        close_or_rejected(run_attn(K, q, kc, vc, bt, ctx, PS, ver), ref, 2e-3, f"D128 {n_q}/{n_kv} ctx{ctx} PS{PS} v{ver}")
 
 
-def test_attention_ctx1_is_v0(K):
+@pytest.mark.parametrize("ver", (3, 4))
+def test_attention_ctx1_is_v0(K, ver):
     """Softmax over one token returns that token's V exactly (fp16 in, fp16 out)."""
     kc, vc, bt = make_cache(1, 4, 16, seed=9)
     q = torch.randn(32, 64, generator=gen(9)).half()
-    out = run_attn(K, q, kc, vc, bt, 1, 64).cpu()
+    out = run_attn(K, q, kc, vc, bt, 1, 64, ver).cpu()
     v0 = vc[bt[0], :, 0]                          # [n_kv, D]
     assert torch.equal(out, v0.repeat_interleave(8, dim=0))
 
 
-def test_attention_split_buffers_ignored_past_live(K):
+@pytest.mark.parametrize("ver", (3, 4))
+def test_attention_split_buffers_ignored_past_live(K, ver):
     """Splits beyond ceil(ctx/PS) must not touch the buffers (grid sized for the cap, surplus splits exit)."""
     ctx, PS, spare = 100, 32, 6
     kc, vc, bt = make_cache(ctx, 4, 16, seed=11)
@@ -215,7 +241,7 @@ def test_attention_split_buffers_ignored_past_live(K):
     l_part = torch.full((32, ms), 7.0, device=DEV)
     out = torch.empty(32, 64, dtype=torch.half, device=DEV)
     pos = torch.tensor([ctx - 1], dtype=torch.int32, device=DEV)
-    K.paged_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), bt.to(DEV), pos, PS, o_part, m_part, l_part, out, 3)
+    K.paged_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), bt.to(DEV), pos, PS, o_part, m_part, l_part, out, ver)
     live = (ctx + PS - 1) // PS
     assert torch.all(o_part[:, live:] == 7.0) and torch.all(m_part[:, live:] == 7.0)
     assert_close(out, R.paged_attention_ref(q, kc, vc, bt, ctx, 16), 2e-3, "spare")
