@@ -198,9 +198,12 @@ int dk_argmax_advance(const void* logits, int V, int64_t* tok, int32_t* pos, voi
  * INT4 format producer on the GPU: round-to-nearest asymmetric group quantization of fp16 W [N, K] and packing,
  * bit-identical to runtime/quant.py quantize (:42-48, RTN branch of group_params :20-28) + pack (:100-109) +
  * pack_scale_zero (:122-124). Writes packed int32 [N, K/8] and sz fp16 [N, K/G, 2].
+ * clip = 1: quantize(clip=True), the per-group range clipping of group_params (:17-38): the group's [min, max] is
+ * shrunk by the factor of (1.0, 0.95, ..., 0.7) with the smallest squared rounding error (summed in fp64; the
+ * reference sums in fp32, so only near-ties of two factors can resolve differently). clip = 0: RTN.
  * group a power of two in [32, 512] with K % group == 0.
  */
-int dk_quantize_w4(const void* w, void* packed, void* sz, int N, int K, int group, void* stream);
+int dk_quantize_w4(const void* w, void* packed, void* sz, int N, int K, int group, int clip, void* stream);
 
 #ifdef __cplusplus
 }

@@ -330,7 +330,7 @@ int dk_argmax_advance(const void* logits, int V, int64_t* tok, int32_t* pos, voi
   return launched("argmax_advance");
 }
 
-int dk_quantize_w4(const void* w, void* packed, void* sz, int N, int K, int group, void* stream) {
+int dk_quantize_w4(const void* w, void* packed, void* sz, int N, int K, int group, int clip, void* stream) {
   if (!w || !packed || !sz) return fail(DK_ERR_NULL, "quantize_w4: null pointer argument");
   if (N <= 0 || K <= 0) return fail(DK_ERR_SHAPE, "quantize_w4: N and K must be positive");
   if (!pow2(group) || group < 32 || group > 512)
@@ -340,7 +340,8 @@ int dk_quantize_w4(const void* w, void* packed, void* sz, int N, int K, int grou
   if (!aligned16(w)) return fail(DK_ERR_ALIGN, "w must be 16B aligned");
   if (!aligned4(packed) || !aligned4(sz)) return fail(DK_ERR_ALIGN, "packed and sz must be 4B aligned");
   clear_error();
-  dk::launch_quantize_w4(w, packed, sz, N, K, ilog2(group), (hipStream_t)stream);
+  if (clip != 0 && clip != 1) return fail(DK_ERR_DOMAIN, "quantize_w4: clip must be 0 or 1, got %d", clip);
+  dk::launch_quantize_w4(w, packed, sz, N, K, ilog2(group), clip, (hipStream_t)stream);
   return launched("quantize_w4");
 }
 

@@ -77,6 +77,6 @@ void launch_rope_append(void* qkv, const float* cos_t, const float* sin_t, const
 
 void launch_argmax_advance(const void* logits, int V, int64_t* tok, int32_t* pos, hipStream_t st);
 
-void launch_quantize_w4(const void* w, void* packed, void* sz, int N, int K, int log2G, hipStream_t st);
+void launch_quantize_w4(const void* w, void* packed, void* sz, int N, int K, int log2G, int clip, hipStream_t st);
 
 }  // namespace dk

@@ -36,7 +36,7 @@ SIGNATURES = {
     "dk_swiglu": ([_P, _P, _I, _P], _I),
     "dk_rope_append": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "dk_argmax_advance": ([_P, _I, _P, _P, _P], _I),
-    "dk_quantize_w4": ([_P, _P, _P, _I, _I, _I, _P], _I),
+    "dk_quantize_w4": ([_P, _P, _P, _I, _I, _I, _I, _P], _I),
 }
 
 _EXT = None
@@ -343,7 +343,7 @@ class DecodeKernels:
         self._call(self.lib.dk_argmax_advance, logits.data_ptr(), logits.numel(), tok.data_ptr(), p, _stream(logits))
 
     # runtime/quant.py:42-48,100-124 on the GPU
-    def quantize_w4(self, w, packed, sz, group):
+    def quantize_w4(self, w, packed, sz, group, clip=False):
         for t, n in ((w, "w"), (packed, "packed"), (sz, "sz")):
             _check_cuda(t, n)
         N, K = w.shape
@@ -353,7 +353,7 @@ class DecodeKernels:
         _check_dtype(packed, torch.int32, "packed")
         _check_dtype(sz, torch.float16, "sz")
         self._call(self.lib.dk_quantize_w4, w.data_ptr(), packed.data_ptr(), sz.data_ptr(), N, K, int(group),
-                   _stream(w))
+                   int(bool(clip)), _stream(w))
 
 
 def load(verbose=False):

@@ -16,7 +16,8 @@ Differences from the reference, all on the device side of the same composition:
   * weights are quantized on the GPU by the HIP RTN kernel;
   * there is no ``backend="ref"``: the CPU reference composition is test infrastructure (``oracle.decode_ref``).
 
-Knobs (DecodeConfig): weights "int4" | "fp16"; group; lm_head "auto" | "fp16" | "int4"; fused (False runs the
+Knobs (DecodeConfig): weights "int4" | "fp16"; group; quant "rtn" | "clip" | "pre" (precomputed codes in qparams, e.g.
+from runtime.gptq.calibrate); lm_head "auto" | "fp16" | "int4"; fused (False runs the
 HF-style torch op sequences for norm and SwiGLU on the GPU, the reference's unfused comparison point); max_ctx, page,
 part_size (0 -> attention policy table), attn_version, gemv_stage ((stage, R, warps, pf) forced everywhere, or None for
 the tuning table), autotune_path, attn_policy_path, shuffle_pages, device; fused_attention, fused_gemv and swiglu
@@ -39,8 +40,9 @@ PKG = Path(__file__).resolve().parents[1]
 class DecodeConfig:
     weights: str = "int4"
     group: int = 128
-    quant: str = "rtn"
-    qparams: dict = field(default=None, repr=False)
+    quant: str = "rtn"             # "rtn" | "clip" (RTN with per-group range clipping, on the GPU) | "pre" (qparams)
+    qparams: dict = field(default=None, repr=False)  # "layers.{i}.{qkv,o,gu,down}" / "lm_head" -> (q, scale, zero),
+                                                     # e.g. runtime.gptq.calibrate
     lm_head: str = "auto"
     fused: bool = True
     backend: str = "hip"
@@ -86,15 +88,20 @@ class Linear:
     dk_gemv_w4a16_gate_up reads); quantization is per row, so this is a pure row permutation of the stacked
     quantization. ``rows_reference_order`` undoes it for anything that needs the reference's row order."""
 
-    def __init__(self, w, cfg: DecodeConfig, quant: bool, interleave_pairs: bool = False):
+    def __init__(self, w, cfg: DecodeConfig, quant: bool, interleave_pairs: bool = False, key: str = None):
         self.N, self.K = w.shape
         self.quant = quant
         self.pairs_interleaved = interleave_pairs and quant
         dev = cfg.device
         if quant:
-            if cfg.quant != "rtn":
-                raise NotImplementedError("only RTN quantization is produced by this runtime")
-            ql = QuantLinear(w.to(dev), cfg.group)
+            if cfg.quant not in ("rtn", "clip", "pre"):
+                raise ValueError(f"quant {cfg.quant!r}: 'rtn', 'clip' or 'pre'")
+            pre = None
+            if cfg.quant == "pre":
+                pre = (cfg.qparams or {}).get(key)
+                if pre is None:
+                    raise ValueError(f"quant='pre': no precomputed codes for {key!r} in qparams")
+            ql = QuantLinear(w.to(dev), cfg.group, clip=cfg.quant == "clip", qsz=pre)
             self.packed, self.sz = ql.packed, ql.sz
             self.nbytes = ql.nbytes()
             if self.pairs_interleaved:
@@ -149,20 +156,20 @@ class Model:
             p = f"model.layers.{i}."
             wqkv = torch.cat([g(p + "self_attn.q_proj.weight"), g(p + "self_attn.k_proj.weight"),
                               g(p + "self_attn.v_proj.weight")], 0)
-            qkv = Linear(wqkv, cfg, quant)
+            qkv = Linear(wqkv, cfg, quant, key=f"layers.{i}.qkv")
             del wqkv
             wgu = torch.cat([g(p + "mlp.gate_proj.weight"), g(p + "mlp.up_proj.weight")], 0)
-            gu = Linear(wgu, cfg, quant, interleave_pairs=self.gate_up_epilogue)
+            gu = Linear(wgu, cfg, quant, interleave_pairs=self.gate_up_epilogue, key=f"layers.{i}.gu")
             del wgu
             self.layers.append({
                 "ln1": g(p + "input_layernorm.weight").to(dev).contiguous(),
                 "ln2": g(p + "post_attention_layernorm.weight").to(dev).contiguous(),
-                "qkv": qkv, "o": Linear(g(p + "self_attn.o_proj.weight"), cfg, quant),
-                "gu": gu, "down": Linear(g(p + "mlp.down_proj.weight"), cfg, quant)})
+                "qkv": qkv, "o": Linear(g(p + "self_attn.o_proj.weight"), cfg, quant, key=f"layers.{i}.o"),
+                "gu": gu, "down": Linear(g(p + "mlp.down_proj.weight"), cfg, quant, key=f"layers.{i}.down")})
         self.norm_f = g("model.norm.weight").to(dev).contiguous()
         lm = sd["lm_head.weight"] if "lm_head.weight" in sd else sd["model.embed_tokens.weight"]
         head_int4 = cfg.lm_head == "int4" or (cfg.lm_head == "auto" and quant)
-        self.lm_head = Linear(lm.half(), cfg, head_int4)
+        self.lm_head = Linear(lm.half(), cfg, head_int4, key="lm_head")
 
         self.gemv_table, self.gemv_tile_table, self.gemv_norm_table, self.gemv_gate_up_table = {}, {}, {}, {}
         self.gemv_f16_table, self.gemv_f16_norm_table = {}, {}

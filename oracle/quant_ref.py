@@ -2,7 +2,7 @@
 
 Follows ``runtime/quant.py`` of the reference:
   * RTN group parameters  ``group_params`` (clip=False branch)      runtime/quant.py:20-39
-  * ``quantize``                                                    runtime/quant.py:42-48
+  * ``quantize`` (RTN, and the clip search of ``group_params``)      runtime/quant.py:17-48
   * ``dequantize``                                                  runtime/quant.py:93-97
   * ``pack`` / ``unpack``                                           runtime/quant.py:100-119
   * ``pack_scale_zero``                                             runtime/quant.py:122-124
@@ -29,27 +29,57 @@ def _as_f32(w):
     return a
 
 
-def group_params(wf):
-    """wf float32 [..., G] -> (scale, zero) float32 [..., 1] (runtime/quant.py:20-28, clip=False).
+CLIP_GRID = (1.0, 0.95, 0.9, 0.85, 0.8, 0.75, 0.7)   # runtime/quant.py:17
 
-    scale is fp16-representable (rounded to fp16 and read back); zero is an integer in [0, 15]."""
-    wf = _as_f32(wf)
-    lo = wf.min(axis=-1, keepdims=True)
-    hi = wf.max(axis=-1, keepdims=True)
+
+def _range_params(lo, hi):
     step = np.maximum((hi - lo) / F32(15), SCALE_FLOOR).astype(F32)
     scale = step.astype(np.float16).astype(F32)
     zero = np.clip(np.rint(-lo / scale), F32(0), F32(15)).astype(F32)
     return scale, zero
 
 
-def quantize(w, group):
+def clip_errors(wf, scale, zero):
+    """Squared rounding error of each group (float64 sum of the float32 terms (q - zero) * scale - w, squared in
+    float32 as runtime/quant.py:33 computes them)."""
+    d = ((np.clip(np.rint(wf / scale) + zero, F32(0), F32(15)) - zero) * scale - wf).astype(F32)
+    return (d * d).astype(np.float64).sum(axis=-1, keepdims=True)
+
+
+def group_params(wf, clip=False):
+    """wf float32 [..., G] -> (scale, zero) float32 [..., 1] (runtime/quant.py:20-38).
+
+    scale is fp16-representable (rounded to fp16 and read back); zero is an integer in [0, 15]. clip=True shrinks the
+    group's [min, max] by the factor of CLIP_GRID (float32, as torch multiplies a float32 tensor by a Python float)
+    whose parameters give the smallest squared rounding error, the first factor on ties (the reference's strict
+    `err < best`). The errors are summed in float64 here (the reference sums in float32), so this is the exact argmin
+    of the reference's float32 terms; the two can differ only where two factors' errors agree within float32
+    summation noise."""
+    wf = _as_f32(wf)
+    lo = wf.min(axis=-1, keepdims=True)
+    hi = wf.max(axis=-1, keepdims=True)
+    if not clip:
+        return _range_params(lo, hi)
+    best = None
+    for a in CLIP_GRID:
+        scale, zero = _range_params((lo * F32(a)).astype(F32), (hi * F32(a)).astype(F32))
+        err = clip_errors(wf, scale, zero)
+        if best is None:
+            best = [err, scale, zero]
+        else:
+            m = err < best[0]
+            best = [np.where(m, err, best[0]), np.where(m, scale, best[1]), np.where(m, zero, best[2])]
+    return best[1], best[2]
+
+
+def quantize(w, group, clip=False):
     """w [N, K] fp16/fp32 -> (q uint8 [N, K], scale fp16 [N, K/G], zero fp16 [N, K/G]) (runtime/quant.py:42-48)."""
     wf = _as_f32(w)
     N, K = wf.shape
     if K % group:
         raise ValueError(f"K={K} is not a multiple of group={group}")
     g = wf.reshape(N, K // group, group)
-    scale, zero = group_params(g)
+    scale, zero = group_params(g, clip)
     q = np.clip(np.rint(g / scale) + zero, F32(0), F32(15))
     return (q.reshape(N, K).astype(np.uint8), scale.reshape(N, -1).astype(np.float16),
             zero.reshape(N, -1).astype(np.float16))
