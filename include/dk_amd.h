@@ -116,6 +116,45 @@ int dk_gemv_f16_rmsnorm(int R, int warps, int pf, const void* w, const void* x, 
                         float eps, void* x_out, void* y, int N, int K, void* stream);
 
 /*
+ * rope_append for a batch of M tokens (prefill): row m of qkv [M, (n_q + 2 n_kv) head_dim] is token *pos + m; each
+ * row is rotated and appended exactly as dk_rope_append does for one token (kernels/bindings.cpp:81-88 per row).
+ * No counterpart in the reference, which appends prompt tokens one decode step at a time.
+ */
+int dk_rope_append_rows(void* qkv, const float* cos_t, const float* sin_t, const int32_t* pos, const int32_t* bt,
+                        void* kc, void* vc, int M, int n_q, int n_kv, int head_dim, int page, int max_pos,
+                        int n_pages, int n_bt, void* stream);
+
+/*
+ * Residual + RMSNorm of M rows (prefill), each with dk_add_rmsnorm's rounding points: xn = x_in[src] + delta[r]
+ * (delta may be NULL; src = rows[r] when rows != NULL, e.g. the embedding rows of the prompt's tokens, else r),
+ * x_out[r] = xn, out[r] = w * fp16(float(xn) * rsqrt-term). x_out may equal x_in when rows is NULL; out aliases
+ * nothing. No counterpart in the reference (its add_rmsnorm is one vector, kernels/bindings.cpp:64-72).
+ */
+int dk_rmsnorm_rows(const void* x_in, const int64_t* rows, const void* delta, const void* w, void* x_out, void* out,
+                    int M, int H, float eps, void* stream);
+
+/*
+ * Causal paged attention of M prompt rows (prefill): row m (position *pos + m) attends tokens [0, *pos + m] of the
+ * cache, which must already hold them (dk_rope_append_rows); q is the first n_q heads of qkv row m, already rotated.
+ * out [M, n_q * head_dim] fp16. One split of max_ctx tokens per (kv head, row), the MFMA kernel of dk_attention_decode
+ * impl 2; positions past max_ctx are not attended. No counterpart in the reference (it teacher-forces prompts through
+ * the decode step).
+ */
+int dk_attention_prefill(const void* qkv, const int32_t* pos, const int32_t* bt, int n_bt, const void* kc,
+                         const void* vc, int n_pages, int page, int n_q, int n_kv, int head_dim, int M, int max_ctx,
+                         void* out, void* stream);
+
+/*
+ * W4A16 GEMM for prefill: Y[M, N] = X[M, K] . dequant(W)[N, K]^T, X and Y fp16 row-major, W in the GEMV's packed
+ * format; fp32 accumulation over exact products of X and the reference's dequantized fp16 weight. epilogue 0 writes
+ * Y [M, N]; epilogue 1 treats columns (2i, 2i + 1) as an interleaved (gate, up) pair and writes act [M, N/2] =
+ * fp16(silu(float(gate))) * up. No counterpart in the reference, which teacher-forces prompts through the decode step
+ * (the prefill row of the scope). K % 32 == 0, group a power of two >= 32.
+ */
+int dk_gemm_w4a16(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int group,
+                  int epilogue, void* stream);
+
+/*
  * Achievable-read-bandwidth microbenchmark: reads `bytes` (multiple of 16) from buf, XOR-folds them and writes sink
  * (uint32[1]) only on a value it never takes. Replaces bw_read (kernels/bindings.cpp:40-43,
  * kernels/gemv_w4a16.cu:133-153). unroll in {1, 4}; threads a multiple of 64 in [64, 1024]; blocks >= 1.

@@ -197,6 +197,27 @@ int dk_gemv_f16_rmsnorm(int R, int warps, int pf, const void* w, const void* x, 
   return launched("gemv_f16_rmsnorm");
 }
 
+int dk_gemm_w4a16(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int group,
+                  int epilogue, void* stream) {
+  if (!packed || !sz || !x || !y) return fail(DK_ERR_NULL, "gemm_w4a16: null pointer argument");
+  if (M <= 0 || N <= 0 || K <= 0) return fail(DK_ERR_SHAPE, "gemm_w4a16: M, N and K must be positive");
+  if (M > 65535 * 64) return fail(DK_ERR_SHAPE, "gemm_w4a16: M too large (%d)", M);
+  if (K % 32 != 0 || K % group != 0)
+    return fail(DK_ERR_SHAPE, "K must be a multiple of 32 and of the group size (K=%d group=%d)", K, group);
+  if (group < 32 || !pow2(group))
+    return fail(DK_ERR_DOMAIN, "group must be a power of two >= 32, got %d", group);
+  if (epilogue != 0 && epilogue != 1)
+    return fail(DK_ERR_DOMAIN, "gemm_w4a16: epilogue must be 0 (rows) or 1 (SwiGLU of gate/up pairs), got %d", epilogue);
+  if (epilogue == 1 && N % 2 != 0)
+    return fail(DK_ERR_SHAPE, "gemm_w4a16: the SwiGLU epilogue needs an even N (interleaved gate/up), got %d", N);
+  if (!aligned16(packed) || !aligned16(x)) return fail(DK_ERR_ALIGN, "gemm_w4a16: packed and x must be 16B aligned");
+  if (!aligned4(sz)) return fail(DK_ERR_ALIGN, "gemm_w4a16: sz must be 4B aligned");
+  if (y == x) return fail(DK_ERR_DOMAIN, "gemm_w4a16: y must not alias x");
+  clear_error();
+  dk::launch_gemm_w4a16(packed, sz, x, y, M, N, K, ilog2(group), epilogue, (hipStream_t)stream);
+  return launched("gemm_w4a16");
+}
+
 int dk_bw_read(const void* buf, size_t bytes, void* sink, int blocks, int threads, int unroll, void* stream) {
   if (!buf || !sink) return fail(DK_ERR_NULL, "bw_read: null pointer argument");
   if (!aligned16(buf)) return fail(DK_ERR_ALIGN, "buf must be 16B aligned");
@@ -317,8 +338,71 @@ int dk_rope_append(void* qkv, const float* cos_t, const float* sin_t, const int3
     return fail(DK_ERR_SHAPE, "rope_append: empty rope table, cache or block table");
   clear_error();
   dk::launch_rope_append(qkv, cos_t, sin_t, pos, bt, kc, vc, n_q, n_kv, head_dim, ilog2(page), max_pos, n_pages,
-                         n_bt, (hipStream_t)stream);
+                         n_bt, 1, (hipStream_t)stream);
   return launched("rope_append");
+}
+
+int dk_rope_append_rows(void* qkv, const float* cos_t, const float* sin_t, const int32_t* pos, const int32_t* bt,
+                        void* kc, void* vc, int M, int n_q, int n_kv, int head_dim, int page, int max_pos,
+                        int n_pages, int n_bt, void* stream) {
+  if (!qkv || !cos_t || !sin_t || !pos || !bt || !kc || !vc)
+    return fail(DK_ERR_NULL, "rope_append_rows: null pointer argument");
+  if (head_dim != 64 && head_dim != 128)
+    return fail(DK_ERR_SHAPE, "rope_append_rows: head_dim must be 64 or 128, got %d", head_dim);
+  if (n_q <= 0 || n_kv <= 0 || n_q > 65535 || n_kv > 65535)
+    return fail(DK_ERR_SHAPE, "rope_append_rows: bad head counts (n_q=%d n_kv=%d)", n_q, n_kv);
+  if (M < 1 || M > 65535) return fail(DK_ERR_SHAPE, "rope_append_rows: M must be 1..65535, got %d", M);
+  if (!pow2(page)) return fail(DK_ERR_DOMAIN, "page size must be a power of two, got %d", page);
+  if (max_pos < 1 || n_pages < 1 || n_bt < 1)
+    return fail(DK_ERR_SHAPE, "rope_append_rows: empty rope table, cache or block table");
+  clear_error();
+  dk::launch_rope_append(qkv, cos_t, sin_t, pos, bt, kc, vc, n_q, n_kv, head_dim, ilog2(page), max_pos, n_pages,
+                         n_bt, M, (hipStream_t)stream);
+  return launched("rope_append_rows");
+}
+
+int dk_rmsnorm_rows(const void* x_in, const int64_t* rows, const void* delta, const void* w, void* x_out, void* out,
+                    int M, int H, float eps, void* stream) {
+  if (!x_in || !w || !x_out || !out) return fail(DK_ERR_NULL, "rmsnorm_rows: null pointer argument");
+  if (M < 1 || M > (1 << 24)) return fail(DK_ERR_SHAPE, "rmsnorm_rows: M must be 1..2^24, got %d", M);
+  if (H <= 0 || H % 8 != 0 || H > (1 << 20))
+    return fail(DK_ERR_SHAPE, "rmsnorm_rows: H must be a positive multiple of 8 (<= 2^20), got %d", H);
+  if (!aligned16(x_in) || !aligned16(w) || !aligned16(x_out) || !aligned16(out) || (delta && !aligned16(delta)))
+    return fail(DK_ERR_ALIGN, "rmsnorm_rows: x_in, delta, w, x_out and out must be 16B aligned");
+  if (rows && (reinterpret_cast<uintptr_t>(rows) & 7u)) return fail(DK_ERR_ALIGN, "rmsnorm_rows: rows must be 8B aligned");
+  if (out == x_in || out == x_out || (delta && out == delta))
+    return fail(DK_ERR_DOMAIN, "rmsnorm_rows: out must not alias x_in, x_out or delta");
+  if (rows && x_out == x_in) return fail(DK_ERR_DOMAIN, "rmsnorm_rows: a gathered x_in must not be x_out");
+  clear_error();
+  dk::launch_rmsnorm_rows(x_in, rows, delta, w, x_out, out, M, H, eps, (hipStream_t)stream);
+  return launched("rmsnorm_rows");
+}
+
+int dk_attention_prefill(const void* qkv, const int32_t* pos, const int32_t* bt, int n_bt, const void* kc,
+                         const void* vc, int n_pages, int page, int n_q, int n_kv, int head_dim, int M, int max_ctx,
+                         void* out, void* stream) {
+  if (!qkv || !pos || !bt || !kc || !vc || !out) return fail(DK_ERR_NULL, "attention_prefill: null pointer argument");
+  if (head_dim != 64 && head_dim != 128)
+    return fail(DK_ERR_SHAPE, "attention_prefill: head_dim must be 64 or 128, got %d", head_dim);
+  if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0)
+    return fail(DK_ERR_SHAPE, "heads-per-group must be 1/2/4/8 (n_q=%d n_kv=%d)", n_q, n_kv);
+  const int hpg = n_q / n_kv;
+  if (hpg != 1 && hpg != 2 && hpg != 4 && hpg != 8)
+    return fail(DK_ERR_SHAPE, "heads-per-group must be 1/2/4/8, got %d", hpg);
+  if (n_kv > 65535) return fail(DK_ERR_SHAPE, "attention_prefill: too many kv heads");
+  if (M < 1 || M > 65535) return fail(DK_ERR_SHAPE, "attention_prefill: M must be 1..65535, got %d", M);
+  if (!pow2(page)) return fail(DK_ERR_DOMAIN, "page size must be a power of two, got %d", page);
+  if (n_pages < 1 || n_bt < 1) return fail(DK_ERR_SHAPE, "attention_prefill: empty cache or block table");
+  const int PS = ((max_ctx + 15) / 16) * 16;
+  if (max_ctx < 1 || !dk::attn_mfma_fits(PS, ilog2(page)))
+    return fail(DK_ERR_DOMAIN, "attention_prefill: max_ctx must be 1..%d at page %d, got %d",
+                ((dk::kAttnMaxSplitPages - 1) * page) / 16 * 16, page, max_ctx);
+  if (!aligned16(qkv) || !aligned16(kc) || !aligned16(vc))
+    return fail(DK_ERR_ALIGN, "qkv, kc and vc must be 16B aligned");
+  clear_error();
+  dk::launch_attention_prefill(qkv, pos, bt, n_bt, kc, vc, n_pages, ilog2(page), n_q, n_kv, head_dim, M, PS, out,
+                               (hipStream_t)stream);
+  return launched("attention_prefill");
 }
 
 int dk_argmax_advance(const void* logits, int V, int64_t* tok, int32_t* pos, void* stream) {

@@ -55,6 +55,55 @@ add_rmsnorm_kernel(f16* __restrict__ x, const f16* __restrict__ delta, const f16
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// The residual + RMSNorm of M rows (prefill), one workgroup per row, with add_rmsnorm's rounding points:
+// xn = fp16(x_in[src] + delta[r]) (delta optional; src = rows[r] when a gather index is given, e.g. embedding rows of
+// the prompt's tokens, else r), x_out[r] = xn, out[r] = w * fp16(float(xn) * r_r), r_r = 1 / sqrt(sum(xn^2) / H + eps).
+// x_out may be x_in itself when there is no gather (a row is read and written by its own workgroup only).
+__global__ void __launch_bounds__(1024)
+rmsnorm_rows_kernel(const f16* x_in, const int64_t* __restrict__ rows, const f16* __restrict__ delta,
+                    const f16* __restrict__ w, f16* x_out, f16* __restrict__ out, int H, float eps) {
+  __shared__ float wsum[16];
+  const int r = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
+  const f16* src = x_in + (size_t)(rows != nullptr ? rows[r] : r) * H;
+  f16* xo = x_out + (size_t)r * H;
+  float ss = 0.f;
+  for (int i = tid * 8; i < H; i += nt * 8) {
+    u32x4 xv = *reinterpret_cast<const u32x4*>(src + i);
+    if (delta != nullptr) {
+      const u32x4 dv = *reinterpret_cast<const u32x4*>(delta + (size_t)r * H + i);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) xv[k] = as_u32(as_f16x2(xv[k]) + as_f16x2(dv[k]));
+    }
+    *reinterpret_cast<u32x4*>(xo + i) = xv;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const f16x2 h = as_f16x2(xv[k]);
+      const float a = (float)h.x, b = (float)h.y;
+      ss = fmaf(a, a, ss);
+      ss = fmaf(b, b, ss);
+    }
+  }
+  ss = group_sum<kWave>(ss);
+  if ((tid & 63) == 0) wsum[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+  for (int i = 0; i < (nt >> 6); ++i) tot += wsum[i];
+  const float rr = 1.0f / sqrtf(tot / (float)H + eps);
+  for (int i = tid * 8; i < H; i += nt * 8) {
+    const u32x4 xv = *reinterpret_cast<const u32x4*>(xo + i);  // this thread's own write above
+    const u32x4 wv = *reinterpret_cast<const u32x4*>(w + i);
+    u32x4 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const f16x2 h = as_f16x2(xv[k]);
+      const f16x2 hn = {(f16)((float)h.x * rr), (f16)((float)h.y * rr)};
+      o[k] = as_u32(as_f16x2(wv[k]) * hn);
+    }
+    *reinterpret_cast<u32x4*>(out + (size_t)r * H + i) = o;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 // out[i] = fp16(silu(float(gate[i]))) * up[i] in fp16, gate = gu[0:I], up = gu[I:2I]   (reference/ref_ops.py:23-27).
 __global__ void __launch_bounds__(256)
 swiglu_kernel(const f16* __restrict__ gu, f16* __restrict__ out, int I) {
@@ -81,13 +130,16 @@ template <int D>
 __global__ void __launch_bounds__(256)
 rope_append_kernel(f16* __restrict__ qkv, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
                    const int32_t* __restrict__ pos_ptr, const int32_t* __restrict__ bt, f16* __restrict__ kc,
-                   f16* __restrict__ vc, int n_q, int n_kv, int log2P, int max_pos, int n_pages, int n_bt) {
+                   f16* __restrict__ vc, int n_q, int n_kv, int log2P, int max_pos, int n_pages, int n_bt,
+                   int row_stride) {
 #pragma clang fp contract(off)
   constexpr int HALF = D / 2;
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   const int head = idx / HALF, i = idx % HALF;
   if (head >= n_q + 2 * n_kv) return;
-  const int pos = *pos_ptr;
+  // row y of a batch of tokens (prefill) sits at position *pos + y; the decode op has one row
+  const int pos = *pos_ptr + (int)blockIdx.y;
+  qkv += (size_t)blockIdx.y * row_stride;
   if (pos < 0 || pos >= max_pos) return;
   const int lp = pos >> log2P;
   int page = -1;
@@ -210,16 +262,25 @@ void launch_swiglu(const void* gu, void* out, int I, hipStream_t st) {
 
 void launch_rope_append(void* qkv, const float* cos_t, const float* sin_t, const int32_t* pos, const int32_t* bt,
                         void* kc, void* vc, int n_q, int n_kv, int head_dim, int log2P, int max_pos, int n_pages,
-                        int n_bt, hipStream_t st) {
+                        int n_bt, int rows, hipStream_t st) {
   const int pairs = (n_q + 2 * n_kv) * (head_dim / 2);
   const int threads = 256;
-  const dim3 grid((pairs + threads - 1) / threads);
+  const dim3 grid((pairs + threads - 1) / threads, rows);
+  const int stride = (n_q + 2 * n_kv) * head_dim;
   if (head_dim == 64)
     hipLaunchKernelGGL((rope_append_kernel<64>), grid, dim3(threads), 0, st, (f16*)qkv, cos_t, sin_t, pos, bt,
-                       (f16*)kc, (f16*)vc, n_q, n_kv, log2P, max_pos, n_pages, n_bt);
+                       (f16*)kc, (f16*)vc, n_q, n_kv, log2P, max_pos, n_pages, n_bt, stride);
   else
     hipLaunchKernelGGL((rope_append_kernel<128>), grid, dim3(threads), 0, st, (f16*)qkv, cos_t, sin_t, pos, bt,
-                       (f16*)kc, (f16*)vc, n_q, n_kv, log2P, max_pos, n_pages, n_bt);
+                       (f16*)kc, (f16*)vc, n_q, n_kv, log2P, max_pos, n_pages, n_bt, stride);
+}
+
+void launch_rmsnorm_rows(const void* x_in, const int64_t* rows, const void* delta, const void* w, void* x_out,
+                         void* out, int M, int H, float eps, hipStream_t st) {
+  int threads = ((H / 8 + 63) / 64) * 64;
+  if (threads > 1024) threads = 1024;
+  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(M), dim3(threads), 0, st, (const f16*)x_in, rows, (const f16*)delta,
+                     (const f16*)w, (f16*)x_out, (f16*)out, H, eps);
 }
 
 void launch_argmax_advance(const void* logits, int V, int64_t* tok, int32_t* pos, hipStream_t st) {

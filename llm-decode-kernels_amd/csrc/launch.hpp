@@ -36,6 +36,11 @@ constexpr int kGemvF16MaxLoads = 16;
 void launch_gemv_f16(int prologue, int R, int waves, int pf, const void* w, const GemvInput& in, void* y, int N,
                      int K, hipStream_t st);
 
+// W4A16 GEMM (prefill): Y[M, N] = X[M, K] . dequant(W)^T; epilogue 1 = SwiGLU of interleaved gate/up column pairs
+// (Y [M, N/2]). K % 32 == 0, group >= 32.
+void launch_gemm_w4a16(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int log2G,
+                       int epilogue, hipStream_t st);
+
 void launch_bw_read(const void* buf, size_t bytes, void* sink, int blocks, int threads, int unroll, hipStream_t st);
 
 // Paged attention arguments. q: the query heads [n_q * D] (reference op) or the fused qkv vector (decode op).
@@ -69,11 +74,20 @@ void launch_paged_attention(const AttnLaunch& a, hipStream_t st);
 // counters are given and max_splits <= 64, else the combine kernel).
 void launch_attention_decode(const AttnLaunch& a, hipStream_t st);
 
+// Causal attention of M prompt rows (prefill): row m at position *pos + m attends tokens [0, *pos + m] of the cache
+// with one split of PS tokens (the MFMA kernel); q is the first n_q heads of qkv row m, already rotated.
+void launch_attention_prefill(const void* qkv, const int32_t* pos, const int32_t* bt, int n_bt, const void* kc,
+                              const void* vc, int n_pages, int log2P, int n_q, int n_kv, int head_dim, int M, int PS,
+                              void* out, hipStream_t st);
+
 void launch_add_rmsnorm(void* x, const void* delta, const void* w, void* out, int H, float eps, hipStream_t st);
 void launch_swiglu(const void* gu, void* out, int I, hipStream_t st);
+// rows > 1: a batch of tokens, row y of qkv [rows, (n_q + 2 n_kv) head_dim] at position *pos + y (prefill)
 void launch_rope_append(void* qkv, const float* cos_t, const float* sin_t, const int32_t* pos, const int32_t* bt,
                         void* kc, void* vc, int n_q, int n_kv, int head_dim, int log2P, int max_pos, int n_pages,
-                        int n_bt, hipStream_t st);
+                        int n_bt, int rows, hipStream_t st);
+void launch_rmsnorm_rows(const void* x_in, const int64_t* rows, const void* delta, const void* w, void* x_out,
+                         void* out, int M, int H, float eps, hipStream_t st);
 
 void launch_argmax_advance(const void* logits, int V, int64_t* tok, int32_t* pos, hipStream_t st);
 

@@ -28,6 +28,10 @@ SIGNATURES = {
     "dk_gemv_w4a16_gate_up": ([_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _I, _I, _P], _I),
     "dk_gemv_f16": ([_I, _I, _I, _P, _P, _P, _I, _I, _P], _I),
     "dk_gemv_f16_rmsnorm": ([_I, _I, _I, _P, _P, _P, _P, _F, _P, _P, _I, _I, _P], _I),
+    "dk_gemm_w4a16": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _P], _I),
+    "dk_rope_append_rows": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
+    "dk_rmsnorm_rows": ([_P, _P, _P, _P, _P, _P, _I, _I, _F, _P], _I),
+    "dk_attention_prefill": ([_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P], _I),
     "dk_bw_read": ([_P, _Z, _P, _I, _I, _I, _P], _I),
     "dk_paged_attention": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
     "dk_attention_decode": ([_P, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P,
@@ -204,6 +208,62 @@ class DecodeKernels:
         ptr = lambda t: None if t is None else t.data_ptr()
         self._call(self.lib.dk_gemv_f16_rmsnorm, int(R), int(warps), int(pf), w.data_ptr(), x.data_ptr(), ptr(delta),
                    norm_w.data_ptr(), float(eps), ptr(x_out), y.data_ptr(), N, Kd, _stream(x))
+
+    # prefill projections: Y = X . dequant(W)^T (epilogue 1: SwiGLU of interleaved gate/up pairs)
+    def gemm_w4a16(self, packed, sz, x, y, group, epilogue=0):
+        for t, n in ((packed, "packed"), (sz, "sz"), (x, "x"), (y, "y")):
+            _check_cuda(t, n)
+        N, K = packed.size(0), packed.size(1) * 8
+        if x.dim() != 2 or x.size(1) != K:
+            raise RuntimeError("gemm_w4a16: x must be [M, K]")
+        M = x.size(0)
+        if sz.size(0) != N or sz.size(1) != K // group or y.shape != (M, N // (1 + int(epilogue))):
+            raise RuntimeError("gemm_w4a16: sz must be [N, K/G, 2] and y [M, N] (epilogue 1: [M, N/2])")
+        _check_dtype(packed, torch.int32, "packed")
+        for t, n in ((sz, "sz"), (x, "x"), (y, "y")):
+            _check_dtype(t, torch.float16, n)
+        self._call(self.lib.dk_gemm_w4a16, packed.data_ptr(), sz.data_ptr(), x.data_ptr(), y.data_ptr(), M, N, K,
+                   int(group), int(epilogue), _stream(x))
+
+    # prefill: rope_append over M token rows (row m at position *pos + m)
+    def rope_append_rows(self, qkv, cos_t, sin_t, pos, bt, kc, vc, n_q, n_kv):
+        for t, n in ((qkv, "qkv"), (cos_t, "cos_t"), (sin_t, "sin_t"), (pos, "pos"), (bt, "bt"), (kc, "kc"),
+                     (vc, "vc")):
+            _check_cuda(t, n)
+        D = kc.size(3)
+        if qkv.dim() != 2 or qkv.size(1) != (n_q + 2 * n_kv) * D:
+            raise RuntimeError("rope_append_rows: qkv must be [M, (n_q + 2 n_kv) * D]")
+        self._call(self.lib.dk_rope_append_rows, qkv.data_ptr(), cos_t.data_ptr(), sin_t.data_ptr(), pos.data_ptr(),
+                   bt.data_ptr(), kc.data_ptr(), vc.data_ptr(), qkv.size(0), int(n_q), int(n_kv), D, kc.size(2),
+                   cos_t.size(0), kc.size(0), bt.numel(), _stream(qkv))
+
+    # prefill: residual + RMSNorm of M rows (rows: optional int64 gather index into x_in)
+    def rmsnorm_rows(self, x_in, rows, delta, w, x_out, out, eps):
+        for t, n in ((x_in, "x_in"), (w, "w"), (x_out, "x_out"), (out, "out")):
+            _check_cuda(t, n)
+            _check_dtype(t, torch.float16, n)
+        M, H = out.shape
+        if x_out.shape != (M, H) or w.numel() != H or x_in.size(-1) != H or (delta is not None and delta.shape != (M, H)):
+            raise RuntimeError("rmsnorm_rows: x_out, out, delta [M, H], w [H], x_in [*, H]")
+        if rows is not None and (rows.dtype != torch.int64 or rows.numel() != M):
+            raise RuntimeError("rmsnorm_rows: rows must be int64 [M]")
+        if rows is None and x_in.shape != (M, H):
+            raise RuntimeError("rmsnorm_rows: without rows x_in must be [M, H]")
+        ptr = lambda t: None if t is None else t.data_ptr()
+        self._call(self.lib.dk_rmsnorm_rows, x_in.data_ptr(), ptr(rows), ptr(delta), w.data_ptr(), x_out.data_ptr(),
+                   out.data_ptr(), M, H, float(eps), _stream(out))
+
+    # prefill: causal attention of M rows over the paged cache
+    def attention_prefill(self, qkv, pos, bt, kc, vc, n_q, n_kv, max_ctx, out):
+        for t, n in ((qkv, "qkv"), (pos, "pos"), (bt, "bt"), (kc, "kc"), (vc, "vc"), (out, "out")):
+            _check_cuda(t, n)
+        D = kc.size(3)
+        M = qkv.size(0)
+        if qkv.dim() != 2 or qkv.size(1) != (n_q + 2 * n_kv) * D or out.shape != (M, n_q * D):
+            raise RuntimeError("attention_prefill: qkv [M, (n_q + 2 n_kv) * D] and out [M, n_q * D]")
+        self._call(self.lib.dk_attention_prefill, qkv.data_ptr(), pos.data_ptr(), bt.data_ptr(), bt.numel(),
+                   kc.data_ptr(), vc.data_ptr(), kc.size(0), kc.size(2), int(n_q), int(n_kv), D, M, int(max_ctx),
+                   out.data_ptr(), _stream(qkv))
 
     # kernels/bindings.cpp:40-43
     def bw_read(self, buf, sink, blocks, threads, unroll):

@@ -463,10 +463,92 @@ class Model:
                 out[i].copy_(self.logits)
         return out
 
-    def generate(self, prompt, n_new, use_graph=True):
-        """Greedy: teacher-force the prompt, then free-run n_new tokens (runtime/model.py:278-286)."""
+    def _prefill_buffers(self, M):
+        if getattr(self, "_pf_rows", 0) < M:
+            h16 = dict(dtype=torch.half, device=self.cfg.device)
+            self._pf_rows = M
+            self._pf = {"x": torch.empty(M, self.H, **h16), "xn": torch.empty(M, self.H, **h16),
+                        "qkv": torch.empty(M, (self.n_q + 2 * self.n_kv) * self.D, **h16),
+                        "attn": torch.empty(M, self.n_q * self.D, **h16), "o": torch.empty(M, self.H, **h16),
+                        "act": torch.empty(M, self.I, **h16), "down": torch.empty(M, self.H, **h16),
+                        "tok": torch.empty(M, dtype=torch.long, device=self.cfg.device)}
+        return {k: v[:M] for k, v in self._pf.items()}
+
+    def gemm(self, lin: Linear, x, y, epilogue=0):
+        """Y [M, N] = X [M, K] . W^T for M prompt rows: the W4A16 GEMM for packed weights, rocBLAS / hipBLASLt for
+        fp16 ones (the reference's cuBLAS call for an fp16 projection)."""
+        if lin.quant:
+            if epilogue == 1:
+                packed, sz = self._gate_up_pairs(lin)
+                self.K.gemm_w4a16(packed, sz, x, y, self.cfg.group, epilogue=1)
+            else:
+                self.K.gemm_w4a16(lin.packed, lin.sz, x, y, self.cfg.group)
+        else:
+            torch.mm(x, lin.w.t(), out=y)
+
+    def _gate_up_pairs(self, lin):
+        """Interleaved (gate_i, up_i) rows for the GEMM's SwiGLU epilogue: the Linear's own storage when the decode
+        step already uses that layout, else a permuted copy made once."""
+        if lin.pairs_interleaved:
+            return lin.packed, lin.sz
+        if not hasattr(lin, "_il"):
+            lin._il = (interleave_halves(lin.packed), interleave_halves(lin.sz))
+        return lin._il
+
+    def prefill(self, tokens):
+        """Process a prompt in one pass: every projection of the M tokens is one W4A16 GEMM, rope/append and the
+        residual + RMSNorm run over all rows, attention is causal over the paged cache (row m at position pos + m).
+        Leaves the state teacher_force(tokens) leaves -- the cache rows of positions pos .. pos + M - 1 written,
+        logits of the last token, tok = their argmax, pos += M -- up to the summation order of the GEMM (the
+        reference teacher-forces prompts through its decode step, runtime/model.py:278-286; this is the batched form
+        of the same composition, runtime/model.py:216-233 per row)."""
+        toks = torch.as_tensor(tokens).long().flatten()
+        M = toks.numel()
+        if M == 0:
+            return
+        if int(toks.min()) < 0 or int(toks.max()) >= self.V:
+            raise ValueError(f"prefill: token ids must lie in [0, {self.V})")
+        start = self.host_pos
+        if start + M > self.cfg.max_ctx:
+            raise RuntimeError(f"prefill: context {start + M} exceeds max_ctx {self.cfg.max_ctx}")
+        B = self._prefill_buffers(M)
+        B["tok"].copy_(toks)
+        x, xn, delta = B["x"], B["xn"], None
+        eps = self.eps
+        for li, lw in enumerate(self.layers):
+            if li == 0:
+                self.K.rmsnorm_rows(self.emb, B["tok"], None, lw["ln1"], x, xn, eps)
+            else:
+                self.K.rmsnorm_rows(x, None, delta, lw["ln1"], x, xn, eps)
+            self.gemm(lw["qkv"], xn, B["qkv"])
+            kc, vc = self.kv[li, 0], self.kv[li, 1]
+            self.K.rope_append_rows(B["qkv"], self.cos, self.sin, self.pos, self.bt, kc, vc, self.n_q, self.n_kv)
+            self.K.attention_prefill(B["qkv"], self.pos, self.bt, kc, vc, self.n_q, self.n_kv, start + M, B["attn"])
+            self.gemm(lw["o"], B["attn"], B["o"])
+            self.K.rmsnorm_rows(x, None, B["o"], lw["ln2"], x, xn, eps)
+            if lw["gu"].quant:
+                self.gemm(lw["gu"], xn, B["act"], epilogue=1)
+            else:
+                gu = torch.mm(xn, lw["gu"].w.t())
+                B["act"].copy_(torch.nn.functional.silu(gu[:, : self.I].float()).half() * gu[:, self.I:])
+            self.gemm(lw["down"], B["act"], B["down"])
+            delta = B["down"]
+        last = slice(M - 1, M)
+        self.K.rmsnorm_rows(x[last], None, delta[last], self.norm_f, x[last], xn[last], eps)
+        self.linear(self.lm_head, xn[M - 1], self.logits)
+        if M > 1:
+            self.pos.add_(M - 1)
+        self.K.argmax_advance(self.logits, self.tok, self.pos)
+        self.host_pos = start + M
+
+    def generate(self, prompt, n_new, use_graph=True, prefill=False):
+        """Greedy: teacher-force the prompt (or prefill it in one pass), then free-run n_new tokens
+        (runtime/model.py:278-286)."""
         self.reset(0)
-        self.teacher_force(prompt, use_graph)
+        if prefill:
+            self.prefill(prompt)
+        else:
+            self.teacher_force(prompt, use_graph)
         new = [int(self.tok)]
         for _ in range(n_new - 1):
             self.run_step(use_graph)

@@ -201,6 +201,28 @@ def test_small_op_validation(lib):
     assert _err(lib, lib.dk_bw_read(A16 + 1, 1024, A16, 4, 256, 1, None))[0] == 2
 
 
+def test_prefill_validation(lib):
+    g = lambda **kw: _err(lib, lib.dk_gemm_w4a16(*dict(dict(p=A16, sz=A16, x=A16, y=B16, M=64, N=128, K=256, G=128,
+                                                            epi=0), **kw).values(), None))
+    assert g(K=240)[0] == 3 and g(K=288, G=96)[0] == 4 and g(G=16)[0] == 4 and g(epi=2)[0] == 4
+    assert g(epi=1, N=127)[0] != 0 and g(y=A16)[0] == 4 and g(x=None)[0] == 1 and g(M=0)[0] == 3
+    rr = lambda **kw: _err(lib, lib.dk_rope_append_rows(*dict(
+        dict(qkv=A16, c=A16, s=A16, pos=A16, bt=A16, kc=A16, vc=A16, M=8, n_q=32, n_kv=4, D=64, page=16, max_pos=100,
+             n_pages=8, n_bt=8), **kw).values(), None))
+    assert rr(M=0)[0] == 3 and rr(M=70000)[0] == 3 and rr(D=96)[0] == 3 and rr(page=12)[0] == 4
+    assert rr(vc=None)[0] == 1 and rr(n_bt=0)[0] == 3
+    nr = lambda **kw: _err(lib, lib.dk_rmsnorm_rows(*dict(dict(x=A16, rows=None, d=None, w=A16, xo=A16, out=B16, M=4,
+                                                               H=2048, eps=1e-5), **kw).values(), None))
+    assert nr(H=2044)[0] == 3 and nr(M=0)[0] == 3 and nr(out=A16)[0] == 4 and nr(d=A16 + 2)[0] == 2
+    assert nr(rows=A16 + 4)[0] == 2 and nr(rows=A16)[0] == 4 and nr(w=None)[0] == 1
+    ap = lambda **kw: _err(lib, lib.dk_attention_prefill(*dict(
+        dict(qkv=A16, pos=A16, bt=A16, n_bt=8, kc=A16, vc=A16, n_pages=8, page=16, n_q=32, n_kv=4, D=64, M=8,
+             max_ctx=128, out=B16), **kw).values(), None))
+    assert ap(n_q=24, n_kv=8)[0] == 3 and ap(n_q=64, n_kv=4)[0] == 3 and ap(D=80)[0] == 3 and ap(M=0)[0] == 3
+    assert ap(page=24)[0] == 4 and ap(max_ctx=0)[0] == 4 and ap(max_ctx=16369)[0] == 4 and ap(qkv=A16 + 2)[0] == 2
+    assert "max_ctx must be 1..16368" in ap(max_ctx=20000)[1] and ap(out=None)[0] == 1
+
+
 def test_error_message_is_cleared_per_thread(lib):
     lib.dk_swiglu(A16, A16, 3, None)
     assert "multiple of 8" in lib.dk_last_error().decode()

@@ -1,0 +1,271 @@
+"""GPU parity of the prefill path (the scope's prefill row; the reference has no prefill kernel and teacher-forces
+prompts through its decode step): the W4A16 GEMM against the oracle's fp32 product with the dequantized weight (the
+reference's GEMV tolerance), one-hot rows bit-exact (each product is an exact fp16 x fp16 product, every other term
+an exact zero), the SwiGLU epilogue bit-exact against the plain GEMM followed by the swiglu kernel."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import DEV, assert_close, dequant_from_gpu, gen, make_cache
+from oracle import ref_ops as R
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def K():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from runtime import ext
+    return ext.load()
+
+
+def _weights(K, N, Kd, G, seed):
+    w = (torch.randn(N, Kd, generator=gen(seed)) * 0.02).half()
+    packed = torch.empty(N, Kd // 8, dtype=torch.int32, device=DEV)
+    sz = torch.empty(N, Kd // G, 2, dtype=torch.half, device=DEV)
+    K.quantize_w4(w.to(DEV), packed, sz, G)
+    return packed, sz
+
+
+@pytest.mark.parametrize("M,N,Kd,G", [(1, 64, 256, 128), (7, 2560, 2048, 128), (64, 2048, 2048, 64),
+                                      (100, 1000, 5632, 128), (512, 11264, 2048, 128), (33, 4096, 4096, 32)])
+def test_gemm_matches_oracle(K, M, N, Kd, G):
+    packed, sz = _weights(K, N, Kd, G, seed=M + N)
+    wref = dequant_from_gpu(packed, sz, G)
+    x = torch.randn(M, Kd, generator=gen(M * 3 + Kd)).half()
+    ref = (x.float() @ wref.float().t())
+    y = torch.full((M, N), 7.0, dtype=torch.half, device=DEV)
+    K.gemm_w4a16(packed, sz, x.to(DEV), y, G)
+    assert_close(y, ref, 5e-3, f"gemm {M}x{N}x{Kd} G{G}")
+
+
+def test_gemm_one_hot_rows_exact(K):
+    N, Kd, G = 200, 512, 64
+    packed, sz = _weights(K, N, Kd, G, seed=9)
+    wref = dequant_from_gpu(packed, sz, G)
+    ks = [0, 1, 7, 8, 31, 32, 127, 128, 300, 511]
+    x = torch.zeros(len(ks), Kd, dtype=torch.half)
+    for i, k in enumerate(ks):
+        x[i, k] = 1.0
+    y = torch.empty(len(ks), N, dtype=torch.half, device=DEV)
+    K.gemm_w4a16(packed, sz, x.to(DEV), y, G)
+    assert torch.equal(y.cpu(), wref[:, ks].t().contiguous())
+
+
+@pytest.mark.parametrize("M,I,Kd", [(16, 5632, 2048), (130, 512, 256), (1, 64, 1024)])
+def test_gemm_swiglu_epilogue(K, M, I, Kd):
+    from runtime.model import interleave_halves
+    G = 128
+    packed, sz = _weights(K, 2 * I, Kd, G, seed=I + M)
+    x = torch.randn(M, Kd, generator=gen(I)).half().to(DEV)
+    gu = torch.empty(M, 2 * I, dtype=torch.half, device=DEV)
+    K.gemm_w4a16(packed, sz, x, gu, G)
+    sep = torch.empty(M, I, dtype=torch.half, device=DEV)
+    for m in range(M):
+        K.swiglu(gu[m], sep[m])
+    act = torch.empty(M, I, dtype=torch.half, device=DEV)
+    K.gemm_w4a16(interleave_halves(packed), interleave_halves(sz), x, act, G, epilogue=1)
+    assert torch.equal(act, sep)
+    ref = R.swiglu_ref((x.cpu().float() @ dequant_from_gpu(packed, sz, G).float().t()).half())
+    assert_close(act, ref, 5e-3, "gemm swiglu vs oracle")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# batched elementwise kernels: bit-exact against their one-token forms, which the decode tests pin to the oracle
+
+def _pos(p):
+    return torch.tensor([p], dtype=torch.int32, device=DEV)
+
+
+@pytest.mark.parametrize("D,n_q,n_kv,page,start,M,max_pos", [(64, 32, 4, 16, 0, 37, 200), (128, 32, 8, 16, 5, 64, 80),
+                                                            (64, 8, 8, 32, 100, 1, 200), (64, 16, 4, 16, 60, 20, 75)])
+def test_rope_append_rows_matches_per_token(K, D, n_q, n_kv, page, start, M, max_pos):
+    """Row m is token start + m; rows at positions >= max_pos (the last case) touch nothing, as the one-token op."""
+    cos, sin = (t.to(DEV) for t in R.rope_tables(max_pos, D))
+    n_pages = (start + M + page - 1) // page + 2
+    bt = torch.randperm(n_pages, generator=gen(D + M)).int().to(DEV)
+    qkv = torch.randn(M, (n_q + 2 * n_kv) * D, generator=gen(M + start)).half()
+    shape = (n_pages, n_kv, page, D)
+    kc1, vc1, kc2, vc2 = (torch.full(shape, -3.0, dtype=torch.half, device=DEV) for _ in range(4))
+    a = qkv.clone().to(DEV)
+    K.rope_append_rows(a, cos, sin, _pos(start), bt, kc1, vc1, n_q, n_kv)
+    rows = []
+    for m in range(M):
+        r = qkv[m].clone().to(DEV)
+        K.rope_append(r, cos, sin, _pos(start + m), bt, kc2, vc2, n_q, n_kv)
+        rows.append(r)
+    assert torch.equal(a, torch.stack(rows))
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    kr, vr = kc2.cpu().clone().fill_(-3.0), vc2.cpu().clone().fill_(-3.0)
+    for m in range(min(M, max_pos - start)):
+        q = R.rope_append_ref(qkv[m], cos.cpu(), sin.cpu(), start + m, kr, vr, bt.cpu(), n_q, n_kv, D, page)
+        assert torch.equal(a[m, : n_q * D].cpu().view(n_q, D), q)
+    assert torch.equal(kc1.cpu(), kr) and torch.equal(vc1.cpu(), vr)
+
+
+@pytest.mark.parametrize("M,H,gather,with_delta,inplace", [(9, 2048, True, False, False), (33, 4096, False, True, True),
+                                                          (1, 256, False, True, False), (130, 2048, True, True, False)])
+def test_rmsnorm_rows_matches_per_row(K, M, H, gather, with_delta, inplace):
+    g = gen(M + H)
+    src = torch.randn(M + 50 if gather else M, H, generator=g).half().to(DEV)
+    rows = torch.randint(0, src.size(0), (M,), generator=g).to(DEV) if gather else None
+    delta = torch.randn(M, H, generator=g).half().to(DEV) if with_delta else None
+    w = (1 + 0.1 * torch.randn(H, generator=g)).half().to(DEV)
+    x_in = src.clone()
+    x_out = x_in if inplace else torch.empty(M, H, dtype=torch.half, device=DEV)
+    out = torch.empty(M, H, dtype=torch.half, device=DEV)
+    K.rmsnorm_rows(x_in, rows, delta, w, x_out, out, 1e-5)
+    for m in range(M):
+        x = src[int(rows[m]) if gather else m].clone()
+        o = torch.empty(H, dtype=torch.half, device=DEV)
+        K.add_rmsnorm(x, None if delta is None else delta[m], w, o, 1e-5)
+        assert torch.equal(x_out[m], x) and torch.equal(out[m], o), m
+        xr, orf = R.add_rmsnorm_ref(src[int(rows[m]) if gather else m].cpu(), None if delta is None else delta[m].cpu(),
+                                    w.cpu(), 1e-5)
+        assert torch.equal(x.cpu(), xr)
+        assert_close(o, orf, 2e-3, f"rmsnorm row {m}")
+    if gather:
+        assert torch.equal(x_in, src)                 # the gathered source is read only
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# causal prefill attention
+
+@pytest.mark.parametrize("D,n_q,n_kv,page,start,M", [(64, 32, 4, 16, 0, 40), (64, 32, 4, 16, 300, 17),
+                                                    (128, 32, 8, 16, 0, 64), (128, 8, 8, 32, 1000, 9),
+                                                    (64, 16, 8, 16, 0, 1), (64, 4, 4, 16, 4000, 96)])
+def test_attention_prefill(K, D, n_q, n_kv, page, start, M):
+    """Row m (position start + m) equals the decode MFMA kernel (dk_paged_attention version 4) at that position with
+    the same split size, bit for bit, and the oracle's attention over tokens [0, start + m] within the attention
+    tolerance; cache tokens past a row's position (later rows' keys) are not attended."""
+    ctx_all = start + M
+    kc, vc, bt = make_cache(ctx_all, n_kv, page, D=D, seed=D + M + start)
+    qkv = torch.randn(M, (n_q + 2 * n_kv) * D, generator=gen(start + M)).half()
+    out = torch.empty(M, n_q * D, dtype=torch.half, device=DEV)
+    kd, vd, btd = kc.to(DEV), vc.to(DEV), bt.to(DEV)
+    K.attention_prefill(qkv.to(DEV), _pos(start), btd, kd, vd, n_q, n_kv, ctx_all, out)
+    PS = (ctx_all + 15) // 16 * 16
+    f32 = dict(dtype=torch.float32, device=DEV)
+    for m in range(M):
+        q = qkv[m, : n_q * D].contiguous()
+        dec = torch.empty(n_q, D, dtype=torch.half, device=DEV)
+        K.paged_attention(q.to(DEV), kd, vd, btd, _pos(start + m), PS, torch.empty(n_q, 1, D, **f32),
+                          torch.empty(n_q, 1, **f32), torch.empty(n_q, 1, **f32), dec, 4)
+        assert torch.equal(out[m].view(n_q, D), dec), f"row {m}"
+        if m in (0, M // 2, M - 1):
+            ref = R.paged_attention_ref(q.view(n_q, D), kc, vc, bt, start + m + 1, page)
+            assert_close(out[m].view(n_q, D), ref, 2e-3, f"row {m} vs oracle")
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Model.prefill
+
+def _model(D=64, **cfg):
+    from runtime.model import DecodeConfig, Model
+    from runtime.synth import LlamaShape, SyntheticLlama
+    shape = LlamaShape(256, 2, 4, 2, 512, 1000) if D == 64 else LlamaShape(512, 2, 4, 2, 1024, 1000)
+    m = Model(SyntheticLlama(shape, seed=4, device=DEV, std=0.05), shape, DecodeConfig(max_ctx=256, device=DEV, **cfg))
+    m.prepare(256)
+    return m, shape
+
+
+def _prompt(n, seed=1):
+    return torch.randint(0, 1000, (n,), generator=gen(seed))
+
+
+def _rel(a, b):
+    a, b = a.float().cpu(), b.float().cpu()
+    return ((a - b).abs().max() / b.abs().max()).item()
+
+
+@pytest.mark.parametrize("D", (64, 128))
+def test_prefill_matches_oracle_and_teacher_force(K, D):
+    from __graft_entry__ import _ref_weights
+    from oracle.decode_ref import RefDecoder
+    m, shape = _model(D)
+    prompt = _prompt(45)
+    ref = RefDecoder(_ref_weights(m, shape), shape, max_ctx=256, page=16, block_table=m.bt.cpu())
+    for p, t in enumerate(prompt.tolist()):
+        lr, tr = ref.step(t, p)
+    m.reset(0)
+    m.prefill(prompt)
+    torch.cuda.synchronize()
+    assert int(m.pos) == 45 and m.host_pos == 45
+    assert _rel(m.logits, lr) <= 2e-2, _rel(m.logits, lr)
+    pre_logits, pre_tok, pre_kv = m.logits.clone(), int(m.tok), m.kv.clone()
+    m.kv.zero_()
+    m.reset(0)
+    tf = m.teacher_force(prompt, collect_logits=True)
+    assert _rel(pre_logits, tf[-1]) <= 2e-2
+    lf = tf[-1].float()
+    assert pre_tok == int(m.tok) or lf.max() - lf[pre_tok] <= 2e-2 * lf.abs().max()
+    assert _rel(pre_kv, m.kv) <= 2e-2
+    # decoding on from the prefilled state follows the oracle
+    m.kv.copy_(pre_kv)
+    m.tok.fill_(tr)
+    m.reset(45)
+    for p, t in enumerate((tr, 17, 3), start=45):
+        m.tok.fill_(t)
+        m.run_step()
+        lr, _ = ref.step(t, p)
+        assert _rel(m.logits, lr) <= 2e-2, (p, _rel(m.logits, lr))
+
+
+def test_prefill_in_chunks_is_bit_exact(K):
+    """Each GEMM row and each attention row is computed independently of the batch it is in: a prompt prefilled in
+    three chunks leaves the same cache and logits as one pass."""
+    m, _ = _model()
+    prompt = _prompt(70, seed=2)
+    m.reset(0)
+    m.prefill(prompt)
+    one = (m.kv.clone(), m.logits.clone(), int(m.tok), int(m.pos))
+    m.kv.fill_(0.5)
+    m.reset(0)
+    for a, b in ((0, 31), (31, 32), (32, 70)):
+        m.prefill(prompt[a:b])
+    n = 70 * 1
+    used = torch.zeros_like(m.kv, dtype=torch.bool)
+    for t in range(n):
+        used[:, :, int(m.bt[t // 16]), :, t % 16, :] = True
+    assert torch.equal(m.kv[used], one[0][used])
+    assert torch.equal(m.logits, one[1]) and int(m.tok) == one[2] and int(m.pos) == one[3] == 70
+
+
+def test_prefill_gate_up_layouts_agree(K):
+    """swiglu='kernel' keeps the [gate; up] rows for decode; prefill then uses an interleaved copy, so both
+    configurations run the same GEMM and agree bit for bit."""
+    prompt = _prompt(23, seed=3)
+    outs = []
+    for sw in ("epilogue", "kernel"):
+        m, _ = _model(swiglu=sw)
+        m.reset(0)
+        m.prefill(prompt)
+        outs.append((m.logits.clone(), m.kv.clone()))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
+def test_prefill_fp16_weights(K):
+    from __graft_entry__ import _ref_weights
+    from oracle.decode_ref import RefDecoder
+    m, shape = _model(weights="fp16")
+    prompt = _prompt(12, seed=5)
+    ref = RefDecoder(_ref_weights(m, shape), shape, max_ctx=256, page=16, block_table=m.bt.cpu())
+    for p, t in enumerate(prompt.tolist()):
+        lr, _ = ref.step(t, p)
+    m.reset(0)
+    m.prefill(prompt)
+    assert _rel(m.logits, lr) <= 2e-2
+
+
+def test_prefill_rejects_bad_prompts(K):
+    m, _ = _model()
+    m.reset(0)
+    with pytest.raises(ValueError, match="token ids"):
+        m.prefill(torch.tensor([3, 1000]))
+    m.reset(250)
+    with pytest.raises(RuntimeError, match="exceeds max_ctx"):
+        m.prefill(_prompt(7))
+    m.reset(0)
+    m.prefill([])
+    assert m.host_pos == 0
