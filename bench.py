@@ -162,9 +162,41 @@ def decode_8b_leg(ctx=4096, steps=64, warmup=8):
                                "build_s": round(built, 1)}
         log(f"llama3-8b ctx {ctx} {head} head: {d['tok_s']:.1f} tok/s, median {d['median_us']:.1f} us "
             f"({d['tok_s'] / roof:.1%} of the {roof:.0f} tok/s roofline)")
+        if head == "int4":
+            out["prefill_512"] = prefill_leg(m, reps=3)
+            log(f"llama3-8b prefill 512: {out['prefill_512']['ms']:.2f} ms ({out['prefill_512']['tflops']:.0f} TFLOP/s)")
         del m
         torch.cuda.empty_cache()
     return out
+
+
+def prefill_leg(model, M=512, reps=5):
+    """Prompt processing: model.prefill of an M-token prompt from position 0 (W4A16 GEMMs, batched rope/append and
+    norms, causal prefill attention), against teacher-forcing the same prompt through the decode step's hipGraph.
+    The compute roofline is 2 x (projection weights) x M FLOPs plus the attention's 4 x n_q x D x (sum of contexts)
+    at MI355X's dense fp16 MFMA peak."""
+    import torch
+    prompt = torch.randint(0, model.V, (M,), generator=torch.Generator().manual_seed(7))
+    times = []
+    for _ in range(reps + 1):
+        model.reset(0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        model.prefill(prompt)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    pf = statistics.median(times[1:])
+    model.reset(0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    model.teacher_force(prompt)
+    torch.cuda.synchronize()
+    tf = time.perf_counter() - t0
+    params = sum(l[k].N * l[k].K for l in model.layers for k in ("qkv", "o", "gu", "down"))
+    flops = 2 * params * M + model.L * 4 * model.n_q * model.D * (M * (M + 1) // 2)
+    return {"prompt_tokens": M, "ms": round(pf * 1e3, 3), "tok_s": round(M / pf, 1),
+            "tflops": round(flops / pf / 1e12, 1), "frac_of_fp16_mfma_peak": round(flops / pf / 2.5e15, 4),
+            "teacher_force_ms": round(tf * 1e3, 2), "speedup_vs_teacher_force": round(tf / pf, 1)}
 
 
 def cpu_baseline_leg(model, shape, ctx, budget_s=15.0, max_tokens=64):
@@ -195,9 +227,9 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--ctx", type=int, default=512)
-    ap.add_argument("--leg", choices=("all", "gemv", "decode", "decode8b"), default="all",
+    ap.add_argument("--leg", choices=("all", "gemv", "decode", "decode8b", "prefill"), default="all",
                     help="gemv: the 4096x14336 GEMV and its calibration copies only; decode: the TinyLlama decode "
-                         "step only; decode8b: the Llama-3-8B decode legs only")
+                         "step only; decode8b: the Llama-3-8B decode legs only; prefill: the TinyLlama prefill leg only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline leg")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -246,12 +278,20 @@ def main():
     if a.leg == "decode":
         print(json.dumps({"leg": "decode", "decode": dec}), flush=True)
         return
+    if a.leg == "prefill":
+        print(json.dumps({"leg": "prefill", "prefill_tinyllama_512": prefill_leg(model)}), flush=True)
+        return
     bpt = model.bytes_per_token(a.ctx + a.steps // 2)
     model.prepare(2048 + 64 + 16)
     dec2k = decode_leg(model, 2048, 64, 8)
     log(f"decode ctx 2048: {dec2k['tok_s']:.1f} tok/s")
     bpt2k = model.bytes_per_token(2048 + 32)
 
+
+    model.prepare(2048 + 64 + 16)
+    pre = prefill_leg(model)
+    log(f"prefill {pre['prompt_tokens']} tokens: {pre['ms']:.2f} ms ({pre['tok_s']:.0f} tok/s, {pre['tflops']:.0f} TFLOP/s, "
+        f"{pre['speedup_vs_teacher_force']:.0f}x teacher forcing)")
 
     d8b = decode_8b_leg()
 
@@ -282,6 +322,7 @@ def main():
                    "frac_of_roofline": round(dec["tok_s"] / (HBM_PEAK_GBS * 1e9 / bpt), 4)},
         "decode_ctx2048": {"tok_s": round(dec2k["tok_s"], 2), "median_us": round(dec2k["median_us"], 2),
                            "bytes_per_token": bpt2k, "frac_of_roofline": round(dec2k["tok_s"] / (HBM_PEAK_GBS * 1e9 / bpt2k), 4)},
+        "prefill_tinyllama_512": pre,
         "decode_llama3_8b_ctx4096": d8b,
         "cpu_baseline": cpu,
     }

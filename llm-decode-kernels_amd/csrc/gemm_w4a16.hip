@@ -136,10 +136,193 @@ gemm_w4a16_kernel(const uint32_t* __restrict__ W, const uint32_t* __restrict__ S
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Wide kernel (K % 64 == 0): block tile BN weight rows x BM tokens, K in chunks of 64, four waves as 2 x 2, each
+// wave (BN/2) x (BM/2) in 16 x 16 tiles of v_mfma_f32_16x16x32_f16 (gfx950's double-K form: 8 fp16 per lane and
+// operand). The weight rows are the A operand, the tokens the B operand, so the accumulator of tile (i, j) leaves
+// lane l = 16 g + c with Y^T[rows n 4g..4g+3][token c]: four consecutive outputs of one token row, stored as one
+// 8-byte word, and the gate/up pairs of the SwiGLU epilogue ((4g, 4g+1), (4g+2, 4g+3)) inside one lane.
+//   Operand k order: lane (g, c) takes halves 8g..8g+7 of its 32-wide k step for both A and B; any k order that is the
+//   same for both operands gives the same dot products, so the result does not depend on the instruction's internal
+//   assignment of k to lanes.
+// Staging per chunk: X [BM x 64] by 16-byte loads (BM / 32 per thread); the W tile [BN x 64] is BN x 2 words of
+// 16 bytes (32 weights), one per thread of the first 2 BN threads, dequantized into LDS. Rows are padded to 72 halves
+// (144 B) so the 16 rows of one 16-byte operand read fall in distinct banks. The next chunk's global loads are issued
+// before the current chunk's MFMAs (two LDS buffers, one barrier per chunk).
+// Workgroup -> tile: workgroups are dealt round-robin to the 8 XCDs, so workgroup b runs on XCD b % 8; the tile
+// order is made XCD-major (the b / 8-th tile of XCD b % 8's contiguous range) with the token tiles fastest, so the
+// token tiles that share a weight tile run together on one XCD and each weight tile is fetched from HBM once.
+constexpr int kWK = 64, kWRow = 72, kXcds = 8;
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f4 mfma32(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+
+template <int BN, int BM, int PD, int EPI>
+__global__ void __launch_bounds__(kGemmThreads, 2)
+gemm_w4a16_wide(const uint32_t* __restrict__ W, const uint32_t* __restrict__ SZ, const f16* __restrict__ X,
+                f16* __restrict__ Y, int M, int N, int K, int gsh, int tiles_m, int tiles) {
+  constexpr int TI = BN / 32, TJ = BM / 32;  // 16 x 16 tiles per wave along n and m
+  constexpr int XL = BM * 8 / kGemmThreads;  // 16-byte X loads per thread per chunk
+  static_assert(XL >= 1 && 2 * BN <= kGemmThreads, "tile shape");
+  __shared__ __align__(16) f16 Ws[2][BN][kWRow];
+  __shared__ __align__(16) f16 Xs[2][BM][kWRow];
+  const int per = gridDim.x / kXcds;
+  const int t = (int)(blockIdx.x % kXcds) * per + (int)(blockIdx.x / kXcds);
+  if (t >= tiles) return;  // uniform: the grid is rounded up to a multiple of the XCD count
+  const int m0 = (t % tiles_m) * BM, n0 = (t / tiles_m) * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 15, g = lane >> 4;
+  const int wn = (wave >> 1) * (BN / 2), wm = (wave & 1) * (BM / 2);
+  const int KW = K >> 3, NG = K >> gsh;
+  // staging roles: X rows tid / 8 + 32 i, 16-byte chunk tid % 8; W row tid / 2, 32-weight half tid % 2
+  const int xr = tid >> 3, xc = tid & 7;
+  const f16* xrow[XL];
+#pragma unroll
+  for (int i = 0; i < XL; ++i) xrow[i] = X + (size_t)min(m0 + xr + 32 * i, M - 1) * K + 8 * xc;
+  const bool wload = tid < 2 * BN;  // uniform per wave
+  const int wr = min(tid >> 1, BN - 1), wh = tid & 1;
+  const int wrg = min(n0 + wr, N - 1);
+  const u32x4* wrow = reinterpret_cast<const u32x4*>(W + (size_t)wrg * KW) + wh;
+  const uint32_t* szrow = SZ + (size_t)wrg * NG;
+
+  const int nk = K / kWK;
+  u32x4 xv[PD][XL], wv[PD];
+  uint32_t sv[PD];
+  // loads are unconditional (threads past 2 BN re-read a valid row, tail fetches re-read the last chunk): loads
+  // behind branches make the compiler wait for every outstanding load before a stage, which defeats the ring
+  auto fetch = [&](int kc, int slot) {
+    const int k0 = min(kc, nk - 1) * kWK;
+#pragma unroll
+    for (int i = 0; i < XL; ++i) xv[slot][i] = *reinterpret_cast<const u32x4*>(xrow[i] + k0);
+    wv[slot] = __builtin_nontemporal_load(wrow + (k0 >> 5));
+    sv[slot] = szrow[(k0 + 32 * wh) >> gsh];
+  };
+  auto stage = [&](int buf, int slot) {
+#pragma unroll
+    for (int i = 0; i < XL; ++i) *reinterpret_cast<u32x4*>(&Xs[buf][xr + 32 * i][8 * xc]) = xv[slot][i];
+    if (wload) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        *reinterpret_cast<u32x4*>(&Ws[buf][wr][32 * wh + 8 * w]) = dequant8(wv[slot][w], sv[slot]);
+    }
+  };
+
+  f4 acc[TI][TJ];
+#pragma unroll
+  for (int i = 0; i < TI; ++i) {
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+  }
+  // chunk kc lives in register slot kc % PD from its fetch until it is staged into LDS buffer kc & 1: its loads are
+  // issued PD chunks of MFMA work before they are needed
+#pragma unroll
+  for (int u = 0; u < PD; ++u) fetch(u, u);
+  stage(0, 0);
+  fetch(PD, 0);
+  __syncthreads();
+  for (int kc0 = 0; kc0 < nk; kc0 += PD) {
+#pragma unroll
+    for (int u = 0; u < PD; ++u) {  // chunk kc = kc0 + u; the slot indices stay compile-time constants
+      const int kc = kc0 + u;
+      if (kc >= nk) break;
+      const int buf = kc & 1;
+#pragma unroll
+      for (int ks = 0; ks < kWK / 32; ++ks) {
+        h8 a[TI], b[TJ];
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+          a[i] = __builtin_bit_cast(h8, *reinterpret_cast<const u32x4*>(&Ws[buf][wn + 16 * i + c][32 * ks + 8 * g]));
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+          b[j] = __builtin_bit_cast(h8, *reinterpret_cast<const u32x4*>(&Xs[buf][wm + 16 * j + c][32 * ks + 8 * g]));
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+#pragma unroll
+          for (int j = 0; j < TJ; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+        }
+      }
+      const int nslot = (u + 1) % PD;  // a constant once the loop is unrolled
+      stage(buf ^ 1, nslot);            // chunk kc + 1 (past the end: a copy of the last chunk, never read)
+      fetch(kc + 1 + PD, nslot);
+      __syncthreads();
+    }
+  }
+  // ---- epilogue: lane holds Y[token m0 + wm + 16 j + c][n0 + wn + 16 i + 4 g + v], v = 0..3
+  const bool vec = (N & 3) == 0;
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int m = m0 + wm + 16 * j + c;
+    if (m >= M) continue;
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+      const int n = n0 + wn + 16 * i + 4 * g;
+      const f16 y0 = (f16)acc[i][j][0], y1 = (f16)acc[i][j][1], y2 = (f16)acc[i][j][2], y3 = (f16)acc[i][j][3];
+      if constexpr (EPI == 0) {
+        f16* dst = Y + (size_t)m * N + n;
+        if (vec && n + 3 < N) {
+          u32x2 o;
+          o[0] = as_u32(f16x2{y0, y1});
+          o[1] = as_u32(f16x2{y2, y3});
+          *reinterpret_cast<u32x2*>(dst) = o;
+        } else {
+          const f16 yy[4] = {y0, y1, y2, y3};
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            if (n + v < N) dst[v] = yy[v];
+        }
+      } else {
+        // rows (n, n + 1) and (n + 2, n + 3) are (gate, up) pairs i = n / 2 and n / 2 + 1 of act[M, N / 2]
+        f16* dst = Y + (size_t)m * (N >> 1) + (n >> 1);
+        const f16 a0 = silu_mul(y0, y1), a1 = silu_mul(y2, y3);
+        if (vec && n + 3 < N) {
+          *reinterpret_cast<uint32_t*>(dst) = as_u32(f16x2{a0, a1});
+        } else {
+          if (n + 1 < N) dst[0] = a0;
+          if (n + 3 < N) dst[1] = a1;
+        }
+      }
+    }
+  }
+}
+
+#ifndef DK_GEMM_PD
+#define DK_GEMM_PD 2
+#endif
+template <int BN, int BM, int PD = DK_GEMM_PD>
+void launch_wide(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int log2G,
+                 int epilogue, hipStream_t st) {
+  const int tiles_m = (M + BM - 1) / BM, tiles = tiles_m * ((N + BN - 1) / BN);
+  const dim3 grid((tiles + kXcds - 1) / kXcds * kXcds);
+  if (epilogue == 1)
+    hipLaunchKernelGGL((gemm_w4a16_wide<BN, BM, PD, 1>), grid, dim3(kGemmThreads), 0, st, (const uint32_t*)packed,
+                       (const uint32_t*)sz, (const f16*)x, (f16*)y, M, N, K, log2G, tiles_m, tiles);
+  else
+    hipLaunchKernelGGL((gemm_w4a16_wide<BN, BM, PD, 0>), grid, dim3(kGemmThreads), 0, st, (const uint32_t*)packed,
+                       (const uint32_t*)sz, (const f16*)x, (f16*)y, M, N, K, log2G, tiles_m, tiles);
+}
+
 }  // namespace
+
+// Tile choice: the largest of 128 x 128, 128 x 64, 64 x 64 whose grid still fills the 256 CUs (one workgroup of
+// 256 threads per CU at least); K % 64 != 0 takes the 64 x 64 16x16x16 kernel above.
+int gemm_w4a16_tile(int M, int N, int K) {
+  if (K % kWK != 0) return 0;
+  const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128);
+  const long long t64m = (long long)((M + 63) / 64) * ((N + 127) / 128);
+  if (t128 >= 256) return 3;
+  if (t64m >= 256) return 2;
+  return 1;
+}
 
 void launch_gemm_w4a16(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int log2G,
                        int epilogue, hipStream_t st) {
+  switch (gemm_w4a16_tile(M, N, K)) {
+    case 3: launch_wide<128, 128>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
+    case 2: launch_wide<128, 64>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
+    case 1: launch_wide<64, 64>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
+    default: break;
+  }
   const dim3 grid((N + kBN - 1) / kBN, (M + kBM - 1) / kBM);
   if (epilogue == 1)
     hipLaunchKernelGGL(gemm_w4a16_kernel<1>, grid, dim3(kGemmThreads), 0, st, (const uint32_t*)packed,
