@@ -192,11 +192,47 @@ def prefill_leg(model, M=512, reps=5):
     model.teacher_force(prompt)
     torch.cuda.synchronize()
     tf = time.perf_counter() - t0
+    gemms = {}
+    lw = model.layers[0]
+    for key, epi in (("qkv", 0), ("o", 0), ("gu", 1), ("down", 0)):
+        lin = lw[key]
+        if not lin.quant:
+            continue
+        gemms[f"{key}_{lin.N}x{lin.K}"] = gemm_timing(model, lin, M, epi)
     params = sum(l[k].N * l[k].K for l in model.layers for k in ("qkv", "o", "gu", "down"))
     flops = 2 * params * M + model.L * 4 * model.n_q * model.D * (M * (M + 1) // 2)
     return {"prompt_tokens": M, "ms": round(pf * 1e3, 3), "tok_s": round(M / pf, 1),
             "tflops": round(flops / pf / 1e12, 1), "frac_of_fp16_mfma_peak": round(flops / pf / 2.5e15, 4),
-            "teacher_force_ms": round(tf * 1e3, 2), "speedup_vs_teacher_force": round(tf / pf, 1)}
+            "teacher_force_ms": round(tf * 1e3, 2), "speedup_vs_teacher_force": round(tf / pf, 1), "gemm": gemms}
+
+
+def gemm_timing(model, lin, M, epilogue, reps=20):
+    """One prefill projection on its own: dk_gemm_w4a16 (the model's packed weights, SwiGLU epilogue for gate|up) and,
+    for comparison, hipBLASLt's fp16 GEMM (torch.mm) on fp16 weights of the same shape; HIP events, mean of reps."""
+    import torch
+    dev = model.cfg.device
+    x = torch.randn(M, lin.K, generator=torch.Generator().manual_seed(3)).half().to(dev)
+    y = torch.empty(M, lin.N // (1 + epilogue), dtype=torch.half, device=dev)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) * 1e3 / reps
+
+    us = timed(lambda: model.gemm(lin, x, y, epilogue))
+    w16 = torch.randn(lin.N, lin.K, device=dev).half()
+    yb = torch.empty(M, lin.N, dtype=torch.half, device=dev)
+    ub = timed(lambda: torch.mm(x, w16.t(), out=yb))
+    fl = 2 * M * lin.N * lin.K
+    return {"us": round(us, 2), "tflops": round(fl / us / 1e6, 1), "hipblaslt_fp16_us": round(ub, 2),
+            "hipblaslt_fp16_tflops": round(fl / ub / 1e6, 1)}
 
 
 def cpu_baseline_leg(model, shape, ctx, budget_s=15.0, max_tokens=64):
