@@ -146,66 +146,103 @@ gemm_w4a16_kernel(const uint32_t* __restrict__ W, const uint32_t* __restrict__ S
 //   same for both operands gives the same dot products, so the result does not depend on the instruction's internal
 //   assignment of k to lanes.
 // Staging per chunk: X [BM x 64] by 16-byte loads (BM / 32 per thread); the W tile [BN x 64] is BN x 2 words of
-// 16 bytes (32 weights), one per thread of the first 2 BN threads, dequantized into LDS. Rows are padded to 72 halves
-// (144 B) so the 16 rows of one 16-byte operand read fall in distinct banks. The next chunk's global loads are issued
+// 16 bytes (32 weights), one per thread of the first 2 BN threads, dequantized into LDS. LDS rows are 128 bytes with
+// an XOR swizzle of their 16-byte chunks (lds_chunk), which keeps operand reads and both stage patterns free of bank
+// conflicts (padded 144-byte rows left the stage writes 2-way conflicted: a third of the LDS cycles). The next chunk's global loads are issued
 // before the current chunk's MFMAs (two LDS buffers, one barrier per chunk).
 // Workgroup -> tile: workgroups are dealt round-robin to the 8 XCDs, so workgroup b runs on XCD b % 8; the tile
 // order is made XCD-major (the b / 8-th tile of XCD b % 8's contiguous range) with the token tiles fastest, so the
 // token tiles that share a weight tile run together on one XCD and each weight tile is fetched from HBM once.
-constexpr int kWK = 64, kWRow = 72, kXcds = 8;
+constexpr int kWK = 64, kXcds = 8;
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ f4 mfma32(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
 
-template <int BN, int BM, int PD, int EPI>
-__global__ void __launch_bounds__(kGemmThreads, 2)
-gemm_w4a16_wide(const uint32_t* __restrict__ W, const uint32_t* __restrict__ SZ, const f16* __restrict__ X,
-                f16* __restrict__ Y, int M, int N, int K, int gsh, int tiles_m, int tiles) {
+#ifndef DK_GEMM_SCHED_FENCE
+#define DK_GEMM_SCHED_FENCE 0
+#endif
+
+// LDS chunk position of 16-byte chunk q (0..7) of row r in the wide kernel's unpadded 128-byte rows. The XOR with
+// (r >> 1) & 7 makes every 16-lane group conflict-free on 64 banks: an operand read (16 consecutive rows, one chunk
+// each) lands on 2 row parities x 8 distinct positions, the X stage (2 rows x 8 chunks) on both parities, the W stage
+// (8 rows x 2 halves, one chunk of each half per store) on 8 distinct positions per parity.
+__device__ __forceinline__ int lds_chunk(int r, int q) { return q ^ ((r >> 1) & 7); }
+
+// Phase fence: nothing moves across it, neither in the IR (the empty asm clobbers memory, so loads are not sunk to
+// their first use) nor in the machine scheduler. The register ring depends on loads being issued where written.
+__device__ __forceinline__ void phase_fence() {
+#if DK_GEMM_SCHED_FENCE
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+#else
+  asm volatile("" ::: "memory");
+#endif
+}
+
+template <int BN, int BM, int PD, int KG, int EPI>
+__global__ void __launch_bounds__(kGemmThreads * KG, KG == 1 ? 2 : 1)
+gemm_w4a16_wide(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int M, int N, int K, int gsh,
+                int tiles_m, int tiles) {
+  // (no __restrict__: the phase fences below must order these loads, and a fence's memory clobber does not reach
+  // memory the compiler knows is only accessed through restrict pointers)
   constexpr int TI = BN / 32, TJ = BM / 32;  // 16 x 16 tiles per wave along n and m
   constexpr int XL = BM * 8 / kGemmThreads;  // 16-byte X loads per thread per chunk
-  static_assert(XL >= 1 && 2 * BN <= kGemmThreads, "tile shape");
-  __shared__ __align__(16) f16 Ws[2][BN][kWRow];
-  __shared__ __align__(16) f16 Xs[2][BM][kWRow];
+  constexpr int WPT = BN / 32;               // packed W words per thread per chunk (BN x 8 words over 256 threads)
+  constexpr int TPR = 8 / WPT;               // threads per W row
+  static_assert(XL >= 1 && (WPT == 2 || WPT == 4), "tile shape");
+  static_assert(KG == 1 || 2 * BN * kWK * 2 >= TI * TJ * 4 * kGemmThreads * 4, "K-group reduction space");
+  // rows of 64 halves = 8 chunks of 16 bytes, chunk q of row r stored at q ^ swz(r) (see lds_chunk)
+  __shared__ u32x4 Ws[KG][2][BN][kWK / 8];
+  __shared__ u32x4 Xs[KG][2][BM][kWK / 8];
   const int per = gridDim.x / kXcds;
   const int t = (int)(blockIdx.x % kXcds) * per + (int)(blockIdx.x / kXcds);
   if (t >= tiles) return;  // uniform: the grid is rounded up to a multiple of the XCD count
   const int m0 = (t % tiles_m) * BM, n0 = (t / tiles_m) * BN;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // K groups: KG groups of four waves; group kg takes chunks kg, kg + KG, ... with LDS buffers of its own, and the
+  // groups' accumulators are summed through LDS at the end (more waves per CU and a KG-times shorter chunk chain
+  // for grids that do not fill the CUs)
+  const int kg = KG == 1 ? 0 : (int)threadIdx.x / kGemmThreads;
+  const int tid = (int)threadIdx.x % kGemmThreads, lane = tid & 63, wave = tid >> 6;
   const int c = lane & 15, g = lane >> 4;
   const int wn = (wave >> 1) * (BN / 2), wm = (wave & 1) * (BM / 2);
   const int KW = K >> 3, NG = K >> gsh;
-  // staging roles: X rows tid / 8 + 32 i, 16-byte chunk tid % 8; W row tid / 2, 32-weight half tid % 2
+  // staging roles: X rows tid / 8 + 32 i, 16-byte chunk tid % 8; W row tid / TPR, words WPT (tid % TPR) .. + WPT - 1
+  // of the chunk (8 WPT weights, inside one group since G >= 32), every thread loading (no branch in the step)
   const int xr = tid >> 3, xc = tid & 7;
   const f16* xrow[XL];
 #pragma unroll
   for (int i = 0; i < XL; ++i) xrow[i] = X + (size_t)min(m0 + xr + 32 * i, M - 1) * K + 8 * xc;
-  const bool wload = tid < 2 * BN;  // uniform per wave
-  const int wr = min(tid >> 1, BN - 1), wh = tid & 1;
+  const int wr = tid / TPR, wq = tid % TPR;
   const int wrg = min(n0 + wr, N - 1);
-  const u32x4* wrow = reinterpret_cast<const u32x4*>(W + (size_t)wrg * KW) + wh;
+  const uint32_t* wrow = W + (size_t)wrg * KW + WPT * wq;
   const uint32_t* szrow = SZ + (size_t)wrg * NG;
 
   const int nk = K / kWK;
-  u32x4 xv[PD][XL], wv[PD];
-  uint32_t sv[PD];
+  u32x4 xv[PD][XL];
+  uint32_t wv[PD][WPT], sv[PD];
   // loads are unconditional (threads past 2 BN re-read a valid row, tail fetches re-read the last chunk): loads
   // behind branches make the compiler wait for every outstanding load before a stage, which defeats the ring
   auto fetch = [&](int kc, int slot) {
     const int k0 = min(kc, nk - 1) * kWK;
 #pragma unroll
     for (int i = 0; i < XL; ++i) xv[slot][i] = *reinterpret_cast<const u32x4*>(xrow[i] + k0);
-    wv[slot] = __builtin_nontemporal_load(wrow + (k0 >> 5));
-    sv[slot] = szrow[(k0 + 32 * wh) >> gsh];
+    if constexpr (WPT == 4) {
+      const u32x4 w4 = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + (k0 >> 3)));
+#pragma unroll
+      for (int w = 0; w < 4; ++w) wv[slot][w] = w4[w];
+    } else {
+      const u32x2 w2 = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(wrow + (k0 >> 3)));
+      wv[slot][0] = w2[0];
+      wv[slot][1] = w2[1];
+    }
+    sv[slot] = szrow[(k0 + 8 * WPT * wq) >> gsh];
   };
   auto stage = [&](int buf, int slot) {
 #pragma unroll
-    for (int i = 0; i < XL; ++i) *reinterpret_cast<u32x4*>(&Xs[buf][xr + 32 * i][8 * xc]) = xv[slot][i];
-    if (wload) {
+    for (int i = 0; i < XL; ++i) Xs[kg][buf][xr + 32 * i][lds_chunk(xr + 32 * i, xc)] = xv[slot][i];
 #pragma unroll
-      for (int w = 0; w < 4; ++w)
-        *reinterpret_cast<u32x4*>(&Ws[buf][wr][32 * wh + 8 * w]) = dequant8(wv[slot][w], sv[slot]);
-    }
+    for (int w = 0; w < WPT; ++w) Ws[kg][buf][wr][lds_chunk(wr, WPT * wq + w)] = dequant8(wv[slot][w], sv[slot]);
   };
 
   f4 acc[TI][TJ];
@@ -214,38 +251,87 @@ gemm_w4a16_wide(const uint32_t* __restrict__ W, const uint32_t* __restrict__ SZ,
 #pragma unroll
     for (int j = 0; j < TJ; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
   }
-  // chunk kc lives in register slot kc % PD from its fetch until it is staged into LDS buffer kc & 1: its loads are
-  // issued PD chunks of MFMA work before they are needed
+  // group kg's j-th chunk is kg + KG j (KG divides nk); it lives in register slot j % PD from its fetch until it is staged into the
+  // group's LDS buffer j & 1, so its loads are issued PD steps of MFMA work before they are needed
+  const int nsteps = nk / KG;
 #pragma unroll
-  for (int u = 0; u < PD; ++u) fetch(u, u);
+  for (int u = 0; u < PD; ++u) {
+    fetch(kg + KG * u, u);
+    phase_fence();  // slot order = issue order, which the in-order wait counts rely on
+  }
   stage(0, 0);
-  fetch(PD, 0);
+  phase_fence();
+  fetch(kg + KG * PD, 0);
+  phase_fence();
   __syncthreads();
-  for (int kc0 = 0; kc0 < nk; kc0 += PD) {
-#pragma unroll
-    for (int u = 0; u < PD; ++u) {  // chunk kc = kc0 + u; the slot indices stay compile-time constants
-      const int kc = kc0 + u;
-      if (kc >= nk) break;
-      const int buf = kc & 1;
+  // one step: MFMAs of step j from LDS buffer j & 1, stage of step j + 1 from register slot (u + 1) % PD, fetch of
+  // step j + 1 + PD into that slot (u = j % PD, a constant wherever this is called)
+  auto step = [&](int j, int u) {
+    const int buf = j & 1;
+    {  // every group has nk / KG steps (the launcher picks KG dividing nk)
 #pragma unroll
       for (int ks = 0; ks < kWK / 32; ++ks) {
         h8 a[TI], b[TJ];
 #pragma unroll
         for (int i = 0; i < TI; ++i)
-          a[i] = __builtin_bit_cast(h8, *reinterpret_cast<const u32x4*>(&Ws[buf][wn + 16 * i + c][32 * ks + 8 * g]));
+          a[i] = __builtin_bit_cast(h8, Ws[kg][buf][wn + 16 * i + c][lds_chunk(wn + 16 * i + c, 4 * ks + g)]);
 #pragma unroll
-        for (int j = 0; j < TJ; ++j)
-          b[j] = __builtin_bit_cast(h8, *reinterpret_cast<const u32x4*>(&Xs[buf][wm + 16 * j + c][32 * ks + 8 * g]));
+        for (int jj = 0; jj < TJ; ++jj)
+          b[jj] = __builtin_bit_cast(h8, Xs[kg][buf][wm + 16 * jj + c][lds_chunk(wm + 16 * jj + c, 4 * ks + g)]);
 #pragma unroll
         for (int i = 0; i < TI; ++i) {
 #pragma unroll
-          for (int j = 0; j < TJ; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+          for (int jj = 0; jj < TJ; ++jj) acc[i][jj] = mfma32(a[i], b[jj], acc[i][jj]);
         }
       }
-      const int nslot = (u + 1) % PD;  // a constant once the loop is unrolled
-      stage(buf ^ 1, nslot);            // chunk kc + 1 (past the end: a copy of the last chunk, never read)
-      fetch(kc + 1 + PD, nslot);
-      __syncthreads();
+    }
+    const int nslot = (u + 1) % PD;
+    // the stage sits in the MFMAs' basic block, so the scheduler can interleave its dequant and LDS stores with
+    // them; the fences keep the fetch after it (the stage then waits only for its own slot's loads, and the other
+    // slots' newer loads stay in flight)
+    stage(buf ^ 1, nslot);  // step j + 1 (past the end: a copy of the last chunk, never read)
+    phase_fence();
+    fetch(kg + KG * (j + 1 + PD), nslot);
+    phase_fence();
+    __syncthreads();
+  };
+  // whole groups of PD steps in the loop and the remainder after it: a loop body that could exit between its steps
+  // and re-enter would leave a path on which the newest loads are a different slot's, and the in-order wait counts
+  // would then have to drain everything
+  int j0 = 0;
+  for (; j0 + PD <= nsteps; j0 += PD) {
+#pragma unroll
+    for (int u = 0; u < PD; ++u) step(j0 + u, u);
+  }
+#pragma unroll
+  for (int u = 0; u + 1 < PD; ++u)
+    if (j0 + u < nsteps) step(j0 + u, u);
+  if constexpr (KG > 1) {
+    // groups 1 .. KG-1 leave their accumulators in their own (now idle) W buffers, lane-major; group 0 adds them
+    float* red = reinterpret_cast<float*>(&Ws[kg][0][0][0]);  // 2 BN kWK halves: room for TI TJ 4 floats a lane
+    if (kg > 0) {
+#pragma unroll
+      for (int i = 0; i < TI; ++i) {
+#pragma unroll
+        for (int jj = 0; jj < TJ; ++jj) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) red[((i * TJ + jj) * 4 + v) * kGemmThreads + tid] = acc[i][jj][v];
+        }
+      }
+    }
+    __syncthreads();
+    if (kg > 0) return;
+#pragma unroll
+    for (int q = 1; q < KG; ++q) {
+      const float* rq = reinterpret_cast<const float*>(&Ws[q][0][0][0]);
+#pragma unroll
+      for (int i = 0; i < TI; ++i) {
+#pragma unroll
+        for (int jj = 0; jj < TJ; ++jj) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[i][jj][v] += rq[((i * TJ + jj) * 4 + v) * kGemmThreads + tid];
+        }
+      }
     }
   }
   // ---- epilogue: lane holds Y[token m0 + wm + 16 j + c][n0 + wn + 16 i + 4 g + v], v = 0..3
@@ -289,38 +375,61 @@ gemm_w4a16_wide(const uint32_t* __restrict__ W, const uint32_t* __restrict__ SZ,
 #ifndef DK_GEMM_PD
 #define DK_GEMM_PD 2
 #endif
-template <int BN, int BM, int PD = DK_GEMM_PD>
+
+template <int BN, int BM, int KG, int PD = DK_GEMM_PD>
 void launch_wide(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int log2G,
                  int epilogue, hipStream_t st) {
   const int tiles_m = (M + BM - 1) / BM, tiles = tiles_m * ((N + BN - 1) / BN);
   const dim3 grid((tiles + kXcds - 1) / kXcds * kXcds);
   if (epilogue == 1)
-    hipLaunchKernelGGL((gemm_w4a16_wide<BN, BM, PD, 1>), grid, dim3(kGemmThreads), 0, st, (const uint32_t*)packed,
-                       (const uint32_t*)sz, (const f16*)x, (f16*)y, M, N, K, log2G, tiles_m, tiles);
+    hipLaunchKernelGGL((gemm_w4a16_wide<BN, BM, PD, KG, 1>), grid, dim3(kGemmThreads * KG), 0, st,
+                       (const uint32_t*)packed, (const uint32_t*)sz, (const f16*)x, (f16*)y, M, N, K, log2G, tiles_m,
+                       tiles);
   else
-    hipLaunchKernelGGL((gemm_w4a16_wide<BN, BM, PD, 0>), grid, dim3(kGemmThreads), 0, st, (const uint32_t*)packed,
-                       (const uint32_t*)sz, (const f16*)x, (f16*)y, M, N, K, log2G, tiles_m, tiles);
+    hipLaunchKernelGGL((gemm_w4a16_wide<BN, BM, PD, KG, 0>), grid, dim3(kGemmThreads * KG), 0, st,
+                       (const uint32_t*)packed, (const uint32_t*)sz, (const f16*)x, (f16*)y, M, N, K, log2G, tiles_m,
+                       tiles);
 }
 
 }  // namespace
 
-// Tile choice: the largest of 128 x 128, 128 x 64, 64 x 64 whose grid still fills the 256 CUs (one workgroup of
-// 256 threads per CU at least); K % 64 != 0 takes the 64 x 64 16x16x16 kernel above.
+// Tile choice: the largest of 128 x 128, 128 x 64, 64 x 64 whose grid still covers the 256 CUs, then K groups
+// (KG = 2 or 4 four-wave groups per workgroup; 2 at most for 128 x 64, by LDS) while the grid leaves CUs with a single
+// workgroup; K % 64 != 0 takes the
+// 64 x 64 16x16x16 kernel above. Returns 10 * tile + KG (tile 3: 128 x 128, 2: 128 x 64, 1: 64 x 64), 0 for that one.
+#ifndef DK_GEMM_KG
+#define DK_GEMM_KG 0
+#endif
 int gemm_w4a16_tile(int M, int N, int K) {
   if (K % kWK != 0) return 0;
   const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128);
   const long long t64m = (long long)((M + 63) / 64) * ((N + 127) / 128);
-  if (t128 >= 256) return 3;
-  if (t64m >= 256) return 2;
-  return 1;
+  const long long t64 = (long long)((M + 63) / 64) * ((N + 63) / 64);
+  int tile, kgr;
+  if (t128 >= 256) {
+    tile = 3;
+    kgr = 1;
+  } else if (t64m >= 256) {
+    tile = 2;
+    kgr = t64m > 256 ? 1 : 2;
+  } else {
+    tile = 1;
+    kgr = t64 > 512 ? 1 : (t64 > 256 ? 2 : 4);
+  }
+  if (DK_GEMM_KG > 0 && tile != 3) kgr = tile == 2 ? (DK_GEMM_KG > 2 ? 2 : DK_GEMM_KG) : DK_GEMM_KG;
+  while ((K / kWK) % kgr != 0) kgr >>= 1;  // every K group takes the same number of chunks
+  return 10 * tile + kgr;
 }
 
 void launch_gemm_w4a16(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int log2G,
                        int epilogue, hipStream_t st) {
   switch (gemm_w4a16_tile(M, N, K)) {
-    case 3: launch_wide<128, 128>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
-    case 2: launch_wide<128, 64>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
-    case 1: launch_wide<64, 64>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
+    case 31: launch_wide<128, 128, 1>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
+    case 21: launch_wide<128, 64, 1>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
+    case 22: launch_wide<128, 64, 2>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
+    case 11: launch_wide<64, 64, 1>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
+    case 12: launch_wide<64, 64, 2>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
+    case 14: launch_wide<64, 64, 4>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
     default: break;
   }
   const dim3 grid((N + kBN - 1) / kBN, (M + kBM - 1) / kBM);
