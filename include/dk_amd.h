@@ -136,9 +136,9 @@ int dk_rmsnorm_rows(const void* x_in, const int64_t* rows, const void* delta, co
 /*
  * Causal paged attention of M prompt rows (prefill): row m (position *pos + m) attends tokens [0, *pos + m] of the
  * cache, which must already hold them (dk_rope_append_rows); q is the first n_q heads of qkv row m, already rotated.
- * out [M, n_q * head_dim] fp16. One split of max_ctx tokens per (kv head, row), the MFMA kernel of dk_attention_decode
- * impl 2; positions past max_ctx are not attended. No counterpart in the reference (it teacher-forces prompts through
- * the decode step).
+ * out [M, n_q * head_dim] fp16. Tokens at positions >= max_ctx (and past the block table) are neither read nor
+ * attended; pass *pos + M to attend the whole prefix. fp32 scores and softmax, as dk_paged_attention. No counterpart
+ * in the reference (it teacher-forces prompts through the decode step).
  */
 int dk_attention_prefill(const void* qkv, const int32_t* pos, const int32_t* bt, int n_bt, const void* kc,
                          const void* vc, int n_pages, int page, int n_q, int n_kv, int head_dim, int M, int max_ctx,

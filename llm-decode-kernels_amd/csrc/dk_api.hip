@@ -393,14 +393,11 @@ int dk_attention_prefill(const void* qkv, const int32_t* pos, const int32_t* bt,
   if (M < 1 || M > 65535) return fail(DK_ERR_SHAPE, "attention_prefill: M must be 1..65535, got %d", M);
   if (!pow2(page)) return fail(DK_ERR_DOMAIN, "page size must be a power of two, got %d", page);
   if (n_pages < 1 || n_bt < 1) return fail(DK_ERR_SHAPE, "attention_prefill: empty cache or block table");
-  const int PS = ((max_ctx + 15) / 16) * 16;
-  if (max_ctx < 1 || !dk::attn_mfma_fits(PS, ilog2(page)))
-    return fail(DK_ERR_DOMAIN, "attention_prefill: max_ctx must be 1..%d at page %d, got %d",
-                ((dk::kAttnMaxSplitPages - 1) * page) / 16 * 16, page, max_ctx);
+  if (max_ctx < 1) return fail(DK_ERR_DOMAIN, "attention_prefill: max_ctx must be >= 1, got %d", max_ctx);
   if (!aligned16(qkv) || !aligned16(kc) || !aligned16(vc))
     return fail(DK_ERR_ALIGN, "qkv, kc and vc must be 16B aligned");
   clear_error();
-  dk::launch_attention_prefill(qkv, pos, bt, n_bt, kc, vc, n_pages, ilog2(page), n_q, n_kv, head_dim, M, PS, out,
+  dk::launch_attention_prefill(qkv, pos, bt, n_bt, kc, vc, n_pages, ilog2(page), n_q, n_kv, head_dim, M, max_ctx, out,
                                (hipStream_t)stream);
   return launched("attention_prefill");
 }

@@ -75,10 +75,10 @@ void launch_paged_attention(const AttnLaunch& a, hipStream_t st);
 void launch_attention_decode(const AttnLaunch& a, hipStream_t st);
 
 // Causal attention of M prompt rows (prefill): row m at position *pos + m attends tokens [0, *pos + m] of the cache
-// with one split of PS tokens (the MFMA kernel); q is the first n_q heads of qkv row m, already rotated.
+// (tokens at max_ctx and beyond are neither read nor attended); q is the first n_q heads of qkv row m, already rotated.
 void launch_attention_prefill(const void* qkv, const int32_t* pos, const int32_t* bt, int n_bt, const void* kc,
-                              const void* vc, int n_pages, int log2P, int n_q, int n_kv, int head_dim, int M, int PS,
-                              void* out, hipStream_t st);
+                              const void* vc, int n_pages, int log2P, int n_q, int n_kv, int head_dim, int M,
+                              int max_ctx, void* out, hipStream_t st);
 
 void launch_add_rmsnorm(void* x, const void* delta, const void* w, void* out, int H, float eps, hipStream_t st);
 void launch_swiglu(const void* gu, void* out, int I, hipStream_t st);

@@ -843,17 +843,202 @@ void launch_attn_hpg(const AttnLaunch& a, hipStream_t st) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Prefill attention: causal attention of M prompt rows (row m at position pos + m) over the paged cache, which already
+// holds their K / V. A workgroup of four waves owns one kv head and QB = 64 / HPG consecutive rows; each wave's 16
+// MFMA columns are (row, query head) pairs, PW = 16 / HPG rows x HPG heads, so every column does work. The K / V of
+// the tokens [0, last row's position] stream through LDS in 64-token blocks (double-buffered, the next block's loads
+// in flight during the current block's MFMAs) and all four waves read them there.
+// Per 16-token tile the math is the MFMA decode kernel's: S^T = K . Q^T (the accumulator is P's A operand as is), the
+// causal bound of each column applied to its own scores, online softmax once per block, P . V with p as fp16 hi + lo
+// parts and V operands built by byte permutes from 4 token rows. Each column's tokens are taken in the same block
+// order whatever workgroup or batch the row is in, so a row's result does not depend on how the prompt is batched.
+constexpr int kPfWaves = 4, kPfThreads = kPfWaves * kWave, kPfBlock = 64;
+
+template <int D, int HPG>
+__global__ void __launch_bounds__(kPfThreads)
+attn_prefill_kernel(const f16* __restrict__ qkv, const int32_t* __restrict__ pos_ptr, const int32_t* __restrict__ bt,
+                    int n_bt, const f16* __restrict__ kc, const f16* __restrict__ vc, int n_pages, int log2P, int n_q,
+                    int n_kv, int M, int ctx_cap, float scale, f16* __restrict__ out) {
+  using S = MfmaAttnShape<D>;
+  constexpr int KD = S::KD, KW = S::KW, QS = S::QS, VD = S::VD;
+  constexpr int PW = 16 / HPG;                           // rows per wave
+  constexpr int QB = kPfWaves * PW;                      // rows per workgroup
+  constexpr int ROW = D + 8;                             // padded LDS row: 16 rows of one K read in distinct banks
+  constexpr int CH = D / 8;                              // 16-byte chunks per K / V row
+  constexpr int LPT = kPfBlock * CH / kPfThreads;        // 16-byte K (and V) loads per thread per block
+  constexpr int RPI = kPfThreads / CH;                   // token rows covered per load index
+  __shared__ __align__(16) f16 Ks[2][kPfBlock][ROW];
+  __shared__ __align__(16) f16 Vs[2][kPfBlock][ROW];
+
+  const int kvh = blockIdx.x, qb = blockIdx.y;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int col = lane & 15, g = lane >> 4;
+  const int P = 1 << log2P;
+  const int pos0 = *pos_ptr;
+  // this lane's query column: prompt row m, head h; tokens t <= lim are attended
+  const int m = qb * QB + wave * PW + col / HPG;
+  const int h = kvh * HPG + col % HPG;
+  const bool live = m < M;
+  const int lim = live ? min(pos0 + m, ctx_cap - 1) : -1;  // the cap bounds the mask as well as the loads
+  const int mlast = min(qb * QB + QB, M) - 1;
+  const int ctx = (int)max(0LL, min((long long)pos0 + mlast + 1, (long long)ctx_cap));  // tokens [0, ctx) are read
+  u32x4 qr[KW];
+  {
+    const f16* qh = qkv + (size_t)(live ? m : 0) * (n_q + 2 * n_kv) * D + (size_t)h * D;
+#pragma unroll
+    for (int w = 0; w < KW; ++w)
+      qr[w] = live ? *reinterpret_cast<const u32x4*>(qh + KD * g + 8 * w) : u32x4{0u, 0u, 0u, 0u};
+  }
+
+  // staging: chunk tid % CH of token rows tid / CH + RPI i; tokens past ctx or without a page read page 0's row
+  // (every cache has one) and are zeroed by select
+  u32x4 kv_k[LPT], kv_v[LPT];
+  auto fetch = [&](int b0) {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int t = b0 + tid / CH + RPI * i;
+      const int lp = t >> log2P;
+      int pg = (t < ctx && lp < n_bt) ? bt[lp] : -1;
+      if (pg >= n_pages) pg = -1;
+      const size_t off =
+          ((((size_t)(pg < 0 ? 0 : pg) * n_kv + kvh) << log2P) + (t & (P - 1))) * D + 8 * (tid % CH);
+      const u32x4 kk = load_stream(reinterpret_cast<const u32x4*>(kc + off));
+      const u32x4 vv = load_stream(reinterpret_cast<const u32x4*>(vc + off));
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      kv_k[i] = pg >= 0 ? kk : z;
+      kv_v[i] = pg >= 0 ? vv : z;
+    }
+  };
+  auto stage = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int r = tid / CH + RPI * i;
+      *reinterpret_cast<u32x4*>(&Ks[buf][r][8 * (tid % CH)]) = kv_k[i];
+      *reinterpret_cast<u32x4*>(&Vs[buf][r][8 * (tid % CH)]) = kv_v[i];
+    }
+  };
+
+  float mrun = -INFINITY, l = 0.f;
+  f4 acc[VD];
+#pragma unroll
+  for (int t = 0; t < VD; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+  const int nblk = (ctx + kPfBlock - 1) / kPfBlock;
+  if (nblk > 0) {
+    fetch(0);
+    stage(0);
+  }
+  __syncthreads();
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int buf = blk & 1;
+    if (blk + 1 < nblk) fetch((blk + 1) * kPfBlock);  // in flight during this block's MFMAs
+    // ---- scores of the block's four 16-token tiles: sc[tt][v] = score of token 16 tt + 4 g + v for column col
+    f4 sc[4];
+    float rmax = -INFINITY;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      u32x4 kr[KW];
+#pragma unroll
+      for (int w = 0; w < KW; ++w) kr[w] = *reinterpret_cast<const u32x4*>(&Ks[buf][16 * tt + col][KD * g + 8 * w]);
+      f4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < QS; ++q) {
+        const int i0 = 2 * q, i1 = 2 * q + 1;
+        c = mfma16(as_h4(kr[i0 >> 2][i0 & 3], kr[i1 >> 2][i1 & 3]), as_h4(qr[i0 >> 2][i0 & 3], qr[i1 >> 2][i1 & 3]),
+                   c);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int t = blk * kPfBlock + 16 * tt + 4 * g + v;
+        sc[tt][v] = t <= lim ? c[v] * scale : -INFINITY;
+        rmax = fmaxf(rmax, sc[tt][v]);
+      }
+    }
+    // ---- online softmax, once per block
+    rmax = rows_max(rmax);
+    const float mn = fmaxf(mrun, rmax);
+    const float alpha = (mrun == -INFINITY) ? 0.f : __expf(mrun - mn);
+    float ps = 0.f;
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float pv = (sc[tt][v] == -INFINITY) ? 0.f : __expf(sc[tt][v] - mn);
+        sc[tt][v] = pv;
+        ps += pv;
+      }
+    }
+    l = alpha * l + rows_sum(ps);
+    mrun = mn;
+    // the accumulator's rows are columns 4 g + v: their rescale factors live in lanes 4 g + v
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float av = __shfl(alpha, 4 * g + v, kWave);
+#pragma unroll
+      for (int t = 0; t < VD; ++t) acc[t][v] *= av;
+    }
+    // ---- P . V: p as fp16 hi + lo parts; V rows 16 tt + 4 g + v, dims VD col .. VD col + VD - 1
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      h4 phi, plo;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        phi[v] = (f16)sc[tt][v];
+        plo[v] = (f16)(sc[tt][v] - (float)phi[v]);
+      }
+      VRow<VD> vr[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const f16* src = &Vs[buf][16 * tt + 4 * g + v][VD * col];
+        if constexpr (VD == 4) {
+          const u32x2 x = *reinterpret_cast<const u32x2*>(src);
+          vr[v].w[0] = x.x;
+          vr[v].w[1] = x.y;
+        } else {
+          const u32x4 x = *reinterpret_cast<const u32x4*>(src);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) vr[v].w[i] = x[i];
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < VD; ++t) {
+        const int wi = t >> 1;
+        const uint32_t sel = (t & 1) ? 0x07060302u : 0x05040100u;
+        const uint32_t lo = __builtin_amdgcn_perm(vr[1].w[wi], vr[0].w[wi], sel);
+        const uint32_t hi = __builtin_amdgcn_perm(vr[3].w[wi], vr[2].w[wi], sel);
+        const h4 vb = as_h4(lo, hi);
+        acc[t] = mfma16(phi, vb, acc[t]);
+        acc[t] = mfma16(plo, vb, acc[t]);
+      }
+    }
+    if (blk + 1 < nblk) stage(buf ^ 1);  // the other buffer: every wave finished reading it before the last barrier
+    __syncthreads();
+  }
+  // ---- output: acc[t][v] = O[column 4 g + v][dim VD col + t]; the column's l lives in lane 4 g + v
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int cc = 4 * g + v;
+    const float lv = __shfl(l, cc, kWave);
+    const int mm = qb * QB + wave * PW + cc / HPG, hh = kvh * HPG + cc % HPG;
+    if (mm < M) {
+      const float inv = lv > 0.f ? 1.0f / lv : 0.f;
+      f16* dst = out + (size_t)mm * n_q * D + (size_t)hh * D + VD * col;
+#pragma unroll
+      for (int t = 0; t < VD; ++t) dst[t] = (f16)(acc[t][v] * inv);
+    }
+  }
+}
+
 template <int D>
 void launch_prefill_hpg(const void* qkv, const int32_t* pos, const int32_t* bt, int n_bt, const void* kc,
-                        const void* vc, int n_pages, int log2P, int n_q, int n_kv, int M, int PS, void* out,
+                        const void* vc, int n_pages, int log2P, int n_q, int n_kv, int M, int max_ctx, void* out,
                         hipStream_t st) {
   const float scale = 1.0f / sqrtf((float)D);
-  const dim3 grid(n_kv, 1, M);
-  const int qstride = (n_q + 2 * n_kv) * D;
-#define DK_PREFILL(H)                                                                                                \
-  hipLaunchKernelGGL((attn_mfma_kernel<D, H, false>), grid, dim3(kMfmaThreads), 0, st, (const f16*)qkv, nullptr,     \
-                     nullptr, 0, pos, bt, n_bt, (f16*)kc, (f16*)vc, n_pages, log2P, n_q, n_kv, PS, 1, scale,        \
-                     nullptr, nullptr, nullptr, (f16*)out, qstride)
+  const int cap = (int)min((long long)max_ctx, (long long)n_bt << log2P);
+#define DK_PREFILL(H)                                                                                               \
+  hipLaunchKernelGGL((attn_prefill_kernel<D, H>), dim3(n_kv, (M + kPfWaves * (16 / H) - 1) / (kPfWaves * (16 / H))), \
+                     dim3(kPfThreads), 0, st, (const f16*)qkv, pos, bt, n_bt, (const f16*)kc, (const f16*)vc,       \
+                     n_pages, log2P, n_q, n_kv, M, cap, scale, (f16*)out)
   switch (n_q / n_kv) {
     case 1: DK_PREFILL(1); break;
     case 2: DK_PREFILL(2); break;
@@ -866,12 +1051,12 @@ void launch_prefill_hpg(const void* qkv, const int32_t* pos, const int32_t* bt, 
 }  // namespace
 
 void launch_attention_prefill(const void* qkv, const int32_t* pos, const int32_t* bt, int n_bt, const void* kc,
-                              const void* vc, int n_pages, int log2P, int n_q, int n_kv, int head_dim, int M, int PS,
-                              void* out, hipStream_t st) {
+                              const void* vc, int n_pages, int log2P, int n_q, int n_kv, int head_dim, int M,
+                              int max_ctx, void* out, hipStream_t st) {
   if (head_dim == 64)
-    launch_prefill_hpg<64>(qkv, pos, bt, n_bt, kc, vc, n_pages, log2P, n_q, n_kv, M, PS, out, st);
+    launch_prefill_hpg<64>(qkv, pos, bt, n_bt, kc, vc, n_pages, log2P, n_q, n_kv, M, max_ctx, out, st);
   else
-    launch_prefill_hpg<128>(qkv, pos, bt, n_bt, kc, vc, n_pages, log2P, n_q, n_kv, M, PS, out, st);
+    launch_prefill_hpg<128>(qkv, pos, bt, n_bt, kc, vc, n_pages, log2P, n_q, n_kv, M, max_ctx, out, st);
 }
 
 void launch_paged_attention(const AttnLaunch& a, hipStream_t st) {
