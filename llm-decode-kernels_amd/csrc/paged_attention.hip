@@ -853,13 +853,17 @@ void launch_attn_hpg(const AttnLaunch& a, hipStream_t st) {
 // causal bound of each column applied to its own scores, online softmax once per block, P . V with p as fp16 hi + lo
 // parts and V operands built by byte permutes from 4 token rows. Each column's tokens are taken in the same block
 // order whatever workgroup or batch the row is in, so a row's result does not depend on how the prompt is batched.
-constexpr int kPfWaves = 4, kPfThreads = kPfWaves * kWave, kPfBlock = 64;
+constexpr int kPfWaves = 4, kPfThreads = kPfWaves * kWave, kPfBlock = 64, kPfPages = 2048, kPfRing = 2;
+
+// Keeps loads where they are written (no sinking to their first use; see the K / V ring below).
+__device__ __forceinline__ void pf_fence() { asm volatile("" ::: "memory"); }
 
 template <int D, int HPG>
 __global__ void __launch_bounds__(kPfThreads)
 attn_prefill_kernel(const f16* __restrict__ qkv, const int32_t* __restrict__ pos_ptr, const int32_t* __restrict__ bt,
-                    int n_bt, const f16* __restrict__ kc, const f16* __restrict__ vc, int n_pages, int log2P, int n_q,
-                    int n_kv, int M, int ctx_cap, float scale, f16* __restrict__ out) {
+                    int n_bt, const f16* kc, const f16* vc, int n_pages, int log2P, int n_q, int n_kv, int M,
+                    int ctx_cap, float scale, f16* __restrict__ out) {
+  // (kc, vc without __restrict__: the fences must order their loads)
   using S = MfmaAttnShape<D>;
   constexpr int KD = S::KD, KW = S::KW, QS = S::QS, VD = S::VD;
   constexpr int PW = 16 / HPG;                           // rows per wave
@@ -870,6 +874,7 @@ attn_prefill_kernel(const f16* __restrict__ qkv, const int32_t* __restrict__ pos
   constexpr int RPI = kPfThreads / CH;                   // token rows covered per load index
   __shared__ __align__(16) f16 Ks[2][kPfBlock][ROW];
   __shared__ __align__(16) f16 Vs[2][kPfBlock][ROW];
+  __shared__ int s_pg[kPfPages];
 
   const int kvh = blockIdx.x, qb = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -883,6 +888,10 @@ attn_prefill_kernel(const f16* __restrict__ qkv, const int32_t* __restrict__ pos
   const int lim = live ? min(pos0 + m, ctx_cap - 1) : -1;  // the cap bounds the mask as well as the loads
   const int mlast = min(qb * QB + QB, M) - 1;
   const int ctx = (int)max(0LL, min((long long)pos0 + mlast + 1, (long long)ctx_cap));  // tokens [0, ctx) are read
+  const int npg = (ctx + P - 1) >> log2P;
+  const bool staged = npg <= kPfPages;  // uniform: block-table pages in LDS, else read per token from global
+  if (staged)
+    for (int i = tid; i < npg; i += kPfThreads) s_pg[i] = bt[i];
   u32x4 qr[KW];
   {
     const f16* qh = qkv + (size_t)(live ? m : 0) * (n_q + 2 * n_kv) * D + (size_t)h * D;
@@ -890,32 +899,36 @@ attn_prefill_kernel(const f16* __restrict__ qkv, const int32_t* __restrict__ pos
     for (int w = 0; w < KW; ++w)
       qr[w] = live ? *reinterpret_cast<const u32x4*>(qh + KD * g + 8 * w) : u32x4{0u, 0u, 0u, 0u};
   }
+  __syncthreads();  // s_pg
 
-  // staging: chunk tid % CH of token rows tid / CH + RPI i; tokens past ctx or without a page read page 0's row
-  // (every cache has one) and are zeroed by select
-  u32x4 kv_k[LPT], kv_v[LPT];
-  auto fetch = [&](int b0) {
+  // K / V ring: block b's loads go into register slot b % kPfRing kPfRing blocks before the block is computed and
+  // are staged into LDS buffer b & 1 one block before. Thread: chunk tid % CH of token rows tid / CH + RPI i; tokens
+  // past ctx or without a page read page 0's row (every cache has one) and are zeroed by select.
+  const int nblk = (ctx + kPfBlock - 1) / kPfBlock;
+  u32x4 kk[kPfRing][LPT], vv[kPfRing][LPT];
+  bool ok[kPfRing][LPT];
+  auto fetch = [&](int blk, int slot) {
+    const int b0 = min(blk, nblk - 1) * kPfBlock;  // past the end: a re-read of the last block, never staged
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int t = b0 + tid / CH + RPI * i;
       const int lp = t >> log2P;
-      int pg = (t < ctx && lp < n_bt) ? bt[lp] : -1;
+      int pg = t < ctx ? (staged ? s_pg[lp] : bt[lp]) : -1;
       if (pg >= n_pages) pg = -1;
       const size_t off =
           ((((size_t)(pg < 0 ? 0 : pg) * n_kv + kvh) << log2P) + (t & (P - 1))) * D + 8 * (tid % CH);
-      const u32x4 kk = load_stream(reinterpret_cast<const u32x4*>(kc + off));
-      const u32x4 vv = load_stream(reinterpret_cast<const u32x4*>(vc + off));
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      kv_k[i] = pg >= 0 ? kk : z;
-      kv_v[i] = pg >= 0 ? vv : z;
+      kk[slot][i] = load_stream(reinterpret_cast<const u32x4*>(kc + off));
+      vv[slot][i] = load_stream(reinterpret_cast<const u32x4*>(vc + off));
+      ok[slot][i] = pg >= 0;
     }
   };
-  auto stage = [&](int buf) {
+  auto stage = [&](int buf, int slot) {
+    const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int r = tid / CH + RPI * i;
-      *reinterpret_cast<u32x4*>(&Ks[buf][r][8 * (tid % CH)]) = kv_k[i];
-      *reinterpret_cast<u32x4*>(&Vs[buf][r][8 * (tid % CH)]) = kv_v[i];
+      *reinterpret_cast<u32x4*>(&Ks[buf][r][8 * (tid % CH)]) = ok[slot][i] ? kk[slot][i] : z;
+      *reinterpret_cast<u32x4*>(&Vs[buf][r][8 * (tid % CH)]) = ok[slot][i] ? vv[slot][i] : z;
     }
   };
 
@@ -923,15 +936,8 @@ attn_prefill_kernel(const f16* __restrict__ qkv, const int32_t* __restrict__ pos
   f4 acc[VD];
 #pragma unroll
   for (int t = 0; t < VD; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
-  const int nblk = (ctx + kPfBlock - 1) / kPfBlock;
-  if (nblk > 0) {
-    fetch(0);
-    stage(0);
-  }
-  __syncthreads();
-  for (int blk = 0; blk < nblk; ++blk) {
-    const int buf = blk & 1;
-    if (blk + 1 < nblk) fetch((blk + 1) * kPfBlock);  // in flight during this block's MFMAs
+
+  auto compute = [&](int blk, int buf) {
     // ---- scores of the block's four 16-token tiles: sc[tt][v] = score of token 16 tt + 4 g + v for column col
     f4 sc[4];
     float rmax = -INFINITY;
@@ -1011,8 +1017,40 @@ attn_prefill_kernel(const f16* __restrict__ qkv, const int32_t* __restrict__ pos
         acc[t] = mfma16(plo, vb, acc[t]);
       }
     }
-    if (blk + 1 < nblk) stage(buf ^ 1);  // the other buffer: every wave finished reading it before the last barrier
+  };
+  // block blk (u = blk % kPfRing, a constant wherever this is called): compute from LDS buffer blk & 1, stage block
+  // blk + 1 from its slot into the other buffer (every wave finished reading it before the last barrier), refill that
+  // slot with block blk + 1 + kPfRing
+  auto step = [&](int blk, int u) {
+    compute(blk, blk & 1);
+    const int ns = (u + 1) % kPfRing;
+    stage((blk + 1) & 1, ns);  // past the end: a stale slot into an unread buffer
+    pf_fence();
+    fetch(blk + 1 + kPfRing, ns);
+    pf_fence();
     __syncthreads();
+  };
+  if (nblk > 0) {  // uniform
+#pragma unroll
+    for (int u = 0; u < kPfRing; ++u) {
+      fetch(u, u);
+      pf_fence();
+    }
+    stage(0, 0);
+    pf_fence();
+    fetch(kPfRing, 0);
+    pf_fence();
+    __syncthreads();
+    // whole groups of kPfRing blocks in the loop, the remainder after it (no exit between a group's blocks, which
+    // would leave a path where another slot's loads are the newest and the in-order waits drain everything)
+    int b0 = 0;
+    for (; b0 + kPfRing <= nblk; b0 += kPfRing) {
+#pragma unroll
+      for (int u = 0; u < kPfRing; ++u) step(b0 + u, u);
+    }
+#pragma unroll
+    for (int u = 0; u + 1 < kPfRing; ++u)
+      if (b0 + u < nblk) step(b0 + u, u);
   }
   // ---- output: acc[t][v] = O[column 4 g + v][dim VD col + t]; the column's l lives in lane 4 g + v
 #pragma unroll
