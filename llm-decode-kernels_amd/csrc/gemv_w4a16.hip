@@ -432,6 +432,11 @@ __device__ __forceinline__ void tile_input_finish(const GemvInput& in, TileRaw& 
 //               separate ops round it. Needs an even tile (T * NT) so that a pair never straddles two workgroups.
 enum { kOutRows = 0, kOutSwiglu = 1 };
 
+#ifndef DK_TILE_DEPTH
+#define DK_TILE_DEPTH 2
+#endif
+constexpr int kTileDepth = DK_TILE_DEPTH;  // weight tiles in flight per workgroup (the buffers of the pipeline)
+
 // Pipeline: operand loads, then the weight loads of tiles 0 and 1, then the operand (waits for the operand loads
 // only), then for each tile t: compute it from its buffer and refill that buffer with tile t + 2. Two tiles are in
 // flight from the first instruction on.
@@ -451,10 +456,11 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
 
   TileRaw raw;
   tile_input_load<PRO>(in, uc, U << 5, raw);
-  u32x4 w[2][T];
-  uint32_t sz[2][T];
-  tile_issue<T>(W, SZ, base, N, U, NG, uc, gsh, w[0], sz[0]);
-  if constexpr (NT > 1) tile_issue<T>(W, SZ, base + T, N, U, NG, uc, gsh, w[1], sz[1]);
+  constexpr int DP = NT < kTileDepth ? NT : kTileDepth;  // tiles in flight
+  u32x4 w[DP][T];
+  uint32_t sz[DP][T];
+#pragma unroll
+  for (int d = 0; d < DP; ++d) tile_issue<T>(W, SZ, base + d * T, N, U, NG, uc, gsh, w[d], sz[d]);
   __builtin_amdgcn_sched_barrier(0);
   u32x4 xc[4];
   tile_input_finish<PRO>(in, raw, uc, live, U << 5, s_ss, wave, nw, xc);
@@ -470,8 +476,8 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     float v[T];
-    tile_rows<T>(w[t & 1], sz[t & 1], xc, SA, SB, live, v);
-    if (t + 2 < NT) tile_issue<T>(W, SZ, base + (t + 2) * T, N, U, NG, uc, gsh, w[t & 1], sz[t & 1]);
+    tile_rows<T>(w[t % DP], sz[t % DP], xc, SA, SB, live, v);
+    if (t + DP < NT) tile_issue<T>(W, SZ, base + (t + DP) * T, N, U, NG, uc, gsh, w[t % DP], sz[t % DP]);
     __builtin_amdgcn_sched_barrier(0);
     if (lane == 63) {
 #pragma unroll

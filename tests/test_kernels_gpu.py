@@ -78,12 +78,10 @@ def _quantized(K, N, Kd, G, seed):
     return w, packed, sz
 
 
-@pytest.mark.parametrize("name", list(SHAPES) + list(SHAPES_8B))
-@pytest.mark.parametrize("G", (64, 128, 256))
+# the TinyLlama shapes at three group sizes, the Llama-3-8B shapes at the model's group size
+@pytest.mark.parametrize("name,G", [(n, g) for g in (64, 128, 256) for n in SHAPES] + [(n, 128) for n in SHAPES_8B])
 def test_gemv_real_shapes(K, name, G):
     N, Kd = {**SHAPES, **SHAPES_8B}[name]
-    if name in SHAPES_8B and G != 128:
-        pytest.skip("8B shapes are gated at the model's group size only")
     w, packed, sz = _quantized(K, N, Kd, G, seed=zlib.crc32(name.encode()) % 1000)
     wref = dequant_from_gpu(packed, sz, G)
     x = torch.randn(Kd, generator=gen(1)).half()
