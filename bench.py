@@ -113,6 +113,77 @@ def calibration_leg(Kx, nbytes, n=16):
     del cold
 
 
+def kernels_leg(Kx, n=64, reps=5):
+    """BASELINE configs 2 and 3: the attention ops (32 q / 4 kv heads, D 64, page 16) at contexts 128..4096 and the
+    fused elementwise ops at TinyLlama sizes, each as the mean over a hipGraph of n back-to-back launches (inputs stay
+    L2-resident across launches, as in the reference's kernel bench), with GB/s by the algorithmic byte counts:
+    attention 1024 ctx (K and V) + 8192 (q, out) + ctx / 4 (block table); add_rmsnorm 10 H; swiglu 6 I; rope_append
+    4 D (n_q + 2 n_kv). Part size and kernel choice are the runtime's attention policy for each context."""
+    import math
+    import torch
+    from runtime.model import DecodeConfig, rope_tables
+    from runtime.timing import graph_time
+
+    dev = "cuda"
+    pol = [e for e in json.load(open(DecodeConfig().attn_policy_path)).get("policy", []) if e["max_ctx"] < (1 << 30)]
+
+    def entry(ctx):
+        below = [e for e in pol if e["max_ctx"] <= ctx]
+        return below[-1] if below else (pol[0] if pol else {"part_size": 64, "impl": 1})
+
+    n_q, n_kv, D, P = 32, 4, 64, 16
+    out = {"attention": {}, "fused": {}}
+    for ctx in (128, 512, 2048, 4096):
+        g = torch.Generator(device=dev).manual_seed(ctx)
+        pages = ctx // P + 3
+        kc = torch.randn(pages, n_kv, P, D, generator=g, device=dev).half()
+        vc = torch.randn(pages, n_kv, P, D, generator=g, device=dev).half()
+        bt = torch.randperm(pages, generator=g, device=dev).int()
+        q = torch.randn(n_q * D, generator=g, device=dev).half()
+        qkv = torch.randn((n_q + 2 * n_kv) * D, generator=g, device=dev).half()
+        pos = torch.tensor([ctx - 1], dtype=torch.int32, device=dev)
+        cos, sin = (t.to(dev) for t in rope_tables(ctx + 1, D))
+        e = entry(ctx)
+        ps, impl = e["part_size"], e.get("impl", 1)
+        S = math.ceil(ctx / ps)
+        f32 = dict(dtype=torch.float32, device=dev)
+        o_part, m_part, l_part = torch.empty(n_q, S, D, **f32), torch.empty(n_q, S, **f32), torch.empty(n_q, S, **f32)
+        o = torch.empty(n_q, D, dtype=torch.half, device=dev)
+        nbytes = 1024 * ctx + 8192 + ctx // 4
+        t_ref = graph_time(lambda i: Kx.paged_attention(q, kc, vc, bt, pos, ps, o_part, m_part, l_part, o, 3), n,
+                           reps)[1]
+        t_dec = graph_time(lambda i: Kx.attention_decode(qkv, cos, sin, pos, bt, kc, vc, n_q, n_kv, ps, o_part, m_part,
+                                                         l_part, o, None, impl), n, reps)[1]
+        out["attention"][str(ctx)] = {
+            "bytes": nbytes, "part_size": ps, "paged_attention_v3_us": round(t_ref, 3),
+            "paged_attention_v3_gbps": round(nbytes / t_ref / 1e3, 1), "attention_decode_impl": impl,
+            "attention_decode_us": round(t_dec, 3), "attention_decode_gbps": round(nbytes / t_dec / 1e3, 1)}
+    g = torch.Generator(device=dev).manual_seed(3)
+    H, I = 2048, 5632
+    x = torch.randn(H, generator=g, device=dev).half()
+    zero = torch.zeros(H, dtype=torch.half, device=dev)
+    w = torch.randn(H, generator=g, device=dev).half()
+    normed = torch.empty(H, dtype=torch.half, device=dev)
+    gu = torch.randn(2 * I, generator=g, device=dev).half()
+    act = torch.empty(I, dtype=torch.half, device=dev)
+    pages = 512 // P + 3
+    kc = torch.zeros(pages, n_kv, P, D, dtype=torch.half, device=dev)
+    vc = torch.zeros_like(kc)
+    bt = torch.arange(pages, dtype=torch.int32, device=dev)
+    qkv = torch.randn((n_q + 2 * n_kv) * D, generator=g, device=dev).half()
+    cos, sin = (t.to(dev) for t in rope_tables(513, D))
+    pos = torch.tensor([511], dtype=torch.int32, device=dev)
+    for name, nbytes, fn in (
+            ("add_rmsnorm_2048", 10 * H, lambda i: Kx.add_rmsnorm(x, zero, w, normed, 1e-5)),
+            ("swiglu_5632", 6 * I, lambda i: Kx.swiglu(gu, act)),
+            ("rope_append_32q4kv_d64", 4 * D * (n_q + 2 * n_kv),
+             lambda i: Kx.rope_append(qkv, cos, sin, pos, bt, kc, vc, n_q, n_kv))):
+        t = graph_time(fn, n, reps)[1]
+        out["fused"][name] = {"bytes": nbytes, "us": round(t, 3), "gbps": round(nbytes / t / 1e3, 2),
+                              "frac": round(nbytes / t / 1e3 / HBM_PEAK_GBS, 5)}
+    return out
+
+
 def decode_leg(model, ctx, steps, warmup):
     import torch
     model.reset(ctx)
@@ -263,9 +334,10 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--ctx", type=int, default=512)
-    ap.add_argument("--leg", choices=("all", "gemv", "decode", "decode8b", "prefill"), default="all",
+    ap.add_argument("--leg", choices=("all", "gemv", "kernels", "decode", "decode8b", "prefill"), default="all",
                     help="gemv: the 4096x14336 GEMV and its calibration copies only; decode: the TinyLlama decode "
-                         "step only; decode8b: the Llama-3-8B decode legs only; prefill: the TinyLlama prefill leg only")
+                         "step only; decode8b: the Llama-3-8B decode legs only; prefill: the TinyLlama prefill leg only; kernels: "
+                         "the attention and fused-op kernels of configs 2 and 3 only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline leg")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -285,6 +357,10 @@ def main():
         print(json.dumps({"leg": "gemv", "gemv_4096x14336": g1}), flush=True)
         return
 
+    if a.leg == "kernels":
+        print(json.dumps({"leg": "kernels", "kernels_cfg2_cfg3": kernels_leg(Kx)}), flush=True)
+        return
+
     if a.leg == "decode8b":
         print(json.dumps({"leg": "decode8b", "decode_llama3_8b_ctx4096": decode_8b_leg()}), flush=True)
         return
@@ -301,6 +377,10 @@ def main():
     log(f"gemv 5632x2048 {g3['cfg']}: {g3['mean_us']:.3f} us/launch -> {g3['gbps']:.0f} GB/s ({g3['frac']:.1%})")
     rc = read_ceiling_leg(Kx, g1["bytes"])
     log(f"bw_read of {rc['bytes']} B: {rc['mean_us']:.3f} us -> {rc['gbps']:.0f} GB/s ({rc['frac']:.1%})")
+    kern = kernels_leg(Kx)
+    log("attention (cfg2) us: " + ", ".join(f"ctx {c}: ref op {v['paged_attention_v3_us']}, fused {v['attention_decode_us']}"
+                                          for c, v in kern["attention"].items()))
+    log("fused ops (cfg3) us: " + ", ".join(f"{k} {v['us']}" for k, v in kern["fused"].items()))
 
     log(f"device {dev_name}; building TinyLlama-shape W4A16 model")
     t0 = time.perf_counter()
@@ -352,7 +432,7 @@ def main():
                      "achieved": g1["gbps"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": g1["frac"],
                      "traffic": traffic, "bytes_per_launch": g1["bytes"], "mean_us": g1["mean_us"],
                      "read_ceiling_frac": rc["frac"]},
-        "gemv_14336x4096": g2, "gemv_cfg1_5632x2048": g3, "read_ceiling": rc,
+        "gemv_14336x4096": g2, "gemv_cfg1_5632x2048": g3, "read_ceiling": rc, "kernels_cfg2_cfg3": kern,
         "decode": {**{k: round(v, 3) if isinstance(v, float) else v for k, v in dec.items()},
                    "bytes_per_token": bpt, "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / bpt, 1),
                    "frac_of_roofline": round(dec["tok_s"] / (HBM_PEAK_GBS * 1e9 / bpt), 4)},
