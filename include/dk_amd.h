@@ -127,11 +127,12 @@ int dk_rope_append_rows(void* qkv, const float* cos_t, const float* sin_t, const
 /*
  * Residual + RMSNorm of M rows (prefill), each with dk_add_rmsnorm's rounding points: xn = x_in[src] + delta[r]
  * (delta may be NULL; src = rows[r] when rows != NULL, e.g. the embedding rows of the prompt's tokens, else r),
- * x_out[r] = xn, out[r] = w * fp16(float(xn) * rsqrt-term). x_out may equal x_in when rows is NULL; out aliases
- * nothing. No counterpart in the reference (its add_rmsnorm is one vector, kernels/bindings.cpp:64-72).
+ * x_out[r] = xn, out[r] = w * fp16(float(xn) * rsqrt-term). x_in has n_src rows (M when rows is NULL); a gathered
+ * index outside [0, n_src) is not read: that row's x_out and out are NaN. x_out may equal x_in when rows is NULL; out
+ * aliases nothing. No counterpart in the reference (its add_rmsnorm is one vector, kernels/bindings.cpp:64-72).
  */
-int dk_rmsnorm_rows(const void* x_in, const int64_t* rows, const void* delta, const void* w, void* x_out, void* out,
-                    int M, int H, float eps, void* stream);
+int dk_rmsnorm_rows(const void* x_in, const int64_t* rows, int n_src, const void* delta, const void* w, void* x_out,
+                    void* out, int M, int H, float eps, void* stream);
 
 /*
  * Causal paged attention of M prompt rows (prefill): row m (position *pos + m) attends tokens [0, *pos + m] of the

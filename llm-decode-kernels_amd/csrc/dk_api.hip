@@ -361,8 +361,8 @@ int dk_rope_append_rows(void* qkv, const float* cos_t, const float* sin_t, const
   return launched("rope_append_rows");
 }
 
-int dk_rmsnorm_rows(const void* x_in, const int64_t* rows, const void* delta, const void* w, void* x_out, void* out,
-                    int M, int H, float eps, void* stream) {
+int dk_rmsnorm_rows(const void* x_in, const int64_t* rows, int n_src, const void* delta, const void* w, void* x_out,
+                    void* out, int M, int H, float eps, void* stream) {
   if (!x_in || !w || !x_out || !out) return fail(DK_ERR_NULL, "rmsnorm_rows: null pointer argument");
   if (M < 1 || M > (1 << 24)) return fail(DK_ERR_SHAPE, "rmsnorm_rows: M must be 1..2^24, got %d", M);
   if (H <= 0 || H % 8 != 0 || H > (1 << 20))
@@ -373,8 +373,10 @@ int dk_rmsnorm_rows(const void* x_in, const int64_t* rows, const void* delta, co
   if (out == x_in || out == x_out || (delta && out == delta))
     return fail(DK_ERR_DOMAIN, "rmsnorm_rows: out must not alias x_in, x_out or delta");
   if (rows && x_out == x_in) return fail(DK_ERR_DOMAIN, "rmsnorm_rows: a gathered x_in must not be x_out");
+  if (rows ? n_src < 1 : n_src != M)
+    return fail(DK_ERR_SHAPE, "rmsnorm_rows: n_src (rows of x_in) must be >= 1 with rows, M without, got %d", n_src);
   clear_error();
-  dk::launch_rmsnorm_rows(x_in, rows, delta, w, x_out, out, M, H, eps, (hipStream_t)stream);
+  dk::launch_rmsnorm_rows(x_in, rows, n_src, delta, w, x_out, out, M, H, eps, (hipStream_t)stream);
   return launched("rmsnorm_rows");
 }
 

@@ -60,11 +60,14 @@ add_rmsnorm_kernel(f16* __restrict__ x, const f16* __restrict__ delta, const f16
 // the prompt's tokens, else r), x_out[r] = xn, out[r] = w * fp16(float(xn) * r_r), r_r = 1 / sqrt(sum(xn^2) / H + eps).
 // x_out may be x_in itself when there is no gather (a row is read and written by its own workgroup only).
 __global__ void __launch_bounds__(1024)
-rmsnorm_rows_kernel(const f16* x_in, const int64_t* __restrict__ rows, const f16* __restrict__ delta,
+rmsnorm_rows_kernel(const f16* x_in, const int64_t* __restrict__ rows, int n_src, const f16* __restrict__ delta,
                     const f16* __restrict__ w, f16* x_out, f16* __restrict__ out, int H, float eps) {
   __shared__ float wsum[16];
   const int r = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
-  const f16* src = x_in + (size_t)(rows != nullptr ? rows[r] : r) * H;
+  // a gathered row index outside [0, n_src) reads row 0 and poisons the row with NaN instead of reading out of bounds
+  const long long sr = rows != nullptr ? rows[r] : r;
+  const bool bad = sr < 0 || sr >= n_src;
+  const f16* src = x_in + (size_t)(bad ? 0 : sr) * H;
   f16* xo = x_out + (size_t)r * H;
   float ss = 0.f;
   for (int i = tid * 8; i < H; i += nt * 8) {
@@ -74,6 +77,7 @@ rmsnorm_rows_kernel(const f16* x_in, const int64_t* __restrict__ rows, const f16
 #pragma unroll
       for (int k = 0; k < 4; ++k) xv[k] = as_u32(as_f16x2(xv[k]) + as_f16x2(dv[k]));
     }
+    if (bad) xv = u32x4{0x7E007E00u, 0x7E007E00u, 0x7E007E00u, 0x7E007E00u};  // fp16 NaN
     *reinterpret_cast<u32x4*>(xo + i) = xv;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -88,7 +92,7 @@ rmsnorm_rows_kernel(const f16* x_in, const int64_t* __restrict__ rows, const f16
   __syncthreads();
   float tot = 0.f;
   for (int i = 0; i < (nt >> 6); ++i) tot += wsum[i];
-  const float rr = 1.0f / sqrtf(tot / (float)H + eps);
+  const float rr = bad ? __builtin_nanf("") : 1.0f / sqrtf(tot / (float)H + eps);
   for (int i = tid * 8; i < H; i += nt * 8) {
     const u32x4 xv = *reinterpret_cast<const u32x4*>(xo + i);  // this thread's own write above
     const u32x4 wv = *reinterpret_cast<const u32x4*>(w + i);
@@ -275,11 +279,11 @@ void launch_rope_append(void* qkv, const float* cos_t, const float* sin_t, const
                        (f16*)kc, (f16*)vc, n_q, n_kv, log2P, max_pos, n_pages, n_bt, stride);
 }
 
-void launch_rmsnorm_rows(const void* x_in, const int64_t* rows, const void* delta, const void* w, void* x_out,
+void launch_rmsnorm_rows(const void* x_in, const int64_t* rows, int n_src, const void* delta, const void* w, void* x_out,
                          void* out, int M, int H, float eps, hipStream_t st) {
   int threads = ((H / 8 + 63) / 64) * 64;
   if (threads > 1024) threads = 1024;
-  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(M), dim3(threads), 0, st, (const f16*)x_in, rows, (const f16*)delta,
+  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(M), dim3(threads), 0, st, (const f16*)x_in, rows, n_src, (const f16*)delta,
                      (const f16*)w, (f16*)x_out, (f16*)out, H, eps);
 }
 

@@ -86,7 +86,7 @@ void launch_swiglu(const void* gu, void* out, int I, hipStream_t st);
 void launch_rope_append(void* qkv, const float* cos_t, const float* sin_t, const int32_t* pos, const int32_t* bt,
                         void* kc, void* vc, int n_q, int n_kv, int head_dim, int log2P, int max_pos, int n_pages,
                         int n_bt, int rows, hipStream_t st);
-void launch_rmsnorm_rows(const void* x_in, const int64_t* rows, const void* delta, const void* w, void* x_out,
+void launch_rmsnorm_rows(const void* x_in, const int64_t* rows, int n_src, const void* delta, const void* w, void* x_out,
                          void* out, int M, int H, float eps, hipStream_t st);
 
 void launch_argmax_advance(const void* logits, int V, int64_t* tok, int32_t* pos, hipStream_t st);

@@ -30,7 +30,7 @@ SIGNATURES = {
     "dk_gemv_f16_rmsnorm": ([_I, _I, _I, _P, _P, _P, _P, _F, _P, _P, _I, _I, _P], _I),
     "dk_gemm_w4a16": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _P], _I),
     "dk_rope_append_rows": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
-    "dk_rmsnorm_rows": ([_P, _P, _P, _P, _P, _P, _I, _I, _F, _P], _I),
+    "dk_rmsnorm_rows": ([_P, _P, _I, _P, _P, _P, _P, _I, _I, _F, _P], _I),
     "dk_attention_prefill": ([_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P], _I),
     "dk_bw_read": ([_P, _Z, _P, _I, _I, _I, _P], _I),
     "dk_paged_attention": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
@@ -250,8 +250,8 @@ class DecodeKernels:
         if rows is None and x_in.shape != (M, H):
             raise RuntimeError("rmsnorm_rows: without rows x_in must be [M, H]")
         ptr = lambda t: None if t is None else t.data_ptr()
-        self._call(self.lib.dk_rmsnorm_rows, x_in.data_ptr(), ptr(rows), ptr(delta), w.data_ptr(), x_out.data_ptr(),
-                   out.data_ptr(), M, H, float(eps), _stream(out))
+        self._call(self.lib.dk_rmsnorm_rows, x_in.data_ptr(), ptr(rows), x_in.numel() // H, ptr(delta), w.data_ptr(),
+                   x_out.data_ptr(), out.data_ptr(), M, H, float(eps), _stream(out))
 
     # prefill: causal attention of M rows over the paged cache
     def attention_prefill(self, qkv, pos, bt, kc, vc, n_q, n_kv, max_ctx, out):

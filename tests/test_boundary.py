@@ -211,10 +211,11 @@ def test_prefill_validation(lib):
              n_pages=8, n_bt=8), **kw).values(), None))
     assert rr(M=0)[0] == 3 and rr(M=70000)[0] == 3 and rr(D=96)[0] == 3 and rr(page=12)[0] == 4
     assert rr(vc=None)[0] == 1 and rr(n_bt=0)[0] == 3
-    nr = lambda **kw: _err(lib, lib.dk_rmsnorm_rows(*dict(dict(x=A16, rows=None, d=None, w=A16, xo=A16, out=B16, M=4,
-                                                               H=2048, eps=1e-5), **kw).values(), None))
+    nr = lambda **kw: _err(lib, lib.dk_rmsnorm_rows(*dict(dict(x=A16, rows=None, ns=4, d=None, w=A16, xo=A16, out=B16,
+                                                               M=4, H=2048, eps=1e-5), **kw).values(), None))
     assert nr(H=2044)[0] == 3 and nr(M=0)[0] == 3 and nr(out=A16)[0] == 4 and nr(d=A16 + 2)[0] == 2
     assert nr(rows=A16 + 4)[0] == 2 and nr(rows=A16)[0] == 4 and nr(w=None)[0] == 1
+    assert nr(ns=5)[0] == 3 and nr(rows=A16, xo=B16 + 0x1000, ns=0)[0] == 3 and "n_src" in nr(ns=3)[1]
     ap = lambda **kw: _err(lib, lib.dk_attention_prefill(*dict(
         dict(qkv=A16, pos=A16, bt=A16, n_bt=8, kc=A16, vc=A16, n_pages=8, page=16, n_q=32, n_kv=4, D=64, M=8,
              max_ctx=128, out=B16), **kw).values(), None))

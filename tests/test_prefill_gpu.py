@@ -136,6 +136,23 @@ def test_rmsnorm_rows_matches_per_row(K, M, H, gather, with_delta, inplace):
         assert torch.equal(x_in, src)                 # the gathered source is read only
 
 
+def test_rmsnorm_rows_out_of_range_gather_is_nan(K):
+    """A gathered index outside the source rows is not read: that row comes out NaN, the others are unaffected."""
+    H = 256
+    src = torch.randn(10, H, generator=gen(77)).half().to(DEV)
+    rows = torch.tensor([3, 10, -1, 9], device=DEV)
+    w = torch.ones(H, dtype=torch.half, device=DEV)
+    x_out = torch.empty(4, H, dtype=torch.half, device=DEV)
+    out = torch.empty(4, H, dtype=torch.half, device=DEV)
+    K.rmsnorm_rows(src, rows, None, w, x_out, out, 1e-5)
+    assert torch.isnan(x_out[1:3]).all() and torch.isnan(out[1:3]).all()
+    for m, r in ((0, 3), (3, 9)):
+        x = src[r].clone()
+        o = torch.empty(H, dtype=torch.half, device=DEV)
+        K.add_rmsnorm(x, None, w, o, 1e-5)
+        assert torch.equal(x_out[m], x) and torch.equal(out[m], o)
+
+
 # ---------------------------------------------------------------------------------------------------------------
 # causal prefill attention
 
