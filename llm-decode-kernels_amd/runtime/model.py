@@ -455,6 +455,8 @@ class Model:
     def teacher_force(self, tokens, use_graph=True, collect_logits=False):
         """Feed tokens[i] at positions pos..; returns logits [len, V] (fp16) if requested."""
         tokens = torch.as_tensor(tokens, device=self.tok.device).long()
+        if len(tokens) and (int(tokens.min()) < 0 or int(tokens.max()) >= self.V):
+            raise ValueError(f"teacher_force: token ids must lie in [0, {self.V})")  # the step gathers embedding rows
         out = torch.empty(len(tokens), self.V, dtype=torch.half, device=self.tok.device) if collect_logits else None
         for i in range(len(tokens)):
             self.tok.copy_(tokens[i:i + 1])

@@ -318,3 +318,5 @@ def test_prefill_rejects_bad_prompts(K):
     m.reset(0)
     m.prefill([])
     assert m.host_pos == 0
+    with pytest.raises(ValueError, match="token ids"):
+        m.teacher_force([5, -2])
