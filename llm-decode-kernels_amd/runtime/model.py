@@ -8,7 +8,8 @@ Mirrors the reference's ``runtime/model.py`` (DecodeConfig :32-50, Linear :56-72
 
 then the final add_rmsnorm -> LM head -> argmax into the device token slot -> pos += 1. State (token id, position)
 lives in device tensors, so ``step()`` is captured once as a hipGraph (``torch.cuda.CUDAGraph`` on ROCm) and replayed
-for every token. Prefill is teacher-forcing through the same graph, as in the reference.
+for every token. A prompt is either teacher-forced through the same graph, as in the reference, or processed in one
+pass by ``prefill()`` (W4A16 MFMA GEMMs over all prompt rows, causal prefill attention), which leaves the same state.
 
 Differences from the reference, all on the device side of the same composition:
   * head_dim 64 and 128 (TinyLlama and Llama-3-8B shapes);
