@@ -522,7 +522,7 @@ attn_mfma_kernel(const f16* __restrict__ qsrc, const float* __restrict__ cos_t, 
                  int max_pos, const int32_t* __restrict__ pos_ptr, const int32_t* __restrict__ bt, int n_bt,
                  f16* __restrict__ kc, f16* __restrict__ vc, int n_pages, int log2P, int n_q, int n_kv, int PS,
                  int max_splits, float scale, float* __restrict__ o_part, float* __restrict__ m_part,
-                 float* __restrict__ l_part, f16* __restrict__ out, int qstride) {
+                 float* __restrict__ l_part, f16* __restrict__ out) {
   using S = MfmaAttnShape<D>;
   constexpr int KD = S::KD, KW = S::KW, QS = S::QS, VD = S::VD, NB = S::NB, CPL = D / 8;
   __shared__ int s_pg[kAttnMaxSplitPages];
@@ -530,10 +530,6 @@ attn_mfma_kernel(const f16* __restrict__ qsrc, const float* __restrict__ cos_t, 
   __shared__ float s_o[kMfmaWaves][HPG][D];
 
   const int kvh = blockIdx.x, split = blockIdx.y;
-  // prefill: query row z of a batch of tokens at position *pos + z (q rows qstride apart, out rows n_q D apart)
-  const int qrow = blockIdx.z;
-  qsrc += (size_t)qrow * qstride;
-  out += (size_t)qrow * n_q * D;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int col = lane & 15, g = lane >> 4;
   const int P = 1 << log2P;
@@ -625,7 +621,7 @@ attn_mfma_kernel(const f16* __restrict__ qsrc, const float* __restrict__ cos_t, 
   const int k0 = t0 >> 4;  // 16-token tiles, aligned to multiples of 16
   if (reachable) load_round(k0, (int)min(t0l + PS, (long long)n_bt << log2P));
 
-  const int pos = *pos_ptr + qrow;
+  const int pos = *pos_ptr;
   if constexpr (ROPE) {
     if (pos < 0 || pos >= max_pos) return;  // uniform: nothing is touched
 #pragma unroll
@@ -642,8 +638,7 @@ attn_mfma_kernel(const f16* __restrict__ qsrc, const float* __restrict__ cos_t, 
       knew[w] = rope_slice<D>(ko[w], kp[w], cs, sn, c < CPL / 2);
     }
   }
-  const long long cap = (long long)n_bt << log2P;
-  const int ctx = pos < 0 ? 0 : (int)min((long long)pos + 1, cap);
+  const int ctx = attn_context(pos_ptr, n_bt, log2P);
   const int nsplit = attn_splits(ctx, PS, max_splits);
   if (ROPE) {
     // the workgroup owning token pos (or the last live split when the cap is below pos) appends k, v
@@ -807,7 +802,7 @@ void launch_attn(const AttnLaunch& a, hipStream_t st) {
     hipLaunchKernelGGL((attn_mfma_kernel<D, HPG, ROPE>), dim3(a.n_kv, a.max_splits), dim3(kMfmaThreads), 0, st,
                        (const f16*)a.q, a.cos_t, a.sin_t, a.max_pos, a.pos, a.bt, a.n_bt, (f16*)a.kc, (f16*)a.vc,
                        a.n_pages, a.log2P, a.n_q, a.n_kv, a.part_size, a.max_splits, scale, a.o_part, a.m_part,
-                       a.l_part, (f16*)a.out, 0);
+                       a.l_part, (f16*)a.out);
     if (a.max_splits > 1)
       hipLaunchKernelGGL((attn_combine_kernel<D>), dim3(a.n_q), dim3(kAttnThreads), 0, st, a.o_part, a.m_part,
                          a.l_part, a.pos, ROPE ? a.max_pos : 0, a.n_bt, a.log2P, a.part_size, a.max_splits,
