@@ -342,7 +342,9 @@ def main():
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one GPU only: the batch-1 decode path is single-GPU by design and every box here "
-              f"has one GPU (got --gpus {a.gpus}); see DESIGN.md for how the path would shard", file=sys.stderr)
+              f"has one GPU (got --gpus {a.gpus}). Across GPUs the path would shard by tensor parallelism: qkv and "
+              f"gate|up column-parallel, o and down row-parallel with one all-reduce each, attention by kv head",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -159,26 +159,16 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ f4 mfma32(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
 
-#ifndef DK_GEMM_SCHED_FENCE
-#define DK_GEMM_SCHED_FENCE 0
-#endif
-
 // LDS chunk position of 16-byte chunk q (0..7) of row r in the wide kernel's unpadded 128-byte rows. The XOR with
 // (r >> 1) & 7 makes every 16-lane group conflict-free on 64 banks: an operand read (16 consecutive rows, one chunk
 // each) lands on 2 row parities x 8 distinct positions, the X stage (2 rows x 8 chunks) on both parities, the W stage
 // (8 rows x 2 halves, one chunk of each half per store) on 8 distinct positions per parity.
 __device__ __forceinline__ int lds_chunk(int r, int q) { return q ^ ((r >> 1) & 7); }
 
-// Phase fence: nothing moves across it, neither in the IR (the empty asm clobbers memory, so loads are not sunk to
-// their first use) nor in the machine scheduler. The register ring depends on loads being issued where written.
-__device__ __forceinline__ void phase_fence() {
-#if DK_GEMM_SCHED_FENCE
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
-#else
-  asm volatile("" ::: "memory");
-#endif
-}
+// Phase fence: no memory operation moves across it (the empty asm clobbers memory), so the ring's loads are issued
+// where they are written instead of being sunk to their first use, and stay behind the stage's LDS stores. Arithmetic
+// may still be scheduled across it, which lets the dequant interleave with the MFMAs.
+__device__ __forceinline__ void phase_fence() { asm volatile("" ::: "memory"); }
 
 template <int BN, int BM, int PD, int KG, int EPI>
 __global__ void __launch_bounds__(kGemmThreads * KG, KG == 1 ? 2 : 1)
