@@ -28,12 +28,14 @@ def _weights(K, N, Kd, G, seed):
     return packed, sz
 
 
-# kernel coverage: K % 128 == 0 -> register-W kernel (tiles 64x64, 128x64, 128x128 by grid size), K % 128 == 64 ->
-# LDS-W wide kernel, K % 64 == 32 -> 16x16x16 kernel; N % 4 != 0 -> the element-wise epilogue stores
+# kernel coverage: K % 64 == 0 -> the wide kernel, tiles 128 x 128, 128 x 64, 64 x 64 and 1, 2 or 4 K groups by
+# grid size (the last three cases are wide grids at G 64 and 32, one ragged); K % 64 == 32 -> the 16x16x16 kernel;
+# N % 4 != 0 -> the element-wise epilogue stores
 @pytest.mark.parametrize("M,N,Kd,G", [(1, 64, 256, 128), (7, 2560, 2048, 128), (64, 2048, 2048, 64),
                                       (100, 1000, 5632, 128), (512, 11264, 2048, 128), (33, 4096, 4096, 32),
                                       (512, 4096, 1024, 128), (70, 999, 256, 128), (40, 300, 320, 64),
-                                      (300, 4100, 448, 64), (512, 8192, 192, 64), (20, 100, 96, 32)])
+                                      (300, 4100, 448, 64), (512, 8192, 192, 64), (20, 100, 96, 32),
+                                      (256, 32768, 256, 64), (512, 16384, 256, 32), (500, 16400, 192, 64)])
 def test_gemm_matches_oracle(K, M, N, Kd, G):
     packed, sz = _weights(K, N, Kd, G, seed=M + N)
     wref = dequant_from_gpu(packed, sz, G)
@@ -57,7 +59,8 @@ def test_gemm_one_hot_rows_exact(K):
     assert torch.equal(y.cpu(), wref[:, ks].t().contiguous())
 
 
-@pytest.mark.parametrize("M,I,Kd", [(16, 5632, 2048), (130, 512, 256), (1, 64, 1024), (9, 513, 320), (33, 70, 96)])
+@pytest.mark.parametrize("M,I,Kd", [(16, 5632, 2048), (130, 512, 256), (1, 64, 1024), (9, 513, 320), (33, 70, 96),
+                                    (512, 8192, 256)])
 def test_gemm_swiglu_epilogue(K, M, I, Kd):
     from runtime.model import interleave_halves
     G = 128 if Kd % 128 == 0 else (64 if Kd % 64 == 0 else 32)
