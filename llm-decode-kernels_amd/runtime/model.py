@@ -577,6 +577,29 @@ class Model:
         return w["body"] + w["lm_head"] + w["embedding_row"] + self.kv_bytes_per_token(ctx) + self.activation_bytes()
 
 
+def byte_model(shape, ctx, group=128, head="fp16", weights="int4"):
+    """Algorithmic bytes one decode token moves at context ctx, from the shape alone (the byte model of
+    runtime/model.py:289-297 and bench/analyze.py:35-40 of the reference): the projections (INT4: packed N K / 2 plus
+    (scale, zero) 4 N K / G each; fp16: 2 N K) and the two fp16 norm weights of every layer, the LM head (fp16 or
+    INT4), one embedding row, the KV cache read for ctx tokens and written for one, and the fp16 activation vectors.
+    Model.bytes_per_token gives the same total from the built tensors. Returns the parts and "total"."""
+    H, L, I, V = shape.hidden_size, shape.num_hidden_layers, shape.intermediate_size, shape.vocab_size
+    n_q, n_kv = shape.num_attention_heads, shape.num_key_value_heads
+    D = H // n_q
+
+    def lin(N, K, fmt):
+        return N * K // 2 + 4 * N * (K // group) if fmt == "int4" else 2 * N * K
+
+    body = L * (lin((n_q + 2 * n_kv) * D, H, weights) + lin(H, n_q * D, weights) + lin(2 * I, H, weights)
+                + lin(H, I, weights) + 2 * 2 * H)
+    row = n_kv * D * 2
+    parts = {"body": body, "lm_head": lin(V, H, head), "embedding_row": 2 * H,
+             "kv": L * (2 * row * ctx + 2 * row),
+             "activations": 2 * (L * (H * 6 + I * 3 + (n_q + 2 * n_kv) * D) + V)}
+    parts["total"] = sum(parts.values())
+    return parts
+
+
 def rope_tables(max_pos, head_dim, theta=10000.0, device="cpu"):
     """fp32 (cos, sin) [max_pos, head_dim/2] of angles p * theta^(-2i/head_dim) computed in float64
     (reference/ref_ops.py:30-33)."""

@@ -1,0 +1,43 @@
+"""CPU checks of the runtime's host logic: the byte model of the decode step (scope row a10) against the figures the
+reference publishes for its configurations (plots/predictions.json of the reference, as recorded for BASELINE configs 4
+and 5), and the gate/up row interleave the SwiGLU epilogues rely on."""
+import torch
+
+from runtime.model import byte_model, deinterleave_halves, interleave_halves
+from runtime.synth import LLAMA3_8B, TINYLLAMA
+
+
+def test_byte_model_tinyllama_matches_reference_figures():
+    """Config 4: TinyLlama, INT4 G128 body, fp16 LM head: 658,993,664 B per token at context 512, 693,596,672 at
+    2048 (body 514,899,968; head 131,072,000; activations 1,460,736)."""
+    b512, b2k = byte_model(TINYLLAMA, 512), byte_model(TINYLLAMA, 2048)
+    assert b512["body"] == 514_899_968 and b512["lm_head"] == 131_072_000
+    assert b512["activations"] == 1_460_736 and b512["embedding_row"] == 4096
+    assert b512["total"] == 658_993_664 and b2k["total"] == 693_596_672
+
+
+def test_byte_model_llama3_8b_matches_reference_figures():
+    """Config 5: Llama-3-8B body 3,708,289,024 B, LM head INT4 279,085,056 or fp16 1,050,673,152, KV at 4096
+    537,001,984; the byte rooflines at 8 TB/s are 1,766 (INT4 head) and 1,509 (fp16 head) tokens/s."""
+    i4, f16 = byte_model(LLAMA3_8B, 4096, head="int4"), byte_model(LLAMA3_8B, 4096, head="fp16")
+    assert i4["body"] == 3_708_289_024 and i4["kv"] == 537_001_984
+    assert i4["lm_head"] == 279_085_056 and f16["lm_head"] == 1_050_673_152
+    assert round(8e12 / i4["total"]) == 1766 and round(8e12 / f16["total"]) == 1509
+
+
+def test_byte_model_fp16_weights_and_context_scaling():
+    """fp16 projections cost 4 x the INT4 payload without the (scale, zero) words; each context token adds the K and
+    V rows of every layer."""
+    i4, f16 = byte_model(TINYLLAMA, 0), byte_model(TINYLLAMA, 0, weights="fp16")
+    norms = TINYLLAMA.num_hidden_layers * 4 * TINYLLAMA.hidden_size
+    sz = TINYLLAMA.num_hidden_layers * 4 * (2560 * 16 + 2048 * 16 + 11264 * 16 + 2048 * 44)
+    assert f16["body"] - norms == 4 * (i4["body"] - norms - sz)
+    row = TINYLLAMA.num_key_value_heads * (TINYLLAMA.hidden_size // TINYLLAMA.num_attention_heads) * 2
+    assert byte_model(TINYLLAMA, 101)["kv"] - byte_model(TINYLLAMA, 100)["kv"] == 2 * row * TINYLLAMA.num_hidden_layers
+
+
+def test_interleave_halves_round_trip_and_order():
+    t = torch.arange(12 * 3).view(12, 3)
+    il = interleave_halves(t)
+    assert torch.equal(il[0::2], t[:6]) and torch.equal(il[1::2], t[6:])
+    assert torch.equal(deinterleave_halves(il), t)

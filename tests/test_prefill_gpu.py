@@ -310,6 +310,15 @@ def test_prefill_fp16_weights(K):
     assert _rel(m.logits, lr) <= 2e-2
 
 
+@pytest.mark.parametrize("head", ("fp16", "int4"))
+def test_model_bytes_match_byte_model(K, head):
+    """The built model's byte count (tensor sizes) equals the shape-only byte model that the CPU tests pin to the
+    reference's published figures."""
+    from runtime.model import byte_model
+    m, shape = _model(lm_head=head)
+    assert m.bytes_per_token(300) == byte_model(shape, 300, head=head)["total"]
+
+
 def test_prefill_rejects_bad_prompts(K):
     m, _ = _model()
     m.reset(0)
