@@ -22,7 +22,9 @@ Also measured in the same run (extra keys of the JSON line):
                 matvec) on the host cores, a bounded sample of tokens on the same weights.
 
 --gpus N > 1 exits with a message: the path is single-GPU by design (one GPU per box here).
---leg gemv runs only the GEMV roofline leg (used under rocprofv3 for the kernel trace and counter passes).
+--leg gemv runs only the GEMV roofline leg (used under rocprofv3 for the kernel trace and counter passes); --leg
+decode / prefill / decode8b / kernels run one leg alone (the decode and prefill legs without the standalone GEMV and
+kernel legs, so that their traces hold only the model's kernels).
 """
 import argparse
 import json
@@ -370,19 +372,21 @@ def main():
     from runtime.model import DecodeConfig, Model
     from runtime.synth import TINYLLAMA, SyntheticLlama
 
-    # the standalone GEMV legs first, while no model occupies the device (cold weights either way)
-    g1 = gemv_leg(Kx, 4096, 14336)
-    log(f"gemv 4096x14336 {g1['cfg']}: {g1['mean_us']:.3f} us/launch -> {g1['gbps']:.0f} GB/s ({g1['frac']:.1%})")
-    g2 = gemv_leg(Kx, 14336, 4096)
-    log(f"gemv 14336x4096 {g2['cfg']}: {g2['mean_us']:.3f} us/launch -> {g2['gbps']:.0f} GB/s ({g2['frac']:.1%})")
-    g3 = gemv_leg(Kx, 5632, 2048)
-    log(f"gemv 5632x2048 {g3['cfg']}: {g3['mean_us']:.3f} us/launch -> {g3['gbps']:.0f} GB/s ({g3['frac']:.1%})")
-    rc = read_ceiling_leg(Kx, g1["bytes"])
-    log(f"bw_read of {rc['bytes']} B: {rc['mean_us']:.3f} us -> {rc['gbps']:.0f} GB/s ({rc['frac']:.1%})")
-    kern = kernels_leg(Kx)
-    log("attention (cfg2) us: " + ", ".join(f"ctx {c}: ref op {v['paged_attention_v3_us']}, fused {v['attention_decode_us']}"
-                                          for c, v in kern["attention"].items()))
-    log("fused ops (cfg3) us: " + ", ".join(f"{k} {v['us']}" for k, v in kern["fused"].items()))
+    # the standalone GEMV and kernel legs first, while no model occupies the device (cold weights either way); the
+    # decode and prefill legs alone skip them, so that their kernel traces hold only the model's kernels
+    if a.leg == "all":
+        g1 = gemv_leg(Kx, 4096, 14336)
+        log(f"gemv 4096x14336 {g1['cfg']}: {g1['mean_us']:.3f} us/launch -> {g1['gbps']:.0f} GB/s ({g1['frac']:.1%})")
+        g2 = gemv_leg(Kx, 14336, 4096)
+        log(f"gemv 14336x4096 {g2['cfg']}: {g2['mean_us']:.3f} us/launch -> {g2['gbps']:.0f} GB/s ({g2['frac']:.1%})")
+        g3 = gemv_leg(Kx, 5632, 2048)
+        log(f"gemv 5632x2048 {g3['cfg']}: {g3['mean_us']:.3f} us/launch -> {g3['gbps']:.0f} GB/s ({g3['frac']:.1%})")
+        rc = read_ceiling_leg(Kx, g1["bytes"])
+        log(f"bw_read of {rc['bytes']} B: {rc['mean_us']:.3f} us -> {rc['gbps']:.0f} GB/s ({rc['frac']:.1%})")
+        kern = kernels_leg(Kx)
+        log("attention (cfg2) us: " + ", ".join(f"ctx {c}: ref op {v['paged_attention_v3_us']}, fused "
+                                              f"{v['attention_decode_us']}" for c, v in kern["attention"].items()))
+        log("fused ops (cfg3) us: " + ", ".join(f"{k} {v['us']}" for k, v in kern["fused"].items()))
 
     log(f"device {dev_name}; building TinyLlama-shape W4A16 model")
     t0 = time.perf_counter()
