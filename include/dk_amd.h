@@ -235,6 +235,14 @@ int dk_rope_append(void* qkv, const float* cos_t, const float* sin_t, const int3
 int dk_argmax_advance(const void* logits, int V, int64_t* tok, int32_t* pos, void* stream);
 
 /*
+ * The same pick and advance spread over ceil(V / 4096) workgroups (one launch), for large vocabularies: the
+ * workgroups meet through `work`, two uint64 words of device memory that must be zero before the first call and that
+ * every call leaves zero again (calls that overlap on one work buffer race). Same result as dk_argmax_advance,
+ * including ties and NaN. No reference counterpart (runtime/model.py:232-233 is torch.argmax + pos += 1).
+ */
+int dk_argmax_advance_split(const void* logits, int V, int64_t* tok, int32_t* pos, uint64_t* work, void* stream);
+
+/*
  * INT4 format producer on the GPU: round-to-nearest asymmetric group quantization of fp16 W [N, K] and packing,
  * bit-identical to runtime/quant.py quantize (:42-48, RTN branch of group_params :20-28) + pack (:100-109) +
  * pack_scale_zero (:122-124). Writes packed int32 [N, K/8] and sz fp16 [N, K/G, 2].

@@ -17,6 +17,15 @@ __device__ __forceinline__ uint32_t as_u32(f16x2 h) { return __builtin_bit_cast(
 // 16-byte load that bypasses cache retention: weights and KV rows are read once per token.
 __device__ __forceinline__ u32x4 load_stream(const u32x4* p) { return __builtin_nontemporal_load(p); }
 
+// A constant moved into a VGPR behind an empty asm, so the optimiser treats it as a per-lane value. Used for the
+// nibble masks of the INT4 dequant: with the mask and the OR constant both literal the compiler emits v_and_b32 +
+// v_or_b32 (a gfx9 VOP3 instruction takes no literal and at most one scalar operand); with the mask in a VGPR it
+// emits one v_and_or_b32. Build it once, ahead of the loops that use it.
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 // Sum / max over aligned groups of WIDTH consecutive lanes (WIDTH a power of two <= 64); every lane of the group
 // ends with the group result.
 template <int WIDTH>

@@ -413,6 +413,16 @@ int dk_argmax_advance(const void* logits, int V, int64_t* tok, int32_t* pos, voi
   return launched("argmax_advance");
 }
 
+int dk_argmax_advance_split(const void* logits, int V, int64_t* tok, int32_t* pos, uint64_t* work, void* stream) {
+  if (!logits || !tok || !work) return fail(DK_ERR_NULL, "argmax_advance_split: null pointer argument");
+  if (V <= 0) return fail(DK_ERR_SHAPE, "argmax_advance_split: V must be positive, got %d", V);
+  if (!aligned4(tok) || (pos && !aligned4(pos))) return fail(DK_ERR_ALIGN, "tok and pos must be 4B aligned");
+  if (reinterpret_cast<uintptr_t>(work) & 7u) return fail(DK_ERR_ALIGN, "argmax_advance_split: work must be 8B aligned");
+  clear_error();
+  dk::launch_argmax_split(logits, V, tok, pos, reinterpret_cast<unsigned long long*>(work), (hipStream_t)stream);
+  return launched("argmax_advance_split");
+}
+
 int dk_quantize_w4(const void* w, void* packed, void* sz, int N, int K, int group, int clip, void* stream) {
   if (!w || !packed || !sz) return fail(DK_ERR_NULL, "quantize_w4: null pointer argument");
   if (N <= 0 || K <= 0) return fail(DK_ERR_SHAPE, "quantize_w4: N and K must be positive");

@@ -248,6 +248,82 @@ argmax_advance_kernel(const f16* __restrict__ logits, int V, int64_t* __restrict
   }
 }
 
+// The same pick over many workgroups (for large V, where one workgroup's compare work dominates: 128256 logits cost a
+// single CU about 20 us). Every element maps to a 64-bit key that orders as argmax ranks:
+//   high word: 0xFFFFFFFF for NaN, else the float's bits made monotonic (negatives inverted, positives with the sign
+//              bit set; -0 first turned into +0 so that the two zeros tie as they compare equal);
+//   low word:  ~index, so that among equal values the lowest index has the largest key.
+// Workgroup w takes the 16-byte chunks [w * kArgmaxWgChunks, (w + 1) * kArgmaxWgChunks), workgroup 0 also the unaligned
+// head and the tail. Each workgroup folds its best key into work[0] with a device-scope atomic max, waits for that to
+// complete, then counts itself in work[1] with a device-scope atomic add; the workgroup that reads n - 1 arrives last,
+// after every other maximum has been applied: it reads work[0] (device-scope load), writes *tok and *pos + 1, and
+// resets work[0] and work[1] to 0 for the next call. No workgroup waits for another.
+constexpr int kArgmaxWgThreads = 256;
+constexpr int kArgmaxWgChunks = 2 * kArgmaxWgThreads;  // two 16-byte chunks (16 logits) per thread
+
+__device__ __forceinline__ uint64_t argmax_key(float v, int i) {
+  uint32_t hi;
+  if (v != v) {
+    hi = 0xFFFFFFFFu;
+  } else {
+    const uint32_t b = __float_as_uint(v == 0.f ? 0.f : v);
+    hi = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  }
+  return ((uint64_t)hi << 32) | (uint32_t)~(uint32_t)i;
+}
+
+__global__ void __launch_bounds__(kArgmaxWgThreads)
+argmax_split_kernel(const f16* __restrict__ logits, int V, int h, int nc, int64_t* __restrict__ tok,
+                    int32_t* __restrict__ pos, unsigned long long* __restrict__ work) {
+  __shared__ unsigned long long s_k[kArgmaxWgThreads / 64];
+  const int tid = threadIdx.x;
+  unsigned long long best = 0;  // below every key (the smallest key, -inf at index 2^32 - 1, is still above 0)
+  const u32x4* C = reinterpret_cast<const u32x4*>(logits + h);
+  const int c0 = blockIdx.x * kArgmaxWgChunks + tid;
+  u32x4 v[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) v[b] = c0 + b * kArgmaxWgThreads < nc ? C[c0 + b * kArgmaxWgThreads] : u32x4{0u, 0u, 0u, 0u};
+  if (blockIdx.x == 0) {
+    if (tid < h) best = max(best, (unsigned long long)argmax_key((float)logits[tid], tid));
+    const int t0 = h + 8 * nc;
+    if (t0 + tid < V) best = max(best, (unsigned long long)argmax_key((float)logits[t0 + tid], t0 + tid));
+  }
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int c = c0 + b * kArgmaxWgThreads;
+    if (c < nc) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const f16x2 p = as_f16x2(v[b][e]);
+        const int i = h + 8 * c + 2 * e;
+        best = max(best, (unsigned long long)argmax_key((float)p.x, i));
+        best = max(best, (unsigned long long)argmax_key((float)p.y, i + 1));
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) best = max(best, (unsigned long long)__shfl_xor(best, o, kWave));
+  if ((tid & 63) == 0) s_k[tid >> 6] = best;
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < kArgmaxWgThreads / 64; ++w) best = max(best, s_k[w]);
+    // a returning atomic: its value comes back only once the maximum has been applied at device scope, and the empty
+    // asm that consumes it makes the counter add below wait for it
+    const unsigned long long seen = __hip_atomic_fetch_max(&work[0], best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("" ::"v"(seen));
+    __builtin_amdgcn_s_waitcnt(0);
+    const unsigned long long prev =
+        __hip_atomic_fetch_add(&work[1], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev == (unsigned long long)(gridDim.x - 1)) {
+      const unsigned long long k = __hip_atomic_load(&work[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      tok[0] = (int64_t)(uint32_t)~(uint32_t)k;
+      if (pos != nullptr) pos[0] += 1;
+      __hip_atomic_store(&work[0], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&work[1], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
 }  // namespace
 
 void launch_add_rmsnorm(void* x, const void* delta, const void* w, void* out, int H, float eps, hipStream_t st) {
@@ -289,6 +365,15 @@ void launch_rmsnorm_rows(const void* x_in, const int64_t* rows, int n_src, const
 
 void launch_argmax_advance(const void* logits, int V, int64_t* tok, int32_t* pos, hipStream_t st) {
   hipLaunchKernelGGL(argmax_advance_kernel, dim3(1), dim3(1024), 0, st, (const f16*)logits, V, tok, pos);
+}
+
+void launch_argmax_split(const void* logits, int V, int64_t* tok, int32_t* pos, unsigned long long* work,
+                         hipStream_t st) {
+  const int h = min(V, (int)(((16u - ((uint32_t)(uintptr_t)logits & 15u)) & 15u) >> 1));
+  const int nc = (V - h) >> 3;
+  const int blocks = max(1, (nc + kArgmaxWgChunks - 1) / kArgmaxWgChunks);
+  hipLaunchKernelGGL(argmax_split_kernel, dim3(blocks), dim3(kArgmaxWgThreads), 0, st, (const f16*)logits, V, h, nc,
+                     tok, pos, work);
 }
 
 }  // namespace dk

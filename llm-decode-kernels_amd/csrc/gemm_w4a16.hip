@@ -32,18 +32,19 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
 
-// 8 weights of one packed word -> fp16((q - zero) * scale), in element order
-__device__ __forceinline__ u32x4 dequant8(uint32_t word, uint32_t szw) {
+// 8 weights of one packed word -> fp16((q - zero) * scale), in element order; mlo = vgpr_const(0x000F000F) (one
+// v_and_or_b32 per pair)
+__device__ __forceinline__ u32x4 dequant8(uint32_t word, uint32_t szw, uint32_t mlo) {
   const f16x2 sz = as_f16x2(szw);
   const f16x2 s2 = {sz.x, sz.x};
   const f16 zb = (f16)1024.0f + sz.y;            // 1024 + zero, exact (zero is an integer in [0, 15])
   const f16x2 z2 = {zb, zb};
   const uint32_t hi = word >> 8;
   // pairs (e0, e1), (e2, e3), (e4, e5), (e6, e7): nibble i of each 16-bit half
-  const uint32_t p0 = (word & 0x000F000Fu) | 0x64006400u;
-  const uint32_t p1 = ((word >> 4) & 0x000F000Fu) | 0x64006400u;
-  const uint32_t p2 = (hi & 0x000F000Fu) | 0x64006400u;
-  const uint32_t p3 = ((hi >> 4) & 0x000F000Fu) | 0x64006400u;
+  const uint32_t p0 = (word & mlo) | 0x64006400u;
+  const uint32_t p1 = ((word >> 4) & mlo) | 0x64006400u;
+  const uint32_t p2 = (hi & mlo) | 0x64006400u;
+  const uint32_t p3 = ((hi >> 4) & mlo) | 0x64006400u;
   u32x4 r;
   r[0] = as_u32((as_f16x2(p0) - z2) * s2);
   r[1] = as_u32((as_f16x2(p1) - z2) * s2);
@@ -70,6 +71,7 @@ gemm_w4a16_kernel(const uint32_t* __restrict__ W, const uint32_t* __restrict__ S
   const uint32_t* wrow = W + (size_t)wr * KW + sc;
   const uint32_t* szrow = SZ + (size_t)wr * NG;
 
+  const uint32_t mlo = vgpr_const(0x000F000Fu);
   auto fetch = [&](int k0, u32x4& xv, uint32_t& wv, uint32_t& sv) {
     xv = *reinterpret_cast<const u32x4*>(xrow + k0);
     wv = __builtin_nontemporal_load(wrow + (k0 >> 3));
@@ -77,7 +79,7 @@ gemm_w4a16_kernel(const uint32_t* __restrict__ W, const uint32_t* __restrict__ S
   };
   auto stage = [&](int buf, const u32x4& xv, uint32_t wv, uint32_t sv) {
     *reinterpret_cast<u32x4*>(&As[buf][sr][8 * sc]) = xv;
-    *reinterpret_cast<u32x4*>(&Bs[buf][sr][8 * sc]) = dequant8(wv, sv);
+    *reinterpret_cast<u32x4*>(&Bs[buf][sr][8 * sc]) = dequant8(wv, sv, mlo);
   };
 
   f4 acc[2][2];
@@ -213,6 +215,7 @@ gemm_w4a16_wide(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int
   uint32_t wv[PD][WPT], sv[PD];
   // loads are unconditional (threads past 2 BN re-read a valid row, tail fetches re-read the last chunk): loads
   // behind branches make the compiler wait for every outstanding load before a stage, which defeats the ring
+  const uint32_t mlo = vgpr_const(0x000F000Fu);
   auto fetch = [&](int kc, int slot) {
     const int k0 = min(kc, nk - 1) * kWK;
 #pragma unroll
@@ -232,7 +235,7 @@ gemm_w4a16_wide(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int
 #pragma unroll
     for (int i = 0; i < XL; ++i) Xs[kg][buf][xr + 32 * i][lds_chunk(xr + 32 * i, xc)] = xv[slot][i];
 #pragma unroll
-    for (int w = 0; w < WPT; ++w) Ws[kg][buf][wr][lds_chunk(wr, WPT * wq + w)] = dequant8(wv[slot][w], sv[slot]);
+    for (int w = 0; w < WPT; ++w) Ws[kg][buf][wr][lds_chunk(wr, WPT * wq + w)] = dequant8(wv[slot][w], sv[slot], mlo);
   };
 
   f4 acc[TI][TJ];

@@ -5,17 +5,17 @@
 // Dequantized weight w = (q - zero) * scale. A "column" u of a row is one 16-byte chunk = 32 weights = 8 words; a row
 // has U = K / 32 columns.
 //
-// Dequant without a per-weight subtract or multiply: OR-ing a nibble into the mantissa of 0x6400 (fp16 1024) gives
-// the fp16 value 1024 + q exactly, and masking the nibble one position higher (bits 4..7) gives 1024 + 16 q. One
-// v_and_or per pair of weights therefore yields packed fp16 operands for v_dot2_f32_f16 against the fp16 x pairs:
-//     dA = sum (1024 + q) x            over the pairs taken from bits 0..3 / 16..19 of w and of w >> 8
-//     dB = sum (1024 + 16 q) x         over the pairs taken from bits 4..7 / 20..23 of w and of w >> 8
-// With SA, SB the sums of the x values that meet dA resp. dB (computed once per column, shared by the R rows):
-//     sum (q - z) x = dA + dB / 16 - (1024 + z) SA - (64 + z) SB
+// Dequant without a per-weight subtract or multiply: OR-ing a nibble into the low mantissa bits of 0x6400 (fp16 1024,
+// mantissa step 1) gives the fp16 value 1024 + q exactly, and OR-ing the nibble one position higher (bits 4..7) into
+// 0x5400 (fp16 64, mantissa step 1/16) gives 64 + q exactly. One v_and_or per pair of weights therefore yields packed
+// fp16 operands for v_dot2_f32_f16 against the fp16 x pairs, all accumulated in one fp32 chain:
+//     d = sum (1024 + q) x + sum (64 + q) x   (bits 0..3 / 16..19, resp. 4..7 / 20..23, of w and of w >> 8)
+// With SA, SB the sums of the x values that meet the 1024 resp. the 64 offsets (computed once per column, shared by
+// the R rows):  sum (q - z) x = d - 1024 SA - 64 SB - z (SA + SB),
 // and the column adds scale * that to the row's fp32 accumulator. All products and the per-column sums are exact or
 // fp32-rounded, so the result agrees with the fp32 matvec of the fp16-dequantized weight far inside fp16 output
 // precision, and the exact cases (integer x, one-hot x) are reproduced bit for bit.
-// Per 8 weights: 1 shift + 4 v_and_or + 4 v_dot2 (no dequant multiply).
+// Per 8 weights: 1 shift + 4 v_and_or + 4 v_dot2 (no dequant multiply); per row and column 1 FMA + 1 multiply.
 //
 // Kernel family (the reference's ladder, kernels/gemv_w4a16.cu:16-130, re-cut for wave64):
 //   stage 0  gemv_w4a16_exact   one wave per row, per-element fp16 dequant, fp32 FMA (correctness rung).
@@ -38,9 +38,54 @@
 namespace dk {
 namespace {
 
-constexpr uint32_t kMagic = 0x64006400u;  // fp16 pair (1024, 1024)
+constexpr uint32_t kMagic = 0x64006400u;    // fp16 pair (1024, 1024): + q at mantissa bits 0..3
+constexpr uint32_t kMagicHi = 0x54005400u;  // fp16 pair (64, 64): + q at mantissa bits 4..7
 constexpr uint32_t kLoMask = 0x000F000Fu;
 constexpr uint32_t kHiMask = 0x00F000F0u;
+
+// The two nibble masks, held in VGPRs (vgpr_const), so that each pair costs one v_and_or_b32 (mask in the VGPR,
+// the magic constant in an SGPR); the kernels build them once, ahead of their loops.
+struct NibbleMasks {
+  uint32_t lo, hi;
+};
+__device__ __forceinline__ NibbleMasks nibble_masks() { return {vgpr_const(kLoMask), vgpr_const(kHiMask)}; }
+__device__ __forceinline__ f16x2 nibble_pair(uint32_t w, uint32_t mask, uint32_t magic) {
+  return as_f16x2((w & mask) | magic);
+}
+
+// Sums of the x values that meet the 1024 and the 64 offsets of one column and the constant part of the column's
+// result: sum (q - z) x = (d - 1024 SA - 64 SB) - z (SA + SB), so the chain d starts at base = -(1024 SA + 64 SB),
+// computed once per column and shared by every row of it, and each row then needs one FMA and the scale multiply.
+struct ColumnSums {
+  float base, S;
+};
+__device__ __forceinline__ ColumnSums column_sums(const u32x4 (&xc)[4]) {
+  const f16x2 one = {(f16)1.0f, (f16)1.0f};
+  float SA = 0.f, SB = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    SA = dot2(as_f16x2(xc[k].x), one, SA);
+    SA = dot2(as_f16x2(xc[k].z), one, SA);
+    SB = dot2(as_f16x2(xc[k].y), one, SB);
+    SB = dot2(as_f16x2(xc[k].w), one, SB);
+  }
+  return {fmaf(-1024.f, SA, -64.f * SB), SA + SB};
+}
+
+// sum (q - z) x of one row over one column, before the scale: the packed word's 32 weights against xc.
+__device__ __forceinline__ float column_row(const u32x4& w, float z, const u32x4 (&xc)[4], ColumnSums cs,
+                                            NibbleMasks m) {
+  float d = cs.base;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t lo = w[k], hi = lo >> 8;
+    d = dot2(nibble_pair(lo, m.lo, kMagic), as_f16x2(xc[k].x), d);
+    d = dot2(nibble_pair(lo, m.hi, kMagicHi), as_f16x2(xc[k].y), d);
+    d = dot2(nibble_pair(hi, m.lo, kMagic), as_f16x2(xc[k].z), d);
+    d = dot2(nibble_pair(hi, m.hi, kMagicHi), as_f16x2(xc[k].w), d);
+  }
+  return fmaf(-z, cs.S, d);
+}
 
 // ---------------------------------------------------------------------------------------------------------------
 // Stage 0: one wave per row, scalar nibble extraction, per-element dequant rounded to fp16 exactly as
@@ -72,33 +117,12 @@ gemv_w4a16_exact(const uint32_t* __restrict__ W, const uint32_t* __restrict__ SZ
 // One column (32 weights) of R rows against the column's 32 x values (xc[0..3], 8 fp16 each).
 template <int R>
 __device__ __forceinline__ void column_fma(const u32x4 (&w)[R], const uint32_t (&szw)[R], const u32x4 (&xc)[4],
-                                           float (&acc)[R]) {
-  const f16x2 one = {(f16)1.0f, (f16)1.0f};
-  float SA = 0.f, SB = 0.f;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    SA = dot2(as_f16x2(xc[k].x), one, SA);
-    SA = dot2(as_f16x2(xc[k].z), one, SA);
-    SB = dot2(as_f16x2(xc[k].y), one, SB);
-    SB = dot2(as_f16x2(xc[k].w), one, SB);
-  }
+                                           NibbleMasks m, float (&acc)[R]) {
+  const ColumnSums cs = column_sums(xc);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    float dA = 0.f, dB = 0.f;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t lo = w[r][k], hi = lo >> 8;
-      dA = dot2(as_f16x2((lo & kLoMask) | kMagic), as_f16x2(xc[k].x), dA);
-      dB = dot2(as_f16x2((lo & kHiMask) | kMagic), as_f16x2(xc[k].y), dB);
-      dA = dot2(as_f16x2((hi & kLoMask) | kMagic), as_f16x2(xc[k].z), dA);
-      dB = dot2(as_f16x2((hi & kHiMask) | kMagic), as_f16x2(xc[k].w), dB);
-    }
     const f16x2 sz = as_f16x2(szw[r]);
-    const float s = (float)sz.x, z = (float)sz.y;
-    float c = fmaf(dB, 0.0625f, dA);
-    c = fmaf(-(1024.f + z), SA, c);
-    c = fmaf(-(64.f + z), SB, c);
-    acc[r] = fmaf(s, c, acc[r]);
+    acc[r] = fmaf((float)sz.x, column_row(w[r], (float)sz.y, xc, cs, m), acc[r]);
   }
 }
 
@@ -141,6 +165,7 @@ gemv_w4a16_rows(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
   }
   __syncthreads();
 
+  const NibbleMasks m = nibble_masks();
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
@@ -153,7 +178,7 @@ gemv_w4a16_rows(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
       if (u < U) {
         const u32x4* xp = xs + (st << 2) * kWave + lane;
         const u32x4 xc[4] = {xp[0], xp[kWave], xp[2 * kWave], xp[3 * kWave]};
-        column_fma<R>(w[p], s[p], xc, acc);
+        column_fma<R>(w[p], s[p], xc, m, acc);
       }
       const int un = u + P * kWave;
       if (un < U) {
@@ -195,6 +220,7 @@ gemv_w4a16_splitk(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, 
     wrow[r] = W + (size_t)rr * U;
     srow[r] = SZ + (size_t)rr * NG;
   }
+  const NibbleMasks m = nibble_masks();
   float acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0.f;
@@ -210,7 +236,7 @@ gemv_w4a16_splitk(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, 
 #pragma unroll
       for (int r = 0; r < R; ++r) szw[r] = srow[r][u >> gsh];
       __builtin_amdgcn_sched_barrier(0);
-      column_fma<R>(w, szw, xc, acc);
+      column_fma<R>(w, szw, xc, m, acc);
     }
   } else {
     int u = t;
@@ -237,7 +263,7 @@ gemv_w4a16_splitk(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, 
         for (int r = 0; r < R; ++r) szn[r] = srow[r][un >> gsh];
       }
       __builtin_amdgcn_sched_barrier(0);
-      column_fma<R>(w, szw, xc, acc);
+      column_fma<R>(w, szw, xc, m, acc);
 #pragma unroll
       for (int k = 0; k < 4; ++k) xc[k] = xn[k];
 #pragma unroll
@@ -288,25 +314,13 @@ __device__ __forceinline__ void tile_issue(const u32x4* __restrict__ W, const ui
 }
 
 template <int T>
-__device__ __forceinline__ void tile_rows(const u32x4 (&w)[T], const uint32_t (&s)[T], const u32x4 (&xc)[4], float SA,
-                                          float SB, bool live, float (&v)[T]) {
+__device__ __forceinline__ void tile_rows(const u32x4 (&w)[T], const uint32_t (&s)[T], const u32x4 (&xc)[4],
+                                          ColumnSums cs, NibbleMasks m, bool live, float (&v)[T]) {
 #pragma unroll
   for (int r = 0; r < T; ++r) {
-    float dA = 0.f, dB = 0.f;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t lo = w[r][k], hi = lo >> 8;
-      dA = dot2(as_f16x2((lo & kLoMask) | kMagic), as_f16x2(xc[k].x), dA);
-      dB = dot2(as_f16x2((lo & kHiMask) | kMagic), as_f16x2(xc[k].y), dB);
-      dA = dot2(as_f16x2((hi & kLoMask) | kMagic), as_f16x2(xc[k].z), dA);
-      dB = dot2(as_f16x2((hi & kHiMask) | kMagic), as_f16x2(xc[k].w), dB);
-    }
     const f16x2 sz = as_f16x2(s[r]);
-    const float sc = (float)sz.x, z = (float)sz.y;
-    float c = fmaf(dB, 0.0625f, dA);
-    c = fmaf(-(1024.f + z), SA, c);
-    c = fmaf(-(64.f + z), SB, c);
-    const float part = live ? sc * c : 0.f;  // dead lanes (u >= U) contribute 0; the DPP sum runs on all lanes
+    const float c = column_row(w[r], (float)sz.y, xc, cs, m);
+    const float part = live ? (float)sz.x * c : 0.f;  // dead lanes (u >= U) contribute 0; the DPP sum runs on all lanes
     v[r] = wave_sum_lane63(part);
   }
 }
@@ -464,19 +478,12 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
   __builtin_amdgcn_sched_barrier(0);
   u32x4 xc[4];
   tile_input_finish<PRO>(in, raw, uc, live, U << 5, s_ss, wave, nw, xc);
-  const f16x2 one = {(f16)1.0f, (f16)1.0f};
-  float SA = 0.f, SB = 0.f;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    SA = dot2(as_f16x2(xc[k].x), one, SA);
-    SA = dot2(as_f16x2(xc[k].z), one, SA);
-    SB = dot2(as_f16x2(xc[k].y), one, SB);
-    SB = dot2(as_f16x2(xc[k].w), one, SB);
-  }
+  const ColumnSums cs = column_sums(xc);
+  const NibbleMasks m = nibble_masks();
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     float v[T];
-    tile_rows<T>(w[t % DP], sz[t % DP], xc, SA, SB, live, v);
+    tile_rows<T>(w[t % DP], sz[t % DP], xc, cs, m, live, v);
     if (t + DP < NT) tile_issue<T>(W, SZ, base + (t + DP) * T, N, U, NG, uc, gsh, w[t % DP], sz[t % DP]);
     __builtin_amdgcn_sched_barrier(0);
     if (lane == 63) {

@@ -90,6 +90,8 @@ void launch_rmsnorm_rows(const void* x_in, const int64_t* rows, int n_src, const
                          void* out, int M, int H, float eps, hipStream_t st);
 
 void launch_argmax_advance(const void* logits, int V, int64_t* tok, int32_t* pos, hipStream_t st);
+void launch_argmax_split(const void* logits, int V, int64_t* tok, int32_t* pos, unsigned long long* work,
+                         hipStream_t st);
 
 void launch_quantize_w4(const void* w, void* packed, void* sz, int N, int K, int log2G, int clip, hipStream_t st);
 

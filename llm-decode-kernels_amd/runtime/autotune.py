@@ -103,13 +103,25 @@ def tune_fused_shape(Kx, kind, N, K, G, reps=5, log=print):
     recs = []
     for cfg in cands:
         _, med = graph_time(lambda i: call(cfg, i), cold.copies, reps)
-        recs.append({"N": N, "K": K, "G": G, "cfg": list(cfg), "median_us": med, "variant": kind,
-                     "gbps": nb / med / 1e3})
-    best = min(recs, key=lambda r: r["median_us"])
+        recs.append({"N": N, "K": K, "G": G, "cfg": list(cfg), "median_us": med, "variant": kind})
+    best = confirm(recs, lambda c: graph_time(lambda i: call(c, i), cold.copies, reps)[1])
+    for r in recs:
+        r["gbps"] = nb / r["median_us"] / 1e3
     log(f"  {kind} {N}x{K}: best {best['cfg']} {best['median_us']:.2f} us {best['gbps']:.0f} GB/s; "
         f"{len(recs)} configs")
     del cold
     return best, recs
+
+
+def confirm(recs, measure, top=5, rounds=3):
+    """Re-time the `top` fastest candidates in `rounds` interleaved passes and keep each one's best median: a single
+    pass over tens of configurations picks an outlier now and then (a 1 us slip at a 14 us shape is within one pass's
+    spread), and the runtime then pays for it in every layer of every token."""
+    lead = sorted(recs, key=lambda r: r["median_us"])[:top]
+    for _ in range(rounds):
+        for r in lead:
+            r["median_us"] = min(r["median_us"], measure(tuple(r["cfg"])))
+    return min(recs, key=lambda r: r["median_us"])
 
 
 def gemv_bytes(N, K, G):
@@ -126,10 +138,14 @@ def tune_shape(Kx, N, K, G, reps=5, log=print):
     recs = []
     for cfg in candidates(N, K):
         mn, med = graph_time(lambda i: Kx.gemv_w4a16(*cfg, *cold[i], x, y, G), cold.copies, reps)
-        recs.append({"N": N, "K": K, "G": G, "cfg": list(cfg), "min_us": mn, "median_us": med,
-                     "gbps": nb / med / 1e3})
+        recs.append({"N": N, "K": K, "G": G, "cfg": list(cfg), "min_us": mn, "median_us": med})
+    best = confirm(recs, lambda c: graph_time(lambda i: Kx.gemv_w4a16(*c, *cold[i], x, y, G), cold.copies, reps)[1])
+    tiles = sorted((r for r in recs if r["cfg"][0] == 4), key=lambda r: r["median_us"])
+    if tiles and tiles[0] is not best:  # the best row-tile entry is a table of its own: confirm it the same way
+        confirm(tiles, lambda c: graph_time(lambda i: Kx.gemv_w4a16(*c, *cold[i], x, y, G), cold.copies, reps)[1])
+    for r in recs:
+        r["gbps"] = nb / r["median_us"] / 1e3
     del cold
-    best = min(recs, key=lambda r: r["median_us"])
     log(f"  {N}x{K} G{G}: best {best['cfg']} {best['median_us']:.2f} us {best['gbps']:.0f} GB/s "
         f"({best['gbps'] / 80:.1f}% of 8 TB/s); {len(recs)} configs")
     return best, recs

@@ -40,6 +40,7 @@ SIGNATURES = {
     "dk_swiglu": ([_P, _P, _I, _P], _I),
     "dk_rope_append": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "dk_argmax_advance": ([_P, _I, _P, _P, _P], _I),
+    "dk_argmax_advance_split": ([_P, _I, _P, _P, _P, _P], _I),
     "dk_quantize_w4": ([_P, _P, _P, _I, _I, _I, _I, _P], _I),
 }
 
@@ -401,6 +402,25 @@ class DecodeKernels:
             _check_dtype(pos, torch.int32, "pos")
             p = pos.data_ptr()
         self._call(self.lib.dk_argmax_advance, logits.data_ptr(), logits.numel(), tok.data_ptr(), p, _stream(logits))
+
+    def argmax_advance_split(self, logits, tok, pos, work):
+        """argmax_advance over ceil(V / 4096) workgroups that meet through `work` (int64 [2], zero before the first
+        call, left zero by every call; one work buffer per stream of calls)."""
+        _check_cuda(logits, "logits")
+        _check_cuda(tok, "tok")
+        _check_cuda(work, "work")
+        _check_dtype(logits, torch.float16, "logits")
+        _check_dtype(tok, torch.int64, "tok")
+        _check_dtype(work, torch.int64, "work")
+        if work.numel() != 2:
+            raise RuntimeError("argmax_advance_split: work must be int64 [2]")
+        p = None
+        if pos is not None:
+            _check_cuda(pos, "pos")
+            _check_dtype(pos, torch.int32, "pos")
+            p = pos.data_ptr()
+        self._call(self.lib.dk_argmax_advance_split, logits.data_ptr(), logits.numel(), tok.data_ptr(), p,
+                   work.data_ptr(), _stream(logits))
 
     # runtime/quant.py:42-48,100-124 on the GPU
     def quantize_w4(self, w, packed, sz, group, clip=False):

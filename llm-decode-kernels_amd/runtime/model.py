@@ -63,6 +63,8 @@ class DecodeConfig:
     combine_in_split: bool = False # with fused_attention: the last split workgroup of each kv head merges the
                                    # partials (per-kv-head counters) instead of a second combine launch; its three
                                    # device-coherent round trips cost what the second launch costs on MI355X
+    argmax_split_min_v: int = 16384  # vocabularies at least this large pick the next token with the multi-workgroup
+                                     # argmax (dk_argmax_advance_split); smaller ones with the one-workgroup kernel
     fused_gemv: bool = True        # residual + RMSNorm (and the embedding gather) computed inside the INT4 GEMV that
                                    # consumes it (dk_gemv_w4a16_rmsnorm) instead of a separate add_rmsnorm kernel
     f16_gemv: bool = True          # fp16-weight projections with K <= 4096 (the fp16 LM head) on the HIP fp16 GEMV
@@ -209,6 +211,8 @@ class Model:
         self.act = torch.empty(self.I, **h16)
         self.down = torch.empty(self.H, **h16)
         self.logits = torch.empty(self.V, **h16)
+        # meeting point of the multi-workgroup argmax: zero here, left zero by every launch
+        self.argmax_work = torch.zeros(2, dtype=torch.int64, device=self.cfg.device)
         self.graph = None
         self.host_pos = 0
 
@@ -346,6 +350,13 @@ class Model:
         else:
             self.act.copy_(torch.nn.functional.silu(self.gu[: self.I].float()).half() * self.gu[self.I:])
 
+    def pick_next(self):
+        """tok <- argmax(logits), pos += 1 (runtime/model.py:232-233) in one launch."""
+        if self.V >= self.cfg.argmax_split_min_v:
+            self.K.argmax_advance_split(self.logits, self.tok, self.pos, self.argmax_work)
+        else:
+            self.K.argmax_advance(self.logits, self.tok, self.pos)
+
     def attention(self, li):
         kc, vc = self.kv[li, 0], self.kv[li, 1]
         if self.cfg.fused_attention:
@@ -378,7 +389,7 @@ class Model:
             delta = self.down
         self.add_norm(delta, self.norm_f)
         self.linear(self.lm_head, self.normed, self.logits)
-        self.K.argmax_advance(self.logits, self.tok, self.pos)
+        self.pick_next()
 
     def step_fused(self):
         """The same composition with every residual + RMSNorm inside the GEMV that consumes it (the layer-0 one also
@@ -419,7 +430,7 @@ class Model:
         else:
             self.K.add_rmsnorm(cur, delta, self.norm_f, self.normed, self.eps)
             self.linear(self.lm_head, self.normed, self.logits)
-        self.K.argmax_advance(self.logits, self.tok, self.pos)
+        self.pick_next()
 
     def capture(self):
         """Capture step() into a hipGraph after warm-up on a side stream (runtime/model.py:235-251)."""
@@ -541,7 +552,7 @@ class Model:
         self.linear(self.lm_head, xn[M - 1], self.logits)
         if M > 1:
             self.pos.add_(M - 1)
-        self.K.argmax_advance(self.logits, self.tok, self.pos)
+        self.pick_next()
         self.host_pos = start + M
 
     def generate(self, prompt, n_new, use_graph=True, prefill=False):

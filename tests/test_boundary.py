@@ -193,6 +193,9 @@ def test_small_op_validation(lib):
     assert rope(D=80)[0] == 3 and rope(page=10)[0] == 4 and rope(max_pos=0)[0] == 3 and rope(bt=None)[0] == 1
     assert _err(lib, lib.dk_argmax_advance(A16, 0, A16, A16, None))[0] == 3
     assert _err(lib, lib.dk_argmax_advance(None, 10, A16, A16, None))[0] == 1
+    assert _err(lib, lib.dk_argmax_advance_split(A16, 0, A16, A16, A16, None))[0] == 3
+    assert _err(lib, lib.dk_argmax_advance_split(A16, 10, A16, A16, None, None))[0] == 1
+    assert _err(lib, lib.dk_argmax_advance_split(A16, 10, A16, A16, A16 + 4, None))[0] == 2
     q = lambda **kw: _err(lib, lib.dk_quantize_w4(*dict(dict(w=A16, p=A16, sz=A16, N=4, K=256, G=128, clip=0),
                                                         **kw).values(), None))
     assert q(G=1024)[0] == 4 and q(G=48)[0] == 4 and q(K=192)[0] == 3 and q(w=A16 + 2)[0] == 2

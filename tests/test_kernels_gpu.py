@@ -337,6 +337,61 @@ def test_argmax_edges(K, V, offset):
         assert int(tok) == int(torch.argmax(c[offset:].float())), (V, offset)
 
 
+@pytest.mark.parametrize("V", (1, 5, 9, 4095, 4096, 4097, 31999, 32000, 128256))
+@pytest.mark.parametrize("offset", (0, 3))
+def test_argmax_split(K, V, offset):
+    """The multi-workgroup pick against torch.argmax on the CPU and against the one-workgroup kernel: the cases of
+    test_argmax_edges plus maxima on workgroup borders (4096 logits each) and exact ties across workgroups; the work
+    buffer is zero again after every call, so back-to-back calls (and graph replays) start clean."""
+    base = torch.randn(V + offset, generator=gen(V * 16 + offset)).half()
+    cases = [base.clone()]
+    for where in (0, V - 1, V // 2, min(V - 1, 4095), min(V - 1, 4096)):
+        t = base.clone()
+        t[offset + where] = 60.0
+        cases.append(t)
+    t = base.clone()
+    for where in (V - 1, V // 3, min(V - 1, 4100)):
+        t[offset + where] = 61.0                    # ties across workgroups: the lowest index wins
+    cases.append(t)
+    t = base.clone()
+    t[offset + V - 1] = float("nan")
+    t[offset + V // 3] = float("nan")
+    cases.append(t)
+    t = torch.full((V + offset,), -0.0, dtype=torch.half)
+    t[offset + V - 1] = 0.0                         # -0 and +0 compare equal: index 0 wins
+    cases.append(t)
+    cases.append(torch.full((V + offset,), float("-inf"), dtype=torch.half))
+    tok, tok1 = (torch.zeros(1, dtype=torch.long, device=DEV) for _ in range(2))
+    pos = torch.tensor([7], dtype=torch.int32, device=DEV)
+    work = torch.zeros(2, dtype=torch.long, device=DEV)
+    for i, c in enumerate(cases):
+        dev = c.to(DEV)[offset:]
+        K.argmax_advance_split(dev, tok, pos, work)
+        K.argmax_advance(dev, tok1, None)
+        want = int(torch.argmax(c[offset:].float()))
+        assert int(tok) == want == int(tok1), (V, offset, i)
+        assert int(pos) == 8 + i and not work.any()
+
+
+def test_argmax_split_in_graph(K):
+    """Captured once, replayed with new logits between replays: every replay picks anew (the work buffer resets)."""
+    V = 128256
+    logits = torch.randn(V, device=DEV).half()
+    tok = torch.zeros(1, dtype=torch.long, device=DEV)
+    pos = torch.zeros(1, dtype=torch.int32, device=DEV)
+    work = torch.zeros(2, dtype=torch.long, device=DEV)
+    K.argmax_advance_split(logits, tok, pos, work)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        K.argmax_advance_split(logits, tok, pos, work)
+    for r in range(5):
+        logits.copy_(torch.randn(V, generator=gen(r)).half().to(DEV))
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(tok) == int(torch.argmax(logits.float().cpu())) and int(pos) == 2 + r and not work.any()
+
+
 def test_graph_replay_of_ops(K):
     """rope -> attention -> GEMV captured into one hipGraph; each replay (with eager work between replays) equals the
     eager result, and the graph reads the device-resident position anew on every replay."""
