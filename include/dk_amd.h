@@ -164,8 +164,8 @@ int dk_bw_read(const void* buf, size_t bytes, void* sink, int blocks, int thread
 
 /*
  * Paged split-K GQA decode attention for one query token at ctx = *pos + 1 (device int32). version 1-3: the block
- * kernel (the reference's three kernel versions share one MI355X kernel); version 4: the MFMA kernel (see
- * dk_attention_decode's impl 2).
+ * kernel (the reference's three kernel versions share one MI355X kernel); version 4: the MFMA kernel, version 5: the
+ * lean MFMA kernel (see dk_attention_decode's impl 2 and 3).
  * Replaces paged_attention (kernels/bindings.cpp:45-62) -> paged_attention_launch (kernels/paged_attention.cu:429-461).
  * Grid = n_kv x max_splits workgroups; split s covers tokens [s*part_size, (s+1)*part_size) of the live context;
  * splits past ceil(ctx/part_size) exit; with one live split the output is written directly, otherwise each split
@@ -192,7 +192,9 @@ int dk_paged_attention(int version, const void* q, const void* kc, const void* v
  * uint32 [n_kv], zero before the first call (every call leaves them zero): when 1 < max_splits <= 64 the split
  * workgroup of each kv head that finishes last merges its partials (one launch in all); calls that share counters
  * must not run concurrently. impl selects the split kernel: 0 or 1 = the block kernel (v_dot2 scores, LDS p.V),
- * 2 = the MFMA kernel (16 x 16 f16 tiles; needs ((part_size - 1) >> log2(page)) + 2 <= 1024 and counters == NULL).
+ * 2 = the MFMA kernel (16 x 16 f16 tiles; needs ((part_size - 1) >> log2(page)) + 2 <= 1024 and counters == NULL),
+ * 3 = the lean MFMA kernel (scalar page lookups, one memory round trip for K / V; needs page >= 16, part_size a
+ * multiple of 16 up to 512 and counters == NULL).
  * The runtime picks impl and part_size per context from its measured policy table. If *pos is outside [0, max_pos)
  * nothing is touched. Other arguments and limits as dk_rope_append / dk_paged_attention.
  */

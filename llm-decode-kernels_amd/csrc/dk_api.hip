@@ -244,10 +244,13 @@ int dk_paged_attention(int version, const void* q, const void* kc, const void* v
     return fail(DK_ERR_SHAPE, "heads-per-group must be 1/2/4/8, got %d", hpg);
   if (!pow2(page)) return fail(DK_ERR_DOMAIN, "page size must be a power of two, got %d", page);
   if (part_size <= 0) return fail(DK_ERR_DOMAIN, "part_size must be > 0");
-  if (version < 1 || version > 4) return fail(DK_ERR_DOMAIN, "attention version must be 1, 2, 3 or 4");
+  if (version < 1 || version > 5) return fail(DK_ERR_DOMAIN, "attention version must be 1, 2, 3, 4 or 5");
   if (version == 4 && !dk::attn_mfma_fits(part_size, ilog2(page)))
     return fail(DK_ERR_DOMAIN, "paged_attention: version 4 stages at most %d block-table pages per split "
                 "(part_size %d, page %d)", dk::kAttnMaxSplitPages, part_size, page);
+  if (version == 5 && !dk::attn_lean_fits(part_size, ilog2(page), head_dim))
+    return fail(DK_ERR_DOMAIN, "paged_attention: version 5 needs pages of >= 16 tokens and a part_size that is a "
+                "multiple of 16 up to %d (part_size %d, page %d)", dk::attn_lean_max_part(head_dim), part_size, page);
   if (max_splits < 1 || max_splits > 65535)
     return fail(DK_ERR_SHAPE, "paged_attention: max_splits must be 1..65535, got %d", max_splits);
   if (n_pages < 1 || n_bt < 1) return fail(DK_ERR_SHAPE, "paged_attention: empty cache or block table");
@@ -258,7 +261,7 @@ int dk_paged_attention(int version, const void* q, const void* kc, const void* v
   clear_error();
   const dk::AttnLaunch a{q, nullptr, nullptr, 0, pos, bt, n_bt, const_cast<void*>(kc), const_cast<void*>(vc), n_pages,
                          ilog2(page), n_q, n_kv, head_dim, part_size, max_splits, o_part, m_part, l_part, out,
-                         nullptr, version == 4 ? 2 : 1};
+                         nullptr, version == 5 ? 3 : version == 4 ? 2 : 1};
   dk::launch_paged_attention(a, (hipStream_t)stream);
   return launched("paged_attention");
 }
@@ -271,8 +274,8 @@ int dk_attention_decode(const void* qkv, const float* cos_t, const float* sin_t,
     return fail(DK_ERR_NULL, "attention_decode: null pointer argument");
   if (counters && (reinterpret_cast<uintptr_t>(counters) & 3u))
     return fail(DK_ERR_ALIGN, "attention_decode: counters must be 4B aligned");
-  if (impl < 0 || impl > 2) return fail(DK_ERR_DOMAIN, "attention_decode: impl must be 0, 1 or 2, got %d", impl);
-  if (impl == 2 && counters)
+  if (impl < 0 || impl > 3) return fail(DK_ERR_DOMAIN, "attention_decode: impl must be 0, 1, 2 or 3, got %d", impl);
+  if (impl >= 2 && counters)
     return fail(DK_ERR_DOMAIN, "attention_decode: the in-split combine (counters) belongs to impl 1");
   if (head_dim != 64 && head_dim != 128)
     return fail(DK_ERR_SHAPE, "attention_decode: head_dim must be 64 or 128, got %d", head_dim);
@@ -295,6 +298,9 @@ int dk_attention_decode(const void* qkv, const float* cos_t, const float* sin_t,
   if (impl == 2 && !dk::attn_mfma_fits(part_size, ilog2(page)))
     return fail(DK_ERR_DOMAIN, "attention_decode: impl 2 stages at most %d block-table pages per split "
                 "(part_size %d, page %d)", dk::kAttnMaxSplitPages, part_size, page);
+  if (impl == 3 && !dk::attn_lean_fits(part_size, ilog2(page), head_dim))
+    return fail(DK_ERR_DOMAIN, "attention_decode: impl 3 needs pages of >= 16 tokens and a part_size that is a "
+                "multiple of 16 up to %d (part_size %d, page %d)", dk::attn_lean_max_part(head_dim), part_size, page);
   const dk::AttnLaunch a{qkv, cos_t, sin_t, max_pos, pos, bt, n_bt, kc, vc, n_pages, ilog2(page), n_q, n_kv,
                          head_dim, part_size, max_splits, o_part, m_part, l_part, out, counters, impl};
   dk::launch_attention_decode(a, (hipStream_t)stream);

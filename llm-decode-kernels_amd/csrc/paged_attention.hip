@@ -795,9 +795,320 @@ attn_mfma_kernel(const f16* __restrict__ qsrc, const float* __restrict__ cos_t, 
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Lean MFMA split kernel (impl 3) for pages of at least 16 tokens: the arithmetic of the MFMA kernel above (16 x 16
+// f16 tiles, p as fp16 hi + lo parts) with a schedule cut down to two dependent memory round trips:
+//   * every kernel argument is read into scalar registers at entry (left to itself the compiler loads some of them
+//     only where they are first used, and each such late load is one more round trip on the critical path);
+//   * each wave owns NT 16-token tiles of the split (tile j = wave + NW i); a tile lies in one page, so its page is a
+//     wave-uniform scalar load, issued at entry together with *pos -- no block-table staging and no barrier;
+//   * then the q slices (for RoPE also their partners and the new k / v), then, once the pages are in, K and V of all
+//     the wave's tiles at once, then the RoPE tables of *pos;
+//   * one online-softmax round per wave, one LDS merge of the NW waves (the per-head weights computed once).
+// The reduction index of QK^T is split so that the 16-byte K load w of lane (g, c) reads dims 8 (4 w + g) .. + 8 of
+// its token row: the four lanes g of a token read 64 contiguous bytes per load (the q operand uses the same
+// bijection), which halves the cache lines one K load touches at head_dim 128. Splits, partials, output and the
+// RoPE / append behaviour are those of the block kernel.
+constexpr int kLeanMaxWaves = 8;
+
+template <int D, int HPG, bool ROPE, int NW, int NT>
+__global__ void __launch_bounds__(NW * kWave)
+attn_lean_kernel(const f16* __restrict__ qsrc, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                 int max_pos, const int32_t* __restrict__ pos_ptr, const int32_t* __restrict__ bt, int n_bt,
+                 f16* __restrict__ kc, f16* __restrict__ vc, int n_pages, int log2P, int n_q, int n_kv, int PS,
+                 int max_splits, float scale, float* __restrict__ o_part, float* __restrict__ m_part,
+                 float* __restrict__ l_part, f16* __restrict__ out) {
+  using S = MfmaAttnShape<D>;
+  constexpr int KW = S::KW, QS = S::QS, VD = S::VD, CPL = D / 8;
+  __shared__ float s_m[NW][HPG], s_l[NW][HPG], s_w[NW][HPG];
+  __shared__ float s_o[NW][HPG][D];
+
+  const int kvh = blockIdx.x, split = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, g = lane >> 4;
+  const int P = 1 << log2P;
+  const long long t0l = (long long)split * PS;
+  const bool reachable = t0l < ((long long)n_bt << log2P);
+  const int t0 = reachable ? (int)t0l : 0;
+
+  // ---- scalar loads: the position and the page of each of this wave's tiles (independent of the position)
+  const int pos = *pos_ptr;
+  int pg[NT];
+#pragma unroll
+  for (int i = 0; i < NT; ++i) {
+    const int tl = (wave + NW * i) << 4;  // tile start within the split
+    const int lp = (t0 + tl) >> log2P;
+    const bool in = reachable && tl < PS && lp < n_bt;
+    const int e = bt[in ? lp : 0];
+    pg[i] = (in && e >= 0 && e < n_pages) ? e : -1;
+  }
+  // every other argument into scalar registers now (see above). After the two lookups: an asm statement counts as
+  // a possible memory write, and loads after it are no longer issued as scalar loads.
+  asm volatile("" ::"s"(qsrc), "s"(cos_t), "s"(sin_t), "s"(max_pos), "s"(kc), "s"(vc), "s"(n_q), "s"(n_kv),
+               "s"(max_splits), "s"(scale), "s"(o_part), "s"(m_part), "s"(l_part), "s"(out));
+  // ---- q operand (head col of the group, zero for col >= HPG): slice 4 w + g of the head for word group w; for RoPE
+  // the partner slices and the new k (same slices) and v (dims VD col ..)
+  const bool qlive = col < HPG;
+  const f16* qh = qsrc + (size_t)(kvh * HPG + (qlive ? col : 0)) * D;
+  u32x4 qr[KW], knew[KW];
+  VRow<VD> vnew{};
+#pragma unroll
+  for (int w = 0; w < KW; ++w) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(qh + 8 * (4 * w + g));
+    qr[w] = qlive ? v : u32x4{0u, 0u, 0u, 0u};
+    knew[w] = u32x4{0u, 0u, 0u, 0u};
+  }
+  u32x4 qp[KW], ko[KW], kp[KW];
+  if constexpr (ROPE) {
+    const f16* kh = qsrc + (size_t)(n_q + kvh) * D;
+    const f16* vh = qsrc + (size_t)(n_q + n_kv + kvh) * D;
+#pragma unroll
+    for (int w = 0; w < KW; ++w) {
+      const int c = 4 * w + g, pc = (c + CPL / 2) % CPL;
+      qp[w] = *reinterpret_cast<const u32x4*>(qh + 8 * pc);
+      ko[w] = *reinterpret_cast<const u32x4*>(kh + 8 * c);
+      kp[w] = *reinterpret_cast<const u32x4*>(kh + 8 * pc);
+    }
+#pragma unroll
+    for (int i = 0; i < VD / 2; ++i) vnew.w[i] = reinterpret_cast<const uint32_t*>(vh + VD * col)[i];
+  }
+  // ---- K / V of every tile of the wave: K row col, V rows 4 g + v (speculative past the context: masked below)
+  auto row_off = [&](int page, int t) -> size_t {
+    return ((((size_t)page * n_kv + kvh) << log2P) + (t & (P - 1))) * D;
+  };
+  u32x4 kr[NT][KW];
+  VRow<VD> vr[NT][4];
+#pragma unroll
+  for (int i = 0; i < NT; ++i) {
+    const int ts = t0 + ((wave + NW * i) << 4);
+    if (pg[i] >= 0) {  // uniform per wave
+#pragma unroll
+      for (int w = 0; w < KW; ++w)
+        kr[i][w] = load_stream(reinterpret_cast<const u32x4*>(kc + row_off(pg[i], ts + col) + 8 * (4 * w + g)));
+#pragma unroll
+      for (int v = 0; v < 4; ++v) vr[i][v] = load_vrow<VD>(vc + row_off(pg[i], ts + 4 * g + v) + VD * col);
+    } else {
+#pragma unroll
+      for (int w = 0; w < KW; ++w) kr[i][w] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+#pragma unroll
+        for (int k = 0; k < VD / 2; ++k) vr[i][v].w[k] = 0u;
+      }
+    }
+  }
+  if constexpr (ROPE) {
+    if (pos < 0 || pos >= max_pos) return;  // uniform: nothing is touched
+#pragma unroll
+    for (int w = 0; w < KW; ++w) {
+      const int c = 4 * w + g;
+      const int ti = (8 * c) % (D / 2);
+      float cs[8], sn[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        cs[e] = cos_t[(size_t)pos * (D / 2) + ti + e];
+        sn[e] = sin_t[(size_t)pos * (D / 2) + ti + e];
+      }
+      qr[w] = qlive ? rope_slice<D>(qr[w], qp[w], cs, sn, c < CPL / 2) : qr[w];
+      knew[w] = rope_slice<D>(ko[w], kp[w], cs, sn, c < CPL / 2);
+    }
+  }
+  const long long cap = (long long)n_bt << log2P;
+  const int ctx = (int)((long long)pos + 1 < cap ? (long long)pos + 1 : cap);
+  const int nsplit = attn_splits(ctx, PS, max_splits);
+  if (ROPE) {
+    // the workgroup owning token pos (or the last live split when the cap is below pos) appends k, v
+    const int owner = min(pos / PS, nsplit - 1);
+    if (split == owner && wave == 0) {
+      const int lp = pos >> log2P;
+      const int page = lp < n_bt ? bt[lp] : -1;
+      if (page >= 0 && page < n_pages) {
+        const size_t row = row_off(page, pos);
+        if (col == 0) {
+#pragma unroll
+          for (int w = 0; w < KW; ++w) *reinterpret_cast<u32x4*>(kc + row + 8 * (4 * w + g)) = knew[w];
+        }
+        if (g == 0) {
+#pragma unroll
+          for (int i = 0; i < VD / 2; ++i) reinterpret_cast<uint32_t*>(vc + row + VD * col)[i] = vnew.w[i];
+        }
+      }
+    }
+  }
+  if (split >= nsplit || !reachable) return;  // uniform per workgroup
+  const int t1 = (int)min((long long)ctx, t0l + PS);
+  const bool pos_here = ROPE && pos >= t0 && pos < t1;  // this split attends token pos (its slot has a page)
+
+  // ---- scores of all the wave's tiles: sc[i][v] = score of token ts_i + 4 g + v for head col
+  f4 sc[NT];
+  float rmax = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < NT; ++i) {
+    const int ts = t0 + ((wave + NW * i) << 4);
+    const bool tile = pg[i] >= 0;
+    if constexpr (ROPE) {  // the slot of pos is being written by this launch: use the fresh k, v
+      if (pos_here && tile && ts + col == pos) {
+#pragma unroll
+        for (int w = 0; w < KW; ++w) kr[i][w] = knew[w];
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (pos_here && tile && ts + 4 * g + v == pos) vr[i][v] = vnew;
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {  // rows past the context: zero V (a stale row must not reach p . V as NaN)
+      const bool keep = tile && ts + 4 * g + v < t1;
+#pragma unroll
+      for (int k = 0; k < VD / 2; ++k) vr[i][v].w[k] = keep ? vr[i][v].w[k] : 0u;
+    }
+    f4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < QS; ++q) {
+      const int i0 = 2 * q, i1 = 2 * q + 1;
+      c = mfma16(as_h4(kr[i][i0 >> 2][i0 & 3], kr[i][i1 >> 2][i1 & 3]), as_h4(qr[i0 >> 2][i0 & 3], qr[i1 >> 2][i1 & 3]),
+                 c);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const bool live = tile && ts + 4 * g + v < t1;
+      sc[i][v] = live ? c[v] * scale : -INFINITY;
+      rmax = fmaxf(rmax, sc[i][v]);
+    }
+  }
+  // ---- one online-softmax round per wave (m, l of head col; acc rows = heads 4 g + v)
+  const float m = rows_max(rmax);
+  float ps = 0.f;
+#pragma unroll
+  for (int i = 0; i < NT; ++i) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float pv = (sc[i][v] == -INFINITY) ? 0.f : __expf(sc[i][v] - m);
+      sc[i][v] = pv;
+      ps += pv;
+    }
+  }
+  const float l = rows_sum(ps);
+  f4 acc[VD];
+#pragma unroll
+  for (int t = 0; t < VD; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < NT; ++i) {
+    h4 phi, plo;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      phi[v] = (f16)sc[i][v];
+      plo[v] = (f16)(sc[i][v] - (float)phi[v]);
+    }
+#pragma unroll
+    for (int t = 0; t < VD; ++t) {
+      // B operand of dim tile t: dim VD col + t of tokens 4 g + 0..3
+      const int wi = t >> 1;
+      const uint32_t sel = (t & 1) ? 0x07060302u : 0x05040100u;
+      const uint32_t lo = __builtin_amdgcn_perm(vr[i][1].w[wi], vr[i][0].w[wi], sel);
+      const uint32_t hi = __builtin_amdgcn_perm(vr[i][3].w[wi], vr[i][2].w[wi], sel);
+      const h4 vb = as_h4(lo, hi);
+      acc[t] = mfma16(phi, vb, acc[t]);
+      acc[t] = mfma16(plo, vb, acc[t]);
+    }
+  }
+  // ---- merge the waves: (m, l) of head col in lanes col < HPG of row 0, O rows = heads 4 g + v
+  if (g == 0 && col < HPG) {
+    s_m[wave][col] = m;
+    s_l[wave][col] = l;
+  }
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int hh = 4 * g + v;
+    if (hh < HPG) {
+#pragma unroll
+      for (int t = 0; t < VD; ++t) s_o[wave][hh][VD * col + t] = acc[t][v];
+    }
+  }
+  __syncthreads();
+  // per head: M = max over the waves, wave weights e^(m_w - M) (divided by L for a direct output); head hh's M and L
+  // go to the partials (thread hh of the loop below keeps them)
+  float Mh = -INFINITY, Lh = 0.f;
+  if (tid < HPG) {
+#pragma unroll
+    for (int w = 0; w < NW; ++w) Mh = fmaxf(Mh, s_m[w][tid]);
+    float ww[NW];
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      ww[w] = (s_m[w][tid] == -INFINITY) ? 0.f : __expf(s_m[w][tid] - Mh);
+      Lh = fmaf(ww[w], s_l[w][tid], Lh);
+    }
+    const float inv = nsplit == 1 ? (Lh > 0.f ? 1.0f / Lh : 0.f) : 1.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) s_w[w][tid] = ww[w] * inv;
+  }
+  __syncthreads();
+  for (int o = tid; o < HPG * D; o += NW * kWave) {
+    const int hh = o / D, d = o % D;
+    float O = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) O = fmaf(s_w[w][hh], s_o[w][hh][d], O);
+    const int head = kvh * HPG + hh;
+    if (nsplit == 1) {
+      out[(size_t)head * D + d] = (f16)O;
+    } else {
+      o_part[((size_t)head * max_splits + split) * D + d] = O;
+    }
+  }
+  if (nsplit > 1 && tid < HPG) {
+    const int head = kvh * HPG + tid;
+    m_part[(size_t)head * max_splits + split] = Mh;
+    l_part[(size_t)head * max_splits + split] = Lh;
+  }
+}
+
+template <int D, int HPG, bool ROPE, int NW, int NT>
+void launch_lean(const AttnLaunch& a, hipStream_t st) {
+  const float scale = 1.0f / sqrtf((float)D);
+  hipLaunchKernelGGL((attn_lean_kernel<D, HPG, ROPE, NW, NT>), dim3(a.n_kv, a.max_splits), dim3(NW * kWave), 0, st,
+                     (const f16*)a.q, a.cos_t, a.sin_t, a.max_pos, a.pos, a.bt, a.n_bt, (f16*)a.kc, (f16*)a.vc,
+                     a.n_pages, a.log2P, a.n_q, a.n_kv, a.part_size, a.max_splits, scale, a.o_part, a.m_part,
+                     a.l_part, (f16*)a.out);
+}
+
+// waves: the smallest power of two >= min(tiles, 8); tiles per wave NT = ceil(tiles / waves) in {1, 2, 4} (2 at most
+// at head_dim 128)
+template <int D, int HPG, bool ROPE, int NW>
+void launch_lean_nt(const AttnLaunch& a, int nt, hipStream_t st) {
+  if (nt == 1) {
+    launch_lean<D, HPG, ROPE, NW, 1>(a, st);
+  } else if (nt == 2 || D == 128) {
+    launch_lean<D, HPG, ROPE, NW, 2>(a, st);
+  } else {
+    if constexpr (D == 64) launch_lean<D, HPG, ROPE, NW, 4>(a, st);
+  }
+}
+
+template <int D, int HPG, bool ROPE>
+void launch_lean_any(const AttnLaunch& a, hipStream_t st) {
+  const int tiles = a.part_size >> 4;
+  int waves = 1;
+  while (waves < tiles && waves < kLeanMaxWaves) waves <<= 1;
+  const int nt = (tiles + waves - 1) / waves;
+  switch (waves) {
+    case 1: launch_lean_nt<D, HPG, ROPE, 1>(a, nt, st); break;
+    case 2: launch_lean_nt<D, HPG, ROPE, 2>(a, nt, st); break;
+    case 4: launch_lean_nt<D, HPG, ROPE, 4>(a, nt, st); break;
+    default: launch_lean_nt<D, HPG, ROPE, 8>(a, nt, st); break;
+  }
+}
+
 template <int D, int HPG, bool ROPE>
 void launch_attn(const AttnLaunch& a, hipStream_t st) {
   const float scale = 1.0f / sqrtf((float)D);
+  if (attn_use_lean(a)) {
+    launch_lean_any<D, HPG, ROPE>(a, st);
+    if (a.max_splits > 1)
+      hipLaunchKernelGGL((attn_combine_kernel<D>), dim3(a.n_q), dim3(kAttnThreads), 0, st, a.o_part, a.m_part,
+                         a.l_part, a.pos, ROPE ? a.max_pos : 0, a.n_bt, a.log2P, a.part_size, a.max_splits,
+                         (f16*)a.out);
+    return;
+  }
   if (attn_use_mfma(a)) {
     hipLaunchKernelGGL((attn_mfma_kernel<D, HPG, ROPE>), dim3(a.n_kv, a.max_splits), dim3(kMfmaThreads), 0, st,
                        (const f16*)a.q, a.cos_t, a.sin_t, a.max_pos, a.pos, a.bt, a.n_bt, (f16*)a.kc, (f16*)a.vc,

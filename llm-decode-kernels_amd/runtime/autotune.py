@@ -248,15 +248,17 @@ def step_time_us(model, ctx, steps=24, warmup=8):
 
 def tune_attention(dims=(64, 128), contexts=ATTN_CONTEXTS, path=ATTN_PATH, log=print):
     """Writes configs/attn_policy.json: per head dim, entries {max_ctx, part_size, impl} (the reference's schema,
-    runtime/model.py:160-178, plus the kernel choice), the last one open-ended. Every candidate (impl 1 block kernel or
-    2 MFMA kernel, split size) is timed inside the decode step of the model that has this head dim (graph replay at
-    context ctx): an attention kernel costs more inside the step, interleaved with the GEMVs, than back to back, and
-    by different amounts per kernel, so isolated launches would choose wrongly."""
+    runtime/model.py:160-178, plus the kernel choice), the last one open-ended. Every candidate (impl 1 block kernel,
+    2 MFMA kernel or 3 lean MFMA kernel, split size) is timed inside the decode step of the model that has this head
+    dim (graph replay at context ctx): an attention kernel costs more inside the step, interleaved with the GEMVs,
+    than back to back, and by different amounts per kernel, so isolated launches would choose wrongly. The three
+    fastest candidates of each context are timed twice more, interleaved, and keep their best time."""
     from . import synth
     from .model import DecodeConfig, Model
     old = json.load(open(path)) if pathlib.Path(path).exists() else {}
     out = {"version": old.get("version", 3),
-           "note": "part_size (tokens per split) and impl (1 block kernel, 2 MFMA kernel) by the largest tuned context "
+           "note": "part_size (tokens per split) and impl (1 block kernel, 2 MFMA kernel, 3 lean MFMA kernel) by the "
+                   "largest tuned context "
                    "<= the prepared cap; chosen by the decode step time of the TinyLlama (head_dim 64) and Llama-3-8B "
                    "(head_dim 128) shapes on MI355X (runtime.autotune.tune_attention). 'policy' is head_dim 64, "
                    "'policy_d128' head_dim 128."}
@@ -267,17 +269,23 @@ def tune_attention(dims=(64, 128), contexts=ATTN_CONTEXTS, path=ATTN_PATH, log=p
         model = Model(synth.SyntheticLlama(shape, seed=0), shape,
                       DecodeConfig(lm_head="int4" if D == 128 else "fp16", max_ctx=cap_max))
         ents = []
+        lean_max = 256 if D == 128 else 512
         for ctx in contexts:
-            best = None
-            for impl in (1, 2):
-                for ps in (32, 64, 128, 256, 512):
-                    if impl == 1 and ps > 128:
-                        continue                       # the block kernel costs about 3 us per extra 64-token block
+            cands = [(1, ps) for ps in (32, 64, 128)]  # the block kernel costs about 3 us per extra 64-token block
+            cands += [(2, ps) for ps in (32, 64, 128, 256, 512)]
+            cands += [(3, ps) for ps in (16, 32, 64, 128, 256, 512) if ps <= lean_max]
+            times = {}
+            for impl, ps in cands:
+                model.prepare(ctx + 48, part_size=ps, impl=impl)
+                times[(impl, ps)] = step_time_us(model, ctx)
+            for _ in range(2):  # confirm the leaders
+                for impl, ps in sorted(times, key=times.get)[:3]:
                     model.prepare(ctx + 48, part_size=ps, impl=impl)
-                    us = step_time_us(model, ctx)
-                    grid.append({"D": D, "ctx": ctx, "impl": impl, "part_size": ps, "step_us": round(us, 2)})
-                    if best is None or us < best[0]:
-                        best = (us, impl, ps)
+                    times[(impl, ps)] = min(times[(impl, ps)], step_time_us(model, ctx))
+            for (impl, ps), us in times.items():
+                grid.append({"D": D, "ctx": ctx, "impl": impl, "part_size": ps, "step_us": round(us, 2)})
+            impl, ps = min(times, key=times.get)
+            best = (times[(impl, ps)], impl, ps)
             log(f"  attention D{D} ctx {ctx}: best impl {best[1]} part_size {best[2]} ({best[0]:.1f} us per step)")
             ents.append({"max_ctx": ctx, "part_size": best[2], "impl": best[1]})
         ents[-1] = dict(ents[-1], max_ctx=1 << 30)

@@ -291,8 +291,8 @@ class DecodeKernels:
             raise RuntimeError("heads-per-group must be 1/2/4/8")
         if part_size <= 0:
             raise RuntimeError("part_size must be > 0")
-        if not 1 <= version <= 4:
-            raise RuntimeError("attention version must be 1, 2, 3 or 4")
+        if not 1 <= version <= 5:
+            raise RuntimeError("attention version must be 1, 2, 3, 4 or 5")
         max_splits = o_part.size(1)
         if not (o_part.size(0) == n_q and o_part.size(2) == D and m_part.size(0) == n_q and l_part.size(0) == n_q
                 and m_part.size(1) == max_splits and l_part.size(1) == max_splits and out.numel() == n_q * D):
@@ -306,7 +306,8 @@ class DecodeKernels:
                          out, counters=None, impl=0):
         """counters: None (split kernel + combine kernel) or int32 [n_kv] zeros, left zero by every call (the last
         split workgroup of each kv head combines; one launch; block kernel only). impl: 0 or 1 = block kernel,
-        2 = MFMA kernel."""
+        2 = MFMA kernel, 3 = lean MFMA kernel (pages >= 16 tokens, part_size a multiple of 16 up to 512, 256 at
+        head_dim 128)."""
         for t, n in ((qkv, "qkv"), (cos_t, "cos_t"), (sin_t, "sin_t"), (pos, "pos"), (bt, "bt"), (kc, "kc"),
                      (vc, "vc"), (o_part, "o_part"), (m_part, "m_part"), (l_part, "l_part"), (out, "out")):
             _check_cuda(t, n)

@@ -51,7 +51,8 @@ class DecodeConfig:
     page: int = 16
     part_size: int = 0
     attn_version: int = 0
-    attn_impl: int = 0             # decode attention kernel: 0 = policy table, 1 = block kernel, 2 = MFMA kernel
+    attn_impl: int = 0             # decode attention kernel: 0 = policy table, 1 = block kernel, 2 = MFMA kernel,
+                                   # 3 = lean MFMA kernel
     gemv_stage: tuple = None
     autotune_path: str = str(PKG / "configs" / "autotune.json")
     attn_policy_path: str = str(PKG / "configs" / "attn_policy.json")
@@ -225,6 +226,8 @@ class Model:
         self.attn_impl = impl or self.cfg.attn_impl or ent.get("impl", 1)
         if self.attn_impl == 2 and ((ps - 1) >> (self.cfg.page.bit_length() - 1)) + 2 > 1024:
             self.attn_impl = 1                      # the MFMA kernel stages at most 1024 pages per split
+        if self.attn_impl == 3 and (self.cfg.page < 16 or ps % 16 or ps > (256 if self.D == 128 else 512)):
+            self.attn_impl = 1                      # the lean kernel takes whole 16-token tiles of one page
         self.part_size = ps
         self.max_splits = max(1, math.ceil(ctx_cap / ps))
         self.ctx_cap = self.max_splits * ps

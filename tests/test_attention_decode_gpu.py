@@ -20,20 +20,34 @@ def K():
     return ext.load()
 
 
-MODES = ("block", "counters", "mfma")   # impl 1, impl 1 with the in-split combine, impl 2
+MODES = ("block", "counters", "mfma", "lean")   # impl 1, impl 1 with the in-split combine, impl 2, impl 3
+IMPL = {"block": 1, "counters": 1, "mfma": 2, "lean": 3}
+
+
+def lean_fits(PS, page, D):
+    """impl 3: pages of >= 16 tokens, part sizes a multiple of 16 up to 512 (256 at head_dim 128)."""
+    return page >= 16 and PS % 16 == 0 and PS <= (256 if D == 128 else 512)
 
 
 def run_fused(K, qkv, cos, sin, kc, vc, bt, pos, n_q, n_kv, PS, max_splits, mode="block"):
-    """mode "counters": the in-split combine (per-kv-head arrival counters, which every launch must leave at zero)."""
+    """mode "counters": the in-split combine (per-kv-head arrival counters, which every launch must leave at zero).
+    A part size the lean kernel cannot take is checked to be rejected; then None is returned."""
     counters = mode == "counters"
     D = kc.shape[-1]
+    if mode == "lean" and not lean_fits(PS, kc.shape[2], D):
+        with pytest.raises(RuntimeError, match="impl 3 needs pages"):
+            K.attention_decode(qkv, cos, sin, torch.tensor([pos], dtype=torch.int32, device=DEV), bt, kc, vc, n_q,
+                               n_kv, PS, torch.empty(n_q, max_splits, D, device=DEV),
+                               torch.empty(n_q, max_splits, device=DEV), torch.empty(n_q, max_splits, device=DEV),
+                               torch.empty(n_q, D, dtype=torch.half, device=DEV), None, impl=3)
+        return None, None, None
     o_part = torch.full((n_q, max_splits, D), 7.0, device=DEV)
     m_part = torch.full((n_q, max_splits), 7.0, device=DEV)
     l_part = torch.full((n_q, max_splits), 7.0, device=DEV)
     out = torch.zeros(n_q, D, dtype=torch.half, device=DEV)
     cnt = torch.zeros(n_kv, dtype=torch.int32, device=DEV) if counters else None
     K.attention_decode(qkv, cos, sin, torch.tensor([pos], dtype=torch.int32, device=DEV), bt, kc, vc, n_q, n_kv, PS,
-                       o_part, m_part, l_part, out, cnt, impl=2 if mode == "mfma" else 1)
+                       o_part, m_part, l_part, out, cnt, impl=IMPL[mode])
     if counters:
         assert torch.all(cnt == 0), "arrival counters must be left at zero"
     return out, o_part, m_part
@@ -64,6 +78,8 @@ def test_fused_attention_matches_rope_then_attention(K, D, n_q, n_kv, ctx, mode)
         kd, vd, qd = kc.to(DEV), vc.to(DEV), qkv.to(DEV)
         out, _, _ = run_fused(K, qd, cos.to(DEV), sin.to(DEV), kd, vd, bt.to(DEV), ctx - 1, n_q, n_kv, PS, ms,
                               mode)
+        if out is None:
+            continue
         assert_close(out, ref, 2e-3, f"fused D{D} {n_q}/{n_kv} ctx{ctx} PS{PS} {mode}")
         assert torch.equal(kd.cpu(), kr) and torch.equal(vd.cpu(), vr), f"cache append D{D} ctx{ctx} PS{PS}"
         assert torch.equal(qd.cpu(), qkv), "qkv must not be modified"
@@ -132,7 +148,7 @@ def test_fused_attention_graph_replays(K, mode):
 
     def body():
         K.attention_decode(qkv, cos, sin, pos, bt, kc, vc, n_q, n_kv, PS, o_part, m_part, l_part, out, cnt,
-                           impl=2 if mode == "mfma" else 1)
+                           impl=IMPL[mode])
 
     expected = {}
     for p in (0, 31, 32, 150, 319):

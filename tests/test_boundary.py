@@ -89,9 +89,13 @@ def _attn(lib, **kw):
     (dict(head_dim=96), 3, "head_dim"),
     (dict(page=12), 4, "page size must be a power of two"),
     (dict(part_size=0), 4, "part_size must be > 0"),
-    (dict(version=5), 4, "version must be 1, 2, 3 or 4"),
-    (dict(version=0), 4, "version must be 1, 2, 3 or 4"),
+    (dict(version=6), 4, "version must be 1, 2, 3, 4 or 5"),
+    (dict(version=0), 4, "version must be 1, 2, 3, 4 or 5"),
     (dict(version=4, part_size=32768), 4, "block-table pages per split"),
+    (dict(version=5, part_size=40), 4, "version 5 needs pages of >= 16 tokens"),
+    (dict(version=5, part_size=1024), 4, "version 5 needs pages"),
+    (dict(version=5, page=8), 4, "version 5 needs pages"),
+    (dict(version=5, head_dim=128, part_size=512), 4, "multiple of 16 up to 256"),
     (dict(max_splits=0), 3, "max_splits"),
     (dict(kc=A16 + 2), 2, "16B aligned"),
     (dict(bt=None), 1, "null"),
@@ -116,8 +120,12 @@ def _dec(lib, **kw):
     (dict(part_size=0), 4, "part_size must be > 0"),
     (dict(max_splits=0), 3, "max_splits"),
     (dict(counters=A16 + 2), 2, "counters must be 4B aligned"),
-    (dict(impl=3), 4, "impl must be 0, 1 or 2"),
+    (dict(impl=4), 4, "impl must be 0, 1, 2 or 3"),
     (dict(impl=2, counters=A16), 4, "belongs to impl 1"),
+    (dict(impl=3, counters=A16), 4, "belongs to impl 1"),
+    (dict(impl=3, part_size=40), 4, "impl 3 needs pages of >= 16 tokens"),
+    (dict(impl=3, page=8), 4, "impl 3 needs pages"),
+    (dict(impl=3, D=128, part_size=512), 4, "multiple of 16 up to 256"),
     (dict(impl=2, part_size=32768, page=16), 4, "block-table pages per split"),
     (dict(max_pos=0), 3, "empty"),
     (dict(c=None), 1, "null"),
