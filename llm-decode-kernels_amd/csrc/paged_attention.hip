@@ -372,7 +372,9 @@ attn_decode_kernel(const f16* __restrict__ qsrc, const float* __restrict__ cos_t
 
 // Combine of the split partials of one query head per workgroup: thread (sl, d4) takes splits sl, sl + SLN, ... and
 // dims [4 d4, 4 d4 + 4); every lane keeps an online maximum over its splits (loads of 4 splits in flight), then the
-// SLN split lanes merge through LDS with the same max-rescale rule.
+// SLN split lanes merge through LDS with the same max-rescale rule. The first 4 SLN splits' loads go out before *pos
+// is read (clamped to the buffer's max_splits; splits past the live count are dropped by select once it is known), so
+// the position's round trip overlaps theirs.
 template <int D>
 __global__ void __launch_bounds__(kAttnThreads)
 attn_combine_kernel(const float* __restrict__ o_part, const float* __restrict__ m_part,
@@ -382,25 +384,43 @@ attn_combine_kernel(const float* __restrict__ o_part, const float* __restrict__ 
   constexpr int SLN = kAttnThreads / NG;    // split lanes
   __shared__ float s_m[SLN], s_l[SLN];
   __shared__ float4 s_a[SLN][NG];
-  if (max_pos > 0 && (*pos_ptr < 0 || *pos_ptr >= max_pos)) return;  // decode op: the split kernel did nothing
-  const int nsplit = attn_splits(attn_context(pos_ptr, n_bt, log2P), PS, max_splits);
-  if (nsplit <= 1) return;
   const int head = blockIdx.x, tid = threadIdx.x, sl = tid / NG, d4 = tid % NG;
   const float* m = m_part + (size_t)head * max_splits;
   const float* l = l_part + (size_t)head * max_splits;
   const float* op = o_part + (size_t)head * max_splits * D + 4 * d4;
+  float ms[4], ls[4];
+  float4 os[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {  // first batch, speculative (in bounds of the partial buffers)
+    const int s = min(sl + k * SLN, max_splits - 1);
+    ms[k] = m[s];
+    ls[k] = l[s];
+    os[k] = *reinterpret_cast<const float4*>(op + (size_t)s * D);
+  }
+  // No early return before the first batch is consumed: the compiler would sink its loads below the test.
+  const int pos = *pos_ptr;
+  const bool skip = max_pos > 0 && (pos < 0 || pos >= max_pos);  // decode op: the split kernel did nothing
+  const long long cap = (long long)n_bt << log2P;
+  const int nsplit = skip ? 0 : attn_splits((int)((long long)pos + 1 < cap ? (long long)pos + 1 : cap), PS, max_splits);
   float M = -INFINITY, L = 0.f;
   float4 a = {0.f, 0.f, 0.f, 0.f};
   for (int s0 = sl; s0 < nsplit; s0 += 4 * SLN) {
-    float ms[4], ls[4];
-    float4 os[4];
+    if (s0 != sl) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int s = s0 + k * SLN;
-      const bool v = s < nsplit;
-      ms[k] = v ? m[s] : -INFINITY;
-      ls[k] = v ? l[s] : 0.f;
-      os[k] = v ? *reinterpret_cast<const float4*>(op + (size_t)s * D) : float4{0.f, 0.f, 0.f, 0.f};
+      for (int k = 0; k < 4; ++k) {
+        const int s = min(s0 + k * SLN, max_splits - 1);
+        ms[k] = m[s];
+        ls[k] = l[s];
+        os[k] = *reinterpret_cast<const float4*>(op + (size_t)s * D);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {  // splits past the live count: dropped (their partials are stale or never written)
+      if (s0 + k * SLN >= nsplit) {
+        ms[k] = -INFINITY;
+        ls[k] = 0.f;
+        os[k] = float4{0.f, 0.f, 0.f, 0.f};
+      }
     }
     const float Mn = fmaxf(fmaxf(M, fmaxf(ms[0], ms[1])), fmaxf(ms[2], ms[3]));
     if (Mn == -INFINITY) continue;
@@ -421,6 +441,7 @@ attn_combine_kernel(const float* __restrict__ o_part, const float* __restrict__ 
     }
     M = Mn;
   }
+  if (nsplit <= 1) return;  // uniform: one live split wrote the output itself (or none was live)
   if (d4 == 0) {
     s_m[sl] = M;
     s_l[sl] = L;
