@@ -105,4 +105,18 @@ __device__ __forceinline__ void unpack8(u32x4 v, float* f) {
   }
 }
 
+// Argmax key of logit v at index i: a 64-bit value whose unsigned order is the argmax ranking (torch.argmax):
+// high word 0xFFFFFFFF for NaN, else the float bits made monotonic (negatives inverted, positives with the sign bit
+// set, -0 first turned into +0 so the two zeros tie); low word ~i, so that among equal values the lowest index wins.
+__device__ __forceinline__ uint64_t argmax_key(float v, int i) {
+  uint32_t hi;
+  if (v != v) {
+    hi = 0xFFFFFFFFu;
+  } else {
+    const uint32_t b = __float_as_uint(v == 0.f ? 0.f : v);
+    hi = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  }
+  return ((uint64_t)hi << 32) | (uint32_t)~(uint32_t)i;
+}
+
 }  // namespace dk

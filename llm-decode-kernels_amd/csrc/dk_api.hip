@@ -444,4 +444,69 @@ int dk_quantize_w4(const void* w, void* packed, void* sz, int N, int K, int grou
   return launched("quantize_w4");
 }
 
+int dk_decode_step_grid(void) {
+  const int g = dk::decode_step_grid(64);
+  const int g2 = dk::decode_step_grid(128);
+  return g < g2 ? g : g2;
+}
+
+size_t dk_decode_step_work_bytes(const dk_step_desc* desc) {
+  if (!desc) return 0;
+  const dk_step_desc& d = *desc;
+  if (d.n_layers <= 0 || d.hidden <= 0 || d.n_q <= 0 || d.n_kv <= 0 || d.head_dim <= 0 || d.inter <= 0 ||
+      d.max_splits <= 0)
+    return 0;
+  return (size_t)d.n_layers * dk::step_layout(d.hidden, d.n_q, d.n_kv, d.head_dim, d.inter, d.max_splits).layer;
+}
+
+int dk_decode_step(const dk_step_desc* desc, void* stream) {
+  if (!desc) return fail(DK_ERR_NULL, "decode_step: null descriptor");
+  const dk_step_desc& d = *desc;
+  if (!d.emb || !d.norm_f || !d.head_w || !d.cos_t || !d.sin_t || !d.tok || !d.pos || !d.bt || !d.work ||
+      !d.logits || !d.sync || !d.layers)
+    return fail(DK_ERR_NULL, "decode_step: null pointer in the descriptor");
+  const int D = d.head_dim, H = d.hidden, I = d.inter;
+  if (D != 64 && D != 128) return fail(DK_ERR_DOMAIN, "decode_step: head_dim must be 64 or 128, got %d", D);
+  if (d.n_layers <= 0 || d.n_q <= 0 || d.n_kv <= 0 || d.vocab <= 0 || H <= 0 || I <= 0)
+    return fail(DK_ERR_SHAPE, "decode_step: sizes must be positive");
+  if (d.n_layers > dk::kStepMaxLayers)
+    return fail(DK_ERR_SHAPE, "decode_step: at most %d layers, got %d", dk::kStepMaxLayers, d.n_layers);
+  if (d.n_q % d.n_kv != 0 || d.n_q / d.n_kv > 8)
+    return fail(DK_ERR_SHAPE, "decode_step: n_q / n_kv must be an integer <= 8 (n_q=%d n_kv=%d)", d.n_q, d.n_kv);
+  if (H != d.n_q * D) return fail(DK_ERR_SHAPE, "decode_step: hidden must equal n_q * head_dim");
+  if (!dk::decode_step_fits(D, H, I))
+    return fail(DK_ERR_SHAPE, "decode_step: head_dim %d takes hidden <= %d and inter <= %d (got %d, %d)", D,
+                D == 64 ? 2048 : 4096, D == 64 ? 6144 : 14336, H, I);
+  if (d.group < 32 || !pow2(d.group)) return fail(DK_ERR_DOMAIN, "decode_step: group must be a power of two >= 32");
+  if (H % 32 || I % 32 || H % d.group || I % d.group)
+    return fail(DK_ERR_SHAPE, "decode_step: hidden and inter must be multiples of 32 and of the group");
+  if (!(d.eps >= 0.f)) return fail(DK_ERR_DOMAIN, "decode_step: eps must be >= 0");
+  if (d.page < 16 || !pow2(d.page)) return fail(DK_ERR_DOMAIN, "decode_step: page must be a power of two >= 16");
+  if (d.part_size != 128 && d.part_size != 256)
+    return fail(DK_ERR_DOMAIN, "decode_step: part_size must be 128 or 256 (8 waves x 1 or 2 tiles of 16), got %d",
+                d.part_size);
+  if (d.n_bt <= 0 || d.n_pages <= 0 || d.max_pos <= 0) return fail(DK_ERR_SHAPE, "decode_step: empty cache or tables");
+  const int grid = dk::decode_step_grid(D);
+  if (grid <= 0) return fail(DK_ERR_LAUNCH, "decode_step: no device, or a CU cannot hold one workgroup");
+  const int widest = (d.n_q + 2 * d.n_kv) * D > I ? (d.n_q + 2 * d.n_kv) * D : I;
+  if ((widest + grid - 1) / grid + 1 > dk::kStepOutMax)
+    return fail(DK_ERR_SHAPE, "decode_step: %d outputs over %d workgroups exceed %d per workgroup", widest, grid,
+                dk::kStepOutMax);
+  if (d.max_splits <= 0 || d.max_splits > dk::kStepMaxSplits || (long long)d.n_kv * d.max_splits > grid)
+    return fail(DK_ERR_SHAPE, "decode_step: max_splits must be in [1, %d] with n_kv * max_splits <= %d (got %d)",
+                dk::kStepMaxSplits, grid, d.max_splits);
+  const void* a16[] = {d.emb, d.norm_f, d.head_w};
+  for (const void* p : a16)
+    if (!aligned16(p)) return fail(DK_ERR_ALIGN, "decode_step: embedding, norm and head weights must be 16B aligned");
+  if ((reinterpret_cast<uintptr_t>(d.work) & 255u) != 0) return fail(DK_ERR_ALIGN, "decode_step: work must be 256B aligned");
+  if (d.work_bytes < dk_decode_step_work_bytes(&d))
+    return fail(DK_ERR_SHAPE, "decode_step: work holds %zu bytes, needs %zu", d.work_bytes,
+                dk_decode_step_work_bytes(&d));
+  if (!aligned4(d.logits) || (d.head_sz && !aligned4(d.head_sz)) || (reinterpret_cast<uintptr_t>(d.sync) & 7u) != 0)
+    return fail(DK_ERR_ALIGN, "decode_step: logits and head scales 4B aligned, sync 8B aligned");
+  clear_error();
+  dk::launch_decode_step(d, grid, (hipStream_t)stream);
+  return launched("decode_step");
+}
+
 }  // extern "C"

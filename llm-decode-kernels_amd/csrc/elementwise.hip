@@ -261,17 +261,6 @@ argmax_advance_kernel(const f16* __restrict__ logits, int V, int64_t* __restrict
 constexpr int kArgmaxWgThreads = 256;
 constexpr int kArgmaxWgChunks = 2 * kArgmaxWgThreads;  // two 16-byte chunks (16 logits) per thread
 
-__device__ __forceinline__ uint64_t argmax_key(float v, int i) {
-  uint32_t hi;
-  if (v != v) {
-    hi = 0xFFFFFFFFu;
-  } else {
-    const uint32_t b = __float_as_uint(v == 0.f ? 0.f : v);
-    hi = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-  }
-  return ((uint64_t)hi << 32) | (uint32_t)~(uint32_t)i;
-}
-
 __global__ void __launch_bounds__(kArgmaxWgThreads)
 argmax_split_kernel(const f16* __restrict__ logits, int V, int h, int nc, int64_t* __restrict__ tok,
                     int32_t* __restrict__ pos, unsigned long long* __restrict__ work) {

@@ -4,6 +4,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "dk_amd.h"
+
 namespace dk {
 
 // W4A16 GEMV. stage 0: exact per-element dequant, `waves` rows per workgroup. stage 1/2: each wave streams R whole
@@ -103,5 +105,37 @@ void launch_argmax_split(const void* logits, int V, int64_t* tok, int32_t* pos, 
                          hipStream_t st);
 
 void launch_quantize_w4(const void* w, void* packed, void* sz, int N, int K, int log2G, int clip, hipStream_t st);
+
+// persistent decode step (decode_step.hip)
+constexpr int kStepMaxSplits = 64;  // most attention splits per kv head (one wave combines a head)
+constexpr int kStepMaxLayers = 64;   // layer table held in LDS
+constexpr int kStepOutMax = 256;    // most outputs of one workgroup in a GEMV phase (gathered in LDS)
+
+// Byte offsets of one layer's slots in the persistent step's work buffer (every slot 256-byte aligned; `layer` is the
+// size of one layer's region, layer i starts at i * layer).
+struct StepLayout {
+  size_t xq, xg, qkv, attn, o, act, down, opart, mpart, lpart, layer;
+};
+__host__ __device__ inline size_t step_align(size_t v) { return (v + 255) & ~(size_t)255; }
+__host__ __device__ inline StepLayout step_layout(int H, int n_q, int n_kv, int D, int I, int max_splits) {
+  StepLayout L;
+  size_t o = 0;
+  L.xq = o;    o += step_align((size_t)H * 2);                      // residual entering the layer
+  L.xg = o;    o += step_align((size_t)H * 2);                      // residual after the attention block
+  L.qkv = o;   o += step_align((size_t)(n_q + 2 * n_kv) * D * 2);
+  L.attn = o;  o += step_align((size_t)H * 2);
+  L.o = o;     o += step_align((size_t)H * 2);
+  L.act = o;   o += step_align((size_t)I * 2);
+  L.down = o;  o += step_align((size_t)H * 2);
+  L.opart = o; o += step_align((size_t)n_q * max_splits * D * 4);
+  L.mpart = o; o += step_align((size_t)n_q * max_splits * 4);
+  L.lpart = o; o += step_align((size_t)n_q * max_splits * 4);
+  L.layer = o;
+  return L;
+}
+int decode_step_threads();
+bool decode_step_fits(int head_dim, int H, int I);
+int decode_step_grid(int head_dim);  // workgroups per launch on the current device (one per CU), -1 if unavailable
+int launch_decode_step(const dk_step_desc& d, int grid, hipStream_t st);
 
 }  // namespace dk

@@ -42,7 +42,32 @@ SIGNATURES = {
     "dk_argmax_advance": ([_P, _I, _P, _P, _P], _I),
     "dk_argmax_advance_split": ([_P, _I, _P, _P, _P, _P], _I),
     "dk_quantize_w4": ([_P, _P, _P, _I, _I, _I, _I, _P], _I),
+    "dk_decode_step_grid": ([], _I),
+    "dk_decode_step_work_bytes": ([_P], _Z),
+    "dk_decode_step": ([_P, _P], _I),
 }
+
+# sync buffer of dk_decode_step (include/dk_amd.h DK_STEP_SYNC_WORDS / DK_STEP_SYNC_ABORT)
+STEP_SYNC_WORDS = 2048
+STEP_SYNC_ABORT = 1056
+
+
+class StepLayer(ctypes.Structure):
+    """dk_step_layer: device pointers of one layer's weights, norms and KV cache."""
+    _fields_ = [(n, _P) for n in ("qkv_packed", "qkv_sz", "o_packed", "o_sz", "gu_packed", "gu_sz", "down_packed",
+                                  "down_sz", "ln1", "ln2", "kc", "vc")]
+
+
+class StepDesc(ctypes.Structure):
+    """dk_step_desc: the whole persistent decode step (sizes, model tensors, activations, split buffers, sync)."""
+    _fields_ = ([(n, _I) for n in ("n_layers", "hidden", "n_q", "n_kv", "head_dim", "inter", "vocab", "group")]
+                + [("eps", _F)]
+                + [(n, _P) for n in ("emb", "norm_f", "head_w", "head_sz", "cos_t", "sin_t")]
+                + [("max_pos", _I)]
+                + [(n, _P) for n in ("tok", "pos", "bt")]
+                + [(n, _I) for n in ("n_bt", "n_pages", "page", "part_size", "max_splits")]
+                + [("work", _P), ("work_bytes", _Z)]
+                + [(n, _P) for n in ("logits", "sync", "layers")])
 
 _EXT = None
 
@@ -422,6 +447,20 @@ class DecodeKernels:
             p = pos.data_ptr()
         self._call(self.lib.dk_argmax_advance_split, logits.data_ptr(), logits.numel(), tok.data_ptr(), p,
                    work.data_ptr(), _stream(logits))
+
+    # No reference counterpart: one launch runs a decode step's whole op sequence (runtime/model.py:216-233)
+    def decode_step(self, desc, device):
+        """Persistent decode step (dk_decode_step) on the current stream of `device`; `desc` is a StepDesc."""
+        self._call(self.lib.dk_decode_step, ctypes.byref(desc),
+                   ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream))
+
+    def decode_step_work_bytes(self, desc):
+        """Bytes of the work buffer dk_decode_step needs for the sizes in `desc` (a StepDesc)."""
+        return int(self.lib.dk_decode_step_work_bytes(ctypes.byref(desc)))
+
+    def decode_step_grid(self):
+        """Workgroups of a dk_decode_step launch on the current device (one per CU); -1 without a usable device."""
+        return int(self.lib.dk_decode_step_grid())
 
     # runtime/quant.py:42-48,100-124 on the GPU
     def quantize_w4(self, w, packed, sz, group, clip=False):

@@ -70,6 +70,11 @@ class DecodeConfig:
                                    # consumes it (dk_gemv_w4a16_rmsnorm) instead of a separate add_rmsnorm kernel
     f16_gemv: bool = True          # fp16-weight projections with K <= 4096 (the fp16 LM head) on the HIP fp16 GEMV
                                    # (dk_gemv_f16 / dk_gemv_f16_rmsnorm) instead of torch.mm
+    persistent: bool = False       # the whole decode step as one launch (dk_decode_step: grid barriers between phases,
+                                   # next-phase weights requested ahead); needs the fused INT4 body with the SwiGLU
+                                   # epilogue layout
+    step_part_size: int = 0        # tokens per attention split of the persistent step (128 or 256: 8 waves x 1 or 2
+                                   # tiles of 16; 0 = the smallest that fits the grid)
     swiglu: str = "epilogue"       # where SwiGLU runs when fused_gemv is on: "epilogue" = inside the gate|up GEMV
                                    # (dk_gemv_w4a16_gate_up, gate/up rows stored interleaved); "prologue" = inside the
                                    # down GEMV (dk_gemv_w4a16_swiglu: every workgroup re-evaluates silu for its columns,
@@ -216,6 +221,72 @@ class Model:
         self.argmax_work = torch.zeros(2, dtype=torch.int64, device=self.cfg.device)
         self.graph = None
         self.host_pos = 0
+        self.step_desc = None
+        if cfg.persistent:
+            self._setup_step()
+            self._step_partition(cfg.max_ctx)
+
+    # ------------------------------------------------------------------ persistent step
+    def _setup_step(self):
+        """Per-layer pointer table (device), sync words and the parts of the dk_decode_step descriptor that never
+        change."""
+        if not (self.use_fused_gemv and self.gate_up_epilogue):
+            raise ValueError("persistent step: needs the fused INT4 body with the SwiGLU epilogue (weights='int4', "
+                             "fused, fused_gemv, swiglu='epilogue')")
+        if not (self.cfg.page >= 16 and self.cfg.page & (self.cfg.page - 1) == 0):
+            raise ValueError("persistent step: page must be a power of two >= 16")
+        rows = []
+        for li, lw in enumerate(self.layers):
+            rows.append([lw["qkv"].packed.data_ptr(), lw["qkv"].sz.data_ptr(), lw["o"].packed.data_ptr(),
+                         lw["o"].sz.data_ptr(), lw["gu"].packed.data_ptr(), lw["gu"].sz.data_ptr(),
+                         lw["down"].packed.data_ptr(), lw["down"].sz.data_ptr(), lw["ln1"].data_ptr(),
+                         lw["ln2"].data_ptr(), self.kv[li, 0].data_ptr(), self.kv[li, 1].data_ptr()])
+        self.step_layers = torch.tensor(rows, dtype=torch.int64, device=self.cfg.device)
+        # barrier words of the step: zero here; every completed step leaves them zero
+        self.step_sync = torch.zeros(ext.STEP_SYNC_WORDS, dtype=torch.int32, device=self.cfg.device)
+        self.step_grid = self.K.decode_step_grid()
+        if self.step_grid <= 0:
+            raise RuntimeError("persistent step: no usable device (dk_decode_step_grid)")
+
+    def _step_partition(self, ctx_cap):
+        """Split size of the step's attention (one workgroup per (kv head, split), all splits of the cap at once) and
+        the descriptor, rebuilt because the split buffers change."""
+        sizes = (self.cfg.step_part_size,) if self.cfg.step_part_size else (128, 256)
+        for ps in sizes:
+            ms = max(1, math.ceil(ctx_cap / ps))
+            if ms <= 64 and self.n_kv * ms <= self.step_grid:
+                break
+        else:
+            raise ValueError(f"persistent step: context {ctx_cap} needs more than {self.step_grid} attention "
+                             f"workgroups at part sizes {sizes}")
+        self.step_part_size, self.step_max_splits = ps, ms
+        head = self.lm_head
+        d = ext.StepDesc()
+        d.n_layers, d.hidden, d.n_q, d.n_kv, d.head_dim = self.L, self.H, self.n_q, self.n_kv, self.D
+        d.inter, d.vocab, d.group, d.eps = self.I, self.V, self.cfg.group, self.eps
+        d.emb, d.norm_f = self.emb.data_ptr(), self.norm_f.data_ptr()
+        d.head_w = (head.packed if head.quant else head.w).data_ptr()
+        d.head_sz = head.sz.data_ptr() if head.quant else None
+        d.cos_t, d.sin_t, d.max_pos = self.cos.data_ptr(), self.sin.data_ptr(), self.cos.shape[0]
+        d.tok, d.pos, d.bt = self.tok.data_ptr(), self.pos.data_ptr(), self.bt.data_ptr()
+        d.n_bt, d.n_pages, d.page = self.bt.numel(), self.n_pages, self.cfg.page
+        d.part_size, d.max_splits = ps, ms
+        d.logits, d.sync, d.layers = self.logits.data_ptr(), self.step_sync.data_ptr(), self.step_layers.data_ptr()
+        nbytes = int(self.K.decode_step_work_bytes(d))
+        # per layer: residual stream, qkv, attention output, o, act, down and the split partials (each written once
+        # per step before it is read)
+        self.step_work = torch.empty(nbytes, dtype=torch.uint8, device=self.cfg.device)
+        d.work, d.work_bytes = self.step_work.data_ptr(), nbytes
+        self.step_desc = d
+        self.graph = None
+
+    def step_status(self):
+        """0 after normal persistent steps; 1 if a grid barrier timed out (the outputs are then invalid and the sync
+        words are reset here)."""
+        ab = int(self.step_sync[ext.STEP_SYNC_ABORT].item())
+        if ab:
+            self.step_sync.zero_()
+        return ab
 
     # ------------------------------------------------------------------ helpers
     def set_attention_partition(self, ctx_cap, part_size=None, impl=None):
@@ -238,6 +309,8 @@ class Model:
         # per-kv-head arrival counters of the in-split combine: zero here, left zero by every launch
         self.attn_counters = torch.zeros(self.n_kv, dtype=torch.int32, device=self.cfg.device)
         self.graph = None
+        if getattr(self, "step_desc", None) is not None:
+            self._step_partition(ctx_cap)
 
     def prepare(self, ctx_cap, use_graph=True, part_size=None, impl=None):
         """Configure attention for contexts <= ctx_cap and (re)capture the decode graph (runtime/model.py:153-158)."""
@@ -375,6 +448,9 @@ class Model:
     # ------------------------------------------------------------------ decode step
     def step(self):
         """One token: reads tok/pos, writes logits, tok <- argmax, pos += 1 (runtime/model.py:216-233)."""
+        if self.step_desc is not None:
+            self.K.decode_step(self.step_desc, self.cfg.device)
+            return
         if self.use_fused_gemv:
             self.step_fused()
             return
