@@ -408,6 +408,14 @@ def main():
     dec2k = decode_leg(model, 2048, 64, 8)
     log(f"decode ctx 2048: {dec2k['tok_s']:.1f} tok/s")
     bpt2k = model.bytes_per_token(2048 + 32)
+    # the same model through the persistent step (one launch per token, dk_decode_step): reported beside the default
+    model.set_persistent(True)
+    model.prepare(a.ctx + a.steps + a.warmup + 16)
+    pers = decode_leg(model, a.ctx, a.steps, a.warmup)
+    pers_status = model.step_status()
+    model.set_persistent(False)
+    log(f"decode ctx {a.ctx}, persistent step: {pers['tok_s']:.1f} tok/s, median {pers['median_us']:.1f} us/token "
+        f"(status {pers_status})")
 
 
     model.prepare(2048 + 64 + 16)
@@ -444,6 +452,8 @@ def main():
                    "frac_of_roofline": round(dec["tok_s"] / (HBM_PEAK_GBS * 1e9 / bpt), 4)},
         "decode_ctx2048": {"tok_s": round(dec2k["tok_s"], 2), "median_us": round(dec2k["median_us"], 2),
                            "bytes_per_token": bpt2k, "frac_of_roofline": round(dec2k["tok_s"] / (HBM_PEAK_GBS * 1e9 / bpt2k), 4)},
+        "decode_persistent": {"tok_s": round(pers["tok_s"], 2), "median_us": round(pers["median_us"], 2),
+                              "status": pers_status, "kernel": "dk_decode_step (one launch per token)"},
         "prefill_tinyllama_512": pre,
         "decode_llama3_8b_ctx4096": d8b,
         "cpu_baseline": cpu,

@@ -283,8 +283,8 @@ struct W4Batch {
 
 // Issues the weight and scale/zero loads of rows [row0, row0 + n) (n <= R, wave-uniform), C column steps each.
 template <int C, int R>
-__device__ __forceinline__ void w4_issue(W4Batch<C, R>& b, const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ,
-                                         int row0, int n, int U, int gsh, int lane) {
+__device__ __forceinline__ void w4_issue(W4Batch<C, R>& b, const void* W, const void* SZ, int row0, int n, int U,
+                                         int gsh, int lane) {
   // wave-uniform row bases (scalar registers) plus 32-bit per-lane byte offsets: the global_load saddr + voffset form,
   // so no 64-bit per-lane address is ever kept live
   const int NG = U >> gsh;
@@ -358,9 +358,8 @@ __device__ __forceinline__ void w4_store(const float (&v)[R], int row, int nb, f
 }
 
 template <int C, int R, int EPI>
-__device__ __forceinline__ void w4_wave(W4Batch<C, R>& a, const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ,
-                                        int row0, int n, int U, int gsh, const u32x4* xs, f16* s_out, int ob,
-                                        int lane) {
+__device__ __forceinline__ void w4_wave(W4Batch<C, R>& a, const void* W, const void* SZ, int row0, int n, int U,
+                                        int gsh, const u32x4* xs, f16* s_out, int ob, int lane) {
   W4Batch<C, R> b;
   float v[R];
   for (int done = 0; done < n; done += 2 * R) {
@@ -468,7 +467,8 @@ enum {
 static_assert(kLayerFields == 12, "dk_step_layer holds 12 pointers");
 __device__ __forceinline__ const void* layer_ptr(const uint64_t* s_tab, int li, int field) {
   const uint64_t v = s_tab[li * kLayerFields + field];
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
   return reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo);
 }
 
@@ -755,7 +755,8 @@ __device__ __forceinline__ void combine_head(const float* o_part, const float* m
     }
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ws), min(s0 + s, 63)));
+      const float w =
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ws), min(s0 + s, 63)));
 #pragma unroll
       for (int k = 0; k < DPL; ++k) acc[k] = s0 + s < nsplit ? fmaf(w, ov[s][k], acc[k]) : acc[k];
     }
@@ -773,7 +774,10 @@ __device__ __forceinline__ void combine_head(const float* o_part, const float* m
 // an fp16 head row (K = H).
 template <int D, int CH, int CI, int CF>
 struct StepCfg {
-  static constexpr int RH = kWBudget / CH >= 2 ? kWBudget / CH : 2;  // rows per batch, K = H (even: gate|up pairs)
+  static constexpr int RH = kWBudget / CH >= 2 ? kWBudget / CH : 2;  // rows per batch, K = H (INT4 head)
+  static constexpr int RQ = CH == 1 ? 2 : 4;                         // qkv rows per batch
+  static constexpr int RO = 2;                                       // o rows per batch
+  static constexpr int RG = CH == 1 ? 6 : 4;                         // gate|up rows per batch (even: pairs)
   static constexpr int RI = kWBudget / CI >= 1 ? kWBudget / CI : 1;  // rows per batch, K = I
   static constexpr int RF = kWBudget / CF >= 1 ? kWBudget / CF : 1;  // rows per batch, fp16 head
   static constexpr int SH = (CH + 1) / 2;                            // staging chunks per thread, K = H
@@ -784,7 +788,7 @@ struct StepCfg {
 template <int D, int CH, int CI, int CF>
 __global__ void __launch_bounds__(kStepThreads, 1) decode_step_kernel(const StepDev sd) {
   using Cfg = StepCfg<D, CH, CI, CF>;
-  constexpr int RH = Cfg::RH, RI = Cfg::RI, RF = Cfg::RF;
+  constexpr int RH = Cfg::RH, RI = Cfg::RI, RF = Cfg::RF, RQ = Cfg::RQ, RO = Cfg::RO, RG = Cfg::RG;
   extern __shared__ u32x4 lds[];
   __shared__ float s_red[kStepWaves];
   __shared__ unsigned long long s_key[kStepWaves];
@@ -834,15 +838,11 @@ __global__ void __launch_bounds__(kStepThreads, 1) decode_step_kernel(const Step
   char* const work = reinterpret_cast<char*>(d.work);
 
   // loads issued ahead: the qkv rows and the attention pages of layer 0
-  W4Batch<CH, RH> pq;
+  W4Batch<CH, RQ> pq;
   AttnPre<D> ap;
-  {
-    const int li = 0;
-    w4_issue<CH, RH>(pq, reinterpret_cast<const u32x4*>(layer_ptr(s_tab, li, kLQkvW)), reinterpret_cast<const uint32_t*>(layer_ptr(s_tab, li, kLQkvS)),
-                     q0, min(qn, RH), UH, gsh, lane);
-    attn_prefetch<D>(ap, sd, reinterpret_cast<const f16*>(layer_ptr(s_tab, li, kLKc)), reinterpret_cast<const f16*>(layer_ptr(s_tab, li, kLVc)), akvh, asplit, nt,
-                     alive, wave, lane);
-  }
+  w4_issue<CH, RQ>(pq, layer_ptr(s_tab, 0, kLQkvW), layer_ptr(s_tab, 0, kLQkvS), q0, min(qn, RQ), UH, gsh, lane);
+  attn_prefetch<D>(ap, sd, reinterpret_cast<const f16*>(layer_ptr(s_tab, 0, kLKc)),
+                   reinterpret_cast<const f16*>(layer_ptr(s_tab, 0, kLVc)), akvh, asplit, nt, alive, wave, lane);
 
   // Per layer: qkv | attention | [combine] | o | gate|up | down, a grid barrier after each phase. Between the arrival
   // and the wait of a barrier every wave issues the loads of a later phase: the o and gate|up rows after the attention,
@@ -883,10 +883,11 @@ __global__ void __launch_bounds__(kStepThreads, 1) decode_step_kernel(const Step
 #pragma unroll
         for (int i = 0; i < Cfg::SH; ++i) st.a[i] = u32x4{0x7E007E00u, 0x7E007E00u, 0x7E007E00u, 0x7E007E00u};
       }
-      stage_finish<Cfg::SH, true>(st, dl != nullptr, reinterpret_cast<const f16*>(layer_ptr(s_tab, li, kLLn1)), d.eps, H,
+      stage_finish<Cfg::SH, true>(st, dl != nullptr, reinterpret_cast<const f16*>(layer_ptr(s_tab, li, kLLn1)), d.eps,
+                                  H,
                                   blockIdx.x == 0 ? xq : nullptr, lds, s_red, tl);
-      w4_wave<CH, RH, kEpiRows>(pq, reinterpret_cast<const u32x4*>(layer_ptr(s_tab, li, kLQkvW)),
-                                reinterpret_cast<const uint32_t*>(layer_ptr(s_tab, li, kLQkvS)), q0, qn, UH, gsh, lds, s_out, bq, ln);
+      w4_wave<CH, RQ, kEpiRows>(pq, layer_ptr(s_tab, li, kLQkvW),
+                                layer_ptr(s_tab, li, kLQkvS), q0, qn, UH, gsh, lds, s_out, bq, ln);
       w4_flush(s_out, qkv, bq, bqn, tl);
     }
     grid_arrive(sync, ++gen);
@@ -900,11 +901,12 @@ __global__ void __launch_bounds__(kStepThreads, 1) decode_step_kernel(const Step
                      reinterpret_cast<float*>(lds), wave, ln, tl);
     }
     grid_arrive(sync, ++gen);
-    W4Batch<CH, RH> po, pg;
-    w4_issue<CH, RH>(po, reinterpret_cast<const u32x4*>(layer_ptr(s_tab, li, kLOW)), reinterpret_cast<const uint32_t*>(layer_ptr(s_tab, li, kLOS)), o0,
-                     min(on, RH), UH, gsh, ln);
-    w4_issue<CH, RH>(pg, reinterpret_cast<const u32x4*>(layer_ptr(s_tab, li, kLGuW)), reinterpret_cast<const uint32_t*>(layer_ptr(s_tab, li, kLGuS)), g0,
-                     min(gn, RH), UH, gsh, ln);
+    W4Batch<CH, RO> po;
+    W4Batch<CH, RG> pg;
+    w4_issue<CH, RO>(po, layer_ptr(s_tab, li, kLOW), layer_ptr(s_tab, li, kLOS), o0,
+                     min(on, RO), UH, gsh, ln);
+    w4_issue<CH, RG>(pg, layer_ptr(s_tab, li, kLGuW), layer_ptr(s_tab, li, kLGuS), g0,
+                     min(gn, RG), UH, gsh, ln);
     if (!grid_wait(sync, gen, &s_flag)) return;
     // ---------------- combine of many partials as a phase of its own (few partials: inside the o staging)
     if (nsplit > kFuseSplits) {
@@ -920,13 +922,13 @@ __global__ void __launch_bounds__(kStepThreads, 1) decode_step_kernel(const Step
       else
         stage_issue<Cfg::SH>(so, attn, nullptr, nullptr, H >> 3, tl);
       stage_finish<Cfg::SH, true>(so, false, nullptr, d.eps, H, nullptr, lds, s_red, tl);
-      w4_wave<CH, RH, kEpiRows>(po, reinterpret_cast<const u32x4*>(layer_ptr(s_tab, li, kLOW)),
-                                reinterpret_cast<const uint32_t*>(layer_ptr(s_tab, li, kLOS)), o0, on, UH, gsh, lds, s_out, bh, ln);
+      w4_wave<CH, RO, kEpiRows>(po, layer_ptr(s_tab, li, kLOW),
+                                layer_ptr(s_tab, li, kLOS), o0, on, UH, gsh, lds, s_out, bh, ln);
       w4_flush(s_out, ob, bh, bhn, tl);
     }
     grid_arrive(sync, ++gen);
     W4Batch<CI, RI> pdn;
-    w4_issue<CI, RI>(pdn, reinterpret_cast<const u32x4*>(layer_ptr(s_tab, li, kLDownW)), reinterpret_cast<const uint32_t*>(layer_ptr(s_tab, li, kLDownS)),
+    w4_issue<CI, RI>(pdn, layer_ptr(s_tab, li, kLDownW), layer_ptr(s_tab, li, kLDownS),
                      d0, min(dn, RI), UI, gsh, ln);
     if (!grid_wait(sync, gen, &s_flag)) return;
     // ---------------- act = swiglu(W_gu . rmsnorm(xq + o)); xg <- xq + o
@@ -935,14 +937,14 @@ __global__ void __launch_bounds__(kStepThreads, 1) decode_step_kernel(const Step
       stage_issue<Cfg::SH>(sg, xq, ob, reinterpret_cast<const f16*>(layer_ptr(s_tab, li, kLLn2)), H >> 3, tl);
       stage_finish<Cfg::SH, true>(sg, true, reinterpret_cast<const f16*>(layer_ptr(s_tab, li, kLLn2)), d.eps, H,
                                   blockIdx.x == 0 ? xg : nullptr, lds, s_red, tl);
-      w4_wave<CH, RH, kEpiSwiglu>(pg, reinterpret_cast<const u32x4*>(layer_ptr(s_tab, li, kLGuW)),
-                                  reinterpret_cast<const uint32_t*>(layer_ptr(s_tab, li, kLGuS)), g0, gn, UH, gsh, lds, s_out, bi, ln);
+      w4_wave<CH, RG, kEpiSwiglu>(pg, layer_ptr(s_tab, li, kLGuW),
+                                  layer_ptr(s_tab, li, kLGuS), g0, gn, UH, gsh, lds, s_out, bi, ln);
       w4_flush(s_out, act, bi, bin, tl);
     }
     grid_arrive(sync, ++gen);
     if (li + 1 < d.n_layers) {
-      w4_issue<CH, RH>(pq, reinterpret_cast<const u32x4*>(layer_ptr(s_tab, li + 1, kLQkvW)), reinterpret_cast<const uint32_t*>(layer_ptr(s_tab, li + 1, kLQkvS)),
-                       q0, min(qn, RH), UH, gsh, ln);
+      w4_issue<CH, RQ>(pq, layer_ptr(s_tab, li + 1, kLQkvW), layer_ptr(s_tab, li + 1, kLQkvS),
+                       q0, min(qn, RQ), UH, gsh, ln);
     }
     if (!grid_wait(sync, gen, &s_flag)) return;
     // ---------------- down = W_down . act
@@ -950,13 +952,14 @@ __global__ void __launch_bounds__(kStepThreads, 1) decode_step_kernel(const Step
       StageRaw<Cfg::SI> sa;
       stage_issue<Cfg::SI>(sa, act, nullptr, nullptr, I >> 3, tl);
       stage_finish<Cfg::SI, true>(sa, false, nullptr, d.eps, I, nullptr, lds, s_red, tl);
-      w4_wave<CI, RI, kEpiRows>(pdn, reinterpret_cast<const u32x4*>(layer_ptr(s_tab, li, kLDownW)),
-                                reinterpret_cast<const uint32_t*>(layer_ptr(s_tab, li, kLDownS)), d0, dn, UI, gsh, lds, s_out, bh, ln);
+      w4_wave<CI, RI, kEpiRows>(pdn, layer_ptr(s_tab, li, kLDownW),
+                                layer_ptr(s_tab, li, kLDownS), d0, dn, UI, gsh, lds, s_out, bh, ln);
       w4_flush(s_out, down, bh, bhn, tl);
     }
     grid_arrive(sync, ++gen);
     if (li + 1 < d.n_layers) {
-      attn_prefetch<D>(ap, sd, reinterpret_cast<const f16*>(layer_ptr(s_tab, li + 1, kLKc)), reinterpret_cast<const f16*>(layer_ptr(s_tab, li + 1, kLVc)), akvh, asplit,
+      attn_prefetch<D>(ap, sd, reinterpret_cast<const f16*>(layer_ptr(s_tab, li + 1, kLKc)),
+                       reinterpret_cast<const f16*>(layer_ptr(s_tab, li + 1, kLVc)), akvh, asplit,
                        nt, alive, wave, ln);
     }
     if (!grid_wait(sync, gen, &s_flag)) return;

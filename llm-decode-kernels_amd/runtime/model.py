@@ -280,6 +280,17 @@ class Model:
         self.step_desc = d
         self.graph = None
 
+    def set_persistent(self, on=True):
+        """Switch the decode step between the persistent launch (dk_decode_step) and the multi-launch sequence, on
+        the same weights and cache; the next prepare() captures the chosen step."""
+        if on:
+            if getattr(self, "step_layers", None) is None:
+                self._setup_step()
+            self._step_partition(self.ctx_cap)
+        else:
+            self.step_desc = None
+        self.graph = None
+
     def step_status(self):
         """0 after normal persistent steps; 1 if a grid barrier timed out (the outputs are then invalid and the sync
         words are reset here)."""

@@ -261,3 +261,46 @@ def test_model_rejects_ref_backend():
     from runtime.synth import LlamaShape
     with pytest.raises(ValueError, match="oracle.decode_ref"):
         Model({}, LlamaShape(128, 1, 2, 1, 256, 64), DecodeConfig(backend="ref", device="cpu"))
+
+
+def _step_desc(**kw):
+    """A dk_step_desc with TinyLlama sizes and dummy (never dereferenced) pointers; kw overrides fields."""
+    d = ext.StepDesc()
+    vals = dict(n_layers=22, hidden=2048, n_q=32, n_kv=4, head_dim=64, inter=5632, vocab=32000, group=128, eps=1e-5,
+                max_pos=4096, n_bt=257, n_pages=257, page=16, part_size=128, max_splits=16, work_bytes=1 << 24)
+    for name, _ in ext.StepDesc._fields_:
+        if name not in vals:
+            vals[name] = 0x1000  # aligned dummy address
+    vals.update(kw)
+    for k, v in vals.items():
+        setattr(d, k, v)
+    return d
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(work=None), 1, "null pointer"),
+    (dict(head_dim=96), 4, "head_dim must be 64 or 128"),
+    (dict(n_layers=65), 3, "at most 64 layers"),
+    (dict(n_q=30), 3, "n_q / n_kv"),
+    (dict(n_q=32, n_kv=2), 3, "<= 8"),
+    (dict(hidden=4096), 3, "hidden must equal n_q * head_dim"),
+    (dict(inter=8192), 3, "inter <= 6144"),
+    (dict(group=96), 4, "group must be a power of two"),
+    (dict(page=8), 4, "page must be a power of two >= 16"),
+    (dict(part_size=64), 4, "part_size must be 128 or 256"),
+])
+def test_decode_step_validation(lib, kw, code, msg):
+    """dk_decode_step rejects bad descriptors on the host, before any HIP call."""
+    d = _step_desc(**kw)
+    assert lib.dk_decode_step(ctypes.byref(d), None) == code
+    assert msg in lib.dk_last_error().decode()
+
+
+def test_decode_step_null_descriptor_and_work_bytes(lib):
+    assert lib.dk_decode_step(None, None) == 1
+    assert lib.dk_decode_step_work_bytes(None) == 0
+    d = _step_desc()
+    one = lib.dk_decode_step_work_bytes(ctypes.byref(d))
+    d2 = _step_desc(n_layers=11)
+    # per-layer slots: half the layers, half the bytes; every slot 256-byte aligned
+    assert one > 0 and one % 256 == 0 and lib.dk_decode_step_work_bytes(ctypes.byref(d2)) * 2 == one
