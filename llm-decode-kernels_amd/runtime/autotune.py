@@ -14,7 +14,7 @@ cold weights (runtime.timing), and writes
 The runtime (runtime.model.Model.gemv_cfg) reads "best"; 3-element entries [R, warps, pf] of the reference's schema
 are read as stage 2. Run:  python -m runtime.autotune [--shapes tinyllama,llama3_8b,baseline] [--groups 128]
 With --attention it tunes the decode attention instead (kernel and split size per head dim and context) and writes
-configs/attn_policy.json.
+configs/attn_policy.json; with --step it chooses the decode step's GEMV configurations by the step time ("best_step").
 """
 import argparse
 import json
@@ -297,6 +297,72 @@ def tune_attention(dims=(64, 128), contexts=ATTN_CONTEXTS, path=ATTN_PATH, log=p
     return out
 
 
+# ------------------------------------------------------------------------------------------ GEMVs inside the step
+STEP_MODELS = {"tinyllama": ("TINYLLAMA", "fp16", 512), "llama3_8b": ("LLAMA3_8B", "int4", 4096)}
+
+
+def step_slots(model):
+    """The GEMV launches of one decode step that the in-step tuner varies: (table kind, projection, candidates).
+    Kinds: "norm" (qkv behind the fused residual + RMSNorm), "plain" (o, down; the INT4 head when the norm does not
+    pay inside it), "gate_up" (gate|up with the SwiGLU epilogue), "f16_norm" (the fp16 head behind the final norm)."""
+    lw = model.layers[0]
+    slots = [("norm", lw["qkv"], fused_candidates("rmsnorm")), ("plain", lw["o"], fused_candidates("rmsnorm")),
+             ("gate_up", lw["gu"], fused_candidates("gate_up")), ("plain", lw["down"], fused_candidates("rmsnorm"))]
+    head = model.lm_head
+    if head.quant:
+        kind = "norm" if model.norm_fusion_pays(head) else "plain"
+        slots.append((kind, head, fused_candidates("rmsnorm")))
+    elif model.use_f16_gemv(head):
+        slots.append(("f16_norm", head, f16_candidates(head.K)))
+    return slots
+
+
+def tune_step(models=("tinyllama", "llama3_8b"), path=CONFIG, rounds=2, log=print):
+    """Writes "best_step" into configs/autotune.json: {"kind:NxK_G": config} for the GEMVs of the decode step, each
+    chosen by the graph-replayed step time of the model it belongs to (coordinate descent over the launches, `rounds`
+    passes). At batch 1 these GEMVs are latency-bound inside the step, where a configuration that keeps every row of
+    a workgroup in flight at once can win although it loses in isolated cold launches; the isolated tables stay the
+    fallback for shapes the step tuner has not seen."""
+    from . import synth
+    from .model import DecodeConfig, Model
+    old = json.load(open(path)) if pathlib.Path(path).exists() else {}
+    table = dict(old.get("best_step", {}))
+    for name in models:
+        shape_name, head, ctx = STEP_MODELS[name]
+        shape = getattr(synth, shape_name)
+        model = Model(synth.SyntheticLlama(shape, seed=0), shape, DecodeConfig(lm_head=head, max_ctx=ctx + 64))
+        model.prepare(ctx + 48)
+        base = step_time_us(model, ctx)
+        log(f"  {name}: step {base:.1f} us with the isolated tables")
+        for _ in range(rounds):
+            for kind, lin, cands in step_slots(model):
+                key = model.step_key(kind, lin)
+                cur = model.step_cfg_override.pop(key, None)
+                isolated = {"plain": model.gemv_cfg, "norm": model.gemv_norm_cfg, "gate_up": model.gemv_gate_up_cfg,
+                            "f16_norm": lambda l: model.gemv_f16_cfg(l, norm=True)}[kind](lin)
+                cands = list(dict.fromkeys([tuple(c) for c in cands] + [tuple(isolated)]))
+                times = {}
+                for c in cands:
+                    model.step_cfg_override[key] = tuple(c)
+                    model.capture()
+                    times[tuple(c)] = step_time_us(model, ctx)
+                for c in sorted(times, key=times.get)[:3]:  # confirm the leaders
+                    model.step_cfg_override[key] = c
+                    model.capture()
+                    times[c] = min(times[c], step_time_us(model, ctx))
+                best = min(times, key=times.get)
+                model.step_cfg_override[key] = best
+                log(f"  {name} {key}: {list(best)} {times[best]:.1f} us per step (was {list(cur) if cur else None})")
+        model.capture()
+        log(f"  {name}: step {step_time_us(model, ctx):.1f} us with the in-step choices (from {base:.1f})")
+        table.update({k: list(v) for k, v in model.step_cfg_override.items()})
+        del model
+        torch.cuda.empty_cache()
+    out = dict(old, best_step=table)
+    write_table(out, path)
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--shapes", default="tinyllama,llama3_8b,baseline")
@@ -304,10 +370,14 @@ def main(argv=None):
     ap.add_argument("--reps", type=int, default=5)
     ap.add_argument("--out", default=None)
     ap.add_argument("--attention", action="store_true", help="tune the attention policy instead of the GEMVs")
+    ap.add_argument("--step", action="store_true", help="tune the decode step's GEMV launches inside the step")
     a = ap.parse_args(argv)
     log = lambda *s: print(*s, flush=True)
     if a.attention:
         tune_attention(path=a.out or ATTN_PATH, log=log)
+        return
+    if a.step:
+        tune_step(path=a.out or CONFIG, log=log)
         return
     tune(a.shapes.split(","), tuple(int(g) for g in a.groups.split(",")), a.reps, a.out or CONFIG, log=log)
 

@@ -183,6 +183,7 @@ class Model:
         self.gemv_table, self.gemv_tile_table, self.gemv_norm_table, self.gemv_gate_up_table = {}, {}, {}, {}
         self.gemv_f16_table, self.gemv_f16_norm_table = {}, {}
         self.gemv_us, self.gemv_norm_us = {}, {}
+        self.step_cfg_override = {}
         if cfg.gemv_stage is None and Path(cfg.autotune_path).exists():
             tab = json.load(open(cfg.autotune_path))
             self.gemv_table, self.gemv_tile_table = tab.get("best", {}), tab.get("best_tile", {})
@@ -191,6 +192,8 @@ class Model:
             self.gemv_gate_up_table = tab.get("best_gate_up", {})
             self.gemv_f16_table = tab.get("best_f16", {})
             self.gemv_f16_norm_table = tab.get("best_f16_norm", {})
+            # configurations chosen by the decode step time (runtime.autotune.tune_step), ahead of the isolated tables
+            self.step_cfg_override = {k: tuple(v) for k, v in tab.get("best_step", {}).items()}
 
         # paged KV cache [L, 2, pages, n_kv, P, D]; one block table shared by all layers (one sequence)
         self.n_pages = (cfg.max_ctx + cfg.page - 1) // cfg.page + 1
@@ -344,9 +347,16 @@ class Model:
         below = [e for e in ents if e["max_ctx"] <= ctx_cap]
         return below[-1] if below else ents[0]
 
+    def step_key(self, kind, lin):
+        """Key of the in-step tuning table: "kind:NxK_G" (INT4) or "kind:NxK" (fp16)."""
+        return f"{kind}:{lin.N}x{lin.K}" + (f"_G{self.cfg.group}" if lin.quant else "")
+
     def gemv_cfg(self, lin):
         if self.cfg.gemv_stage is not None:
             return self.cfg.gemv_stage
+        e = self.step_cfg_override.get(self.step_key("plain", lin))
+        if e is not None:
+            return tuple(e)
         e = self.gemv_table.get(f"{lin.N}x{lin.K}_G{self.cfg.group}")
         if e is None:
             return default_gemv_config(lin.N, lin.K)
@@ -363,7 +373,9 @@ class Model:
     def gemv_norm_cfg(self, lin):
         """Configuration of the fused-norm GEMV: its own tuned entry (every workgroup recomputes the norm, so larger
         row tiles pay off), else 4-row tiles."""
-        e = self.gemv_norm_table.get(f"{lin.N}x{lin.K}_G{self.cfg.group}")
+        e = self.step_cfg_override.get(self.step_key("norm", lin))
+        if e is None:
+            e = self.gemv_norm_table.get(f"{lin.N}x{lin.K}_G{self.cfg.group}")
         return tuple(e) if e is not None else (4, 4, 0, 1)
 
     # in-graph time of the separate add_rmsnorm launch at hidden 2048-4096 on MI355X (decode-step kernel trace)
@@ -387,7 +399,8 @@ class Model:
         """Configuration of the gate|up GEMV with the SwiGLU epilogue: its tuned entry, else the fused-norm one; the
         row tile R * 2^pf must hold a gate/up pair."""
         key = f"{lin.N}x{lin.K}_G{self.cfg.group}"
-        e = self.gemv_gate_up_table.get(key) or self.gemv_norm_table.get(key) or (4, 4, 0, 1)
+        e = (self.step_cfg_override.get(self.step_key("gate_up", lin)) or self.gemv_gate_up_table.get(key)
+             or self.gemv_norm_table.get(key) or (4, 4, 0, 1))
         s, r, wv, pf = e
         if (r << pf) < 2:
             r = 2
@@ -410,7 +423,9 @@ class Model:
     def gemv_f16_cfg(self, lin, norm=False):
         """(R, waves, pf) of the fp16 GEMV (norm: the variant behind the final RMSNorm): tuned entry, else 2-row tiles
         (1 for K > 2048), 1 wave per workgroup, 4 tiles per wave."""
-        e = (self.gemv_f16_norm_table if norm else self.gemv_f16_table).get(f"{lin.N}x{lin.K}")
+        e = self.step_cfg_override.get(self.step_key("f16_norm", lin)) if norm else None
+        if e is None:
+            e = (self.gemv_f16_norm_table if norm else self.gemv_f16_table).get(f"{lin.N}x{lin.K}")
         return tuple(e) if e is not None else ((2 if lin.K <= 2048 else 1), 1, 2)
 
     def linear(self, lin: Linear, x, y):
