@@ -341,6 +341,8 @@ def main():
                          "step only; decode8b: the Llama-3-8B decode legs only; prefill: the TinyLlama prefill leg only; kernels: "
                          "the attention and fused-op kernels of configs 2 and 3 only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline leg")
+    ap.add_argument("--persistent", action="store_true",
+                    help="with --leg decode: time the persistent step (dk_decode_step) instead of the multi-launch one")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one GPU only: the batch-1 decode path is single-GPU by design and every box here "
@@ -392,6 +394,8 @@ def main():
     t0 = time.perf_counter()
     cap = max(2048, a.ctx) + a.steps + a.warmup + 16
     model = Model(SyntheticLlama(TINYLLAMA, seed=0), TINYLLAMA, DecodeConfig(lm_head="fp16", max_ctx=cap))
+    if a.persistent and a.leg == "decode":
+        model.set_persistent(True)
     model.prepare(a.ctx + a.steps + a.warmup + 16)
     log(f"model built + graph captured in {time.perf_counter() - t0:.1f}s (part_size {model.part_size}, "
         f"max_splits {model.max_splits})")

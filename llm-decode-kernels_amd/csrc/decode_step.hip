@@ -14,22 +14,25 @@
 //                 lane l takes the 32-weight columns l, l + 64, ... of each row, x comes from LDS (staged once per
 //                 workgroup, transposed so that the lanes of a step read consecutive 16-byte words), the row is summed
 //                 by DPP. The column arithmetic is the W4A16 GEMV's (w4_common.hpp): nibbles OR-ed into fp16 magic
-//                 numbers, v_dot2_f32_f16, offsets and zero point removed once per column, exact products.
+//                 numbers, v_dot2_f32_f16, offsets and zero point removed once per column, exact products. Row
+//                 results are gathered per workgroup in LDS and written with one coalesced store.
 //   attention     workgroup u owns (kv head u % n_kv, split u / n_kv); split = 8 waves x nt 16-token tiles
 //                 (part_size 128 nt); the lean MFMA arithmetic of paged_attention.hip (16 x 16 f16 tiles, p as fp16
 //                 hi + lo, one online-softmax round per wave, waves merged in LDS), RoPE of q and k and the KV append
 //                 by the split that owns *pos; one live split writes the output, else (o, m, l) partials.
-//   combine       wave h merges the partials of query head h with the log-sum-exp rule.
-// Data produced inside the launch (activations, residual, partials, barrier words) is written with device-scope
-// stores (write-through, coherent across the XCDs' L2s) and read with device-scope loads; weights, KV rows written by
-// earlier launches, tables and norm weights are ordinary loads.
+//   combine       up to kFuseSplits partials: inside the o projection's operand staging (every workgroup merges them
+//                 for its own copy); more: a phase of its own, wave h merging query head h.
+// Every activation, residual and partial has its own slot per layer in the caller's work buffer, written once per
+// launch (device-scope stores, write-through across the XCDs' L2s) before the barrier that precedes its reads, so no
+// cache can hold an older copy and the reads are ordinary cached loads.
 //
-// Grid barrier: every thread waits for its own stores (s_waitcnt 0), the workgroup meets at s_barrier, thread 0 adds 1
-// to the arrival counter of its group (workgroup % 8, eight counters on separate 256-byte lines, to spread the
-// atomics), and wave 0 polls the eight counters until each has reached (barriers so far) x (workgroups of the group).
-// The poll is bounded: after kSpinLimit rounds (about a second) the waiting workgroup sets the abort word and every
-// workgroup returns at its next poll, so a launch always ends. At the end every workgroup counts itself out; the last
-// one writes *tok / *pos and zeroes every counter, so the next launch (e.g. the next graph replay) starts from zero.
+// Grid barrier, in two halves: arrival (every thread waits for its own stores, the workgroup meets at s_barrier,
+// thread 0 adds 1 to its group's counter: workgroup % 32, 32 counters on separate 128-byte lines), then every wave
+// issues the loads of a later phase, then the wait (wave 0 polls the counters until each has reached (barriers so
+// far) x (workgroups of the group)). The poll is bounded: after kSpinLimit rounds (about a second) the waiting
+// workgroup sets the abort word and every workgroup returns at its next poll, so a launch always ends. At the end
+// every workgroup counts itself out; the last one writes *tok / *pos and zeroes every counter, so the next launch
+// (e.g. the next graph replay) starts from zero.
 #include "common.hpp"
 #include "launch.hpp"
 #include "w4_common.hpp"
