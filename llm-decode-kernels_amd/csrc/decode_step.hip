@@ -1091,8 +1091,6 @@ int launch_step_t(const StepDev& sd, int grid, hipStream_t st) {
 
 }  // namespace
 
-int decode_step_threads() { return kStepThreads; }
-
 // Limits of the two instances (head_dim 64: H <= 2048, I <= 6144; head_dim 128: H <= 4096, I <= 14336).
 bool decode_step_fits(int head_dim, int H, int I) {
   if (head_dim == 64) return H <= 2048 && I <= 6144;

@@ -133,7 +133,6 @@ __host__ __device__ inline StepLayout step_layout(int H, int n_q, int n_kv, int 
   L.layer = o;
   return L;
 }
-int decode_step_threads();
 bool decode_step_fits(int head_dim, int H, int I);
 int decode_step_grid(int head_dim);  // workgroups per launch on the current device (one per CU), -1 if unavailable
 int launch_decode_step(const dk_step_desc& d, int grid, hipStream_t st);
