@@ -99,6 +99,23 @@ int dk_gemv_w4a16_gate_up(int stage, int R, int warps, int pf, const void* packe
                           int N, int K, int group, void* stream);
 
 /*
+ * The qkv W4A16 GEMV with RoPE + KV append applied to its output: fuses gemv_w4a16 of the attention's qkv
+ * projection with rope_append (kernels/bindings.cpp:27-38 then the rope_append binding, as runtime/model.py:220-221
+ * calls them; no single counterpart in the reference's binding). The N = (n_q + 2 n_kv) * head_dim weight rows are
+ * stored per head as rotation pairs, row h*D + 2j = row h*D + j and row h*D + 2j + 1 = row h*D + j + D/2 of the
+ * reference's layout (a row permutation, quantized per row exactly as before). Writes qkv in the reference's order
+ * and the cache exactly as gemv_w4a16 followed by dk_rope_append would: q rotated in qkv, k and v as projected in
+ * qkv, rotated k and v at the cache slot of *pos (none when *pos is outside [0, max_pos) or its page is unmapped).
+ * Input: x as dk_gemv_w4a16 when norm_w is NULL (row, delta and x_out must then be NULL), else the residual +
+ * RMSNorm input of dk_gemv_w4a16_rmsnorm. stage must be 4 and R * 2^pf >= 2.
+ */
+int dk_gemv_w4a16_qkv_rope(int stage, int R, int warps, int pf, const void* packed, const void* sz, const void* x,
+                           const int64_t* row, const void* delta, const void* norm_w, float eps, void* x_out,
+                           void* qkv, const float* cos_t, const float* sin_t, const int32_t* pos, const int32_t* bt,
+                           void* kc, void* vc, int n_q, int n_kv, int head_dim, int page, int max_pos, int n_pages,
+                           int n_bt, int K, int group, void* stream);
+
+/*
  * fp16-weight GEMV y[N] = W[N, K] . x[K] (W row-major fp16, fp32 accumulation, fp16 out). Replaces the fp16 LM head's
  * torch.mm(x, W^T) (runtime/model.py:187 of the reference; cuBLAS there, no custom kernel). R rows per tile (1, 2, 4),
  * warps waves per workgroup (0 = 4; 1, 2, 4, 8), 2^pf tiles per wave (pf 0..3). K % 8 == 0, K <= 4096 and

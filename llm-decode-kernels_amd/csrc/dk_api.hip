@@ -152,6 +152,42 @@ int dk_gemv_w4a16_gate_up(int stage, int R, int warps, int pf, const void* packe
   return launched("gemv_w4a16_gate_up");
 }
 
+int dk_gemv_w4a16_qkv_rope(int stage, int R, int warps, int pf, const void* packed, const void* sz, const void* x,
+                           const int64_t* row, const void* delta, const void* norm_w, float eps, void* x_out,
+                           void* qkv, const float* cos_t, const float* sin_t, const int32_t* pos, const int32_t* bt,
+                           void* kc, void* vc, int n_q, int n_kv, int head_dim, int page, int max_pos, int n_pages,
+                           int n_bt, int K, int group, void* stream) {
+  if (head_dim != 64 && head_dim != 128)
+    return fail(DK_ERR_SHAPE, "gemv_w4a16_qkv_rope: head_dim must be 64 or 128, got %d", head_dim);
+  if (n_q <= 0 || n_kv <= 0 || n_q > 65535 || n_kv > 65535)
+    return fail(DK_ERR_SHAPE, "gemv_w4a16_qkv_rope: bad head counts (n_q=%d n_kv=%d)", n_q, n_kv);
+  const int N = (n_q + 2 * n_kv) * head_dim;
+  const int rc = check_fused_gemv("gemv_w4a16_qkv_rope", stage, R, warps, pf, packed, sz, N, K, group);
+  if (rc != DK_OK) return rc;
+  if ((R << pf) < 2)
+    return fail(DK_ERR_DOMAIN, "gemv_w4a16_qkv_rope: the row tile R * 2^pf must hold a rotation pair (>= 2), got R=%d "
+                "pf=%d", R, pf);
+  if (!x || !qkv || !cos_t || !sin_t || !pos || !bt || !kc || !vc)
+    return fail(DK_ERR_NULL, "gemv_w4a16_qkv_rope: null pointer argument");
+  if (!pow2(page)) return fail(DK_ERR_DOMAIN, "page size must be a power of two, got %d", page);
+  if (max_pos < 1 || n_pages < 1 || n_bt < 1)
+    return fail(DK_ERR_SHAPE, "gemv_w4a16_qkv_rope: empty rope table, cache or block table");
+  if (!norm_w && (row || delta || x_out))
+    return fail(DK_ERR_DOMAIN, "gemv_w4a16_qkv_rope: row, delta and x_out belong to the RMSNorm input (norm_w)");
+  if (!aligned16(x) || (norm_w && !aligned16(norm_w)) || (delta && !aligned16(delta)) || (x_out && !aligned16(x_out)))
+    return fail(DK_ERR_ALIGN, "x, delta, norm_w and x_out must be 16B aligned");
+  if (row && (reinterpret_cast<uintptr_t>(row) & 7u)) return fail(DK_ERR_ALIGN, "row must be 8B aligned");
+  if (x_out && (x_out == x || (delta && x_out == delta)))
+    return fail(DK_ERR_DOMAIN, "gemv_w4a16_qkv_rope: x_out must not alias x or delta (other workgroups still read them)");
+  if (qkv == x || (delta && qkv == delta))
+    return fail(DK_ERR_DOMAIN, "gemv_w4a16_qkv_rope: qkv must not alias x or delta");
+  clear_error();
+  dk::GemvInput in{x, row, delta, norm_w, eps, x_out,
+                   {cos_t, sin_t, pos, bt, kc, vc, n_q, n_kv, ilog2(head_dim), ilog2(page), max_pos, n_pages, n_bt}};
+  dk::launch_gemv_w4a16_fused(norm_w ? 1 : 0, 2, R, pf, packed, sz, in, qkv, N, K, ilog2(group), (hipStream_t)stream);
+  return launched("gemv_w4a16_qkv_rope");
+}
+
 // Checks shared by the fp16 GEMVs.
 static int check_gemv_f16(const char* what, int R, int warps, int pf, const void* w, const void* x, const void* y,
                           int N, int K) {

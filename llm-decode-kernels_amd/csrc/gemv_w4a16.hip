@@ -396,7 +396,21 @@ __device__ __forceinline__ void tile_input_finish(const GemvInput& in, TileRaw& 
 //               y[i] = silu_mul(fp16(row 2i), fp16(row 2i + 1))              (y has N / 2 entries)
 //               = swiglu (kernels/fused_swiglu.cu:7-21) of the gate|up GEMV's output, rounded exactly as the two
 //               separate ops round it. Needs an even tile (T * NT) so that a pair never straddles two workgroups.
-enum { kOutRows = 0, kOutSwiglu = 1 };
+//   kOutRope    the qkv projection with its rows stored per head as rotation pairs (row 2j of head h = row h*D + j,
+//               row 2j + 1 = row h*D + j + D/2 of the reference's layout) followed by the reference's rope_append
+//               (kernels/rope.cu, as restated by rope_append_kernel): y receives the qkv vector in the reference's
+//               order with q rotated and k, v as projected; rotated k and v go to the cache slot of *pos. Nothing
+//               is rotated or appended when *pos is outside [0, max_pos); no append when its page is unmapped.
+enum { kOutRows = 0, kOutSwiglu = 1, kOutRope = 2 };
+
+// (lo, hi) = (a c - b s, b c + a s) with both products rounded, as the reference's RoPE rounds them.
+__device__ __forceinline__ void rope_rotate(f16 a16, f16 b16, float c, float s, f16& lo, f16& hi) {
+#pragma clang fp contract(off)
+  const float a = (float)a16, b = (float)b16;
+  const float ac = a * c, bs = b * s, bc = b * c, as = a * s;
+  lo = (f16)(ac - bs);
+  hi = (f16)(bc + as);
+}
 
 #ifndef DK_TILE_DEPTH
 #define DK_TILE_DEPTH 2
@@ -410,7 +424,7 @@ template <int T, int NT, int PRO, int EPI>
 __global__ void __launch_bounds__(1024)
 gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, const GemvInput in,
                 f16* __restrict__ y, int N, int U, int gsh) {
-  static_assert(EPI == kOutRows || (T * NT) % 2 == 0, "gate/up pairs need an even row tile");
+  static_assert(EPI == kOutRows || (T * NT) % 2 == 0, "gate/up and rotation pairs need an even row tile");
   __shared__ float red[16][T * NT];
   __shared__ float s_ss[16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
@@ -419,6 +433,8 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
   const int uc = live ? u : U - 1;  // dead lanes load a valid column and contribute 0
   const int base = blockIdx.x * T * NT;
   const int NG = U >> gsh;
+  int rpos = -1;
+  if constexpr (EPI == kOutRope) rpos = *in.rope.pos;
 
   TileRaw raw;
   tile_input_load<PRO>(in, uc, U << 5, raw);
@@ -432,6 +448,25 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
   tile_input_finish<PRO>(in, raw, uc, live, U << 5, s_ss, wave, nw, xc);
   const ColumnSums cs = column_sums(xc);
   const NibbleMasks m = nibble_masks();
+  // rotation-pair operands of the RoPE epilogue, requested before the tiles are computed
+  const int hb = EPI == kOutRope ? in.rope.log2D - 1 : 0;
+  const int rp = (base >> 1) + tid, rhead = rp >> hb, ri = rp & ((1 << hb) - 1);
+  const bool rvalid = rpos >= 0 && rpos < in.rope.max_pos;
+  float rc = 1.f, rs = 0.f;
+  int rpage = -1;
+  if constexpr (EPI == kOutRope) {
+    if (tid < T * NT / 2 && 2 * rp + 1 < N && rvalid) {
+      if (rhead < in.rope.n_q + in.rope.n_kv) {
+        rc = in.rope.cos_t[((size_t)rpos << hb) + ri];
+        rs = in.rope.sin_t[((size_t)rpos << hb) + ri];
+      }
+      const int lp = rpos >> in.rope.log2P;
+      if (lp < in.rope.n_bt) {
+        rpage = in.rope.bt[lp];
+        if (rpage < 0 || rpage >= in.rope.n_pages) rpage = -1;
+      }
+    }
+  }
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     float v[T];
@@ -449,6 +484,30 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
       float acc = 0.f;
       for (int i = 0; i < nw; ++i) acc += red[i][tid];
       y[base + tid] = (f16)acc;
+    }
+  } else if constexpr (EPI == kOutRope) {
+    if (tid < T * NT / 2 && 2 * rp + 1 < N) {
+      float a = 0.f, b = 0.f;
+      for (int i = 0; i < nw; ++i) {
+        a += red[i][2 * tid];
+        b += red[i][2 * tid + 1];
+      }
+      const f16 a16 = (f16)a, b16 = (f16)b;
+      const int nq = in.rope.n_q, nkv = in.rope.n_kv, half = 1 << hb;
+      f16 lo = a16, hi = b16;
+      if (rvalid && rhead < nq + nkv) rope_rotate(a16, b16, rc, rs, lo, hi);
+      f16* yh = y + ((size_t)rhead << in.rope.log2D);
+      yh[ri] = rhead < nq ? lo : a16;
+      yh[ri + half] = rhead < nq ? hi : b16;
+      if (rvalid && rhead >= nq && rpage >= 0) {
+        const bool is_k = rhead < nq + nkv;
+        const int kvh = is_k ? rhead - nq : rhead - nq - nkv;
+        const int slot = rpos & ((1 << in.rope.log2P) - 1);
+        f16* dst = static_cast<f16*>(is_k ? in.rope.kc : in.rope.vc) +
+                   (((((size_t)rpage * nkv + kvh) << in.rope.log2P) + slot) << in.rope.log2D);
+        dst[ri] = lo;
+        dst[ri + half] = hi;
+      }
     }
   } else {
     if (tid < T * NT / 2 && base + 2 * tid + 1 < N) {
@@ -492,7 +551,7 @@ void launch_rows_p(int waves, int pf, const void* packed, const void* sz, const 
 template <int T, int NT, int PRO, int EPI>
 void launch_tile_nt(const void* packed, const void* sz, const GemvInput& in, void* y, int N, int K, int log2G,
                     hipStream_t st) {
-  if constexpr (EPI == kOutSwiglu && (T * NT) % 2 != 0) {
+  if constexpr (EPI != kOutRows && (T * NT) % 2 != 0) {
     return;  // rejected by the host checks (R * 2^pf >= 2); never instantiated as a kernel
   } else {
     const int U = K >> 5;
@@ -596,6 +655,13 @@ void launch_gemv_w4a16_fused(int prologue, int epilogue, int R, int pf, const vo
       launch_tile_r<kInRmsNorm, kOutSwiglu>(R, pf, packed, sz, in, y, N, K, log2G, st);
     else
       launch_tile_r<kInPlain, kOutSwiglu>(R, pf, packed, sz, in, y, N, K, log2G, st);
+    return;
+  }
+  if (epilogue == kOutRope) {
+    if (prologue == kInRmsNorm)
+      launch_tile_r<kInRmsNorm, kOutRope>(R, pf, packed, sz, in, y, N, K, log2G, st);
+    else
+      launch_tile_r<kInPlain, kOutRope>(R, pf, packed, sz, in, y, N, K, log2G, st);
     return;
   }
   if (prologue == kInRmsNorm)

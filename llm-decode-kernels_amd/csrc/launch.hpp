@@ -16,6 +16,17 @@ void launch_gemv_w4a16(int stage, int R, int waves, int pf, const void* packed, 
                        void* y, int N, int K, int log2G, hipStream_t st);
 // x operand of the fused row-tile GEMVs (prologue 0 = plain x, 1 = residual + RMSNorm, 2 = SwiGLU; see
 // gemv_w4a16.hip).
+// The RoPE + KV-append epilogue of the qkv GEMV: the arguments of the reference's rope_append op
+// (kernels/bindings.cpp rope_append) with the head count split into q and kv heads.
+struct GemvRope {
+  const float* cos_t;     // [max_pos, D / 2]
+  const float* sin_t;
+  const int32_t* pos;     // device position of the token
+  const int32_t* bt;      // block table [n_bt]
+  void* kc;               // [n_pages, n_kv, 2^log2P, D]
+  void* vc;
+  int n_q, n_kv, log2D, log2P, max_pos, n_pages, n_bt;
+};
 struct GemvInput {
   const void* x;          // plain / swiglu: the input vector; rmsnorm: the residual stream (or the embedding table)
   const int64_t* row;     // rmsnorm: device row index into x (embedding gather) or null
@@ -23,8 +34,10 @@ struct GemvInput {
   const void* norm_w;     // rmsnorm: weight
   float eps;
   void* x_out;            // rmsnorm: receives x + delta (written by workgroup 0) or null
+  GemvRope rope;          // epilogue 2 only
 };
-// epilogue 0 = one fp16 output per row, 1 = SwiGLU of interleaved gate / up row pairs (N / 2 outputs).
+// epilogue 0 = one fp16 output per row, 1 = SwiGLU of interleaved gate / up row pairs (N / 2 outputs), 2 = RoPE +
+// KV append of rotation-pair rows (qkv rows stored per head as j, j + D/2 for j < D/2; N outputs in head order).
 void launch_gemv_w4a16_fused(int prologue, int epilogue, int R, int pf, const void* packed, const void* sz,
                              const GemvInput& in, void* y, int N, int K, int log2G, hipStream_t st);
 // Default configuration for a shape: (stage, R, waves, pf).

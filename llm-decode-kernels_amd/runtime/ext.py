@@ -26,6 +26,8 @@ SIGNATURES = {
     "dk_gemv_w4a16_rmsnorm": ([_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _I, _I, _P], _I),
     "dk_gemv_w4a16_swiglu": ([_I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P], _I),
     "dk_gemv_w4a16_gate_up": ([_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _I, _I, _P], _I),
+    "dk_gemv_w4a16_qkv_rope": ([_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I,
+                                _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "dk_gemv_f16": ([_I, _I, _I, _P, _P, _P, _I, _I, _P], _I),
     "dk_gemv_f16_rmsnorm": ([_I, _I, _I, _P, _P, _P, _P, _F, _P, _P, _I, _I, _P], _I),
     "dk_gemm_w4a16": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _P], _I),
@@ -207,6 +209,38 @@ class DecodeKernels:
         self._call(self.lib.dk_gemv_w4a16_gate_up, int(stage), int(R), int(warps), int(pf), packed.data_ptr(),
                    sz.data_ptr(), x.data_ptr(), ptr(row), ptr(delta), ptr(norm_w), float(eps), ptr(x_out),
                    act.data_ptr(), N, K, int(group), _stream(x))
+
+    # gemv_w4a16 of the qkv rows stored as per-head rotation pairs followed by rope_append (kernels/bindings.cpp
+    # gemv_w4a16 then rope_append), one launch; the input is x itself (norm_w None) or the residual + RMSNorm input
+    def gemv_w4a16_qkv_rope(self, stage, R, warps, pf, packed, sz, x, row, delta, norm_w, eps, x_out, qkv, cos_t,
+                            sin_t, pos, bt, kc, vc, n_q, n_kv, group):
+        for t, n in ((packed, "packed"), (sz, "sz"), (x, "x"), (qkv, "qkv"), (cos_t, "cos_t"), (sin_t, "sin_t"),
+                     (pos, "pos"), (bt, "bt"), (kc, "kc"), (vc, "vc")):
+            _check_cuda(t, n)
+        for t, n in (row, "row"), (delta, "delta"), (norm_w, "norm_w"), (x_out, "x_out"):
+            if t is not None:
+                _check_cuda(t, n)
+        _check_dtype(packed, torch.int32, "packed")
+        _check_dtype(sz, torch.float16, "sz")
+        for t, n in ((x, "x"), (qkv, "qkv"), (kc, "kc"), (vc, "vc")):
+            _check_dtype(t, torch.float16, n)
+        for t, n in ((cos_t, "cos_t"), (sin_t, "sin_t")):
+            _check_dtype(t, torch.float32, n)
+        for t, n in ((pos, "pos"), (bt, "bt")):
+            _check_dtype(t, torch.int32, n)
+        if kc.dim() != 4 or vc.shape != kc.shape:
+            raise RuntimeError("gemv_w4a16_qkv_rope: cache must be [pages, n_kv, P, head_dim]")
+        D = kc.size(3)
+        K = packed.size(1) * 8
+        N = (n_q + 2 * n_kv) * D
+        if packed.size(0) != N or qkv.numel() != N or kc.size(1) != n_kv or cos_t.size(1) * 2 != D:
+            raise RuntimeError("gemv_w4a16_qkv_rope: packed / qkv rows, cache heads and rope table width disagree")
+        ptr = lambda t: None if t is None else t.data_ptr()
+        self._call(self.lib.dk_gemv_w4a16_qkv_rope, int(stage), int(R), int(warps), int(pf), packed.data_ptr(),
+                   sz.data_ptr(), x.data_ptr(), ptr(row), ptr(delta), ptr(norm_w), float(eps), ptr(x_out),
+                   qkv.data_ptr(), cos_t.data_ptr(), sin_t.data_ptr(), pos.data_ptr(), bt.data_ptr(), kc.data_ptr(),
+                   vc.data_ptr(), int(n_q), int(n_kv), D, kc.size(2), cos_t.size(0), kc.size(0), bt.numel(), K,
+                   int(group), _stream(x))
 
     def _f16_shape(self, w, x, y, what):
         for t, n in ((w, "w"), (x, "x"), (y, "y")):

@@ -59,7 +59,7 @@ class DecodeConfig:
     shuffle_pages: bool = True
     device: str = "cuda"
     seed: int = 0            # block-table permutation seed
-    fused_attention: bool = True   # dk_attention_decode (RoPE + append inside the split kernel) instead of
+    fused_attention: bool = True   # rope_epilogue off: dk_attention_decode (RoPE + append in the split kernel) vs
                                    # rope_append + paged_attention
     combine_in_split: bool = False # with fused_attention: the last split workgroup of each kv head merges the
                                    # partials (per-kv-head counters) instead of a second combine launch; its three
@@ -73,6 +73,10 @@ class DecodeConfig:
     persistent: bool = False       # the whole decode step as one launch (dk_decode_step: grid barriers between phases,
                                    # next-phase weights requested ahead); needs the fused INT4 body with the SwiGLU
                                    # epilogue layout
+    rope_epilogue: bool = True     # with fused_gemv: RoPE + KV append in the qkv GEMV's epilogue
+                                   # (dk_gemv_w4a16_qkv_rope over a rotation-pair copy of the qkv rows) and attention
+                                   # without RoPE (dk_paged_attention) instead of dk_attention_decode; on MI355X
+                                   # 1410 -> 1349 us per Llama-3-8B token at context 4096, unchanged on TinyLlama
     step_part_size: int = 0        # tokens per attention split of the persistent step (128 or 256: 8 waves x 1 or 2
                                    # tiles of 16; 0 = the smallest that fits the grid)
     swiglu: str = "epilogue"       # where SwiGLU runs when fused_gemv is on: "epilogue" = inside the gate|up GEMV
@@ -125,6 +129,13 @@ class Linear:
         return deinterleave_halves(t) if self.pairs_interleaved else t
 
 
+def rope_pair_rows(t, head_dim):
+    """Rows of each head of a qkv stack [h*D + j] -> rotation pairs: row h*D + 2j = h*D + j, row h*D + 2j + 1 =
+    h*D + j + D/2 (the layout dk_gemv_w4a16_qkv_rope reads)."""
+    nh, half = t.size(0) // head_dim, head_dim // 2
+    return t.view(nh, 2, half, *t.shape[1:]).transpose(1, 2).contiguous().view(t.shape)
+
+
 def interleave_halves(t):
     """[a_0 .. a_{n-1}, b_0 .. b_{n-1}] rows -> [a_0, b_0, a_1, b_1, ...]."""
     n = t.size(0) // 2
@@ -157,6 +168,7 @@ class Model:
             raise ValueError(f"swiglu {cfg.swiglu!r}: 'epilogue', 'prologue' or 'kernel'")
         self.use_fused_gemv = (cfg.fused and cfg.fused_gemv and quant and self.H <= 32768 and self.I <= 32768)
         self.gate_up_epilogue = self.use_fused_gemv and cfg.swiglu == "epilogue"
+        self.rope_epilogue = self.use_fused_gemv and cfg.rope_epilogue
         sd = hf_state
         g = lambda k: sd[k].half()
         self.emb = g("model.embed_tokens.weight").to(dev).contiguous()
@@ -167,6 +179,8 @@ class Model:
                               g(p + "self_attn.v_proj.weight")], 0)
             qkv = Linear(wqkv, cfg, quant, key=f"layers.{i}.qkv")
             del wqkv
+            if self.rope_epilogue:  # decode-only copy; prefill and the persistent step read the reference order
+                qkv.rope_rows = (rope_pair_rows(qkv.packed, self.D), rope_pair_rows(qkv.sz, self.D))
             wgu = torch.cat([g(p + "mlp.gate_proj.weight"), g(p + "mlp.up_proj.weight")], 0)
             gu = Linear(wgu, cfg, quant, interleave_pairs=self.gate_up_epilogue, key=f"layers.{i}.gu")
             del wgu
@@ -459,8 +473,30 @@ class Model:
         else:
             self.K.argmax_advance(self.logits, self.tok, self.pos)
 
+    def qkv_proj(self, lin: Linear, li, x_in, delta, w, x_out, row=None):
+        """qkv = W_qkv . x (w None: x is the normed input) or W_qkv . rmsnorm(x_in + delta); with the RoPE epilogue
+        the same launch also rotates q and appends k, v to layer li's cache."""
+        if not self.rope_epilogue:
+            if w is None:
+                self.linear(lin, x_in, self.qkv)
+            else:
+                self.linear_norm(lin, x_in, delta, w, x_out, self.qkv, row=row)
+            return
+        _, r, wv, pf = self.gemv_norm_cfg(lin)
+        if (r << pf) < 2:
+            r = 2
+        packed, sz = lin.rope_rows
+        self.K.gemv_w4a16_qkv_rope(4, r, wv, pf, packed, sz, x_in, row, delta, w, self.eps, x_out, self.qkv, self.cos,
+                                   self.sin, self.pos, self.bt, self.kv[li, 0], self.kv[li, 1], self.n_q, self.n_kv,
+                                   self.cfg.group)
+
     def attention(self, li):
         kc, vc = self.kv[li, 0], self.kv[li, 1]
+        if self.rope_epilogue:  # q rotated and k, v appended by the qkv GEMV
+            version = {3: 5, 2: 4}.get(self.attn_impl, 2)
+            self.K.paged_attention(self.qkv[: self.n_q * self.D], kc, vc, self.bt, self.pos, self.part_size,
+                                   self.o_part, self.m_part, self.l_part, self.attn, version)
+            return
         if self.cfg.fused_attention:
             self.K.attention_decode(self.qkv, self.cos, self.sin, self.pos, self.bt, kc, vc, self.n_q, self.n_kv,
                                     self.part_size, self.o_part, self.m_part, self.l_part, self.attn,
@@ -505,13 +541,13 @@ class Model:
         delta = None
         for li, lw in enumerate(self.layers):
             if li == 0:
-                self.linear_norm(lw["qkv"], self.emb, None, lw["ln1"], cur, self.qkv, row=self.tok)
+                self.qkv_proj(lw["qkv"], li, self.emb, None, lw["ln1"], cur, row=self.tok)
             elif self.norm_fusion_pays(lw["qkv"]):
-                self.linear_norm(lw["qkv"], cur, delta, lw["ln1"], nxt, self.qkv)
+                self.qkv_proj(lw["qkv"], li, cur, delta, lw["ln1"], nxt)
                 cur, nxt = nxt, cur
             else:
                 self.K.add_rmsnorm(cur, delta, lw["ln1"], self.normed, self.eps)
-                self.linear(lw["qkv"], self.normed, self.qkv)
+                self.qkv_proj(lw["qkv"], li, self.normed, None, None, None)
             self.attention(li)
             self.linear(lw["o"], self.attn.view(-1), self.o)
             if self.gate_up_epilogue:

@@ -609,3 +609,72 @@ def test_fused_step_equals_unfused_step(K):
         assert err <= 5e-3, err
     # the gate|up SwiGLU epilogue rounds exactly where the separate swiglu kernel does
     assert torch.equal(out[1], out[3])
+
+
+# ------------------------------------------------------------------------------- qkv GEMV with the RoPE + append epilogue
+@pytest.mark.parametrize("D,n_q,n_kv,norm", [(64, 4, 2, True), (64, 6, 2, False), (128, 4, 1, True),
+                                             (128, 2, 2, False)])
+def test_gemv_qkv_rope_epilogue(K, D, n_q, n_kv, norm):
+    """qkv = W_qkv . x with RoPE + KV append in one launch over rotation-pair rows: bit-exact against the two
+    separate HIP ops (gemv_w4a16 / gemv_w4a16_rmsnorm on the reference's row order, then rope_append, whose own test
+    holds it to the oracle) for the qkv vector and both caches; positions on mapped pages, on an unmapped page (no
+    append) and outside [0, max_pos) (nothing rotated or appended)."""
+    from runtime.model import rope_pair_rows, rope_tables
+    G, Kd = 64, (256 if D == 64 else 512)
+    N = (n_q + 2 * n_kv) * D
+    _, packed, sz = _quantized(K, N, Kd, G, seed=N + Kd)
+    pk, szp = rope_pair_rows(packed, D), rope_pair_rows(sz, D)
+    cos, sin = (t.to(DEV) for t in rope_tables(64, D, 10000.0))
+    bt = torch.tensor([3, 0, -1, 5], dtype=torch.int32, device=DEV)  # positions 32..47 sit on an unmapped page
+    g = gen(N + D)
+    xd = (torch.randn(Kd, generator=g) * (1 if norm else 0.5)).half().to(DEV)
+    dd = torch.randn(Kd, generator=g).half().to(DEV) if norm else None
+    nwd = (1 + 0.1 * torch.randn(Kd, generator=g)).half().to(DEV) if norm else None
+    for pos_v in (0, 21, 37, 63, 64, -1):
+        for cfg in ((4, 2, 0, 0), (4, 1, 0, 1), (4, 4, 0, 2)):
+            print(f"qkv rope D{D} n_q{n_q} n_kv{n_kv} norm={norm} pos {pos_v} cfg {cfg}", flush=True)
+            pos = torch.tensor([pos_v], dtype=torch.int32, device=DEV)
+            kc_a = torch.randn(6, n_kv, 16, D, generator=g).half().to(DEV)
+            vc_a = torch.randn(6, n_kv, 16, D, generator=g).half().to(DEV)
+            kc_b, vc_b = kc_a.clone(), vc_a.clone()
+            qa = torch.empty(N, dtype=torch.half, device=DEV)
+            qb = torch.empty(N, dtype=torch.half, device=DEV)
+            if norm:
+                xo_a, xo_b = torch.empty_like(xd), torch.empty_like(xd)
+                K.gemv_w4a16_qkv_rope(*cfg, pk, szp, xd, None, dd, nwd, 1e-5, xo_a, qa, cos, sin, pos, bt, kc_a,
+                                      vc_a, n_q, n_kv, G)
+                K.gemv_w4a16_rmsnorm(*cfg, packed, sz, xd, None, dd, nwd, 1e-5, xo_b, qb, G)
+                assert torch.equal(xo_a, xo_b)
+            else:
+                K.gemv_w4a16_qkv_rope(*cfg, pk, szp, xd, None, None, None, 0.0, None, qa, cos, sin, pos, bt, kc_a,
+                                      vc_a, n_q, n_kv, G)
+                K.gemv_w4a16(*cfg, packed, sz, xd, qb, G)
+            K.rope_append(qb, cos, sin, pos, bt, kc_b, vc_b, n_q, n_kv)
+            assert torch.equal(qa, qb), f"qkv pos {pos_v} {cfg}"
+            assert torch.equal(kc_a, kc_b), f"k cache pos {pos_v} {cfg}"
+            assert torch.equal(vc_a, vc_b), f"v cache pos {pos_v} {cfg}"
+
+
+@pytest.mark.parametrize("shape_t", [(256, 2, 4, 2, 512, 1000), (512, 2, 4, 2, 1024, 1000)])
+def test_decode_rope_epilogue_matches_default_step(K, shape_t):
+    """The decode step with RoPE + append in the qkv GEMV and attention without RoPE gives the default step's logits
+    (attention_decode with RoPE inside) within 5e-3 and the same KV cache bit for bit, over 300 teacher-forced
+    tokens (several attention splits); head dims 64 and 128."""
+    from runtime.model import DecodeConfig, Model
+    from runtime.synth import LlamaShape, SyntheticLlama
+    shape = LlamaShape(*shape_t)
+    print(f"rope epilogue decode {shape_t}", flush=True)
+    sd = SyntheticLlama(shape, seed=3, device=DEV, std=0.05, norm_std=0.1)
+    a = Model(sd, shape, DecodeConfig(max_ctx=512, device=DEV, rope_epilogue=False))
+    b = Model(sd, shape, DecodeConfig(max_ctx=512, device=DEV, rope_epilogue=True))
+    assert b.rope_epilogue
+    for m in (a, b):
+        m.prepare(512)
+        m.reset(0)
+    toks = torch.randint(0, shape.vocab_size, (300,), generator=torch.Generator().manual_seed(0)).tolist()
+    la = a.teacher_force(toks, collect_logits=True)
+    lb = b.teacher_force(toks, collect_logits=True)
+    for i in (0, 1, 150, 299):
+        assert_close(lb[i], la[i], 5e-3, f"logits at position {i}")
+    rows = a.bt[: (300 + 15) // 16].long()
+    assert torch.equal(b.kv[:, :, rows], a.kv[:, :, rows])
