@@ -164,6 +164,35 @@ def test_gate_up_validation(lib, kw, code, msg):
     assert rc == code and msg in m, (rc, m)
 
 
+def _qkv_rope(lib, **kw):
+    a = dict(stage=4, R=2, warps=0, pf=0, packed=A16, sz=A16, x=A16, row=None, delta=None, norm_w=A16, eps=1e-5,
+             x_out=None, qkv=B16, cos_t=A16, sin_t=A16, pos=A16, bt=A16, kc=A16, vc=A16, n_q=4, n_kv=2,
+             head_dim=64, page=16, max_pos=64, n_pages=4, n_bt=4, K=256, group=128)
+    a.update(kw)
+    return _err(lib, lib.dk_gemv_w4a16_qkv_rope(*a.values(), None))
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(head_dim=96), 3, "head_dim must be 64 or 128"),
+    (dict(n_kv=0), 3, "bad head counts"),
+    (dict(stage=3), 4, "stage 4 only"),
+    (dict(R=1, pf=0), 4, "rotation pair"),
+    (dict(cos_t=None), 1, "null pointer"),
+    (dict(vc=None), 1, "null pointer"),
+    (dict(page=24), 4, "power of two"),
+    (dict(max_pos=0), 3, "empty rope table"),
+    (dict(n_bt=0), 3, "empty rope table"),
+    (dict(norm_w=None, delta=A16), 4, "RMSNorm input"),
+    (dict(x=A16 + 2), 2, "16B aligned"),
+    (dict(qkv=A16), 4, "must not alias"),
+    (dict(K=250), 3, "multiple of 32"),
+])
+def test_qkv_rope_validation(lib, kw, code, msg):
+    """dk_gemv_w4a16_qkv_rope rejects bad shapes, tiles, pointers and aliasing before any launch."""
+    rc, m = _qkv_rope(lib, **kw)
+    assert rc == code and msg in m, (rc, m)
+
+
 def test_fused_gemv_validation(lib):
     assert _fused(lib, lib.dk_gemv_w4a16_rmsnorm, stage=3)[0] == 4
     assert _fused(lib, lib.dk_gemv_w4a16_rmsnorm, norm_w=None)[0] == 1
