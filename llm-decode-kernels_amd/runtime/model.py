@@ -482,7 +482,8 @@ class Model:
             else:
                 self.linear_norm(lin, x_in, delta, w, x_out, self.qkv, row=row)
             return
-        _, r, wv, pf = self.gemv_norm_cfg(lin)
+        e = self.step_cfg_override.get(self.step_key("rope", lin))
+        _, r, wv, pf = tuple(e) if e is not None else self.gemv_norm_cfg(lin)
         if (r << pf) < 2:
             r = 2
         packed, sz = lin.rope_rows
