@@ -12,14 +12,19 @@ Also measured in the same run (extra keys of the JSON line):
                 configuration: algorithmic bytes per launch (packed + scale/zero + x + y = 31,232,000 B) / mean launch
                 duration. The duration comes from HIP events around a hipGraph of back-to-back launches on the
                 capture stream, each launch reading a different cold copy of the weights (> 2.5 x the 256 MB MALL),
-                so every byte comes from HBM. `traffic` is the HBM bytes per launch measured by rocprofv3 PMC
-                (FETCH_SIZE + WRITE_SIZE, scaled by a plain read / copy of known size) when that summary is present
-                in profiles/, else null.
+                so every byte comes from HBM. `traffic` is the HBM bytes per launch measured in this run: two
+                rocprofv3 counter passes (FETCH_SIZE, then WRITE_SIZE) over `bench.py --leg gemv` in child
+                processes, each scaled by what the same counter reads for a plain read / copy of known size in the
+                same child (null, with the reason, when rocprofv3 or the counters are unavailable).
   gemv_14336x4096, gemv_cfg1   the other BASELINE GEMV shapes the same way;
   read_ceiling  the library's bw_read streaming the same number of bytes: what a kernel that only reads gets;
   decode        per-token statistics, the bytes-per-token roofline of the step, ctx 2048 as well;
+  clocks        shader / memory clock and temperature of the GPU sampled from sysfs while each leg runs (the role of
+                the reference's NVML sampling, bench/timing.py:35-49,119-138), so a slow box can be told from a slow
+                kernel;
   cpu_baseline  the CPU oracle's decode step (oracle.decode_ref: the reference backend="ref" composition, torch fp32
-                matvec) on the host cores, a bounded sample of tokens on the same weights.
+                matvec) on the host cores: median and IQR of 30 timed steps after 5 warm-up steps, at ctx 512 (the
+                value) and at ctx 2048, on the same weights.
 
 --gpus N > 1 exits with a message: the path is single-GPU by design (one GPU per box here).
 --leg gemv runs only the GEMV roofline leg (used under rocprofv3 for the kernel trace and counter passes); --leg
@@ -41,11 +46,133 @@ for _p in (str(ROOT), str(ROOT / "llm-decode-kernels_amd")):
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "W4A16 GEMV HBM GB/s (% of peak) + batch-1 decode tokens/s, TinyLlama shape"
-PMC_SUMMARY = ROOT / "profiles" / "gemv_w4a16_4096x14336_pmc.json"
+# second TinyLlama decode leg (BASELINE config 4 names contexts 512 and 2048) and the prefill prompt
+CTX_LONG, CTX_LONG_STEPS, CTX_LONG_WARMUP = 2048, 64, 8
+PREFILL_TOKENS = 512
+GEMV_KERNEL = "gemv_w4a16"          # kernel-name substring of the roofline GEMV in counter output
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def leg_caps(ctx, steps, warmup):
+    """Context caps of the legs that share one TinyLlama model. A decode leg starts at `ctx`, runs `warmup` steps,
+    resets to `ctx` and runs `steps` steps, so its cap is ctx + max(steps, warmup) (+ slack); the model's max_ctx
+    covers every cap that a later prepare() asks for, whatever --ctx / --steps / --warmup are."""
+    slack = 16
+    caps = {"decode": ctx + max(steps, warmup) + slack,
+            "decode_long": CTX_LONG + max(CTX_LONG_STEPS, CTX_LONG_WARMUP) + slack,
+            "prefill": PREFILL_TOKENS + slack}
+    caps["max_ctx"] = max(caps.values())
+    return caps
+
+
+def _pci_dir():
+    import torch
+    p = torch.cuda.get_device_properties(0)
+    return pathlib.Path(f"/sys/bus/pci/devices/{p.pci_domain_id:04x}:{p.pci_bus_id:02x}:{p.pci_device_id:02x}.0")
+
+
+def read_clocks(pci):
+    """One sample: current shader / memory / fabric clock (the starred line of pp_dpm_*) and edge temperature."""
+    out = {}
+    for key, f in (("sclk_mhz", "pp_dpm_sclk"), ("mclk_mhz", "pp_dpm_mclk"), ("fclk_mhz", "pp_dpm_fclk")):
+        try:
+            for line in (pci / f).read_text().splitlines():
+                if line.rstrip().endswith("*"):
+                    out[key] = int("".join(ch for ch in line.split(":", 1)[1] if ch.isdigit()))
+        except (OSError, ValueError, IndexError):
+            pass
+    for t in sorted(pci.glob("hwmon/hwmon*/temp1_input")):
+        try:
+            out["temp_c"] = int(t.read_text()) / 1000
+        except (OSError, ValueError):
+            pass
+    return out
+
+
+class ClockSampler:
+    """Samples read_clocks every `period` s in a thread while a leg runs; summary() gives per-field min / median /
+    max and the sample count (empty when sysfs exposes no clock for this device)."""
+
+    def __init__(self, period=0.02):
+        import threading
+        self.period, self.samples, self.stop = period, [], threading.Event()
+        try:
+            self.pci = _pci_dir()
+        except Exception:                                 # noqa: BLE001 (no device properties: no samples)
+            self.pci = None
+        self.thread = threading.Thread(target=self._run, daemon=True)
+
+    def _run(self):
+        while not self.stop.is_set():
+            s = read_clocks(self.pci)
+            if s:
+                self.samples.append(s)
+            self.stop.wait(self.period)
+
+    def __enter__(self):
+        if self.pci is not None:
+            self.thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        self.stop.set()
+        if self.thread.is_alive():
+            self.thread.join()
+
+    def summary(self):
+        out = {"samples": len(self.samples)}
+        for k in ("sclk_mhz", "mclk_mhz", "fclk_mhz", "temp_c"):
+            v = sorted(s[k] for s in self.samples if k in s)
+            if v:
+                out[k] = {"min": v[0], "median": v[len(v) // 2], "max": v[-1]}
+        return out
+
+
+def traffic_leg(nbytes, timeout=180):
+    """HBM bytes per launch of the roofline GEMV, measured now: rocprofv3 runs `bench.py --leg gemv` twice in a child
+    process, once collecting FETCH_SIZE and once WRITE_SIZE (one counter group per pass); each counter is scaled by
+    what it reads for the bw_read / copy kernels of known size that the same child runs (runtime.rocprof_summary.pmc).
+    Returns (summary dict, None) or (None, reason)."""
+    import shutil
+    import signal
+    import subprocess
+    import tempfile
+    from runtime import rocprof_summary
+
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None, "rocprofv3 not on PATH"
+    tmp = pathlib.Path(tempfile.mkdtemp(prefix="dk_pmc_", dir="/tmp"))
+    env = {**os.environ, "TMPDIR": "/tmp"}
+    dirs = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tmp / counter.lower()
+        cmd = [exe, "--pmc", counter, "--output-format", "csv", "-d", str(d), "-o", "pmc", "--",
+               sys.executable, str(ROOT / "bench.py"), "--leg", "gemv"]
+        log(f"traffic: rocprofv3 --pmc {counter} over bench.py --leg gemv")
+        p = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL, stderr=subprocess.PIPE,
+                             start_new_session=True)
+        try:
+            _, err = p.communicate(timeout=timeout)
+        except subprocess.TimeoutExpired:
+            os.killpg(p.pid, signal.SIGKILL)
+            p.communicate()
+            return None, f"rocprofv3 --pmc {counter} did not finish in {timeout} s"
+        if p.returncode != 0 and not list(d.glob("**/*counter_collection.csv")):
+            tail = err.decode(errors="replace").strip().splitlines()[-3:]
+            return None, f"rocprofv3 --pmc {counter} exited {p.returncode}: {' | '.join(tail)}"
+        dirs[counter] = str(d)
+    try:
+        res = rocprof_summary.pmc(dirs["FETCH_SIZE"], dirs["WRITE_SIZE"], GEMV_KERNEL, nbytes)
+    except SystemExit as e:
+        return None, f"counter output incomplete: {e}"
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    res["traffic_over_algorithmic"] = round(res["hbm_bytes_per_launch"] / nbytes, 4)
+    return res, None
 
 
 def tuned_config(N, K, G=128):
@@ -308,26 +435,48 @@ def gemm_timing(model, lin, M, epilogue, reps=20):
             "hipblaslt_fp16_tflops": round(fl / ub / 1e6, 1)}
 
 
-def cpu_baseline_leg(model, shape, ctx, budget_s=15.0, max_tokens=64):
-    """Tokens/s of the CPU oracle decode step on the host cores (a bounded sample)."""
+def step_stats(times_s):
+    """Median and interquartile range of per-step times (the reference's statistics, bench/timing.py:134-138)."""
+    t = sorted(times_s)
+    q = statistics.quantiles(t, n=4, method="inclusive")
+    return {"n": len(t), "median_ms": round(statistics.median(t) * 1e3, 2), "q1_ms": round(q[0] * 1e3, 2),
+            "q3_ms": round(q[2] * 1e3, 2), "iqr_ms": round((q[2] - q[0]) * 1e3, 2)}
+
+
+def cpu_baseline_leg(model, shape, ctxs=(512, CTX_LONG), warmup=5, steps=30):
+    """The CPU oracle's decode step on the host cores: `warmup` untimed then `steps` timed steps at each context
+    (positions ctx, ctx + 1, ...; the cache below ctx holds zeros, which costs the same as real keys), timed one step
+    at a time with perf_counter. value = 1 / median step time at the first context."""
     import torch
     from __graft_entry__ import _ref_weights
     from oracle.decode_ref import RefDecoder
 
     cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     torch.set_num_threads(cores)
-    cap = ctx + max_tokens + 2
-    dec = RefDecoder(_ref_weights(model, shape), shape, max_ctx=cap, page=model.cfg.page,
-                     block_table=torch.arange(cap // model.cfg.page + 2, dtype=torch.int32))
-    dec.step(1, ctx)                                   # warm-up (first touch of the weights)
-    n, t0 = 0, time.perf_counter()
-    while n < max_tokens and (time.perf_counter() - t0) < budget_s:
-        dec.step(1 + n, ctx + 1 + n)
-        n += 1
-    dt = time.perf_counter() - t0
-    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"{n} TinyLlama decode steps of oracle.decode_ref (torch fp32 CPU restatement of the reference "
-                      f"backend='ref' composition) at ctx {ctx}, after 1 warm-up step, {dt:.1f} s"}
+    t0 = time.perf_counter()
+    weights = _ref_weights(model, shape)
+    prep = time.perf_counter() - t0
+    per_ctx = {}
+    for ctx in ctxs:
+        cap = ctx + warmup + steps + 2
+        dec = RefDecoder(weights, shape, max_ctx=cap, page=model.cfg.page,
+                         block_table=torch.arange(cap // model.cfg.page + 2, dtype=torch.int32))
+        times = []
+        for i in range(warmup + steps):
+            s = time.perf_counter()
+            dec.step(1 + i, ctx + i)
+            times.append(time.perf_counter() - s)
+        st = step_stats(times[warmup:])
+        st["tok_s"] = round(1e3 / st["median_ms"], 3)
+        per_ctx[str(ctx)] = st
+        log(f"cpu baseline ctx {ctx}: median {st['median_ms']} ms/token (IQR {st['iqr_ms']} ms) on {cores} cores")
+    first = per_ctx[str(ctxs[0])]
+    return {"value": first["tok_s"], "unit": "tok/s", "cores": cores, "kind": "port", "per_ctx": per_ctx,
+            "sample": f"TinyLlama decode steps of oracle.decode_ref (torch fp32 CPU restatement of the reference "
+                      f"backend='ref' composition, runtime/model.py:216-233) on the same dequantized weights: "
+                      f"{warmup} warm-up + {steps} timed steps at each of ctx {', '.join(map(str, ctxs))}; value = "
+                      f"1 / median step at ctx {ctxs[0]}; weights dequantized on the CPU once ({prep:.1f} s, "
+                      f"untimed)"}
 
 
 def main():
@@ -338,11 +487,10 @@ def main():
     ap.add_argument("--ctx", type=int, default=512)
     ap.add_argument("--leg", choices=("all", "gemv", "kernels", "decode", "decode8b", "prefill"), default="all",
                     help="gemv: the 4096x14336 GEMV and its calibration copies only; decode: the TinyLlama decode "
-                         "step only; decode8b: the Llama-3-8B decode legs only; prefill: the TinyLlama prefill leg only; kernels: "
-                         "the attention and fused-op kernels of configs 2 and 3 only")
+                         "step only; decode8b: the Llama-3-8B decode legs only; prefill: the TinyLlama prefill leg "
+                         "only; kernels: the attention and fused-op kernels of configs 2 and 3 only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline leg")
-    ap.add_argument("--persistent", action="store_true",
-                    help="with --leg decode: time the persistent step (dk_decode_step) instead of the multi-launch one")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one GPU only: the batch-1 decode path is single-GPU by design and every box here "
@@ -350,6 +498,15 @@ def main():
               f"gate|up column-parallel, o and down row-parallel with one all-reduce each, attention by kv head",
               file=sys.stderr)
         sys.exit(2)
+
+    from runtime.autotune import gemv_bytes
+
+    # the counter passes run in child processes before this process touches the GPU
+    traffic, traffic_note = None, "not measured (--no-traffic)"
+    if a.leg == "all" and not a.no_traffic:
+        traffic, traffic_note = traffic_leg(gemv_bytes(4096, 14336, 128))
+        log(f"traffic: {traffic['hbm_bytes_per_launch'] if traffic else None} B per launch "
+            f"({traffic['traffic_over_algorithmic'] if traffic else traffic_note})")
 
     import torch
     from runtime import ext
@@ -374,69 +531,63 @@ def main():
     from runtime.model import DecodeConfig, Model
     from runtime.synth import TINYLLAMA, SyntheticLlama
 
+    clocks = {}
+
+    def sampled(name, fn, *args, **kw):
+        with ClockSampler() as cs:
+            r = fn(*args, **kw)
+        clocks[name] = cs.summary()
+        return r
+
     # the standalone GEMV and kernel legs first, while no model occupies the device (cold weights either way); the
     # decode and prefill legs alone skip them, so that their kernel traces hold only the model's kernels
     if a.leg == "all":
-        g1 = gemv_leg(Kx, 4096, 14336)
+        g1 = sampled("gemv_4096x14336", gemv_leg, Kx, 4096, 14336)
         log(f"gemv 4096x14336 {g1['cfg']}: {g1['mean_us']:.3f} us/launch -> {g1['gbps']:.0f} GB/s ({g1['frac']:.1%})")
-        g2 = gemv_leg(Kx, 14336, 4096)
+        g2 = sampled("gemv_14336x4096", gemv_leg, Kx, 14336, 4096)
         log(f"gemv 14336x4096 {g2['cfg']}: {g2['mean_us']:.3f} us/launch -> {g2['gbps']:.0f} GB/s ({g2['frac']:.1%})")
-        g3 = gemv_leg(Kx, 5632, 2048)
+        g3 = sampled("gemv_5632x2048", gemv_leg, Kx, 5632, 2048)
         log(f"gemv 5632x2048 {g3['cfg']}: {g3['mean_us']:.3f} us/launch -> {g3['gbps']:.0f} GB/s ({g3['frac']:.1%})")
-        rc = read_ceiling_leg(Kx, g1["bytes"])
+        rc = sampled("read_ceiling", read_ceiling_leg, Kx, g1["bytes"])
         log(f"bw_read of {rc['bytes']} B: {rc['mean_us']:.3f} us -> {rc['gbps']:.0f} GB/s ({rc['frac']:.1%})")
-        kern = kernels_leg(Kx)
+        kern = sampled("kernels", kernels_leg, Kx)
         log("attention (cfg2) us: " + ", ".join(f"ctx {c}: ref op {v['paged_attention_v3_us']}, fused "
                                               f"{v['attention_decode_us']}" for c, v in kern["attention"].items()))
         log("fused ops (cfg3) us: " + ", ".join(f"{k} {v['us']}" for k, v in kern["fused"].items()))
 
-    log(f"device {dev_name}; building TinyLlama-shape W4A16 model")
+    caps = leg_caps(a.ctx, a.steps, a.warmup)
+    log(f"device {dev_name}; building TinyLlama-shape W4A16 model (max_ctx {caps['max_ctx']})")
     t0 = time.perf_counter()
-    cap = max(2048, a.ctx) + a.steps + a.warmup + 16
-    model = Model(SyntheticLlama(TINYLLAMA, seed=0), TINYLLAMA, DecodeConfig(lm_head="fp16", max_ctx=cap))
-    if a.persistent and a.leg == "decode":
-        model.set_persistent(True)
-    model.prepare(a.ctx + a.steps + a.warmup + 16)
+    model = Model(SyntheticLlama(TINYLLAMA, seed=0), TINYLLAMA, DecodeConfig(lm_head="fp16", max_ctx=caps["max_ctx"]))
+    model.prepare(caps["decode"])
     log(f"model built + graph captured in {time.perf_counter() - t0:.1f}s (part_size {model.part_size}, "
         f"max_splits {model.max_splits})")
-    dec = decode_leg(model, a.ctx, a.steps, a.warmup)
+    dec = sampled("decode", decode_leg, model, a.ctx, a.steps, a.warmup)
     log(f"decode ctx {a.ctx}: {dec['tok_s']:.1f} tok/s, median {dec['median_us']:.1f} us/token")
     if a.leg == "decode":
-        print(json.dumps({"leg": "decode", "decode": dec}), flush=True)
+        print(json.dumps({"leg": "decode", "decode": dec, "clocks": clocks}), flush=True)
         return
     if a.leg == "prefill":
-        print(json.dumps({"leg": "prefill", "prefill_tinyllama_512": prefill_leg(model)}), flush=True)
+        model.prepare(caps["prefill"])
+        print(json.dumps({"leg": "prefill", "prefill_tinyllama_512": prefill_leg(model, PREFILL_TOKENS)}), flush=True)
         return
     bpt = model.bytes_per_token(a.ctx + a.steps // 2)
-    model.prepare(2048 + 64 + 16)
-    dec2k = decode_leg(model, 2048, 64, 8)
-    log(f"decode ctx 2048: {dec2k['tok_s']:.1f} tok/s")
-    bpt2k = model.bytes_per_token(2048 + 32)
-    # the same model through the persistent step (one launch per token, dk_decode_step): reported beside the default
-    model.set_persistent(True)
-    model.prepare(a.ctx + a.steps + a.warmup + 16)
-    pers = decode_leg(model, a.ctx, a.steps, a.warmup)
-    pers_status = model.step_status()
-    model.set_persistent(False)
-    log(f"decode ctx {a.ctx}, persistent step: {pers['tok_s']:.1f} tok/s, median {pers['median_us']:.1f} us/token "
-        f"(status {pers_status})")
+    model.prepare(caps["decode_long"])
+    dec2k = sampled("decode_ctx2048", decode_leg, model, CTX_LONG, CTX_LONG_STEPS, CTX_LONG_WARMUP)
+    log(f"decode ctx {CTX_LONG}: {dec2k['tok_s']:.1f} tok/s")
+    bpt2k = model.bytes_per_token(CTX_LONG + CTX_LONG_STEPS // 2)
 
+    model.prepare(caps["prefill"])
+    pre = sampled("prefill", prefill_leg, model, PREFILL_TOKENS)
+    log(f"prefill {pre['prompt_tokens']} tokens: {pre['ms']:.2f} ms ({pre['tok_s']:.0f} tok/s, {pre['tflops']:.0f} "
+        f"TFLOP/s, {pre['speedup_vs_teacher_force']:.0f}x teacher forcing)")
 
-    model.prepare(2048 + 64 + 16)
-    pre = prefill_leg(model)
-    log(f"prefill {pre['prompt_tokens']} tokens: {pre['ms']:.2f} ms ({pre['tok_s']:.0f} tok/s, {pre['tflops']:.0f} TFLOP/s, "
-        f"{pre['speedup_vs_teacher_force']:.0f}x teacher forcing)")
-
-    d8b = decode_8b_leg()
+    d8b = sampled("decode_llama3_8b", decode_8b_leg)
 
     cpu = None
     if not a.no_cpu:
-        cpu = cpu_baseline_leg(model, TINYLLAMA, a.ctx)
+        cpu = cpu_baseline_leg(model, TINYLLAMA)
         log(f"cpu baseline: {cpu['value']:.3f} tok/s on {cpu['cores']} cores")
-
-    traffic = None
-    if PMC_SUMMARY.exists():
-        traffic = json.load(open(PMC_SUMMARY)).get("hbm_bytes_per_launch")
 
     out = {
         "metric": METRIC, "value": round(dec["tok_s"], 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps,
@@ -448,18 +599,20 @@ def main():
                    "parallelism": "single GPU", "device": dev_name},
         "roofline": {"bound": "hbm", "kernel": f"gemv_w4a16 4096x14336 G128 cfg {g1['cfg']}",
                      "achieved": g1["gbps"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": g1["frac"],
-                     "traffic": traffic, "bytes_per_launch": g1["bytes"], "mean_us": g1["mean_us"],
-                     "read_ceiling_frac": rc["frac"]},
+                     "traffic": traffic["hbm_bytes_per_launch"] if traffic else None,
+                     "traffic_detail": traffic or traffic_note, "bytes_per_launch": g1["bytes"],
+                     "mean_us": g1["mean_us"], "read_ceiling_frac": rc["frac"]},
         "gemv_14336x4096": g2, "gemv_cfg1_5632x2048": g3, "read_ceiling": rc, "kernels_cfg2_cfg3": kern,
         "decode": {**{k: round(v, 3) if isinstance(v, float) else v for k, v in dec.items()},
                    "bytes_per_token": bpt, "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / bpt, 1),
                    "frac_of_roofline": round(dec["tok_s"] / (HBM_PEAK_GBS * 1e9 / bpt), 4)},
         "decode_ctx2048": {"tok_s": round(dec2k["tok_s"], 2), "median_us": round(dec2k["median_us"], 2),
-                           "bytes_per_token": bpt2k, "frac_of_roofline": round(dec2k["tok_s"] / (HBM_PEAK_GBS * 1e9 / bpt2k), 4)},
-        "decode_persistent": {"tok_s": round(pers["tok_s"], 2), "median_us": round(pers["median_us"], 2),
-                              "status": pers_status, "kernel": "dk_decode_step (one launch per token)"},
+                           "p10_us": round(dec2k["p10_us"], 2), "p90_us": round(dec2k["p90_us"], 2),
+                           "bytes_per_token": bpt2k,
+                           "frac_of_roofline": round(dec2k["tok_s"] / (HBM_PEAK_GBS * 1e9 / bpt2k), 4)},
         "prefill_tinyllama_512": pre,
         "decode_llama3_8b_ctx4096": d8b,
+        "clocks": clocks,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

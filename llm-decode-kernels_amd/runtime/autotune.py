@@ -64,7 +64,8 @@ def candidates(N, K):
 
 
 def fused_candidates(kind):
-    """stage-4 configurations of the fused INT4 GEMVs (the gate|up SwiGLU epilogue needs an even row tile)."""
+    """stage-4 configurations of the fused INT4 GEMVs (the gate|up SwiGLU epilogue needs an even row tile; so does
+    the qkv RoPE epilogue, which takes the same candidates)."""
     return [(4, R, 0, pf) for R in (1, 2, 4, 8) for pf in range(4) if kind != "gate_up" or (R << pf) >= 2]
 
 
@@ -303,10 +304,13 @@ STEP_MODELS = {"tinyllama": ("TINYLLAMA", "fp16", 512), "llama3_8b": ("LLAMA3_8B
 
 def step_slots(model):
     """The GEMV launches of one decode step that the in-step tuner varies: (table kind, projection, candidates).
-    Kinds: "norm" (qkv behind the fused residual + RMSNorm), "plain" (o, down; the INT4 head when the norm does not
-    pay inside it), "gate_up" (gate|up with the SwiGLU epilogue), "f16_norm" (the fp16 head behind the final norm)."""
+    Kinds: "norm" (qkv behind the fused residual + RMSNorm), "rope" (the same qkv launch with the RoPE + append
+    epilogue, whose row tile must hold a rotation pair), "plain" (o, down; the INT4 head when the norm does not pay
+    inside it), "gate_up" (gate|up with the SwiGLU epilogue), "f16_norm" (the fp16 head behind the final norm)."""
     lw = model.layers[0]
-    slots = [("norm", lw["qkv"], fused_candidates("rmsnorm")), ("plain", lw["o"], fused_candidates("rmsnorm")),
+    qkv = (("rope", lw["qkv"], fused_candidates("gate_up")) if model.rope_epilogue
+           else ("norm", lw["qkv"], fused_candidates("rmsnorm")))
+    slots = [qkv, ("plain", lw["o"], fused_candidates("rmsnorm")),
              ("gate_up", lw["gu"], fused_candidates("gate_up")), ("plain", lw["down"], fused_candidates("rmsnorm"))]
     head = model.lm_head
     if head.quant:
@@ -339,6 +343,7 @@ def tune_step(models=("tinyllama", "llama3_8b"), path=CONFIG, rounds=2, log=prin
                 key = model.step_key(kind, lin)
                 cur = model.step_cfg_override.pop(key, None)
                 isolated = {"plain": model.gemv_cfg, "norm": model.gemv_norm_cfg, "gate_up": model.gemv_gate_up_cfg,
+                            "rope": model.qkv_rope_cfg,
                             "f16_norm": lambda l: model.gemv_f16_cfg(l, norm=True)}[kind](lin)
                 cands = list(dict.fromkeys([tuple(c) for c in cands] + [tuple(isolated)]))
                 times = {}

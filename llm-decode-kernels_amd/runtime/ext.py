@@ -214,27 +214,48 @@ class DecodeKernels:
     # gemv_w4a16 then rope_append), one launch; the input is x itself (norm_w None) or the residual + RMSNorm input
     def gemv_w4a16_qkv_rope(self, stage, R, warps, pf, packed, sz, x, row, delta, norm_w, eps, x_out, qkv, cos_t,
                             sin_t, pos, bt, kc, vc, n_q, n_kv, group):
-        for t, n in ((packed, "packed"), (sz, "sz"), (x, "x"), (qkv, "qkv"), (cos_t, "cos_t"), (sin_t, "sin_t"),
-                     (pos, "pos"), (bt, "bt"), (kc, "kc"), (vc, "vc")):
-            _check_cuda(t, n)
-        for t, n in (row, "row"), (delta, "delta"), (norm_w, "norm_w"), (x_out, "x_out"):
-            if t is not None:
-                _check_cuda(t, n)
-        _check_dtype(packed, torch.int32, "packed")
-        _check_dtype(sz, torch.float16, "sz")
-        for t, n in ((x, "x"), (qkv, "qkv"), (kc, "kc"), (vc, "vc")):
+        """Shapes and dtypes are checked first, then that every tensor is a contiguous CUDA tensor, so no bad
+        argument reaches the kernel."""
+        what = "gemv_w4a16_qkv_rope"
+        if kc.dim() != 4 or vc.shape != kc.shape or kc.size(1) != n_kv:
+            raise RuntimeError(f"{what}: cache must be [pages, n_kv, P, head_dim] (kc and vc alike)")
+        D = kc.size(3)
+        K = packed.size(1) * 8
+        N = (n_q + 2 * n_kv) * D
+        if packed.dim() != 2 or packed.size(0) != N or qkv.numel() != N:
+            raise RuntimeError(f"{what}: packed must hold (n_q + 2 n_kv) * head_dim rows and qkv as many values")
+        if K % 32 != 0 or group < 32 or K % group != 0:
+            raise RuntimeError(f"{what}: K must be a multiple of 32 and of the group size (>= 32)")
+        self._gemv_shape(packed, sz, qkv, K, group)
+        if cos_t.dim() != 2 or cos_t.size(1) * 2 != D or sin_t.shape != cos_t.shape:
+            raise RuntimeError(f"{what}: cos_t and sin_t must both be [max_pos, head_dim / 2]")
+        for t, n in ((x, "x"), (kc, "kc"), (vc, "vc")):
             _check_dtype(t, torch.float16, n)
         for t, n in ((cos_t, "cos_t"), (sin_t, "sin_t")):
             _check_dtype(t, torch.float32, n)
         for t, n in ((pos, "pos"), (bt, "bt")):
             _check_dtype(t, torch.int32, n)
-        if kc.dim() != 4 or vc.shape != kc.shape:
-            raise RuntimeError("gemv_w4a16_qkv_rope: cache must be [pages, n_kv, P, head_dim]")
-        D = kc.size(3)
-        K = packed.size(1) * 8
-        N = (n_q + 2 * n_kv) * D
-        if packed.size(0) != N or qkv.numel() != N or kc.size(1) != n_kv or cos_t.size(1) * 2 != D:
-            raise RuntimeError("gemv_w4a16_qkv_rope: packed / qkv rows, cache heads and rope table width disagree")
+        if pos.numel() < 1:
+            raise RuntimeError(f"{what}: pos must hold the position (int32 [1])")
+        if norm_w is None:
+            if row is not None or delta is not None or x_out is not None or x.numel() != K:
+                raise RuntimeError(f"{what}: without norm_w, x must hold K values and row/delta/x_out be None")
+        else:
+            if norm_w.numel() != K or norm_w.dtype != torch.float16:
+                raise RuntimeError(f"{what}: norm_w must be fp16 [K]")
+            if row is None and x.numel() != K:
+                raise RuntimeError(f"{what}: x must hold K values (or be a [*, K] table with row)")
+            if row is not None and (x.dim() != 2 or x.size(1) != K or row.dtype != torch.int64 or row.numel() != 1
+                                    or delta is not None):
+                raise RuntimeError(f"{what}: row needs one int64 index into a [*, K] x and no delta")
+            for t, n in ((delta, "delta"), (x_out, "x_out")):
+                if t is not None and (t.numel() != K or t.dtype != torch.float16):
+                    raise RuntimeError(f"{what}: {n} must be fp16 [K]")
+        for t, n in ((packed, "packed"), (sz, "sz"), (x, "x"), (qkv, "qkv"), (cos_t, "cos_t"), (sin_t, "sin_t"),
+                     (pos, "pos"), (bt, "bt"), (kc, "kc"), (vc, "vc"), (row, "row"), (delta, "delta"),
+                     (norm_w, "norm_w"), (x_out, "x_out")):
+            if t is not None:
+                _check_cuda(t, n)
         ptr = lambda t: None if t is None else t.data_ptr()
         self._call(self.lib.dk_gemv_w4a16_qkv_rope, int(stage), int(R), int(warps), int(pf), packed.data_ptr(),
                    sz.data_ptr(), x.data_ptr(), ptr(row), ptr(delta), ptr(norm_w), float(eps), ptr(x_out),

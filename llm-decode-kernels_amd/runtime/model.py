@@ -473,6 +473,15 @@ class Model:
         else:
             self.K.argmax_advance(self.logits, self.tok, self.pos)
 
+    def qkv_rope_cfg(self, lin):
+        """Row tile of the qkv GEMV with the RoPE + append epilogue: its in-step entry ("rope:" key, written by
+        runtime.autotune.tune_step), else the fused-norm one; a tile (R * 2^pf rows) must hold a rotation pair."""
+        e = self.step_cfg_override.get(self.step_key("rope", lin))
+        _, r, wv, pf = tuple(e) if e is not None else self.gemv_norm_cfg(lin)
+        if (r << pf) < 2:
+            r = 2
+        return 4, r, wv, pf
+
     def qkv_proj(self, lin: Linear, li, x_in, delta, w, x_out, row=None):
         """qkv = W_qkv . x (w None: x is the normed input) or W_qkv . rmsnorm(x_in + delta); with the RoPE epilogue
         the same launch also rotates q and appends k, v to layer li's cache."""
@@ -482,10 +491,7 @@ class Model:
             else:
                 self.linear_norm(lin, x_in, delta, w, x_out, self.qkv, row=row)
             return
-        e = self.step_cfg_override.get(self.step_key("rope", lin))
-        _, r, wv, pf = tuple(e) if e is not None else self.gemv_norm_cfg(lin)
-        if (r << pf) < 2:
-            r = 2
+        _, r, wv, pf = self.qkv_rope_cfg(lin)
         packed, sz = lin.rope_rows
         self.K.gemv_w4a16_qkv_rope(4, r, wv, pf, packed, sz, x_in, row, delta, w, self.eps, x_out, self.qkv, self.cos,
                                    self.sin, self.pos, self.bt, self.kv[li, 0], self.kv[li, 1], self.n_q, self.n_kv,

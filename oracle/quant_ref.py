@@ -7,6 +7,8 @@ Follows ``runtime/quant.py`` of the reference:
   * ``pack`` / ``unpack``                                           runtime/quant.py:100-119
   * ``pack_scale_zero``                                             runtime/quant.py:122-124
   * ``QuantLinear.nbytes``                                          runtime/quant.py:139-140
+  * ``dequantize_packed``: unpack + dequantize in torch on any device (the same arithmetic as ``unpack`` and
+    ``dequantize``, for weights too large for numpy in a test's time budget)   runtime/quant.py:93-97,114-119
 
 All arithmetic is IEEE float32 with round-half-to-even, exactly the points at which the reference rounds:
 ``scale = fp16(max((max - min) / 15, 1e-6))`` read back as float32; ``zero = clip(rint(-min / scale), 0, 15)``;
@@ -141,16 +143,19 @@ def gemv_bytes(N, K, group):
     return nbytes(N, K, group) + 2 * K + 2 * N
 
 
-class QuantLinearRef:
-    """CPU holder mirroring ``QuantLinear`` (runtime/quant.py:127-137): codes, packed words, scale/zero, w_ref."""
+# bit offset of element e (0..7) inside its packed word: element 8j+2i at 4i, element 8j+2i+1 at 16+4i
+_SHIFTS = tuple(4 * (e // 2) + 16 * (e % 2) for e in range(8))
 
-    def __init__(self, w, group):
-        self.N, self.K = np.asarray(w).shape
-        self.group = group
-        self.q, self.scale, self.zero = quantize(w, group)
-        self.packed = pack(self.q)
-        self.sz = pack_scale_zero(self.scale, self.zero)
-        self.w_ref = dequantize(self.q, self.scale, self.zero, group)
 
-    def nbytes(self):
-        return nbytes(self.N, self.K, self.group)
+def dequantize_packed(packed, sz, group):
+    """torch int32 packed [N, K/8] + fp16 sz [N, K/G, 2] -> fp16 w_ref [N, K] on packed's device: each nibble is
+    extracted at its bit offset (``unpack``), then fp16((q - zero) * scale) with the product in float32 (exact: a
+    4-bit integer times an fp16 scale) and one rounding to fp16 (``dequantize``, runtime/quant.py:93-97)."""
+    import torch
+    N, W = packed.shape
+    K = W * 8
+    sh = torch.tensor(_SHIFTS, dtype=torch.int32, device=packed.device)
+    q = ((packed.unsqueeze(-1) >> sh) & 15).reshape(N, K // group, group).to(torch.float32)
+    scale = sz[..., 0].to(torch.float32).unsqueeze(-1)
+    zero = sz[..., 1].to(torch.float32).unsqueeze(-1)
+    return ((q - zero) * scale).to(torch.float16).reshape(N, K)

@@ -280,6 +280,54 @@ def test_shim_rejects_cpu_tensors(lib):
         K.swiglu(torch.zeros(16, dtype=torch.half), torch.zeros(8, dtype=torch.half))
 
 
+def _qkv_rope_args(**kw):
+    """CPU tensors of consistent shapes for the qkv RoPE shim (n_q 4, n_kv 2, head_dim 64, K 256, G 128)."""
+    n_q, n_kv, D, K, G = 4, 2, 64, 256, 128
+    N = (n_q + 2 * n_kv) * D
+    h = dict(dtype=torch.half)
+    a = dict(stage=4, R=2, warps=0, pf=0, packed=torch.zeros(N, K // 8, dtype=torch.int32),
+             sz=torch.zeros(N, K // G, 2, **h), x=torch.zeros(K, **h), row=None, delta=torch.zeros(K, **h),
+             norm_w=torch.ones(K, **h), eps=1e-5, x_out=torch.zeros(K, **h), qkv=torch.zeros(N, **h),
+             cos_t=torch.zeros(64, D // 2), sin_t=torch.zeros(64, D // 2), pos=torch.zeros(1, dtype=torch.int32),
+             bt=torch.zeros(4, dtype=torch.int32), kc=torch.zeros(4, n_kv, 16, D, **h),
+             vc=torch.zeros(4, n_kv, 16, D, **h), n_q=n_q, n_kv=n_kv, group=G)
+    a.update(kw)
+    return a
+
+
+@pytest.mark.parametrize("kw,msg", [
+    ({}, "must be a contiguous CUDA tensor"),                      # consistent: only the device check is left
+    ({"sz": torch.zeros(512, 1, 2, dtype=torch.half)}, "shape mismatch"),
+    ({"group": 64}, "shape mismatch"),                              # sz groups disagree with K / group
+    ({"packed": torch.zeros(512, 32, dtype=torch.int16)}, "int32"),
+    ({"qkv": torch.zeros(500, dtype=torch.half)}, "qkv as many values"),
+    ({"sin_t": torch.zeros(32, 32)}, "cos_t and sin_t"),
+    ({"cos_t": torch.zeros(64, 16)}, "cos_t and sin_t"),
+    ({"x": torch.zeros(255, dtype=torch.half)}, "x must hold K values"),
+    ({"x": torch.zeros(256)}, "x must be torch.float16"),
+    ({"row": torch.zeros(1, dtype=torch.int32), "delta": None, "x": torch.zeros(10, 256, dtype=torch.half)},
+     "int64 index"),
+    ({"row": torch.zeros(1, dtype=torch.int64), "x": torch.zeros(10, 256, dtype=torch.half)}, "no delta"),
+    ({"row": torch.zeros(1, dtype=torch.int64), "delta": None, "x": torch.zeros(256, dtype=torch.half)},
+     "int64 index"),
+    ({"delta": torch.zeros(128, dtype=torch.half)}, "delta must be fp16 \\[K\\]"),
+    ({"x_out": torch.zeros(256)}, "x_out must be fp16 \\[K\\]"),
+    ({"norm_w": torch.ones(128, dtype=torch.half)}, "norm_w must be fp16 \\[K\\]"),
+    ({"norm_w": None}, "without norm_w"),
+    ({"vc": torch.zeros(4, 2, 16, 128, dtype=torch.half)}, "cache must be"),
+    ({"n_kv": 1}, "cache must be"),
+    ({"pos": torch.zeros(1, dtype=torch.int64)}, "pos must be torch.int32"),
+    ({"bt": torch.zeros(4, dtype=torch.int64)}, "bt must be torch.int32"),
+    ({"pos": torch.zeros(0, dtype=torch.int32)}, "pos must hold"),
+])
+def test_qkv_rope_shim_checks_every_argument(lib, kw, msg):
+    """The torch shim of dk_gemv_w4a16_qkv_rope rejects each inconsistent argument with its own message before any
+    launch (shape and dtype checks run ahead of the device check, so they are reachable with CPU tensors)."""
+    K = ext.DecodeKernels(lib)
+    with pytest.raises(RuntimeError, match=msg):
+        K.gemv_w4a16_qkv_rope(*_qkv_rope_args(**kw).values())
+
+
 def test_load_without_library_fails_loudly(tmp_path):
     with pytest.raises(RuntimeError, match="not built"):
         ext.open_library(tmp_path / "missing.so")

@@ -41,3 +41,11 @@ def test_interleave_halves_round_trip_and_order():
     il = interleave_halves(t)
     assert torch.equal(il[0::2], t[:6]) and torch.equal(il[1::2], t[6:])
     assert torch.equal(deinterleave_halves(il), t)
+
+
+def test_gemv_byte_count_matches_oracle():
+    """The runtime's per-GEMV byte count (the roofline's `bytes_per_launch`) equals the oracle's format-derived one."""
+    from oracle import quant_ref as Q
+    from runtime.autotune import gemv_bytes
+    for N, K, G in ((4096, 14336, 128), (14336, 4096, 128), (5632, 2048, 128), (2560, 2048, 64), (32000, 2048, 256)):
+        assert gemv_bytes(N, K, G) == Q.gemv_bytes(N, K, G)

@@ -66,7 +66,7 @@ def test_gemv_shape1_and_onehot(K, cfg):
 
 
 SHAPES = {"qkv": (2560, 2048), "o": (2048, 2048), "gate_up": (11264, 2048), "down": (2048, 5632),
-          "lm_head": (32000, 2048)}
+          "lm_head": (32000, 2048), "cfg1": (5632, 2048)}       # cfg1: BASELINE config 1, the plain 5632 x 2048 GEMV
 SHAPES_8B = {"qkv8b": (6144, 4096), "o8b": (4096, 4096), "down8b": (4096, 14336), "up8b": (14336, 4096)}
 
 
@@ -180,7 +180,7 @@ def test_attention_ctx128(K, n_q, n_kv, page):
     k, v = R.gather_kv(kc, vc, bt, 128, page)
     ref = R.attention_contiguous_ref(q, k, v)
     for PS in (4096, 64, 32, 48, 16):
-        for ver in (1, 2, 3, 4):
+        for ver in (1, 2, 3, 4, 5):
             close_or_rejected(run_attn(K, q, kc, vc, bt, 128, PS, ver), ref, 2e-3,
                          f"ctx128 {n_q}/{n_kv} P{page} PS{PS} v{ver}")
 

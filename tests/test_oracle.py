@@ -121,6 +121,37 @@ def test_dequantize_single_rounding():
     assert np.array_equal(Q.dequantize(q, s, z, 128), exact.reshape(8, 256).astype(np.float16))
 
 
+@pytest.mark.parametrize("group", [32, 64, 128, 256])
+def test_dequantize_packed_equals_unpack_then_dequantize(group):
+    """The torch form bit for bit equals the numpy unpack + dequantize, on random words (every nibble value, negative
+    int32 words, so the arithmetic shift of the sign bit is exercised) and on a real RTN quantization."""
+    rng = np.random.default_rng(group)
+    words = rng.integers(-2**31, 2**31, (24, 512 // 8), dtype=np.int64).astype(np.int32)
+    s = (rng.random((24, 512 // group)) * 0.02 + 1e-5).astype(np.float16)
+    z = rng.integers(0, 16, (24, 512 // group)).astype(np.float16)
+    sz = Q.pack_scale_zero(s, z)
+    want = Q.dequantize(Q.unpack(words), s, z, group)
+    got = Q.dequantize_packed(torch.from_numpy(words), torch.from_numpy(sz), group).numpy()
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+    w = (rng.standard_normal((16, 1024)) * 0.02).astype(np.float16)
+    q, s, z = Q.quantize(w, group)
+    got = Q.dequantize_packed(torch.from_numpy(Q.pack(q)), torch.from_numpy(Q.pack_scale_zero(s, z)), group).numpy()
+    assert np.array_equal(got.view(np.uint16), Q.dequantize(q, s, z, group).view(np.uint16))
+
+
+def test_byte_counts_match_arrays_and_published_figures():
+    """nbytes is the size of the packed words plus the scale/zero pairs the format produces; gemv_bytes adds x and y.
+    Published figures: 6,142,976 B for the reference's 2048 x 5632 G128 down GEMV (RESULTS.md:204, the same bytes as
+    BASELINE config 1) and 31,232,000 B at 4096 x 14336 G128."""
+    rng = np.random.default_rng(5)
+    for N, K, G in ((48, 256, 64), (8, 1024, 128), (16, 512, 256)):
+        q, s, z = Q.quantize((rng.standard_normal((N, K)) * 0.02).astype(np.float16), G)
+        assert Q.nbytes(N, K, G) == Q.pack(q).nbytes + Q.pack_scale_zero(s, z).nbytes
+        assert Q.gemv_bytes(N, K, G) == Q.nbytes(N, K, G) + 2 * K + 2 * N
+    assert Q.gemv_bytes(2048, 5632, 128) == Q.gemv_bytes(5632, 2048, 128) == 6_142_976
+    assert Q.gemv_bytes(4096, 14336, 128) == Q.gemv_bytes(14336, 4096, 128) == 31_232_000
+
+
 def _shape1():
     """tests/test_kernels.py:47-56: q[r,k] = (k+r) % 16, zero 8, scale (r+1)/2, K = G = 128."""
     N, K = 4, 128
