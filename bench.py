@@ -282,7 +282,7 @@ def kernels_leg(Kx, n=64, reps=5):
         t_ref = graph_time(lambda i: Kx.paged_attention(q, kc, vc, bt, pos, ps, o_part, m_part, l_part, o, 3), n,
                            reps)[1]
         t_dec = graph_time(lambda i: Kx.attention_decode(qkv, cos, sin, pos, bt, kc, vc, n_q, n_kv, ps, o_part, m_part,
-                                                         l_part, o, None, impl), n, reps)[1]
+                                                         l_part, o, impl), n, reps)[1]
         out["attention"][str(ctx)] = {
             "bytes": nbytes, "part_size": ps, "paged_attention_v3_us": round(t_ref, 3),
             "paged_attention_v3_gbps": round(nbytes / t_ref / 1e3, 1), "attention_decode_impl": impl,

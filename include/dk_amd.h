@@ -77,14 +77,6 @@ int dk_gemv_w4a16_rmsnorm(int stage, int R, int warps, int pf, const void* packe
                           int N, int K, int group, void* stream);
 
 /*
- * W4A16 GEMV whose input is SwiGLU of gu = [gate | up] (fp16 [2K]): x[i] = fp16(silu(float(gate[i]))) * up[i],
- * computed inside the GEMV (fuses swiglu, kernels/bindings.cpp:74-79, with the down-projection gemv_w4a16 of
- * runtime/model.py:227-228; no counterpart in the reference's binding). Rounding as dk_swiglu; stage must be 4.
- */
-int dk_gemv_w4a16_swiglu(int stage, int R, int warps, int pf, const void* packed, const void* sz, const void* gu,
-                         void* y, int N, int K, int group, void* stream);
-
-/*
  * The gate|up W4A16 GEMV with SwiGLU applied to its output: fuses gemv_w4a16 of the MLP's gate|up projection with
  * swiglu (kernels/bindings.cpp:27-38 then :74-79, as runtime/model.py:226-227 calls them; no single counterpart in
  * the reference's binding). The N = 2I weight rows are stored interleaved, row 2i = gate row i and row 2i + 1 = up
@@ -205,20 +197,17 @@ int dk_paged_attention(int version, const void* q, const void* kc, const void* v
  * back). qkv: the fused [q | k | v] vector, fp16 [(n_q + 2 n_kv) * head_dim], read only (q is rotated in registers,
  * not written back). k (rotated) and v of position *pos are written into page bt[pos / page], slot pos % page exactly
  * as dk_rope_append writes them, and the attention over ctx = *pos + 1 tokens uses them. Split partials go to
- * o_part / m_part / l_part. counters == NULL: a combine kernel merges them, as for dk_paged_attention. counters =
- * uint32 [n_kv], zero before the first call (every call leaves them zero): when 1 < max_splits <= 64 the split
- * workgroup of each kv head that finishes last merges its partials (one launch in all); calls that share counters
- * must not run concurrently. impl selects the split kernel: 0 or 1 = the block kernel (v_dot2 scores, LDS p.V),
- * 2 = the MFMA kernel (16 x 16 f16 tiles; needs ((part_size - 1) >> log2(page)) + 2 <= 1024 and counters == NULL),
- * 3 = the lean MFMA kernel (scalar page lookups, one memory round trip for K / V; needs page >= 16, part_size a
- * multiple of 16 up to 512 and counters == NULL).
+ * o_part / m_part / l_part and a combine kernel merges them, as for dk_paged_attention. impl selects the split
+ * kernel: 0 or 1 = the block kernel (v_dot2 scores, LDS p.V), 2 = the MFMA kernel (16 x 16 f16 tiles; needs
+ * ((part_size - 1) >> log2(page)) + 2 <= 1024), 3 = the lean MFMA kernel (scalar page lookups, one memory round trip
+ * for K / V; needs page >= 16 and a part_size that is a multiple of 16 up to 512, 256 at head_dim 128).
  * The runtime picks impl and part_size per context from its measured policy table. If *pos is outside [0, max_pos)
  * nothing is touched. Other arguments and limits as dk_rope_append / dk_paged_attention.
  */
 int dk_attention_decode(const void* qkv, const float* cos_t, const float* sin_t, int max_pos, const int32_t* pos,
                         const int32_t* bt, int n_bt, void* kc, void* vc, int n_pages, int page, int n_q, int n_kv,
                         int head_dim, int part_size, int max_splits, int impl, float* o_part, float* m_part,
-                        float* l_part, uint32_t* counters, void* out, void* stream);
+                        float* l_part, void* out, void* stream);
 
 /*
  * Fused residual add + RMSNorm:  x <- x + delta (fp16 add, written back; skipped if delta == NULL);
@@ -271,81 +260,6 @@ int dk_argmax_advance_split(const void* logits, int V, int64_t* tok, int32_t* po
  * group a power of two in [32, 512] with K % group == 0.
  */
 int dk_quantize_w4(const void* w, void* packed, void* sz, int N, int K, int group, int clip, void* stream);
-
-/*
- * ---- Persistent decode step ---------------------------------------------------------------------------------------
- * One launch runs the whole fused decode step of runtime/model.py:216-233 (the composition Model.step issues as
- * 6 launches per layer plus the head and the argmax): per layer the qkv GEMV behind residual + RMSNorm (layer 0 gathers
- * the embedding row of *tok), RoPE + KV append + split attention, the split combine, the o GEMV, the gate|up GEMV
- * behind residual + RMSNorm with the SwiGLU epilogue, the down GEMV; then the LM head behind the final residual +
- * RMSNorm, argmax, *tok = argmax and *pos += 1. It has no single counterpart in the reference: it replaces the
- * sequence of gemv_w4a16 / paged_attention / add_rmsnorm / swiglu / rope_append calls (kernels/bindings.cpp:90-99)
- * that one decode step makes, with the same arithmetic (rounding points of kernels/fused_norm.cu:2-3,
- * fused_swiglu.cu:2, rope_kv.cu:1-2, the log-sum-exp combine of paged_attention.cu:366-427).
- *
- * The grid is one workgroup per compute unit (dk_decode_step_grid); the phases are separated by grid barriers over
- * `sync`, and every workgroup requests the next phase's weights (and its attention pages) before it waits.
- * Activations, the residual stream and the split partials live in caller buffers; the KV cache is written in place.
- */
-typedef struct dk_step_layer {
-  const void* qkv_packed; /* int32 [(n_q + 2 n_kv) D, H/8], rows q | k | v       */
-  const void* qkv_sz;     /* fp16  [(n_q + 2 n_kv) D, H/G, 2]                      */
-  const void* o_packed;   /* [H, n_q D / 8]                                         */
-  const void* o_sz;
-  const void* gu_packed;  /* [2 I, H/8], rows interleaved gate_0, up_0, gate_1, ... */
-  const void* gu_sz;
-  const void* down_packed; /* [H, I/8]                                              */
-  const void* down_sz;
-  const void* ln1;        /* fp16 [H] input_layernorm weight                         */
-  const void* ln2;        /* fp16 [H] post_attention_layernorm weight                */
-  void* kc;               /* fp16 [pages, n_kv, page, D] this layer's K cache        */
-  void* vc;               /* fp16 [pages, n_kv, page, D] this layer's V cache        */
-} dk_step_layer;
-
-typedef struct dk_step_desc {
-  int n_layers, hidden, n_q, n_kv, head_dim, inter, vocab, group;
-  float eps;
-  const void* emb;         /* fp16 [vocab, H] */
-  const void* norm_f;      /* fp16 [H] */
-  const void* head_w;      /* fp16 [vocab, H], or INT4 packed [vocab, H/8] when head_sz != NULL */
-  const void* head_sz;     /* NULL, or fp16 [vocab, H/G, 2] of the INT4 head */
-  const float* cos_t;      /* fp32 [max_pos, D/2] */
-  const float* sin_t;
-  int max_pos;
-  int64_t* tok;            /* device [1]: read (embedding row), then the argmax */
-  int32_t* pos;            /* device [1]: the position of the token; += 1 */
-  const int32_t* bt;       /* block table [n_bt] shared by the layers */
-  int n_bt, n_pages, page;
-  int part_size;           /* 128 or 256 tokens per split (8 waves x 1 or 2 tiles of 16) */
-  int max_splits;          /* split buffers' second dim; n_kv * max_splits <= dk_decode_step_grid(), <= 64 */
-  void* work;              /* 256-byte aligned, work_bytes >= dk_decode_step_work_bytes(desc): per layer the
-                              residual stream, qkv, attention output, o, act, down and the split partials, each slot
-                              written once per step before it is read (so ordinary cached loads read them) */
-  size_t work_bytes;
-  void* logits;            /* fp16 [vocab] */
-  uint32_t* sync;          /* DK_STEP_SYNC_WORDS words, zero before the first call; every completed call leaves them
-                              zero. Calls that overlap on one sync buffer race. */
-  const dk_step_layer* layers; /* DEVICE array of n_layers entries */
-} dk_step_desc;
-
-#define DK_STEP_SYNC_WORDS 2048
-#define DK_STEP_SYNC_ABORT 1056 /* word set to 1 when a grid barrier timed out (the step's outputs are then invalid and
-                                  the caller must zero the sync buffer before the next call) */
-
-/* Number of workgroups of a dk_decode_step launch on the current device (one per compute unit), or -1. */
-int dk_decode_step_grid(void);
-
-/* Size in bytes of the `work` buffer of dk_decode_step for this descriptor's sizes (n_layers, hidden, n_q, n_kv,
- * head_dim, inter, max_splits), or 0 if they are not positive. */
-size_t dk_decode_step_work_bytes(const dk_step_desc* desc);
-
-/*
- * The persistent decode step described above. Limits: head_dim 64 or 128; n_q % n_kv == 0 with n_q / n_kv <= 8;
- * H == n_q * D; H, I multiples of 32 and of the group (power of two >= 32); head_dim 64: H <= 2048, I <= 6144;
- * head_dim 128: H <= 4096, I <= 14336; page a power of two >= 16; part_size 128 or 256. If *pos is outside
- * [0, max_pos) the launch does nothing.
- */
-int dk_decode_step(const dk_step_desc* desc, void* stream);
 
 #ifdef __cplusplus
 }

@@ -115,17 +115,6 @@ int dk_gemv_w4a16_rmsnorm(int stage, int R, int warps, int pf, const void* packe
   return launched("gemv_w4a16_rmsnorm");
 }
 
-int dk_gemv_w4a16_swiglu(int stage, int R, int warps, int pf, const void* packed, const void* sz, const void* gu,
-                         void* y, int N, int K, int group, void* stream) {
-  const int rc = check_fused_gemv("gemv_w4a16_swiglu", stage, R, warps, pf, packed, sz, N, K, group);
-  if (rc != DK_OK) return rc;
-  if (!gu || !y) return fail(DK_ERR_NULL, "gemv_w4a16_swiglu: null pointer argument");
-  if (!aligned16(gu)) return fail(DK_ERR_ALIGN, "gu must be 16B aligned");
-  clear_error();
-  dk::GemvInput in{gu, nullptr, nullptr, nullptr, 0.f, nullptr};
-  dk::launch_gemv_w4a16_fused(2, 0, R, pf, packed, sz, in, y, N, K, ilog2(group), (hipStream_t)stream);
-  return launched("gemv_w4a16_swiglu");
-}
 
 int dk_gemv_w4a16_gate_up(int stage, int R, int warps, int pf, const void* packed, const void* sz, const void* x,
                           const int64_t* row, const void* delta, const void* norm_w, float eps, void* x_out, void* act,
@@ -297,7 +286,7 @@ int dk_paged_attention(int version, const void* q, const void* kc, const void* v
   clear_error();
   const dk::AttnLaunch a{q, nullptr, nullptr, 0, pos, bt, n_bt, const_cast<void*>(kc), const_cast<void*>(vc), n_pages,
                          ilog2(page), n_q, n_kv, head_dim, part_size, max_splits, o_part, m_part, l_part, out,
-                         nullptr, version == 5 ? 3 : version == 4 ? 2 : 1};
+                         version == 5 ? 3 : version == 4 ? 2 : 1};
   dk::launch_paged_attention(a, (hipStream_t)stream);
   return launched("paged_attention");
 }
@@ -305,14 +294,10 @@ int dk_paged_attention(int version, const void* q, const void* kc, const void* v
 int dk_attention_decode(const void* qkv, const float* cos_t, const float* sin_t, int max_pos, const int32_t* pos,
                         const int32_t* bt, int n_bt, void* kc, void* vc, int n_pages, int page, int n_q, int n_kv,
                         int head_dim, int part_size, int max_splits, int impl, float* o_part, float* m_part,
-                        float* l_part, uint32_t* counters, void* out, void* stream) {
+                        float* l_part, void* out, void* stream) {
   if (!qkv || !cos_t || !sin_t || !pos || !bt || !kc || !vc || !o_part || !m_part || !l_part || !out)
     return fail(DK_ERR_NULL, "attention_decode: null pointer argument");
-  if (counters && (reinterpret_cast<uintptr_t>(counters) & 3u))
-    return fail(DK_ERR_ALIGN, "attention_decode: counters must be 4B aligned");
   if (impl < 0 || impl > 3) return fail(DK_ERR_DOMAIN, "attention_decode: impl must be 0, 1, 2 or 3, got %d", impl);
-  if (impl >= 2 && counters)
-    return fail(DK_ERR_DOMAIN, "attention_decode: the in-split combine (counters) belongs to impl 1");
   if (head_dim != 64 && head_dim != 128)
     return fail(DK_ERR_SHAPE, "attention_decode: head_dim must be 64 or 128, got %d", head_dim);
   if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0)
@@ -338,7 +323,7 @@ int dk_attention_decode(const void* qkv, const float* cos_t, const float* sin_t,
     return fail(DK_ERR_DOMAIN, "attention_decode: impl 3 needs pages of >= 16 tokens and a part_size that is a "
                 "multiple of 16 up to %d (part_size %d, page %d)", dk::attn_lean_max_part(head_dim), part_size, page);
   const dk::AttnLaunch a{qkv, cos_t, sin_t, max_pos, pos, bt, n_bt, kc, vc, n_pages, ilog2(page), n_q, n_kv,
-                         head_dim, part_size, max_splits, o_part, m_part, l_part, out, counters, impl};
+                         head_dim, part_size, max_splits, o_part, m_part, l_part, out, impl};
   dk::launch_attention_decode(a, (hipStream_t)stream);
   return launched("attention_decode");
 }
@@ -480,69 +465,5 @@ int dk_quantize_w4(const void* w, void* packed, void* sz, int N, int K, int grou
   return launched("quantize_w4");
 }
 
-int dk_decode_step_grid(void) {
-  const int g = dk::decode_step_grid(64);
-  const int g2 = dk::decode_step_grid(128);
-  return g < g2 ? g : g2;
-}
-
-size_t dk_decode_step_work_bytes(const dk_step_desc* desc) {
-  if (!desc) return 0;
-  const dk_step_desc& d = *desc;
-  if (d.n_layers <= 0 || d.hidden <= 0 || d.n_q <= 0 || d.n_kv <= 0 || d.head_dim <= 0 || d.inter <= 0 ||
-      d.max_splits <= 0)
-    return 0;
-  return (size_t)d.n_layers * dk::step_layout(d.hidden, d.n_q, d.n_kv, d.head_dim, d.inter, d.max_splits).layer;
-}
-
-int dk_decode_step(const dk_step_desc* desc, void* stream) {
-  if (!desc) return fail(DK_ERR_NULL, "decode_step: null descriptor");
-  const dk_step_desc& d = *desc;
-  if (!d.emb || !d.norm_f || !d.head_w || !d.cos_t || !d.sin_t || !d.tok || !d.pos || !d.bt || !d.work ||
-      !d.logits || !d.sync || !d.layers)
-    return fail(DK_ERR_NULL, "decode_step: null pointer in the descriptor");
-  const int D = d.head_dim, H = d.hidden, I = d.inter;
-  if (D != 64 && D != 128) return fail(DK_ERR_DOMAIN, "decode_step: head_dim must be 64 or 128, got %d", D);
-  if (d.n_layers <= 0 || d.n_q <= 0 || d.n_kv <= 0 || d.vocab <= 0 || H <= 0 || I <= 0)
-    return fail(DK_ERR_SHAPE, "decode_step: sizes must be positive");
-  if (d.n_layers > dk::kStepMaxLayers)
-    return fail(DK_ERR_SHAPE, "decode_step: at most %d layers, got %d", dk::kStepMaxLayers, d.n_layers);
-  if (d.n_q % d.n_kv != 0 || d.n_q / d.n_kv > 8)
-    return fail(DK_ERR_SHAPE, "decode_step: n_q / n_kv must be an integer <= 8 (n_q=%d n_kv=%d)", d.n_q, d.n_kv);
-  if (H != d.n_q * D) return fail(DK_ERR_SHAPE, "decode_step: hidden must equal n_q * head_dim");
-  if (!dk::decode_step_fits(D, H, I))
-    return fail(DK_ERR_SHAPE, "decode_step: head_dim %d takes hidden <= %d and inter <= %d (got %d, %d)", D,
-                D == 64 ? 2048 : 4096, D == 64 ? 6144 : 14336, H, I);
-  if (d.group < 32 || !pow2(d.group)) return fail(DK_ERR_DOMAIN, "decode_step: group must be a power of two >= 32");
-  if (H % 32 || I % 32 || H % d.group || I % d.group)
-    return fail(DK_ERR_SHAPE, "decode_step: hidden and inter must be multiples of 32 and of the group");
-  if (!(d.eps >= 0.f)) return fail(DK_ERR_DOMAIN, "decode_step: eps must be >= 0");
-  if (d.page < 16 || !pow2(d.page)) return fail(DK_ERR_DOMAIN, "decode_step: page must be a power of two >= 16");
-  if (d.part_size != 128 && d.part_size != 256)
-    return fail(DK_ERR_DOMAIN, "decode_step: part_size must be 128 or 256 (8 waves x 1 or 2 tiles of 16), got %d",
-                d.part_size);
-  if (d.n_bt <= 0 || d.n_pages <= 0 || d.max_pos <= 0) return fail(DK_ERR_SHAPE, "decode_step: empty cache or tables");
-  const int grid = dk::decode_step_grid(D);
-  if (grid <= 0) return fail(DK_ERR_LAUNCH, "decode_step: no device, or a CU cannot hold one workgroup");
-  const int widest = (d.n_q + 2 * d.n_kv) * D > I ? (d.n_q + 2 * d.n_kv) * D : I;
-  if ((widest + grid - 1) / grid + 1 > dk::kStepOutMax)
-    return fail(DK_ERR_SHAPE, "decode_step: %d outputs over %d workgroups exceed %d per workgroup", widest, grid,
-                dk::kStepOutMax);
-  if (d.max_splits <= 0 || d.max_splits > dk::kStepMaxSplits || (long long)d.n_kv * d.max_splits > grid)
-    return fail(DK_ERR_SHAPE, "decode_step: max_splits must be in [1, %d] with n_kv * max_splits <= %d (got %d)",
-                dk::kStepMaxSplits, grid, d.max_splits);
-  const void* a16[] = {d.emb, d.norm_f, d.head_w};
-  for (const void* p : a16)
-    if (!aligned16(p)) return fail(DK_ERR_ALIGN, "decode_step: embedding, norm and head weights must be 16B aligned");
-  if ((reinterpret_cast<uintptr_t>(d.work) & 255u) != 0) return fail(DK_ERR_ALIGN, "decode_step: work must be 256B aligned");
-  if (d.work_bytes < dk_decode_step_work_bytes(&d))
-    return fail(DK_ERR_SHAPE, "decode_step: work holds %zu bytes, needs %zu", d.work_bytes,
-                dk_decode_step_work_bytes(&d));
-  if (!aligned4(d.logits) || (d.head_sz && !aligned4(d.head_sz)) || (reinterpret_cast<uintptr_t>(d.sync) & 7u) != 0)
-    return fail(DK_ERR_ALIGN, "decode_step: logits and head scales 4B aligned, sync 8B aligned");
-  clear_error();
-  dk::launch_decode_step(d, grid, (hipStream_t)stream);
-  return launched("decode_step");
-}
 
 }  // extern "C"

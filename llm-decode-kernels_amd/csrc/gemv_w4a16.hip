@@ -284,15 +284,14 @@ __device__ __forceinline__ void tile_rows(const u32x4 (&w)[T], const uint32_t (&
 //               squares over the workgroup's K values (DPP within waves, LDS across), r = 1 / sqrt(ss / K + eps),
 //               value = norm_w * fp16(float(xn) * r). Workgroup 0 writes xn to x_out (a different buffer: every other
 //               workgroup still reads xi).
-//   kInSwiglu   fp16(silu(float(gate))) * up with gate = x[0..I), up = x[I..2I), K == I (kernels/fused_swiglu.cu:7-21).
 // Split in two: tile_input_load issues the operand loads and tile_input_finish computes the operand. The loads are
 // issued before any weight load of the workgroup: a wave's vector loads return in issue order, so operand loads
 // issued after the weights would wait behind an HBM round trip and hold back the prologue and the next tile's loads.
-enum { kInPlain = 0, kInRmsNorm = 1, kInSwiglu = 2 };
+enum { kInPlain = 0, kInRmsNorm = 1 };
 
 struct TileRaw {
-  u32x4 a[4];  // x / gate / residual
-  u32x4 b[4];  // up / delta
+  u32x4 a[4];  // x / residual
+  u32x4 b[4];  // delta
   u32x4 c[4];  // norm weight
 };
 
@@ -302,14 +301,6 @@ __device__ __forceinline__ void tile_input_load(const GemvInput& in, int uc, int
     const u32x4* X = reinterpret_cast<const u32x4*>(in.x);
 #pragma unroll
     for (int k = 0; k < 4; ++k) raw.a[k] = X[4 * uc + k];
-  } else if constexpr (PRO == kInSwiglu) {
-    const u32x4* G = reinterpret_cast<const u32x4*>(in.x);
-    const u32x4* Up = G + (K >> 3);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      raw.a[k] = G[4 * uc + k];
-      raw.b[k] = Up[4 * uc + k];
-    }
   } else {
     const long long off = in.row != nullptr ? (long long)(*in.row) * (K >> 3) : 0;
     const u32x4* X = reinterpret_cast<const u32x4*>(in.x) + off;
@@ -333,16 +324,6 @@ __device__ __forceinline__ void tile_input_finish(const GemvInput& in, TileRaw& 
   if constexpr (PRO == kInPlain) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) xc[k] = raw.a[k];
-  } else if constexpr (PRO == kInSwiglu) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const f16x2 g2 = as_f16x2(raw.a[k][e]), u2 = as_f16x2(raw.b[k][e]);
-        const f16x2 r = {silu_mul(g2.x, u2.x), silu_mul(g2.y, u2.y)};
-        xc[k][e] = as_u32(r);
-      }
-    }
   } else {
     u32x4 (&xr)[4] = raw.a;
     if (in.delta != nullptr) {
@@ -664,10 +645,7 @@ void launch_gemv_w4a16_fused(int prologue, int epilogue, int R, int pf, const vo
       launch_tile_r<kInPlain, kOutRope>(R, pf, packed, sz, in, y, N, K, log2G, st);
     return;
   }
-  if (prologue == kInRmsNorm)
-    launch_tile_r<kInRmsNorm>(R, pf, packed, sz, in, y, N, K, log2G, st);
-  else
-    launch_tile_r<kInSwiglu>(R, pf, packed, sz, in, y, N, K, log2G, st);
+  launch_tile_r<kInRmsNorm>(R, pf, packed, sz, in, y, N, K, log2G, st);
 }
 
 }  // namespace dk

@@ -14,8 +14,7 @@ namespace dk {
 constexpr int kGemvRowsMaxK = 32768;  // x in LDS: K * 2 bytes <= 64 KB per workgroup
 void launch_gemv_w4a16(int stage, int R, int waves, int pf, const void* packed, const void* sz, const void* x,
                        void* y, int N, int K, int log2G, hipStream_t st);
-// x operand of the fused row-tile GEMVs (prologue 0 = plain x, 1 = residual + RMSNorm, 2 = SwiGLU; see
-// gemv_w4a16.hip).
+// x operand of the fused row-tile GEMVs (prologue 0 = plain x, 1 = residual + RMSNorm; see gemv_w4a16.hip).
 // The RoPE + KV-append epilogue of the qkv GEMV: the arguments of the reference's rope_append op
 // (kernels/bindings.cpp rope_append) with the head count split into q and kv heads.
 struct GemvRope {
@@ -28,7 +27,7 @@ struct GemvRope {
   int n_q, n_kv, log2D, log2P, max_pos, n_pages, n_bt;
 };
 struct GemvInput {
-  const void* x;          // plain / swiglu: the input vector; rmsnorm: the residual stream (or the embedding table)
+  const void* x;          // plain: the input vector; rmsnorm: the residual stream (or the embedding table)
   const int64_t* row;     // rmsnorm: device row index into x (embedding gather) or null
   const void* delta;      // rmsnorm: residual delta or null
   const void* norm_w;     // rmsnorm: weight
@@ -76,7 +75,6 @@ struct AttnLaunch {
   float* m_part;
   float* l_part;
   void* out;
-  uint32_t* counters;  // decode op: one per kv head (zero, left zero) -> combine in the last split workgroup; or null
   int impl;            // 0 or 1 = block kernel; 2 = MFMA kernel; 3 = lean MFMA kernel
 };
 // The MFMA attention kernel stages a split's block-table pages in LDS: ((part_size - 1) >> log2P) + 2 of them at most.
@@ -94,8 +92,7 @@ inline bool attn_use_lean(const AttnLaunch& a) {
 }
 // Reference-compatible op: split kernel + combine kernel.
 void launch_paged_attention(const AttnLaunch& a, hipStream_t st);
-// Fused decode op: RoPE + KV append + split-K attention, then the combine (in the last split workgroup when
-// counters are given and max_splits <= 64, else the combine kernel).
+// Fused decode op: RoPE + KV append + split-K attention, then the combine kernel.
 void launch_attention_decode(const AttnLaunch& a, hipStream_t st);
 
 // Causal attention of M prompt rows (prefill): row m at position *pos + m attends tokens [0, *pos + m] of the cache
@@ -119,35 +116,5 @@ void launch_argmax_split(const void* logits, int V, int64_t* tok, int32_t* pos, 
 
 void launch_quantize_w4(const void* w, void* packed, void* sz, int N, int K, int log2G, int clip, hipStream_t st);
 
-// persistent decode step (decode_step.hip)
-constexpr int kStepMaxSplits = 64;  // most attention splits per kv head (one wave combines a head)
-constexpr int kStepMaxLayers = 64;   // layer table held in LDS
-constexpr int kStepOutMax = 256;    // most outputs of one workgroup in a GEMV phase (gathered in LDS)
-
-// Byte offsets of one layer's slots in the persistent step's work buffer (every slot 256-byte aligned; `layer` is the
-// size of one layer's region, layer i starts at i * layer).
-struct StepLayout {
-  size_t xq, xg, qkv, attn, o, act, down, opart, mpart, lpart, layer;
-};
-__host__ __device__ inline size_t step_align(size_t v) { return (v + 255) & ~(size_t)255; }
-__host__ __device__ inline StepLayout step_layout(int H, int n_q, int n_kv, int D, int I, int max_splits) {
-  StepLayout L;
-  size_t o = 0;
-  L.xq = o;    o += step_align((size_t)H * 2);                      // residual entering the layer
-  L.xg = o;    o += step_align((size_t)H * 2);                      // residual after the attention block
-  L.qkv = o;   o += step_align((size_t)(n_q + 2 * n_kv) * D * 2);
-  L.attn = o;  o += step_align((size_t)H * 2);
-  L.o = o;     o += step_align((size_t)H * 2);
-  L.act = o;   o += step_align((size_t)I * 2);
-  L.down = o;  o += step_align((size_t)H * 2);
-  L.opart = o; o += step_align((size_t)n_q * max_splits * D * 4);
-  L.mpart = o; o += step_align((size_t)n_q * max_splits * 4);
-  L.lpart = o; o += step_align((size_t)n_q * max_splits * 4);
-  L.layer = o;
-  return L;
-}
-bool decode_step_fits(int head_dim, int H, int I);
-int decode_step_grid(int head_dim);  // workgroups per launch on the current device (one per CU), -1 if unavailable
-int launch_decode_step(const dk_step_desc& d, int grid, hipStream_t st);
 
 }  // namespace dk

@@ -1,5 +1,4 @@
-// Paged split-K GQA decode attention (one query token) on gfx950, with an optional fused RoPE + KV append and an
-// optional in-kernel combine.
+// Paged split-K GQA decode attention (one query token) on gfx950, with an optional fused RoPE + KV append.
 //
 // Cache layout (runtime/model.py:117-120 of the reference): kc / vc fp16 [pages, n_kv, P, D]; token t of the
 // sequence lives in physical page bt[t / P], slot t % P, so one (page, kv head) holds P contiguous D-vectors.
@@ -20,18 +19,8 @@
 // With one live split the normalised output acc / l is written directly. Otherwise each split writes unnormalized
 // o, m = M, l, and the combine
 //     M* = max_s m_s;  L = sum_s e^(m_s - M*) l_s;  O = sum_s e^(m_s - M*) o_s / L
-// runs either in a second kernel, one workgroup per query head (split lanes x 4-dim groups issue all their partial
-// loads at once, keep an online maximum, and merge through LDS), or, when the caller passes a counter per kv head
-// (COMB), in the split workgroup of that kv head that finishes last:
-//   * every live split writes its partials with device-scope (agent) relaxed atomic stores, which the gfx950 L2s
-//     keep coherent across XCDs (write-through), waits until they have completed (s_waitcnt 0), and only then
-//     increments counters[kvh] with a device-scope atomic add;
-//   * the workgroup that reads nsplit - 1 from the add is the last one: it resets the counter to 0 (so the next
-//     launch, e.g. the next graph replay, starts from 0), reads every partial of its kv head with device-scope atomic
-//     loads (never a stale line of its own L2) and combines them.
-// No workgroup ever waits for another one, so the scheme cannot stall; it replaces agent-scope release / acquire
-// fences (L2 writeback / invalidate on gfx950, measured slower than a second launch) with coherent accesses to the
-// few KB of partials only.
+// runs in a second kernel, one workgroup per query head (split lanes x 4-dim groups issue all their partial loads at
+// once, keep an online maximum, and merge through LDS).
 //
 // ROPE mode (fused decode step): q and the new k come from the fused qkv vector, rotated with the rotate_half
 // convention (pairs (i, i + D/2), fp32 tables), each product rounded separately as the reference's elementwise fp32
@@ -65,23 +54,13 @@ __device__ __forceinline__ int attn_context(const int32_t* pos_ptr, int n_bt, in
   return (int)(ctx < cap ? ctx : cap);
 }
 
-// Largest split count combined inside the split kernel (the last workgroup reads HPG x nsplit x D partials).
-constexpr int kFusedCombineMaxSplits = 64;
-
-__device__ __forceinline__ void store_coherent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_coherent(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-template <int D, int HPG, bool ROPE, bool COMB>
+template <int D, int HPG, bool ROPE>
 __global__ void __launch_bounds__(kAttnThreads)
 attn_decode_kernel(const f16* __restrict__ qsrc, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
                    int max_pos, const int32_t* __restrict__ pos_ptr, const int32_t* __restrict__ bt, int n_bt,
                    f16* __restrict__ kc, f16* __restrict__ vc, int n_pages, int log2P, int n_q, int n_kv, int PS,
                    int max_splits, float scale, float* __restrict__ o_part, float* __restrict__ m_part,
-                   float* __restrict__ l_part, uint32_t* __restrict__ counters, f16* __restrict__ out) {
+                   float* __restrict__ l_part, f16* __restrict__ out) {
   using S = AttnShape<D, HPG>;
   constexpr int CPL = S::CPL, TPL = S::TPL, TB = S::TB, NTH = S::NTH, DPT = S::DPT;
   __shared__ float s_s[HPG][TB];
@@ -281,59 +260,12 @@ attn_decode_kernel(const f16* __restrict__ qsrc, const float* __restrict__ cos_t
     }
     return;
   }
-  if constexpr (!COMB) {
-    if (d0 >= D) return;
+  if (d0 >= D) return;
 #pragma unroll
-    for (int e = 0; e < DPT; ++e) o_part[((size_t)head * max_splits + split) * D + d0 + e] = acc[e];
-    if (j3 == 0) {
-      m_part[(size_t)head * max_splits + split] = M;
-      l_part[(size_t)head * max_splits + split] = l;
-    }
-  } else {
-    __shared__ float s_cm[HPG][kFusedCombineMaxSplits], s_cl[HPG][kFusedCombineMaxSplits];
-    __shared__ int s_last;
-    if (d0 < D) {
-#pragma unroll
-      for (int e = 0; e < DPT; ++e) store_coherent(&o_part[((size_t)head * max_splits + split) * D + d0 + e], acc[e]);
-      if (j3 == 0) {
-        store_coherent(&m_part[(size_t)head * max_splits + split], M);
-        store_coherent(&l_part[(size_t)head * max_splits + split], l);
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed at device scope
-    __syncthreads();                // ... and so have every other thread's
-    if (tid == 0)
-      s_last = __hip_atomic_fetch_add(&counters[kvh], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-               (uint32_t)(nsplit - 1);
-    __syncthreads();
-    if (!s_last) return;
-    if (tid == 0) __hip_atomic_store(&counters[kvh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // M* = max_s m_s;  L = sum_s e^(m_s - M*) l_s;  O = sum_s e^(m_s - M*) o_s / L   for the HPG heads of kvh
-    for (int i = tid; i < HPG * nsplit; i += kAttnThreads) {
-      const int hh = i / nsplit, ss = i % nsplit;
-      const size_t mi = (size_t)(kvh * HPG + hh) * max_splits + ss;
-      s_cm[hh][ss] = load_coherent(&m_part[mi]);
-      s_cl[hh][ss] = load_coherent(&l_part[mi]);
-    }
-    __syncthreads();
-    if (d0 >= D) return;
-    float Mx = -INFINITY;
-    for (int ss = 0; ss < nsplit; ++ss) Mx = fmaxf(Mx, s_cm[h3][ss]);
-    float Lt = 0.f, o[DPT];
-#pragma unroll
-    for (int e = 0; e < DPT; ++e) o[e] = 0.f;
-    const float* op = o_part + (size_t)head * max_splits * D + d0;
-#pragma unroll 4
-    for (int ss = 0; ss < nsplit; ++ss) {
-      const float ms = s_cm[h3][ss];
-      const float w = (ms == -INFINITY) ? 0.f : __expf(ms - Mx);
-      Lt = fmaf(w, s_cl[h3][ss], Lt);
-#pragma unroll
-      for (int e = 0; e < DPT; ++e) o[e] = fmaf(w, load_coherent(op + (size_t)ss * D + e), o[e]);
-    }
-    const float inv = Lt > 0.f ? 1.0f / Lt : 0.f;
-#pragma unroll
-    for (int e = 0; e < DPT; ++e) out[(size_t)head * D + d0 + e] = (f16)(o[e] * inv);
+  for (int e = 0; e < DPT; ++e) o_part[((size_t)head * max_splits + split) * D + d0 + e] = acc[e];
+  if (j3 == 0) {
+    m_part[(size_t)head * max_splits + split] = M;
+    l_part[(size_t)head * max_splits + split] = l;
   }
 }
 
@@ -1073,19 +1005,10 @@ void launch_attn(const AttnLaunch& a, hipStream_t st) {
                          (f16*)a.out);
     return;
   }
-  if constexpr (ROPE) {  // the in-kernel combine is offered by the decode op only
-    if (a.counters != nullptr && a.max_splits > 1 && a.max_splits <= kFusedCombineMaxSplits) {
-      hipLaunchKernelGGL((attn_decode_kernel<D, HPG, ROPE, true>), dim3(a.n_kv, a.max_splits), dim3(kAttnThreads), 0,
-                         st, (const f16*)a.q, a.cos_t, a.sin_t, a.max_pos, a.pos, a.bt, a.n_bt, (f16*)a.kc,
-                         (f16*)a.vc, a.n_pages, a.log2P, a.n_q, a.n_kv, a.part_size, a.max_splits, scale, a.o_part,
-                         a.m_part, a.l_part, a.counters, (f16*)a.out);
-      return;
-    }
-  }
-  hipLaunchKernelGGL((attn_decode_kernel<D, HPG, ROPE, false>), dim3(a.n_kv, a.max_splits), dim3(kAttnThreads), 0,
+  hipLaunchKernelGGL((attn_decode_kernel<D, HPG, ROPE>), dim3(a.n_kv, a.max_splits), dim3(kAttnThreads), 0,
                      st, (const f16*)a.q, a.cos_t, a.sin_t, a.max_pos, a.pos, a.bt, a.n_bt, (f16*)a.kc, (f16*)a.vc,
                      a.n_pages, a.log2P, a.n_q, a.n_kv, a.part_size, a.max_splits, scale, a.o_part, a.m_part,
-                     a.l_part, nullptr, (f16*)a.out);
+                     a.l_part, (f16*)a.out);
   if (a.max_splits > 1)
     hipLaunchKernelGGL((attn_combine_kernel<D>), dim3(a.n_q), dim3(kAttnThreads), 0, st, a.o_part, a.m_part,
                        a.l_part, a.pos, ROPE ? a.max_pos : 0, a.n_bt, a.log2P, a.part_size, a.max_splits,

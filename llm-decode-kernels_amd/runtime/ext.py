@@ -24,7 +24,6 @@ SIGNATURES = {
     "dk_runtime_version": ([], _I),
     "dk_gemv_w4a16": ([_I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P], _I),
     "dk_gemv_w4a16_rmsnorm": ([_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _I, _I, _P], _I),
-    "dk_gemv_w4a16_swiglu": ([_I, _I, _I, _I, _P, _P, _P, _P, _I, _I, _I, _P], _I),
     "dk_gemv_w4a16_gate_up": ([_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _I, _I, _P], _I),
     "dk_gemv_w4a16_qkv_rope": ([_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I,
                                 _I, _I, _I, _I, _I, _I, _I, _P], _I),
@@ -36,40 +35,15 @@ SIGNATURES = {
     "dk_attention_prefill": ([_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P], _I),
     "dk_bw_read": ([_P, _Z, _P, _I, _I, _I, _P], _I),
     "dk_paged_attention": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
-    "dk_attention_decode": ([_P, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P,
-                             _P], _I),
+    "dk_attention_decode": ([_P, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P],
+                            _I),
     "dk_add_rmsnorm": ([_P, _P, _P, _P, _I, _F, _P], _I),
     "dk_swiglu": ([_P, _P, _I, _P], _I),
     "dk_rope_append": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "dk_argmax_advance": ([_P, _I, _P, _P, _P], _I),
     "dk_argmax_advance_split": ([_P, _I, _P, _P, _P, _P], _I),
     "dk_quantize_w4": ([_P, _P, _P, _I, _I, _I, _I, _P], _I),
-    "dk_decode_step_grid": ([], _I),
-    "dk_decode_step_work_bytes": ([_P], _Z),
-    "dk_decode_step": ([_P, _P], _I),
 }
-
-# sync buffer of dk_decode_step (include/dk_amd.h DK_STEP_SYNC_WORDS / DK_STEP_SYNC_ABORT)
-STEP_SYNC_WORDS = 2048
-STEP_SYNC_ABORT = 1056
-
-
-class StepLayer(ctypes.Structure):
-    """dk_step_layer: device pointers of one layer's weights, norms and KV cache."""
-    _fields_ = [(n, _P) for n in ("qkv_packed", "qkv_sz", "o_packed", "o_sz", "gu_packed", "gu_sz", "down_packed",
-                                  "down_sz", "ln1", "ln2", "kc", "vc")]
-
-
-class StepDesc(ctypes.Structure):
-    """dk_step_desc: the whole persistent decode step (sizes, model tensors, activations, split buffers, sync)."""
-    _fields_ = ([(n, _I) for n in ("n_layers", "hidden", "n_q", "n_kv", "head_dim", "inter", "vocab", "group")]
-                + [("eps", _F)]
-                + [(n, _P) for n in ("emb", "norm_f", "head_w", "head_sz", "cos_t", "sin_t")]
-                + [("max_pos", _I)]
-                + [(n, _P) for n in ("tok", "pos", "bt")]
-                + [(n, _I) for n in ("n_bt", "n_pages", "page", "part_size", "max_splits")]
-                + [("work", _P), ("work_bytes", _Z)]
-                + [(n, _P) for n in ("logits", "sync", "layers")])
 
 _EXT = None
 
@@ -161,18 +135,6 @@ class DecodeKernels:
         self._call(self.lib.dk_gemv_w4a16_rmsnorm, int(stage), int(R), int(warps), int(pf), packed.data_ptr(),
                    sz.data_ptr(), x.data_ptr(), ptr(row), ptr(delta), norm_w.data_ptr(), float(eps), ptr(x_out),
                    y.data_ptr(), N, K, int(group), _stream(x))
-
-    # swiglu (kernels/bindings.cpp:74-79) fused into the down-projection gemv_w4a16
-    def gemv_w4a16_swiglu(self, stage, R, warps, pf, packed, sz, gu, y, group):
-        for t, n in ((packed, "packed"), (sz, "sz"), (gu, "gu"), (y, "y")):
-            _check_cuda(t, n)
-        K = packed.size(1) * 8
-        N = self._gemv_shape(packed, sz, y, K, group)
-        if gu.numel() != 2 * K:
-            raise RuntimeError("gemv_w4a16_swiglu: gu must hold 2 K values ([gate | up])")
-        _check_dtype(gu, torch.float16, "gu")
-        self._call(self.lib.dk_gemv_w4a16_swiglu, int(stage), int(R), int(warps), int(pf), packed.data_ptr(),
-                   sz.data_ptr(), gu.data_ptr(), y.data_ptr(), N, K, int(group), _stream(gu))
 
     # gemv_w4a16 of the interleaved gate|up rows followed by swiglu (kernels/bindings.cpp:27-38, 74-79), one launch;
     # the input is x itself (norm_w None) or the residual + RMSNorm of gemv_w4a16_rmsnorm
@@ -383,11 +345,9 @@ class DecodeKernels:
 
     # rope_append (kernels/bindings.cpp:81-88) + paged_attention (kernels/bindings.cpp:45-62) fused into one launch
     def attention_decode(self, qkv, cos_t, sin_t, pos, bt, kc, vc, n_q, n_kv, part_size, o_part, m_part, l_part,
-                         out, counters=None, impl=0):
-        """counters: None (split kernel + combine kernel) or int32 [n_kv] zeros, left zero by every call (the last
-        split workgroup of each kv head combines; one launch; block kernel only). impl: 0 or 1 = block kernel,
-        2 = MFMA kernel, 3 = lean MFMA kernel (pages >= 16 tokens, part_size a multiple of 16 up to 512, 256 at
-        head_dim 128)."""
+                         out, impl=0):
+        """impl: 0 or 1 = block kernel, 2 = MFMA kernel, 3 = lean MFMA kernel (pages >= 16 tokens, part_size a
+        multiple of 16 up to 512, 256 at head_dim 128); the split kernel is followed by the combine kernel."""
         for t, n in ((qkv, "qkv"), (cos_t, "cos_t"), (sin_t, "sin_t"), (pos, "pos"), (bt, "bt"), (kc, "kc"),
                      (vc, "vc"), (o_part, "o_part"), (m_part, "m_part"), (l_part, "l_part"), (out, "out")):
             _check_cuda(t, n)
@@ -409,16 +369,10 @@ class DecodeKernels:
         if not (o_part.size(0) == n_q and o_part.size(2) == D and m_part.shape == (n_q, max_splits)
                 and l_part.shape == (n_q, max_splits) and out.numel() == n_q * D):
             raise RuntimeError("attention_decode: buffers must be o [n_q, S, D], m/l [n_q, S], out [n_q, D]")
-        if counters is not None:
-            _check_cuda(counters, "counters")
-            _check_dtype(counters, torch.int32, "counters")
-            if counters.numel() != n_kv:
-                raise RuntimeError("attention_decode: counters must be int32 [n_kv]")
         self._call(self.lib.dk_attention_decode, qkv.data_ptr(), cos_t.data_ptr(), sin_t.data_ptr(), cos_t.size(0),
                    pos.data_ptr(), bt.data_ptr(), bt.numel(), kc.data_ptr(), vc.data_ptr(), kc.size(0), kc.size(2),
                    int(n_q), int(n_kv), D, int(part_size), max_splits, int(impl), o_part.data_ptr(),
-                   m_part.data_ptr(), l_part.data_ptr(), None if counters is None else counters.data_ptr(),
-                   out.data_ptr(), _stream(qkv))
+                   m_part.data_ptr(), l_part.data_ptr(), out.data_ptr(), _stream(qkv))
 
     # kernels/bindings.cpp:64-72
     def add_rmsnorm(self, x, delta, w, out, eps):
@@ -502,20 +456,6 @@ class DecodeKernels:
             p = pos.data_ptr()
         self._call(self.lib.dk_argmax_advance_split, logits.data_ptr(), logits.numel(), tok.data_ptr(), p,
                    work.data_ptr(), _stream(logits))
-
-    # No reference counterpart: one launch runs a decode step's whole op sequence (runtime/model.py:216-233)
-    def decode_step(self, desc, device):
-        """Persistent decode step (dk_decode_step) on the current stream of `device`; `desc` is a StepDesc."""
-        self._call(self.lib.dk_decode_step, ctypes.byref(desc),
-                   ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream))
-
-    def decode_step_work_bytes(self, desc):
-        """Bytes of the work buffer dk_decode_step needs for the sizes in `desc` (a StepDesc)."""
-        return int(self.lib.dk_decode_step_work_bytes(ctypes.byref(desc)))
-
-    def decode_step_grid(self):
-        """Workgroups of a dk_decode_step launch on the current device (one per CU); -1 without a usable device."""
-        return int(self.lib.dk_decode_step_grid())
 
     # runtime/quant.py:42-48,100-124 on the GPU
     def quantize_w4(self, w, packed, sz, group, clip=False):

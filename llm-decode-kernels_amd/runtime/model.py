@@ -61,28 +61,19 @@ class DecodeConfig:
     seed: int = 0            # block-table permutation seed
     fused_attention: bool = True   # rope_epilogue off: dk_attention_decode (RoPE + append in the split kernel) vs
                                    # rope_append + paged_attention
-    combine_in_split: bool = False # with fused_attention: the last split workgroup of each kv head merges the
-                                   # partials (per-kv-head counters) instead of a second combine launch; its three
-                                   # device-coherent round trips cost what the second launch costs on MI355X
     argmax_split_min_v: int = 16384  # vocabularies at least this large pick the next token with the multi-workgroup
                                      # argmax (dk_argmax_advance_split); smaller ones with the one-workgroup kernel
     fused_gemv: bool = True        # residual + RMSNorm (and the embedding gather) computed inside the INT4 GEMV that
                                    # consumes it (dk_gemv_w4a16_rmsnorm) instead of a separate add_rmsnorm kernel
     f16_gemv: bool = True          # fp16-weight projections with K <= 4096 (the fp16 LM head) on the HIP fp16 GEMV
                                    # (dk_gemv_f16 / dk_gemv_f16_rmsnorm) instead of torch.mm
-    persistent: bool = False       # the whole decode step as one launch (dk_decode_step: grid barriers between phases,
-                                   # next-phase weights requested ahead); needs the fused INT4 body with the SwiGLU
-                                   # epilogue layout
     rope_epilogue: bool = True     # with fused_gemv: RoPE + KV append in the qkv GEMV's epilogue
                                    # (dk_gemv_w4a16_qkv_rope over a rotation-pair copy of the qkv rows) and attention
                                    # without RoPE (dk_paged_attention) instead of dk_attention_decode; on MI355X
                                    # 1410 -> 1349 us per Llama-3-8B token at context 4096, unchanged on TinyLlama
-    step_part_size: int = 0        # tokens per attention split of the persistent step (128 or 256: 8 waves x 1 or 2
-                                   # tiles of 16; 0 = the smallest that fits the grid)
     swiglu: str = "epilogue"       # where SwiGLU runs when fused_gemv is on: "epilogue" = inside the gate|up GEMV
-                                   # (dk_gemv_w4a16_gate_up, gate/up rows stored interleaved); "prologue" = inside the
-                                   # down GEMV (dk_gemv_w4a16_swiglu: every workgroup re-evaluates silu for its columns,
-                                   # slower on MI355X); "kernel" = the separate dk_swiglu launch
+                                   # (dk_gemv_w4a16_gate_up, gate/up rows stored interleaved); "kernel" = the separate
+                                   # dk_swiglu launch
 
 
 def default_gemv_config(N, K):
@@ -164,8 +155,8 @@ class Model:
         dev = cfg.device
         self.K = ext.load()
         quant = cfg.weights == "int4"
-        if cfg.swiglu not in ("epilogue", "prologue", "kernel"):
-            raise ValueError(f"swiglu {cfg.swiglu!r}: 'epilogue', 'prologue' or 'kernel'")
+        if cfg.swiglu not in ("epilogue", "kernel"):
+            raise ValueError(f"swiglu {cfg.swiglu!r}: 'epilogue' or 'kernel'")
         self.use_fused_gemv = (cfg.fused and cfg.fused_gemv and quant and self.H <= 32768 and self.I <= 32768)
         self.gate_up_epilogue = self.use_fused_gemv and cfg.swiglu == "epilogue"
         self.rope_epilogue = self.use_fused_gemv and cfg.rope_epilogue
@@ -179,7 +170,7 @@ class Model:
                               g(p + "self_attn.v_proj.weight")], 0)
             qkv = Linear(wqkv, cfg, quant, key=f"layers.{i}.qkv")
             del wqkv
-            if self.rope_epilogue:  # decode-only copy; prefill and the persistent step read the reference order
+            if self.rope_epilogue:  # decode-only copy; prefill reads the reference order
                 qkv.rope_rows = (rope_pair_rows(qkv.packed, self.D), rope_pair_rows(qkv.sz, self.D))
             wgu = torch.cat([g(p + "mlp.gate_proj.weight"), g(p + "mlp.up_proj.weight")], 0)
             gu = Linear(wgu, cfg, quant, interleave_pairs=self.gate_up_epilogue, key=f"layers.{i}.gu")
@@ -238,111 +229,34 @@ class Model:
         self.argmax_work = torch.zeros(2, dtype=torch.int64, device=self.cfg.device)
         self.graph = None
         self.host_pos = 0
-        self.step_desc = None
-        if cfg.persistent:
-            self._setup_step()
-            self._step_partition(cfg.max_ctx)
-
-    # ------------------------------------------------------------------ persistent step
-    def _setup_step(self):
-        """Per-layer pointer table (device), sync words and the parts of the dk_decode_step descriptor that never
-        change."""
-        if not (self.use_fused_gemv and self.gate_up_epilogue):
-            raise ValueError("persistent step: needs the fused INT4 body with the SwiGLU epilogue (weights='int4', "
-                             "fused, fused_gemv, swiglu='epilogue')")
-        if not (self.cfg.page >= 16 and self.cfg.page & (self.cfg.page - 1) == 0):
-            raise ValueError("persistent step: page must be a power of two >= 16")
-        rows = []
-        for li, lw in enumerate(self.layers):
-            rows.append([lw["qkv"].packed.data_ptr(), lw["qkv"].sz.data_ptr(), lw["o"].packed.data_ptr(),
-                         lw["o"].sz.data_ptr(), lw["gu"].packed.data_ptr(), lw["gu"].sz.data_ptr(),
-                         lw["down"].packed.data_ptr(), lw["down"].sz.data_ptr(), lw["ln1"].data_ptr(),
-                         lw["ln2"].data_ptr(), self.kv[li, 0].data_ptr(), self.kv[li, 1].data_ptr()])
-        self.step_layers = torch.tensor(rows, dtype=torch.int64, device=self.cfg.device)
-        # barrier words of the step: zero here; every completed step leaves them zero
-        self.step_sync = torch.zeros(ext.STEP_SYNC_WORDS, dtype=torch.int32, device=self.cfg.device)
-        self.step_grid = self.K.decode_step_grid()
-        if self.step_grid <= 0:
-            raise RuntimeError("persistent step: no usable device (dk_decode_step_grid)")
-
-    def _step_partition(self, ctx_cap):
-        """Split size of the step's attention (one workgroup per (kv head, split), all splits of the cap at once) and
-        the descriptor, rebuilt because the split buffers change."""
-        sizes = (self.cfg.step_part_size,) if self.cfg.step_part_size else (128, 256)
-        for ps in sizes:
-            ms = max(1, math.ceil(ctx_cap / ps))
-            if ms <= 64 and self.n_kv * ms <= self.step_grid:
-                break
-        else:
-            raise ValueError(f"persistent step: context {ctx_cap} needs more than {self.step_grid} attention "
-                             f"workgroups at part sizes {sizes}")
-        self.step_part_size, self.step_max_splits = ps, ms
-        head = self.lm_head
-        d = ext.StepDesc()
-        d.n_layers, d.hidden, d.n_q, d.n_kv, d.head_dim = self.L, self.H, self.n_q, self.n_kv, self.D
-        d.inter, d.vocab, d.group, d.eps = self.I, self.V, self.cfg.group, self.eps
-        d.emb, d.norm_f = self.emb.data_ptr(), self.norm_f.data_ptr()
-        d.head_w = (head.packed if head.quant else head.w).data_ptr()
-        d.head_sz = head.sz.data_ptr() if head.quant else None
-        d.cos_t, d.sin_t, d.max_pos = self.cos.data_ptr(), self.sin.data_ptr(), self.cos.shape[0]
-        d.tok, d.pos, d.bt = self.tok.data_ptr(), self.pos.data_ptr(), self.bt.data_ptr()
-        d.n_bt, d.n_pages, d.page = self.bt.numel(), self.n_pages, self.cfg.page
-        d.part_size, d.max_splits = ps, ms
-        d.logits, d.sync, d.layers = self.logits.data_ptr(), self.step_sync.data_ptr(), self.step_layers.data_ptr()
-        nbytes = int(self.K.decode_step_work_bytes(d))
-        # per layer: residual stream, qkv, attention output, o, act, down and the split partials (each written once
-        # per step before it is read)
-        self.step_work = torch.empty(nbytes, dtype=torch.uint8, device=self.cfg.device)
-        d.work, d.work_bytes = self.step_work.data_ptr(), nbytes
-        self.step_desc = d
-        self.graph = None
-
-    def set_persistent(self, on=True):
-        """Switch the decode step between the persistent launch (dk_decode_step) and the multi-launch sequence, on
-        the same weights and cache; the next prepare() captures the chosen step."""
-        if on:
-            if getattr(self, "step_layers", None) is None:
-                self._setup_step()
-            self._step_partition(self.ctx_cap)
-        else:
-            self.step_desc = None
-        self.graph = None
-
-    def step_status(self):
-        """0 after normal persistent steps; 1 if a grid barrier timed out (the outputs are then invalid and the sync
-        words are reset here)."""
-        ab = int(self.step_sync[ext.STEP_SYNC_ABORT].item())
-        if ab:
-            self.step_sync.zero_()
-        return ab
 
     # ------------------------------------------------------------------ helpers
     def set_attention_partition(self, ctx_cap, part_size=None, impl=None):
-        """Split size (and attention kernel) for contexts up to ctx_cap and the split buffers (runtime/model.py:140-151):
-        the grid is fixed at ceil(ctx_cap / part_size) splits, surplus ones exit."""
+        """Choose the attention kernel and split size for contexts up to ctx_cap (explicit arguments, then the
+        config, then the policy entry tuned for the largest context <= ctx_cap) and allocate the split partials for
+        a grid of ceil(ctx_cap / part_size) splits; splits past the live context exit at once. The effective cap is
+        rounded up to whole splits and guarded by run_step (the behaviour of runtime/model.py:140-151)."""
         ent = self._policy_entry(ctx_cap)
         ps = part_size or self.cfg.part_size or ent.get("part_size", 64)
-        self.attn_impl = impl or self.cfg.attn_impl or ent.get("impl", 1)
-        if self.attn_impl == 2 and ((ps - 1) >> (self.cfg.page.bit_length() - 1)) + 2 > 1024:
-            self.attn_impl = 1                      # the MFMA kernel stages at most 1024 pages per split
-        if self.attn_impl == 3 and (self.cfg.page < 16 or ps % 16 or ps > (256 if self.D == 128 else 512)):
-            self.attn_impl = 1                      # the lean kernel takes whole 16-token tiles of one page
-        self.part_size = ps
-        self.max_splits = max(1, math.ceil(ctx_cap / ps))
-        self.ctx_cap = self.max_splits * ps
-        f32 = dict(dtype=torch.float32, device=self.cfg.device)
-        self.o_part = torch.empty(self.n_q, self.max_splits, self.D, **f32)
-        self.m_part = torch.empty(self.n_q, self.max_splits, **f32)
-        self.l_part = torch.empty(self.n_q, self.max_splits, **f32)
-        # per-kv-head arrival counters of the in-split combine: zero here, left zero by every launch
-        self.attn_counters = torch.zeros(self.n_kv, dtype=torch.int32, device=self.cfg.device)
+        impl = impl or self.cfg.attn_impl or ent.get("impl", 1)
+        log2p = self.cfg.page.bit_length() - 1
+        if impl == 2 and ((ps - 1) >> log2p) + 2 > 1024:
+            impl = 1                                # the MFMA kernel stages at most 1024 pages per split
+        lean_max = 256 if self.D == 128 else 512
+        if impl == 3 and (self.cfg.page < 16 or ps % 16 or ps > lean_max):
+            impl = 1                                # the lean kernel takes whole 16-token tiles of one page
+        splits = -(-ctx_cap // ps)
+        self.attn_impl, self.part_size, self.max_splits, self.ctx_cap = impl, ps, max(1, splits), max(1, splits) * ps
+        dev = self.cfg.device
+        self.o_part, self.m_part, self.l_part = (
+            torch.empty(*shape, dtype=torch.float32, device=dev)
+            for shape in ((self.n_q, self.max_splits, self.D), (self.n_q, self.max_splits), (self.n_q, self.max_splits)))
         self.graph = None
-        if getattr(self, "step_desc", None) is not None:
-            self._step_partition(ctx_cap)
 
     def prepare(self, ctx_cap, use_graph=True, part_size=None, impl=None):
         """Configure attention for contexts <= ctx_cap and (re)capture the decode graph (runtime/model.py:153-158)."""
-        assert ctx_cap <= self.cfg.max_ctx
+        if ctx_cap > self.cfg.max_ctx:
+            raise ValueError(f"prepare: context cap {ctx_cap} exceeds the cache's max_ctx {self.cfg.max_ctx}")
         self.set_attention_partition(ctx_cap, part_size, impl)
         if use_graph:
             self.capture()
@@ -427,10 +341,6 @@ class Model:
         self.K.gemv_w4a16_gate_up(s, r, wv, pf, lin.packed, lin.sz, x_in, None, delta, w, self.eps, x_out, act,
                                   self.cfg.group)
 
-    def linear_swiglu(self, lin: Linear, gu, y):
-        s, r, wv, pf = self.gemv_tile_cfg(lin)
-        self.K.gemv_w4a16_swiglu(s, r, wv, pf, lin.packed, lin.sz, gu, y, self.cfg.group)
-
     def use_f16_gemv(self, lin):
         return self.cfg.fused and self.cfg.f16_gemv and not lin.quant and lin.K <= 4096 and lin.K % 8 == 0
 
@@ -506,9 +416,7 @@ class Model:
             return
         if self.cfg.fused_attention:
             self.K.attention_decode(self.qkv, self.cos, self.sin, self.pos, self.bt, kc, vc, self.n_q, self.n_kv,
-                                    self.part_size, self.o_part, self.m_part, self.l_part, self.attn,
-                                    self.attn_counters if self.cfg.combine_in_split else None,
-                                    1 if self.cfg.combine_in_split else self.attn_impl)
+                                    self.part_size, self.o_part, self.m_part, self.l_part, self.attn, self.attn_impl)
             return
         self.K.rope_append(self.qkv, self.cos, self.sin, self.pos, self.bt, kc, vc, self.n_q, self.n_kv)
         self.K.paged_attention(self.qkv[: self.n_q * self.D], kc, vc, self.bt, self.pos, self.part_size,
@@ -517,9 +425,6 @@ class Model:
     # ------------------------------------------------------------------ decode step
     def step(self):
         """One token: reads tok/pos, writes logits, tok <- argmax, pos += 1 (runtime/model.py:216-233)."""
-        if self.step_desc is not None:
-            self.K.decode_step(self.step_desc, self.cfg.device)
-            return
         if self.use_fused_gemv:
             self.step_fused()
             return
@@ -564,11 +469,8 @@ class Model:
             else:
                 self.linear_norm(lw["gu"], cur, self.o, lw["ln2"], nxt, self.gu)
                 cur, nxt = nxt, cur
-                if self.cfg.swiglu == "prologue":
-                    self.linear_swiglu(lw["down"], self.gu, self.down)
-                else:
-                    self.K.swiglu(self.gu, self.act)
-                    self.linear(lw["down"], self.act, self.down)
+                self.K.swiglu(self.gu, self.act)
+                self.linear(lw["down"], self.act, self.down)
             delta = self.down
         if self.lm_head.quant and self.norm_fusion_pays(self.lm_head):
             self.linear_norm(self.lm_head, cur, delta, self.norm_f, None, self.logits)
@@ -580,50 +482,75 @@ class Model:
             self.linear(self.lm_head, self.normed, self.logits)
         self.pick_next()
 
+    def _keep_state(self):
+        """Context manager: the device token and position as they are now, put back on exit."""
+        model = self
+
+        class _Keep:
+            def __enter__(self):
+                self.saved = torch.cat([model.tok, model.pos.to(torch.long)])
+                return self
+
+            def __exit__(self, *exc):
+                model.tok.copy_(self.saved[:1])
+                model.pos.copy_(self.saved[1:].to(torch.int32))
+                return False
+
+        return _Keep()
+
     def capture(self):
-        """Capture step() into a hipGraph after warm-up on a side stream (runtime/model.py:235-251)."""
-        saved_tok, saved_pos = self.tok.clone(), self.pos.clone()
-        self.pos.zero_()
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            for _ in range(2):
+        """Record step() into a hipGraph (torch.cuda.CUDAGraph), the role of runtime/model.py:235-251: two warm-up
+        steps run on a side stream at position 0 (the split buffers are sized for the prepared cap, which a stale
+        position could exceed; the K/V the warm-up writes sit at positions every real step overwrites before reading),
+        then one step is recorded. Token and position are left as they were."""
+        with self._keep_state():
+            self.pos.zero_()
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
                 self.step()
-        torch.cuda.current_stream().wait_stream(s)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self.step()
-        self.tok.copy_(saved_tok)
-        self.pos.copy_(saved_pos)
+                self.step()
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self.step()
+            self.graph = graph
         torch.cuda.synchronize()
 
+    def _claim_positions(self, n):
+        """Account for n more steps on the host and refuse them if attention was not prepared that far (tokens past
+        the cap would silently not be attended)."""
+        end = self.host_pos + n
+        if end > self.ctx_cap:
+            raise RuntimeError(f"context {end} exceeds the prepared attention cap {self.ctx_cap}; call prepare()")
+        self.host_pos = end
+
     def run_step(self, use_graph=True):
-        self.host_pos += 1
-        if self.host_pos > self.ctx_cap:
-            raise RuntimeError(f"context {self.host_pos} exceeds the prepared attention cap {self.ctx_cap}; "
-                               "call prepare()")
-        if use_graph and self.graph is not None:
-            self.graph.replay()
-        else:
-            self.step()
+        """One token through the captured graph (or eagerly without one)."""
+        self._claim_positions(1)
+        (self.graph.replay if use_graph and self.graph is not None else self.step)()
 
     # ------------------------------------------------------------------ high level
     def reset(self, pos=0):
-        self.pos.fill_(pos)
-        self.host_pos = pos
+        """Start a sequence at position pos (device and host mirror); the cache below pos is kept."""
+        self.host_pos = int(pos)
+        self.pos.fill_(self.host_pos)
 
     def teacher_force(self, tokens, use_graph=True, collect_logits=False):
-        """Feed tokens[i] at positions pos..; returns logits [len, V] (fp16) if requested."""
-        tokens = torch.as_tensor(tokens, device=self.tok.device).long()
-        if len(tokens) and (int(tokens.min()) < 0 or int(tokens.max()) >= self.V):
-            raise ValueError(f"teacher_force: token ids must lie in [0, {self.V})")  # the step gathers embedding rows
-        out = torch.empty(len(tokens), self.V, dtype=torch.half, device=self.tok.device) if collect_logits else None
-        for i in range(len(tokens)):
-            self.tok.copy_(tokens[i:i + 1])
+        """Step through the given token ids (each fed as the step's input token) from the current position; returns
+        the logits of every step (fp16 [len, V]) when collect_logits is set."""
+        ids = torch.as_tensor(tokens, dtype=torch.long).reshape(-1).to(self.tok.device)
+        if ids.numel() and not bool(((ids >= 0) & (ids < self.V)).all()):
+            raise ValueError(f"teacher_force: token ids must lie in [0, {self.V})")  # they index embedding rows
+        rows = []
+        for t in range(ids.numel()):
+            self.tok.copy_(ids[t:t + 1])
             self.run_step(use_graph)
             if collect_logits:
-                out[i].copy_(self.logits)
-        return out
+                rows.append(self.logits.clone())
+        if not collect_logits:
+            return None
+        return torch.stack(rows) if rows else torch.empty(0, self.V, dtype=torch.half, device=self.tok.device)
 
     def _prefill_buffers(self, M):
         if getattr(self, "_pf_rows", 0) < M:
@@ -704,28 +631,33 @@ class Model:
         self.host_pos = start + M
 
     def generate(self, prompt, n_new, use_graph=True, prefill=False):
-        """Greedy: teacher-force the prompt (or prefill it in one pass), then free-run n_new tokens
-        (runtime/model.py:278-286)."""
+        """Greedy decoding from position 0 (runtime/model.py:278-286): the prompt teacher-forced (or prefilled in one
+        pass), then n_new tokens. The tokens are gathered on the device and read back once at the end."""
         self.reset(0)
-        if prefill:
-            self.prefill(prompt)
-        else:
-            self.teacher_force(prompt, use_graph)
-        new = [int(self.tok)]
-        for _ in range(n_new - 1):
+        (self.prefill if prefill else lambda p: self.teacher_force(p, use_graph))(prompt)
+        picked = torch.empty(max(n_new, 1), dtype=torch.long, device=self.tok.device)
+        picked[:1].copy_(self.tok)
+        for i in range(1, n_new):
             self.run_step(use_graph)
-            new.append(int(self.tok))
-        return new
+            picked[i:i + 1].copy_(self.tok)
+        return picked[:n_new].tolist()
 
     # ------------------------------------------------------------------ byte accounting (roofline)
+    def _projections(self):
+        for lw in self.layers:
+            yield from (lw[k] for k in ("qkv", "o", "gu", "down"))
+
     def weight_bytes(self):
-        b = sum(l[k].nbytes for l in self.layers for k in ("qkv", "o", "gu", "down"))
-        b += sum(l["ln1"].numel() * 2 + l["ln2"].numel() * 2 for l in self.layers)
-        return {"body": b, "lm_head": self.lm_head.nbytes, "embedding_row": self.H * 2}
+        """Bytes of weights one token reads, from the built tensors: every projection of the body with the two norm
+        vectors per layer, the LM head, and one embedding row (the byte model of runtime/model.py:289-297)."""
+        norms = sum(lw[k].numel() * lw[k].element_size() for lw in self.layers for k in ("ln1", "ln2"))
+        return {"body": sum(p.nbytes for p in self._projections()) + norms, "lm_head": self.lm_head.nbytes,
+                "embedding_row": self.emb[0].numel() * self.emb.element_size()}
 
     def kv_bytes_per_token(self, ctx):
-        row = self.n_kv * self.D * 2
-        return self.L * (2 * row * ctx + 2 * row)
+        """K and V bytes of all layers that one token moves: ctx cached rows read, one new row written."""
+        row = self.kv[0, 0, 0, :, 0].numel() * self.kv.element_size()    # one token's K (or V) of one layer
+        return 2 * row * self.L * (ctx + 1)
 
     def activation_bytes(self):
         """fp16 activation vectors read/written per token (bench/analyze.py:40 of the reference)."""

@@ -37,72 +37,87 @@ def quantize_pack(w: torch.Tensor, group: int, clip: bool = False):
 
 
 def group_params(wf: torch.Tensor, clip: bool = False):
-    """wf fp32 [..., G] -> (scale, zero) fp32 [..., 1] (runtime/quant.py:20-38): the fp16-rounded scale and integer
-    zero of the group's [min, max]; with clip, of the range shrunk by the CLIP_GRID factor with the smallest squared
-    rounding error (fp32 sums, first factor on ties). Used inside GPTQ, where each group's parameters come from the
-    error-updated weights."""
-    mn0 = wf.amin(-1, keepdim=True)
-    mx0 = wf.amax(-1, keepdim=True)
-    best = None
-    for a in (CLIP_GRID if clip else (1.0,)):
-        mn, mx = mn0 * a, mx0 * a
-        scale = ((mx - mn) / 15).clamp(min=1e-6).half().float()
-        zero = torch.round(-mn / scale).clamp(0, 15)
-        if not clip:
-            return scale, zero
-        err = ((torch.clamp(torch.round(wf / scale) + zero, 0, 15) - zero) * scale - wf).pow(2).sum(-1, keepdim=True)
-        if best is None:
-            best = [err, scale, zero]
-        else:
-            m = err < best[0]
-            best = [torch.where(m, err, best[0]), torch.where(m, scale, best[1]), torch.where(m, zero, best[2])]
-    return best[1], best[2]
+    """wf fp32 [..., G] -> (scale, zero) fp32 [..., 1]: the parameters of each group of G weights (the convention of
+    runtime/quant.py:20-38 of the reference): scale = fp16((hi - lo) / 15) floored at 1e-6 and read back as fp32,
+    zero = rint(-lo / scale) clamped to [0, 15].
+
+    Without clip, [lo, hi] is the group's range. With clip, every factor a of CLIP_GRID shrinks it to [a lo, a hi];
+    the candidates are evaluated together along a leading grid axis and each group keeps the factor with the
+    smallest sum of squared rounding errors (fp32 terms, summed over the group in fp32), the first one on ties
+    (argmin's choice, the same as a strict-less-than scan over the grid in order)."""
+    lo, hi = wf.amin(-1, keepdim=True), wf.amax(-1, keepdim=True)
+
+    def params(a_lo, a_hi):
+        scale = ((a_hi - a_lo) / 15).clamp(min=1e-6).half().float()
+        return scale, torch.round(-a_lo / scale).clamp(0, 15)
+
+    if not clip:
+        return params(lo, hi)
+    a = torch.tensor(CLIP_GRID, dtype=wf.dtype, device=wf.device).view(-1, *([1] * wf.dim()))
+    scale, zero = params(lo.unsqueeze(0) * a, hi.unsqueeze(0) * a)                  # [F, ..., 1]
+    wq = torch.clamp(torch.round(wf.unsqueeze(0) / scale) + zero, 0, 15)
+    err = ((wq - zero) * scale - wf.unsqueeze(0)).pow(2).sum(-1, keepdim=True)       # [F, ..., 1]
+    pick = err.argmin(dim=0, keepdim=True)
+    return scale.gather(0, pick).squeeze(0), zero.gather(0, pick).squeeze(0)
+
+
+class _InverseHessianFactor:
+    """U = the upper Cholesky factor of (H + damp * mean(diag H) * I)^-1, the quantity GPTQ propagates rounding errors
+    through (Frantar et al. 2022, section 3.3: row j of U holds the error weights of column j onto columns >= j).
+    Input channels that never fire (H_jj = 0) are given H_jj = 1 before damping; their weights are zeroed by the
+    caller, so they quantize to the zero point and spread no error."""
+
+    def __init__(self, H: torch.Tensor, damp: float):
+        H = H.float().clone()
+        self.dead = torch.diag(H) == 0
+        H[self.dead, self.dead] = 1
+        H += damp * torch.diag(H).mean() * torch.eye(H.shape[0], device=H.device)
+        chol = torch.linalg.cholesky(H)                       # H = L L^T
+        self.U = torch.linalg.cholesky(torch.cholesky_inverse(chol), upper=True)
 
 
 @torch.no_grad()
 def quantize_gptq(w: torch.Tensor, H: torch.Tensor, group: int, clip: bool = False, damp: float = 0.01,
                   block: int = 128):
-    """GPTQ (Frantar et al. 2022) into the format of ``quantize``: (q uint8 [N, K], scale, zero fp16 [N, K/G]).
+    """GPTQ (Frantar et al. 2022, Algorithm 1) into the format of ``quantize``: returns (q uint8 [N, K], scale,
+    zero fp16 [N, K/G]), with the numbers of runtime/quant.py:51-90 of the reference.
 
-    The algorithm of runtime/quant.py:51-90 of the reference: columns are quantized left to right in blocks of
-    ``block``; each column's rounding error, divided by the diagonal of the upper Cholesky factor of H^-1, is spread
-    over the block's remaining columns, and a block's errors over the later blocks with one GEMM, so the error of the
-    layer output X W^T (H = 2 X^T X / n) is minimised rather than the weight error. A group's (scale, zero) are taken
-    when the group starts, from the error-updated weights; no activation reordering, so groups stay contiguous and
-    the GEMV reads the result unchanged. Dead input channels (H_jj = 0) get zero weights; ``damp`` adds
-    damp * mean(diag H) to the diagonal."""
+    The weight is swept left to right in blocks of ``block`` columns, in place on an fp32 copy:
+      * when a column starts a group, the group's (scale, zero) come from its columns as they stand then, i.e.
+        after the errors of every earlier column were spread onto them (``group_params``; no activation
+        reordering, so groups stay contiguous and the GEMV reads the result unchanged);
+      * column j is rounded with its group's parameters; its error e = (w_j - deq(q_j)) / U_jj is subtracted,
+        weighted by row j of U, from the columns j .. end of the block (a rank-1 update);
+      * at the end of a block, the block's errors reach every later column at once through one GEMM with the
+        U rows of the block ("lazy batch update").
+    The layer output error ||X W^T - X deq(Q)^T|| (H = 2 X^T X / n) is minimised rather than the weight error."""
     N, K = w.shape
     if K % group or block % group:
         raise ValueError(f"K={K} and block={block} must be multiples of group={group}")
+    hf = _InverseHessianFactor(H, damp)
+    U = hf.U
     W = w.float().clone()
-    H = H.float().clone()
-    dead = torch.diag(H) == 0
-    H[dead, dead] = 1
-    W[:, dead] = 0
-    H += damp * torch.diag(H).mean() * torch.eye(K, device=H.device)
-    Hinv = torch.linalg.cholesky(torch.cholesky_inverse(torch.linalg.cholesky(H)), upper=True)
-    Q = torch.zeros(N, K, dtype=torch.uint8, device=W.device)
-    S = torch.zeros(N, K // group, device=W.device)
-    Z = torch.zeros(N, K // group, device=W.device)
-    for i1 in range(0, K, block):
-        i2 = min(i1 + block, K)
-        W1 = W[:, i1:i2].clone()
-        Err = torch.zeros_like(W1)
-        Hi = Hinv[i1:i2, i1:i2]
-        for i in range(i2 - i1):
-            c = i1 + i
-            if c % group == 0:                # the group lies inside this block (block % group == 0)
-                s, z = group_params(W1[:, i:i + group], clip)
-                S[:, c // group], Z[:, c // group] = s[:, 0], z[:, 0]
-                scale, zero = s[:, 0], z[:, 0]
-            col = W1[:, i]
-            q = torch.clamp(torch.round(col / scale) + zero, 0, 15)
-            Q[:, c] = q.to(torch.uint8)
-            e = (col - (q - zero) * scale) / Hi[i, i]
-            W1[:, i:] -= e[:, None] * Hi[i, i:][None, :]
-            Err[:, i] = e
-        W[:, i2:] -= Err @ Hinv[i1:i2, i2:]
-    return Q, S.half(), Z.half()
+    W[:, hf.dead] = 0
+    codes = torch.zeros(N, K, dtype=torch.uint8, device=W.device)
+    scales = torch.zeros(N, K // group, device=W.device)
+    zeros = torch.zeros(N, K // group, device=W.device)
+    for b0 in range(0, K, block):
+        b1 = min(b0 + block, K)
+        errs = torch.zeros(N, b1 - b0, device=W.device)
+        for j in range(b0, b1):
+            if j % group == 0:                                   # block % group == 0: the group lies in this block
+                s, z = group_params(W[:, j:j + group], clip)
+                scales[:, j // group], zeros[:, j // group] = s[:, 0], z[:, 0]
+            g = j // group
+            sc, zp = scales[:, g], zeros[:, g]
+            col = W[:, j]
+            qj = torch.clamp(torch.round(col / sc) + zp, 0, 15)
+            codes[:, j] = qj.to(torch.uint8)
+            e = (col - (qj - zp) * sc) / U[j, j]
+            W[:, j:b1] -= e[:, None] * U[j, j:b1][None, :]
+            errs[:, j - b0] = e
+        W[:, b1:] -= errs @ U[b0:b1, b1:]
+    return codes, scales.half(), zeros.half()
 
 
 def pack_codes(q: torch.Tensor, scale: torch.Tensor, zero: torch.Tensor):

@@ -20,8 +20,8 @@ def K():
     return ext.load()
 
 
-MODES = ("block", "counters", "mfma", "lean")   # impl 1, impl 1 with the in-split combine, impl 2, impl 3
-IMPL = {"block": 1, "counters": 1, "mfma": 2, "lean": 3}
+MODES = ("block", "mfma", "lean")   # impl 1, impl 2, impl 3
+IMPL = {"block": 1, "mfma": 2, "lean": 3}
 
 
 def lean_fits(PS, page, D):
@@ -30,26 +30,21 @@ def lean_fits(PS, page, D):
 
 
 def run_fused(K, qkv, cos, sin, kc, vc, bt, pos, n_q, n_kv, PS, max_splits, mode="block"):
-    """mode "counters": the in-split combine (per-kv-head arrival counters, which every launch must leave at zero).
-    A part size the lean kernel cannot take is checked to be rejected; then None is returned."""
-    counters = mode == "counters"
+    """A part size the lean kernel cannot take is checked to be rejected; then None is returned."""
     D = kc.shape[-1]
     if mode == "lean" and not lean_fits(PS, kc.shape[2], D):
         with pytest.raises(RuntimeError, match="impl 3 needs pages"):
             K.attention_decode(qkv, cos, sin, torch.tensor([pos], dtype=torch.int32, device=DEV), bt, kc, vc, n_q,
                                n_kv, PS, torch.empty(n_q, max_splits, D, device=DEV),
                                torch.empty(n_q, max_splits, device=DEV), torch.empty(n_q, max_splits, device=DEV),
-                               torch.empty(n_q, D, dtype=torch.half, device=DEV), None, impl=3)
+                               torch.empty(n_q, D, dtype=torch.half, device=DEV), impl=3)
         return None, None, None
     o_part = torch.full((n_q, max_splits, D), 7.0, device=DEV)
     m_part = torch.full((n_q, max_splits), 7.0, device=DEV)
     l_part = torch.full((n_q, max_splits), 7.0, device=DEV)
     out = torch.zeros(n_q, D, dtype=torch.half, device=DEV)
-    cnt = torch.zeros(n_kv, dtype=torch.int32, device=DEV) if counters else None
     K.attention_decode(qkv, cos, sin, torch.tensor([pos], dtype=torch.int32, device=DEV), bt, kc, vc, n_q, n_kv, PS,
-                       o_part, m_part, l_part, out, cnt, impl=IMPL[mode])
-    if counters:
-        assert torch.all(cnt == 0), "arrival counters must be left at zero"
+                       o_part, m_part, l_part, out, impl=IMPL[mode])
     return out, o_part, m_part
 
 
@@ -132,7 +127,7 @@ def test_fused_attention_position_outside_table_is_noop(K, mode):
 @pytest.mark.parametrize("mode", MODES)
 def test_fused_attention_graph_replays(K, mode):
     """One captured launch replayed at several positions (the graph reads *pos anew), eager work between replays;
-    every replay equals the eager result; the in-split combine's counters are back at zero after every replay."""
+    every replay equals the eager result."""
     D, n_q, n_kv, page, PS, ms = 64, 32, 4, 16, 32, 10
     cap = PS * ms
     cos, sin = (t.to(DEV) for t in R.rope_tables(cap + 1, D))
@@ -144,10 +139,9 @@ def test_fused_attention_graph_replays(K, mode):
     m_part = torch.empty(n_q, ms, device=DEV)
     l_part = torch.empty_like(m_part)
     out = torch.empty(n_q, D, dtype=torch.half, device=DEV)
-    cnt = torch.zeros(n_kv, dtype=torch.int32, device=DEV) if mode == "counters" else None
 
     def body():
-        K.attention_decode(qkv, cos, sin, pos, bt, kc, vc, n_q, n_kv, PS, o_part, m_part, l_part, out, cnt,
+        K.attention_decode(qkv, cos, sin, pos, bt, kc, vc, n_q, n_kv, PS, o_part, m_part, l_part, out,
                            impl=IMPL[mode])
 
     expected = {}
@@ -174,5 +168,4 @@ def test_fused_attention_graph_replays(K, mode):
             graph.replay()
             torch.cuda.synchronize()
             assert torch.equal(out, expected[p][0]) and torch.equal(kc, expected[p][1]), (rep, p)
-            assert cnt is None or torch.all(cnt == 0), (rep, p)
             _ = (qkv.float() * 2).sum().item()

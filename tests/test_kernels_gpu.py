@@ -478,19 +478,6 @@ def test_gemv_rmsnorm_fused(K, N, Kd, mode):
         assert torch.equal(x_out.cpu(), xr), f"residual {mode} {cfg}"
 
 
-@pytest.mark.parametrize("N,Kd", [(2048, 5632), (4096, 14336), (512, 2048)])
-def test_gemv_swiglu_fused(K, N, Kd):
-    G = 128
-    w, packed, sz = _quantized(K, N, Kd, G, seed=N + 3)
-    wref = dequant_from_gpu(packed, sz, G)
-    gu = (torch.randn(2 * Kd, generator=gen(Kd)) * 2).half()
-    ref = R.gemv_ref(wref, R.swiglu_ref(gu))
-    y = torch.empty(N, dtype=torch.half, device=DEV)
-    for cfg in ((4, 2, 0, 0), (4, 1, 0, 1), (4, 4, 0, 3)):
-        K.gemv_w4a16_swiglu(*cfg, packed, sz, gu.to(DEV), y, G)
-        assert_close(y, ref, 5e-3, f"gemv_swiglu {N}x{Kd} {cfg}")
-
-
 @pytest.mark.parametrize("I,Kd", [(5632, 2048), (14336, 4096), (40, 256), (1000, 5632)])
 @pytest.mark.parametrize("norm", (False, True))
 def test_gemv_gate_up_swiglu_epilogue(K, I, Kd, norm):
@@ -598,7 +585,7 @@ def test_fused_step_equals_unfused_step(K):
     from runtime.synth import LlamaShape, SyntheticLlama
     shape = LlamaShape(512, 3, 8, 2, 1024, 700)
     out = []
-    for fused, swiglu in ((False, "kernel"), (True, "kernel"), (True, "prologue"), (True, "epilogue")):
+    for fused, swiglu in ((False, "kernel"), (True, "kernel"), (True, "epilogue")):
         m = Model(SyntheticLlama(shape, seed=4, device=DEV, std=0.05), shape,
                   DecodeConfig(max_ctx=64, device=DEV, fused_gemv=fused, swiglu=swiglu))
         m.prepare(64)
@@ -608,7 +595,7 @@ def test_fused_step_equals_unfused_step(K):
         err = ((o - out[0]).abs().max() / out[0].abs().max()).item()
         assert err <= 5e-3, err
     # the gate|up SwiGLU epilogue rounds exactly where the separate swiglu kernel does
-    assert torch.equal(out[1], out[3])
+    assert torch.equal(out[1], out[2])
 
 
 # ------------------------------------------------------------------------------- qkv GEMV with the RoPE + append epilogue
