@@ -191,6 +191,25 @@ int dk_paged_attention(int version, const void* q, const void* kc, const void* v
                        void* stream);
 
 /*
+ * dk_paged_attention without caller-provided split buffers, for callers that cannot allocate device memory (code
+ * under hipGraph capture that must not call hipMalloc, tight serving loops, harnesses that forbid allocation). It
+ * has no counterpart in the reference. The split partials live in a library-owned device array of
+ * DK_NOALLOC_SCRATCH_BYTES bytes, one per GPU, held until the process ends; the call allocates nothing. Every call
+ * on a GPU shares that GPU's array: calls that overlap on one GPU (two streams, two threads) race, so serialize them.
+ * Nothing in the array has to start at zero (every partial the combine reads is written by the same call). Must be
+ * called with the stream's device current (its first call on a device resolves the array's address there).
+ * Arguments, limits and results as dk_paged_attention; additionally the partials of n_q x max_splits x head_dim must
+ * fit: dk_paged_attention_noalloc_bytes(n_q, head_dim, max_splits) <= DK_NOALLOC_SCRATCH_BYTES, else DK_ERR_SHAPE.
+ */
+#define DK_NOALLOC_SCRATCH_BYTES (4u << 20)
+int dk_paged_attention_noalloc(int version, const void* q, const void* kc, const void* vc, const int32_t* bt,
+                               const int32_t* pos, int n_q, int n_kv, int head_dim, int page, int n_pages, int n_bt,
+                               int part_size, int max_splits, void* out, void* stream);
+
+/* Bytes of scratch dk_paged_attention_noalloc needs for these sizes (0 for non-positive sizes). */
+size_t dk_paged_attention_noalloc_bytes(int n_q, int head_dim, int max_splits);
+
+/*
  * Fused decode attention: rope_append followed by paged_attention with one fewer launch, for callers that own the
  * whole decode step (no counterpart in the reference's binding: it fuses rope_append, kernels/bindings.cpp:81-88,
  * and the split kernel of paged_attention, kernels/bindings.cpp:45-62, as runtime/model.py:205-213 calls them back to

@@ -4,6 +4,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "dk_amd.h"
 #include "launch.hpp"
 
@@ -254,12 +256,15 @@ int dk_bw_read(const void* buf, size_t bytes, void* sink, int blocks, int thread
   return launched("bw_read");
 }
 
-int dk_paged_attention(int version, const void* q, const void* kc, const void* vc, const int32_t* bt,
-                       const int32_t* pos, int n_q, int n_kv, int head_dim, int page, int n_pages, int n_bt,
-                       int part_size, int max_splits, float* o_part, float* m_part, float* l_part, void* out,
-                       void* stream) {
-  if (!q || !kc || !vc || !bt || !pos || !out || !o_part || !m_part || !l_part)
-    return fail(DK_ERR_NULL, "paged_attention: null pointer argument");
+}  // extern "C"
+
+namespace {
+
+// Argument checks shared by dk_paged_attention and dk_paged_attention_noalloc (everything but the split buffers).
+int check_paged_attention(int version, const void* q, const void* kc, const void* vc, const int32_t* bt,
+                          const int32_t* pos, int n_q, int n_kv, int head_dim, int page, int n_pages, int n_bt,
+                          int part_size, int max_splits, const void* out) {
+  if (!q || !kc || !vc || !bt || !pos || !out) return fail(DK_ERR_NULL, "paged_attention: null pointer argument");
   if (head_dim != 64 && head_dim != 128)
     return fail(DK_ERR_SHAPE, "paged_attention: head_dim must be 64 or 128, got %d", head_dim);
   if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0)
@@ -282,13 +287,98 @@ int dk_paged_attention(int version, const void* q, const void* kc, const void* v
   if (n_kv > 65535 || n_q > 65535) return fail(DK_ERR_SHAPE, "paged_attention: too many heads");
   if (!aligned16(q) || !aligned16(kc) || !aligned16(vc))
     return fail(DK_ERR_ALIGN, "q, kc and vc must be 16B aligned");
-  if (!aligned16(o_part)) return fail(DK_ERR_ALIGN, "o_part must be 16B aligned");
-  clear_error();
+  return DK_OK;
+}
+
+void launch_reference_attention(int version, const void* q, const void* kc, const void* vc, const int32_t* bt,
+                                const int32_t* pos, int n_q, int n_kv, int head_dim, int page, int n_pages, int n_bt,
+                                int part_size, int max_splits, float* o_part, float* m_part, float* l_part,
+                                void* out, void* stream) {
   const dk::AttnLaunch a{q, nullptr, nullptr, 0, pos, bt, n_bt, const_cast<void*>(kc), const_cast<void*>(vc), n_pages,
                          ilog2(page), n_q, n_kv, head_dim, part_size, max_splits, o_part, m_part, l_part, out,
                          version == 5 ? 3 : version == 4 ? 2 : 1};
   dk::launch_paged_attention(a, (hipStream_t)stream);
+}
+
+// ---- scratch of dk_paged_attention_noalloc ---------------------------------------------------------------------
+// The split partials of the allocation-free attention live in this file-scope device array; every GPU the library
+// runs on holds its own copy until the process ends, and every call on a GPU shares it (calls that overlap on one
+// GPU race). In host code the name `scratch` is a stand-in, not a device address: the entry point's first call on a
+// device resolves the device address with hipGetSymbolAddress, with that device current, keeps it per device, and
+// only that address is ever passed to a kernel.
+static __device__ __align__(256) unsigned char scratch[DK_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_of_current_device(void** ptr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(DK_ERR_LAUNCH, "paged_attention_noalloc: no current device (or device id >= %d)", kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(DK_ERR_LAUNCH, "paged_attention_noalloc: hipGetSymbolAddress of the scratch array failed: %s",
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return DK_OK;
+}
+
+size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+}  // namespace
+
+extern "C" {
+
+int dk_paged_attention(int version, const void* q, const void* kc, const void* vc, const int32_t* bt,
+                       const int32_t* pos, int n_q, int n_kv, int head_dim, int page, int n_pages, int n_bt,
+                       int part_size, int max_splits, float* o_part, float* m_part, float* l_part, void* out,
+                       void* stream) {
+  if (!o_part || !m_part || !l_part) return fail(DK_ERR_NULL, "paged_attention: null pointer argument");
+  const int rc = check_paged_attention(version, q, kc, vc, bt, pos, n_q, n_kv, head_dim, page, n_pages, n_bt,
+                                       part_size, max_splits, out);
+  if (rc != DK_OK) return rc;
+  if (!aligned16(o_part)) return fail(DK_ERR_ALIGN, "o_part must be 16B aligned");
+  clear_error();
+  launch_reference_attention(version, q, kc, vc, bt, pos, n_q, n_kv, head_dim, page, n_pages, n_bt, part_size,
+                             max_splits, o_part, m_part, l_part, out, stream);
   return launched("paged_attention");
+}
+
+size_t dk_paged_attention_noalloc_bytes(int n_q, int head_dim, int max_splits) {
+  if (n_q <= 0 || head_dim <= 0 || max_splits <= 0) return 0;
+  const size_t cells = (size_t)n_q * (size_t)max_splits;
+  return round256(cells * (size_t)head_dim * 4) + 2 * round256(cells * 4);
+}
+
+int dk_paged_attention_noalloc(int version, const void* q, const void* kc, const void* vc, const int32_t* bt,
+                               const int32_t* pos, int n_q, int n_kv, int head_dim, int page, int n_pages, int n_bt,
+                               int part_size, int max_splits, void* out, void* stream) {
+  const int rc = check_paged_attention(version, q, kc, vc, bt, pos, n_q, n_kv, head_dim, page, n_pages, n_bt,
+                                       part_size, max_splits, out);
+  if (rc != DK_OK) return rc;
+  const size_t need = dk_paged_attention_noalloc_bytes(n_q, head_dim, max_splits);
+  if (need > (size_t)DK_NOALLOC_SCRATCH_BYTES)
+    return fail(DK_ERR_SHAPE, "paged_attention_noalloc: the split partials of %d heads x %d splits x head_dim %d "
+                "need %zu bytes, more than the %u-byte scratch array; use dk_paged_attention with caller buffers "
+                "or a larger part_size", n_q, max_splits, head_dim, need, (unsigned)DK_NOALLOC_SCRATCH_BYTES);
+  void* base = nullptr;
+  const int rs = scratch_of_current_device(&base);
+  if (rs != DK_OK) return rs;
+  const size_t cells = (size_t)n_q * (size_t)max_splits;
+  unsigned char* b = static_cast<unsigned char*>(base);
+  float* o_part = reinterpret_cast<float*>(b);
+  float* m_part = reinterpret_cast<float*>(b + round256(cells * (size_t)head_dim * 4));
+  float* l_part = reinterpret_cast<float*>(b + round256(cells * (size_t)head_dim * 4) + round256(cells * 4));
+  clear_error();
+  launch_reference_attention(version, q, kc, vc, bt, pos, n_q, n_kv, head_dim, page, n_pages, n_bt, part_size,
+                             max_splits, o_part, m_part, l_part, out, stream);
+  return launched("paged_attention_noalloc");
 }
 
 int dk_attention_decode(const void* qkv, const float* cos_t, const float* sin_t, int max_pos, const int32_t* pos,

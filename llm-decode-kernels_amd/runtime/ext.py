@@ -35,6 +35,8 @@ SIGNATURES = {
     "dk_attention_prefill": ([_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P], _I),
     "dk_bw_read": ([_P, _Z, _P, _I, _I, _I, _P], _I),
     "dk_paged_attention": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
+    "dk_paged_attention_noalloc": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P], _I),
+    "dk_paged_attention_noalloc_bytes": ([_I, _I, _I], _Z),
     "dk_attention_decode": ([_P, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P],
                             _I),
     "dk_add_rmsnorm": ([_P, _P, _P, _P, _I, _F, _P], _I),
@@ -342,6 +344,29 @@ class DecodeKernels:
         self._call(self.lib.dk_paged_attention, int(version), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
                    bt.data_ptr(), pos.data_ptr(), n_q, n_kv, D, P, kc.size(0), bt.numel(), int(part_size),
                    max_splits, o_part.data_ptr(), m_part.data_ptr(), l_part.data_ptr(), out.data_ptr(), _stream(q))
+
+    # paged_attention with its split partials in the library's per-device scratch array (no caller buffers, no
+    # allocation); calls that overlap on one GPU race
+    def paged_attention_noalloc(self, q, kc, vc, bt, pos, part_size, max_splits, out, version=5):
+        for t, n in ((q, "q"), (kc, "kc"), (vc, "vc"), (bt, "bt"), (pos, "pos"), (out, "out")):
+            _check_cuda(t, n)
+        if kc.dim() != 4 or kc.size(3) not in (64, 128) or vc.shape != kc.shape:
+            raise RuntimeError("cache must be [pages, n_kv, P, 64|128]")
+        if bt.dtype != torch.int32 or pos.dtype != torch.int32:
+            raise RuntimeError("bt and pos must be int32")
+        for t, n in ((q, "q"), (kc, "kc"), (vc, "vc"), (out, "out")):
+            _check_dtype(t, torch.float16, n)
+        D = kc.size(3)
+        n_q, n_kv, P = q.numel() // D, kc.size(1), kc.size(2)
+        if n_q * D != q.numel() or out.numel() != n_q * D:
+            raise RuntimeError("paged_attention_noalloc: q and out must hold n_q * head_dim values")
+        with torch.cuda.device(q.device):      # the scratch address is resolved on the current device
+            self._call(self.lib.dk_paged_attention_noalloc, int(version), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                       bt.data_ptr(), pos.data_ptr(), n_q, n_kv, D, P, kc.size(0), bt.numel(), int(part_size),
+                       int(max_splits), out.data_ptr(), _stream(q))
+
+    def paged_attention_noalloc_bytes(self, n_q, head_dim, max_splits):
+        return int(self.lib.dk_paged_attention_noalloc_bytes(int(n_q), int(head_dim), int(max_splits)))
 
     # rope_append (kernels/bindings.cpp:81-88) + paged_attention (kernels/bindings.cpp:45-62) fused into one launch
     def attention_decode(self, qkv, cos_t, sin_t, pos, bt, kc, vc, n_q, n_kv, part_size, o_part, m_part, l_part,
