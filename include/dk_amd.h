@@ -173,8 +173,8 @@ int dk_bw_read(const void* buf, size_t bytes, void* sink, int blocks, int thread
 
 /*
  * Paged split-K GQA decode attention for one query token at ctx = *pos + 1 (device int32). version 1-3: the block
- * kernel (the reference's three kernel versions share one MI355X kernel); version 4: the MFMA kernel, version 5: the
- * lean MFMA kernel (see dk_attention_decode's impl 2 and 3).
+ * kernel (the reference's three kernel versions share one MI355X kernel); version 5: the lean MFMA kernel (see
+ * dk_attention_decode's impl 3); version 4 (an earlier MFMA kernel) is no longer accepted.
  * Replaces paged_attention (kernels/bindings.cpp:45-62) -> paged_attention_launch (kernels/paged_attention.cu:429-461).
  * Grid = n_kv x max_splits workgroups; split s covers tokens [s*part_size, (s+1)*part_size) of the live context;
  * splits past ceil(ctx/part_size) exit; with one live split the output is written directly, otherwise each split
@@ -217,9 +217,9 @@ size_t dk_paged_attention_noalloc_bytes(int n_q, int head_dim, int max_splits);
  * not written back). k (rotated) and v of position *pos are written into page bt[pos / page], slot pos % page exactly
  * as dk_rope_append writes them, and the attention over ctx = *pos + 1 tokens uses them. Split partials go to
  * o_part / m_part / l_part and a combine kernel merges them, as for dk_paged_attention. impl selects the split
- * kernel: 0 or 1 = the block kernel (v_dot2 scores, LDS p.V), 2 = the MFMA kernel (16 x 16 f16 tiles; needs
- * ((part_size - 1) >> log2(page)) + 2 <= 1024), 3 = the lean MFMA kernel (scalar page lookups, one memory round trip
- * for K / V; needs page >= 16 and a part_size that is a multiple of 16 up to 512, 256 at head_dim 128).
+ * kernel: 0 or 1 = the block kernel (v_dot2 scores, LDS p.V), 3 = the lean MFMA kernel (16 x 16 f16 tiles, scalar
+ * page lookups, one memory round trip for K / V; needs page >= 16 and a part_size that is a multiple of 16 up to 512,
+ * 256 at head_dim 128).
  * The runtime picks impl and part_size per context from its measured policy table. If *pos is outside [0, max_pos)
  * nothing is touched. Other arguments and limits as dk_rope_append / dk_paged_attention.
  */

@@ -274,10 +274,8 @@ int check_paged_attention(int version, const void* q, const void* kc, const void
     return fail(DK_ERR_SHAPE, "heads-per-group must be 1/2/4/8, got %d", hpg);
   if (!pow2(page)) return fail(DK_ERR_DOMAIN, "page size must be a power of two, got %d", page);
   if (part_size <= 0) return fail(DK_ERR_DOMAIN, "part_size must be > 0");
-  if (version < 1 || version > 5) return fail(DK_ERR_DOMAIN, "attention version must be 1, 2, 3, 4 or 5");
-  if (version == 4 && !dk::attn_mfma_fits(part_size, ilog2(page)))
-    return fail(DK_ERR_DOMAIN, "paged_attention: version 4 stages at most %d block-table pages per split "
-                "(part_size %d, page %d)", dk::kAttnMaxSplitPages, part_size, page);
+  if (version < 1 || version > 5 || version == 4)
+    return fail(DK_ERR_DOMAIN, "attention version must be 1, 2, 3 or 5, got %d", version);
   if (version == 5 && !dk::attn_lean_fits(part_size, ilog2(page), head_dim))
     return fail(DK_ERR_DOMAIN, "paged_attention: version 5 needs pages of >= 16 tokens and a part_size that is a "
                 "multiple of 16 up to %d (part_size %d, page %d)", dk::attn_lean_max_part(head_dim), part_size, page);
@@ -296,7 +294,7 @@ void launch_reference_attention(int version, const void* q, const void* kc, cons
                                 void* out, void* stream) {
   const dk::AttnLaunch a{q, nullptr, nullptr, 0, pos, bt, n_bt, const_cast<void*>(kc), const_cast<void*>(vc), n_pages,
                          ilog2(page), n_q, n_kv, head_dim, part_size, max_splits, o_part, m_part, l_part, out,
-                         version == 5 ? 3 : version == 4 ? 2 : 1};
+                         version == 5 ? 3 : 1};
   dk::launch_paged_attention(a, (hipStream_t)stream);
 }
 
@@ -387,7 +385,8 @@ int dk_attention_decode(const void* qkv, const float* cos_t, const float* sin_t,
                         float* l_part, void* out, void* stream) {
   if (!qkv || !cos_t || !sin_t || !pos || !bt || !kc || !vc || !o_part || !m_part || !l_part || !out)
     return fail(DK_ERR_NULL, "attention_decode: null pointer argument");
-  if (impl < 0 || impl > 3) return fail(DK_ERR_DOMAIN, "attention_decode: impl must be 0, 1, 2 or 3, got %d", impl);
+  if (impl < 0 || impl > 3 || impl == 2)
+    return fail(DK_ERR_DOMAIN, "attention_decode: impl must be 0, 1 or 3, got %d", impl);
   if (head_dim != 64 && head_dim != 128)
     return fail(DK_ERR_SHAPE, "attention_decode: head_dim must be 64 or 128, got %d", head_dim);
   if (n_q <= 0 || n_kv <= 0 || n_q % n_kv != 0)
@@ -406,9 +405,6 @@ int dk_attention_decode(const void* qkv, const float* cos_t, const float* sin_t,
     return fail(DK_ERR_ALIGN, "qkv, kc and vc must be 16B aligned");
   if (!aligned16(o_part)) return fail(DK_ERR_ALIGN, "o_part must be 16B aligned");
   clear_error();
-  if (impl == 2 && !dk::attn_mfma_fits(part_size, ilog2(page)))
-    return fail(DK_ERR_DOMAIN, "attention_decode: impl 2 stages at most %d block-table pages per split "
-                "(part_size %d, page %d)", dk::kAttnMaxSplitPages, part_size, page);
   if (impl == 3 && !dk::attn_lean_fits(part_size, ilog2(page), head_dim))
     return fail(DK_ERR_DOMAIN, "attention_decode: impl 3 needs pages of >= 16 tokens and a part_size that is a "
                 "multiple of 16 up to %d (part_size %d, page %d)", dk::attn_lean_max_part(head_dim), part_size, page);

@@ -75,12 +75,8 @@ struct AttnLaunch {
   float* m_part;
   float* l_part;
   void* out;
-  int impl;            // 0 or 1 = block kernel; 2 = MFMA kernel; 3 = lean MFMA kernel
+  int impl;            // 0 or 1 = block kernel; 3 = lean MFMA kernel
 };
-// The MFMA attention kernel stages a split's block-table pages in LDS: ((part_size - 1) >> log2P) + 2 of them at most.
-constexpr int kAttnMaxSplitPages = 1024;
-inline bool attn_mfma_fits(int part_size, int log2P) { return ((part_size - 1) >> log2P) + 2 <= kAttnMaxSplitPages; }
-inline bool attn_use_mfma(const AttnLaunch& a) { return a.impl == 2 && attn_mfma_fits(a.part_size, a.log2P); }
 // The lean MFMA kernel: pages of at least 16 tokens, splits of whole 16-token tiles, at most 8 waves x 4 tiles (x 2
 // tiles at head_dim 128, whose RoPE variant would not fit 4 tiles in registers).
 inline int attn_lean_max_part(int head_dim) { return head_dim == 128 ? 256 : 512; }

@@ -372,8 +372,8 @@ attn_combine_kernel(const float* __restrict__ o_part, const float* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// MFMA formulation (impl 2) of the same split workgroup: the HPG query heads of a kv head are the columns of 16 x 16
-// matrix tiles, 16 tokens are the rows.
+// MFMA formulation of the split workgroup (the arithmetic of the lean kernel below): the HPG query heads of a kv head
+// are the columns of 16 x 16 matrix tiles, 16 tokens are the rows.
 //   QK^T: S[token][head] = K_tile (16 tokens x D) . Q^T (D x 16 heads) with v_mfma_f32_16x16x16_f16 (fp16 products are
 //         exact, fp32 sums), D / 16 steps. Lane l = 16 g + c of a wave feeds K row c (its token) and q head c, both
 //         over dims [D/4 g, D/4 (g+1)): any bijection of the reduction index is valid as long as both operands use it,
@@ -383,13 +383,9 @@ attn_combine_kernel(const float* __restrict__ o_part, const float* __restrict__ 
 //         as p_hi = fp16(p) plus p_lo = fp16(p - p_hi) in two MFMAs (about 22 significant bits, products with the fp16
 //         V exact, fp32 accumulation), so the result keeps the fp32 quality of the reference's softmax. Output column c
 //         of dim tile t holds dim (D/16) c + t, so each lane's V operand is D/16 contiguous dims of 4 token rows.
-// The workgroup's 8 waves split the tokens: per round each wave loads K and V of NB 16-token tiles at once (one
-// memory round trip per round; the split's block-table pages are staged in LDS first, so no page lookup sits in the
-// wave's in-order load queue), runs the online softmax once per round per head, then the waves merge their (m, l, O)
-// through LDS with the log-sum-exp rule. Output, partials and the RoPE / append behaviour are those of the block
-// kernel above.
+// An earlier kernel of this shape (8 waves, the split's block-table pages staged in LDS) was never chosen by the
+// attention tuner over the lean kernel or the block kernel and was removed.
 constexpr int kMfmaWaves = 8;
-constexpr int kMfmaThreads = kMfmaWaves * kWave;
 
 template <int D>
 struct MfmaAttnShape {
@@ -401,288 +397,9 @@ struct MfmaAttnShape {
   static constexpr int RT = kMfmaWaves * NB;    // tiles per round
 };
 
-template <int D, int HPG, bool ROPE>
-__global__ void __launch_bounds__(kMfmaThreads)
-attn_mfma_kernel(const f16* __restrict__ qsrc, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-                 int max_pos, const int32_t* __restrict__ pos_ptr, const int32_t* __restrict__ bt, int n_bt,
-                 f16* __restrict__ kc, f16* __restrict__ vc, int n_pages, int log2P, int n_q, int n_kv, int PS,
-                 int max_splits, float scale, float* __restrict__ o_part, float* __restrict__ m_part,
-                 float* __restrict__ l_part, f16* __restrict__ out) {
-  using S = MfmaAttnShape<D>;
-  constexpr int KD = S::KD, KW = S::KW, QS = S::QS, VD = S::VD, NB = S::NB, CPL = D / 8;
-  __shared__ int s_pg[kAttnMaxSplitPages];
-  __shared__ float s_m[kMfmaWaves][HPG], s_l[kMfmaWaves][HPG];
-  __shared__ float s_o[kMfmaWaves][HPG][D];
-
-  const int kvh = blockIdx.x, split = blockIdx.y;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int col = lane & 15, g = lane >> 4;
-  const int P = 1 << log2P;
-  const long long t0l = (long long)split * PS;
-  const bool reachable = t0l < ((long long)n_bt << log2P);
-  const int t0 = reachable ? (int)t0l : 0;
-  // block-table pages of the split's token range, staged in LDS (independent of pos, so issued first)
-  const int lp0 = t0 >> log2P;
-  const int npg = reachable ? (int)(min((long long)n_bt, ((t0l + PS - 1) >> log2P) + 1) - lp0) : 0;
-  for (int i = tid; i < npg; i += kMfmaThreads) s_pg[i] = bt[lp0 + i];
-
-  // q operand: head col of this kv head's group (zero for col >= HPG), dims [KD g, KD g + KD)
-  const bool qlive = col < HPG;
-  const f16* qh = qsrc + (size_t)(kvh * HPG + (qlive ? col : 0)) * D;
-  u32x4 qr[KW], knew[KW];
-  VRow<VD> vnew{};
-#pragma unroll
-  for (int w = 0; w < KW; ++w) {
-    qr[w] = qlive ? *reinterpret_cast<const u32x4*>(qh + KD * g + 8 * w) : u32x4{0u, 0u, 0u, 0u};
-    knew[w] = u32x4{0u, 0u, 0u, 0u};
-  }
-  u32x4 qp[KW], ko[KW], kp[KW];
-  if constexpr (ROPE) {
-    const f16* kh = qsrc + (size_t)(n_q + kvh) * D;
-    const f16* vh = qsrc + (size_t)(n_q + n_kv + kvh) * D;
-#pragma unroll
-    for (int w = 0; w < KW; ++w) {
-      const int c = KW * g + w, pc = (c + CPL / 2) % CPL;
-      qp[w] = qlive ? *reinterpret_cast<const u32x4*>(qh + 8 * pc) : u32x4{0u, 0u, 0u, 0u};
-      ko[w] = *reinterpret_cast<const u32x4*>(kh + 8 * c);
-      kp[w] = *reinterpret_cast<const u32x4*>(kh + 8 * pc);
-    }
-#pragma unroll
-    for (int i = 0; i < VD / 2; ++i) vnew.w[i] = reinterpret_cast<const uint32_t*>(vh + VD * col)[i];
-  }
-  __syncthreads();  // s_pg
-
-  // Page of token t if t lies in [t0, tend) and its page is in the cache, else -1. Branch-free (the LDS reads of a
-  // tile batch behind one wait): out-of-range tokens read entry 0 and are discarded by the select.
-  auto page_at = [&](int t, int tend) -> int {
-    const bool in = t >= t0 && t < tend;
-    const int pg = s_pg[in ? (t >> log2P) - lp0 : 0];
-    return (in && pg >= 0 && pg < n_pages) ? pg : -1;
-  };
-  auto row_off = [&](int pg, int t) -> size_t {
-    return ((((size_t)(pg < 0 ? 0 : pg) * n_kv + kvh) << log2P) + (t & (P - 1))) * D;
-  };
-  // K / V of the round starting at tile r0, tokens in [t0, tend): K row col and V rows 4 g + v of NB tiles. A tile
-  // wholly outside [t0, tend) is skipped by a wave-uniform branch; inside a tile every lane loads (a token without a
-  // page reads a row of page 0) and the value is zeroed by select, so there is no per-load branch. vmask collects
-  // per tile bit 0 = K row col has a page, bit 1 + v = V row 4 g + v has a page (for the masks once *pos is known).
-  u32x4 kr[NB][KW];
-  VRow<VD> vr[NB][4];
-  uint32_t vmask = 0;
-  auto load_round = [&](int r0, int tend) {
-    vmask = 0;
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const int ts = (r0 + b * kMfmaWaves + wave) << 4;
-      if (ts >= tend || ts + 16 <= t0) {  // uniform per wave
-#pragma unroll
-        for (int w = 0; w < KW; ++w) kr[b][w] = u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-#pragma unroll
-          for (int i = 0; i < VD / 2; ++i) vr[b][v].w[i] = 0u;
-        }
-        continue;
-      }
-      const int tk = ts + col;
-      const int pk = page_at(tk, tend);
-      int pv[4];
-#pragma unroll
-      for (int v = 0; v < 4; ++v) pv[v] = page_at(ts + 4 * g + v, tend);
-#pragma unroll
-      for (int w = 0; w < KW; ++w)
-        kr[b][w] = load_stream(reinterpret_cast<const u32x4*>(kc + row_off(pk, tk) + KD * g + 8 * w));
-#pragma unroll
-      for (int v = 0; v < 4; ++v) vr[b][v] = load_vrow<VD>(vc + row_off(pv[v], ts + 4 * g + v) + VD * col);
-      uint32_t mb = pk >= 0 ? 1u : 0u;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) mb |= pv[v] >= 0 ? (2u << v) : 0u;
-      vmask |= mb << (5 * b);
-    }
-  };
-  // The first round's K / V go out before anything that needs *pos (the RoPE tables, the context bound), over the
-  // whole split range: tokens past the context are masked below (score -inf by select, V row zeroed by select), so
-  // the speculative loads never reach the result. Only valid cache pages are read.
-  const int k0 = t0 >> 4;  // 16-token tiles, aligned to multiples of 16
-  if (reachable) load_round(k0, (int)min(t0l + PS, (long long)n_bt << log2P));
-
-  const int pos = *pos_ptr;
-  if constexpr (ROPE) {
-    if (pos < 0 || pos >= max_pos) return;  // uniform: nothing is touched
-#pragma unroll
-    for (int w = 0; w < KW; ++w) {
-      const int c = KW * g + w;
-      const int ti = (8 * c) % (D / 2);
-      float cs[8], sn[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        cs[e] = cos_t[(size_t)pos * (D / 2) + ti + e];
-        sn[e] = sin_t[(size_t)pos * (D / 2) + ti + e];
-      }
-      qr[w] = rope_slice<D>(qr[w], qp[w], cs, sn, c < CPL / 2);
-      knew[w] = rope_slice<D>(ko[w], kp[w], cs, sn, c < CPL / 2);
-    }
-  }
-  const int ctx = attn_context(pos_ptr, n_bt, log2P);
-  const int nsplit = attn_splits(ctx, PS, max_splits);
-  if (ROPE) {
-    // the workgroup owning token pos (or the last live split when the cap is below pos) appends k, v
-    const int owner = min(pos / PS, nsplit - 1);
-    if (split == owner && wave == 0) {
-      const int lp = pos >> log2P;
-      const int page = lp < n_bt ? bt[lp] : -1;
-      if (page >= 0 && page < n_pages) {
-        const size_t row = ((((size_t)page * n_kv + kvh) << log2P) + (pos & (P - 1))) * D;
-        if (col == 0) {
-#pragma unroll
-          for (int w = 0; w < KW; ++w) *reinterpret_cast<u32x4*>(kc + row + KD * g + 8 * w) = knew[w];
-        }
-        if (g == 0) {
-#pragma unroll
-          for (int i = 0; i < VD / 2; ++i) reinterpret_cast<uint32_t*>(vc + row + VD * col)[i] = vnew.w[i];
-        }
-      }
-    }
-  }
-  if (split >= nsplit || !reachable) return;  // uniform per workgroup
-  const int t1 = (int)min((long long)ctx, t0l + PS);
-
-  float m = -INFINITY, l = 0.f;  // running max / sum of head col
-  f4 acc[VD];
-#pragma unroll
-  for (int t = 0; t < VD; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
-  const int k1 = (t1 + 15) >> 4;
-  const bool pos_here = ROPE && pos >= t0 && pos < t1;  // this split attends token pos (its slot has a page)
-  for (int r0 = k0; r0 < k1; r0 += S::RT) {
-    if (r0 != k0) load_round(r0, t1);
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const int ts = (r0 + b * kMfmaWaves + wave) << 4;
-      const uint32_t mb = vmask >> (5 * b);
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const bool keep = ((mb >> (1 + v)) & 1u) && ts + 4 * g + v < t1;  // past the context or no page: zero row
-#pragma unroll
-        for (int i = 0; i < VD / 2; ++i) vr[b][v].w[i] = keep ? vr[b][v].w[i] : 0u;
-      }
-      if constexpr (ROPE) {  // the slot of pos is being written by this launch: use the fresh k, v
-        if (pos_here && ts + col == pos && (mb & 1u)) {
-#pragma unroll
-          for (int w = 0; w < KW; ++w) kr[b][w] = knew[w];
-        }
-#pragma unroll
-        for (int v = 0; v < 4; ++v)
-          if (pos_here && ts + 4 * g + v == pos && ((mb >> (1 + v)) & 1u)) vr[b][v] = vnew;
-      }
-    }
-    // ---- scores of the round: sc[b][v] = score of token ts_b + 4 g + v for head col
-    f4 sc[NB];
-    float rmax = -INFINITY;
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      f4 c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int q = 0; q < QS; ++q) {
-        const int i0 = 2 * q, i1 = 2 * q + 1;
-        c = mfma16(as_h4(kr[b][i0 >> 2][i0 & 3], kr[b][i1 >> 2][i1 & 3]),
-                   as_h4(qr[i0 >> 2][i0 & 3], qr[i1 >> 2][i1 & 3]), c);
-      }
-      const int ts = (r0 + b * kMfmaWaves + wave) << 4;
-      const uint32_t mb = vmask >> (5 * b);
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const bool live = ((mb >> (1 + v)) & 1u) && ts + 4 * g + v < t1;
-        sc[b][v] = live ? c[v] * scale : -INFINITY;
-        rmax = fmaxf(rmax, sc[b][v]);
-      }
-    }
-    // ---- online softmax, once per round
-    rmax = rows_max(rmax);
-    const float mn = fmaxf(m, rmax);
-    const float alpha = (m == -INFINITY) ? 0.f : __expf(m - mn);
-    float ps = 0.f;
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const float pv = (sc[b][v] == -INFINITY) ? 0.f : __expf(sc[b][v] - mn);
-        sc[b][v] = pv;
-        ps += pv;
-      }
-    }
-    l = alpha * l + rows_sum(ps);
-    m = mn;
-    // the accumulator's rows are heads 4 g + v: their rescale factors live in lanes 4 g + v
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const float av = __shfl(alpha, 4 * g + v, kWave);
-#pragma unroll
-      for (int t = 0; t < VD; ++t) acc[t][v] *= av;
-    }
-    // ---- P . V: p as fp16 hi + lo parts
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      h4 phi, plo;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        phi[v] = (f16)sc[b][v];
-        plo[v] = (f16)(sc[b][v] - (float)phi[v]);
-      }
-#pragma unroll
-      for (int t = 0; t < VD; ++t) {
-        // B operand of dim tile t: dim VD col + t of tokens 4 g + 0..3
-        const int wi = t >> 1;
-        const uint32_t sel = (t & 1) ? 0x07060302u : 0x05040100u;
-        const uint32_t lo = __builtin_amdgcn_perm(vr[b][1].w[wi], vr[b][0].w[wi], sel);
-        const uint32_t hi = __builtin_amdgcn_perm(vr[b][3].w[wi], vr[b][2].w[wi], sel);
-        const h4 vb = as_h4(lo, hi);
-        acc[t] = mfma16(phi, vb, acc[t]);
-        acc[t] = mfma16(plo, vb, acc[t]);
-      }
-    }
-  }
-  // ---- merge the waves: (m, l) of head col in lanes col < HPG of row 0, O rows = heads 4 g + v
-  if (g == 0 && col < HPG) {
-    s_m[wave][col] = m;
-    s_l[wave][col] = l;
-  }
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int hh = 4 * g + v;
-    if (hh < HPG) {
-#pragma unroll
-      for (int t = 0; t < VD; ++t) s_o[wave][hh][VD * col + t] = acc[t][v];
-    }
-  }
-  __syncthreads();
-  for (int o = tid; o < HPG * D; o += kMfmaThreads) {
-    const int hh = o / D, d = o % D;
-    float Mx = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kMfmaWaves; ++w) Mx = fmaxf(Mx, s_m[w][hh]);
-    float L = 0.f, O = 0.f;
-#pragma unroll
-    for (int w = 0; w < kMfmaWaves; ++w) {
-      const float ww = (s_m[w][hh] == -INFINITY) ? 0.f : __expf(s_m[w][hh] - Mx);
-      L = fmaf(ww, s_l[w][hh], L);
-      O = fmaf(ww, s_o[w][hh][d], O);
-    }
-    const int head = kvh * HPG + hh;
-    if (nsplit == 1) {
-      out[(size_t)head * D + d] = (f16)(O * (L > 0.f ? 1.0f / L : 0.f));
-    } else {
-      o_part[((size_t)head * max_splits + split) * D + d] = O;
-      if (d == 0) {
-        m_part[(size_t)head * max_splits + split] = Mx;
-        l_part[(size_t)head * max_splits + split] = L;
-      }
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------------------------------------------
-// Lean MFMA split kernel (impl 3) for pages of at least 16 tokens: the arithmetic of the MFMA kernel above (16 x 16
-// f16 tiles, p as fp16 hi + lo parts) with a schedule cut down to two dependent memory round trips:
+// Lean MFMA split kernel (impl 3) for pages of at least 16 tokens: the MFMA arithmetic above (16 x 16 f16 tiles, p as
+// fp16 hi + lo parts) with a schedule cut down to two dependent memory round trips:
 //   * every kernel argument is read into scalar registers at entry (left to itself the compiler loads some of them
 //     only where they are first used, and each such late load is one more round trip on the critical path);
 //   * each wave owns NT 16-token tiles of the split (tile j = wave + NW i); a tile lies in one page, so its page is a
@@ -988,17 +705,6 @@ void launch_attn(const AttnLaunch& a, hipStream_t st) {
   const float scale = 1.0f / sqrtf((float)D);
   if (attn_use_lean(a)) {
     launch_lean_any<D, HPG, ROPE>(a, st);
-    if (a.max_splits > 1)
-      hipLaunchKernelGGL((attn_combine_kernel<D>), dim3(a.n_q), dim3(kAttnThreads), 0, st, a.o_part, a.m_part,
-                         a.l_part, a.pos, ROPE ? a.max_pos : 0, a.n_bt, a.log2P, a.part_size, a.max_splits,
-                         (f16*)a.out);
-    return;
-  }
-  if (attn_use_mfma(a)) {
-    hipLaunchKernelGGL((attn_mfma_kernel<D, HPG, ROPE>), dim3(a.n_kv, a.max_splits), dim3(kMfmaThreads), 0, st,
-                       (const f16*)a.q, a.cos_t, a.sin_t, a.max_pos, a.pos, a.bt, a.n_bt, (f16*)a.kc, (f16*)a.vc,
-                       a.n_pages, a.log2P, a.n_q, a.n_kv, a.part_size, a.max_splits, scale, a.o_part, a.m_part,
-                       a.l_part, (f16*)a.out);
     if (a.max_splits > 1)
       hipLaunchKernelGGL((attn_combine_kernel<D>), dim3(a.n_q), dim3(kAttnThreads), 0, st, a.o_part, a.m_part,
                          a.l_part, a.pos, ROPE ? a.max_pos : 0, a.n_bt, a.log2P, a.part_size, a.max_splits,

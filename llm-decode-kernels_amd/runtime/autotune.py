@@ -258,7 +258,7 @@ def tune_attention(dims=(64, 128), contexts=ATTN_CONTEXTS, path=ATTN_PATH, log=p
     from .model import DecodeConfig, Model
     old = json.load(open(path)) if pathlib.Path(path).exists() else {}
     out = {"version": old.get("version", 3),
-           "note": "part_size (tokens per split) and impl (1 block kernel, 2 MFMA kernel, 3 lean MFMA kernel) by the "
+           "note": "part_size (tokens per split) and impl (1 block kernel, 3 lean MFMA kernel) by the "
                    "largest tuned context "
                    "<= the prepared cap; chosen by the decode step time of the TinyLlama (head_dim 64) and Llama-3-8B "
                    "(head_dim 128) shapes on MI355X (runtime.autotune.tune_attention). 'policy' is head_dim 64, "
@@ -273,7 +273,6 @@ def tune_attention(dims=(64, 128), contexts=ATTN_CONTEXTS, path=ATTN_PATH, log=p
         lean_max = 256 if D == 128 else 512
         for ctx in contexts:
             cands = [(1, ps) for ps in (32, 64, 128)]  # the block kernel costs about 3 us per extra 64-token block
-            cands += [(2, ps) for ps in (32, 64, 128, 256, 512)]
             cands += [(3, ps) for ps in (16, 32, 64, 128, 256, 512) if ps <= lean_max]
             times = {}
             for impl, ps in cands:

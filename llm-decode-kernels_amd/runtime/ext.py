@@ -335,8 +335,8 @@ class DecodeKernels:
             raise RuntimeError("heads-per-group must be 1/2/4/8")
         if part_size <= 0:
             raise RuntimeError("part_size must be > 0")
-        if not 1 <= version <= 5:
-            raise RuntimeError("attention version must be 1, 2, 3, 4 or 5")
+        if version not in (1, 2, 3, 5):
+            raise RuntimeError("attention version must be 1, 2, 3 or 5")
         max_splits = o_part.size(1)
         if not (o_part.size(0) == n_q and o_part.size(2) == D and m_part.size(0) == n_q and l_part.size(0) == n_q
                 and m_part.size(1) == max_splits and l_part.size(1) == max_splits and out.numel() == n_q * D):

@@ -240,8 +240,8 @@ class Model:
         ps = part_size or self.cfg.part_size or ent.get("part_size", 64)
         impl = impl or self.cfg.attn_impl or ent.get("impl", 1)
         log2p = self.cfg.page.bit_length() - 1
-        if impl == 2 and ((ps - 1) >> log2p) + 2 > 1024:
-            impl = 1                                # the MFMA kernel stages at most 1024 pages per split
+        if impl == 2:
+            impl = 1                                # tables written before the MFMA kernel's removal
         lean_max = 256 if self.D == 128 else 512
         if impl == 3 and (self.cfg.page < 16 or ps % 16 or ps > lean_max):
             impl = 1                                # the lean kernel takes whole 16-token tiles of one page
@@ -410,7 +410,7 @@ class Model:
     def attention(self, li):
         kc, vc = self.kv[li, 0], self.kv[li, 1]
         if self.rope_epilogue:  # q rotated and k, v appended by the qkv GEMV
-            version = {3: 5, 2: 4}.get(self.attn_impl, 2)
+            version = 5 if self.attn_impl == 3 else 2
             self.K.paged_attention(self.qkv[: self.n_q * self.D], kc, vc, self.bt, self.pos, self.part_size,
                                    self.o_part, self.m_part, self.l_part, self.attn, version)
             return

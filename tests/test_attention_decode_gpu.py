@@ -20,8 +20,8 @@ def K():
     return ext.load()
 
 
-MODES = ("block", "mfma", "lean")   # impl 1, impl 2, impl 3
-IMPL = {"block": 1, "mfma": 2, "lean": 3}
+MODES = ("block", "lean")   # impl 1, impl 3
+IMPL = {"block": 1, "lean": 3}
 
 
 def lean_fits(PS, page, D):

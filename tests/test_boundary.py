@@ -89,9 +89,9 @@ def _attn(lib, **kw):
     (dict(head_dim=96), 3, "head_dim"),
     (dict(page=12), 4, "page size must be a power of two"),
     (dict(part_size=0), 4, "part_size must be > 0"),
-    (dict(version=6), 4, "version must be 1, 2, 3, 4 or 5"),
-    (dict(version=0), 4, "version must be 1, 2, 3, 4 or 5"),
-    (dict(version=4, part_size=32768), 4, "block-table pages per split"),
+    (dict(version=6), 4, "version must be 1, 2, 3 or 5"),
+    (dict(version=0), 4, "version must be 1, 2, 3 or 5"),
+    (dict(version=4), 4, "version must be 1, 2, 3 or 5"),
     (dict(version=5, part_size=40), 4, "version 5 needs pages of >= 16 tokens"),
     (dict(version=5, part_size=1024), 4, "version 5 needs pages"),
     (dict(version=5, page=8), 4, "version 5 needs pages"),
@@ -119,11 +119,11 @@ def _dec(lib, **kw):
     (dict(page=12), 4, "page size must be a power of two"),
     (dict(part_size=0), 4, "part_size must be > 0"),
     (dict(max_splits=0), 3, "max_splits"),
-    (dict(impl=4), 4, "impl must be 0, 1, 2 or 3"),
+    (dict(impl=4), 4, "impl must be 0, 1 or 3"),
     (dict(impl=3, part_size=40), 4, "impl 3 needs pages of >= 16 tokens"),
     (dict(impl=3, page=8), 4, "impl 3 needs pages"),
     (dict(impl=3, D=128, part_size=512), 4, "multiple of 16 up to 256"),
-    (dict(impl=2, part_size=32768, page=16), 4, "block-table pages per split"),
+    (dict(impl=2), 4, "impl must be 0, 1 or 3"),
     (dict(max_pos=0), 3, "empty"),
     (dict(c=None), 1, "null"),
     (dict(qkv=A16 + 2), 2, "16B aligned"),

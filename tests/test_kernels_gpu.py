@@ -134,24 +134,14 @@ def close_or_rejected(out, ref, tol, what):
         assert_close(out, ref, tol, what)
 
 
-def mfma_fits(PS, page):
-    """version 4 / impl 2 stage a split's block-table pages in LDS (at most 1024 of them)."""
-    return ((PS - 1) >> (page.bit_length() - 1)) + 2 <= 1024
-
-
 def lean_fits(PS, page, D):
     """version 5 / impl 3: pages of >= 16 tokens, part sizes a multiple of 16 up to 512 (256 at head_dim 128)."""
     return page >= 16 and PS % 16 == 0 and PS <= (256 if D == 128 else 512)
 
 
 def run_attn(K, q, kc, vc, bt, ctx, PS, version=3, spare=0):
-    """spare > 0 sizes the split buffers for more splits than ctx needs, as the runtime does. A part size the MFMA
-    kernels (versions 4 and 5) cannot take must be rejected: then the call is checked to raise and None is
-    returned."""
-    if version == 4 and not mfma_fits(PS, kc.shape[2]):
-        with pytest.raises(RuntimeError, match="block-table pages per split"):
-            _run_attn(K, q, kc, vc, bt, ctx, PS, version, spare)
-        return None
+    """spare > 0 sizes the split buffers for more splits than ctx needs, as the runtime does. A part size the lean
+    MFMA kernel (version 5) cannot take must be rejected: then the call is checked to raise and None is returned."""
     if version == 5 and not lean_fits(PS, kc.shape[2], kc.shape[3]):
         with pytest.raises(RuntimeError, match="version 5 needs pages"):
             _run_attn(K, q, kc, vc, bt, ctx, PS, version, spare)
@@ -180,13 +170,13 @@ def test_attention_ctx128(K, n_q, n_kv, page):
     k, v = R.gather_kv(kc, vc, bt, 128, page)
     ref = R.attention_contiguous_ref(q, k, v)
     for PS in (4096, 64, 32, 48, 16):
-        for ver in (1, 2, 3, 4, 5):
+        for ver in (1, 2, 3, 5):
             close_or_rejected(run_attn(K, q, kc, vc, bt, 128, PS, ver), ref, 2e-3,
                          f"ctx128 {n_q}/{n_kv} P{page} PS{PS} v{ver}")
 
 
 @pytest.mark.parametrize("ctx", (1, 2, 17, 63, 65, 129, 1000))
-@pytest.mark.parametrize("ver", (3, 4, 5))
+@pytest.mark.parametrize("ver", (3, 5))
 def test_attention_odd_ctx(K, ver, ctx):
     kc, vc, bt = make_cache(ctx, 4, 16, seed=ctx)
     q = torch.randn(32, 64, generator=gen(ctx + 1)).half()
@@ -197,7 +187,7 @@ def test_attention_odd_ctx(K, ver, ctx):
 
 @pytest.mark.parametrize("ctx", (512, 1024, 2048, 4096, 8192, 16384))
 @pytest.mark.parametrize("peaky", (1.0, 6.0))
-@pytest.mark.parametrize("ver", (3, 4, 5))
+@pytest.mark.parametrize("ver", (3, 5))
 def test_attention_real_ctx(K, ver, ctx, peaky):
     kc, vc, bt = make_cache(ctx, 4, 16, peaky=peaky, seed=ctx)
     q = torch.randn(32, 64, generator=gen(ctx + 2)).half()
@@ -207,7 +197,7 @@ def test_attention_real_ctx(K, ver, ctx, peaky):
 
 
 @pytest.mark.parametrize("ctx", (1, 40, 64, 100, 700, 2048, 5000))
-@pytest.mark.parametrize("ver", (3, 4, 5))
+@pytest.mark.parametrize("ver", (3, 5))
 def test_attention_runtime_spare_splits(K, ver, ctx):
     kc, vc, bt = make_cache(ctx, 4, 16, peaky=6.0, seed=ctx + 3)
     q = torch.randn(32, 64, generator=gen(ctx + 4)).half()
@@ -218,7 +208,7 @@ def test_attention_runtime_spare_splits(K, ver, ctx):
 
 @pytest.mark.parametrize("n_q,n_kv", [(32, 8), (8, 8), (16, 8), (64, 8)])
 @pytest.mark.parametrize("ctx", (1, 100, 777, 4096))
-@pytest.mark.parametrize("ver", (3, 4, 5))
+@pytest.mark.parametrize("ver", (3, 5))
 def test_attention_head_dim_128(K, ver, n_q, n_kv, ctx):
     kc, vc, bt = make_cache(ctx, n_kv, 16, D=128, peaky=2.0, seed=ctx + n_q)
     q = torch.randn(n_q, 128, generator=gen(ctx)).half()
@@ -227,7 +217,7 @@ def test_attention_head_dim_128(K, ver, n_q, n_kv, ctx):
         close_or_rejected(run_attn(K, q, kc, vc, bt, ctx, PS, ver), ref, 2e-3, f"D128 {n_q}/{n_kv} ctx{ctx} PS{PS} v{ver}")
 
 
-@pytest.mark.parametrize("ver", (3, 4, 5))
+@pytest.mark.parametrize("ver", (3, 5))
 def test_attention_ctx1_is_v0(K, ver):
     """Softmax over one token returns that token's V exactly (fp16 in, fp16 out)."""
     kc, vc, bt = make_cache(1, 4, 16, seed=9)
@@ -237,7 +227,7 @@ def test_attention_ctx1_is_v0(K, ver):
     assert torch.equal(out, v0.repeat_interleave(8, dim=0))
 
 
-@pytest.mark.parametrize("ver", (3, 4, 5))
+@pytest.mark.parametrize("ver", (3, 5))
 def test_attention_split_buffers_ignored_past_live(K, ver):
     """Splits beyond ceil(ctx/PS) must not touch the buffers (grid sized for the cap, surplus splits exit)."""
     ctx, PS, spare = 100, 32, 6
