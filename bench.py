@@ -27,7 +27,8 @@ Also measured in the same run (extra keys of the JSON line):
                 value) and at ctx 2048, on the same weights.
 
 --gpus N > 1 exits with a message: the path is single-GPU by design (one GPU per box here).
---leg gemv runs only the GEMV roofline leg (used under rocprofv3 for the kernel trace and counter passes); --leg
+--leg gemv runs only the GEMV roofline leg (used under rocprofv3 for the kernel trace and counter passes); --leg attn8b
+only the Llama-3-8B ctx-4096 attention and bw_read of its K/V bytes (the same, for the attention kernels); --leg
 decode / prefill / decode8b / kernels run one leg alone (the decode and prefill legs without the standalone GEMV and
 kernel legs, so that their traces hold only the model's kernels).
 """
@@ -313,6 +314,62 @@ def kernels_leg(Kx, n=64, reps=5):
     return out
 
 
+def attn8b_leg(Kx, ctx=4096, reps=5, eager=8):
+    """Decode attention of BASELINE config 5 alone: Llama-3-8B heads (32 q / 8 kv, D 128, page 16) at context ctx,
+    the reference op (split kernel + combine) with the runtime's policy entry for that context, each launch on a
+    different cold copy of the paged K/V (block table a seeded permutation), then bw_read over the same K/V bytes on
+    the split kernel's workgroup count and on the whole chip. Timed as hipGraphs of back-to-back launches; `eager`
+    extra launches of each run outside any graph first, for the counter passes (rocprofv3 --pmc over this leg)."""
+    import math
+    import torch
+    from runtime.model import DecodeConfig, Model
+    from runtime.timing import ColdCopies, graph_time, n_copies
+
+    dev = "cuda"
+    n_q, n_kv, D, P = 32, 8, 128, 16
+    cap = ctx + 48
+    ent = Model._policy_entry_of(json.load(open(DecodeConfig().attn_policy_path)), D, cap)
+    ps, impl = ent["part_size"], ent.get("impl", 1)
+    version = 5 if impl == 3 else 3
+    S = math.ceil(cap / ps)
+    pages = math.ceil(cap / P)
+    g = torch.Generator(device=dev).manual_seed(ctx)
+    kc = torch.randn(pages, n_kv, P, D, generator=g, device=dev).half()
+    vc = torch.randn(pages, n_kv, P, D, generator=g, device=dev).half()
+    kv = ColdCopies([kc, vc], n_copies(2 * kc.numel() * 2))
+    del kc, vc
+    bt = torch.randperm(pages, generator=g, device=dev).int()
+    q = torch.randn(n_q * D, generator=g, device=dev).half()
+    pos = torch.tensor([ctx - 1], dtype=torch.int32, device=dev)
+    f32 = dict(dtype=torch.float32, device=dev)
+    o_part, m_part, l_part = torch.empty(n_q, S, D, **f32), torch.empty(n_q, S, **f32), torch.empty(n_q, S, **f32)
+    o = torch.empty(n_q, D, dtype=torch.half, device=dev)
+    kv_bytes = 2 * ctx * n_kv * D * 2
+    nbytes = kv_bytes + 2 * n_q * D * 2 + 4 * math.ceil(ctx / P)
+    attn = lambda i: Kx.paged_attention(q, *kv[i], bt, pos, ps, o_part, m_part, l_part, o, version)
+    src = ColdCopies([torch.empty(kv_bytes, dtype=torch.uint8, device=dev)], n_copies(kv_bytes))
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    grids = {"split_workgroups": n_kv * S, "whole_chip": kv_bytes // 16 // 512}
+    reads = {k: (lambda i, b=b: Kx.bw_read(src[i][0], sink, b, 512, 4 if b * 512 * 4 * 16 <= kv_bytes else 1))
+             for k, b in grids.items()}
+    for i in range(eager):
+        attn(i)
+    for fn in reads.values():
+        for i in range(eager):
+            fn(i)
+    torch.cuda.synchronize()
+    t_attn = graph_time(attn, kv.copies, reps)[1]
+    res = {"ctx": ctx, "part_size": ps, "splits": S, "version": version, "bytes": nbytes,
+           "us": round(t_attn, 3), "gbps": round(nbytes / t_attn / 1e3, 1),
+           "frac": round(nbytes / t_attn / 1e3 / HBM_PEAK_GBS, 4), "bw_read": {}}
+    for k, fn in reads.items():
+        t = graph_time(fn, src.copies, reps)[1]
+        res["bw_read"][k] = {"blocks": grids[k], "threads": 512, "bytes": kv_bytes, "us": round(t, 3),
+                             "gbps": round(kv_bytes / t / 1e3, 1)}
+    del kv, src
+    return res
+
+
 def decode_leg(model, ctx, steps, warmup):
     import torch
     model.reset(ctx)
@@ -485,10 +542,12 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--ctx", type=int, default=512)
-    ap.add_argument("--leg", choices=("all", "gemv", "kernels", "decode", "decode8b", "prefill"), default="all",
+    ap.add_argument("--leg", choices=("all", "gemv", "kernels", "decode", "decode8b", "attn8b", "prefill"),
+                    default="all",
                     help="gemv: the 4096x14336 GEMV and its calibration copies only; decode: the TinyLlama decode "
-                         "step only; decode8b: the Llama-3-8B decode legs only; prefill: the TinyLlama prefill leg "
-                         "only; kernels: the attention and fused-op kernels of configs 2 and 3 only")
+                         "step only; decode8b: the Llama-3-8B decode legs only; attn8b: the Llama-3-8B ctx-4096 "
+                         "attention alone and bw_read of its K/V bytes; prefill: the TinyLlama prefill leg only; "
+                         "kernels: the attention and fused-op kernels of configs 2 and 3 only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline leg")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
     a = ap.parse_args()
@@ -526,6 +585,14 @@ def main():
 
     if a.leg == "decode8b":
         print(json.dumps({"leg": "decode8b", "decode_llama3_8b_ctx4096": decode_8b_leg()}), flush=True)
+        return
+
+    if a.leg == "attn8b":
+        r = attn8b_leg(Kx)
+        log(f"llama3-8b attention ctx {r['ctx']} (part {r['part_size']}, {r['splits']} splits): {r['us']:.3f} us -> "
+            f"{r['gbps']:.0f} GB/s; bw_read of the K/V bytes: " +
+            ", ".join(f"{k} {v['us']:.3f} us" for k, v in r["bw_read"].items()))
+        print(json.dumps({"leg": "attn8b", "attention_llama3_8b_ctx4096": r}), flush=True)
         return
 
     from runtime.model import DecodeConfig, Model

@@ -53,10 +53,11 @@ int dk_runtime_version(void);
  *          x is staged in LDS, so K <= 32768 (as the reference's gemv_rb<R,PF>, kernels/gemv_w4a16.cu:39-100).
  * stage 3: split-K: the workgroup's `warps` waves (1..16, 0 = one per 64 columns of 32 weights) share R rows,
  *          pf in {0,1} = one-step prefetch (for narrow N).
- * stage 4: row tiles: a workgroup of ceil(K / 2048) waves covers K once, one 32-weight column per lane with its
+ * stage 4: row tiles: a row group of ceil(K / 2048) waves covers K once, one 32-weight column per lane with its
  *          x slice in registers, and walks 2^pf tiles (pf in 0..3) of R rows (R in {1,2,4,8}), the next tile's loads
- *          in flight while the current one is computed. `warps` must be 0 or >= ceil(K / 2048) (the workgroup
- *          size is always ceil(K / 2048) waves); K <= 32768. The default when no tuning entry exists.
+ *          in flight while the current one is computed. `warps` = waves per workgroup: 0 (one row group) or a
+ *          multiple of ceil(K / 2048) up to 16 (warps / ceil(K / 2048) row groups of consecutive row runs per
+ *          workgroup); K <= 32768. The default when no tuning entry exists.
  * Requires K % 32 == 0, group a power of two >= 32 with K % group == 0, packed and x 16-byte aligned.
  */
 int dk_gemv_w4a16(int stage, int R, int warps, int pf, const void* packed, const void* sz, const void* x, void* y,
@@ -70,7 +71,7 @@ int dk_gemv_w4a16(int stage, int R, int warps, int pf, const void* packed, const
  *        table [*, K] and delta must be NULL: the decode step's embedding gather);
  *   y  = dequant(W) . (norm_w * fp16(float(xn) * rsqrt(mean(float(xn)^2) + eps)))
  *   x_out (if not NULL) receives xn; it must not alias x or delta (the residual stream is double-buffered).
- * Rounding points as dk_add_rmsnorm and dk_gemv_w4a16. stage must be 4; R and pf as for stage 4; K <= 32768.
+ * Rounding points as dk_add_rmsnorm and dk_gemv_w4a16. stage must be 4; R, warps and pf as for stage 4; K <= 32768.
  */
 int dk_gemv_w4a16_rmsnorm(int stage, int R, int warps, int pf, const void* packed, const void* sz, const void* x,
                           const int64_t* row, const void* delta, const void* norm_w, float eps, void* x_out, void* y,

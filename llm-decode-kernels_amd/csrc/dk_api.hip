@@ -52,6 +52,9 @@ int dk_runtime_version(void) {
   return v;
 }
 
+// Waves of one stage-4 row group: one 32-weight column per lane covers K.
+static int tile_waves(int K) { return (K / 32 + 63) / 64; }
+
 int dk_gemv_w4a16(int stage, int R, int warps, int pf, const void* packed, const void* sz, const void* x, void* y,
                   int N, int K, int group, void* stream) {
   if (!packed || !sz || !x || !y) return fail(DK_ERR_NULL, "gemv_w4a16: null pointer argument");
@@ -61,9 +64,9 @@ int dk_gemv_w4a16(int stage, int R, int warps, int pf, const void* packed, const
   if (stage == 3 ? (pf != 0 && pf != 1) : (pf < 0 || pf > 3))
     return fail(DK_ERR_DOMAIN, "gemv_w4a16: pf must be %s for stage %d, got %d", stage == 3 ? "0 or 1" : "0..3",
                 stage, pf);
-  if (stage == 4 && K > 0 && warps != 0 && warps * 2048 < K)
-    return fail(DK_ERR_SHAPE, "gemv_w4a16: stage 4 needs warps * 2048 >= K (one column per lane), got warps=%d K=%d",
-                warps, K);
+  if (stage == 4 && K > 0 && warps != 0 && warps % tile_waves(K) != 0)
+    return fail(DK_ERR_SHAPE, "gemv_w4a16: stage 4 needs warps 0 or a multiple of ceil(K / 2048) = %d (whole row "
+                "groups), got warps=%d K=%d", tile_waves(K), warps, K);
   if ((stage == 1 || stage == 2 || stage == 4) && K > dk::kGemvRowsMaxK)
     return fail(DK_ERR_SHAPE, "gemv_w4a16: stage %d stages x in LDS and needs K <= %d, got %d", stage,
                 dk::kGemvRowsMaxK, K);
@@ -90,6 +93,9 @@ static int check_fused_gemv(const char* what, int stage, int R, int warps, int p
   if (warps < 0 || warps > 16) return fail(DK_ERR_DOMAIN, "%s: warps must be 0..16, got %d", what, warps);
   if (pf < 0 || pf > 3) return fail(DK_ERR_DOMAIN, "%s: pf must be 0..3 for stage 4, got %d", what, pf);
   if (N <= 0 || K <= 0) return fail(DK_ERR_SHAPE, "%s: N and K must be positive (N=%d K=%d)", what, N, K);
+  if (warps != 0 && warps % tile_waves(K) != 0)
+    return fail(DK_ERR_SHAPE, "%s: warps must be 0 or a multiple of ceil(K / 2048) = %d (whole row groups), got %d",
+                what, tile_waves(K), warps);
   if (K > dk::kGemvRowsMaxK) return fail(DK_ERR_SHAPE, "%s: K <= %d required, got %d", what, dk::kGemvRowsMaxK, K);
   if (K % 32 != 0 || K % group != 0)
     return fail(DK_ERR_SHAPE, "K must be a multiple of 32 and of the group size (K=%d group=%d)", K, group);
@@ -113,7 +119,7 @@ int dk_gemv_w4a16_rmsnorm(int stage, int R, int warps, int pf, const void* packe
     return fail(DK_ERR_DOMAIN, "gemv_w4a16_rmsnorm: x_out must not alias x or delta (other workgroups still read them)");
   clear_error();
   dk::GemvInput in{x, row, delta, norm_w, eps, x_out};
-  dk::launch_gemv_w4a16_fused(1, 0, R, pf, packed, sz, in, y, N, K, ilog2(group), (hipStream_t)stream);
+  dk::launch_gemv_w4a16_fused(1, 0, R, warps, pf, packed, sz, in, y, N, K, ilog2(group), (hipStream_t)stream);
   return launched("gemv_w4a16_rmsnorm");
 }
 
@@ -139,7 +145,8 @@ int dk_gemv_w4a16_gate_up(int stage, int R, int warps, int pf, const void* packe
     return fail(DK_ERR_DOMAIN, "gemv_w4a16_gate_up: act must not alias x or delta");
   clear_error();
   dk::GemvInput in{x, row, delta, norm_w, eps, x_out};
-  dk::launch_gemv_w4a16_fused(norm_w ? 1 : 0, 1, R, pf, packed, sz, in, act, N, K, ilog2(group), (hipStream_t)stream);
+  dk::launch_gemv_w4a16_fused(norm_w ? 1 : 0, 1, R, warps, pf, packed, sz, in, act, N, K, ilog2(group),
+                              (hipStream_t)stream);
   return launched("gemv_w4a16_gate_up");
 }
 
@@ -175,7 +182,8 @@ int dk_gemv_w4a16_qkv_rope(int stage, int R, int warps, int pf, const void* pack
   clear_error();
   dk::GemvInput in{x, row, delta, norm_w, eps, x_out,
                    {cos_t, sin_t, pos, bt, kc, vc, n_q, n_kv, ilog2(head_dim), ilog2(page), max_pos, n_pages, n_bt}};
-  dk::launch_gemv_w4a16_fused(norm_w ? 1 : 0, 2, R, pf, packed, sz, in, qkv, N, K, ilog2(group), (hipStream_t)stream);
+  dk::launch_gemv_w4a16_fused(norm_w ? 1 : 0, 2, R, warps, pf, packed, sz, in, qkv, N, K, ilog2(group),
+                              (hipStream_t)stream);
   return launched("gemv_w4a16_qkv_rope");
 }
 

@@ -320,7 +320,8 @@ __device__ __forceinline__ void tile_input_load(const GemvInput& in, int uc, int
 
 template <int PRO>
 __device__ __forceinline__ void tile_input_finish(const GemvInput& in, TileRaw& raw, int uc, bool live, int K,
-                                                  float* s_ss, int wave, int nw, u32x4 (&xc)[4]) {
+                                                  float* s_ss, int wave, int gw0, int nw, bool writer,
+                                                  u32x4 (&xc)[4]) {
   if constexpr (PRO == kInPlain) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) xc[k] = raw.a[k];
@@ -348,9 +349,9 @@ __device__ __forceinline__ void tile_input_finish(const GemvInput& in, TileRaw& 
     if ((threadIdx.x & 63) == 0) s_ss[wave] = ss;
     __syncthreads();
     float tot = 0.f;
-    for (int i = 0; i < nw; ++i) tot += s_ss[i];
+    for (int i = 0; i < nw; ++i) tot += s_ss[gw0 + i];
     const float r = 1.0f / sqrtf(tot / (float)K + in.eps);
-    if (blockIdx.x == 0 && in.x_out != nullptr && live) {
+    if (writer && in.x_out != nullptr && live) {
       u32x4* Xo = reinterpret_cast<u32x4*>(in.x_out);
 #pragma unroll
       for (int k = 0; k < 4; ++k) Xo[4 * uc + k] = xr[k];
@@ -401,6 +402,9 @@ constexpr int kTileDepth = DK_TILE_DEPTH;  // weight tiles in flight per workgro
 // Pipeline: operand loads, then the weight loads of tiles 0 and 1, then the operand (waits for the operand loads
 // only), then for each tile t: compute it from its buffer and refill that buffer with tile t + 2. Two tiles are in
 // flight from the first instruction on.
+// A workgroup holds blockDim / (64 nw) independent row groups of nw = ceil(U / 64) waves each (group g takes the
+// workgroup's g-th run of T * NT rows): at small K a group is one wave, and several groups per workgroup cost fewer
+// workgroup dispatches than one single-wave workgroup per row tile.
 template <int T, int NT, int PRO, int EPI>
 __global__ void __launch_bounds__(1024)
 gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, const GemvInput in,
@@ -408,11 +412,14 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
   static_assert(EPI == kOutRows || (T * NT) % 2 == 0, "gate/up and rotation pairs need an even row tile");
   __shared__ float red[16][T * NT];
   __shared__ float s_ss[16];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
-  const int u = wave * kWave + lane;
+  const int nw = (U + kWave - 1) / kWave;  // waves of one row group
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int grp = wave / nw, gw0 = grp * nw;    // row group, its first wave
+  const int tid = threadIdx.x - gw0 * kWave;    // thread within the row group
+  const int u = (wave - gw0) * kWave + lane;
   const bool live = u < U;
   const int uc = live ? u : U - 1;  // dead lanes load a valid column and contribute 0
-  const int base = blockIdx.x * T * NT;
+  const int base = (blockIdx.x * (int)(blockDim.x / (nw * kWave)) + grp) * T * NT;
   const int NG = U >> gsh;
   int rpos = -1;
   if constexpr (EPI == kOutRope) rpos = *in.rope.pos;
@@ -426,7 +433,7 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
   for (int d = 0; d < DP; ++d) tile_issue<T>(W, SZ, base + d * T, N, U, NG, uc, gsh, w[d], sz[d]);
   __builtin_amdgcn_sched_barrier(0);
   u32x4 xc[4];
-  tile_input_finish<PRO>(in, raw, uc, live, U << 5, s_ss, wave, nw, xc);
+  tile_input_finish<PRO>(in, raw, uc, live, U << 5, s_ss, wave, gw0, nw, blockIdx.x == 0 && grp == 0, xc);
   const ColumnSums cs = column_sums(xc);
   const NibbleMasks m = nibble_masks();
   // rotation-pair operands of the RoPE epilogue, requested before the tiles are computed
@@ -463,15 +470,15 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
   if constexpr (EPI == kOutRows) {
     if (tid < T * NT && base + tid < N) {
       float acc = 0.f;
-      for (int i = 0; i < nw; ++i) acc += red[i][tid];
+      for (int i = 0; i < nw; ++i) acc += red[gw0 + i][tid];
       y[base + tid] = (f16)acc;
     }
   } else if constexpr (EPI == kOutRope) {
     if (tid < T * NT / 2 && 2 * rp + 1 < N) {
       float a = 0.f, b = 0.f;
       for (int i = 0; i < nw; ++i) {
-        a += red[i][2 * tid];
-        b += red[i][2 * tid + 1];
+        a += red[gw0 + i][2 * tid];
+        b += red[gw0 + i][2 * tid + 1];
       }
       const f16 a16 = (f16)a, b16 = (f16)b;
       const int nq = in.rope.n_q, nkv = in.rope.n_kv, half = 1 << hb;
@@ -494,8 +501,8 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
     if (tid < T * NT / 2 && base + 2 * tid + 1 < N) {
       float g = 0.f, up = 0.f;
       for (int i = 0; i < nw; ++i) {
-        g += red[i][2 * tid];
-        up += red[i][2 * tid + 1];
+        g += red[gw0 + i][2 * tid];
+        up += red[gw0 + i][2 * tid + 1];
       }
       y[(base >> 1) + tid] = silu_mul((f16)g, (f16)up);
     }
@@ -529,38 +536,42 @@ void launch_rows_p(int waves, int pf, const void* packed, const void* sz, const 
   launch_rows<R, 1>(waves, packed, sz, x, y, N, K, log2G, st);
 }
 
+// warps: waves per workgroup, 0 or a multiple of ceil(K / 2048) up to 16 (checked by the C ABI): that many / ceil(K /
+// 2048) row groups per workgroup (0 = one).
 template <int T, int NT, int PRO, int EPI>
-void launch_tile_nt(const void* packed, const void* sz, const GemvInput& in, void* y, int N, int K, int log2G,
-                    hipStream_t st) {
+void launch_tile_nt(int warps, const void* packed, const void* sz, const GemvInput& in, void* y, int N, int K,
+                    int log2G, hipStream_t st) {
   if constexpr (EPI != kOutRows && (T * NT) % 2 != 0) {
     return;  // rejected by the host checks (R * 2^pf >= 2); never instantiated as a kernel
   } else {
     const int U = K >> 5;
-    const int waves = (U + 63) / 64;
-    hipLaunchKernelGGL((gemv_w4a16_tile<T, NT, PRO, EPI>), dim3((N + T * NT - 1) / (T * NT)), dim3(64 * waves), 0,
+    const int nw = (U + 63) / 64;
+    const int groups = warps > 0 ? warps / nw : 1;
+    const int rows = T * NT * groups;
+    hipLaunchKernelGGL((gemv_w4a16_tile<T, NT, PRO, EPI>), dim3((N + rows - 1) / rows), dim3(64 * nw * groups), 0,
                        st, (const u32x4*)packed, (const uint32_t*)sz, in, (f16*)y, N, U, log2G - 5);
   }
 }
 
 template <int T, int PRO, int EPI>
-void launch_tile(int pf, const void* packed, const void* sz, const GemvInput& in, void* y, int N, int K, int log2G,
-                 hipStream_t st) {
+void launch_tile(int warps, int pf, const void* packed, const void* sz, const GemvInput& in, void* y, int N, int K,
+                 int log2G, hipStream_t st) {
   switch (pf) {
-    case 0: launch_tile_nt<T, 1, PRO, EPI>(packed, sz, in, y, N, K, log2G, st); break;
-    case 1: launch_tile_nt<T, 2, PRO, EPI>(packed, sz, in, y, N, K, log2G, st); break;
-    case 2: launch_tile_nt<T, 4, PRO, EPI>(packed, sz, in, y, N, K, log2G, st); break;
-    default: launch_tile_nt<T, 8, PRO, EPI>(packed, sz, in, y, N, K, log2G, st); break;
+    case 0: launch_tile_nt<T, 1, PRO, EPI>(warps, packed, sz, in, y, N, K, log2G, st); break;
+    case 1: launch_tile_nt<T, 2, PRO, EPI>(warps, packed, sz, in, y, N, K, log2G, st); break;
+    case 2: launch_tile_nt<T, 4, PRO, EPI>(warps, packed, sz, in, y, N, K, log2G, st); break;
+    default: launch_tile_nt<T, 8, PRO, EPI>(warps, packed, sz, in, y, N, K, log2G, st); break;
   }
 }
 
 template <int PRO, int EPI = kOutRows>
-void launch_tile_r(int R, int pf, const void* packed, const void* sz, const GemvInput& in, void* y, int N, int K,
-                   int log2G, hipStream_t st) {
+void launch_tile_r(int R, int warps, int pf, const void* packed, const void* sz, const GemvInput& in, void* y, int N,
+                   int K, int log2G, hipStream_t st) {
   switch (R) {
-    case 1: launch_tile<1, PRO, EPI>(pf, packed, sz, in, y, N, K, log2G, st); break;
-    case 2: launch_tile<2, PRO, EPI>(pf, packed, sz, in, y, N, K, log2G, st); break;
-    case 4: launch_tile<4, PRO, EPI>(pf, packed, sz, in, y, N, K, log2G, st); break;
-    default: launch_tile<8, PRO, EPI>(pf, packed, sz, in, y, N, K, log2G, st); break;
+    case 1: launch_tile<1, PRO, EPI>(warps, pf, packed, sz, in, y, N, K, log2G, st); break;
+    case 2: launch_tile<2, PRO, EPI>(warps, pf, packed, sz, in, y, N, K, log2G, st); break;
+    case 4: launch_tile<4, PRO, EPI>(warps, pf, packed, sz, in, y, N, K, log2G, st); break;
+    default: launch_tile<8, PRO, EPI>(warps, pf, packed, sz, in, y, N, K, log2G, st); break;
   }
 }
 
@@ -604,13 +615,13 @@ void launch_gemv_w4a16(int stage, int R, int waves, int pf, const void* packed, 
                        (const uint32_t*)sz, (const f16*)x, (f16*)y, N, K, log2G);
     return;
   }
-  if (waves <= 0) waves = stage == 3 ? min(16, ((K >> 5) + 63) / 64) : 4;
   if (stage == 4) {
     GemvInput in{};
     in.x = x;
-    launch_tile_r<kInPlain>(R, pf, packed, sz, in, y, N, K, log2G, st);
+    launch_tile_r<kInPlain>(R, waves, pf, packed, sz, in, y, N, K, log2G, st);
     return;
   }
+  if (waves <= 0) waves = stage == 3 ? min(16, ((K >> 5) + 63) / 64) : 4;
   if (stage == 1) R = 1;
   if (stage == 1 || stage == 2) {
     switch (R) {
@@ -629,23 +640,23 @@ void launch_gemv_w4a16(int stage, int R, int waves, int pf, const void* packed, 
   }
 }
 
-void launch_gemv_w4a16_fused(int prologue, int epilogue, int R, int pf, const void* packed, const void* sz,
+void launch_gemv_w4a16_fused(int prologue, int epilogue, int R, int warps, int pf, const void* packed, const void* sz,
                              const GemvInput& in, void* y, int N, int K, int log2G, hipStream_t st) {
   if (epilogue == kOutSwiglu) {
     if (prologue == kInRmsNorm)
-      launch_tile_r<kInRmsNorm, kOutSwiglu>(R, pf, packed, sz, in, y, N, K, log2G, st);
+      launch_tile_r<kInRmsNorm, kOutSwiglu>(R, warps, pf, packed, sz, in, y, N, K, log2G, st);
     else
-      launch_tile_r<kInPlain, kOutSwiglu>(R, pf, packed, sz, in, y, N, K, log2G, st);
+      launch_tile_r<kInPlain, kOutSwiglu>(R, warps, pf, packed, sz, in, y, N, K, log2G, st);
     return;
   }
   if (epilogue == kOutRope) {
     if (prologue == kInRmsNorm)
-      launch_tile_r<kInRmsNorm, kOutRope>(R, pf, packed, sz, in, y, N, K, log2G, st);
+      launch_tile_r<kInRmsNorm, kOutRope>(R, warps, pf, packed, sz, in, y, N, K, log2G, st);
     else
-      launch_tile_r<kInPlain, kOutRope>(R, pf, packed, sz, in, y, N, K, log2G, st);
+      launch_tile_r<kInPlain, kOutRope>(R, warps, pf, packed, sz, in, y, N, K, log2G, st);
     return;
   }
-  launch_tile_r<kInRmsNorm>(R, pf, packed, sz, in, y, N, K, log2G, st);
+  launch_tile_r<kInRmsNorm>(R, warps, pf, packed, sz, in, y, N, K, log2G, st);
 }
 
 }  // namespace dk

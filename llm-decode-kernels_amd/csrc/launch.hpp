@@ -10,7 +10,8 @@ namespace dk {
 
 // W4A16 GEMV. stage 0: exact per-element dequant, `waves` rows per workgroup. stage 1/2: each wave streams R whole
 // rows, `waves` waves per workgroup, 2^pf column steps in flight, x staged in LDS (K <= kGemvRowsMaxK). stage 3: the
-// workgroup's `waves` waves split K for R rows, pf = one-step prefetch.
+// workgroup's `waves` waves split K for R rows, pf = one-step prefetch. stage 4: row groups of ceil(K / 2048) waves
+// walk 2^pf tiles of R rows; `waves` = waves per workgroup (0 = one row group).
 constexpr int kGemvRowsMaxK = 32768;  // x in LDS: K * 2 bytes <= 64 KB per workgroup
 void launch_gemv_w4a16(int stage, int R, int waves, int pf, const void* packed, const void* sz, const void* x,
                        void* y, int N, int K, int log2G, hipStream_t st);
@@ -37,7 +38,7 @@ struct GemvInput {
 };
 // epilogue 0 = one fp16 output per row, 1 = SwiGLU of interleaved gate / up row pairs (N / 2 outputs), 2 = RoPE +
 // KV append of rotation-pair rows (qkv rows stored per head as j, j + D/2 for j < D/2; N outputs in head order).
-void launch_gemv_w4a16_fused(int prologue, int epilogue, int R, int pf, const void* packed, const void* sz,
+void launch_gemv_w4a16_fused(int prologue, int epilogue, int R, int warps, int pf, const void* packed, const void* sz,
                              const GemvInput& in, void* y, int N, int K, int log2G, hipStream_t st);
 // Default configuration for a shape: (stage, R, waves, pf).
 void gemv_default_config(int N, int K, int* stage, int* R, int* waves, int* pf);

@@ -270,11 +270,12 @@ attn_decode_kernel(const f16* __restrict__ qsrc, const float* __restrict__ cos_t
 }
 
 // Combine of the split partials of one query head per workgroup: thread (sl, d4) takes splits sl, sl + SLN, ... and
-// dims [4 d4, 4 d4 + 4); every lane keeps an online maximum over its splits (loads of 4 splits in flight), then the
-// SLN split lanes merge through LDS with the same max-rescale rule. The first 4 SLN splits' loads go out before *pos
+// dims [4 d4, 4 d4 + 4); every lane keeps an online maximum over its splits (loads of B splits in flight), then the
+// SLN split lanes merge through LDS with the same max-rescale rule. The first B SLN splits' loads go out before *pos
 // is read (clamped to the buffer's max_splits; splits past the live count are dropped by select once it is known), so
-// the position's round trip overlaps theirs.
-template <int D>
+// the position's round trip overlaps theirs. The launcher picks B so that one batch covers max_splits (up to
+// 16 SLN splits): every later batch would be one more dependent round trip.
+template <int D, int B>
 __global__ void __launch_bounds__(kAttnThreads)
 attn_combine_kernel(const float* __restrict__ o_part, const float* __restrict__ m_part,
                     const float* __restrict__ l_part, const int32_t* __restrict__ pos_ptr, int max_pos, int n_bt,
@@ -287,10 +288,10 @@ attn_combine_kernel(const float* __restrict__ o_part, const float* __restrict__ 
   const float* m = m_part + (size_t)head * max_splits;
   const float* l = l_part + (size_t)head * max_splits;
   const float* op = o_part + (size_t)head * max_splits * D + 4 * d4;
-  float ms[4], ls[4];
-  float4 os[4];
+  float ms[B], ls[B];
+  float4 os[B];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {  // first batch, speculative (in bounds of the partial buffers)
+  for (int k = 0; k < B; ++k) {  // first batch, speculative (in bounds of the partial buffers)
     const int s = min(sl + k * SLN, max_splits - 1);
     ms[k] = m[s];
     ls[k] = l[s];
@@ -303,10 +304,10 @@ attn_combine_kernel(const float* __restrict__ o_part, const float* __restrict__ 
   const int nsplit = skip ? 0 : attn_splits((int)((long long)pos + 1 < cap ? (long long)pos + 1 : cap), PS, max_splits);
   float M = -INFINITY, L = 0.f;
   float4 a = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = sl; s0 < nsplit; s0 += 4 * SLN) {
+  for (int s0 = sl; s0 < nsplit; s0 += B * SLN) {
     if (s0 != sl) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
+      for (int k = 0; k < B; ++k) {
         const int s = min(s0 + k * SLN, max_splits - 1);
         ms[k] = m[s];
         ls[k] = l[s];
@@ -314,14 +315,16 @@ attn_combine_kernel(const float* __restrict__ o_part, const float* __restrict__ 
       }
     }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {  // splits past the live count: dropped (their partials are stale or never written)
+    for (int k = 0; k < B; ++k) {  // splits past the live count: dropped (their partials are stale or never written)
       if (s0 + k * SLN >= nsplit) {
         ms[k] = -INFINITY;
         ls[k] = 0.f;
         os[k] = float4{0.f, 0.f, 0.f, 0.f};
       }
     }
-    const float Mn = fmaxf(fmaxf(M, fmaxf(ms[0], ms[1])), fmaxf(ms[2], ms[3]));
+    float Mn = M;
+#pragma unroll
+    for (int k = 0; k < B; ++k) Mn = fmaxf(Mn, ms[k]);
     if (Mn == -INFINITY) continue;
     const float r = (M == -INFINITY) ? 0.f : __expf(M - Mn);
     L *= r;
@@ -330,7 +333,7 @@ attn_combine_kernel(const float* __restrict__ o_part, const float* __restrict__ 
     a.z *= r;
     a.w *= r;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < B; ++k) {
       const float w = (ms[k] == -INFINITY) ? 0.f : __expf(ms[k] - Mn);
       L = fmaf(w, ls[k], L);
       a.x = fmaf(w, os[k].x, a.x);
@@ -664,6 +667,23 @@ attn_lean_kernel(const f16* __restrict__ qsrc, const float* __restrict__ cos_t, 
   }
 }
 
+// The combine with the smallest batch B in {4, 8, 16} whose B * SLN splits cover max_splits (16 beyond: the kernel
+// then loops over batches).
+template <int D>
+void launch_combine(const AttnLaunch& a, bool rope, hipStream_t st) {
+  constexpr int SLN = kAttnThreads / (D / 4);
+  const int mp = rope ? a.max_pos : 0;
+  if (a.max_splits <= 4 * SLN)
+    hipLaunchKernelGGL((attn_combine_kernel<D, 4>), dim3(a.n_q), dim3(kAttnThreads), 0, st, a.o_part, a.m_part,
+                       a.l_part, a.pos, mp, a.n_bt, a.log2P, a.part_size, a.max_splits, (f16*)a.out);
+  else if (a.max_splits <= 8 * SLN)
+    hipLaunchKernelGGL((attn_combine_kernel<D, 8>), dim3(a.n_q), dim3(kAttnThreads), 0, st, a.o_part, a.m_part,
+                       a.l_part, a.pos, mp, a.n_bt, a.log2P, a.part_size, a.max_splits, (f16*)a.out);
+  else
+    hipLaunchKernelGGL((attn_combine_kernel<D, 16>), dim3(a.n_q), dim3(kAttnThreads), 0, st, a.o_part, a.m_part,
+                       a.l_part, a.pos, mp, a.n_bt, a.log2P, a.part_size, a.max_splits, (f16*)a.out);
+}
+
 template <int D, int HPG, bool ROPE, int NW, int NT>
 void launch_lean(const AttnLaunch& a, hipStream_t st) {
   const float scale = 1.0f / sqrtf((float)D);
@@ -705,20 +725,14 @@ void launch_attn(const AttnLaunch& a, hipStream_t st) {
   const float scale = 1.0f / sqrtf((float)D);
   if (attn_use_lean(a)) {
     launch_lean_any<D, HPG, ROPE>(a, st);
-    if (a.max_splits > 1)
-      hipLaunchKernelGGL((attn_combine_kernel<D>), dim3(a.n_q), dim3(kAttnThreads), 0, st, a.o_part, a.m_part,
-                         a.l_part, a.pos, ROPE ? a.max_pos : 0, a.n_bt, a.log2P, a.part_size, a.max_splits,
-                         (f16*)a.out);
+    if (a.max_splits > 1) launch_combine<D>(a, ROPE, st);
     return;
   }
   hipLaunchKernelGGL((attn_decode_kernel<D, HPG, ROPE>), dim3(a.n_kv, a.max_splits), dim3(kAttnThreads), 0,
                      st, (const f16*)a.q, a.cos_t, a.sin_t, a.max_pos, a.pos, a.bt, a.n_bt, (f16*)a.kc, (f16*)a.vc,
                      a.n_pages, a.log2P, a.n_q, a.n_kv, a.part_size, a.max_splits, scale, a.o_part, a.m_part,
                      a.l_part, (f16*)a.out);
-  if (a.max_splits > 1)
-    hipLaunchKernelGGL((attn_combine_kernel<D>), dim3(a.n_q), dim3(kAttnThreads), 0, st, a.o_part, a.m_part,
-                       a.l_part, a.pos, ROPE ? a.max_pos : 0, a.n_bt, a.log2P, a.part_size, a.max_splits,
-                       (f16*)a.out);
+  if (a.max_splits > 1) launch_combine<D>(a, ROPE, st);
 }
 
 template <int D, bool ROPE>

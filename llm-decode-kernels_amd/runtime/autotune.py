@@ -59,14 +59,23 @@ def candidates(N, K):
                     continue
                 out.append((3, R, w, pf))
     if K <= 32768:
-        out += [(4, R, 0, pf) for R in (1, 2, 4, 8) for pf in range(4)]
+        out += tile_candidates(K)
     return [c for c in out if not (c[0] == 2 and K > 32768)]
 
 
-def fused_candidates(kind):
+def tile_candidates(K):
+    """stage-4 configurations: one row group per workgroup over R x 2^pf, and 2 or 4 row groups of ceil(K / 2048)
+    waves each (warps = groups x ceil(K / 2048) <= 16) over the smaller tiles."""
+    tw = -(-K // 2048)
+    out = [(4, R, 0, pf) for R in (1, 2, 4, 8) for pf in range(4)]
+    out += [(4, R, g * tw, pf) for g in (2, 4) if g * tw <= 16 for R in (1, 2, 4) for pf in range(3)]
+    return out
+
+
+def fused_candidates(kind, K):
     """stage-4 configurations of the fused INT4 GEMVs (the gate|up SwiGLU epilogue needs an even row tile; so does
     the qkv RoPE epilogue, which takes the same candidates)."""
-    return [(4, R, 0, pf) for R in (1, 2, 4, 8) for pf in range(4) if kind != "gate_up" or (R << pf) >= 2]
+    return [c for c in tile_candidates(K) if kind != "gate_up" or (c[1] << c[3]) >= 2]
 
 
 def f16_candidates(K):
@@ -92,7 +101,7 @@ def tune_fused_shape(Kx, kind, N, K, G, reps=5, log=print):
     if kind in ("f16", "f16_norm"):
         ops, nb, cands = [w], N * K * 2, f16_candidates(K)
     else:
-        ops, nb, cands = list(quantize_pack(w, G)), gemv_bytes(N, K, G), fused_candidates(kind)
+        ops, nb, cands = list(quantize_pack(w, G)), gemv_bytes(N, K, G), fused_candidates(kind, K)
     del w
     cold = ColdCopies(ops, n_copies(nb))
     call = {
@@ -307,14 +316,16 @@ def step_slots(model):
     epilogue, whose row tile must hold a rotation pair), "plain" (o, down; the INT4 head when the norm does not pay
     inside it), "gate_up" (gate|up with the SwiGLU epilogue), "f16_norm" (the fp16 head behind the final norm)."""
     lw = model.layers[0]
-    qkv = (("rope", lw["qkv"], fused_candidates("gate_up")) if model.rope_epilogue
-           else ("norm", lw["qkv"], fused_candidates("rmsnorm")))
-    slots = [qkv, ("plain", lw["o"], fused_candidates("rmsnorm")),
-             ("gate_up", lw["gu"], fused_candidates("gate_up")), ("plain", lw["down"], fused_candidates("rmsnorm"))]
+    K = lambda lin: lin.K
+    qkv = (("rope", lw["qkv"], fused_candidates("gate_up", K(lw["qkv"]))) if model.rope_epilogue
+           else ("norm", lw["qkv"], fused_candidates("rmsnorm", K(lw["qkv"]))))
+    slots = [qkv, ("plain", lw["o"], fused_candidates("rmsnorm", K(lw["o"]))),
+             ("gate_up", lw["gu"], fused_candidates("gate_up", K(lw["gu"]))),
+             ("plain", lw["down"], fused_candidates("rmsnorm", K(lw["down"])))]
     head = model.lm_head
     if head.quant:
         kind = "norm" if model.norm_fusion_pays(head) else "plain"
-        slots.append((kind, head, fused_candidates("rmsnorm")))
+        slots.append((kind, head, fused_candidates("rmsnorm", head.K)))
     elif model.use_f16_gemv(head):
         slots.append(("f16_norm", head, f16_candidates(head.K)))
     return slots

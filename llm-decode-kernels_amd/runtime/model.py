@@ -266,10 +266,13 @@ class Model:
         return json.load(open(p)) if p.exists() else {}
 
     def _policy_entry(self, ctx_cap):
+        return self._policy_entry_of(self._policy(), self.D, ctx_cap)
+
+    @staticmethod
+    def _policy_entry_of(pol, head_dim, ctx_cap):
         """Entry tuned at the largest context <= ctx_cap (runtime/model.py:164-172), from the head-dim-specific table
         ("policy_d128") when there is one: {"part_size", "impl"}."""
-        pol = self._policy()
-        ents = [e for e in pol.get(f"policy_d{self.D}", pol.get("policy", [])) if e["max_ctx"] < (1 << 30)]
+        ents = [e for e in pol.get(f"policy_d{head_dim}", pol.get("policy", [])) if e["max_ctx"] < (1 << 30)]
         if not ents:
             return {"part_size": 64, "impl": 1}
         below = [e for e in ents if e["max_ctx"] <= ctx_cap]

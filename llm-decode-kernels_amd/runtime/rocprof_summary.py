@@ -8,6 +8,14 @@
         WRITE_SIZE pass over ``bench.py --leg gemv``. The counters are scaled by what they read for kernels of known
         size run in the same process (bench.py calibration_leg): bw_read streaming B bytes once (FETCH_SIZE per B read)
         and the last 16 device copies of B bytes (WRITE_SIZE per B written).
+
+    python -m runtime.rocprof_summary counters <dir> [<dir> ...] [--kernel <substring> ...] [--out f.json]
+        Per kernel launch shape (name, grid, workgroup): the mean per dispatch of every counter found in the
+        counter_collection.csv files of the given passes, and the ratios derived from them when their counters are
+        present: mean L2 read latency seen by the vector caches (TCP_TCC_READ_REQ_LATENCY / TCP_TCC_READ_REQ, cycles),
+        mean HBM-side read latency (TCC_EA0_RDREQ_LEVEL / TCC_EA0_RDREQ, Little's law, cycles), the share of wave
+        time spent waiting on a memory dependency (SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES), vector reads per wave, and
+        the L2 hit rate.
 """
 import argparse
 import csv
@@ -72,6 +80,44 @@ def pmc(fetch_dir, write_dir, kernel, nbytes, n_cal=16):
             "hbm_bytes_per_launch": round(fetch + write)}
 
 
+def _derive(c):
+    d = {}
+    ratio = lambda a, b: round(c[a] / c[b], 4) if a in c and c.get(b) else None
+    for key, a, b in (("l2_read_latency_cycles", "TCP_TCC_READ_REQ_LATENCY_sum", "TCP_TCC_READ_REQ_sum"),
+                      ("hbm_read_latency_cycles", "TCC_EA0_RDREQ_LEVEL_sum", "TCC_EA0_RDREQ_sum"),
+                      ("wave_time_waiting_on_memory", "SQ_WAIT_INST_ANY", "SQ_WAVE_CYCLES"),
+                      ("wave_time_waiting_any", "SQ_WAIT_ANY", "SQ_WAVE_CYCLES"),
+                      ("vmem_reads_per_wave", "SQ_INSTS_VMEM_RD", "SQ_WAVES"),
+                      ("l2_read_requests_per_wave", "TCP_TCC_READ_REQ_sum", "SQ_WAVES"),
+                      ("hbm_read_requests_per_wave", "TCC_EA0_RDREQ_sum", "SQ_WAVES")):
+        v = ratio(a, b)
+        if v is not None:
+            d[key] = v
+    if "TCC_HIT_sum" in c and "TCC_MISS_sum" in c and c["TCC_HIT_sum"] + c["TCC_MISS_sum"] > 0:
+        d["l2_hit_rate"] = round(c["TCC_HIT_sum"] / (c["TCC_HIT_sum"] + c["TCC_MISS_sum"]), 4)
+    return d
+
+
+def counters(dirs, kernels=()):
+    """{launch shape: {"dispatches": n, "counters": {name: mean per dispatch}, "derived": {...}}}."""
+    acc = {}
+    for d in dirs:
+        for f in sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)):
+            for r in csv.DictReader(open(f)):
+                name = r["Kernel_Name"]
+                if kernels and not any(k in name for k in kernels):
+                    continue
+                key = f"{_short(name, 60)} grid {r['Grid_Size']} wg {r['Workgroup_Size']}"
+                e = acc.setdefault(key, {})
+                e.setdefault(r["Counter_Name"], {})[(d, r["Dispatch_Id"])] = float(r["Counter_Value"])
+    out = {}
+    for key, e in acc.items():
+        means = {c: statistics.mean(v.values()) for c, v in e.items()}
+        out[key] = {"dispatches": max(len(v) for v in e.values()),
+                    "counters": {c: round(m, 2) for c, m in sorted(means.items())}, "derived": _derive(means)}
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -84,9 +130,19 @@ def main(argv=None):
     p.add_argument("--kernel", required=True)
     p.add_argument("--bytes", type=int, required=True)
     p.add_argument("--out")
+    c = sub.add_parser("counters")
+    c.add_argument("dirs", nargs="+")
+    c.add_argument("--kernel", action="append", default=[])
+    c.add_argument("--out")
     a = ap.parse_args(argv)
     if a.cmd == "stats":
         print(stats(a.dir, a.top))
+        return
+    if a.cmd == "counters":
+        res = counters(a.dirs, a.kernel)
+        print(json.dumps(res, indent=1))
+        if a.out:
+            json.dump(res, open(a.out, "w"), indent=1)
         return
     res = pmc(a.fetch, a.write, a.kernel, a.bytes)
     res["algorithmic_bytes_per_launch"] = a.bytes

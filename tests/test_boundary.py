@@ -57,7 +57,9 @@ def _err(lib, rc):
     ((5, 1, 0, 0, A16, A16, A16, A16, 4, 128, 128), 4, "stage"),
     ((4, 16, 0, 0, A16, A16, A16, A16, 4, 128, 128), 4, "R must be 1,2,4,8"),
     ((4, 4, 0, 4, A16, A16, A16, A16, 4, 128, 128), 4, "pf must be 0..3"),
-    ((4, 4, 2, 0, A16, A16, A16, A16, 4, 8192, 128), 3, "warps * 2048 >= K"),
+    ((4, 4, 2, 0, A16, A16, A16, A16, 4, 8192, 128), 3, "multiple of ceil(K / 2048) = 4"),
+    ((4, 4, 6, 0, A16, A16, A16, A16, 4, 8192, 128), 3, "whole row groups"),
+    ((4, 4, 17, 0, A16, A16, A16, A16, 4, 2048, 128), 4, "warps must be 0..16"),
     ((2, 1, 17, 0, A16, A16, A16, A16, 4, 128, 128), 4, "warps"),
     ((2, 1, 0, 4, A16, A16, A16, A16, 4, 128, 128), 4, "pf must be 0..3"),
     ((3, 1, 0, 2, A16, A16, A16, A16, 4, 128, 128), 4, "pf must be 0 or 1"),
@@ -195,6 +197,9 @@ def test_fused_gemv_validation(lib):
     assert _fused(lib, lib.dk_gemv_w4a16_rmsnorm, norm_w=None)[0] == 1
     assert _fused(lib, lib.dk_gemv_w4a16_rmsnorm, x_out=A16)[0] == 4
     assert _fused(lib, lib.dk_gemv_w4a16_rmsnorm, pf=4)[0] == 4
+    rc, m = _fused(lib, lib.dk_gemv_w4a16_rmsnorm, warps=3, K=4096)     # row groups of 2 waves at K 4096
+    assert rc == 3 and "whole row groups" in m
+    assert _fused(lib, lib.dk_gemv_w4a16_gate_up, warps=17)[0] == 4
 
 
 def test_gemv_f16_validation(lib):

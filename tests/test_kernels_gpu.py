@@ -37,6 +37,19 @@ GEMV_CFGS = [(0, 1, 4, 0), (0, 1, 1, 0), (1, 1, 0, 0), (1, 1, 4, 3)] + \
             [(4, r, 0, pf) for r in (1, 2, 4, 8) for pf in (0, 1, 2, 3)] + [(4, 4, 16, 1)]
 
 
+def tile_groups(Kd, cfgs=((4, 1, 2, 1), (4, 2, 4, 1), (4, 4, 2, 2), (4, 2, 16, 0))):
+    """Stage-4 configurations with several row groups per workgroup, their `warps` scaled to whole row groups of
+    ceil(Kd / 2048) waves (those that fit 16 waves); the rest of a list passes through."""
+    tw = -(-Kd // 2048)
+    out = []
+    for c in cfgs:
+        if c[0] != 4 or c[2] == 0:
+            out.append(c)
+        elif c[2] * tw <= 16:
+            out.append((4, c[1], c[2] * tw, c[3]))
+    return out
+
+
 def gemv(K, cfg, packed, sz, x, N, group):
     y = torch.empty(N, dtype=torch.half, device=DEV)
     K.gemv_w4a16(cfg[0], cfg[1], cfg[2], cfg[3], packed, sz, x, y, group)
@@ -91,7 +104,7 @@ def test_gemv_real_shapes(K, name, G):
                                                            (2, 2, 1, 3), (3, 4, 0, 0), (3, 2, 1, 1), (4, 2, 0, 0),
                                                            (4, 8, 0, 3)]
     from runtime.model import default_gemv_config
-    cfgs = cfgs + [default_gemv_config(N, Kd)]
+    cfgs = [c for c in cfgs if not (c[0] == 4 and c[2])] + tile_groups(Kd) + [default_gemv_config(N, Kd)]
     for cfg in cfgs:
         assert_close(gemv(K, cfg, packed, sz, xd, N, G), ref, 5e-3, f"gemv {name} {N}x{Kd} G{G} {cfg}")
 
@@ -457,7 +470,7 @@ def test_gemv_rmsnorm_fused(K, N, Kd, mode):
     ref = R.gemv_ref(wref, normed)
     y = torch.empty(N, dtype=torch.half, device=DEV)
     x_out = torch.zeros(Kd, dtype=torch.half, device=DEV)
-    for cfg in ((4, 2, 0, 0), (4, 1, 0, 1), (4, 4, 0, 3), (4, 8, 0, 2)):
+    for cfg in ((4, 2, 0, 0), (4, 1, 0, 1), (4, 4, 0, 3), (4, 8, 0, 2)) + tuple(tile_groups(Kd)):
         if mode == "row":
             K.gemv_w4a16_rmsnorm(*cfg, packed, sz, table.to(DEV), torch.tensor([3], device=DEV), None, nw.to(DEV),
                                  1e-5, x_out, y, G)
@@ -494,7 +507,7 @@ def test_gemv_gate_up_swiglu_epilogue(K, I, Kd, norm):
     sep = torch.empty(I, dtype=torch.half, device=DEV)
     x_out = torch.zeros(Kd, dtype=torch.half, device=DEV) if norm else None
     xd = x.to(DEV)
-    for cfg in ((4, 2, 0, 0), (4, 1, 0, 1), (4, 4, 0, 2), (4, 8, 0, 3)):
+    for cfg in ((4, 2, 0, 0), (4, 1, 0, 1), (4, 4, 0, 2), (4, 8, 0, 3)) + tuple(tile_groups(Kd)):
         if norm:
             K.gemv_w4a16_gate_up(*cfg, pk_il, sz_il, xd, None, d.to(DEV), nw.to(DEV), 1e-5, x_out, act, G)
             K.gemv_w4a16_rmsnorm(*cfg, packed, sz, xd, None, d.to(DEV), nw.to(DEV), 1e-5,
@@ -608,7 +621,7 @@ def test_gemv_qkv_rope_epilogue(K, D, n_q, n_kv, norm):
     dd = torch.randn(Kd, generator=g).half().to(DEV) if norm else None
     nwd = (1 + 0.1 * torch.randn(Kd, generator=g)).half().to(DEV) if norm else None
     for pos_v in (0, 21, 37, 63, 64, -1):
-        for cfg in ((4, 2, 0, 0), (4, 1, 0, 1), (4, 4, 0, 2)):
+        for cfg in ((4, 2, 0, 0), (4, 1, 0, 1), (4, 4, 0, 2)) + tuple(tile_groups(Kd)):
             print(f"qkv rope D{D} n_q{n_q} n_kv{n_kv} norm={norm} pos {pos_v} cfg {cfg}", flush=True)
             pos = torch.tensor([pos_v], dtype=torch.int32, device=DEV)
             kc_a = torch.randn(6, n_kv, 16, D, generator=g).half().to(DEV)
