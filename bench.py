@@ -314,12 +314,13 @@ def kernels_leg(Kx, n=64, reps=5):
     return out
 
 
-def attn8b_leg(Kx, ctx=4096, reps=5, eager=8):
+def attn8b_leg(Kx, ctx=4096, reps=5, eager=8, part_size=0):
     """Decode attention of BASELINE config 5 alone: Llama-3-8B heads (32 q / 8 kv, D 128, page 16) at context ctx,
     the reference op (split kernel + combine) with the runtime's policy entry for that context, each launch on a
     different cold copy of the paged K/V (block table a seeded permutation), then bw_read over the same K/V bytes on
     the split kernel's workgroup count and on the whole chip. Timed as hipGraphs of back-to-back launches; `eager`
-    extra launches of each run outside any graph first, for the counter passes (rocprofv3 --pmc over this leg)."""
+    extra launches of each run outside any graph first, for the counter passes (rocprofv3 --pmc over this leg).
+    part_size > 0 replaces the policy's split size (lean kernel when it fits, else the block kernel)."""
     import math
     import torch
     from runtime.model import DecodeConfig, Model
@@ -330,6 +331,8 @@ def attn8b_leg(Kx, ctx=4096, reps=5, eager=8):
     cap = ctx + 48
     ent = Model._policy_entry_of(json.load(open(DecodeConfig().attn_policy_path)), D, cap)
     ps, impl = ent["part_size"], ent.get("impl", 1)
+    if part_size > 0:
+        ps, impl = part_size, (3 if part_size % 16 == 0 and part_size <= 256 else 1)
     version = 5 if impl == 3 else 3
     S = math.ceil(cap / ps)
     pages = math.ceil(cap / P)
@@ -549,6 +552,7 @@ def main():
                          "attention alone and bw_read of its K/V bytes; prefill: the TinyLlama prefill leg only; "
                          "kernels: the attention and fused-op kernels of configs 2 and 3 only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline leg")
+    ap.add_argument("--attn-part", type=int, default=0, help="attn8b: split size instead of the policy's")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -588,7 +592,7 @@ def main():
         return
 
     if a.leg == "attn8b":
-        r = attn8b_leg(Kx)
+        r = attn8b_leg(Kx, part_size=a.attn_part)
         log(f"llama3-8b attention ctx {r['ctx']} (part {r['part_size']}, {r['splits']} splits): {r['us']:.3f} us -> "
             f"{r['gbps']:.0f} GB/s; bw_read of the K/V bytes: " +
             ", ".join(f"{k} {v['us']:.3f} us" for k, v in r["bw_read"].items()))

@@ -370,7 +370,9 @@ def tune_step(models=("tinyllama", "llama3_8b"), path=CONFIG, rounds=2, log=prin
                 log(f"  {name} {key}: {list(best)} {times[best]:.1f} us per step (was {list(cur) if cur else None})")
         model.capture()
         log(f"  {name}: step {step_time_us(model, ctx):.1f} us with the in-step choices (from {base:.1f})")
-        table.update({k: list(v) for k, v in model.step_cfg_override.items()})
+        # only this model's slots: its override map also holds the other models' entries read from the old table
+        tuned = {model.step_key(kind, lin) for kind, lin, _ in step_slots(model)}
+        table.update({k: list(v) for k, v in model.step_cfg_override.items() if k in tuned})
         del model
         torch.cuda.empty_cache()
     out = dict(old, best_step=table)
