@@ -29,8 +29,9 @@ Also measured in the same run (extra keys of the JSON line):
 --gpus N > 1 exits with a message: the path is single-GPU by design (one GPU per box here).
 --leg gemv runs only the GEMV roofline leg (used under rocprofv3 for the kernel trace and counter passes); --leg attn8b
 only the Llama-3-8B ctx-4096 attention and bw_read of its K/V bytes (the same, for the attention kernels); --leg
-decode / prefill / decode8b / kernels run one leg alone (the decode and prefill legs without the standalone GEMV and
-kernel legs, so that their traces hold only the model's kernels).
+readsweep bw_read from 2 to 512 MB with a fixed-cost + bandwidth fit; --leg decode / prefill / decode8b / kernels run
+one leg alone (the decode and prefill legs without the standalone GEMV and kernel legs, so that their traces hold only
+the model's kernels).
 """
 import argparse
 import json
@@ -223,6 +224,32 @@ def read_ceiling_leg(Kx, nbytes, reps=5):
     del cold
     return {"bytes": nbytes, "mean_us": round(best[0], 3), "gbps": round(nbytes / best[0] / 1e3, 1),
             "frac": round(nbytes / best[0] / 1e3 / HBM_PEAK_GBS, 4), "grid": [best[1], best[2]]}
+
+
+def read_sweep_leg(Kx, sizes_mb=(2, 4, 8, 16, 31.232, 64, 128, 256, 512), reps=5):
+    """bw_read over cold copies at sizes from 2 MB to 512 MB (best of two grids per size), and the least-squares fit
+    time = fixed + bytes / bandwidth: the per-launch fixed cost and the streaming bandwidth that bound any kernel
+    reading that many bytes once."""
+    import torch
+    from runtime.timing import ColdCopies, graph_time, n_copies
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    pts = []
+    for mb in sizes_mb:
+        nbytes = int(mb * 1e6) // (16 * 512) * (16 * 512)
+        cold = ColdCopies([torch.empty(nbytes, dtype=torch.uint8, device="cuda")], n_copies(nbytes, min_copies=2))
+        best = min(graph_time(lambda i: Kx.bw_read(cold[i][0], sink, nbytes // 16 // t, t, 1), cold.copies, reps)[1]
+                   for t in (512, 256))
+        pts.append({"bytes": nbytes, "us": round(best, 3), "gbps": round(nbytes / best / 1e3, 1),
+                    "frac": round(nbytes / best / 1e3 / HBM_PEAK_GBS, 4)})
+        del cold
+        torch.cuda.empty_cache()
+    n = len(pts)
+    mx = sum(p["bytes"] for p in pts) / n
+    my = sum(p["us"] for p in pts) / n
+    slope = sum((p["bytes"] - mx) * (p["us"] - my) for p in pts) / sum((p["bytes"] - mx) ** 2 for p in pts)
+    fixed = my - slope * mx
+    return {"points": pts, "fit_fixed_us": round(fixed, 3), "fit_gbps": round(1e-3 / slope, 1),
+            "fit_frac": round(1e-3 / slope / HBM_PEAK_GBS, 4)}
 
 
 def calibration_leg(Kx, nbytes, n=16):
@@ -545,11 +572,12 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--ctx", type=int, default=512)
-    ap.add_argument("--leg", choices=("all", "gemv", "kernels", "decode", "decode8b", "attn8b", "prefill"),
+    ap.add_argument("--leg", choices=("all", "gemv", "kernels", "decode", "decode8b", "attn8b", "readsweep", "prefill"),
                     default="all",
                     help="gemv: the 4096x14336 GEMV and its calibration copies only; decode: the TinyLlama decode "
                          "step only; decode8b: the Llama-3-8B decode legs only; attn8b: the Llama-3-8B ctx-4096 "
-                         "attention alone and bw_read of its K/V bytes; prefill: the TinyLlama prefill leg only; "
+                         "attention alone and bw_read of its K/V bytes; readsweep: bw_read from 2 to 512 MB and "
+                         "its fixed-cost + bandwidth fit; prefill: the TinyLlama prefill leg only; "
                          "kernels: the attention and fused-op kernels of configs 2 and 3 only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline leg")
     ap.add_argument("--attn-part", type=int, default=0, help="attn8b: split size instead of the policy's")
@@ -589,6 +617,13 @@ def main():
 
     if a.leg == "decode8b":
         print(json.dumps({"leg": "decode8b", "decode_llama3_8b_ctx4096": decode_8b_leg()}), flush=True)
+        return
+
+    if a.leg == "readsweep":
+        r = read_sweep_leg(Kx)
+        log(f"bw_read: time = {r['fit_fixed_us']} us + bytes / {r['fit_gbps']} GB/s; " +
+            ", ".join(f"{p['bytes'] / 1e6:.0f} MB {p['us']} us ({p['frac']:.0%})" for p in r["points"]))
+        print(json.dumps({"leg": "readsweep", "read_sweep": r}), flush=True)
         return
 
     if a.leg == "attn8b":
