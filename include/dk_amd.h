@@ -139,7 +139,8 @@ int dk_rope_append_rows(void* qkv, const float* cos_t, const float* sin_t, const
  * (delta may be NULL; src = rows[r] when rows != NULL, e.g. the embedding rows of the prompt's tokens, else r),
  * x_out[r] = xn, out[r] = w * fp16(float(xn) * rsqrt-term). x_in has n_src rows (M when rows is NULL); a gathered
  * index outside [0, n_src) is not read: that row's x_out and out are NaN. x_out may equal x_in when rows is NULL; out
- * aliases nothing. No counterpart in the reference (its add_rmsnorm is one vector, kernels/bindings.cpp:64-72).
+ * aliases nothing; H as for dk_add_rmsnorm. No counterpart in the reference (its add_rmsnorm is one vector,
+ * kernels/bindings.cpp:64-72).
  */
 int dk_rmsnorm_rows(const void* x_in, const int64_t* rows, int n_src, const void* delta, const void* w, void* x_out,
                     void* out, int M, int H, float eps, void* stream);
@@ -233,7 +234,8 @@ int dk_attention_decode(const void* qkv, const float* cos_t, const float* sin_t,
  * Fused residual add + RMSNorm:  x <- x + delta (fp16 add, written back; skipped if delta == NULL);
  * out = w * fp16(float(x) * rsqrt(mean(float(x)^2) + eps)).
  * Replaces add_rmsnorm (kernels/bindings.cpp:64-72) -> add_rmsnorm_launch (kernels/fused_norm.cu:56-58).
- * H % 8 == 0, 8 <= H <= 2^20; x, delta, w, out 16-byte aligned.
+ * H % 8 == 0, 8 <= H <= 65536 (the row is held in registers: 8 chunks of 8 for each of 1024 threads); x, delta, w,
+ * out 16-byte aligned.
  */
 int dk_add_rmsnorm(void* x, const void* delta, const void* w, void* out, int H, float eps, void* stream);
 

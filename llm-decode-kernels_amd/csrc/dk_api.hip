@@ -424,8 +424,8 @@ int dk_attention_decode(const void* qkv, const float* cos_t, const float* sin_t,
 
 int dk_add_rmsnorm(void* x, const void* delta, const void* w, void* out, int H, float eps, void* stream) {
   if (!x || !w || !out) return fail(DK_ERR_NULL, "add_rmsnorm: null pointer argument");
-  if (H <= 0 || H % 8 != 0 || H > (1 << 20))
-    return fail(DK_ERR_SHAPE, "add_rmsnorm: H must be a positive multiple of 8 (<= 2^20), got %d", H);
+  if (H <= 0 || H % 8 != 0 || H > dk::kRowNormMaxH)
+    return fail(DK_ERR_SHAPE, "add_rmsnorm: H must be a positive multiple of 8 (<= %d), got %d", dk::kRowNormMaxH, H);
   if (!aligned16(x)) return fail(DK_ERR_ALIGN, "x must be 16B aligned");
   if (!aligned16(w)) return fail(DK_ERR_ALIGN, "w must be 16B aligned");
   if (!aligned16(out)) return fail(DK_ERR_ALIGN, "out must be 16B aligned");
@@ -486,8 +486,8 @@ int dk_rmsnorm_rows(const void* x_in, const int64_t* rows, int n_src, const void
                     void* out, int M, int H, float eps, void* stream) {
   if (!x_in || !w || !x_out || !out) return fail(DK_ERR_NULL, "rmsnorm_rows: null pointer argument");
   if (M < 1 || M > (1 << 24)) return fail(DK_ERR_SHAPE, "rmsnorm_rows: M must be 1..2^24, got %d", M);
-  if (H <= 0 || H % 8 != 0 || H > (1 << 20))
-    return fail(DK_ERR_SHAPE, "rmsnorm_rows: H must be a positive multiple of 8 (<= 2^20), got %d", H);
+  if (H <= 0 || H % 8 != 0 || H > dk::kRowNormMaxH)
+    return fail(DK_ERR_SHAPE, "rmsnorm_rows: H must be a positive multiple of 8 (<= %d), got %d", dk::kRowNormMaxH, H);
   if (!aligned16(x_in) || !aligned16(w) || !aligned16(x_out) || !aligned16(out) || (delta && !aligned16(delta)))
     return fail(DK_ERR_ALIGN, "rmsnorm_rows: x_in, delta, w, x_out and out must be 16B aligned");
   if (rows && (reinterpret_cast<uintptr_t>(rows) & 7u)) return fail(DK_ERR_ALIGN, "rmsnorm_rows: rows must be 8B aligned");

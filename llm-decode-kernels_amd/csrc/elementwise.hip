@@ -7,103 +7,74 @@ namespace dk {
 namespace {
 
 // ---------------------------------------------------------------------------------------------------------------
-// x <- x + delta (fp16 add, one rounding, written back; skipped when delta is null);
-// out = w * fp16(float(x) * r), r = 1 / sqrt(sum(float(x)^2) / H + eps)   (reference/ref_ops.py:15-20).
-// One workgroup; each thread owns 8-element (16 B) chunks. The residual is bit-exact; the product float(x) * r is
-// rounded to fp16 before the fp16 multiply by w, as the reference does.
+// Residual + RMSNorm of one row per workgroup, the row held in registers (dk_add_rmsnorm is the one-row case, in
+// place; dk_rmsnorm_rows the prefill rows, with an optional gather):
+//   xn = fp16(x_in[src] + delta[r])   (delta optional; src = rows[r] with a gather index, else r)
+//   x_out[r] = xn,  out[r] = w * fp16(float(xn) * rr),  rr = 1 / sqrt(sum(float(xn)^2) / H + eps)
+// with the reference's rounding points (reference/ref_ops.py:15-20). Thread t of T owns the C 16-byte chunks t, t + T,
+// ..., t + (C - 1) T. Every operand load -- the row, the delta and the norm weight, which is needed only after the
+// reduction -- is issued unconditionally before any arithmetic (chunk indices clamped; a missing delta re-reads the
+// row), so the weight's latency hides behind the sum and the row is never read back. One wave sum per wave, one LDS
+// exchange. x_out may be x_in itself when there is no gather: a thread writes only chunks it has already read.
+// A gathered row index outside [0, n_src) reads row 0 and poisons the row with NaN instead of reading out of bounds.
+template <int C>
 __global__ void __launch_bounds__(1024)
-add_rmsnorm_kernel(f16* __restrict__ x, const f16* __restrict__ delta, const f16* __restrict__ w,
-                   f16* __restrict__ out, int H, float eps) {
-  __shared__ float wsum[16];
-  const int tid = threadIdx.x, nt = blockDim.x;
-  float ss = 0.f;
-  for (int i = tid * 8; i < H; i += nt * 8) {
-    u32x4 xv = *reinterpret_cast<const u32x4*>(x + i);
-    if (delta != nullptr) {
-      const u32x4 dv = *reinterpret_cast<const u32x4*>(delta + i);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) xv[k] = as_u32(as_f16x2(xv[k]) + as_f16x2(dv[k]));
-      *reinterpret_cast<u32x4*>(x + i) = xv;
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const f16x2 h = as_f16x2(xv[k]);
-      const float a = (float)h.x, b = (float)h.y;
-      ss = fmaf(a, a, ss);
-      ss = fmaf(b, b, ss);
-    }
-  }
-  ss = group_sum<kWave>(ss);
-  if ((tid & 63) == 0) wsum[tid >> 6] = ss;
-  __syncthreads();
-  float tot = 0.f;
-  const int nw = nt >> 6;
-  for (int i = 0; i < nw; ++i) tot += wsum[i];
-  const float r = 1.0f / sqrtf(tot / (float)H + eps);
-  for (int i = tid * 8; i < H; i += nt * 8) {
-    const u32x4 xv = *reinterpret_cast<const u32x4*>(x + i);  // this thread's own write above
-    const u32x4 wv = *reinterpret_cast<const u32x4*>(w + i);
-    u32x4 o;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const f16x2 h = as_f16x2(xv[k]);
-      const f16x2 hn = {(f16)((float)h.x * r), (f16)((float)h.y * r)};
-      o[k] = as_u32(as_f16x2(wv[k]) * hn);
-    }
-    *reinterpret_cast<u32x4*>(out + i) = o;
-  }
-}
-
-// ---------------------------------------------------------------------------------------------------------------
-// The residual + RMSNorm of M rows (prefill), one workgroup per row, with add_rmsnorm's rounding points:
-// xn = fp16(x_in[src] + delta[r]) (delta optional; src = rows[r] when a gather index is given, e.g. embedding rows of
-// the prompt's tokens, else r), x_out[r] = xn, out[r] = w * fp16(float(xn) * r_r), r_r = 1 / sqrt(sum(xn^2) / H + eps).
-// x_out may be x_in itself when there is no gather (a row is read and written by its own workgroup only).
-__global__ void __launch_bounds__(1024)
-rmsnorm_rows_kernel(const f16* x_in, const int64_t* __restrict__ rows, int n_src, const f16* __restrict__ delta,
-                    const f16* __restrict__ w, f16* x_out, f16* __restrict__ out, int H, float eps) {
-  __shared__ float wsum[16];
-  const int r = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
-  // a gathered row index outside [0, n_src) reads row 0 and poisons the row with NaN instead of reading out of bounds
+row_norm_kernel(const f16* x_in, const int64_t* __restrict__ rows, int n_src, const f16* __restrict__ delta,
+                const f16* __restrict__ w, f16* x_out, f16* __restrict__ out, int H, float eps) {
+  __shared__ float part[16];
+  const int r = blockIdx.x, tid = threadIdx.x, T = blockDim.x, U = H >> 3;
   const long long sr = rows != nullptr ? rows[r] : r;
   const bool bad = sr < 0 || sr >= n_src;
-  const f16* src = x_in + (size_t)(bad ? 0 : sr) * H;
-  f16* xo = x_out + (size_t)r * H;
+  const u32x4* src = reinterpret_cast<const u32x4*>(x_in + (size_t)(bad ? 0 : sr) * H);
+  const u32x4* dl = delta != nullptr ? reinterpret_cast<const u32x4*>(delta + (size_t)r * H) : src;
+  const u32x4* wc = reinterpret_cast<const u32x4*>(w);
+  u32x4 xv[C], dv[C], wv[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) xv[c] = src[min(tid + c * T, U - 1)];
+#pragma unroll
+  for (int c = 0; c < C; ++c) dv[c] = dl[min(tid + c * T, U - 1)];
+#pragma unroll
+  for (int c = 0; c < C; ++c) wv[c] = wc[min(tid + c * T, U - 1)];
+  u32x4* xo = reinterpret_cast<u32x4*>(x_out + (size_t)r * H);
   float ss = 0.f;
-  for (int i = tid * 8; i < H; i += nt * 8) {
-    u32x4 xv = *reinterpret_cast<const u32x4*>(src + i);
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int u = tid + c * T;
     if (delta != nullptr) {
-      const u32x4 dv = *reinterpret_cast<const u32x4*>(delta + (size_t)r * H + i);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) xv[k] = as_u32(as_f16x2(xv[k]) + as_f16x2(dv[k]));
+      for (int k = 0; k < 4; ++k) xv[c][k] = as_u32(as_f16x2(xv[c][k]) + as_f16x2(dv[c][k]));
     }
-    if (bad) xv = u32x4{0x7E007E00u, 0x7E007E00u, 0x7E007E00u, 0x7E007E00u};  // fp16 NaN
-    *reinterpret_cast<u32x4*>(xo + i) = xv;
+    if (bad) xv[c] = u32x4{0x7E007E00u, 0x7E007E00u, 0x7E007E00u, 0x7E007E00u};  // fp16 NaN
+    if (u < U) {
+      xo[u] = xv[c];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const f16x2 h = as_f16x2(xv[k]);
-      const float a = (float)h.x, b = (float)h.y;
-      ss = fmaf(a, a, ss);
-      ss = fmaf(b, b, ss);
+      for (int k = 0; k < 4; ++k) {
+        const f16x2 h = as_f16x2(xv[c][k]);
+        const float a = (float)h.x, b = (float)h.y;
+        ss = fmaf(a, a, ss);
+        ss = fmaf(b, b, ss);
+      }
     }
   }
   ss = group_sum<kWave>(ss);
-  if ((tid & 63) == 0) wsum[tid >> 6] = ss;
+  if ((tid & 63) == 0) part[tid >> 6] = ss;
   __syncthreads();
   float tot = 0.f;
-  for (int i = 0; i < (nt >> 6); ++i) tot += wsum[i];
+  for (int i = 0; i < (T >> 6); ++i) tot += part[i];
   const float rr = bad ? __builtin_nanf("") : 1.0f / sqrtf(tot / (float)H + eps);
-  for (int i = tid * 8; i < H; i += nt * 8) {
-    const u32x4 xv = *reinterpret_cast<const u32x4*>(xo + i);  // this thread's own write above
-    const u32x4 wv = *reinterpret_cast<const u32x4*>(w + i);
-    u32x4 o;
+  u32x4* o = reinterpret_cast<u32x4*>(out + (size_t)r * H);
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int u = tid + c * T;
+    if (u >= U) continue;
+    u32x4 ov;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const f16x2 h = as_f16x2(xv[k]);
+      const f16x2 h = as_f16x2(xv[c][k]);
       const f16x2 hn = {(f16)((float)h.x * rr), (f16)((float)h.y * rr)};
-      o[k] = as_u32(as_f16x2(wv[k]) * hn);
+      ov[k] = as_u32(as_f16x2(wv[c][k]) * hn);
     }
-    *reinterpret_cast<u32x4*>(out + (size_t)r * H + i) = o;
+    o[u] = ov;
   }
 }
 
@@ -315,11 +286,22 @@ argmax_split_kernel(const f16* __restrict__ logits, int V, int h, int nc, int64_
 
 }  // namespace
 
+// Chunks per thread: the smallest C in {1, 2, 4, 8} with 1024 C 16-byte chunks covering the row (H <= kRowNormMaxH).
+static void launch_row_norm(const void* x_in, const int64_t* rows, int n_src, const void* delta, const void* w,
+                            void* x_out, void* out, int M, int H, float eps, hipStream_t st) {
+  const int U = H >> 3;
+  int C = 1;
+  while (C < 8 && C * 1024 < U) C *= 2;
+  const int T = min(1024, ((U + C - 1) / C + 63) / 64 * 64);
+  const f16 *xi = (const f16*)x_in, *d = (const f16*)delta, *wn = (const f16*)w;
+  f16 *xo = (f16*)x_out, *o = (f16*)out;
+  auto kernel = C == 1 ? row_norm_kernel<1> : C == 2 ? row_norm_kernel<2> : C == 4 ? row_norm_kernel<4>
+                                                                            : row_norm_kernel<8>;
+  hipLaunchKernelGGL(kernel, dim3(M), dim3(T), 0, st, xi, rows, n_src, d, wn, xo, o, H, eps);
+}
+
 void launch_add_rmsnorm(void* x, const void* delta, const void* w, void* out, int H, float eps, hipStream_t st) {
-  int threads = ((H / 8 + 63) / 64) * 64;
-  if (threads > 1024) threads = 1024;
-  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(1), dim3(threads), 0, st, (f16*)x, (const f16*)delta, (const f16*)w,
-                     (f16*)out, H, eps);
+  launch_row_norm(x, nullptr, 1, delta, w, x, out, 1, H, eps, st);
 }
 
 void launch_swiglu(const void* gu, void* out, int I, hipStream_t st) {
@@ -346,10 +328,7 @@ void launch_rope_append(void* qkv, const float* cos_t, const float* sin_t, const
 
 void launch_rmsnorm_rows(const void* x_in, const int64_t* rows, int n_src, const void* delta, const void* w, void* x_out,
                          void* out, int M, int H, float eps, hipStream_t st) {
-  int threads = ((H / 8 + 63) / 64) * 64;
-  if (threads > 1024) threads = 1024;
-  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(M), dim3(threads), 0, st, (const f16*)x_in, rows, n_src, (const f16*)delta,
-                     (const f16*)w, (f16*)x_out, (f16*)out, H, eps);
+  launch_row_norm(x_in, rows, n_src, delta, w, x_out, out, M, H, eps, st);
 }
 
 void launch_argmax_advance(const void* logits, int V, int64_t* tok, int32_t* pos, hipStream_t st) {

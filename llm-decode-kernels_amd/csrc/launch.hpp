@@ -98,6 +98,8 @@ void launch_attention_prefill(const void* qkv, const int32_t* pos, const int32_t
                               const void* vc, int n_pages, int log2P, int n_q, int n_kv, int head_dim, int M,
                               int max_ctx, void* out, hipStream_t st);
 
+// Residual + RMSNorm with the row in registers: up to 8 16-byte chunks for each of 1024 threads.
+constexpr int kRowNormMaxH = 8 * 8 * 1024;
 void launch_add_rmsnorm(void* x, const void* delta, const void* w, void* out, int H, float eps, hipStream_t st);
 void launch_swiglu(const void* gu, void* out, int I, hipStream_t st);
 // rows > 1: a batch of tokens, row y of qkv [rows, (n_q + 2 n_kv) head_dim] at position *pos + y (prefill)

@@ -217,6 +217,8 @@ def test_gemv_f16_validation(lib):
 
 def test_small_op_validation(lib):
     assert _err(lib, lib.dk_add_rmsnorm(A16, None, A16, A16, 2047, 1e-5, None))[0] == 3
+    rc, m = _err(lib, lib.dk_add_rmsnorm(A16, None, A16, A16, 65544, 1e-5, None))     # past the register-resident row
+    assert rc == 3 and "65536" in m
     assert _err(lib, lib.dk_add_rmsnorm(A16 + 2, None, A16, A16, 2048, 1e-5, None))[0] == 2
     assert _err(lib, lib.dk_add_rmsnorm(A16, A16 + 8, A16, A16, 2048, 1e-5, None))[0] == 2
     assert _err(lib, lib.dk_add_rmsnorm(None, None, A16, A16, 2048, 1e-5, None))[0] == 1
@@ -251,7 +253,8 @@ def test_prefill_validation(lib):
     assert rr(vc=None)[0] == 1 and rr(n_bt=0)[0] == 3
     nr = lambda **kw: _err(lib, lib.dk_rmsnorm_rows(*dict(dict(x=A16, rows=None, ns=4, d=None, w=A16, xo=A16, out=B16,
                                                                M=4, H=2048, eps=1e-5), **kw).values(), None))
-    assert nr(H=2044)[0] == 3 and nr(M=0)[0] == 3 and nr(out=A16)[0] == 4 and nr(d=A16 + 2)[0] == 2
+    assert nr(H=2044)[0] == 3 and nr(H=65544)[0] == 3 and nr(M=0)[0] == 3 and nr(out=A16)[0] == 4
+    assert nr(d=A16 + 2)[0] == 2
     assert nr(rows=A16 + 4)[0] == 2 and nr(rows=A16)[0] == 4 and nr(w=None)[0] == 1
     assert nr(ns=5)[0] == 3 and nr(rows=A16, xo=B16 + 0x1000, ns=0)[0] == 3 and "n_src" in nr(ns=3)[1]
     ap = lambda **kw: _err(lib, lib.dk_attention_prefill(*dict(

@@ -259,7 +259,8 @@ def test_attention_split_buffers_ignored_past_live(K, ver):
 
 
 # ----------------------------------------------------------------------------------------------- fused elementwise
-@pytest.mark.parametrize("H", (2048, 4096, 64))
+# 1, 2, 4 and 8 chunks per thread, partial last chunk rounds (8200, 32776) and the largest row (65536)
+@pytest.mark.parametrize("H", (2048, 4096, 64, 8200, 16384, 32776, 65536))
 def test_add_rmsnorm(K, H):
     g = gen(H)
     w = (1 + 0.1 * torch.randn(H, generator=g)).half()

@@ -115,7 +115,8 @@ def test_rope_append_rows_matches_per_token(K, D, n_q, n_kv, page, start, M, max
 
 
 @pytest.mark.parametrize("M,H,gather,with_delta,inplace", [(9, 2048, True, False, False), (33, 4096, False, True, True),
-                                                          (1, 256, False, True, False), (130, 2048, True, True, False)])
+                                                          (1, 256, False, True, False), (130, 2048, True, True, False),
+                                                          (3, 16384, True, True, False), (2, 65536, False, False, True)])
 def test_rmsnorm_rows_matches_per_row(K, M, H, gather, with_delta, inplace):
     g = gen(M + H)
     src = torch.randn(M + 50 if gather else M, H, generator=g).half().to(DEV)
