@@ -423,7 +423,7 @@ def decode_leg(model, ctx, steps, warmup):
     tok_us = sorted(s.elapsed_time(e) * 1e3 for s, e in per)
     return {"ctx_start": ctx, "steps": steps, "ms_per_step": total_ms / steps, "tok_s": steps / (total_ms / 1e3),
             "median_us": statistics.median(tok_us), "p10_us": tok_us[len(tok_us) // 10],
-            "p90_us": tok_us[(9 * len(tok_us)) // 10], "wall_tok_s": steps / wall}
+            "p90_us": tok_us[(9 * len(tok_us)) // 10], **token_quartiles(tok_us), "wall_tok_s": steps / wall}
 
 
 def decode_8b_leg(ctx=4096, steps=64, warmup=8):
@@ -520,6 +520,15 @@ def gemm_timing(model, lin, M, epilogue, reps=20):
     fl = 2 * M * lin.N * lin.K
     return {"us": round(us, 2), "tflops": round(fl / us / 1e6, 1), "hipblaslt_fp16_us": round(ub, 2),
             "hipblaslt_fp16_tflops": round(fl / ub / 1e6, 1)}
+
+
+def token_quartiles(tok_us):
+    """First and third quartile and the interquartile range of per-token times in us (bench/timing.py:134-138 of the
+    reference reports median + IQR); empty for fewer than two tokens."""
+    if len(tok_us) < 2:
+        return {}
+    q = statistics.quantiles(sorted(tok_us), n=4, method="inclusive")
+    return {"q1_us": q[0], "q3_us": q[2], "iqr_us": q[2] - q[0]}
 
 
 def step_stats(times_s):
@@ -714,6 +723,7 @@ def main():
                    "frac_of_roofline": round(dec["tok_s"] / (HBM_PEAK_GBS * 1e9 / bpt), 4)},
         "decode_ctx2048": {"tok_s": round(dec2k["tok_s"], 2), "median_us": round(dec2k["median_us"], 2),
                            "p10_us": round(dec2k["p10_us"], 2), "p90_us": round(dec2k["p90_us"], 2),
+                           "iqr_us": round(dec2k["iqr_us"], 2),
                            "bytes_per_token": bpt2k,
                            "frac_of_roofline": round(dec2k["tok_s"] / (HBM_PEAK_GBS * 1e9 / bpt2k), 4)},
         "prefill_tinyllama_512": pre,

@@ -51,8 +51,8 @@ class DecodeConfig:
     page: int = 16
     part_size: int = 0
     attn_version: int = 0
-    attn_impl: int = 0             # decode attention kernel: 0 = policy table, 1 = block kernel, 2 = MFMA kernel,
-                                   # 3 = lean MFMA kernel
+    attn_impl: int = 0             # decode attention kernel: 0 = policy table, 1 = block kernel, 3 = lean MFMA
+                                   # kernel (2, a removed MFMA kernel, runs the block kernel)
     gemv_stage: tuple = None
     autotune_path: str = str(PKG / "configs" / "autotune.json")
     attn_policy_path: str = str(PKG / "configs" / "attn_policy.json")
@@ -239,7 +239,6 @@ class Model:
         ent = self._policy_entry(ctx_cap)
         ps = part_size or self.cfg.part_size or ent.get("part_size", 64)
         impl = impl or self.cfg.attn_impl or ent.get("impl", 1)
-        log2p = self.cfg.page.bit_length() - 1
         if impl == 2:
             impl = 1                                # tables written before the MFMA kernel's removal
         lean_max = 256 if self.D == 128 else 512

@@ -34,3 +34,9 @@ def test_read_clocks_parses_starred_levels(tmp_path: pathlib.Path):
     (hw / "temp1_input").write_text("61000\n")
     assert bench.read_clocks(tmp_path) == {"sclk_mhz": 2400, "mclk_mhz": 1900, "temp_c": 61.0}
     assert bench.read_clocks(tmp_path / "absent") == {}
+
+
+def test_token_quartiles():
+    q = bench.token_quartiles([float(v) for v in range(1, 10)])          # 1..9: quartiles 3 and 7 (inclusive method)
+    assert q == {"q1_us": 3.0, "q3_us": 7.0, "iqr_us": 4.0}
+    assert bench.token_quartiles([5.0]) == {}
