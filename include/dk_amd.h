@@ -109,6 +109,24 @@ int dk_gemv_w4a16_qkv_rope(int stage, int R, int warps, int pf, const void* pack
                            int n_bt, int K, int group, void* stream);
 
 /*
+ * y = dequant(W) . x where x is the attention output merged from dk_paged_attention_split's partials inside this
+ * launch: the combine of paged_attention (kernels/paged_attention.cu:368-427, the log-sum-exp merge of the live
+ * splits of each head, x rounded to fp16 as the combine rounds its output) followed by gemv_w4a16 of the o
+ * projection (runtime/model.py:220-222), one launch instead of two. Every workgroup merges all of x (one thread per
+ * 8 values) into LDS while its weight loads are in flight. With at most one live split (or none, max_pos > 0 and
+ * *pos outside [0, max_pos): the RoPE split kernel's skip) x is read from attn, the output the split kernel wrote.
+ * o_part [n_q, max_splits, head_dim], m_part / l_part [n_q, max_splits] fp32; attn [n_q * head_dim] fp16;
+ * ctx = min(*pos + 1, n_bt * page), live splits = min(ceil(ctx / part_size), max_splits). K = n_q * head_dim,
+ * head_dim 64 or 128, max_splits 1..16; stage 4, R and pf as for stage 4, warps = waves per workgroup with
+ * 64 warps >= K / 8 and warps <= 8 (a multiple of ceil(K / 2048)); o_part and attn 16-byte aligned. No single
+ * counterpart in the reference.
+ */
+int dk_gemv_w4a16_attn(int stage, int R, int warps, int pf, const void* packed, const void* sz, const float* o_part,
+                       const float* m_part, const float* l_part, const void* attn, const int32_t* pos, int n_bt,
+                       int page, int part_size, int max_splits, int max_pos, int n_q, int head_dim, void* y, int N,
+                       int K, int group, void* stream);
+
+/*
  * fp16-weight GEMV y[N] = W[N, K] . x[K] (W row-major fp16, fp32 accumulation, fp16 out). Replaces the fp16 LM head's
  * torch.mm(x, W^T) (runtime/model.py:187 of the reference; cuBLAS there, no custom kernel). R rows per tile (1, 2, 4),
  * warps waves per workgroup (0 = 4; 1, 2, 4, 8), 2^pf tiles per wave (pf 0..3). K % 8 == 0, K <= 4096 and
@@ -191,6 +209,18 @@ int dk_paged_attention(int version, const void* q, const void* kc, const void* v
                        const int32_t* pos, int n_q, int n_kv, int head_dim, int page, int n_pages, int n_bt,
                        int part_size, int max_splits, float* o_part, float* m_part, float* l_part, void* out,
                        void* stream);
+
+/*
+ * The first of dk_paged_attention's two kernels alone: the split kernel (same arguments, checks and split rules),
+ * without the combine. With one live split it writes out itself; otherwise out is left as it was and the partials
+ * are for a consumer that merges them, dk_gemv_w4a16_attn. It has no single counterpart in the reference: it is the
+ * paged_attn_partial launch of paged_attention_launch (kernels/paged_attention.cu:429-461), the reference's combine
+ * (:368-427) moving into the o projection that follows in the decode step (runtime/model.py:220-222).
+ */
+int dk_paged_attention_split(int version, const void* q, const void* kc, const void* vc, const int32_t* bt,
+                             const int32_t* pos, int n_q, int n_kv, int head_dim, int page, int n_pages, int n_bt,
+                             int part_size, int max_splits, float* o_part, float* m_part, float* l_part, void* out,
+                             void* stream);
 
 /*
  * dk_paged_attention without caller-provided split buffers, for callers that cannot allocate device memory (code

@@ -1,5 +1,5 @@
-// Decode-attention helpers shared by the split kernels and the persistent decode step: split count, RoPE of a
-// 16-byte slice, and the 16 x 16 f16 MFMA tile helpers.
+// Decode-attention helpers shared by the split kernels, the prefill kernel and the o projection's combine prologue:
+// split count, RoPE of a 16-byte slice, and the 16 x 16 f16 MFMA tile helpers.
 #pragma once
 #include "common.hpp"
 

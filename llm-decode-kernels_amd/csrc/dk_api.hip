@@ -299,10 +299,10 @@ int check_paged_attention(int version, const void* q, const void* kc, const void
 void launch_reference_attention(int version, const void* q, const void* kc, const void* vc, const int32_t* bt,
                                 const int32_t* pos, int n_q, int n_kv, int head_dim, int page, int n_pages, int n_bt,
                                 int part_size, int max_splits, float* o_part, float* m_part, float* l_part,
-                                void* out, void* stream) {
+                                void* out, void* stream, bool split_only = false) {
   const dk::AttnLaunch a{q, nullptr, nullptr, 0, pos, bt, n_bt, const_cast<void*>(kc), const_cast<void*>(vc), n_pages,
                          ilog2(page), n_q, n_kv, head_dim, part_size, max_splits, o_part, m_part, l_part, out,
-                         version == 5 ? 3 : 1};
+                         version == 5 ? 3 : 1, split_only};
   dk::launch_paged_attention(a, (hipStream_t)stream);
 }
 
@@ -354,6 +354,55 @@ int dk_paged_attention(int version, const void* q, const void* kc, const void* v
   launch_reference_attention(version, q, kc, vc, bt, pos, n_q, n_kv, head_dim, page, n_pages, n_bt, part_size,
                              max_splits, o_part, m_part, l_part, out, stream);
   return launched("paged_attention");
+}
+
+int dk_paged_attention_split(int version, const void* q, const void* kc, const void* vc, const int32_t* bt,
+                             const int32_t* pos, int n_q, int n_kv, int head_dim, int page, int n_pages, int n_bt,
+                             int part_size, int max_splits, float* o_part, float* m_part, float* l_part, void* out,
+                             void* stream) {
+  if (!o_part || !m_part || !l_part) return fail(DK_ERR_NULL, "paged_attention_split: null pointer argument");
+  const int rc = check_paged_attention(version, q, kc, vc, bt, pos, n_q, n_kv, head_dim, page, n_pages, n_bt,
+                                       part_size, max_splits, out);
+  if (rc != DK_OK) return rc;
+  if (!aligned16(o_part)) return fail(DK_ERR_ALIGN, "o_part must be 16B aligned");
+  clear_error();
+  launch_reference_attention(version, q, kc, vc, bt, pos, n_q, n_kv, head_dim, page, n_pages, n_bt, part_size,
+                             max_splits, o_part, m_part, l_part, out, stream, true);
+  return launched("paged_attention_split");
+}
+
+int dk_gemv_w4a16_attn(int stage, int R, int warps, int pf, const void* packed, const void* sz, const float* o_part,
+                       const float* m_part, const float* l_part, const void* attn, const int32_t* pos, int n_bt,
+                       int page, int part_size, int max_splits, int max_pos, int n_q, int head_dim, void* y, int N,
+                       int K, int group, void* stream) {
+  const int rc = check_fused_gemv("gemv_w4a16_attn", stage, R, warps, pf, packed, sz, N, K, group);
+  if (rc != DK_OK) return rc;
+  if (!o_part || !m_part || !l_part || !attn || !pos || !y)
+    return fail(DK_ERR_NULL, "gemv_w4a16_attn: null pointer argument");
+  if (head_dim != 64 && head_dim != 128)
+    return fail(DK_ERR_SHAPE, "gemv_w4a16_attn: head_dim must be 64 or 128, got %d", head_dim);
+  if (n_q <= 0 || (long long)n_q * head_dim != K)
+    return fail(DK_ERR_SHAPE, "gemv_w4a16_attn: K must be n_q * head_dim (K=%d n_q=%d head_dim=%d)", K, n_q,
+                head_dim);
+  if (max_splits < 1 || max_splits > dk::kGemvCombineMaxSplits)
+    return fail(DK_ERR_SHAPE, "gemv_w4a16_attn: max_splits must be 1..%d, got %d", dk::kGemvCombineMaxSplits,
+                max_splits);
+  if (part_size <= 0) return fail(DK_ERR_DOMAIN, "gemv_w4a16_attn: part_size must be > 0");
+  if (!pow2(page)) return fail(DK_ERR_DOMAIN, "gemv_w4a16_attn: page size must be a power of two, got %d", page);
+  if (n_bt < 1 || ((long long)n_bt << ilog2(page)) > (1ll << 30))
+    return fail(DK_ERR_SHAPE, "gemv_w4a16_attn: n_bt must be >= 1 with n_bt * page <= 2^30, got %d", n_bt);
+  if (max_pos < 0) return fail(DK_ERR_DOMAIN, "gemv_w4a16_attn: max_pos must be >= 0 (0 = no range check)");
+  if (warps * 64 < K / 8 || warps > dk::kGemvCombineMaxWarps)
+    return fail(DK_ERR_SHAPE, "gemv_w4a16_attn: the workgroup needs one thread per 8 values of x and at most %d "
+                "waves: warps %d..%d for K=%d, got %d", dk::kGemvCombineMaxWarps, (K / 8 + 63) / 64,
+                dk::kGemvCombineMaxWarps, K, warps);
+  if (!aligned16(o_part) || !aligned16(attn)) return fail(DK_ERR_ALIGN, "o_part and attn must be 16B aligned");
+  dk::GemvInput in{};
+  in.comb = dk::GemvCombine{o_part, m_part, l_part, attn, pos, n_bt << ilog2(page), part_size, max_splits, max_pos,
+                            ilog2(head_dim)};
+  clear_error();
+  dk::launch_gemv_w4a16_fused(2, 0, R, warps, pf, packed, sz, in, y, N, K, ilog2(group), (hipStream_t)stream);
+  return launched("gemv_w4a16_attn");
 }
 
 size_t dk_paged_attention_noalloc_bytes(int n_q, int head_dim, int max_splits) {

@@ -32,6 +32,7 @@
 //                               computed; x is read once per workgroup, row sums by DPP within waves, LDS across.
 // The compiler's scheduler, left alone, issues only two of a tile's weight loads before it starts computing (it keeps
 // register pressure low); __builtin_amdgcn_sched_barrier pins every load of a step ahead of its arithmetic.
+#include "attn_common.hpp"
 #include "common.hpp"
 #include "launch.hpp"
 #include "w4_common.hpp"
@@ -287,7 +288,9 @@ __device__ __forceinline__ void tile_rows(const u32x4 (&w)[T], const uint32_t (&
 // Split in two: tile_input_load issues the operand loads and tile_input_finish computes the operand. The loads are
 // issued before any weight load of the workgroup: a wave's vector loads return in issue order, so operand loads
 // issued after the weights would wait behind an HBM round trip and hold back the prologue and the next tile's loads.
-enum { kInPlain = 0, kInRmsNorm = 1 };
+enum { kInPlain = 0, kInRmsNorm = 1, kInCombine4 = 2, kInCombine8 = 3, kInCombine16 = 4 };
+constexpr bool is_combine(int pro) { return pro >= kInCombine4; }
+constexpr int combine_splits(int pro) { return pro == kInCombine4 ? 4 : pro == kInCombine8 ? 8 : 16; }
 
 struct TileRaw {
   u32x4 a[4];  // x / residual
@@ -372,6 +375,76 @@ __device__ __forceinline__ void tile_input_finish(const GemvInput& in, TileRaw& 
   }
 }
 
+// The attention-combine operand (prologues kInCombine4/8/16, MS = 4, 8 or 16 >= max_splits): the o projection
+// merges the split kernel's partials itself instead of a separate combine launch (the log-sum-exp merge of
+// kernels/paged_attention.cu:368-427). Thread t of the workgroup takes the 8 values 8t .. 8t + 8 of x (head h, dims
+// d0 .. d0 + 8): x = sum_s w_s o_s / sum_s w_s l_s with w_s = e^(m_s - M), M the largest live m_s; with at most one
+// live split (or none, when the RoPE split kernel skipped an out-of-range position) x is the attention output the
+// split kernel wrote itself. The loads of all max_splits splits (<= MS) go out before the position is known, then
+// splits past the live count are dropped by select. The workgroup leaves x in LDS; each lane then
+// reads its 32-value column from there.
+template <int MS>
+struct CombineRaw {
+  float4 o[MS][2];
+  float m[MS], l[MS];
+  u32x4 a;
+};
+
+template <int MS>
+__device__ __forceinline__ void combine_load(const GemvCombine& c, int K, CombineRaw<MS>& raw) {
+  const int chunk = min((int)threadIdx.x, (K >> 3) - 1);
+  const int D = 1 << c.log2D;
+  const int h = (chunk << 3) >> c.log2D, d0 = (chunk << 3) & (D - 1);
+  const size_t hb = (size_t)h * c.max_splits;
+#pragma unroll
+  for (int s = 0; s < MS; ++s) {
+    raw.o[s][0] = raw.o[s][1] = float4{0.f, 0.f, 0.f, 0.f};
+    raw.m[s] = -INFINITY;
+    raw.l[s] = 0.f;
+    if (s < c.max_splits) {  // uniform: no load for the batch's slots past the buffer's splits
+      const size_t hs = hb + s;
+      const float4* op = reinterpret_cast<const float4*>(c.o_part + hs * D + d0);
+      raw.o[s][0] = op[0];
+      raw.o[s][1] = op[1];
+      raw.m[s] = c.m_part[hs];
+      raw.l[s] = c.l_part[hs];
+    }
+  }
+  raw.a = reinterpret_cast<const u32x4*>(c.attn)[chunk];
+}
+
+template <int MS>
+__device__ __forceinline__ void combine_finish(const GemvCombine& c, const CombineRaw<MS>& raw, int pos, int K,
+                                               u32x4* xs) {
+  const bool skip = c.max_pos > 0 && (pos < 0 || pos >= c.max_pos);
+  const int ctx = (int)min((long long)pos + 1, (long long)c.cap);
+  const int nsplit = skip ? 0 : attn_splits(ctx, c.part_size, c.max_splits);
+  u32x4 xv = raw.a;
+  if (nsplit > 1) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < MS; ++s) M = s < nsplit ? fmaxf(M, raw.m[s]) : M;
+    float L = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < MS; ++s) {
+      // splits past the live count are replaced, not weighted by 0: their partials are stale or were never written
+      // (0 * NaN would poison the sums)
+      const bool on = s < nsplit;
+      const float ms = on ? raw.m[s] : -INFINITY;
+      const float w = ms == -INFINITY ? 0.f : __expf(ms - M);
+      L = fmaf(w, on ? raw.l[s] : 0.f, L);
+      const float v[8] = {raw.o[s][0].x, raw.o[s][0].y, raw.o[s][0].z, raw.o[s][0].w,
+                          raw.o[s][1].x, raw.o[s][1].y, raw.o[s][1].z, raw.o[s][1].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = fmaf(w, on ? v[e] : 0.f, acc[e]);
+    }
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xv[k] = as_u32(f16x2{(f16)(acc[2 * k] * inv), (f16)(acc[2 * k + 1] * inv)});
+  }
+  if ((int)threadIdx.x < (K >> 3)) xs[threadIdx.x] = xv;
+}
+
 // The output of the row-tile kernel:
 //   kOutRows    y[n] = fp16(row sum n)                                      (y has N entries)
 //   kOutSwiglu  the rows are interleaved gate / up pairs (row 2i = gate_i, row 2i + 1 = up_i) and
@@ -406,12 +479,14 @@ constexpr int kTileDepth = DK_TILE_DEPTH;  // weight tiles in flight per workgro
 // workgroup's g-th run of T * NT rows): at small K a group is one wave, and several groups per workgroup cost fewer
 // workgroup dispatches than one single-wave workgroup per row tile.
 template <int T, int NT, int PRO, int EPI>
-__global__ void __launch_bounds__(1024)
+__global__ void __launch_bounds__(is_combine(PRO) ? 64 * kGemvCombineMaxWarps : 1024)
 gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, const GemvInput in,
                 f16* __restrict__ y, int N, int U, int gsh) {
   static_assert(EPI == kOutRows || (T * NT) % 2 == 0, "gate/up and rotation pairs need an even row tile");
+  static_assert(!is_combine(PRO) || EPI == kOutRows, "the combine prologue feeds the plain epilogue");
   __shared__ float red[16][T * NT];
   __shared__ float s_ss[16];
+  __shared__ u32x4 xs[is_combine(PRO) ? kGemvCombineMaxWarps * 64 : 1];   // combine: x, 8 values per thread
   const int nw = (U + kWave - 1) / kWave;  // waves of one row group
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int grp = wave / nw, gw0 = grp * nw;    // row group, its first wave
@@ -423,9 +498,15 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
   const int NG = U >> gsh;
   int rpos = -1;
   if constexpr (EPI == kOutRope) rpos = *in.rope.pos;
+  int cpos = 0;
+  if constexpr (is_combine(PRO)) cpos = *in.comb.pos;
 
   TileRaw raw;
-  tile_input_load<PRO>(in, uc, U << 5, raw);
+  CombineRaw<is_combine(PRO) ? combine_splits(PRO) : 1> craw;
+  if constexpr (is_combine(PRO))
+    combine_load(in.comb, U << 5, craw);
+  else
+    tile_input_load<PRO>(in, uc, U << 5, raw);
   constexpr int DP = NT < kTileDepth ? NT : kTileDepth;  // tiles in flight
   u32x4 w[DP][T];
   uint32_t sz[DP][T];
@@ -433,7 +514,14 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
   for (int d = 0; d < DP; ++d) tile_issue<T>(W, SZ, base + d * T, N, U, NG, uc, gsh, w[d], sz[d]);
   __builtin_amdgcn_sched_barrier(0);
   u32x4 xc[4];
-  tile_input_finish<PRO>(in, raw, uc, live, U << 5, s_ss, wave, gw0, nw, blockIdx.x == 0 && grp == 0, xc);
+  if constexpr (is_combine(PRO)) {
+    combine_finish(in.comb, craw, cpos, U << 5, xs);
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) xc[k] = live ? xs[4 * uc + k] : u32x4{0u, 0u, 0u, 0u};
+  } else {
+    tile_input_finish<PRO>(in, raw, uc, live, U << 5, s_ss, wave, gw0, nw, blockIdx.x == 0 && grp == 0, xc);
+  }
   const ColumnSums cs = column_sums(xc);
   const NibbleMasks m = nibble_masks();
   // rotation-pair operands of the RoPE epilogue, requested before the tiles are computed
@@ -654,6 +742,16 @@ void launch_gemv_w4a16_fused(int prologue, int epilogue, int R, int warps, int p
       launch_tile_r<kInRmsNorm, kOutRope>(R, warps, pf, packed, sz, in, y, N, K, log2G, st);
     else
       launch_tile_r<kInPlain, kOutRope>(R, warps, pf, packed, sz, in, y, N, K, log2G, st);
+    return;
+  }
+  if (prologue == 2) {
+    const int ms = in.comb.max_splits;
+    if (ms <= 4)
+      launch_tile_r<kInCombine4>(R, warps, pf, packed, sz, in, y, N, K, log2G, st);
+    else if (ms <= 8)
+      launch_tile_r<kInCombine8>(R, warps, pf, packed, sz, in, y, N, K, log2G, st);
+    else
+      launch_tile_r<kInCombine16>(R, warps, pf, packed, sz, in, y, N, K, log2G, st);
     return;
   }
   launch_tile_r<kInRmsNorm>(R, warps, pf, packed, sz, in, y, N, K, log2G, st);

@@ -27,6 +27,20 @@ struct GemvRope {
   void* vc;
   int n_q, n_kv, log2D, log2P, max_pos, n_pages, n_bt;
 };
+// The attention-combine prologue of the o projection: the split kernel's partials, merged into x by every workgroup
+// (the arguments of the reference's combine, kernels/paged_attention.cu:368-427, plus the attention output the split
+// kernel writes itself when a single split is live).
+struct GemvCombine {
+  const float* o_part;    // [n_q, max_splits, D] unnormalised split outputs
+  const float* m_part;    // [n_q, max_splits] split maxima
+  const float* l_part;    // [n_q, max_splits] split sums
+  const void* attn;       // [n_q * D] fp16: the output when at most one split is live
+  const int32_t* pos;     // device position: ctx = min(pos + 1, cap)
+  int cap;                // n_bt << log2(page)
+  int part_size, max_splits;
+  int max_pos;            // > 0: the RoPE split kernel's range check (pos outside [0, max_pos): nothing was written)
+  int log2D;
+};
 struct GemvInput {
   const void* x;          // plain: the input vector; rmsnorm: the residual stream (or the embedding table)
   const int64_t* row;     // rmsnorm: device row index into x (embedding gather) or null
@@ -35,9 +49,14 @@ struct GemvInput {
   float eps;
   void* x_out;            // rmsnorm: receives x + delta (written by workgroup 0) or null
   GemvRope rope;          // epilogue 2 only
+  GemvCombine comb;       // prologue 2 only
 };
 // epilogue 0 = one fp16 output per row, 1 = SwiGLU of interleaved gate / up row pairs (N / 2 outputs), 2 = RoPE +
 // KV append of rotation-pair rows (qkv rows stored per head as j, j + D/2 for j < D/2; N outputs in head order).
+// prologue 2 = the attention combine (GemvCombine; epilogue 0 only): the workgroup needs one thread per 8 values of
+// x (64 warps >= K / 8, warps <= kGemvCombineMaxWarps) and max_splits <= kGemvCombineMaxSplits.
+constexpr int kGemvCombineMaxSplits = 16;
+constexpr int kGemvCombineMaxWarps = 8;
 void launch_gemv_w4a16_fused(int prologue, int epilogue, int R, int warps, int pf, const void* packed, const void* sz,
                              const GemvInput& in, void* y, int N, int K, int log2G, hipStream_t st);
 // Default configuration for a shape: (stage, R, waves, pf).
@@ -77,6 +96,7 @@ struct AttnLaunch {
   float* l_part;
   void* out;
   int impl;            // 0 or 1 = block kernel; 3 = lean MFMA kernel
+  bool split_only;     // the split kernel alone: the consumer merges the partials (gemv prologue 2)
 };
 // The lean MFMA kernel: pages of at least 16 tokens, splits of whole 16-token tiles, at most 8 waves x 4 tiles (x 2
 // tiles at head_dim 128, whose RoPE variant would not fit 4 tiles in registers).

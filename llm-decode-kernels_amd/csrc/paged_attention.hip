@@ -725,14 +725,14 @@ void launch_attn(const AttnLaunch& a, hipStream_t st) {
   const float scale = 1.0f / sqrtf((float)D);
   if (attn_use_lean(a)) {
     launch_lean_any<D, HPG, ROPE>(a, st);
-    if (a.max_splits > 1) launch_combine<D>(a, ROPE, st);
+    if (a.max_splits > 1 && !a.split_only) launch_combine<D>(a, ROPE, st);
     return;
   }
   hipLaunchKernelGGL((attn_decode_kernel<D, HPG, ROPE>), dim3(a.n_kv, a.max_splits), dim3(kAttnThreads), 0,
                      st, (const f16*)a.q, a.cos_t, a.sin_t, a.max_pos, a.pos, a.bt, a.n_bt, (f16*)a.kc, (f16*)a.vc,
                      a.n_pages, a.log2P, a.n_q, a.n_kv, a.part_size, a.max_splits, scale, a.o_part, a.m_part,
                      a.l_part, (f16*)a.out);
-  if (a.max_splits > 1) launch_combine<D>(a, ROPE, st);
+  if (a.max_splits > 1 && !a.split_only) launch_combine<D>(a, ROPE, st);
 }
 
 template <int D, bool ROPE>

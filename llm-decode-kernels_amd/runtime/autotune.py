@@ -72,6 +72,14 @@ def tile_candidates(K):
     return out
 
 
+def attn_candidates(K):
+    """stage-4 configurations of the o projection with the attention combine in its prologue: one thread per 8
+    values of x, so at least ceil(K / 512) waves (a multiple of ceil(K / 2048)) and at most 8."""
+    tw = -(-K // 2048)
+    need = -(-max(-(-K // 512), tw) // tw) * tw
+    return [(4, R, w, pf) for w in sorted({need, 2 * need}) if w <= 8 for R in (1, 2, 4) for pf in range(3)]
+
+
 def fused_candidates(kind, K):
     """stage-4 configurations of the fused INT4 GEMVs (the gate|up SwiGLU epilogue needs an even row tile; so does
     the qkv RoPE epilogue, which takes the same candidates)."""
@@ -313,13 +321,16 @@ STEP_MODELS = {"tinyllama": ("TINYLLAMA", "fp16", 512), "llama3_8b": ("LLAMA3_8B
 def step_slots(model):
     """The GEMV launches of one decode step that the in-step tuner varies: (table kind, projection, candidates).
     Kinds: "norm" (qkv behind the fused residual + RMSNorm), "rope" (the same qkv launch with the RoPE + append
-    epilogue, whose row tile must hold a rotation pair), "plain" (o, down; the INT4 head when the norm does not pay
-    inside it), "gate_up" (gate|up with the SwiGLU epilogue), "f16_norm" (the fp16 head behind the final norm)."""
+    epilogue, whose row tile must hold a rotation pair), "attn" (o with the attention combine in its prologue),
+    "plain" (o, down; the INT4 head when the norm does not pay inside it), "gate_up" (gate|up with the SwiGLU
+    epilogue), "f16_norm" (the fp16 head behind the final norm)."""
     lw = model.layers[0]
     K = lambda lin: lin.K
     qkv = (("rope", lw["qkv"], fused_candidates("gate_up", K(lw["qkv"]))) if model.rope_epilogue
            else ("norm", lw["qkv"], fused_candidates("rmsnorm", K(lw["qkv"]))))
-    slots = [qkv, ("plain", lw["o"], fused_candidates("rmsnorm", K(lw["o"]))),
+    o = (("attn", lw["o"], attn_candidates(K(lw["o"]))) if model.attn_in_o
+         else ("plain", lw["o"], fused_candidates("rmsnorm", K(lw["o"]))))
+    slots = [qkv, o,
              ("gate_up", lw["gu"], fused_candidates("gate_up", K(lw["gu"]))),
              ("plain", lw["down"], fused_candidates("rmsnorm", K(lw["down"])))]
     head = model.lm_head
@@ -353,7 +364,7 @@ def tune_step(models=("tinyllama", "llama3_8b"), path=CONFIG, rounds=2, log=prin
                 key = model.step_key(kind, lin)
                 cur = model.step_cfg_override.pop(key, None)
                 isolated = {"plain": model.gemv_cfg, "norm": model.gemv_norm_cfg, "gate_up": model.gemv_gate_up_cfg,
-                            "rope": model.qkv_rope_cfg,
+                            "rope": model.qkv_rope_cfg, "attn": model.gemv_attn_cfg,
                             "f16_norm": lambda l: model.gemv_f16_cfg(l, norm=True)}[kind](lin)
                 cands = list(dict.fromkeys([tuple(c) for c in cands] + [tuple(isolated)]))
                 times = {}

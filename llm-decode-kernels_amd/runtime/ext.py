@@ -27,6 +27,8 @@ SIGNATURES = {
     "dk_gemv_w4a16_gate_up": ([_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _F, _P, _P, _I, _I, _I, _P], _I),
     "dk_gemv_w4a16_qkv_rope": ([_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I,
                                 _I, _I, _I, _I, _I, _I, _I, _P], _I),
+    "dk_gemv_w4a16_attn": ([_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _I, _I, _I,
+                            _P], _I),
     "dk_gemv_f16": ([_I, _I, _I, _P, _P, _P, _I, _I, _P], _I),
     "dk_gemv_f16_rmsnorm": ([_I, _I, _I, _P, _P, _P, _P, _F, _P, _P, _I, _I, _P], _I),
     "dk_gemm_w4a16": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _P], _I),
@@ -35,6 +37,7 @@ SIGNATURES = {
     "dk_attention_prefill": ([_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P], _I),
     "dk_bw_read": ([_P, _Z, _P, _I, _I, _I, _P], _I),
     "dk_paged_attention": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
+    "dk_paged_attention_split": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
     "dk_paged_attention_noalloc": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P], _I),
     "dk_paged_attention_noalloc_bytes": ([_I, _I, _I], _Z),
     "dk_attention_decode": ([_P, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P],
@@ -316,8 +319,8 @@ class DecodeKernels:
         self._call(self.lib.dk_bw_read, buf.data_ptr(), buf.numel() * buf.element_size(), sink.data_ptr(),
                    int(blocks), int(threads), int(unroll), _stream(buf))
 
-    # kernels/bindings.cpp:45-62 (head_dim generalised from 64 to {64, 128})
-    def paged_attention(self, q, kc, vc, bt, pos, part_size, o_part, m_part, l_part, out, version=2):
+    # the checks of kernels/bindings.cpp:45-62 (head_dim generalised from 64 to {64, 128}) -> C arguments
+    def _attention_args(self, q, kc, vc, bt, pos, part_size, o_part, m_part, l_part, out, version):
         for t, n in ((q, "q"), (kc, "kc"), (vc, "vc"), (bt, "bt"), (pos, "pos"), (out, "out"),
                      (o_part, "o_part"), (m_part, "m_part"), (l_part, "l_part")):
             _check_cuda(t, n)
@@ -341,9 +344,44 @@ class DecodeKernels:
         if not (o_part.size(0) == n_q and o_part.size(2) == D and m_part.size(0) == n_q and l_part.size(0) == n_q
                 and m_part.size(1) == max_splits and l_part.size(1) == max_splits and out.numel() == n_q * D):
             raise RuntimeError("paged_attention: split buffers must be o [n_q, S, D], m/l [n_q, S], out [n_q, D]")
-        self._call(self.lib.dk_paged_attention, int(version), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
-                   bt.data_ptr(), pos.data_ptr(), n_q, n_kv, D, P, kc.size(0), bt.numel(), int(part_size),
-                   max_splits, o_part.data_ptr(), m_part.data_ptr(), l_part.data_ptr(), out.data_ptr(), _stream(q))
+        return (int(version), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(), pos.data_ptr(), n_q, n_kv, D,
+                P, kc.size(0), bt.numel(), int(part_size), max_splits, o_part.data_ptr(), m_part.data_ptr(),
+                l_part.data_ptr(), out.data_ptr(), _stream(q))
+
+    # kernels/bindings.cpp:45-62 (head_dim generalised from 64 to {64, 128})
+    def paged_attention(self, q, kc, vc, bt, pos, part_size, o_part, m_part, l_part, out, version=2):
+        self._call(self.lib.dk_paged_attention,
+                   *self._attention_args(q, kc, vc, bt, pos, part_size, o_part, m_part, l_part, out, version))
+
+    # paged_attention's split kernel alone (no combine): with one live split it writes out, otherwise the partials
+    # are left for gemv_w4a16_attn, the o projection that merges them in its prologue
+    def paged_attention_split(self, q, kc, vc, bt, pos, part_size, o_part, m_part, l_part, out, version=5):
+        self._call(self.lib.dk_paged_attention_split,
+                   *self._attention_args(q, kc, vc, bt, pos, part_size, o_part, m_part, l_part, out, version))
+
+    # the combine of paged_attention (kernels/paged_attention.cu:368-427) fused as the x prologue of gemv_w4a16 (the
+    # o projection, runtime/model.py:220-222): y = W . combine(o_part, m_part, l_part), or W . attn with one live split
+    def gemv_w4a16_attn(self, stage, R, warps, pf, packed, sz, o_part, m_part, l_part, attn, pos, bt, page, part_size,
+                        max_pos, y, group):
+        for t, n in ((packed, "packed"), (sz, "sz"), (o_part, "o_part"), (m_part, "m_part"), (l_part, "l_part"),
+                     (attn, "attn"), (pos, "pos"), (bt, "bt"), (y, "y")):
+            _check_cuda(t, n)
+        for t, n in ((o_part, "o_part"), (m_part, "m_part"), (l_part, "l_part")):
+            _check_dtype(t, torch.float32, n)
+        _check_dtype(attn, torch.float16, "attn")
+        if pos.dtype != torch.int32 or bt.dtype != torch.int32:
+            raise RuntimeError("pos and bt must be int32")
+        if o_part.dim() != 3:
+            raise RuntimeError("gemv_w4a16_attn: o_part must be [n_q, S, D]")
+        n_q, S, D = o_part.shape
+        if m_part.shape != (n_q, S) or l_part.shape != (n_q, S) or attn.numel() != n_q * D:
+            raise RuntimeError("gemv_w4a16_attn: split buffers must be o [n_q, S, D], m/l [n_q, S], attn [n_q * D]")
+        K = n_q * D
+        N = self._gemv_shape(packed, sz, y, K, group)
+        self._call(self.lib.dk_gemv_w4a16_attn, int(stage), int(R), int(warps), int(pf), packed.data_ptr(),
+                   sz.data_ptr(), o_part.data_ptr(), m_part.data_ptr(), l_part.data_ptr(), attn.data_ptr(),
+                   pos.data_ptr(), bt.numel(), int(page), int(part_size), S, int(max_pos), n_q, D, y.data_ptr(), N, K,
+                   int(group), _stream(y))
 
     # paged_attention with its split partials in the library's per-device scratch array (no caller buffers, no
     # allocation); calls that overlap on one GPU race

@@ -71,6 +71,10 @@ class DecodeConfig:
                                    # (dk_gemv_w4a16_qkv_rope over a rotation-pair copy of the qkv rows) and attention
                                    # without RoPE (dk_paged_attention) instead of dk_attention_decode; on MI355X
                                    # 1410 -> 1349 us per Llama-3-8B token at context 4096, unchanged on TinyLlama
+    combine_in_o: bool = True      # with rope_epilogue: attention's split kernel alone (dk_paged_attention_split) and
+                                   # its log-sum-exp combine merged by the o projection (dk_gemv_w4a16_attn) instead
+                                   # of a combine launch, while every o workgroup's partials (splits x n_q x D fp32)
+                                   # stay within Model.COMBINE_MAX_BYTES
     swiglu: str = "epilogue"       # where SwiGLU runs when fused_gemv is on: "epilogue" = inside the gate|up GEMV
                                    # (dk_gemv_w4a16_gate_up, gate/up rows stored interleaved); "kernel" = the separate
                                    # dk_swiglu launch
@@ -246,6 +250,11 @@ class Model:
             impl = 1                                # the lean kernel takes whole 16-token tiles of one page
         splits = -(-ctx_cap // ps)
         self.attn_impl, self.part_size, self.max_splits, self.ctx_cap = impl, ps, max(1, splits), max(1, splits) * ps
+        # the o projection merges the split partials itself (one thread per 8 values of x, at most 8 waves) while
+        # the partials one of its workgroups reads (every split of all of x) stay small
+        self.attn_in_o = (self.cfg.combine_in_o and self.rope_epilogue and self.layers[0]["o"].quant
+                          and self.max_splits <= self.COMBINE_MAX_SPLITS and self.n_q * self.D <= 4096
+                          and self.max_splits * self.n_q * self.D * 4 <= self.COMBINE_MAX_BYTES)
         dev = self.cfg.device
         self.o_part, self.m_part, self.l_part = (
             torch.empty(*shape, dtype=torch.float32, device=dev)
@@ -310,6 +319,19 @@ class Model:
 
     # in-graph time of the separate add_rmsnorm launch at hidden 2048-4096 on MI355X (decode-step kernel trace)
     ADD_RMSNORM_US = 2.5
+    COMBINE_MAX_SPLITS = 16            # dk_gemv_w4a16_attn merges at most this many splits
+    # partial bytes per o workgroup up to which the merge pays on MI355X: TinyLlama ctx 512, part 128 (5 splits, 40 KB)
+    # 530 -> 504 us per step; Llama-3-8B ctx 1024, part 128 (9 splits, 144 KB) 1266 -> 1528
+    COMBINE_MAX_BYTES = 64 << 10
+
+    def gemv_attn_cfg(self, lin):
+        """Configuration of the o projection with the attention combine in its prologue: its in-step entry ("attn:"
+        key), else 1-row tiles, 2 per row group, and the fewest waves that give every 8 values of x a thread."""
+        tw = -(-lin.K // 2048)
+        need = -(-max(-(-lin.K // 512), tw) // tw) * tw
+        e = self.step_cfg_override.get(self.step_key("attn", lin))
+        s, r, wv, pf = tuple(e) if e is not None else (4, 1, need, 1)
+        return 4, r, max(wv, need), pf
 
     def norm_fusion_pays(self, lin):
         """Whether the residual + RMSNorm should run inside this INT4 GEMV: the tuned fused time against the tuned
@@ -413,6 +435,10 @@ class Model:
         kc, vc = self.kv[li, 0], self.kv[li, 1]
         if self.rope_epilogue:  # q rotated and k, v appended by the qkv GEMV
             version = 5 if self.attn_impl == 3 else 2
+            if self.attn_in_o:  # the o projection merges the partials
+                self.K.paged_attention_split(self.qkv[: self.n_q * self.D], kc, vc, self.bt, self.pos,
+                                             self.part_size, self.o_part, self.m_part, self.l_part, self.attn, version)
+                return
             self.K.paged_attention(self.qkv[: self.n_q * self.D], kc, vc, self.bt, self.pos, self.part_size,
                                    self.o_part, self.m_part, self.l_part, self.attn, version)
             return
@@ -449,7 +475,8 @@ class Model:
     def step_fused(self):
         """The same composition with every residual + RMSNorm inside the GEMV that consumes it (the layer-0 one also
         gathers the embedding row of the device token) and, by default, SwiGLU in the gate|up GEMV's epilogue: per
-        layer qkv, attention (split + combine), o, gate|up, down = 6 launches. The residual stream alternates between
+        layer qkv, attention (split + combine), o, gate|up, down = 6 launches, 5 when the o projection merges the
+        attention's split partials itself (attn_in_o). The residual stream alternates between
         two buffers because a fused GEMV's workgroups all read x_in while workgroup 0 writes x_in + delta."""
         cur, nxt = self.x, self.x_alt
         delta = None
@@ -463,7 +490,13 @@ class Model:
                 self.K.add_rmsnorm(cur, delta, lw["ln1"], self.normed, self.eps)
                 self.qkv_proj(lw["qkv"], li, self.normed, None, None, None)
             self.attention(li)
-            self.linear(lw["o"], self.attn.view(-1), self.o)
+            if self.attn_in_o:
+                s, r, wv, pf = self.gemv_attn_cfg(lw["o"])
+                self.K.gemv_w4a16_attn(s, r, wv, pf, lw["o"].packed, lw["o"].sz, self.o_part, self.m_part,
+                                       self.l_part, self.attn, self.pos, self.bt, self.cfg.page, self.part_size, 0,
+                                       self.o, self.cfg.group)
+            else:
+                self.linear(lw["o"], self.attn.view(-1), self.o)
             if self.gate_up_epilogue:
                 self.linear_gate_up(lw["gu"], cur, self.o, lw["ln2"], nxt, self.act)
                 cur, nxt = nxt, cur

@@ -106,6 +106,41 @@ def _attn(lib, **kw):
 def test_attention_validation(lib, kw, code, msg):
     rc, m = _attn(lib, **kw)
     assert rc == code and msg in m, (rc, m)
+    # the split kernel alone checks exactly what paged_attention checks
+    a = dict(version=2, q=A16, kc=A16, vc=A16, bt=A16, pos=A16, n_q=32, n_kv=4, head_dim=64, page=16, n_pages=8,
+             n_bt=8, part_size=64, max_splits=4, o=A16, m=A16, l=A16, out=A16)
+    a.update(kw)
+    rs, ms = _err(lib, lib.dk_paged_attention_split(*a.values(), None))
+    assert rs == code and msg in ms, (rs, ms)
+
+
+def _gemv_attn(lib, **kw):
+    a = dict(stage=4, R=1, warps=4, pf=1, packed=A16, sz=A16, o=A16, m=A16, l=A16, attn=A16, pos=A16, n_bt=8, page=16,
+             part_size=64, max_splits=5, max_pos=0, n_q=32, head_dim=64, y=B16, N=2048, K=2048, group=128)
+    a.update(kw)
+    return _err(lib, lib.dk_gemv_w4a16_attn(*a.values(), None))
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(stage=2), 4, "stage 4 only"),
+    (dict(K=1024), 3, "K must be n_q * head_dim"),
+    (dict(head_dim=96, K=3072), 3, "head_dim"),
+    (dict(max_splits=17), 3, "max_splits must be 1..16"),
+    (dict(max_splits=0), 3, "max_splits must be 1..16"),
+    (dict(warps=2), 3, "one thread per 8 values of x"),                  # 128 threads for 256 chunks
+    (dict(warps=16), 3, "at most 8 waves"),                                # more than the kernel's 8 waves
+    (dict(n_q=64, K=4096, warps=7), 3, "whole row groups"),               # a multiple of ceil(K / 2048) = 2
+    (dict(n_q=64, K=4096, warps=4), 3, "one thread per 8 values"),
+    (dict(part_size=0), 4, "part_size"),
+    (dict(page=12), 4, "power of two"),
+    (dict(n_bt=0), 3, "n_bt"),
+    (dict(max_pos=-1), 4, "max_pos"),
+    (dict(o=None), 1, "null"),
+    (dict(attn=A16 + 8), 2, "16B aligned"),
+])
+def test_gemv_attn_validation(lib, kw, code, msg):
+    rc, m = _gemv_attn(lib, **kw)
+    assert rc == code and msg in m, (rc, m)
 
 
 def _dec(lib, **kw):
