@@ -223,31 +223,6 @@ int dk_paged_attention_split(int version, const void* q, const void* kc, const v
                              void* stream);
 
 /*
- * A stage-4 W4A16 GEMV launch (dk_gemv_w4a16 stage 4 or one of its fused variants, which share its row tiles): the
- * weights and the tile configuration it is launched with.
- */
-typedef struct dk_gemv_desc {
-  const void* packed;
-  const void* sz;
-  int N, K, group;
-  int R, warps, pf;
-} dk_gemv_desc;
-
-/*
- * dk_paged_attention (split_only = 0) or dk_paged_attention_split (split_only = 1): same arguments, checks and
- * results, bit for bit. The launch carries warm_wgs more workgroups (0..2048) that read the weights of the n_next
- * (0..2) stage-4 GEMV launches described by next[] while the split workgroups run, so that those launches, issued
- * next on the stream, find them in L2: the split grid (n_kv x splits workgroups) leaves most of the chip idle. The
- * chunk a GEMV workgroup reads is read on the XCD that workgroup will run on (workgroup c of a launch runs on XCD
- * c mod 8). Nothing is written. Each GEMV passes the stage-4 checks of dk_gemv_w4a16; packed and sz below 2^31 bytes
- * each. No counterpart in the reference: an MI355X use of the idle part of the chip during the split kernel.
- */
-int dk_paged_attention_warm(int version, const void* q, const void* kc, const void* vc, const int32_t* bt,
-                            const int32_t* pos, int n_q, int n_kv, int head_dim, int page, int n_pages, int n_bt,
-                            int part_size, int max_splits, float* o_part, float* m_part, float* l_part, void* out,
-                            int split_only, const dk_gemv_desc* next, int n_next, int warm_wgs, void* stream);
-
-/*
  * dk_paged_attention without caller-provided split buffers, for callers that cannot allocate device memory (code
  * under hipGraph capture that must not call hipMalloc, tight serving loops, harnesses that forbid allocation). It
  * has no counterpart in the reference. The split partials live in a library-owned device array of

@@ -299,10 +299,10 @@ int check_paged_attention(int version, const void* q, const void* kc, const void
 void launch_reference_attention(int version, const void* q, const void* kc, const void* vc, const int32_t* bt,
                                 const int32_t* pos, int n_q, int n_kv, int head_dim, int page, int n_pages, int n_bt,
                                 int part_size, int max_splits, float* o_part, float* m_part, float* l_part,
-                                void* out, void* stream, bool split_only = false, const dk::L2Warm& warm = {}) {
+                                void* out, void* stream, bool split_only = false) {
   const dk::AttnLaunch a{q, nullptr, nullptr, 0, pos, bt, n_bt, const_cast<void*>(kc), const_cast<void*>(vc), n_pages,
                          ilog2(page), n_q, n_kv, head_dim, part_size, max_splits, o_part, m_part, l_part, out,
-                         version == 5 ? 3 : 1, split_only, warm};
+                         version == 5 ? 3 : 1, split_only};
   dk::launch_paged_attention(a, (hipStream_t)stream);
 }
 
@@ -369,45 +369,6 @@ int dk_paged_attention_split(int version, const void* q, const void* kc, const v
   launch_reference_attention(version, q, kc, vc, bt, pos, n_q, n_kv, head_dim, page, n_pages, n_bt, part_size,
                              max_splits, o_part, m_part, l_part, out, stream, true);
   return launched("paged_attention_split");
-}
-
-int dk_paged_attention_warm(int version, const void* q, const void* kc, const void* vc, const int32_t* bt,
-                            const int32_t* pos, int n_q, int n_kv, int head_dim, int page, int n_pages, int n_bt,
-                            int part_size, int max_splits, float* o_part, float* m_part, float* l_part, void* out,
-                            int split_only, const dk_gemv_desc* next, int n_next, int warm_wgs, void* stream) {
-  const char* what = "paged_attention_warm";
-  if (!o_part || !m_part || !l_part) return fail(DK_ERR_NULL, "%s: null pointer argument", what);
-  int rc = check_paged_attention(version, q, kc, vc, bt, pos, n_q, n_kv, head_dim, page, n_pages, n_bt, part_size,
-                                 max_splits, out);
-  if (rc != DK_OK) return rc;
-  if (!aligned16(o_part)) return fail(DK_ERR_ALIGN, "o_part must be 16B aligned");
-  if (split_only != 0 && split_only != 1)
-    return fail(DK_ERR_DOMAIN, "%s: split_only must be 0 or 1, got %d", what, split_only);
-  if (n_next < 0 || 2 * n_next > dk::kL2WarmRanges)
-    return fail(DK_ERR_DOMAIN, "%s: n_next must be 0..%d, got %d", what, dk::kL2WarmRanges / 2, n_next);
-  if (n_next > 0 && !next) return fail(DK_ERR_NULL, "%s: null pointer argument", what);
-  if (warm_wgs < 0 || warm_wgs > 2048)
-    return fail(DK_ERR_DOMAIN, "%s: warm_wgs must be 0..2048, got %d", what, warm_wgs);
-  if (max_splits + (warm_wgs + n_kv - 1) / n_kv > 65535)
-    return fail(DK_ERR_SHAPE, "%s: max_splits + ceil(warm_wgs / n_kv) must be <= 65535", what);
-  dk::L2Warm warm{};
-  for (int i = 0; i < n_next; ++i) {
-    const dk_gemv_desc& g = next[i];
-    rc = check_fused_gemv(what, 4, g.R, g.warps, g.pf, g.packed, g.sz, g.N, g.K, g.group);
-    if (rc != DK_OK) return rc;
-    const long long wbytes = (long long)g.N * (g.K / 2), sbytes = (long long)g.N * (g.K / g.group) * 4;
-    if (wbytes >= (1LL << 31) || sbytes >= (1LL << 31))
-      return fail(DK_ERR_SHAPE, "%s: GEMV %d: packed and sz must each be below 2^31 bytes", what, i);
-    const int rows = dk::gemv_tile_rows_per_workgroup(g.R, g.warps, g.pf, g.K);
-    warm.r[warm.n++] = {static_cast<const uint8_t*>(g.packed), (uint32_t)wbytes, (uint32_t)rows * (uint32_t)(g.K / 2)};
-    warm.r[warm.n++] = {static_cast<const uint8_t*>(g.sz), (uint32_t)sbytes,
-                        (uint32_t)rows * (uint32_t)(g.K / g.group) * 4u};
-  }
-  warm.wgs = warm.n > 0 ? warm_wgs : 0;
-  clear_error();
-  launch_reference_attention(version, q, kc, vc, bt, pos, n_q, n_kv, head_dim, page, n_pages, n_bt, part_size,
-                             max_splits, o_part, m_part, l_part, out, stream, split_only == 1, warm);
-  return launched(what);
 }
 
 int dk_gemv_w4a16_attn(int stage, int R, int warps, int pf, const void* packed, const void* sz, const float* o_part,

@@ -679,13 +679,6 @@ void launch_splitk(int waves, int pf, const void* packed, const void* sz, const 
 
 }  // namespace
 
-// Rows per workgroup of the stage-4 launch (launch_tile_nt's grid): R * 2^pf rows per row group, warps / ceil(K / 2048)
-// row groups (warps 0: one).
-int gemv_tile_rows_per_workgroup(int R, int warps, int pf, int K) {
-  const int nw = ((K >> 5) + 63) / 64;
-  return R * (1 << pf) * (warps > 0 ? warps / nw : 1);
-}
-
 void gemv_default_config(int N, int K, int* stage, int* R, int* waves, int* pf) {
   // Row tiles of 2 rows, one tile per workgroup, while the workgroup can cover K (K <= 32768); split-K beyond.
   (void)N;

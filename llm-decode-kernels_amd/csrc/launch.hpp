@@ -77,25 +77,6 @@ void launch_gemm_w4a16(const void* packed, const void* sz, const void* x, void* 
 
 void launch_bw_read(const void* buf, size_t bytes, void* sink, int blocks, int threads, int unroll, hipStream_t st);
 
-// L2 warm-up by the spare workgroups of an attention launch: byte ranges that the launches after it will read, each
-// cut into chunks of `chunk` bytes; chunk c is read by the consumer's workgroup c, which the dispatcher places on XCD
-// c % 8 (workgroups go round-robin over the 8 XCDs in linear-id order, every launch starting at XCD 0), so the warm-up
-// reads chunk c from a workgroup on that XCD and the line lands in the L2 that workgroup will read through (and in
-// the MALL on the way). wgs = 0: no warm-up workgroups.
-constexpr int kL2WarmRanges = 4;
-struct L2WarmRange {
-  const uint8_t* base;  // 64-byte aligned
-  uint32_t bytes;       // multiple of 4, < 2^31
-  uint32_t chunk;       // > 0
-};
-struct L2Warm {
-  L2WarmRange r[kL2WarmRanges];
-  int n;
-  int wgs;
-};
-// The chunking of a stage-4 GEMV's weights: workgroup c reads rows [c * rows, (c + 1) * rows) of packed and sz.
-int gemv_tile_rows_per_workgroup(int R, int warps, int pf, int K);
-
 // Paged attention arguments. q: the query heads [n_q * D] (reference op) or the fused qkv vector (decode op).
 struct AttnLaunch {
   const void* q;
@@ -116,7 +97,6 @@ struct AttnLaunch {
   void* out;
   int impl;            // 0 or 1 = block kernel; 3 = lean MFMA kernel
   bool split_only;     // the split kernel alone: the consumer merges the partials (gemv prologue 2)
-  L2Warm warm;         // warm-up workgroups after the split grid (warm.wgs = 0: none)
 };
 // The lean MFMA kernel: pages of at least 16 tokens, splits of whole 16-token tiles, at most 8 waves x 4 tiles (x 2
 // tiles at head_dim 128, whose RoPE variant would not fit 4 tiles in registers).

@@ -5,8 +5,7 @@
 // Context = min(*pos + 1, n_bt * P) read from device memory, so one captured graph serves every decode step.
 //
 // Grid (n_kv, max_splits), 256 threads. Workgroup (kvh, s) owns tokens [s*PS, min(ctx, (s+1)*PS)) for all HPG query
-// heads of kv head kvh, so every K/V byte is read from HBM once. Splits past ceil(ctx / PS) exit at once. Grid rows
-// past max_splits, when asked for, hold L2 warm-up workgroups (l2_warm below) and no attention work.
+// heads of kv head kvh, so every K/V byte is read from HBM once. Splits past ceil(ctx / PS) exit at once.
 // The split is processed in blocks of TB tokens, three phases per block:
 //   1. token-major: lane (g, c) of a wave holds the 16-byte slice c (dims 8c..8c+7) of token slot g; CPL = D/8 lanes
 //      cover one token, so one wave load reads TPL = 64/CPL consecutive tokens (1 KB contiguous inside a page).
@@ -55,69 +54,13 @@ __device__ __forceinline__ int attn_context(const int32_t* pos_ptr, int n_bt, in
   return (int)(ctx < cap ? ctx : cap);
 }
 
-// ---------------------------------------------------------------------------------------------------------------
-// L2 warm-up role of the workgroups past the split grid (blockIdx.y >= max_splits; first_wg = the first one's linear
-// id). A split grid of n_kv x splits workgroups leaves most of the chip idle for the kernel's few microseconds; these
-// workgroups meanwhile read the weights of the launches that follow, so that those find them in their XCD's L2.
-// A workgroup's XCD is its linear id mod 8; the warm-up workgroups of one XCD share that XCD's chunks (c = xcd,
-// xcd + 8, ...) of every range, taken as one sequence of 64-byte lines and walked grid-stride, one dword load per
-// line (the line is what lands in L2), eight loads in flight per thread and all ranges in one batch. Nothing is
-// written; an empty asm that takes the loaded values keeps the loads.
-template <int THREADS>
-__device__ __forceinline__ void l2_warm(const L2Warm& w, int first_wg) {
-  const int L = (int)(blockIdx.x + blockIdx.y * gridDim.x);
-  const int wi = L - first_wg;
-  if (wi >= w.wgs) return;
-  const uint32_t xcd = (uint32_t)L & 7u;
-  const uint32_t i = (uint32_t)wi >> 3, nx = (uint32_t)(w.wgs - (wi & 7) + 7) >> 3;
-  uint32_t P[kL2WarmRanges + 1], LPC[kL2WarmRanges];
-  P[0] = 0;
-#pragma unroll
-  for (int r = 0; r < kL2WarmRanges; ++r) {
-    const uint32_t nch = r < w.n ? (w.r[r].bytes + w.r[r].chunk - 1) / w.r[r].chunk : 0u;
-    const uint32_t mine = xcd < nch ? (nch - xcd + 7) >> 3 : 0u;
-    LPC[r] = r < w.n ? (w.r[r].chunk + 127) >> 6 : 0u;  // lines [s & ~63, s + chunk) can touch, s = chunk start
-    P[r + 1] = P[r] + mine * LPC[r];
-  }
-  const uint32_t U = P[kL2WarmRanges], stride = (uint32_t)THREADS * nx;
-  for (uint32_t u0 = i * THREADS + threadIdx.x; u0 < U; u0 += 8 * stride) {
-    uint32_t v[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const uint32_t u = u0 + q * stride;
-      const uint8_t* base = w.r[0].base;
-      uint32_t p0 = 0, lpc = LPC[0], chunk = w.r[0].chunk, bytes = w.r[0].bytes;
-#pragma unroll
-      for (int r = 1; r < kL2WarmRanges; ++r)
-        if (u >= P[r] && P[r] < P[r + 1]) {
-          base = w.r[r].base;
-          p0 = P[r];
-          lpc = LPC[r];
-          chunk = w.r[r].chunk;
-          bytes = w.r[r].bytes;
-        }
-      const uint32_t k = (u - p0) / max(lpc, 1u), j = (u - p0) - k * lpc;
-      const uint32_t s = (xcd + 8 * k) * chunk;
-      const uint32_t e = min(s + chunk, bytes);
-      const uint32_t a = (s & ~63u) + 64 * j;
-      v[q] = (u < U && a < e) ? *reinterpret_cast<const uint32_t*>(base + a) : 0u;
-    }
-#pragma unroll
-    for (int q = 0; q < 8; ++q) asm volatile("" ::"v"(v[q]));
-  }
-}
-
 template <int D, int HPG, bool ROPE>
 __global__ void __launch_bounds__(kAttnThreads)
 attn_decode_kernel(const f16* __restrict__ qsrc, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
                    int max_pos, const int32_t* __restrict__ pos_ptr, const int32_t* __restrict__ bt, int n_bt,
                    f16* __restrict__ kc, f16* __restrict__ vc, int n_pages, int log2P, int n_q, int n_kv, int PS,
                    int max_splits, float scale, float* __restrict__ o_part, float* __restrict__ m_part,
-                   float* __restrict__ l_part, f16* __restrict__ out, L2Warm warm) {
-  if ((int)blockIdx.y >= max_splits) {  // a warm-up workgroup (uniform)
-    l2_warm<kAttnThreads>(warm, max_splits * (int)gridDim.x);
-    return;
-  }
+                   float* __restrict__ l_part, f16* __restrict__ out) {
   using S = AttnShape<D, HPG>;
   constexpr int CPL = S::CPL, TPL = S::TPL, TB = S::TB, NTH = S::NTH, DPT = S::DPT;
   __shared__ float s_s[HPG][TB];
@@ -479,11 +422,7 @@ attn_lean_kernel(const f16* __restrict__ qsrc, const float* __restrict__ cos_t, 
                  int max_pos, const int32_t* __restrict__ pos_ptr, const int32_t* __restrict__ bt, int n_bt,
                  f16* __restrict__ kc, f16* __restrict__ vc, int n_pages, int log2P, int n_q, int n_kv, int PS,
                  int max_splits, float scale, float* __restrict__ o_part, float* __restrict__ m_part,
-                 float* __restrict__ l_part, f16* __restrict__ out, L2Warm warm) {
-  if ((int)blockIdx.y >= max_splits) {  // a warm-up workgroup (uniform)
-    l2_warm<NW * kWave>(warm, max_splits * (int)gridDim.x);
-    return;
-  }
+                 float* __restrict__ l_part, f16* __restrict__ out) {
   using S = MfmaAttnShape<D>;
   constexpr int KW = S::KW, QS = S::QS, VD = S::VD, CPL = D / 8;
   __shared__ float s_m[NW][HPG], s_l[NW][HPG], s_w[NW][HPG];
@@ -728,9 +667,6 @@ attn_lean_kernel(const f16* __restrict__ qsrc, const float* __restrict__ cos_t, 
   }
 }
 
-// Grid rows of warm-up workgroups after the n_kv x max_splits split grid.
-inline int warm_rows(const AttnLaunch& a) { return a.warm.wgs > 0 ? (a.warm.wgs + a.n_kv - 1) / a.n_kv : 0; }
-
 // The combine with the smallest batch B in {4, 8, 16} whose B * SLN splits cover max_splits (16 beyond: the kernel
 // then loops over batches).
 template <int D>
@@ -751,10 +687,10 @@ void launch_combine(const AttnLaunch& a, bool rope, hipStream_t st) {
 template <int D, int HPG, bool ROPE, int NW, int NT>
 void launch_lean(const AttnLaunch& a, hipStream_t st) {
   const float scale = 1.0f / sqrtf((float)D);
-  hipLaunchKernelGGL((attn_lean_kernel<D, HPG, ROPE, NW, NT>), dim3(a.n_kv, a.max_splits + warm_rows(a)),
-                     dim3(NW * kWave), 0, st, (const f16*)a.q, a.cos_t, a.sin_t, a.max_pos, a.pos, a.bt, a.n_bt,
-                     (f16*)a.kc, (f16*)a.vc, a.n_pages, a.log2P, a.n_q, a.n_kv, a.part_size, a.max_splits, scale,
-                     a.o_part, a.m_part, a.l_part, (f16*)a.out, a.warm);
+  hipLaunchKernelGGL((attn_lean_kernel<D, HPG, ROPE, NW, NT>), dim3(a.n_kv, a.max_splits), dim3(NW * kWave), 0, st,
+                     (const f16*)a.q, a.cos_t, a.sin_t, a.max_pos, a.pos, a.bt, a.n_bt, (f16*)a.kc, (f16*)a.vc,
+                     a.n_pages, a.log2P, a.n_q, a.n_kv, a.part_size, a.max_splits, scale, a.o_part, a.m_part,
+                     a.l_part, (f16*)a.out);
 }
 
 // waves: the smallest power of two >= min(tiles, 8); tiles per wave NT = ceil(tiles / waves) in {1, 2, 4} (2 at most
@@ -792,10 +728,10 @@ void launch_attn(const AttnLaunch& a, hipStream_t st) {
     if (a.max_splits > 1 && !a.split_only) launch_combine<D>(a, ROPE, st);
     return;
   }
-  hipLaunchKernelGGL((attn_decode_kernel<D, HPG, ROPE>), dim3(a.n_kv, a.max_splits + warm_rows(a)),
-                     dim3(kAttnThreads), 0, st, (const f16*)a.q, a.cos_t, a.sin_t, a.max_pos, a.pos, a.bt, a.n_bt,
-                     (f16*)a.kc, (f16*)a.vc, a.n_pages, a.log2P, a.n_q, a.n_kv, a.part_size, a.max_splits, scale,
-                     a.o_part, a.m_part, a.l_part, (f16*)a.out, a.warm);
+  hipLaunchKernelGGL((attn_decode_kernel<D, HPG, ROPE>), dim3(a.n_kv, a.max_splits), dim3(kAttnThreads), 0,
+                     st, (const f16*)a.q, a.cos_t, a.sin_t, a.max_pos, a.pos, a.bt, a.n_bt, (f16*)a.kc, (f16*)a.vc,
+                     a.n_pages, a.log2P, a.n_q, a.n_kv, a.part_size, a.max_splits, scale, a.o_part, a.m_part,
+                     a.l_part, (f16*)a.out);
   if (a.max_splits > 1 && !a.split_only) launch_combine<D>(a, ROPE, st);
 }
 

@@ -17,14 +17,6 @@ PKG_DIR = pathlib.Path(__file__).resolve().parents[1]
 LIB_PATH = PKG_DIR / "libdk_amd.so"
 HEADER = PKG_DIR.parent / "include" / "dk_amd.h"
 
-
-
-class GemvDesc(ctypes.Structure):
-    """dk_gemv_desc: a stage-4 W4A16 GEMV launch, its weights and tile configuration."""
-    _fields_ = [("packed", ctypes.c_void_p), ("sz", ctypes.c_void_p), ("N", ctypes.c_int), ("K", ctypes.c_int),
-                ("group", ctypes.c_int), ("R", ctypes.c_int), ("warps", ctypes.c_int), ("pf", ctypes.c_int)]
-
-
 # Every exported entry point, with its ctypes signature (kept in the order of include/dk_amd.h).
 _P, _I, _F, _Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
 SIGNATURES = {
@@ -46,8 +38,6 @@ SIGNATURES = {
     "dk_bw_read": ([_P, _Z, _P, _I, _I, _I, _P], _I),
     "dk_paged_attention": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
     "dk_paged_attention_split": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
-    "dk_paged_attention_warm": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, _I,
-                                 _I, _P], _I),
     "dk_paged_attention_noalloc": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P], _I),
     "dk_paged_attention_noalloc_bytes": ([_I, _I, _I], _Z),
     "dk_attention_decode": ([_P, _P, _P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P],
@@ -368,23 +358,6 @@ class DecodeKernels:
     def paged_attention_split(self, q, kc, vc, bt, pos, part_size, o_part, m_part, l_part, out, version=5):
         self._call(self.lib.dk_paged_attention_split,
                    *self._attention_args(q, kc, vc, bt, pos, part_size, o_part, m_part, l_part, out, version))
-
-    # paged_attention (split_only False) or paged_attention_split (True) whose warm_wgs spare workgroups read the
-    # weights of the stage-4 GEMVs launched next into L2; nxt: [(packed, sz, group, (4, R, warps, pf)), ...] (<= 2)
-    def paged_attention_warm(self, q, kc, vc, bt, pos, part_size, o_part, m_part, l_part, out, version, split_only,
-                             nxt, warm_wgs):
-        args = self._attention_args(q, kc, vc, bt, pos, part_size, o_part, m_part, l_part, out, version)
-        descs = (GemvDesc * max(1, len(nxt)))()
-        for i, (packed, sz, group, cfg) in enumerate(nxt):
-            _check_cuda(packed, "packed")
-            _check_cuda(sz, "sz")
-            stage, R, warps, pf = cfg
-            if stage != 4:
-                raise RuntimeError("paged_attention_warm: the GEMVs must be stage-4 launches")
-            descs[i] = GemvDesc(packed.data_ptr(), sz.data_ptr(), packed.size(0), packed.size(1) * 8, int(group),
-                                int(R), int(warps), int(pf))
-        self._call(self.lib.dk_paged_attention_warm, *args[:-1], int(bool(split_only)), ctypes.addressof(descs),
-                   len(nxt), int(warm_wgs), args[-1])
 
     # the combine of paged_attention (kernels/paged_attention.cu:368-427) fused as the x prologue of gemv_w4a16 (the
     # o projection, runtime/model.py:220-222): y = W . combine(o_part, m_part, l_part), or W . attn with one live split

@@ -78,9 +78,6 @@ class DecodeConfig:
     swiglu: str = "epilogue"       # where SwiGLU runs when fused_gemv is on: "epilogue" = inside the gate|up GEMV
                                    # (dk_gemv_w4a16_gate_up, gate/up rows stored interleaved); "kernel" = the separate
                                    # dk_swiglu launch
-    l2_warm: bool = True           # with rope_epilogue: the attention launch's spare workgroups read the weights of
-                                   # the GEMVs that follow it (o, then gate|up) into their XCDs' L2
-                                   # (dk_paged_attention_warm), up to Model.L2_WARM_BYTES
 
 
 def default_gemv_config(N, K):
@@ -167,7 +164,6 @@ class Model:
         self.use_fused_gemv = (cfg.fused and cfg.fused_gemv and quant and self.H <= 32768 and self.I <= 32768)
         self.gate_up_epilogue = self.use_fused_gemv and cfg.swiglu == "epilogue"
         self.rope_epilogue = self.use_fused_gemv and cfg.rope_epilogue
-        self.n_cu = torch.cuda.get_device_properties(dev).multi_processor_count if cfg.l2_warm else 0
         sd = hf_state
         g = lambda k: sd[k].half()
         self.emb = g("model.embed_tokens.weight").to(dev).contiguous()
@@ -435,44 +431,10 @@ class Model:
                                    self.sin, self.pos, self.bt, self.kv[li, 0], self.kv[li, 1], self.n_q, self.n_kv,
                                    self.cfg.group)
 
-    # weights read into L2 by one attention launch's spare workgroups. The warm-up has to end within the split
-    # kernel's few microseconds: on MI355X TinyLlama's o projection (2.2 MB) pays (492 -> 484 us per step at ctx
-    # 512), o + gate|up (14.4 MB) or Llama-3-8B's o (8.9 MB) outlast the split kernel and cost 9-50 us per step
-    L2_WARM_BYTES = 4 << 20
-
-    def l2_warm_next(self, li):
-        """The GEMV launches after layer li's attention (in the fused step) whose weights the attention launch reads
-        into L2: the o projection, then gate|up, while both are stage-4 launches and the total stays within
-        L2_WARM_BYTES. Each as (packed, sz, group, (stage, R, warps, pf))."""
-        lw = self.layers[li]
-        o_cfg = self.gemv_attn_cfg(lw["o"]) if self.attn_in_o else self.gemv_cfg(lw["o"])
-        gu_cfg = self.gemv_gate_up_cfg(lw["gu"]) if self.gate_up_epilogue else self.gemv_norm_cfg(lw["gu"])
-        out, total = [], 0
-        for lin, cfg in ((lw["o"], o_cfg), (lw["gu"], gu_cfg)):
-            if not lin.quant or cfg[0] != 4:
-                break
-            total += lin.packed.numel() * 4 + lin.sz.numel() * 2
-            if total > self.L2_WARM_BYTES:
-                break
-            out.append((lin.packed, lin.sz, self.cfg.group, tuple(cfg)))
-        return out
-
-    def l2_warm_wgs(self):
-        """Warm-up workgroups: the CUs the split grid (n_kv x max_splits workgroups) leaves free, in whole XCD
-        rounds (a multiple of 8); 0 when it covers the chip."""
-        free = self.n_cu - self.n_kv * self.max_splits
-        return max(0, free - free % 8)
-
     def attention(self, li):
         kc, vc = self.kv[li, 0], self.kv[li, 1]
         if self.rope_epilogue:  # q rotated and k, v appended by the qkv GEMV
             version = 5 if self.attn_impl == 3 else 2
-            nxt = self.l2_warm_next(li) if self.cfg.l2_warm and self.use_fused_gemv else []
-            if nxt and self.l2_warm_wgs() > 0:
-                self.K.paged_attention_warm(self.qkv[: self.n_q * self.D], kc, vc, self.bt, self.pos, self.part_size,
-                                            self.o_part, self.m_part, self.l_part, self.attn, version,
-                                            self.attn_in_o, nxt, self.l2_warm_wgs())
-                return
             if self.attn_in_o:  # the o projection merges the partials
                 self.K.paged_attention_split(self.qkv[: self.n_q * self.D], kc, vc, self.bt, self.pos,
                                              self.part_size, self.o_part, self.m_part, self.l_part, self.attn, version)

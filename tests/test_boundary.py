@@ -112,46 +112,6 @@ def test_attention_validation(lib, kw, code, msg):
     a.update(kw)
     rs, ms = _err(lib, lib.dk_paged_attention_split(*a.values(), None))
     assert rs == code and msg in ms, (rs, ms)
-    rw, mw = _warm(lib, **kw)
-    assert rw == code and msg in mw, (rw, mw)
-
-
-def _warm(lib, descs=((),), n_next=None, warm_wgs=64, split_only=0, null_next=False, **kw):
-    a = dict(version=2, q=A16, kc=A16, vc=A16, bt=A16, pos=A16, n_q=32, n_kv=4, head_dim=64, page=16, n_pages=8,
-             n_bt=8, part_size=64, max_splits=4, o=A16, m=A16, l=A16, out=A16)
-    a.update(kw)
-    arr = (ext.GemvDesc * max(1, len(descs)))()
-    for i, d in enumerate(descs):
-        g = dict(packed=A16, sz=A16, N=2048, K=2048, group=128, R=2, warps=4, pf=0)
-        g.update(dict(d))
-        arr[i] = ext.GemvDesc(**g)
-    nxt = None if null_next else ctypes.addressof(arr)
-    n = len(descs) if n_next is None else n_next
-    return _err(lib, lib.dk_paged_attention_warm(*a.values(), split_only, nxt, n, warm_wgs, None))
-
-
-@pytest.mark.parametrize("kw,code,msg", [
-    (dict(n_next=3, descs=((), (), ())), 4, "n_next must be 0..2"),
-    (dict(n_next=-1), 4, "n_next must be 0..2"),
-    (dict(null_next=True), 1, "null"),
-    (dict(warm_wgs=2049), 4, "warm_wgs must be 0..2048"),
-    (dict(warm_wgs=-1), 4, "warm_wgs must be 0..2048"),
-    (dict(split_only=2), 4, "split_only must be 0 or 1"),
-    (dict(max_splits=65535, warm_wgs=8), 3, "65535"),
-    (dict(descs=((("R", 3),),)), 4, "R must be 1,2,4,8"),
-    (dict(descs=((("K", 8192), ("warps", 3)),)), 3, "whole row groups"),
-    (dict(descs=((("pf", 4),),)), 4, "pf must be 0..3"),
-    (dict(descs=((("K", 100),),)), 3, "multiple of 32"),
-    (dict(descs=((("packed", A16 + 4),),)), 2, "packed must be 16B aligned"),
-    (dict(descs=((("sz", None),),)), 1, "null"),
-    (dict(descs=((("N", 1 << 20), ("K", 8192)),)), 3, "below 2^31"),
-    (dict(descs=((), (("group", 16),))), 4, "group must be >= 32"),     # the second GEMV is checked too
-    (dict(version=4), 4, "version must be 1, 2, 3 or 5"),               # the attention checks come first
-    (dict(o=None), 1, "null"),
-])
-def test_attention_warm_validation(lib, kw, code, msg):
-    rc, m = _warm(lib, **kw)
-    assert rc == code and msg in m, (rc, m)
 
 
 def _gemv_attn(lib, **kw):
