@@ -401,25 +401,34 @@ def attn8b_leg(Kx, ctx=4096, reps=5, eager=8, part_size=0):
 
 
 def decode_leg(model, ctx, steps, warmup):
+    """`steps` decode steps from context ctx after `warmup` untimed ones. The throughput comes from one pass with HIP
+    events only at its two ends; the per-token distribution (median, quartiles: bench/e2e.py:178-197) from a second
+    pass over the same positions with an event pair around every step, because those events cost the stream about
+    10 us per TinyLlama step (495-498 against 485-486 us per step, same model and box)."""
     import torch
     model.reset(ctx)
     for _ in range(warmup):
         model.run_step()
     torch.cuda.synchronize()
     model.reset(ctx)
-    per = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     start.record()
-    for s, e in per:
-        s.record()
+    for _ in range(steps):
         model.run_step()
-        e.record()
     end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     total_ms = start.elapsed_time(end)
+    model.reset(ctx)
+    per = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for s, e in per:
+        s.record()
+        model.run_step()
+        e.record()
+    torch.cuda.synchronize()
     tok_us = sorted(s.elapsed_time(e) * 1e3 for s, e in per)
     return {"ctx_start": ctx, "steps": steps, "ms_per_step": total_ms / steps, "tok_s": steps / (total_ms / 1e3),
             "median_us": statistics.median(tok_us), "p10_us": tok_us[len(tok_us) // 10],
