@@ -39,6 +39,12 @@ SHAPE_SETS = {
                   "lm_head8b": (128256, 4096)},
     # BASELINE config 1 and the standalone target shapes
     "baseline": {"cfg1": (5632, 2048), "w4096x14336": (4096, 14336), "w14336x4096": (14336, 4096)},
+    # one GPU's share under tensor parallelism (qkv and gate|up split by rows, o and down by columns): Llama-3-8B over
+    # 8 GPUs (one kv head each) and TinyLlama over 4 (its kv head count)
+    "llama3_8b_tp8": {"qkv8b_tp8": (768, 4096), "o8b_tp8": (4096, 512), "gate_up8b_tp8": (3584, 4096),
+                      "down8b_tp8": (4096, 1792)},
+    "tinyllama_tp4": {"qkv_tp4": (640, 2048), "o_tp4": (2048, 512), "gate_up_tp4": (2816, 2048),
+                      "down_tp4": (2048, 1408)},
 }
 
 

@@ -81,6 +81,10 @@ def test_gemv_shape1_and_onehot(K, cfg):
 SHAPES = {"qkv": (2560, 2048), "o": (2048, 2048), "gate_up": (11264, 2048), "down": (2048, 5632),
           "lm_head": (32000, 2048), "cfg1": (5632, 2048)}       # cfg1: BASELINE config 1, the plain 5632 x 2048 GEMV
 SHAPES_8B = {"qkv8b": (6144, 4096), "o8b": (4096, 4096), "down8b": (4096, 14336), "up8b": (14336, 4096)}
+# one GPU's share of each projection under tensor parallelism (Llama-3-8B over 8 GPUs, TinyLlama over 4)
+SHAPES_TP = {"qkv8b_tp8": (768, 4096), "o8b_tp8": (4096, 512), "gate_up8b_tp8": (3584, 4096),
+             "down8b_tp8": (4096, 1792), "qkv_tp4": (640, 2048), "o_tp4": (2048, 512), "gate_up_tp4": (2816, 2048),
+             "down_tp4": (2048, 1408)}
 
 
 def _quantized(K, N, Kd, G, seed):
@@ -91,10 +95,12 @@ def _quantized(K, N, Kd, G, seed):
     return w, packed, sz
 
 
-# the TinyLlama shapes at three group sizes, the Llama-3-8B shapes at the model's group size
-@pytest.mark.parametrize("name,G", [(n, g) for g in (64, 128, 256) for n in SHAPES] + [(n, 128) for n in SHAPES_8B])
+# the TinyLlama shapes at three group sizes, the Llama-3-8B shapes and the tensor-parallel shard shapes at the
+# models' group size
+@pytest.mark.parametrize("name,G", [(n, g) for g in (64, 128, 256) for n in SHAPES] + [(n, 128) for n in SHAPES_8B]
+                         + [(n, 128) for n in SHAPES_TP])
 def test_gemv_real_shapes(K, name, G):
-    N, Kd = {**SHAPES, **SHAPES_8B}[name]
+    N, Kd = {**SHAPES, **SHAPES_8B, **SHAPES_TP}[name]
     w, packed, sz = _quantized(K, N, Kd, G, seed=zlib.crc32(name.encode()) % 1000)
     wref = dequant_from_gpu(packed, sz, G)
     x = torch.randn(Kd, generator=gen(1)).half()
