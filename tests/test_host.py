@@ -1,6 +1,6 @@
 """CPU checks of the runtime's host logic: the byte model of the decode step (scope row a10) against the figures the
 reference publishes for its configurations (plots/predictions.json of the reference, as recorded for BASELINE configs 4
-and 5), and the gate/up row interleave the SwiGLU epilogues rely on."""
+and 5), the gate/up row interleave the SwiGLU epilogues rely on, and the committed attention policy table."""
 import torch
 
 from runtime.model import byte_model, deinterleave_halves, interleave_halves
@@ -49,3 +49,22 @@ def test_gemv_byte_count_matches_oracle():
     from runtime.autotune import gemv_bytes
     for N, K, G in ((4096, 14336, 128), (14336, 4096, 128), (5632, 2048, 128), (2560, 2048, 64), (32000, 2048, 256)):
         assert gemv_bytes(N, K, G) == Q.gemv_bytes(N, K, G)
+
+
+def test_attention_policy_entries_are_launchable():
+    """Every entry of the committed attention policy is one the C ABI accepts for its head dim: impl 1 (block kernel)
+    or 3 (lean kernel, part size a multiple of 16 up to 512 at head dim 64 and 256 at 128, as
+    dk_paged_attention's version-5 check requires), contexts increasing, the last entry open-ended."""
+    import json
+    from runtime.model import DecodeConfig, Model
+    pol = json.load(open(DecodeConfig().attn_policy_path))
+    for key, D in (("policy", 64), ("policy_d128", 128)):
+        ents = pol[key]
+        assert [e["max_ctx"] for e in ents] == sorted(e["max_ctx"] for e in ents) and ents[-1]["max_ctx"] >= 1 << 30
+        for e in ents:
+            assert e["impl"] in (1, 3) and e["part_size"] > 0, e
+            if e["impl"] == 3:
+                assert e["part_size"] % 16 == 0 and e["part_size"] <= (256 if D == 128 else 512), e
+        # the lookup picks the entry tuned at the largest context <= the cap
+        for e in ents[:-1]:
+            assert Model._policy_entry_of(pol, D, e["max_ctx"]) == e
