@@ -43,7 +43,8 @@ def _cfgs(Kd):
 CASES = [(64, 32, 4, 1, 64, 0), (64, 32, 4, 40, 64, 2), (64, 32, 4, 500, 64, 1), (64, 32, 4, 1000, 64, 0),
          (64, 32, 4, 129, 16, 7), (64, 16, 2, 2048, 128, 0), (128, 32, 8, 1, 256, 3), (128, 32, 8, 700, 128, 2),
          (128, 32, 8, 4000, 256, 0), (128, 16, 16, 300, 32, 6),
-         (64, 32, 4, 300, 40, 1)]                                    # part size 40: the block kernel (version 3)
+         (64, 32, 4, 300, 40, 1),                                    # part size 40: the block kernel (version 3)
+         (64, 32, 4, 500, 96, 1), (64, 32, 4, 1000, 160, 0), (128, 32, 8, 700, 80, 1)]   # bands between powers of 2
 
 
 @pytest.mark.parametrize("D,n_q,n_kv,ctx,PS,spare", CASES)

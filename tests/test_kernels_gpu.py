@@ -236,6 +236,19 @@ def test_attention_head_dim_128(K, ver, n_q, n_kv, ctx):
         close_or_rejected(run_attn(K, q, kc, vc, bt, ctx, PS, ver), ref, 2e-3, f"D128 {n_q}/{n_kv} ctx{ctx} PS{PS} v{ver}")
 
 
+# every multiple-of-16 band the lean kernel takes at each head dim (the attention policy picks among them): 1-8 waves
+# of 1, 2 or 4 tiles with idle tile slots (e.g. 80 = 5 tiles on 8 waves, 160 = 10 tiles on 8 waves x 2, 320 = 20 on
+# 8 x 4), with spare splits
+@pytest.mark.parametrize("D,n_q,n_kv", [(64, 32, 4), (128, 32, 8)])
+@pytest.mark.parametrize("ctx", (700, 2100))
+def test_attention_lean_part_bands(K, D, n_q, n_kv, ctx):
+    kc, vc, bt = make_cache(ctx, n_kv, 16, D=D, peaky=3.0, seed=ctx + D)
+    q = torch.randn(n_q, D, generator=gen(ctx + D)).half()
+    ref = R.paged_attention_ref(q, kc, vc, bt, ctx, 16)
+    for PS in (48, 80, 96, 112, 144, 160, 176, 192, 208, 224, 240) + ((320, 384, 448) if D == 64 else ()):
+        close_or_rejected(run_attn(K, q, kc, vc, bt, ctx, PS, 5, spare=2), ref, 2e-3, f"D{D} ctx{ctx} PS{PS} lean")
+
+
 @pytest.mark.parametrize("ver", (3, 5))
 def test_attention_ctx1_is_v0(K, ver):
     """Softmax over one token returns that token's V exactly (fp16 in, fp16 out)."""
