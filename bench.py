@@ -187,8 +187,15 @@ def tuned_config(N, K, G=128):
     return tuple(e) if len(e) == 4 else (2, *e)
 
 
+# replays per timed sample of the GEMV legs and their read ceiling: the cold copies' graph is replayed back to back,
+# so the GPU stays busy across replays as in the decode loop (a replay that follows a host synchronisation with an
+# idle GPU runs its first launches slower: 7.53-7.58 us per launch one replay at a time, 7.36 back to back)
+GEMV_BATCH = 4
+
+
 def gemv_leg(Kx, N, Kd, G=128, reps=7):
-    """Mean per-launch duration of the tuned W4A16 GEMV with cold weights (hipGraph of back-to-back launches)."""
+    """Mean per-launch duration of the tuned W4A16 GEMV with cold weights (hipGraph of back-to-back launches, GEMV_BATCH
+    replays per timed sample)."""
     import torch
     from runtime.autotune import gemv_bytes
     from runtime.quant import quantize_pack
@@ -201,8 +208,8 @@ def gemv_leg(Kx, N, Kd, G=128, reps=7):
     y = torch.empty(N, dtype=torch.half, device="cuda")
     cfg = tuned_config(N, Kd, G)
     cold = ColdCopies([packed, sz], n_copies(nbytes))
-    mn, med = graph_time(lambda i: Kx.gemv_w4a16(*cfg, *cold[i], x, y, G), cold.copies, reps)
-    launches = cold.copies * (reps + 2)
+    mn, med = graph_time(lambda i: Kx.gemv_w4a16(*cfg, *cold[i], x, y, G), cold.copies, reps, batch=GEMV_BATCH)
+    launches = cold.copies * (reps * GEMV_BATCH + 2)
     del cold
     return {"N": N, "K": Kd, "group": G, "cfg": list(cfg), "bytes": nbytes, "mean_us": round(med, 3),
             "min_us": round(mn, 3), "gbps": round(nbytes / med / 1e3, 1), "frac": round(nbytes / med / 1e3 / HBM_PEAK_GBS, 4),
@@ -218,7 +225,8 @@ def read_ceiling_leg(Kx, nbytes, reps=5):
     sink = torch.zeros(4, dtype=torch.int32, device="cuda")
     best = None
     for blocks, threads in ((nbytes // 16 // 512, 512), (nbytes // 16 // 256, 256)):
-        mn, med = graph_time(lambda i: Kx.bw_read(cold[i][0], sink, blocks, threads, 1), cold.copies, reps)
+        mn, med = graph_time(lambda i: Kx.bw_read(cold[i][0], sink, blocks, threads, 1), cold.copies, reps,
+                             batch=GEMV_BATCH)
         if best is None or med < best[0]:
             best = (med, blocks, threads)
     del cold
@@ -237,8 +245,8 @@ def read_sweep_leg(Kx, sizes_mb=(2, 4, 8, 16, 31.232, 64, 128, 256, 512), reps=5
     for mb in sizes_mb:
         nbytes = int(mb * 1e6) // (16 * 512) * (16 * 512)
         cold = ColdCopies([torch.empty(nbytes, dtype=torch.uint8, device="cuda")], n_copies(nbytes, min_copies=2))
-        best = min(graph_time(lambda i: Kx.bw_read(cold[i][0], sink, nbytes // 16 // t, t, 1), cold.copies, reps)[1]
-                   for t in (512, 256))
+        best = min(graph_time(lambda i: Kx.bw_read(cold[i][0], sink, nbytes // 16 // t, t, 1), cold.copies, reps,
+                              batch=GEMV_BATCH)[1] for t in (512, 256))
         pts.append({"bytes": nbytes, "us": round(best, 3), "gbps": round(nbytes / best / 1e3, 1),
                     "frac": round(nbytes / best / 1e3 / HBM_PEAK_GBS, 4)})
         del cold

@@ -6,8 +6,8 @@ back-to-back kernels, not Python/ctypes launch cost. To keep the weights out of 
 so every launch reads its weights from HBM; the reference flushed L2 with a 16 MB read between iterations instead
 (bench/timing.py:28-32), which would not evict a 256 MB MALL.
 
-Per-launch time = replay time (HIP events on the replay stream) / launches per replay; the minimum and median over
-``reps`` replays are reported.
+Per-launch time = time of ``batch`` back-to-back replays (HIP events on the replay stream) / launches in them; the
+minimum and median over ``reps`` such samples are reported.
 """
 import statistics
 
@@ -43,9 +43,11 @@ class ColdCopies:
         return self.views[i % self.copies]
 
 
-def graph_time(launch, n, reps=5):
-    """Capture launch(i) for i in range(n) into one graph; returns (min_us, median_us) per launch over reps replays.
-    launch(i) is called once eagerly first so that code objects are loaded outside the capture."""
+def graph_time(launch, n, reps=5, batch=1):
+    """Capture launch(i) for i in range(n) into one graph; returns (min_us, median_us) per launch over reps samples,
+    each sample `batch` replays back to back between one pair of events (batch > 1 keeps the GPU busy across replays,
+    as in a decode loop: the first launches after the host synchronises with an idle GPU run slower). launch(i) is
+    called once eagerly first so that code objects are loaded outside the capture."""
     launch(0)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
@@ -58,9 +60,10 @@ def graph_time(launch, n, reps=5):
     for _ in range(reps):
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
-        g.replay()
+        for _ in range(batch):
+            g.replay()
         e.record()
         e.synchronize()
-        ts.append(s.elapsed_time(e) * 1e3 / n)
+        ts.append(s.elapsed_time(e) * 1e3 / (n * batch))
     del g
     return min(ts), statistics.median(ts)
