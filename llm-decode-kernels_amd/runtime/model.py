@@ -15,7 +15,9 @@ Differences from the reference, all on the device side of the same composition:
   * head_dim 64 and 128 (TinyLlama and Llama-3-8B shapes);
   * the argmax and the position increment run as one kernel (dk_argmax_advance) instead of two torch ops;
   * weights are quantized on the GPU by the HIP RTN kernel;
-  * there is no ``backend="ref"``: the CPU reference composition is test infrastructure (``oracle.decode_ref``).
+  * there is no ``backend="ref"``: the CPU reference composition is test infrastructure (``oracle.decode_ref``);
+  * the RoPE base is also found where transformers 5 keeps it (``rope_parameters``), and scaled RoPE types raise
+    (``rope_theta_of``).
 
 Knobs (DecodeConfig): weights "int4" | "fp16"; group; quant "rtn" | "clip" | "pre" (precomputed codes in qparams, e.g.
 from runtime.gptq.calibrate); lm_head "auto" | "fp16" | "int4"; fused (False runs the
@@ -78,6 +80,23 @@ class DecodeConfig:
     swiglu: str = "epilogue"       # where SwiGLU runs when fused_gemv is on: "epilogue" = inside the gate|up GEMV
                                    # (dk_gemv_w4a16_gate_up, gate/up rows stored interleaved); "kernel" = the separate
                                    # dk_swiglu launch
+
+
+def rope_theta_of(config):
+    """RoPE base of an HF-style config: its `rope_theta` attribute (transformers 4.x), else the "rope_theta" of its
+    `rope_parameters` / `rope_scaling` dict (transformers 5.x keeps it only there), else 10000. The reference reads
+    only the attribute (runtime/model.py:121) and so falls back to 10000 for a transformers-5 Llama-3 config (theta
+    500000). Scaled RoPE variants (a rope_type other than "default", e.g. Llama-3.1's "llama3") are not implemented
+    here and raise rather than rotate with the wrong frequencies."""
+    theta = getattr(config, "rope_theta", None)
+    params = getattr(config, "rope_parameters", None) or getattr(config, "rope_scaling", None)
+    if isinstance(params, dict):
+        rope_type = params.get("rope_type", params.get("type", "default"))
+        if rope_type not in (None, "default"):
+            raise NotImplementedError(f"rope_type {rope_type!r}: only the default (unscaled) RoPE is implemented")
+        if theta is None:
+            theta = params.get("rope_theta")
+    return float(theta) if theta is not None else 10000.0
 
 
 def default_gemv_config(N, K):
@@ -156,6 +175,8 @@ class Model:
                              "composition is oracle.decode_ref (test infrastructure)")
         if self.D not in (64, 128):
             raise ValueError(f"head_dim {self.D} not supported (64 or 128)")
+        if getattr(c, "head_dim", None) not in (None, self.D):
+            raise ValueError(f"config head_dim {c.head_dim} != hidden_size / num_attention_heads = {self.D}")
         dev = cfg.device
         self.K = ext.load()
         quant = cfg.weights == "int4"
@@ -210,8 +231,7 @@ class Model:
         gen = torch.Generator().manual_seed(cfg.seed)
         perm = torch.randperm(self.n_pages, generator=gen) if cfg.shuffle_pages else torch.arange(self.n_pages)
         self.bt = perm.int().to(dev)
-        theta = getattr(c, "rope_theta", 10000.0)
-        self.cos, self.sin = (t.to(dev) for t in rope_tables(cfg.max_ctx + 1, self.D, theta))
+        self.cos, self.sin = (t.to(dev) for t in rope_tables(cfg.max_ctx + 1, self.D, rope_theta_of(c)))
 
         self.attn_version = cfg.attn_version or self._policy().get("version", 3)
         self.set_attention_partition(cfg.max_ctx)

@@ -1,0 +1,63 @@
+"""The decode runtime against an independent implementation of the architecture: transformers' LlamaForCausalLM in
+fp32 on the CPU, on the same random-init weights (the role of the reference's tests/test_runtime_local.py, which
+compares its runtime with HF on the TinyLlama checkpoint; no checkpoint can be fetched here, so the weights are
+seeded random values and the prompt is random token ids). This pins the composition itself -- fused qkv / gate|up
+rows, the rotate_half RoPE convention and its theta, GQA head grouping, the paged cache with shuffled pages, the
+residual flow and both norms -- against code that shares nothing with this build or its oracle.
+
+Bars: the reference's (tests/test_runtime_local.py:26-27) with fp16 weights -- max |logit difference| < 0.5 over the
+prompt and top-1 flips only where HF's top1 - top2 margin is below 0.25 -- and, because these random-weight logits
+spread over only a few units, also this build's whole-step bar, 2e-2 normwise. INT4 weights carry quantization
+error, so as in the reference they are only reported (and required to be finite)."""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _hf(hidden, layers, heads, kv_heads, inter, vocab, theta, seed):
+    from transformers import LlamaConfig, LlamaForCausalLM
+    torch.manual_seed(seed)
+    cfg = LlamaConfig(vocab_size=vocab, hidden_size=hidden, intermediate_size=inter, num_hidden_layers=layers,
+                      num_attention_heads=heads, num_key_value_heads=kv_heads, max_position_embeddings=256,
+                      rms_norm_eps=1e-5, rope_theta=theta, tie_word_embeddings=False)
+    hf = LlamaForCausalLM(cfg).eval()
+    with torch.no_grad():  # HF's default init (std 0.02, unit norms) leaves logits nearly flat; spread them
+        for name, p in hf.named_parameters():
+            if name.endswith("norm.weight"):
+                p.copy_(1.0 + 0.1 * torch.randn_like(p))
+            else:
+                p.copy_(torch.randn_like(p) * (0.08 if "embed" in name else 0.05))
+    return hf
+
+
+@pytest.mark.parametrize("dims", [(256, 2, 4, 2, 512, 1000, 10000.0), (512, 2, 4, 2, 1024, 1000, 500000.0),
+                                  (512, 3, 8, 2, 1536, 2000, 10000.0)],
+                         ids=["D64", "D128-theta5e5", "D64-GQA4"])
+def test_runtime_matches_hf(dims):
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from runtime.model import DecodeConfig, Model
+    hf = _hf(*dims, seed=sum(dims[:6]))
+    ids = torch.randint(0, dims[5], (40,), generator=torch.Generator().manual_seed(dims[0]))
+    with torch.no_grad():
+        ref = hf(ids[None]).logits[0].float()
+    sd = {k: v.half() for k, v in hf.state_dict().items()}
+    top2 = ref.topk(2, -1).values
+    margin = top2[:, 0] - top2[:, 1]
+    for wfmt in ("fp16", "int4"):
+        m = Model(sd, hf.config, DecodeConfig(weights=wfmt, lm_head="fp16", max_ctx=64, device=DEV))
+        m.prepare(48)
+        m.reset(0)
+        out = m.teacher_force(ids, collect_logits=True).float().cpu()
+        diff = (out - ref).abs().max().item()
+        rel = ((out - ref).norm() / ref.norm()).item()
+        flips = out.argmax(-1) != ref.argmax(-1)
+        print(f"{dims} {wfmt}: max |dlogit| {diff:.4f}, normwise {rel:.2e}, top-1 agreement {1 - flips.float().mean().item():.3f}, "
+              f"flipped at {flips.nonzero().flatten().tolist()} (HF margins {margin[flips].tolist()})", flush=True)
+        assert torch.isfinite(out).all()
+        if wfmt == "fp16":
+            assert diff < 0.5 and rel < 2e-2 and bool((margin[flips] < 0.25).all()), (diff, rel, margin[flips])
+        del m
+        torch.cuda.empty_cache()

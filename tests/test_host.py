@@ -68,3 +68,25 @@ def test_attention_policy_entries_are_launchable():
         # the lookup picks the entry tuned at the largest context <= the cap
         for e in ents[:-1]:
             assert Model._policy_entry_of(pol, D, e["max_ctx"]) == e
+
+
+def test_rope_theta_from_hf_configs():
+    """The RoPE base comes from the config whichever way transformers stores it: the rope_theta attribute (4.x) or
+    the rope_parameters dict (5.x, which has no attribute: reading only the attribute, as the reference's
+    runtime/model.py:121 does, would rotate a Llama-3 config with base 10000 instead of 500000). Scaled RoPE types
+    are refused instead of computed with the wrong frequencies."""
+    import types
+    import pytest
+    from runtime.model import rope_theta_of
+    assert rope_theta_of(types.SimpleNamespace(rope_theta=500000.0)) == 500000.0
+    assert rope_theta_of(types.SimpleNamespace(rope_parameters={"rope_theta": 500000.0, "rope_type": "default"})) == 5e5
+    assert rope_theta_of(types.SimpleNamespace(rope_scaling=None)) == 10000.0
+    assert rope_theta_of(LLAMA3_8B) == 500000.0 and rope_theta_of(TINYLLAMA) == 10000.0
+    with pytest.raises(NotImplementedError, match="llama3"):
+        rope_theta_of(types.SimpleNamespace(rope_parameters={"rope_theta": 5e5, "rope_type": "llama3", "factor": 8.0}))
+    try:
+        from transformers import LlamaConfig
+    except ImportError:
+        return
+    assert rope_theta_of(LlamaConfig(rope_theta=500000.0)) == 500000.0
+    assert rope_theta_of(LlamaConfig()) == 10000.0
