@@ -3,7 +3,8 @@ fp32 on the CPU, on the same random-init weights (the role of the reference's te
 compares its runtime with HF on the TinyLlama checkpoint; no checkpoint can be fetched here, so the weights are
 seeded random values and the prompt is random token ids). This pins the composition itself -- fused qkv / gate|up
 rows, the rotate_half RoPE convention and its theta, GQA head grouping, the paged cache with shuffled pages, the
-residual flow and both norms -- against code that shares nothing with this build or its oracle.
+residual flow and both norms -- against code that shares nothing with this build or its oracle; with fp16 weights
+also the one-pass prompt path (Model.prefill), by the last prompt position's logits.
 
 Bars: the reference's (tests/test_runtime_local.py:26-27) with fp16 weights -- max |logit difference| < 0.5 over the
 prompt and top-1 flips only where HF's top1 - top2 margin is below 0.25 -- and, because these random-weight logits
@@ -59,5 +60,12 @@ def test_runtime_matches_hf(dims):
         assert torch.isfinite(out).all()
         if wfmt == "fp16":
             assert diff < 0.5 and rel < 2e-2 and bool((margin[flips] < 0.25).all()), (diff, rel, margin[flips])
+            # the one-pass prompt path (Model.prefill) against the same HF forward: last-position logits
+            m.reset(0)
+            m.prefill(ids)
+            last = m.logits.float().cpu()
+            prel = ((last - ref[-1]).norm() / ref[-1].norm()).item()
+            print(f"{dims} {wfmt} prefill: last-token logits normwise {prel:.2e}", flush=True)
+            assert prel < 2e-2 and int(m.tok) == int(last.argmax()), prel
         del m
         torch.cuda.empty_cache()
