@@ -177,6 +177,12 @@ class Model:
             raise ValueError(f"head_dim {self.D} not supported (64 or 128)")
         if getattr(c, "head_dim", None) not in (None, self.D):
             raise ValueError(f"config head_dim {c.head_dim} != hidden_size / num_attention_heads = {self.D}")
+        if getattr(c, "attention_bias", False) or getattr(c, "mlp_bias", False):
+            raise NotImplementedError("projection biases (attention_bias / mlp_bias): the Llama composition this "
+                                      "runtime implements has none")
+        if getattr(c, "hidden_act", "silu") not in ("silu", "swish"):
+            raise NotImplementedError(f"hidden_act {c.hidden_act!r}: the SwiGLU kernels implement silu only")
+        self.rope_theta = rope_theta_of(c)   # raises for scaled RoPE types
         dev = cfg.device
         self.K = ext.load()
         quant = cfg.weights == "int4"
@@ -231,7 +237,7 @@ class Model:
         gen = torch.Generator().manual_seed(cfg.seed)
         perm = torch.randperm(self.n_pages, generator=gen) if cfg.shuffle_pages else torch.arange(self.n_pages)
         self.bt = perm.int().to(dev)
-        self.cos, self.sin = (t.to(dev) for t in rope_tables(cfg.max_ctx + 1, self.D, rope_theta_of(c)))
+        self.cos, self.sin = (t.to(dev) for t in rope_tables(cfg.max_ctx + 1, self.D, self.rope_theta))
 
         self.attn_version = cfg.attn_version or self._policy().get("version", 3)
         self.set_attention_partition(cfg.max_ctx)

@@ -374,3 +374,21 @@ def test_model_rejects_ref_backend():
     from runtime.synth import LlamaShape
     with pytest.raises(ValueError, match="oracle.decode_ref"):
         Model({}, LlamaShape(128, 1, 2, 1, 256, 64), DecodeConfig(backend="ref", device="cpu"))
+
+
+@pytest.mark.parametrize("extra,exc,msg", [
+    (dict(attention_bias=True), NotImplementedError, "projection biases"),
+    (dict(mlp_bias=True), NotImplementedError, "projection biases"),
+    (dict(hidden_act="gelu"), NotImplementedError, "silu only"),
+    (dict(rope_parameters={"rope_theta": 5e5, "rope_type": "llama3", "factor": 8.0}), NotImplementedError, "llama3"),
+    (dict(head_dim=96), ValueError, "head_dim"),
+])
+def test_model_rejects_unsupported_configs(extra, exc, msg):
+    """Configurations outside the Llama composition the kernels implement are refused before any weight is read,
+    instead of running with parts of the model silently dropped."""
+    import types
+    from runtime.model import DecodeConfig, Model
+    c = types.SimpleNamespace(hidden_size=128, num_hidden_layers=1, num_attention_heads=2, num_key_value_heads=1,
+                              intermediate_size=256, vocab_size=64, rms_norm_eps=1e-5, **extra)
+    with pytest.raises(exc, match=msg):
+        Model({}, c, DecodeConfig(device="cpu"))
