@@ -11,7 +11,8 @@ cold weights (runtime.timing), and writes
                              "best_f16_norm": {"NxK": [R, waves, pf]} of the fp16 GEMV, "us_*": times,
                              "grid": [every measurement]}
 
-The runtime (runtime.model.Model.gemv_cfg) reads "best"; 3-element entries [R, warps, pf] of the reference's schema
+The runtime (runtime.model.Model.gemv_cfg) reads "best" ("best_tile" is informational: the fastest stage-4
+configuration of a shape whose overall best is another stage); 3-element entries [R, warps, pf] of the reference's schema
 are read as stage 2. Run:  python -m runtime.autotune [--shapes tinyllama,llama3_8b,baseline] [--groups 128]
 With --attention it tunes the decode attention instead (kernel and split size per head dim and context) and writes
 configs/attn_policy.json; with --step it chooses the decode step's GEMV configurations by the step time ("best_step").

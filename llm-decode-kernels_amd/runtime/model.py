@@ -216,13 +216,13 @@ class Model:
         head_int4 = cfg.lm_head == "int4" or (cfg.lm_head == "auto" and quant)
         self.lm_head = Linear(lm.half(), cfg, head_int4, key="lm_head")
 
-        self.gemv_table, self.gemv_tile_table, self.gemv_norm_table, self.gemv_gate_up_table = {}, {}, {}, {}
+        self.gemv_table, self.gemv_norm_table, self.gemv_gate_up_table = {}, {}, {}
         self.gemv_f16_table, self.gemv_f16_norm_table = {}, {}
         self.gemv_us, self.gemv_norm_us = {}, {}
         self.step_cfg_override = {}
         if cfg.gemv_stage is None and Path(cfg.autotune_path).exists():
             tab = json.load(open(cfg.autotune_path))
-            self.gemv_table, self.gemv_tile_table = tab.get("best", {}), tab.get("best_tile", {})
+            self.gemv_table = tab.get("best", {})
             self.gemv_norm_table = tab.get("best_norm", {})
             self.gemv_us, self.gemv_norm_us = tab.get("us", {}), tab.get("us_norm", {})
             self.gemv_gate_up_table = tab.get("best_gate_up", {})
@@ -326,14 +326,6 @@ class Model:
         if e is None:
             return default_gemv_config(lin.N, lin.K)
         return tuple(e) if len(e) == 4 else (2, *e)      # [R, warps, pf] is the reference's stage-2 schema
-
-    def gemv_tile_cfg(self, lin):
-        """Stage-4 (row tile) configuration for the fused-prologue GEMVs: the tuned stage-4 entry, else R=2, 1 tile."""
-        e = self.gemv_tile_table.get(f"{lin.N}x{lin.K}_G{self.cfg.group}")
-        if e is None:
-            e = self.gemv_table.get(f"{lin.N}x{lin.K}_G{self.cfg.group}")
-            e = tuple(e) if e is not None and len(e) == 4 and e[0] == 4 else None
-        return tuple(e) if e is not None else (4, 2, 0, 0)
 
     def gemv_norm_cfg(self, lin):
         """Configuration of the fused-norm GEMV: its own tuned entry (every workgroup recomputes the norm, so larger
