@@ -4,7 +4,8 @@ compares its runtime with HF on the TinyLlama checkpoint; no checkpoint can be f
 seeded random values and the prompt is random token ids). This pins the composition itself -- fused qkv / gate|up
 rows, the rotate_half RoPE convention and its theta, GQA head grouping, the paged cache with shuffled pages, the
 residual flow and both norms -- against code that shares nothing with this build or its oracle; with fp16 weights
-also the one-pass prompt path (Model.prefill), by the last prompt position's logits.
+also the one-pass prompt path (Model.prefill), by the last prompt position's logits, and greedy generation against
+HF's generate.
 
 Bars: the reference's (tests/test_runtime_local.py:26-27) with fp16 weights -- max |logit difference| < 0.5 over the
 prompt and top-1 flips only where HF's top1 - top2 margin is below 0.25 -- and, because these random-weight logits
@@ -55,8 +56,8 @@ def test_runtime_matches_hf(dims):
         diff = (out - ref).abs().max().item()
         rel = ((out - ref).norm() / ref.norm()).item()
         flips = out.argmax(-1) != ref.argmax(-1)
-        print(f"{dims} {wfmt}: max |dlogit| {diff:.4f}, normwise {rel:.2e}, top-1 agreement {1 - flips.float().mean().item():.3f}, "
-              f"flipped at {flips.nonzero().flatten().tolist()} (HF margins {margin[flips].tolist()})", flush=True)
+        print(f"{dims} {wfmt}: max |dlogit| {diff:.4f}, normwise {rel:.2e}, "
+              f"top-1 agreement {1 - flips.float().mean().item():.3f}, flipped at {flips.nonzero().flatten().tolist()} (HF margins {margin[flips].tolist()})", flush=True)
         assert torch.isfinite(out).all()
         if wfmt == "fp16":
             assert diff < 0.5 and rel < 2e-2 and bool((margin[flips] < 0.25).all()), (diff, rel, margin[flips])
@@ -67,5 +68,18 @@ def test_runtime_matches_hf(dims):
             prel = ((last - ref[-1]).norm() / ref[-1].norm()).item()
             print(f"{dims} {wfmt} prefill: last-token logits normwise {prel:.2e}", flush=True)
             assert prel < 2e-2 and int(m.tok) == int(last.argmax()), prel
+            # greedy generation (runtime/model.py:278-286) against HF's greedy generate: the same tokens up to the
+            # first position where HF's own top1 - top2 margin is a near-tie
+            with torch.no_grad():
+                hf_new = hf.generate(ids[None], max_new_tokens=8, do_sample=False, pad_token_id=0)[0, len(ids):]
+                seq = torch.cat([ids, hf_new[:-1]])
+                t2 = hf(seq[None]).logits[0, len(ids) - 1:].float().topk(2, -1).values
+            gm = (t2[:, 0] - t2[:, 1]).tolist()
+            for mode, got in (("teacher-forced prompt", m.generate(ids, 8)),
+                              ("prefill", m.generate(ids, 8, prefill=True))):
+                for i, (a, b) in enumerate(zip(got, hf_new.tolist())):
+                    if a != b:
+                        assert gm[i] < 0.05, (mode, i, a, b, gm[i])
+                        break
         del m
         torch.cuda.empty_cache()
