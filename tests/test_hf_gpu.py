@@ -57,7 +57,8 @@ def test_runtime_matches_hf(dims):
         rel = ((out - ref).norm() / ref.norm()).item()
         flips = out.argmax(-1) != ref.argmax(-1)
         print(f"{dims} {wfmt}: max |dlogit| {diff:.4f}, normwise {rel:.2e}, "
-              f"top-1 agreement {1 - flips.float().mean().item():.3f}, flipped at {flips.nonzero().flatten().tolist()} (HF margins {margin[flips].tolist()})", flush=True)
+              f"top-1 agreement {1 - flips.float().mean().item():.3f}, flipped at {flips.nonzero().flatten().tolist()} "
+              f"(HF margins {margin[flips].tolist()})", flush=True)
         assert torch.isfinite(out).all()
         if wfmt == "fp16":
             assert diff < 0.5 and rel < 2e-2 and bool((margin[flips] < 0.25).all()), (diff, rel, margin[flips])
