@@ -35,8 +35,9 @@ def _hf(hidden, layers, heads, kv_heads, inter, vocab, theta, seed):
 
 
 @pytest.mark.parametrize("dims", [(256, 2, 4, 2, 512, 1000, 10000.0), (512, 2, 4, 2, 1024, 1000, 500000.0),
-                                  (512, 3, 8, 2, 1536, 2000, 10000.0)],
-                         ids=["D64", "D128-theta5e5", "D64-GQA4"])
+                                  (512, 3, 8, 2, 1536, 2000, 10000.0), (256, 2, 4, 4, 512, 1000, 10000.0),
+                                  (1024, 2, 16, 2, 2048, 1000, 10000.0)],
+                         ids=["D64", "D128-theta5e5", "D64-GQA4", "D64-MHA", "D64-GQA8"])
 def test_runtime_matches_hf(dims):
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
