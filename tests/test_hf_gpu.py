@@ -10,7 +10,8 @@ HF's generate.
 Bars: the reference's (tests/test_runtime_local.py:26-27) with fp16 weights -- max |logit difference| < 0.5 over the
 prompt and top-1 flips only where HF's top1 - top2 margin is below 0.25 -- and, because these random-weight logits
 spread over only a few units, also this build's whole-step bar, 2e-2 normwise. INT4 weights carry quantization
-error, so as in the reference they are only reported (and required to be finite)."""
+error, so as in the reference they are only reported (and required to be finite); with projection weights chosen on
+the INT4 grid, where RTN is lossless, the INT4 path is held to the fp16 bars."""
 import pytest
 import torch
 
@@ -85,3 +86,55 @@ def test_runtime_matches_hf(dims):
                         break
         del m
         torch.cuda.empty_cache()
+
+
+def _int4_exact_(w, group=128, seed=0):
+    """Overwrite w [N, K] with values RTN reproduces exactly: per (row, group of `group`) an fp16 scale s = m 2^-10
+    (m in 4..7) and integer zero z, codes q in [0, 15] with 0 and 15 both present, w = (q - z) s (at most 7 significant
+    bits: exact in fp16). runtime/quant.py's group_params then recovers s and z exactly, so the INT4 model computes
+    with exactly these weights."""
+    g = torch.Generator().manual_seed(seed)
+    N, K = w.shape
+    q = torch.randint(0, 16, (N, K // group, group), generator=g)
+    q[:, :, 0], q[:, :, 1] = 0, 15
+    perm = torch.argsort(torch.rand(N, K // group, group, generator=g), -1)
+    q = torch.gather(q, -1, perm)
+    z = torch.randint(0, 16, (N, K // group, 1), generator=g)
+    s = torch.randint(4, 8, (N, K // group, 1), generator=g).float() * 2.0 ** -10
+    w.copy_(((q - z).float() * s).reshape(N, K))
+
+
+@pytest.mark.parametrize("dims", [(256, 2, 4, 2, 512, 1000, 10000.0), (512, 2, 4, 2, 1024, 1000, 500000.0)],
+                         ids=["D64", "D128-theta5e5"])
+def test_int4_runtime_matches_hf_on_exact_weights(dims):
+    """The INT4 path end to end against HF: projection weights chosen on the INT4 grid (RTN loses nothing), so the
+    runtime's packed codes dequantize to exactly HF's weights and its logits must meet the fp16 bars (the embedding,
+    the norms and the fp16 LM head stay random)."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from runtime.model import DecodeConfig, Model
+    hf = _hf(*dims, seed=7 + dims[0])
+    with torch.no_grad():
+        for i, (name, p) in enumerate(hf.named_parameters()):
+            if name.endswith("_proj.weight"):
+                _int4_exact_(p, seed=i)
+        ids = torch.randint(0, dims[5], (40,), generator=torch.Generator().manual_seed(dims[0] + 1))
+        ref = hf(ids[None]).logits[0].float()
+    sd = {k: v.half() for k, v in hf.state_dict().items()}
+    m = Model(sd, hf.config, DecodeConfig(weights="int4", group=128, lm_head="fp16", max_ctx=64, device=DEV))
+    qkv = m.layers[0]["qkv"]                  # the codes' dequantization is HF's weight, bit for bit
+    from oracle import quant_ref as Q
+    w_hf = torch.cat([sd["model.layers.0.self_attn.q_proj.weight"], sd["model.layers.0.self_attn.k_proj.weight"],
+                      sd["model.layers.0.self_attn.v_proj.weight"]], 0)
+    assert torch.equal(Q.dequantize_packed(qkv.packed, qkv.sz, 128).cpu(), w_hf)
+    m.prepare(48)
+    m.reset(0)
+    out = m.teacher_force(ids, collect_logits=True).float().cpu()
+    rel = ((out - ref).norm() / ref.norm()).item()
+    diff = (out - ref).abs().max().item()
+    top2 = ref.topk(2, -1).values
+    margin = top2[:, 0] - top2[:, 1]
+    flips = out.argmax(-1) != ref.argmax(-1)
+    print(f"{dims} int4 on the INT4 grid: max |dlogit| {diff:.4f}, normwise {rel:.2e}, flips {int(flips.sum())}",
+          flush=True)
+    assert diff < 0.5 and rel < 2e-2 and bool((margin[flips] < 0.25).all()), (diff, rel, margin[flips])
