@@ -138,3 +138,9 @@ def test_int4_runtime_matches_hf_on_exact_weights(dims):
     print(f"{dims} int4 on the INT4 grid: max |dlogit| {diff:.4f}, normwise {rel:.2e}, flips {int(flips.sum())}",
           flush=True)
     assert diff < 0.5 and rel < 2e-2 and bool((margin[flips] < 0.25).all()), (diff, rel, margin[flips])
+    m.reset(0)
+    m.prefill(ids)                            # the W4A16 MFMA GEMM path of the prompt
+    last = m.logits.float().cpu()
+    prel = ((last - ref[-1]).norm() / ref[-1].norm()).item()
+    print(f"{dims} int4 prefill: last-token logits normwise {prel:.2e}", flush=True)
+    assert prel < 2e-2, prel
