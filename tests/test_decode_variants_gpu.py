@@ -8,11 +8,12 @@ the reference's backend="ref" composition, runtime/model.py:216-233) with the ba
   * head_dim 128 (Llama-3-8B widths: hidden 4096, 32 q / 8 kv heads, SwiGLU 14336) with G64 and an INT4 head over
     2 layers.
 
-Each case starts both decoders from the same seeded K/V cache at its context and steps 8 greedy tokens."""
+Each case starts both decoders from the same seeded K/V cache at its context and steps 32 greedy tokens (the oracle
+runs the GPU's greedy tokens as one batch of teacher-forced steps)."""
 import pytest
 import torch
 
-from test_full_depth_gpu import check, fill_cache, oracle_weights, run_greedy
+from test_full_depth_gpu import check, fill_cache, greedy_on_gpu, oracle_steps, oracle_weights, records
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -35,13 +36,15 @@ def test_decode_variant_against_oracle(name, widths, over, ctx):
     from runtime.model import DecodeConfig, Model
     from runtime.synth import LlamaShape, SyntheticLlama
     shape = LlamaShape(*widths)
-    steps = 8
+    steps = 32
     print(f"decode variant {name}: ctx {ctx}", flush=True)
-    m = Model(SyntheticLlama(shape, seed=len(name)), shape, DecodeConfig(max_ctx=ctx + 32, device=DEV, **over))
+    m = Model(SyntheticLlama(shape, seed=len(name)), shape, DecodeConfig(max_ctx=ctx + 64, device=DEV, **over))
     m.prepare(ctx + steps + 16)
     ref = RefDecoder(oracle_weights(m), shape, max_ctx=m.cfg.max_ctx, page=m.cfg.page, block_table=m.bt.cpu(),
                      rope_theta=shape.rope_theta)
     fill_cache(m, ref, seed=ctx + 1)
-    check(run_greedy(m, ref, ctx, steps, seed=ctx + 2), m, ref, ctx, name)
+    inputs, gpu_logits, gpu_tok = greedy_on_gpu(m, ctx, steps, seed=ctx + 2)
+    ref_logits, ref_tok = oracle_steps(ref, inputs, ctx, keep_from=ctx)
+    check(records(gpu_logits, gpu_tok, ref_logits, ref_tok), m, ref, ctx, ctx + steps, name)
     del m, ref
     torch.cuda.empty_cache()

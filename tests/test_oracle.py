@@ -414,3 +414,35 @@ def test_decode_ref_matches_float64_llama():
         logits, _ = dec.step(t, pos)
         err = (logits.double() - want[pos]).abs().max()
         assert err <= 2e-2 * want[pos].abs().max(), (pos, float(err))
+
+
+def test_decode_ref_batched_steps_equal_sequential_steps():
+    """RefDecoder.steps (T teacher-forced steps in one pass) is T calls of RefDecoder.step: same logits up to the fp32
+    summation order of the products, same greedy tokens, same cache rows; also from a pre-filled cache (pos0 > 0)."""
+    sh = _Shape
+    g = torch.Generator().manual_seed(12)
+    H, I, V = sh.hidden_size, sh.intermediate_size, sh.vocab_size
+    D = H // sh.num_attention_heads
+    qkv_rows = (sh.num_attention_heads + 2 * sh.num_key_value_heads) * D
+    mk = lambda *s: (torch.randn(*s, generator=g) * 0.1).half()
+    w = {"emb": mk(V, H), "norm_f": (1 + 0.1 * torch.randn(H, generator=g)).half(), "lm_head": mk(V, H),
+         "layers": [{"ln1": (1 + 0.1 * torch.randn(H, generator=g)).half(),
+                     "ln2": (1 + 0.1 * torch.randn(H, generator=g)).half(),
+                     "qkv": mk(qkv_rows, H), "o": mk(H, H), "gu": mk(2 * I, H), "down": mk(H, I)}
+                    for _ in range(sh.num_hidden_layers)]}
+    bt = torch.randperm(5, generator=g).int()
+    tokens = [3, 17, 60, 5, 41, 22, 9, 33, 1, 50, 7, 28, 44, 12, 36, 19, 58, 2, 11, 40]
+    seq = RefDecoder(w, sh, max_ctx=64, page=16, block_table=bt)
+    want = [seq.step(t, p) for p, t in enumerate(tokens)]
+    for split in (0, 7):                                   # all rows at once; 7 sequential steps then a batch
+        bat = RefDecoder(w, sh, max_ctx=64, page=16, block_table=bt)
+        for p in range(split):
+            bat.step(tokens[p], p)
+        logits, top = bat.steps(tokens[split:], split)
+        for r, (lw, tw) in enumerate(want[split:]):
+            d = (logits[r].float() - lw.float()).abs().max()
+            assert d <= 2e-3 * lw.float().abs().max(), (split, r, float(d))
+            margin = lw.float().topk(2).values
+            assert int(top[r]) == tw or float(margin[0] - margin[1]) <= 2 * float(d), (split, r)
+        d = (bat.kv.float() - seq.kv.float()).abs().max()
+        assert d <= 2e-3 * seq.kv.float().abs().max(), float(d)
