@@ -70,28 +70,10 @@ def leg_caps(ctx, steps, warmup):
     return caps
 
 
-def _pci_dir():
-    import torch
-    p = torch.cuda.get_device_properties(0)
-    return pathlib.Path(f"/sys/bus/pci/devices/{p.pci_domain_id:04x}:{p.pci_bus_id:02x}:{p.pci_device_id:02x}.0")
-
-
 def read_clocks(pci):
-    """One sample: current shader / memory / fabric clock (the starred line of pp_dpm_*) and edge temperature."""
-    out = {}
-    for key, f in (("sclk_mhz", "pp_dpm_sclk"), ("mclk_mhz", "pp_dpm_mclk"), ("fclk_mhz", "pp_dpm_fclk")):
-        try:
-            for line in (pci / f).read_text().splitlines():
-                if line.rstrip().endswith("*"):
-                    out[key] = int("".join(ch for ch in line.split(":", 1)[1] if ch.isdigit()))
-        except (OSError, ValueError, IndexError):
-            pass
-    for t in sorted(pci.glob("hwmon/hwmon*/temp1_input")):
-        try:
-            out["temp_c"] = int(t.read_text()) / 1000
-        except (OSError, ValueError):
-            pass
-    return out
+    """One clock sample of the GPU at sysfs directory pci (runtime.timing.read_clocks)."""
+    from runtime.timing import read_clocks as rc
+    return rc(pci)
 
 
 class ClockSampler:
@@ -100,11 +82,9 @@ class ClockSampler:
 
     def __init__(self, period=0.02):
         import threading
+        from runtime.timing import gpu_sysfs_dir
         self.period, self.samples, self.stop = period, [], threading.Event()
-        try:
-            self.pci = _pci_dir()
-        except Exception:                                 # noqa: BLE001 (no device properties: no samples)
-            self.pci = None
+        self.pci = gpu_sysfs_dir()
         self.thread = threading.Thread(target=self._run, daemon=True)
 
     def _run(self):
@@ -125,12 +105,8 @@ class ClockSampler:
             self.thread.join()
 
     def summary(self):
-        out = {"samples": len(self.samples)}
-        for k in ("sclk_mhz", "mclk_mhz", "fclk_mhz", "temp_c"):
-            v = sorted(s[k] for s in self.samples if k in s)
-            if v:
-                out[k] = {"min": v[0], "median": v[len(v) // 2], "max": v[-1]}
-        return out
+        from runtime.timing import clock_summary
+        return clock_summary(self.samples)
 
 
 def traffic_leg(nbytes, timeout=180):
@@ -153,7 +129,7 @@ def traffic_leg(nbytes, timeout=180):
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
         d = tmp / counter.lower()
         cmd = [exe, "--pmc", counter, "--output-format", "csv", "-d", str(d), "-o", "pmc", "--",
-               sys.executable, str(ROOT / "bench.py"), "--leg", "gemv"]
+               sys.executable, str(ROOT / "bench.py"), "--leg", "gemv", "--warm-ms", "2", "--window-ms", "5"]
         log(f"traffic: rocprofv3 --pmc {counter} over bench.py --leg gemv")
         p = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL, stderr=subprocess.PIPE,
                              start_new_session=True)
@@ -187,19 +163,26 @@ def tuned_config(N, K, G=128):
     return tuple(e) if len(e) == 4 else (2, *e)
 
 
-# replays per timed sample of the GEMV legs and their read ceiling: the cold copies' graph is replayed back to back,
-# so the GPU stays busy across replays as in the decode loop (a replay that follows a host synchronisation with an
-# idle GPU runs its first launches slower: 7.53-7.58 us per launch one replay at a time, 7.36 back to back)
-GEMV_BATCH = 4
+# Clock-gated timing windows of the standalone kernel legs (runtime.timing.windowed_time): warm_ms of back-to-back
+# replays queued ahead of window_ms of timed samples, the shader clock read inside the window. The counter passes
+# (traffic_leg) shorten them, since every dispatch under rocprofv3 --pmc is serialized and counted.
+WINDOW = {"warm_ms": 300.0, "window_ms": 60.0}
+
+
+def window_record(w):
+    """The timing window's fields that a leg reports."""
+    return {"window_samples_us": w["samples_us"], "window_batch": w["batch"], "warm_ms": w["warm_ms"],
+            "window_attempts": w["attempts"], "window_clocks": w["clocks"], "throttled": w["throttled"]}
 
 
 def gemv_leg(Kx, N, Kd, G=128, reps=7):
-    """Mean per-launch duration of the tuned W4A16 GEMV with cold weights (hipGraph of back-to-back launches, GEMV_BATCH
-    replays per timed sample)."""
+    """Per-launch duration of the tuned W4A16 GEMV with cold weights: a hipGraph of back-to-back launches over cold
+    copies, clock-warmed, `reps` timed samples (runtime.timing.windowed_time); mean_us is the median over the samples
+    of the per-launch mean of each."""
     import torch
     from runtime.autotune import gemv_bytes
     from runtime.quant import quantize_pack
-    from runtime.timing import ColdCopies, graph_time, n_copies
+    from runtime.timing import ColdCopies, n_copies, windowed_time
 
     nbytes = gemv_bytes(N, Kd, G)
     g = torch.Generator(device="cuda").manual_seed(N * 7 + Kd)
@@ -208,47 +191,74 @@ def gemv_leg(Kx, N, Kd, G=128, reps=7):
     y = torch.empty(N, dtype=torch.half, device="cuda")
     cfg = tuned_config(N, Kd, G)
     cold = ColdCopies([packed, sz], n_copies(nbytes))
-    mn, med = graph_time(lambda i: Kx.gemv_w4a16(*cfg, *cold[i], x, y, G), cold.copies, reps, batch=GEMV_BATCH)
-    launches = cold.copies * (reps * GEMV_BATCH + 2)
+    w = windowed_time(lambda i: Kx.gemv_w4a16(*cfg, *cold[i], x, y, G), cold.copies, reps, **WINDOW)
+    med = w["median_us"]
     del cold
     return {"N": N, "K": Kd, "group": G, "cfg": list(cfg), "bytes": nbytes, "mean_us": round(med, 3),
-            "min_us": round(mn, 3), "gbps": round(nbytes / med / 1e3, 1), "frac": round(nbytes / med / 1e3 / HBM_PEAK_GBS, 4),
-            "launches": launches}
+            "min_us": round(w["min_us"], 3), "gbps": round(nbytes / med / 1e3, 1),
+            "frac": round(nbytes / med / 1e3 / HBM_PEAK_GBS, 4), **window_record(w)}
+
+
+# read-probe launch shapes swept for the read ceiling: persistent grids of 256..2048 workgroups of 256..1024 threads
+# with 4..16 16-byte loads in flight per lane, and the one-load-per-thread full grid (no grid stride) for comparison
+PROBE_GRIDS = [(b, t, u) for b in (256, 512, 1024, 2048) for t in (256, 512, 1024) for u in (4, 8, 16)]
+
+
+def probe_time(Kx, cold, nbytes, blocks, threads, unroll, reps=5, warm_ms=None, window_ms=None):
+    import torch
+    from runtime.timing import windowed_time
+    sink = torch.zeros(blocks * threads // 64, dtype=torch.int32, device="cuda")
+    return windowed_time(lambda i: Kx.bw_read(cold[i][0], sink, blocks, threads, unroll), cold.copies, reps,
+                         warm_ms=WINDOW["warm_ms"] if warm_ms is None else warm_ms,
+                         window_ms=WINDOW["window_ms"] / 2 if window_ms is None else window_ms)
 
 
 def read_ceiling_leg(Kx, nbytes, reps=5):
-    """Best bw_read time for the same byte count, cold (what a read-only kernel achieves at this size)."""
+    """The read probe over the same byte count, cold, at every launch shape of PROBE_GRIDS plus the full
+    one-load-per-thread grid: the best is what a read-only kernel achieves at this size (the GEMV's ceiling)."""
     import torch
-    from runtime.timing import ColdCopies, graph_time, n_copies
+    from runtime.timing import ColdCopies, n_copies
     src = torch.empty(nbytes // 16 * 16, dtype=torch.uint8, device="cuda")
     cold = ColdCopies([src], n_copies(nbytes))
-    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
-    best = None
-    for blocks, threads in ((nbytes // 16 // 512, 512), (nbytes // 16 // 256, 256)):
-        mn, med = graph_time(lambda i: Kx.bw_read(cold[i][0], sink, blocks, threads, 1), cold.copies, reps,
-                             batch=GEMV_BATCH)
-        if best is None or med < best[0]:
-            best = (med, blocks, threads)
+    grids = PROBE_GRIDS + [(nbytes // 16 // 512, 512, 1)]
+    sweep = []
+    for k, (b, t, u) in enumerate(grids):
+        w = probe_time(Kx, cold, nbytes, b, t, u, reps, warm_ms=WINDOW["warm_ms"] if k == 0 else 50.0)
+        sweep.append({"blocks": b, "threads": t, "unroll": u, "us": round(w["median_us"], 3),
+                      "sclk_median": w["clocks"].get("sclk_mhz", {}).get("median"), "throttled": w["throttled"]})
+    best = min(sweep, key=lambda r: r["us"])
+    full = sweep[-1]
+    # the best shape re-timed with the full warm-up and window (the reported figure)
+    w = probe_time(Kx, cold, nbytes, best["blocks"], best["threads"], best["unroll"], reps,
+                   window_ms=WINDOW["window_ms"])
     del cold
-    return {"bytes": nbytes, "mean_us": round(best[0], 3), "gbps": round(nbytes / best[0] / 1e3, 1),
-            "frac": round(nbytes / best[0] / 1e3 / HBM_PEAK_GBS, 4), "grid": [best[1], best[2]]}
+    med = w["median_us"]
+    return {"bytes": nbytes, "mean_us": round(med, 3), "gbps": round(nbytes / med / 1e3, 1),
+            "frac": round(nbytes / med / 1e3 / HBM_PEAK_GBS, 4),
+            "grid": [best["blocks"], best["threads"], best["unroll"]], **window_record(w),
+            "full_grid_one_load": {"grid": [full["blocks"], full["threads"], 1], "us": full["us"],
+                                   "frac": round(nbytes / full["us"] / 1e3 / HBM_PEAK_GBS, 4)},
+            "sweep": sweep}
 
 
-def read_sweep_leg(Kx, sizes_mb=(2, 4, 8, 16, 31.232, 64, 128, 256, 512), reps=5):
-    """bw_read over cold copies at sizes from 2 MB to 512 MB (best of two grids per size), and the least-squares fit
-    time = fixed + bytes / bandwidth: the per-launch fixed cost and the streaming bandwidth that bound any kernel
-    reading that many bytes once."""
+def read_sweep_leg(Kx, sizes_mb=(2, 4, 8, 16, 31.232, 64, 128, 256, 512), reps=5,
+                   grids=((256, 512, 8), (512, 512, 8), (1024, 512, 8), (1024, 1024, 16), (2048, 512, 16))):
+    """The read probe over cold copies at sizes from 2 MB to 512 MB (best of a few persistent grids per size), and the
+    least-squares fit time = fixed + bytes / bandwidth: the per-launch fixed cost and the streaming bandwidth that
+    bound any kernel reading that many bytes once."""
     import torch
-    from runtime.timing import ColdCopies, graph_time, n_copies
-    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    from runtime.timing import ColdCopies, n_copies
     pts = []
-    for mb in sizes_mb:
+    for k, mb in enumerate(sizes_mb):
         nbytes = int(mb * 1e6) // (16 * 512) * (16 * 512)
         cold = ColdCopies([torch.empty(nbytes, dtype=torch.uint8, device="cuda")], n_copies(nbytes, min_copies=2))
-        best = min(graph_time(lambda i: Kx.bw_read(cold[i][0], sink, nbytes // 16 // t, t, 1), cold.copies, reps,
-                              batch=GEMV_BATCH)[1] for t in (512, 256))
-        pts.append({"bytes": nbytes, "us": round(best, 3), "gbps": round(nbytes / best / 1e3, 1),
-                    "frac": round(nbytes / best / 1e3 / HBM_PEAK_GBS, 4)})
+        ts = []
+        for j, (b, t, u) in enumerate(grids):
+            w = probe_time(Kx, cold, nbytes, b, t, u, reps, warm_ms=WINDOW["warm_ms"] if k == j == 0 else 50.0)
+            ts.append((w["median_us"], [b, t, u], w["clocks"].get("sclk_mhz", {}).get("median")))
+        best = min(ts)
+        pts.append({"bytes": nbytes, "us": round(best[0], 3), "grid": best[1], "sclk_median": best[2],
+                    "gbps": round(nbytes / best[0] / 1e3, 1), "frac": round(nbytes / best[0] / 1e3 / HBM_PEAK_GBS, 4)})
         del cold
         torch.cuda.empty_cache()
     n = len(pts)
@@ -261,16 +271,16 @@ def read_sweep_leg(Kx, sizes_mb=(2, 4, 8, 16, 31.232, 64, 128, 256, 512), reps=5
 
 
 def calibration_leg(Kx, nbytes, n=16):
-    """Known-size kernels for scaling hardware byte counters: n bw_read launches that each read `nbytes` once
+    """Known-size kernels for scaling hardware byte counters: n read-probe launches that each read `nbytes` once
     (cold copies) and n device copies of `nbytes` (read + write once). Their FETCH_SIZE / WRITE_SIZE per dispatch,
     divided by nbytes, are the counter-to-HBM-bytes factors (runtime.rocprof_summary)."""
     import torch
     from runtime.timing import ColdCopies
     src = torch.empty(nbytes // 16 * 16, dtype=torch.uint8, device="cuda")
     cold = ColdCopies([src], n + 1)
-    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    sink = torch.zeros(1024 * 8, dtype=torch.int32, device="cuda")
     for i in range(n):
-        Kx.bw_read(cold[i][0], sink, nbytes // 16 // 512, 512, 1)
+        Kx.bw_read(cold[i][0], sink, 1024, 512, 8)
     torch.cuda.synchronize()
     for i in range(n):
         cold[i + 1][0].copy_(cold[i][0])
@@ -280,14 +290,19 @@ def calibration_leg(Kx, nbytes, n=16):
 
 def kernels_leg(Kx, n=64, reps=5):
     """BASELINE configs 2 and 3: the attention ops (32 q / 4 kv heads, D 64, page 16) at contexts 128..4096 and the
-    fused elementwise ops at TinyLlama sizes, each as the mean over a hipGraph of n back-to-back launches (inputs stay
-    L2-resident across launches, as in the reference's kernel bench), with GB/s by the algorithmic byte counts:
-    attention 1024 ctx (K and V) + 8192 (q, out) + ctx / 4 (block table); add_rmsnorm 10 H; swiglu 6 I; rope_append
-    4 D (n_q + 2 n_kv). Part size and kernel choice are the runtime's attention policy for each context."""
+    fused elementwise ops at TinyLlama sizes, with GB/s by the algorithmic byte counts: attention 1024 ctx (K and V)
+    + 8192 (q, out) + ctx / 4 (block table); add_rmsnorm 10 H; swiglu 6 I; rope_append 4 D (n_q + 2 n_kv). Part size
+    and kernel choice are the runtime's attention policy for each context; the reference op gets the policy's part
+    size (its caller passes it, runtime/model.py:160-178 of the reference) and version 3.
+    Attention is timed cold, as the reference times it with its read flush between iterations
+    (bench/kernel_bench.py:147-160, bench/timing.py:28-32): a clock-warmed hipGraph of back-to-back launches, each on
+    its own copy of the paged K/V, the copies together well over the 256 MB MALL (keys *_us, *_gbps); the hot figure
+    (one K/V for n launches, L2-resident) is kept beside it (*_hot_us). The elementwise ops are timed hot (their
+    operands are 10-34 KB; in the decode step they come from the producing kernel through L2)."""
     import math
     import torch
     from runtime.model import DecodeConfig, rope_tables
-    from runtime.timing import graph_time
+    from runtime.timing import ColdCopies, graph_time, n_copies, windowed_time
 
     dev = "cuda"
     pol = [e for e in json.load(open(DecodeConfig().attn_policy_path)).get("policy", []) if e["max_ctx"] < (1 << 30)]
@@ -315,14 +330,26 @@ def kernels_leg(Kx, n=64, reps=5):
         o_part, m_part, l_part = torch.empty(n_q, S, D, **f32), torch.empty(n_q, S, **f32), torch.empty(n_q, S, **f32)
         o = torch.empty(n_q, D, dtype=torch.half, device=dev)
         nbytes = 1024 * ctx + 8192 + ctx // 4
-        t_ref = graph_time(lambda i: Kx.paged_attention(q, kc, vc, bt, pos, ps, o_part, m_part, l_part, o, 3), n,
-                           reps)[1]
-        t_dec = graph_time(lambda i: Kx.attention_decode(qkv, cos, sin, pos, bt, kc, vc, n_q, n_kv, ps, o_part, m_part,
-                                                         l_part, o, impl), n, reps)[1]
+        hot_ref = graph_time(lambda i: Kx.paged_attention(q, kc, vc, bt, pos, ps, o_part, m_part, l_part, o, 3), n,
+                             reps)[1]
+        hot_dec = graph_time(lambda i: Kx.attention_decode(qkv, cos, sin, pos, bt, kc, vc, n_q, n_kv, ps, o_part,
+                                                           m_part, l_part, o, impl), n, reps)[1]
+        kv = ColdCopies([kc, vc], n_copies(2 * kc.numel() * 2))
+        w_ref = windowed_time(lambda i: Kx.paged_attention(q, *kv[i], bt, pos, ps, o_part, m_part, l_part, o, 3),
+                              kv.copies, reps, warm_ms=100.0, window_ms=30.0)
+        w_dec = windowed_time(lambda i: Kx.attention_decode(qkv, cos, sin, pos, bt, *kv[i], n_q, n_kv, ps, o_part,
+                                                            m_part, l_part, o, impl),
+                              kv.copies, reps, warm_ms=30.0, window_ms=30.0)
+        del kv
+        t_ref, t_dec = w_ref["median_us"], w_dec["median_us"]
         out["attention"][str(ctx)] = {
             "bytes": nbytes, "part_size": ps, "paged_attention_v3_us": round(t_ref, 3),
-            "paged_attention_v3_gbps": round(nbytes / t_ref / 1e3, 1), "attention_decode_impl": impl,
-            "attention_decode_us": round(t_dec, 3), "attention_decode_gbps": round(nbytes / t_dec / 1e3, 1)}
+            "paged_attention_v3_gbps": round(nbytes / t_ref / 1e3, 1), "paged_attention_v3_hot_us": round(hot_ref, 3),
+            "attention_decode_impl": impl, "attention_decode_us": round(t_dec, 3),
+            "attention_decode_gbps": round(nbytes / t_dec / 1e3, 1), "attention_decode_hot_us": round(hot_dec, 3),
+            "ref_over_decode": round(t_ref / t_dec, 4),
+            "sclk_median": w_ref["clocks"].get("sclk_mhz", {}).get("median"),
+            "throttled": bool(w_ref["throttled"] or w_dec["throttled"])}
     g = torch.Generator(device=dev).manual_seed(3)
     H, I = 2048, 5632
     x = torch.randn(H, generator=g, device=dev).half()
@@ -343,23 +370,26 @@ def kernels_leg(Kx, n=64, reps=5):
             ("swiglu_5632", 6 * I, lambda i: Kx.swiglu(gu, act)),
             ("rope_append_32q4kv_d64", 4 * D * (n_q + 2 * n_kv),
              lambda i: Kx.rope_append(qkv, cos, sin, pos, bt, kc, vc, n_q, n_kv))):
-        t = graph_time(fn, n, reps)[1]
+        w = windowed_time(fn, n, reps, warm_ms=30.0, window_ms=20.0)
+        t = w["median_us"]
         out["fused"][name] = {"bytes": nbytes, "us": round(t, 3), "gbps": round(nbytes / t / 1e3, 2),
-                              "frac": round(nbytes / t / 1e3 / HBM_PEAK_GBS, 5)}
+                              "frac": round(nbytes / t / 1e3 / HBM_PEAK_GBS, 5),
+                              "sclk_median": w["clocks"].get("sclk_mhz", {}).get("median")}
     return out
 
 
 def attn8b_leg(Kx, ctx=4096, reps=5, eager=8, part_size=0):
     """Decode attention of BASELINE config 5 alone: Llama-3-8B heads (32 q / 8 kv, D 128, page 16) at context ctx,
     the reference op (split kernel + combine) with the runtime's policy entry for that context, each launch on a
-    different cold copy of the paged K/V (block table a seeded permutation), then bw_read over the same K/V bytes on
-    the split kernel's workgroup count and on the whole chip. Timed as hipGraphs of back-to-back launches; `eager`
+    different cold copy of the paged K/V (block table a seeded permutation), then the read probe over the same K/V
+    bytes on the split kernel's workgroup count and on a whole-chip persistent grid. Timed as clock-warmed hipGraphs
+    of back-to-back launches (runtime.timing.windowed_time); `eager`
     extra launches of each run outside any graph first, for the counter passes (rocprofv3 --pmc over this leg).
     part_size > 0 replaces the policy's split size (lean kernel when it fits, else the block kernel)."""
     import math
     import torch
     from runtime.model import DecodeConfig, Model
-    from runtime.timing import ColdCopies, graph_time, n_copies
+    from runtime.timing import ColdCopies, n_copies, windowed_time
 
     dev = "cuda"
     n_q, n_kv, D, P = 32, 8, 128, 16
@@ -386,23 +416,24 @@ def attn8b_leg(Kx, ctx=4096, reps=5, eager=8, part_size=0):
     nbytes = kv_bytes + 2 * n_q * D * 2 + 4 * math.ceil(ctx / P)
     attn = lambda i: Kx.paged_attention(q, *kv[i], bt, pos, ps, o_part, m_part, l_part, o, version)
     src = ColdCopies([torch.empty(kv_bytes, dtype=torch.uint8, device=dev)], n_copies(kv_bytes))
-    sink = torch.zeros(4, dtype=torch.int32, device=dev)
-    grids = {"split_workgroups": n_kv * S, "whole_chip": kv_bytes // 16 // 512}
-    reads = {k: (lambda i, b=b: Kx.bw_read(src[i][0], sink, b, 512, 4 if b * 512 * 4 * 16 <= kv_bytes else 1))
-             for k, b in grids.items()}
+    sink = torch.zeros(2048 * 8, dtype=torch.int32, device=dev)
+    grids = {"split_workgroups": (n_kv * S, 512, 8), "whole_chip": (1024, 512, 8)}
+    reads = {k: (lambda i, b=b: Kx.bw_read(src[i][0], sink, *b)) for k, b in grids.items()}
     for i in range(eager):
         attn(i)
     for fn in reads.values():
         for i in range(eager):
             fn(i)
     torch.cuda.synchronize()
-    t_attn = graph_time(attn, kv.copies, reps)[1]
+    w = windowed_time(attn, kv.copies, reps, warm_ms=200.0, window_ms=30.0)
+    t_attn = w["median_us"]
     res = {"ctx": ctx, "part_size": ps, "splits": S, "version": version, "bytes": nbytes,
            "us": round(t_attn, 3), "gbps": round(nbytes / t_attn / 1e3, 1),
-           "frac": round(nbytes / t_attn / 1e3 / HBM_PEAK_GBS, 4), "bw_read": {}}
+           "frac": round(nbytes / t_attn / 1e3 / HBM_PEAK_GBS, 4),
+           "sclk_median": w["clocks"].get("sclk_mhz", {}).get("median"), "throttled": w["throttled"], "bw_read": {}}
     for k, fn in reads.items():
-        t = graph_time(fn, src.copies, reps)[1]
-        res["bw_read"][k] = {"blocks": grids[k], "threads": 512, "bytes": kv_bytes, "us": round(t, 3),
+        t = windowed_time(fn, src.copies, reps, warm_ms=50.0, window_ms=30.0)["median_us"]
+        res["bw_read"][k] = {"grid": list(grids[k]), "bytes": kv_bytes, "us": round(t, 3),
                              "gbps": round(kv_bytes / t / 1e3, 1)}
     del kv, src
     return res
@@ -419,6 +450,8 @@ def decode_leg(model, ctx, steps, warmup):
         model.run_step()
     torch.cuda.synchronize()
     model.reset(ctx)
+    from runtime.timing import clock_summary, gpu_sysfs_dir, read_clocks
+    pci = gpu_sysfs_dir()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -426,6 +459,13 @@ def decode_leg(model, ctx, steps, warmup):
     for _ in range(steps):
         model.run_step()
     end.record()
+    samples = []                                   # clocks read while the timed steps run
+    while not end.query():
+        if start.query():
+            c = read_clocks(pci)
+            if c:
+                samples.append(c)
+        time.sleep(0.0005)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     total_ms = start.elapsed_time(end)
@@ -440,7 +480,8 @@ def decode_leg(model, ctx, steps, warmup):
     tok_us = sorted(s.elapsed_time(e) * 1e3 for s, e in per)
     return {"ctx_start": ctx, "steps": steps, "ms_per_step": total_ms / steps, "tok_s": steps / (total_ms / 1e3),
             "median_us": statistics.median(tok_us), "p10_us": tok_us[len(tok_us) // 10],
-            "p90_us": tok_us[(9 * len(tok_us)) // 10], **token_quartiles(tok_us), "wall_tok_s": steps / wall}
+            "p90_us": tok_us[(9 * len(tok_us)) // 10], **token_quartiles(tok_us), "wall_tok_s": steps / wall,
+            "window_clocks": clock_summary(samples)}
 
 
 def decode_8b_leg(ctx=4096, steps=64, warmup=8):
@@ -598,16 +639,22 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--ctx", type=int, default=512)
-    ap.add_argument("--leg", choices=("all", "gemv", "kernels", "decode", "decode8b", "attn8b", "readsweep", "prefill"),
+    ap.add_argument("--leg", choices=("all", "gemv", "kernels", "decode", "decode8b", "attn8b", "readsweep",
+                                      "readceiling", "prefill"),
                     default="all",
                     help="gemv: the 4096x14336 GEMV and its calibration copies only; decode: the TinyLlama decode "
                          "step only; decode8b: the Llama-3-8B decode legs only; attn8b: the Llama-3-8B ctx-4096 "
-                         "attention alone and bw_read of its K/V bytes; readsweep: bw_read from 2 to 512 MB and "
-                         "its fixed-cost + bandwidth fit; prefill: the TinyLlama prefill leg only; "
+                         "attention alone and the read probe over its K/V bytes; readsweep: the read probe from 2 "
+                         "to 512 MB and its fixed-cost + bandwidth fit; readceiling: the read probe's launch-shape "
+                         "sweep at the roofline GEMV's byte count; prefill: the TinyLlama prefill leg only; "
                          "kernels: the attention and fused-op kernels of configs 2 and 3 only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline leg")
     ap.add_argument("--attn-part", type=int, default=0, help="attn8b: split size instead of the policy's")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
+    ap.add_argument("--warm-ms", type=float, default=WINDOW["warm_ms"],
+                    help="GPU time of back-to-back replays ahead of each standalone kernel's timed window")
+    ap.add_argument("--window-ms", type=float, default=WINDOW["window_ms"],
+                    help="GPU time of a standalone kernel's timed samples")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one GPU only: the batch-1 decode path is single-GPU by design and every box here "
@@ -618,6 +665,7 @@ def main():
 
     from runtime.autotune import gemv_bytes
 
+    WINDOW.update({"warm_ms": a.warm_ms, "window_ms": a.window_ms})
     # the counter passes run in child processes before this process touches the GPU
     traffic, traffic_note = None, "not measured (--no-traffic)"
     if a.leg == "all" and not a.no_traffic:
@@ -647,15 +695,22 @@ def main():
 
     if a.leg == "readsweep":
         r = read_sweep_leg(Kx)
-        log(f"bw_read: time = {r['fit_fixed_us']} us + bytes / {r['fit_gbps']} GB/s; " +
+        log(f"read probe: time = {r['fit_fixed_us']} us + bytes / {r['fit_gbps']} GB/s; " +
             ", ".join(f"{p['bytes'] / 1e6:.0f} MB {p['us']} us ({p['frac']:.0%})" for p in r["points"]))
         print(json.dumps({"leg": "readsweep", "read_sweep": r}), flush=True)
+        return
+
+    if a.leg == "readceiling":
+        rc = read_ceiling_leg(Kx, gemv_bytes(4096, 14336, 128))
+        log(f"read probe of {rc['bytes']} B: best {rc['grid']} {rc['mean_us']:.3f} us -> {rc['gbps']:.0f} GB/s "
+            f"({rc['frac']:.1%}); one load per thread over the full grid {rc['full_grid_one_load']['us']} us")
+        print(json.dumps({"leg": "readceiling", "read_ceiling": rc}), flush=True)
         return
 
     if a.leg == "attn8b":
         r = attn8b_leg(Kx, part_size=a.attn_part)
         log(f"llama3-8b attention ctx {r['ctx']} (part {r['part_size']}, {r['splits']} splits): {r['us']:.3f} us -> "
-            f"{r['gbps']:.0f} GB/s; bw_read of the K/V bytes: " +
+            f"{r['gbps']:.0f} GB/s; read probe over the K/V bytes: " +
             ", ".join(f"{k} {v['us']:.3f} us" for k, v in r["bw_read"].items()))
         print(json.dumps({"leg": "attn8b", "attention_llama3_8b_ctx4096": r}), flush=True)
         return
@@ -681,7 +736,8 @@ def main():
         g3 = sampled("gemv_5632x2048", gemv_leg, Kx, 5632, 2048)
         log(f"gemv 5632x2048 {g3['cfg']}: {g3['mean_us']:.3f} us/launch -> {g3['gbps']:.0f} GB/s ({g3['frac']:.1%})")
         rc = sampled("read_ceiling", read_ceiling_leg, Kx, g1["bytes"])
-        log(f"bw_read of {rc['bytes']} B: {rc['mean_us']:.3f} us -> {rc['gbps']:.0f} GB/s ({rc['frac']:.1%})")
+        log(f"read probe of {rc['bytes']} B: best {rc['grid']} {rc['mean_us']:.3f} us -> {rc['gbps']:.0f} GB/s "
+            f"({rc['frac']:.1%})")
         kern = sampled("kernels", kernels_leg, Kx)
         log("attention (cfg2) us: " + ", ".join(f"ctx {c}: ref op {v['paged_attention_v3_us']}, fused "
                                               f"{v['attention_decode_us']}" for c, v in kern["attention"].items()))
@@ -733,7 +789,9 @@ def main():
                      "achieved": g1["gbps"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": g1["frac"],
                      "traffic": traffic["hbm_bytes_per_launch"] if traffic else None,
                      "traffic_detail": traffic or traffic_note, "bytes_per_launch": g1["bytes"],
-                     "mean_us": g1["mean_us"], "read_ceiling_frac": rc["frac"]},
+                     "mean_us": g1["mean_us"], "read_ceiling_frac": rc["frac"],
+                     "frac_of_read_ceiling": round(rc["mean_us"] / g1["mean_us"], 4),
+                     "window_sclk_mhz": g1["window_clocks"].get("sclk_mhz"), "throttled": g1["throttled"]},
         "gemv_14336x4096": g2, "gemv_cfg1_5632x2048": g3, "read_ceiling": rc, "kernels_cfg2_cfg3": kern,
         "decode": {**{k: round(v, 3) if isinstance(v, float) else v for k, v in dec.items()},
                    "bytes_per_token": bpt, "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / bpt, 1),

@@ -185,22 +185,29 @@ int dk_gemm_w4a16(const void* packed, const void* sz, const void* x, void* y, in
                   int epilogue, void* stream);
 
 /*
- * Achievable-read-bandwidth microbenchmark: reads `bytes` (multiple of 16) from buf, XOR-folds them and writes sink
- * (uint32[1]) only on a value it never takes. Replaces bw_read (kernels/bindings.cpp:40-43,
- * kernels/gemv_w4a16.cu:133-153). unroll in {1, 4}; threads a multiple of 64 in [64, 1024]; blocks >= 1.
+ * Read-bandwidth probe: `blocks` workgroups of `threads` threads read the first floor(bytes / 16) 16-byte words of buf
+ * once, workgroup b the contiguous slab [b n / blocks, (b + 1) n / blocks) of the n words, in rounds of
+ * unroll x threads words (every lane's `unroll` loads of a round in flight together). Wave w of workgroup b stores the
+ * sum of the 32-bit words it read (mod 2^32) to sink[(b * threads / 64 + w) mod sink_words]. With
+ * sink_words >= blocks * threads / 64 the slots add up to the sum of every 32-bit word read (a check that the whole
+ * buffer was streamed); with fewer slots a slot holds the sum of one of the waves that map to it.
+ * Replaces bw_read (kernels/bindings.cpp:40-43, the reference's read microbenchmark, kernels/gemv_w4a16.cu:133-153):
+ * same knobs (grid, workgroup size, loads in flight per lane), own kernel. unroll in {1, 2, 4, 8, 16}; threads a
+ * multiple of 64 in [64, 1024]; blocks in [1, 2^22]; bytes >= 16; buf 16-byte and sink 4-byte aligned.
  */
-int dk_bw_read(const void* buf, size_t bytes, void* sink, int blocks, int threads, int unroll, void* stream);
+int dk_bw_read(const void* buf, size_t bytes, uint32_t* sink, int sink_words, int blocks, int threads, int unroll,
+               void* stream);
 
 /*
- * Paged split-K GQA decode attention for one query token at ctx = *pos + 1 (device int32). version 1-3: the block
- * kernel (the reference's three kernel versions share one MI355X kernel); version 5: the lean MFMA kernel (see
- * dk_attention_decode's impl 3); version 4 (an earlier MFMA kernel) is no longer accepted.
+ * Paged split-K GQA decode attention for one query token at ctx = *pos + 1 (device int32). The version selects the
+ * split kernel: 1-3 (the reference's three kernel versions) the fastest this build has for the arguments, the lean
+ * MFMA kernel (see dk_attention_decode's impl 3) whenever it takes the part size and page, else the block kernel;
+ * 4 the block kernel; 5 the lean kernel (rejected where it does not fit).
  * Replaces paged_attention (kernels/bindings.cpp:45-62) -> paged_attention_launch (kernels/paged_attention.cu:429-461).
  * Grid = n_kv x max_splits workgroups; split s covers tokens [s*part_size, (s+1)*part_size) of the live context;
  * splits past ceil(ctx/part_size) exit; with one live split the output is written directly, otherwise each split
  * writes unnormalized o and its (m, l) and a combine kernel merges them with the log-sum-exp rule.
- * head_dim in {64, 128}; n_q / n_kv in {1, 2, 4, 8}; page a power of two; version in {1, 2, 3} (accepted for
- * signature compatibility; every version runs the same kernel). Context is clamped to n_bt * page (tokens without a
+ * head_dim in {64, 128}; n_q / n_kv in {1, 2, 4, 8}; page a power of two; version in 1..5. Context is clamped to n_bt * page (tokens without a
  * block-table entry do not exist); a block-table entry outside [0, n_pages) masks its tokens; tokens past
  * max_splits * part_size are not attended (as in the reference). softmax scale 1/sqrt(head_dim). q, kc, vc and
  * o_part 16-byte aligned.
@@ -264,8 +271,9 @@ int dk_attention_decode(const void* qkv, const float* cos_t, const float* sin_t,
  * Fused residual add + RMSNorm:  x <- x + delta (fp16 add, written back; skipped if delta == NULL);
  * out = w * fp16(float(x) * rsqrt(mean(float(x)^2) + eps)).
  * Replaces add_rmsnorm (kernels/bindings.cpp:64-72) -> add_rmsnorm_launch (kernels/fused_norm.cu:56-58).
- * H % 8 == 0, 8 <= H <= 65536 (the row is held in registers: 8 chunks of 8 for each of 1024 threads); x, delta, w,
- * out 16-byte aligned.
+ * H % 8 == 0, H >= 8. Up to H = 65536 the row is held in registers (8 chunks of 8 for each of 1024 threads); a longer
+ * row is normalised in two passes over memory, and then x, delta and out must not alias. x, delta, w, out 16-byte
+ * aligned.
  */
 int dk_add_rmsnorm(void* x, const void* delta, const void* w, void* out, int H, float eps, void* stream);
 

@@ -253,14 +253,21 @@ int dk_gemm_w4a16(const void* packed, const void* sz, const void* x, void* y, in
   return launched("gemm_w4a16");
 }
 
-int dk_bw_read(const void* buf, size_t bytes, void* sink, int blocks, int threads, int unroll, void* stream) {
+int dk_bw_read(const void* buf, size_t bytes, uint32_t* sink, int sink_words, int blocks, int threads, int unroll,
+               void* stream) {
   if (!buf || !sink) return fail(DK_ERR_NULL, "bw_read: null pointer argument");
   if (!aligned16(buf)) return fail(DK_ERR_ALIGN, "buf must be 16B aligned");
-  if (blocks < 1 || blocks > (1 << 30)) return fail(DK_ERR_SHAPE, "bw_read: blocks must be >= 1, got %d", blocks);
-  if (threads < 1 || threads > 1024) return fail(DK_ERR_SHAPE, "bw_read: threads must be 1..1024, got %d", threads);
-  if (unroll != 1 && unroll != 4) return fail(DK_ERR_DOMAIN, "bw_read: unroll must be 1 or 4, got %d", unroll);
+  if (!aligned4(sink)) return fail(DK_ERR_ALIGN, "bw_read: sink must be 4B aligned");
+  if (bytes < 16) return fail(DK_ERR_SHAPE, "bw_read: the buffer must hold at least one 16-byte word, got %zu B", bytes);
+  if (sink_words < 1) return fail(DK_ERR_SHAPE, "bw_read: sink_words must be >= 1, got %d", sink_words);
+  if (blocks < 1 || blocks > (1 << 22))
+    return fail(DK_ERR_SHAPE, "bw_read: blocks must be 1..%d, got %d", 1 << 22, blocks);
+  if (threads < 64 || threads > 1024 || threads % 64 != 0)
+    return fail(DK_ERR_SHAPE, "bw_read: threads must be a multiple of 64 in [64, 1024], got %d", threads);
+  if (unroll != 1 && unroll != 2 && unroll != 4 && unroll != 8 && unroll != 16)
+    return fail(DK_ERR_DOMAIN, "bw_read: unroll must be 1, 2, 4, 8 or 16, got %d", unroll);
   clear_error();
-  dk::launch_bw_read(buf, bytes, sink, blocks, threads, unroll, (hipStream_t)stream);
+  dk::launch_read_probe(buf, bytes, sink, (uint32_t)sink_words, blocks, threads, unroll, (hipStream_t)stream);
   return launched("bw_read");
 }
 
@@ -282,8 +289,8 @@ int check_paged_attention(int version, const void* q, const void* kc, const void
     return fail(DK_ERR_SHAPE, "heads-per-group must be 1/2/4/8, got %d", hpg);
   if (!pow2(page)) return fail(DK_ERR_DOMAIN, "page size must be a power of two, got %d", page);
   if (part_size <= 0) return fail(DK_ERR_DOMAIN, "part_size must be > 0");
-  if (version < 1 || version > 5 || version == 4)
-    return fail(DK_ERR_DOMAIN, "attention version must be 1, 2, 3 or 5, got %d", version);
+  if (version < 1 || version > 5)
+    return fail(DK_ERR_DOMAIN, "attention version must be 1..5, got %d", version);
   if (version == 5 && !dk::attn_lean_fits(part_size, ilog2(page), head_dim))
     return fail(DK_ERR_DOMAIN, "paged_attention: version 5 needs pages of >= 16 tokens and a part_size that is a "
                 "multiple of 16 up to %d (part_size %d, page %d)", dk::attn_lean_max_part(head_dim), part_size, page);
@@ -296,13 +303,21 @@ int check_paged_attention(int version, const void* q, const void* kc, const void
   return DK_OK;
 }
 
+// Split kernel of a paged_attention version: 1-3 (the reference's versions, kernels/bindings.cpp:56) the lean MFMA
+// kernel wherever it takes the part size and page, else the block kernel; 4 the block kernel; 5 the lean kernel.
+int attention_impl_of(int version, int part_size, int page, int head_dim) {
+  if (version == 4) return 1;
+  if (version == 5) return 3;
+  return dk::attn_lean_fits(part_size, ilog2(page), head_dim) ? 3 : 1;
+}
+
 void launch_reference_attention(int version, const void* q, const void* kc, const void* vc, const int32_t* bt,
                                 const int32_t* pos, int n_q, int n_kv, int head_dim, int page, int n_pages, int n_bt,
                                 int part_size, int max_splits, float* o_part, float* m_part, float* l_part,
                                 void* out, void* stream, bool split_only = false) {
   const dk::AttnLaunch a{q, nullptr, nullptr, 0, pos, bt, n_bt, const_cast<void*>(kc), const_cast<void*>(vc), n_pages,
                          ilog2(page), n_q, n_kv, head_dim, part_size, max_splits, o_part, m_part, l_part, out,
-                         version == 5 ? 3 : 1, split_only};
+                         attention_impl_of(version, part_size, page, head_dim), split_only};
   dk::launch_paged_attention(a, (hipStream_t)stream);
 }
 
@@ -397,6 +412,10 @@ int dk_gemv_w4a16_attn(int stage, int R, int warps, int pf, const void* packed, 
                 "waves: warps %d..%d for K=%d, got %d", dk::kGemvCombineMaxWarps, (K / 8 + 63) / 64,
                 dk::kGemvCombineMaxWarps, K, warps);
   if (!aligned16(o_part) || !aligned16(attn)) return fail(DK_ERR_ALIGN, "o_part and attn must be 16B aligned");
+  if (!aligned4(m_part) || !aligned4(l_part)) return fail(DK_ERR_ALIGN, "m_part and l_part must be 4B aligned");
+  if (y == attn || y == o_part || y == m_part || y == l_part)
+    return fail(DK_ERR_DOMAIN, "gemv_w4a16_attn: y must not alias attn, o_part, m_part or l_part (every workgroup "
+                "reads all of them while others write y)");
   dk::GemvInput in{};
   in.comb = dk::GemvCombine{o_part, m_part, l_part, attn, pos, n_bt << ilog2(page), part_size, max_splits, max_pos,
                             ilog2(head_dim)};
@@ -473,12 +492,15 @@ int dk_attention_decode(const void* qkv, const float* cos_t, const float* sin_t,
 
 int dk_add_rmsnorm(void* x, const void* delta, const void* w, void* out, int H, float eps, void* stream) {
   if (!x || !w || !out) return fail(DK_ERR_NULL, "add_rmsnorm: null pointer argument");
-  if (H <= 0 || H % 8 != 0 || H > dk::kRowNormMaxH)
-    return fail(DK_ERR_SHAPE, "add_rmsnorm: H must be a positive multiple of 8 (<= %d), got %d", dk::kRowNormMaxH, H);
+  if (H <= 0 || H % 8 != 0)
+    return fail(DK_ERR_SHAPE, "add_rmsnorm: H must be a positive multiple of 8, got %d", H);
   if (!aligned16(x)) return fail(DK_ERR_ALIGN, "x must be 16B aligned");
   if (!aligned16(w)) return fail(DK_ERR_ALIGN, "w must be 16B aligned");
   if (!aligned16(out)) return fail(DK_ERR_ALIGN, "out must be 16B aligned");
   if (delta && !aligned16(delta)) return fail(DK_ERR_ALIGN, "delta must be 16B aligned");
+  if (H > dk::kRowNormMaxH && (out == x || (delta && (out == delta || x == delta))))
+    return fail(DK_ERR_DOMAIN, "add_rmsnorm: for H > %d (two passes over the row in memory) x, delta and out must "
+                "not alias", dk::kRowNormMaxH);
   clear_error();
   dk::launch_add_rmsnorm(x, delta, w, out, H, eps, (hipStream_t)stream);
   return launched("add_rmsnorm");

@@ -78,6 +78,55 @@ row_norm_kernel(const f16* x_in, const int64_t* __restrict__ rows, int n_src, co
   }
 }
 
+// Residual + RMSNorm of one row too long for registers (H > kRowNormMaxH; the reference's add_rmsnorm takes any
+// H % 8 == 0, kernels/bindings.cpp:64-72): the same arithmetic in two passes over the row in memory. Pass 1 adds the
+// delta, writes xn to x (in place) and sums the squares; pass 2 re-reads the chunks this thread wrote and writes
+// out = w * fp16(float(xn) * rr). One workgroup; thread t owns chunks t, t + T, ...
+__global__ void __launch_bounds__(1024)
+row_norm_long_kernel(f16* x, const f16* __restrict__ delta, const f16* __restrict__ w, f16* __restrict__ out, int H,
+                     float eps) {
+  __shared__ float part[16];
+  const int tid = threadIdx.x, T = blockDim.x, U = H >> 3;
+  u32x4* xc = reinterpret_cast<u32x4*>(x);
+  const u32x4* dl = reinterpret_cast<const u32x4*>(delta);
+  float ss = 0.f;
+  for (int u = tid; u < U; u += T) {
+    u32x4 xv = xc[u];
+    if (delta != nullptr) {
+      const u32x4 dv = dl[u];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) xv[k] = as_u32(as_f16x2(xv[k]) + as_f16x2(dv[k]));
+      xc[u] = xv;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const f16x2 h = as_f16x2(xv[k]);
+      const float a = (float)h.x, b = (float)h.y;
+      ss = fmaf(a, a, ss);
+      ss = fmaf(b, b, ss);
+    }
+  }
+  ss = group_sum<kWave>(ss);
+  if ((tid & 63) == 0) part[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+  for (int i = 0; i < (T >> 6); ++i) tot += part[i];
+  const float rr = 1.0f / sqrtf(tot / (float)H + eps);
+  const u32x4* wc = reinterpret_cast<const u32x4*>(w);
+  u32x4* o = reinterpret_cast<u32x4*>(out);
+  for (int u = tid; u < U; u += T) {
+    const u32x4 xv = xc[u], wv = wc[u];
+    u32x4 ov;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const f16x2 h = as_f16x2(xv[k]);
+      const f16x2 hn = {(f16)((float)h.x * rr), (f16)((float)h.y * rr)};
+      ov[k] = as_u32(as_f16x2(wv[k]) * hn);
+    }
+    o[u] = ov;
+  }
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // out[i] = fp16(silu(float(gate[i]))) * up[i] in fp16, gate = gu[0:I], up = gu[I:2I]   (reference/ref_ops.py:23-27).
 __global__ void __launch_bounds__(256)
@@ -225,10 +274,10 @@ argmax_advance_kernel(const f16* __restrict__ logits, int V, int64_t* __restrict
 //              bit set; -0 first turned into +0 so that the two zeros tie as they compare equal);
 //   low word:  ~index, so that among equal values the lowest index has the largest key.
 // Workgroup w takes the 16-byte chunks [w * kArgmaxWgChunks, (w + 1) * kArgmaxWgChunks), workgroup 0 also the unaligned
-// head and the tail. Each workgroup folds its best key into work[0] with a device-scope atomic max, waits for that to
-// complete, then counts itself in work[1] with a device-scope atomic add; the workgroup that reads n - 1 arrives last,
-// after every other maximum has been applied: it reads work[0] (device-scope load), writes *tok and *pos + 1, and
-// resets work[0] and work[1] to 0 for the next call. No workgroup waits for another.
+// head and the tail. Each workgroup folds its best key into work[0] with a device-scope atomic max, then counts itself
+// in work[1] with a device-scope release / acquire atomic add; the workgroup that reads n - 1 arrives last, and every
+// other maximum happens before its load of work[0]: it writes *tok and *pos + 1, and resets work[0] and work[1] to 0
+// for the next call. No workgroup waits for another.
 constexpr int kArgmaxWgThreads = 256;
 constexpr int kArgmaxWgChunks = 2 * kArgmaxWgThreads;  // two 16-byte chunks (16 logits) per thread
 
@@ -267,13 +316,12 @@ argmax_split_kernel(const f16* __restrict__ logits, int V, int h, int nc, int64_
   __syncthreads();
   if (tid == 0) {
     for (int w = 1; w < kArgmaxWgThreads / 64; ++w) best = max(best, s_k[w]);
-    // a returning atomic: its value comes back only once the maximum has been applied at device scope, and the empty
-    // asm that consumes it makes the counter add below wait for it
-    const unsigned long long seen = __hip_atomic_fetch_max(&work[0], best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    asm volatile("" ::"v"(seen));
-    __builtin_amdgcn_s_waitcnt(0);
+    // The arrival is a release / acquire RMW at device scope: this workgroup's maximum (sequenced before its arrival)
+    // happens before the last arrival's load of work[0], because the last arrival's acquire reads the end of the
+    // counter's release sequence, which holds every earlier arrival.
+    __hip_atomic_fetch_max(&work[0], best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const unsigned long long prev =
-        __hip_atomic_fetch_add(&work[1], 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(&work[1], 1ull, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     if (prev == (unsigned long long)(gridDim.x - 1)) {
       const unsigned long long k = __hip_atomic_load(&work[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       tok[0] = (int64_t)(uint32_t)~(uint32_t)k;
@@ -301,6 +349,11 @@ static void launch_row_norm(const void* x_in, const int64_t* rows, int n_src, co
 }
 
 void launch_add_rmsnorm(void* x, const void* delta, const void* w, void* out, int H, float eps, hipStream_t st) {
+  if (H > kRowNormMaxH) {
+    hipLaunchKernelGGL(row_norm_long_kernel, dim3(1), dim3(1024), 0, st, (f16*)x, (const f16*)delta, (const f16*)w,
+                       (f16*)out, H, eps);
+    return;
+  }
   launch_row_norm(x, nullptr, 1, delta, w, x, out, 1, H, eps, st);
 }
 

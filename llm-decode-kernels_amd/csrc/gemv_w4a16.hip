@@ -438,9 +438,10 @@ __device__ __forceinline__ void combine_finish(const GemvCombine& c, const Combi
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] = fmaf(w, on ? v[e] : 0.f, acc[e]);
     }
-    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    // o / L, divided as the reference's combine divides (kernels/paged_attention.cu:381); no live weight: 0
 #pragma unroll
-    for (int k = 0; k < 4; ++k) xv[k] = as_u32(f16x2{(f16)(acc[2 * k] * inv), (f16)(acc[2 * k + 1] * inv)});
+    for (int k = 0; k < 4; ++k)
+      xv[k] = as_u32(L > 0.f ? f16x2{(f16)(acc[2 * k] / L), (f16)(acc[2 * k + 1] / L)} : f16x2{(f16)0.f, (f16)0.f});
   }
   if ((int)threadIdx.x < (K >> 3)) xs[threadIdx.x] = xv;
 }

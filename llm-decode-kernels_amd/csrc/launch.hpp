@@ -75,7 +75,11 @@ void launch_gemv_f16(int prologue, int R, int waves, int pf, const void* w, cons
 void launch_gemm_w4a16(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int log2G,
                        int epilogue, hipStream_t st);
 
-void launch_bw_read(const void* buf, size_t bytes, void* sink, int blocks, int threads, int unroll, hipStream_t st);
+// Read-ceiling probe (read_probe.hip): `blocks` workgroups of `threads` threads, workgroup b streaming the b-th of
+// `blocks` equal contiguous slabs in rounds of depth x threads 16-byte words; sink[(b W + w) mod sink_words] receives
+// the sum of the 32-bit words wave w of workgroup b read (W = threads / 64). depth in {1,2,4,8,16}.
+void launch_read_probe(const void* buf, size_t bytes, uint32_t* sink, uint32_t sink_words, int blocks, int threads,
+                       int depth, hipStream_t st);
 
 // Paged attention arguments. q: the query heads [n_q * D] (reference op) or the fused qkv vector (decode op).
 struct AttnLaunch {

@@ -1,5 +1,5 @@
-// INT4 column arithmetic shared by the W4A16 GEMV kernels and the persistent decode step (see the
-// gemv_w4a16.hip header for the derivation of the magic-number dequant).
+// INT4 column arithmetic shared by the W4A16 GEMV kernels (see the gemv_w4a16.hip header for the derivation of the
+// magic-number dequant).
 #pragma once
 #include "common.hpp"
 

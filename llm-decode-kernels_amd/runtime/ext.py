@@ -35,7 +35,7 @@ SIGNATURES = {
     "dk_rope_append_rows": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "dk_rmsnorm_rows": ([_P, _P, _I, _P, _P, _P, _P, _I, _I, _F, _P], _I),
     "dk_attention_prefill": ([_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P], _I),
-    "dk_bw_read": ([_P, _Z, _P, _I, _I, _I, _P], _I),
+    "dk_bw_read": ([_P, _Z, _P, _I, _I, _I, _I, _P], _I),
     "dk_paged_attention": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
     "dk_paged_attention_split": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P], _I),
     "dk_paged_attention_noalloc": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P], _I),
@@ -315,8 +315,15 @@ class DecodeKernels:
 
     # kernels/bindings.cpp:40-43
     def bw_read(self, buf, sink, blocks, threads, unroll):
+        """Read probe over buf with the caller's grid (blocks x threads, `unroll` 16-byte loads in flight per lane).
+        sink's 32-bit words receive per-wave sums of the words read (slot (b * threads / 64 + w) mod its word count),
+        so a sink of at least blocks * threads / 64 words adds up to the 32-bit word sum of the buffer."""
         _check_cuda(buf, "buf")
-        self._call(self.lib.dk_bw_read, buf.data_ptr(), buf.numel() * buf.element_size(), sink.data_ptr(),
+        _check_cuda(sink, "sink")
+        words = sink.numel() * sink.element_size() // 4
+        if words < 1:
+            raise RuntimeError("bw_read: sink must hold at least one 32-bit word")
+        self._call(self.lib.dk_bw_read, buf.data_ptr(), buf.numel() * buf.element_size(), sink.data_ptr(), words,
                    int(blocks), int(threads), int(unroll), _stream(buf))
 
     # the checks of kernels/bindings.cpp:45-62 (head_dim generalised from 64 to {64, 128}) -> C arguments
@@ -338,8 +345,8 @@ class DecodeKernels:
             raise RuntimeError("heads-per-group must be 1/2/4/8")
         if part_size <= 0:
             raise RuntimeError("part_size must be > 0")
-        if version not in (1, 2, 3, 5):
-            raise RuntimeError("attention version must be 1, 2, 3 or 5")
+        if version not in (1, 2, 3, 4, 5):
+            raise RuntimeError("attention version must be 1..5")
         max_splits = o_part.size(1)
         if not (o_part.size(0) == n_q and o_part.size(2) == D and m_part.size(0) == n_q and l_part.size(0) == n_q
                 and m_part.size(1) == max_splits and l_part.size(1) == max_splits and out.numel() == n_q * D):
@@ -409,8 +416,9 @@ class DecodeKernels:
     # rope_append (kernels/bindings.cpp:81-88) + paged_attention (kernels/bindings.cpp:45-62) fused into one launch
     def attention_decode(self, qkv, cos_t, sin_t, pos, bt, kc, vc, n_q, n_kv, part_size, o_part, m_part, l_part,
                          out, impl=0):
-        """impl: 0 or 1 = block kernel, 2 = MFMA kernel, 3 = lean MFMA kernel (pages >= 16 tokens, part_size a
-        multiple of 16 up to 512, 256 at head_dim 128); the split kernel is followed by the combine kernel."""
+        """impl: 0 or 1 = block kernel, 3 = lean MFMA kernel (pages >= 16 tokens, part_size a multiple of 16 up to
+        512, 256 at head_dim 128); 2 (an MFMA kernel since removed) is rejected. The split kernel is followed by the
+        combine kernel."""
         for t, n in ((qkv, "qkv"), (cos_t, "cos_t"), (sin_t, "sin_t"), (pos, "pos"), (bt, "bt"), (kc, "kc"),
                      (vc, "vc"), (o_part, "o_part"), (m_part, "m_part"), (l_part, "l_part"), (out, "out")):
             _check_cuda(t, n)

@@ -452,7 +452,7 @@ class Model:
     def attention(self, li):
         kc, vc = self.kv[li, 0], self.kv[li, 1]
         if self.rope_epilogue:  # q rotated and k, v appended by the qkv GEMV
-            version = 5 if self.attn_impl == 3 else 2
+            version = 5 if self.attn_impl == 3 else 4     # the policy's kernel, explicitly
             if self.attn_in_o:  # the o projection merges the partials
                 self.K.paged_attention_split(self.qkv[: self.n_q * self.D], kc, vc, self.bt, self.pos,
                                              self.part_size, self.o_part, self.m_part, self.l_part, self.attn, version)

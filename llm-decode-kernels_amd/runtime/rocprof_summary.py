@@ -6,7 +6,7 @@
     python -m runtime.rocprof_summary pmc --fetch <dir> --write <dir> --kernel <substring> --bytes <B> [--out f.json]
         HBM bytes per dispatch of the kernel whose name contains <substring>, from one FETCH_SIZE pass and one
         WRITE_SIZE pass over ``bench.py --leg gemv``. The counters are scaled by what they read for kernels of known
-        size run in the same process (bench.py calibration_leg): bw_read streaming B bytes once (FETCH_SIZE per B read)
+        size run in the same process (bench.py calibration_leg): the read probe streaming B bytes once (FETCH_SIZE per B read)
         and the last 16 device copies of B bytes (WRITE_SIZE per B written).
 
     python -m runtime.rocprof_summary counters <dir> [<dir> ...] [--kernel <substring> ...] [--out f.json]
@@ -65,10 +65,10 @@ def pmc(fetch_dir, write_dir, kernel, nbytes, n_cal=16):
     kib = lambda rs: [float(r["Counter_Value"]) * 1024 for r in rs]
     g_f = kib([r for r in fr if kernel in r["Kernel_Name"]])
     g_w = kib([r for r in wr if kernel in r["Kernel_Name"]])
-    rd = kib([r for r in fr if "bw_read_kernel" in r["Kernel_Name"]][-n_cal:])
+    rd = kib([r for r in fr if "read_probe_kernel" in r["Kernel_Name"]][-n_cal:])
     cp = kib([r for r in wr if "copyBuffer" in r["Kernel_Name"]][-n_cal:])
     if not (g_f and g_w and rd and cp):
-        raise SystemExit("missing dispatches: need the kernel, bw_read and copy dispatches in both passes")
+        raise SystemExit("missing dispatches: need the kernel, read-probe and copy dispatches in both passes")
     f_factor = statistics.median(rd) / nbytes
     w_factor = statistics.median(cp) / nbytes
     fetch = statistics.mean(g_f) / f_factor

@@ -133,3 +133,44 @@ def test_decode_step_with_merged_combine(K, shape_t):
     # in the last fp16 bit: the cache is held to the logits' bar, not bit for bit
     rows = a.bt[: (300 + 15) // 16].long()
     assert_close(b.kv[:, :, rows], a.kv[:, :, rows], 5e-3, "kv cache")
+
+
+@pytest.mark.parametrize("D,n_q,live,spare", [(64, 32, 2, 0), (64, 32, 5, 3), (128, 32, 9, 1), (64, 16, 16, 0)])
+def test_merged_combine_is_the_reference_combine_bit_for_bit(K, D, n_q, live, spare):
+    """The merge the o projection runs is the reference's combine (kernels/paged_attention.cu:368-382): M = max_s m_s,
+    L = sum_s e^(m_s - M) l_s and o = sum_s e^(m_s - M) o_s in split order, x = fp16(o / L). With equal maxima every
+    weight is e^0 = 1 exactly, so the sums and the division are exactly reproducible in float32 on the host. x is
+    observed without rounding through the GEMV: x is non-zero only at indices 32 n and weight row n is the one-hot
+    e_(32 n) (code 1, scale 1, zero 0), so every column product is exact and y_n = x_(32 n) bit for bit."""
+    import numpy as np
+    Kd, PS, page = n_q * D, 64, 16
+    S = live + spare
+    N = Kd // 32
+    rng = np.random.default_rng(D * 100 + live)
+    o = np.zeros((n_q, S, D), np.float32)
+    o[:, :, ::32] = rng.standard_normal((n_q, S, D // 32)).astype(np.float32) * 4
+    m = np.full((n_q, S), 0.75, np.float32)
+    l = rng.uniform(0.5, 40.0, (n_q, S)).astype(np.float32)
+    o[:, live:], m[:, live:], l[:, live:] = np.nan, np.nan, np.nan    # spare splits: stale partials
+    acc = np.zeros((n_q, D), np.float32)
+    L = np.zeros((n_q, 1), np.float32)
+    for s in range(live):
+        acc = (acc + o[:, s]).astype(np.float32)
+        L = (L + l[:, s:s + 1]).astype(np.float32)
+    x_ref = (acc / L).astype(np.float32).astype(np.float16).reshape(-1)
+    packed = torch.zeros(N, Kd // 8, dtype=torch.int32)
+    packed[torch.arange(N), 4 * torch.arange(N)] = 1               # element 32 n of row n: code 1 (bits 0..3)
+    sz = torch.zeros(N, Kd // G, 2, dtype=torch.half)
+    sz[..., 0] = 1.0
+    pos = torch.tensor([live * PS - 1], dtype=torch.int32, device=DEV)
+    bt = torch.arange(live * PS // page + 1, dtype=torch.int32, device=DEV)
+    attn = torch.full((Kd,), float("nan"), dtype=torch.half, device=DEV)   # read only with at most one live split
+    warps = max(-(-Kd // 512), -(-Kd // 2048))
+    for cfg in ((4, 1, warps, 1), (4, 2, warps, 0)):
+        y = torch.empty(N, dtype=torch.half, device=DEV)
+        K.gemv_w4a16_attn(*cfg, packed.to(DEV), sz.to(DEV), torch.from_numpy(o).to(DEV), torch.from_numpy(m).to(DEV),
+                          torch.from_numpy(l).to(DEV), attn, pos, bt, page, PS, 0, y, G)
+        got = y.cpu().numpy()
+        want = x_ref[::32]
+        assert np.array_equal(got.view(np.uint16), want.view(np.uint16)), \
+            f"cfg {cfg}: {np.flatnonzero(got.view(np.uint16) != want.view(np.uint16))[:8]}"

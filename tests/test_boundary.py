@@ -46,6 +46,7 @@ def test_runtime_is_torch_runtime(lib):
 
 
 A16 = 0x10000          # a 16-byte aligned fake address: validation fails before it is ever dereferenced
+B16 = 0x20000          # a second one
 
 
 def _err(lib, rc):
@@ -91,9 +92,8 @@ def _attn(lib, **kw):
     (dict(head_dim=96), 3, "head_dim"),
     (dict(page=12), 4, "page size must be a power of two"),
     (dict(part_size=0), 4, "part_size must be > 0"),
-    (dict(version=6), 4, "version must be 1, 2, 3 or 5"),
-    (dict(version=0), 4, "version must be 1, 2, 3 or 5"),
-    (dict(version=4), 4, "version must be 1, 2, 3 or 5"),
+    (dict(version=6), 4, "version must be 1..5"),
+    (dict(version=0), 4, "version must be 1..5"),
     (dict(version=5, part_size=40), 4, "version 5 needs pages of >= 16 tokens"),
     (dict(version=5, part_size=1024), 4, "version 5 needs pages"),
     (dict(version=5, page=8), 4, "version 5 needs pages"),
@@ -137,6 +137,11 @@ def _gemv_attn(lib, **kw):
     (dict(max_pos=-1), 4, "max_pos"),
     (dict(o=None), 1, "null"),
     (dict(attn=A16 + 8), 2, "16B aligned"),
+    (dict(m=A16 + 2), 2, "4B aligned"),
+    (dict(l=A16 + 1), 2, "4B aligned"),
+    (dict(y=A16), 4, "must not alias"),                                    # y == attn (and the partials)
+    (dict(y=B16, o=B16, attn=A16 + 4096), 4, "must not alias"),          # y == o_part
+    (dict(y=B16, m=B16, attn=A16 + 4096), 4, "must not alias"),          # y == m_part
 ])
 def test_gemv_attn_validation(lib, kw, code, msg):
     rc, m = _gemv_attn(lib, **kw)
@@ -170,7 +175,6 @@ def test_attention_decode_validation(lib, kw, code, msg):
     assert rc == code and msg in m, (rc, m)
 
 
-B16 = 0x20000
 
 
 def _fused(lib, fn, **kw):
@@ -252,8 +256,9 @@ def test_gemv_f16_validation(lib):
 
 def test_small_op_validation(lib):
     assert _err(lib, lib.dk_add_rmsnorm(A16, None, A16, A16, 2047, 1e-5, None))[0] == 3
-    rc, m = _err(lib, lib.dk_add_rmsnorm(A16, None, A16, A16, 65544, 1e-5, None))     # past the register-resident row
-    assert rc == 3 and "65536" in m
+    rc, m = _err(lib, lib.dk_add_rmsnorm(A16, None, A16, A16, 65544, 1e-5, None))     # two-pass row: no aliasing
+    assert rc == 4 and "must not alias" in m
+    assert _err(lib, lib.dk_add_rmsnorm(A16, B16, A16 + 4096, B16, 65544, 1e-5, None))[0] == 4  # out == delta
     assert _err(lib, lib.dk_add_rmsnorm(A16 + 2, None, A16, A16, 2048, 1e-5, None))[0] == 2
     assert _err(lib, lib.dk_add_rmsnorm(A16, A16 + 8, A16, A16, 2048, 1e-5, None))[0] == 2
     assert _err(lib, lib.dk_add_rmsnorm(None, None, A16, A16, 2048, 1e-5, None))[0] == 1
@@ -272,8 +277,12 @@ def test_small_op_validation(lib):
                                                         **kw).values(), None))
     assert q(G=1024)[0] == 4 and q(G=48)[0] == 4 and q(K=192)[0] == 3 and q(w=A16 + 2)[0] == 2
     assert q(clip=2)[0] == 4
-    assert _err(lib, lib.dk_bw_read(A16, 1024, A16, 4, 256, 2, None))[0] == 4
-    assert _err(lib, lib.dk_bw_read(A16 + 1, 1024, A16, 4, 256, 1, None))[0] == 2
+    bw = lambda **kw: _err(lib, lib.dk_bw_read(*dict(dict(buf=A16, n=1024, sink=A16, words=4, blocks=4, threads=256,
+                                                         unroll=4), **kw).values(), None))
+    assert bw(unroll=3)[0] == 4 and bw(unroll=32)[0] == 4 and bw(buf=A16 + 1)[0] == 2 and bw(sink=A16 + 2)[0] == 2
+    assert bw(threads=96)[0] == 3 and bw(threads=2048)[0] == 3 and bw(blocks=0)[0] == 3 and bw(words=0)[0] == 3
+    assert bw(blocks=(1 << 22) + 1)[0] == 3
+    assert bw(n=8)[0] == 3 and bw(sink=None)[0] == 1 and bw(buf=None)[0] == 1
 
 
 def test_prefill_validation(lib):

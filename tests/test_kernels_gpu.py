@@ -189,13 +189,13 @@ def test_attention_ctx128(K, n_q, n_kv, page):
     k, v = R.gather_kv(kc, vc, bt, 128, page)
     ref = R.attention_contiguous_ref(q, k, v)
     for PS in (4096, 64, 32, 48, 16):
-        for ver in (1, 2, 3, 5):
+        for ver in (1, 2, 3, 4, 5):
             close_or_rejected(run_attn(K, q, kc, vc, bt, 128, PS, ver), ref, 2e-3,
                          f"ctx128 {n_q}/{n_kv} P{page} PS{PS} v{ver}")
 
 
 @pytest.mark.parametrize("ctx", (1, 2, 17, 63, 65, 129, 1000))
-@pytest.mark.parametrize("ver", (3, 5))
+@pytest.mark.parametrize("ver", (3, 4, 5))
 def test_attention_odd_ctx(K, ver, ctx):
     kc, vc, bt = make_cache(ctx, 4, 16, seed=ctx)
     q = torch.randn(32, 64, generator=gen(ctx + 1)).half()
@@ -206,7 +206,7 @@ def test_attention_odd_ctx(K, ver, ctx):
 
 @pytest.mark.parametrize("ctx", (512, 1024, 2048, 4096, 8192, 16384))
 @pytest.mark.parametrize("peaky", (1.0, 6.0))
-@pytest.mark.parametrize("ver", (3, 5))
+@pytest.mark.parametrize("ver", (3, 4, 5))
 def test_attention_real_ctx(K, ver, ctx, peaky):
     kc, vc, bt = make_cache(ctx, 4, 16, peaky=peaky, seed=ctx)
     q = torch.randn(32, 64, generator=gen(ctx + 2)).half()
@@ -216,7 +216,7 @@ def test_attention_real_ctx(K, ver, ctx, peaky):
 
 
 @pytest.mark.parametrize("ctx", (1, 40, 64, 100, 700, 2048, 5000))
-@pytest.mark.parametrize("ver", (3, 5))
+@pytest.mark.parametrize("ver", (3, 4, 5))
 def test_attention_runtime_spare_splits(K, ver, ctx):
     kc, vc, bt = make_cache(ctx, 4, 16, peaky=6.0, seed=ctx + 3)
     q = torch.randn(32, 64, generator=gen(ctx + 4)).half()
@@ -227,7 +227,7 @@ def test_attention_runtime_spare_splits(K, ver, ctx):
 
 @pytest.mark.parametrize("n_q,n_kv", [(32, 8), (8, 8), (16, 8), (64, 8)])
 @pytest.mark.parametrize("ctx", (1, 100, 777, 4096))
-@pytest.mark.parametrize("ver", (3, 5))
+@pytest.mark.parametrize("ver", (3, 4, 5))
 def test_attention_head_dim_128(K, ver, n_q, n_kv, ctx):
     kc, vc, bt = make_cache(ctx, n_kv, 16, D=128, peaky=2.0, seed=ctx + n_q)
     q = torch.randn(n_q, 128, generator=gen(ctx)).half()
@@ -249,7 +249,7 @@ def test_attention_lean_part_bands(K, D, n_q, n_kv, ctx):
         close_or_rejected(run_attn(K, q, kc, vc, bt, ctx, PS, 5, spare=2), ref, 2e-3, f"D{D} ctx{ctx} PS{PS} lean")
 
 
-@pytest.mark.parametrize("ver", (3, 5))
+@pytest.mark.parametrize("ver", (3, 4, 5))
 def test_attention_ctx1_is_v0(K, ver):
     """Softmax over one token returns that token's V exactly (fp16 in, fp16 out)."""
     kc, vc, bt = make_cache(1, 4, 16, seed=9)
@@ -259,7 +259,7 @@ def test_attention_ctx1_is_v0(K, ver):
     assert torch.equal(out, v0.repeat_interleave(8, dim=0))
 
 
-@pytest.mark.parametrize("ver", (3, 5))
+@pytest.mark.parametrize("ver", (3, 4, 5))
 def test_attention_split_buffers_ignored_past_live(K, ver):
     """Splits beyond ceil(ctx/PS) must not touch the buffers (grid sized for the cap, surplus splits exit)."""
     ctx, PS, spare = 100, 32, 6
@@ -279,7 +279,7 @@ def test_attention_split_buffers_ignored_past_live(K, ver):
 
 # ----------------------------------------------------------------------------------------------- fused elementwise
 # 1, 2, 4 and 8 chunks per thread, partial last chunk rounds (8200, 32776) and the largest row (65536)
-@pytest.mark.parametrize("H", (2048, 4096, 64, 8200, 16384, 32776, 65536))
+@pytest.mark.parametrize("H", (2048, 4096, 64, 8200, 16384, 32776, 65536, 65544, 200008))  # > 65536: two-pass kernel
 def test_add_rmsnorm(K, H):
     g = gen(H)
     w = (1 + 0.1 * torch.randn(H, generator=g)).half()
