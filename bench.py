@@ -207,7 +207,7 @@ PROBE_GRIDS = [(b, t, u) for b in (256, 512, 1024, 2048) for t in (256, 512, 102
 def probe_time(Kx, cold, nbytes, blocks, threads, unroll, reps=5, warm_ms=None, window_ms=None):
     import torch
     from runtime.timing import windowed_time
-    sink = torch.zeros(blocks * threads // 64, dtype=torch.int32, device="cuda")
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")      # a one-word sink: the probe writes nothing
     return windowed_time(lambda i: Kx.bw_read(cold[i][0], sink, blocks, threads, unroll), cold.copies, reps,
                          warm_ms=WINDOW["warm_ms"] if warm_ms is None else warm_ms,
                          window_ms=WINDOW["window_ms"] / 2 if window_ms is None else window_ms)
@@ -416,7 +416,7 @@ def attn8b_leg(Kx, ctx=4096, reps=5, eager=8, part_size=0):
     nbytes = kv_bytes + 2 * n_q * D * 2 + 4 * math.ceil(ctx / P)
     attn = lambda i: Kx.paged_attention(q, *kv[i], bt, pos, ps, o_part, m_part, l_part, o, version)
     src = ColdCopies([torch.empty(kv_bytes, dtype=torch.uint8, device=dev)], n_copies(kv_bytes))
-    sink = torch.zeros(2048 * 8, dtype=torch.int32, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
     grids = {"split_workgroups": (n_kv * S, 512, 8), "whole_chip": (1024, 512, 8)}
     reads = {k: (lambda i, b=b: Kx.bw_read(src[i][0], sink, *b)) for k, b in grids.items()}
     for i in range(eager):

@@ -186,11 +186,11 @@ int dk_gemm_w4a16(const void* packed, const void* sz, const void* x, void* y, in
 
 /*
  * Read-bandwidth probe: `blocks` workgroups of `threads` threads read the first floor(bytes / 16) 16-byte words of buf
- * once, workgroup b the contiguous slab [b n / blocks, (b + 1) n / blocks) of the n words, in rounds of
- * unroll x threads words (every lane's `unroll` loads of a round in flight together). Wave w of workgroup b stores the
- * sum of the 32-bit words it read (mod 2^32) to sink[(b * threads / 64 + w) mod sink_words]. With
- * sink_words >= blocks * threads / 64 the slots add up to the sum of every 32-bit word read (a check that the whole
- * buffer was streamed); with fewer slots a slot holds the sum of one of the waves that map to it.
+ * once, workgroup b the b-th of `blocks` contiguous slabs of n / blocks or n / blocks + 1 of the n words, in rounds of
+ * unroll x threads words (every lane's `unroll` loads of a round in flight together). With
+ * sink_words >= blocks * threads / 64 (one slot per wave) wave w of workgroup b stores the sum of the 32-bit words it
+ * read (mod 2^32) to sink[b * threads / 64 + w], so the slots add up to the sum of every 32-bit word read (a check that
+ * the whole buffer was streamed); with a smaller sink (the reference's callers pass one word) nothing is written.
  * Replaces bw_read (kernels/bindings.cpp:40-43, the reference's read microbenchmark, kernels/gemv_w4a16.cu:133-153):
  * same knobs (grid, workgroup size, loads in flight per lane), own kernel. unroll in {1, 2, 4, 8, 16}; threads a
  * multiple of 64 in [64, 1024]; blocks in [1, 2^22]; bytes >= 16; buf 16-byte and sink 4-byte aligned.

@@ -479,23 +479,28 @@ constexpr int kTileDepth = DK_TILE_DEPTH;  // weight tiles in flight per workgro
 // A workgroup holds blockDim / (64 nw) independent row groups of nw = ceil(U / 64) waves each (group g takes the
 // workgroup's g-th run of T * NT rows): at small K a group is one wave, and several groups per workgroup cost fewer
 // workgroup dispatches than one single-wave workgroup per row tile.
+// `groups` (row groups per workgroup, blockDim / (64 nw)) comes from the host: the kernel's address arithmetic ahead
+// of its first load holds no integer division (two of them, at 20-30 dependent instructions each, cost 0.2 us per
+// launch at 4096 x 14336).
 template <int T, int NT, int PRO, int EPI>
 __global__ void __launch_bounds__(is_combine(PRO) ? 64 * kGemvCombineMaxWarps : 1024)
 gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, const GemvInput in,
-                f16* __restrict__ y, int N, int U, int gsh) {
+                f16* __restrict__ y, int N, int U, int gsh, int groups) {
   static_assert(EPI == kOutRows || (T * NT) % 2 == 0, "gate/up and rotation pairs need an even row tile");
   static_assert(!is_combine(PRO) || EPI == kOutRows, "the combine prologue feeds the plain epilogue");
   __shared__ float red[16][T * NT];
   __shared__ float s_ss[16];
   __shared__ u32x4 xs[is_combine(PRO) ? kGemvCombineMaxWarps * 64 : 1];   // combine: x, 8 values per thread
   const int nw = (U + kWave - 1) / kWave;  // waves of one row group
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int grp = wave / nw, gw0 = grp * nw;    // row group, its first wave
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int grp = 0;                                  // row group: wave / nw, by comparisons (groups <= 16)
+  for (int g = 1; g < groups; ++g) grp += wave >= g * nw ? 1 : 0;
+  const int gw0 = grp * nw;                     // its first wave
   const int tid = threadIdx.x - gw0 * kWave;    // thread within the row group
   const int u = (wave - gw0) * kWave + lane;
   const bool live = u < U;
   const int uc = live ? u : U - 1;  // dead lanes load a valid column and contribute 0
-  const int base = (blockIdx.x * (int)(blockDim.x / (nw * kWave)) + grp) * T * NT;
+  const int base = (blockIdx.x * groups + grp) * T * NT;
   const int NG = U >> gsh;
   int rpos = -1;
   if constexpr (EPI == kOutRope) rpos = *in.rope.pos;
@@ -638,7 +643,7 @@ void launch_tile_nt(int warps, const void* packed, const void* sz, const GemvInp
     const int groups = warps > 0 ? warps / nw : 1;
     const int rows = T * NT * groups;
     hipLaunchKernelGGL((gemv_w4a16_tile<T, NT, PRO, EPI>), dim3((N + rows - 1) / rows), dim3(64 * nw * groups), 0,
-                       st, (const u32x4*)packed, (const uint32_t*)sz, in, (f16*)y, N, U, log2G - 5);
+                       st, (const u32x4*)packed, (const uint32_t*)sz, in, (f16*)y, N, U, log2G - 5, groups);
   }
 }
 

@@ -76,8 +76,9 @@ void launch_gemm_w4a16(const void* packed, const void* sz, const void* x, void* 
                        int epilogue, hipStream_t st);
 
 // Read-ceiling probe (read_probe.hip): `blocks` workgroups of `threads` threads, workgroup b streaming the b-th of
-// `blocks` equal contiguous slabs in rounds of depth x threads 16-byte words; sink[(b W + w) mod sink_words] receives
-// the sum of the 32-bit words wave w of workgroup b read (W = threads / 64). depth in {1,2,4,8,16}.
+// `blocks` equal contiguous slabs in rounds of depth x threads 16-byte words; with sink_words >= blocks x W (W =
+// threads / 64) sink[b W + w] receives the sum of the 32-bit words wave w of workgroup b read, else nothing is written.
+// depth in {1,2,4,8,16}.
 void launch_read_probe(const void* buf, size_t bytes, uint32_t* sink, uint32_t sink_words, int blocks, int threads,
                        int depth, hipStream_t st);
 

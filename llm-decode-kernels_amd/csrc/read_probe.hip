@@ -9,10 +9,12 @@
 //     of the next round before it sums the current one (scheduling barriers pin the order), so DEPTH to 2 DEPTH
 //     16-byte loads per lane stay in flight; loads past the slab end are clamped to its last word and masked to zero
 //     afterwards, so no load sits behind a branch;
-//   - each wave sums its words (mod 2^32) with DPP and lane 63 stores the wave's sum to sink[(b W + w) mod sink_words]
-//     (W waves per workgroup): no LDS and no barrier, every wave retires on its own. With sink_words >= gridDim x W
-//     every wave has its own slot and the slots add up to the sum of all 32-bit words of the buffer, so a caller can
-//     check that every byte was read; with fewer slots a slot holds the sum of one of the waves that map to it.
+//   - the words are summed (mod 2^32); with a sink of at least one slot per wave (sink_words >= gridDim x W, W waves
+//     per workgroup) each wave sums over its lanes with DPP and lane 63 stores the wave's sum to sink[b W + w], so the
+//     slots add up to the sum of all 32-bit words of the buffer and a caller can check that every byte was read.
+//     With a smaller sink (the reference callers pass one word) nothing is written: an empty asm statement takes
+//     the sums as inputs, so the loads cannot be dropped, and the kernel ends without a store to wait for (a store
+//     of a checksum at the end of each wave cost 0.65 us of a 6 us read of 31.2 MB).
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -35,10 +37,10 @@ __device__ __forceinline__ uint32_t wave_sum_u32_lane63(uint32_t v) {
   return v;
 }
 
-// Slab b: `per` words, one more for the first `rem` workgroups (per = n / G, rem = n % G from the host, so the kernel
-// divides nothing). Rounds are double-buffered: round r + 1's loads are issued before round r is summed, so a lane
-// keeps DEPTH to 2 DEPTH loads in flight across round boundaries; a round past the slab's end loads its last word
-// (clamped) and sums nothing.
+// Slab b: `per` words, one more for the first `rem` workgroups; the host passes per, rem and the round counts of both
+// slab lengths, so the kernel divides nothing. Rounds are double-buffered: round r + 1's loads are issued before
+// round r is summed, so a lane keeps DEPTH to 2 DEPTH loads in flight across round boundaries; a round past the
+// slab's end loads its last word (clamped) and sums nothing.
 template <int DEPTH>
 __device__ __forceinline__ void probe_issue(const u32x4* __restrict__ p, size_t first, size_t T, size_t hi,
                                             u32x4 (&v)[DEPTH]) {
@@ -56,17 +58,19 @@ __device__ __forceinline__ uint32_t probe_sum(const u32x4 (&v)[DEPTH], size_t fi
 
 template <int DEPTH>
 __global__ void __launch_bounds__(1024)
-read_probe_kernel(const u32x4* __restrict__ p, size_t per, uint32_t rem, uint32_t* __restrict__ sink,
-                  uint32_t sink_words) {
+read_probe_kernel(const u32x4* __restrict__ p, size_t per, uint32_t rem, uint32_t rounds_short,
+                  uint32_t rounds_long, uint32_t* __restrict__ sink, uint32_t sink_words) {
   const size_t T = blockDim.x, R = DEPTH * T;
   const uint32_t b = blockIdx.x;
-  const size_t lo = (size_t)b * per + min(b, rem), hi = lo + per + (b < rem ? 1 : 0);
+  const bool longer = b < rem;
+  const size_t lo = (size_t)b * per + (longer ? b : rem), hi = lo + per + (longer ? 1 : 0);
+  const uint32_t rounds = longer ? rounds_long : rounds_short;  // 0 for an empty slab
   uint32_t acc = 0;
-  if (lo < hi) {  // uniform per workgroup (an empty slab reads nothing)
-    const size_t rounds = (hi - lo + R - 1) / R, f0 = lo + threadIdx.x;
+  if (rounds > 0) {  // uniform per workgroup
+    const size_t f0 = lo + threadIdx.x;
     u32x4 va[DEPTH], vb[DEPTH];
     probe_issue<DEPTH>(p, f0, T, hi, va);
-    size_t r = 0;
+    uint32_t r = 0;
     for (; r + 2 <= rounds; r += 2) {  // whole pairs of rounds, no exit in between (the waits stay partial)
       probe_issue<DEPTH>(p, f0 + (r + 1) * R, T, hi, vb);
       __builtin_amdgcn_sched_barrier(0);
@@ -77,18 +81,22 @@ read_probe_kernel(const u32x4* __restrict__ p, size_t per, uint32_t rem, uint32_
     }
     if (r < rounds) acc += probe_sum<DEPTH>(va, f0 + r * R, T, hi);
   }
-  acc = wave_sum_u32_lane63(acc);
-  if ((threadIdx.x & 63) == 63) {
-    const uint32_t slot = (b * (blockDim.x >> 6) + (threadIdx.x >> 6)) % sink_words;  // < 2^28: no overflow
-    __hip_atomic_store(sink + slot, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t waves = blockDim.x >> 6;
+  if (sink_words >= gridDim.x * waves) {  // uniform: one slot per wave, the checksum is stored
+    acc = wave_sum_u32_lane63(acc);
+    if ((threadIdx.x & 63) == 63) sink[b * waves + (threadIdx.x >> 6)] = acc;
+  } else {
+    asm volatile("" ::"v"(acc));  // the sums are kept (so are the loads), nothing is written
   }
 }
 
 template <int DEPTH>
 void launch_depth(const void* buf, size_t n, uint32_t* sink, uint32_t sink_words, int blocks, int threads,
                   hipStream_t st) {
-  hipLaunchKernelGGL((read_probe_kernel<DEPTH>), dim3(blocks), dim3(threads), 0, st, (const u32x4*)buf,
-                     n / (size_t)blocks, (uint32_t)(n % (size_t)blocks), sink, sink_words);
+  const size_t per = n / (size_t)blocks, R = (size_t)DEPTH * threads;
+  hipLaunchKernelGGL((read_probe_kernel<DEPTH>), dim3(blocks), dim3(threads), 0, st, (const u32x4*)buf, per,
+                     (uint32_t)(n % (size_t)blocks), (uint32_t)((per + R - 1) / R), (uint32_t)((per + R) / R), sink,
+                     sink_words);
 }
 
 }  // namespace

@@ -316,8 +316,8 @@ class DecodeKernels:
     # kernels/bindings.cpp:40-43
     def bw_read(self, buf, sink, blocks, threads, unroll):
         """Read probe over buf with the caller's grid (blocks x threads, `unroll` 16-byte loads in flight per lane).
-        sink's 32-bit words receive per-wave sums of the words read (slot (b * threads / 64 + w) mod its word count),
-        so a sink of at least blocks * threads / 64 words adds up to the 32-bit word sum of the buffer."""
+        A sink of at least blocks * threads / 64 32-bit words receives per-wave sums of the words read (slot
+        b * threads / 64 + w), which add up to the 32-bit word sum of the buffer; a smaller sink is not written."""
         _check_cuda(buf, "buf")
         _check_cuda(sink, "sink")
         words = sink.numel() * sink.element_size() // 4

@@ -44,12 +44,12 @@ def test_read_probe_reads_every_word_once(K, nbytes, blocks, threads, unroll):
     assert word_sum(sink.cpu().numpy().view(np.uint32)) == word_sum(words)
 
 
-def test_read_probe_single_slot(K):
-    """A one-word sink (the reference callers' shape) receives the sum of one of the waves."""
-    n = 4 * 64 * 4 * 16                            # 4 one-wave workgroups, slabs of one round of 64 threads x 4 words
+def test_read_probe_small_sink_untouched(K):
+    """A sink smaller than one slot per wave (the reference callers pass one word) is not written."""
+    n = 4 * 64 * 4 * 16
     host = torch.randint(0, 256, (n,), generator=torch.Generator().manual_seed(5), dtype=torch.uint8)
-    sink = torch.zeros(1, dtype=torch.int32, device=DEV)
-    K.bw_read(host.to(DEV), sink, 4, 64, 4)
-    torch.cuda.synchronize()
-    per_wg = [word_sum(c) for c in host.numpy().view(np.uint32).reshape(4, -1)]
-    assert int(sink.cpu().numpy().view(np.uint32)[0]) in per_wg
+    for words in (1, 3):
+        sink = torch.full((words,), 0x5A5A5A5A, dtype=torch.int32, device=DEV)
+        K.bw_read(host.to(DEV), sink, 4, 64, 4)
+        torch.cuda.synchronize()
+        assert torch.all(sink.cpu() == 0x5A5A5A5A)
