@@ -53,9 +53,9 @@ __device__ __forceinline__ void f16_rows(const u32x4 (&w)[T][C], const u32x4 (&x
 // order, so operand loads queued behind the weight stream would hold back the prologue); f16_input_finish computes
 // the operand once they have arrived.
 template <int C, int PRO>
-__device__ __forceinline__ void f16_input_load(const GemvInput& in, int lane, int U, u32x4 (&xr)[C], u32x4 (&dr)[C],
-                                               u32x4 (&wn)[C]) {
-  const u32x4* X = reinterpret_cast<const u32x4*>(in.x);
+__device__ __forceinline__ void f16_input_load(const GemvInput& in, const void* x, int lane, int U, u32x4 (&xr)[C],
+                                               u32x4 (&dr)[C], u32x4 (&wn)[C]) {
+  const u32x4* X = reinterpret_cast<const u32x4*>(x);
 #pragma unroll
   for (int c = 0; c < C; ++c) xr[c] = X[min(lane + 64 * c, U - 1)];
   if constexpr (PRO == 1) {
@@ -113,13 +113,14 @@ __device__ __forceinline__ void f16_input_finish(const GemvInput& in, int lane, 
 // Pipeline: operand loads, the weight loads of tiles 0 and 1, the operand, then per tile: compute it from its buffer
 // and refill that buffer with tile t + 2.
 template <int C, int T, int NT, int PRO>
+// The arguments the first loads need come first (preloaded into scalar registers at launch).
 __global__ void __launch_bounds__(512)
-gemv_f16_rows(const u32x4* __restrict__ W, const GemvInput in, f16* __restrict__ y, int N, int U) {
+gemv_f16_rows(const u32x4* __restrict__ W, const void* X, int N, int U, f16* __restrict__ y, const GemvInput in) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row0 = (blockIdx.x * (blockDim.x >> 6) + wave) * (T * NT);
   if (row0 >= N) return;  // whole wave past the last row (no barrier follows)
   u32x4 xc[C], dr[C], wn[C];
-  f16_input_load<C, PRO>(in, lane, U, xc, dr, wn);
+  f16_input_load<C, PRO>(in, X, lane, U, xc, dr, wn);
   u32x4 w[2][T][C];
   f16_issue<C, T>(W, row0, N, U, lane, w[0]);
   if constexpr (NT > 1) f16_issue<C, T>(W, row0 + T, N, U, lane, w[1]);
@@ -146,7 +147,7 @@ void launch_f16_nt(int waves, const void* w, const GemvInput& in, void* y, int N
   } else {
     const int rows_per_block = waves * T * NT;
     hipLaunchKernelGGL((gemv_f16_rows<C, T, NT, PRO>), dim3((N + rows_per_block - 1) / rows_per_block),
-                       dim3(64 * waves), 0, st, (const u32x4*)w, in, (f16*)y, N, K >> 3);
+                       dim3(64 * waves), 0, st, (const u32x4*)w, in.x, N, K >> 3, (f16*)y, in);
   }
 }
 

@@ -299,14 +299,14 @@ struct TileRaw {
 };
 
 template <int PRO>
-__device__ __forceinline__ void tile_input_load(const GemvInput& in, int uc, int K, TileRaw& raw) {
+__device__ __forceinline__ void tile_input_load(const GemvInput& in, const void* x, int uc, int K, TileRaw& raw) {
   if constexpr (PRO == kInPlain) {
-    const u32x4* X = reinterpret_cast<const u32x4*>(in.x);
+    const u32x4* X = reinterpret_cast<const u32x4*>(x);
 #pragma unroll
     for (int k = 0; k < 4; ++k) raw.a[k] = X[4 * uc + k];
   } else {
     const long long off = in.row != nullptr ? (long long)(*in.row) * (K >> 3) : 0;
-    const u32x4* X = reinterpret_cast<const u32x4*>(in.x) + off;
+    const u32x4* X = reinterpret_cast<const u32x4*>(x) + off;
     const u32x4* Wn = reinterpret_cast<const u32x4*>(in.norm_w);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -481,11 +481,13 @@ constexpr int kTileDepth = DK_TILE_DEPTH;  // weight tiles in flight per workgro
 // workgroup dispatches than one single-wave workgroup per row tile.
 // `groups` (row groups per workgroup, blockDim / (64 nw)) comes from the host: the kernel's address arithmetic ahead
 // of its first load holds no integer division (two of them, at 20-30 dependent instructions each, cost 0.2 us per
-// launch at 4096 x 14336).
+// launch at 4096 x 14336). The arguments that the first loads need (weights, scales, the x operand, the sizes) come
+// first, so that they are preloaded into scalar registers at launch (-amdgpu-kernarg-preload-count): reading them
+// from the kernel-argument segment was one more dependent round trip ahead of the first load (0.2 us per launch).
 template <int T, int NT, int PRO, int EPI>
 __global__ void __launch_bounds__(is_combine(PRO) ? 64 * kGemvCombineMaxWarps : 1024)
-gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, const GemvInput in,
-                f16* __restrict__ y, int N, int U, int gsh, int groups) {
+gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, const void* X, int N, int U, int gsh,
+                int groups, f16* __restrict__ y, const GemvInput in) {
   static_assert(EPI == kOutRows || (T * NT) % 2 == 0, "gate/up and rotation pairs need an even row tile");
   static_assert(!is_combine(PRO) || EPI == kOutRows, "the combine prologue feeds the plain epilogue");
   __shared__ float red[16][T * NT];
@@ -512,7 +514,7 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
   if constexpr (is_combine(PRO))
     combine_load(in.comb, U << 5, craw);
   else
-    tile_input_load<PRO>(in, uc, U << 5, raw);
+    tile_input_load<PRO>(in, X, uc, U << 5, raw);
   constexpr int DP = NT < kTileDepth ? NT : kTileDepth;  // tiles in flight
   u32x4 w[DP][T];
   uint32_t sz[DP][T];
@@ -643,7 +645,7 @@ void launch_tile_nt(int warps, const void* packed, const void* sz, const GemvInp
     const int groups = warps > 0 ? warps / nw : 1;
     const int rows = T * NT * groups;
     hipLaunchKernelGGL((gemv_w4a16_tile<T, NT, PRO, EPI>), dim3((N + rows - 1) / rows), dim3(64 * nw * groups), 0,
-                       st, (const u32x4*)packed, (const uint32_t*)sz, in, (f16*)y, N, U, log2G - 5, groups);
+                       st, (const u32x4*)packed, (const uint32_t*)sz, in.x, N, U, log2G - 5, groups, (f16*)y, in);
   }
 }
 

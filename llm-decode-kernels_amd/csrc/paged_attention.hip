@@ -416,12 +416,14 @@ struct MfmaAttnShape {
 // RoPE / append behaviour are those of the block kernel.
 constexpr int kLeanMaxWaves = 8;
 
+// Arguments in the order the kernel needs them (position, block table and split geometry for the page lookups, then
+// the q and K / V pointers), so that the first ones are preloaded into scalar registers at launch.
 template <int D, int HPG, bool ROPE, int NW, int NT>
 __global__ void __launch_bounds__(NW * kWave)
-attn_lean_kernel(const f16* __restrict__ qsrc, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-                 int max_pos, const int32_t* __restrict__ pos_ptr, const int32_t* __restrict__ bt, int n_bt,
-                 f16* __restrict__ kc, f16* __restrict__ vc, int n_pages, int log2P, int n_q, int n_kv, int PS,
-                 int max_splits, float scale, float* __restrict__ o_part, float* __restrict__ m_part,
+attn_lean_kernel(const int32_t* __restrict__ pos_ptr, const int32_t* __restrict__ bt, int n_bt, int log2P, int PS,
+                 int n_pages, const f16* __restrict__ qsrc, f16* __restrict__ kc, f16* __restrict__ vc, int n_kv,
+                 int n_q, int max_splits, float scale, const float* __restrict__ cos_t,
+                 const float* __restrict__ sin_t, int max_pos, float* __restrict__ o_part, float* __restrict__ m_part,
                  float* __restrict__ l_part, f16* __restrict__ out) {
   using S = MfmaAttnShape<D>;
   constexpr int KW = S::KW, QS = S::QS, VD = S::VD, CPL = D / 8;
@@ -688,9 +690,9 @@ template <int D, int HPG, bool ROPE, int NW, int NT>
 void launch_lean(const AttnLaunch& a, hipStream_t st) {
   const float scale = 1.0f / sqrtf((float)D);
   hipLaunchKernelGGL((attn_lean_kernel<D, HPG, ROPE, NW, NT>), dim3(a.n_kv, a.max_splits), dim3(NW * kWave), 0, st,
-                     (const f16*)a.q, a.cos_t, a.sin_t, a.max_pos, a.pos, a.bt, a.n_bt, (f16*)a.kc, (f16*)a.vc,
-                     a.n_pages, a.log2P, a.n_q, a.n_kv, a.part_size, a.max_splits, scale, a.o_part, a.m_part,
-                     a.l_part, (f16*)a.out);
+                     a.pos, a.bt, a.n_bt, a.log2P, a.part_size, a.n_pages, (const f16*)a.q, (f16*)a.kc, (f16*)a.vc,
+                     a.n_kv, a.n_q, a.max_splits, scale, a.cos_t, a.sin_t, a.max_pos, a.o_part, a.m_part, a.l_part,
+                     (f16*)a.out);
 }
 
 // waves: the smallest power of two >= min(tiles, 8); tiles per wave NT = ceil(tiles / waves) in {1, 2, 4} (2 at most
