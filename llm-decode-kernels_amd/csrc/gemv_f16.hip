@@ -53,17 +53,17 @@ __device__ __forceinline__ void f16_rows(const u32x4 (&w)[T][C], const u32x4 (&x
 // order, so operand loads queued behind the weight stream would hold back the prologue); f16_input_finish computes
 // the operand once they have arrived.
 template <int C, int PRO>
-__device__ __forceinline__ void f16_input_load(const GemvInput& in, const void* x, int lane, int U, u32x4 (&xr)[C],
-                                               u32x4 (&dr)[C], u32x4 (&wn)[C]) {
+__device__ __forceinline__ void f16_input_load(const void* x, const void* norm_w, const void* delta, int lane, int U,
+                                               u32x4 (&xr)[C], u32x4 (&dr)[C], u32x4 (&wn)[C]) {
   const u32x4* X = reinterpret_cast<const u32x4*>(x);
 #pragma unroll
   for (int c = 0; c < C; ++c) xr[c] = X[min(lane + 64 * c, U - 1)];
   if constexpr (PRO == 1) {
-    const u32x4* Wn = reinterpret_cast<const u32x4*>(in.norm_w);
+    const u32x4* Wn = reinterpret_cast<const u32x4*>(norm_w);
 #pragma unroll
     for (int c = 0; c < C; ++c) wn[c] = Wn[min(lane + 64 * c, U - 1)];
-    if (in.delta != nullptr) {
-      const u32x4* Dl = reinterpret_cast<const u32x4*>(in.delta);
+    if (delta != nullptr) {
+      const u32x4* Dl = reinterpret_cast<const u32x4*>(delta);
 #pragma unroll
       for (int c = 0; c < C; ++c) dr[c] = Dl[min(lane + 64 * c, U - 1)];
     }
@@ -71,8 +71,8 @@ __device__ __forceinline__ void f16_input_load(const GemvInput& in, const void* 
 }
 
 template <int C, int PRO>
-__device__ __forceinline__ void f16_input_finish(const GemvInput& in, int lane, int U, bool writer, u32x4 (&xc)[C],
-                                                 const u32x4 (&dr)[C], const u32x4 (&wn)[C]) {
+__device__ __forceinline__ void f16_input_finish(const GemvInput& in, const void* delta, int lane, int U, bool writer,
+                                                 u32x4 (&xc)[C], const u32x4 (&dr)[C], const u32x4 (&wn)[C]) {
   if constexpr (PRO == 0) {
 #pragma unroll
     for (int c = 0; c < C; ++c)
@@ -83,7 +83,7 @@ __device__ __forceinline__ void f16_input_finish(const GemvInput& in, int lane, 
     for (int c = 0; c < C; ++c) {
       const int ci = lane + 64 * c;
       const bool live = ci < U;
-      if (in.delta != nullptr) {
+      if (delta != nullptr) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) xc[c][e] = as_u32(as_f16x2(xc[c][e]) + as_f16x2(dr[c][e]));
       }
@@ -115,17 +115,18 @@ __device__ __forceinline__ void f16_input_finish(const GemvInput& in, int lane, 
 template <int C, int T, int NT, int PRO>
 // The arguments the first loads need come first (preloaded into scalar registers at launch).
 __global__ void __launch_bounds__(512)
-gemv_f16_rows(const u32x4* __restrict__ W, const void* X, int N, int U, f16* __restrict__ y, const GemvInput in) {
+gemv_f16_rows(const u32x4* __restrict__ W, const void* X, int N, int U, const void* norm_w, const void* delta,
+              f16* __restrict__ y, const GemvInput in) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row0 = (blockIdx.x * (blockDim.x >> 6) + wave) * (T * NT);
   if (row0 >= N) return;  // whole wave past the last row (no barrier follows)
   u32x4 xc[C], dr[C], wn[C];
-  f16_input_load<C, PRO>(in, X, lane, U, xc, dr, wn);
+  f16_input_load<C, PRO>(X, norm_w, delta, lane, U, xc, dr, wn);
   u32x4 w[2][T][C];
   f16_issue<C, T>(W, row0, N, U, lane, w[0]);
   if constexpr (NT > 1) f16_issue<C, T>(W, row0 + T, N, U, lane, w[1]);
   __builtin_amdgcn_sched_barrier(0);
-  f16_input_finish<C, PRO>(in, lane, U, blockIdx.x == 0 && wave == 0, xc, dr, wn);
+  f16_input_finish<C, PRO>(in, delta, lane, U, blockIdx.x == 0 && wave == 0, xc, dr, wn);
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     float v[T];
@@ -147,7 +148,7 @@ void launch_f16_nt(int waves, const void* w, const GemvInput& in, void* y, int N
   } else {
     const int rows_per_block = waves * T * NT;
     hipLaunchKernelGGL((gemv_f16_rows<C, T, NT, PRO>), dim3((N + rows_per_block - 1) / rows_per_block),
-                       dim3(64 * waves), 0, st, (const u32x4*)w, in.x, N, K >> 3, (f16*)y, in);
+                       dim3(64 * waves), 0, st, (const u32x4*)w, in.x, N, K >> 3, in.norm_w, in.delta, (f16*)y, in);
   }
 }
 

@@ -299,7 +299,8 @@ struct TileRaw {
 };
 
 template <int PRO>
-__device__ __forceinline__ void tile_input_load(const GemvInput& in, const void* x, int uc, int K, TileRaw& raw) {
+__device__ __forceinline__ void tile_input_load(const GemvInput& in, const void* x, const void* norm_w,
+                                                const void* delta, int uc, int K, TileRaw& raw) {
   if constexpr (PRO == kInPlain) {
     const u32x4* X = reinterpret_cast<const u32x4*>(x);
 #pragma unroll
@@ -307,14 +308,14 @@ __device__ __forceinline__ void tile_input_load(const GemvInput& in, const void*
   } else {
     const long long off = in.row != nullptr ? (long long)(*in.row) * (K >> 3) : 0;
     const u32x4* X = reinterpret_cast<const u32x4*>(x) + off;
-    const u32x4* Wn = reinterpret_cast<const u32x4*>(in.norm_w);
+    const u32x4* Wn = reinterpret_cast<const u32x4*>(norm_w);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       raw.a[k] = X[4 * uc + k];
       raw.c[k] = Wn[4 * uc + k];
     }
-    if (in.delta != nullptr) {
-      const u32x4* Dl = reinterpret_cast<const u32x4*>(in.delta);
+    if (delta != nullptr) {
+      const u32x4* Dl = reinterpret_cast<const u32x4*>(delta);
 #pragma unroll
       for (int k = 0; k < 4; ++k) raw.b[k] = Dl[4 * uc + k];
     }
@@ -322,15 +323,15 @@ __device__ __forceinline__ void tile_input_load(const GemvInput& in, const void*
 }
 
 template <int PRO>
-__device__ __forceinline__ void tile_input_finish(const GemvInput& in, TileRaw& raw, int uc, bool live, int K,
-                                                  float* s_ss, int wave, int gw0, int nw, bool writer,
-                                                  u32x4 (&xc)[4]) {
+__device__ __forceinline__ void tile_input_finish(const GemvInput& in, const void* delta, TileRaw& raw, int uc,
+                                                  bool live, int K, float* s_ss, int wave, int gw0, int nw,
+                                                  bool writer, u32x4 (&xc)[4]) {
   if constexpr (PRO == kInPlain) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) xc[k] = raw.a[k];
   } else {
     u32x4 (&xr)[4] = raw.a;
-    if (in.delta != nullptr) {
+    if (delta != nullptr) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
 #pragma unroll
@@ -391,7 +392,8 @@ struct CombineRaw {
 };
 
 template <int MS>
-__device__ __forceinline__ void combine_load(const GemvCombine& c, int K, CombineRaw<MS>& raw) {
+__device__ __forceinline__ void combine_load(const GemvCombine& c, const float* o_part, const float* m_part,
+                                             const float* l_part, int K, CombineRaw<MS>& raw) {
   const int chunk = min((int)threadIdx.x, (K >> 3) - 1);
   const int D = 1 << c.log2D;
   const int h = (chunk << 3) >> c.log2D, d0 = (chunk << 3) & (D - 1);
@@ -403,11 +405,11 @@ __device__ __forceinline__ void combine_load(const GemvCombine& c, int K, Combin
     raw.l[s] = 0.f;
     if (s < c.max_splits) {  // uniform: no load for the batch's slots past the buffer's splits
       const size_t hs = hb + s;
-      const float4* op = reinterpret_cast<const float4*>(c.o_part + hs * D + d0);
+      const float4* op = reinterpret_cast<const float4*>(o_part + hs * D + d0);
       raw.o[s][0] = op[0];
       raw.o[s][1] = op[1];
-      raw.m[s] = c.m_part[hs];
-      raw.l[s] = c.l_part[hs];
+      raw.m[s] = m_part[hs];
+      raw.l[s] = l_part[hs];
     }
   }
   raw.a = reinterpret_cast<const u32x4*>(c.attn)[chunk];
@@ -481,13 +483,15 @@ constexpr int kTileDepth = DK_TILE_DEPTH;  // weight tiles in flight per workgro
 // workgroup dispatches than one single-wave workgroup per row tile.
 // `groups` (row groups per workgroup, blockDim / (64 nw)) comes from the host: the kernel's address arithmetic ahead
 // of its first load holds no integer division (two of them, at 20-30 dependent instructions each, cost 0.2 us per
-// launch at 4096 x 14336). The arguments that the first loads need (weights, scales, the x operand, the sizes) come
-// first, so that they are preloaded into scalar registers at launch (-amdgpu-kernarg-preload-count): reading them
-// from the kernel-argument segment was one more dependent round trip ahead of the first load (0.2 us per launch).
+// launch at 4096 x 14336). The arguments that the first loads need (weights, scales, the prologue's operands, the
+// sizes) come first, so that they are preloaded into scalar registers at launch (-amdgpu-kernarg-preload-count):
+// reading them from the kernel-argument segment was one more dependent round trip ahead of the first load (0.2 us
+// per launch). The prologue's operands: op0 = x (the residual or embedding table for the norm), op1 = the norm
+// weight, op2 = delta (may be null); for the combine prologue o_part, m_part and l_part.
 template <int T, int NT, int PRO, int EPI>
 __global__ void __launch_bounds__(is_combine(PRO) ? 64 * kGemvCombineMaxWarps : 1024)
-gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, const void* X, int N, int U, int gsh,
-                int groups, f16* __restrict__ y, const GemvInput in) {
+gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, const void* op0, int N, int U, int gsh,
+                int groups, const void* op1, const void* op2, f16* __restrict__ y, const GemvInput in) {
   static_assert(EPI == kOutRows || (T * NT) % 2 == 0, "gate/up and rotation pairs need an even row tile");
   static_assert(!is_combine(PRO) || EPI == kOutRows, "the combine prologue feeds the plain epilogue");
   __shared__ float red[16][T * NT];
@@ -512,9 +516,10 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
   TileRaw raw;
   CombineRaw<is_combine(PRO) ? combine_splits(PRO) : 1> craw;
   if constexpr (is_combine(PRO))
-    combine_load(in.comb, U << 5, craw);
+    combine_load(in.comb, static_cast<const float*>(op0), static_cast<const float*>(op1),
+                 static_cast<const float*>(op2), U << 5, craw);
   else
-    tile_input_load<PRO>(in, X, uc, U << 5, raw);
+    tile_input_load<PRO>(in, op0, op1, op2, uc, U << 5, raw);
   constexpr int DP = NT < kTileDepth ? NT : kTileDepth;  // tiles in flight
   u32x4 w[DP][T];
   uint32_t sz[DP][T];
@@ -528,7 +533,7 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
 #pragma unroll
     for (int k = 0; k < 4; ++k) xc[k] = live ? xs[4 * uc + k] : u32x4{0u, 0u, 0u, 0u};
   } else {
-    tile_input_finish<PRO>(in, raw, uc, live, U << 5, s_ss, wave, gw0, nw, blockIdx.x == 0 && grp == 0, xc);
+    tile_input_finish<PRO>(in, op2, raw, uc, live, U << 5, s_ss, wave, gw0, nw, blockIdx.x == 0 && grp == 0, xc);
   }
   const ColumnSums cs = column_sums(xc);
   const NibbleMasks m = nibble_masks();
@@ -645,7 +650,10 @@ void launch_tile_nt(int warps, const void* packed, const void* sz, const GemvInp
     const int groups = warps > 0 ? warps / nw : 1;
     const int rows = T * NT * groups;
     hipLaunchKernelGGL((gemv_w4a16_tile<T, NT, PRO, EPI>), dim3((N + rows - 1) / rows), dim3(64 * nw * groups), 0,
-                       st, (const u32x4*)packed, (const uint32_t*)sz, in.x, N, U, log2G - 5, groups, (f16*)y, in);
+                       st, (const u32x4*)packed, (const uint32_t*)sz,
+                       is_combine(PRO) ? static_cast<const void*>(in.comb.o_part) : in.x, N, U, log2G - 5, groups,
+                       is_combine(PRO) ? static_cast<const void*>(in.comb.m_part) : in.norm_w,
+                       is_combine(PRO) ? static_cast<const void*>(in.comb.l_part) : in.delta, (f16*)y, in);
   }
 }
 
