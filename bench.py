@@ -792,7 +792,8 @@ def main():
                      "mean_us": g1["mean_us"], "read_ceiling_frac": rc["frac"],
                      "frac_of_read_ceiling": round(rc["mean_us"] / g1["mean_us"], 4),
                      "window_sclk_mhz": g1["window_clocks"].get("sclk_mhz"), "throttled": g1["throttled"]},
-        "gemv_14336x4096": g2, "gemv_cfg1_5632x2048": g3, "read_ceiling": rc, "kernels_cfg2_cfg3": kern,
+        "gemv_4096x14336": g1, "gemv_14336x4096": g2, "gemv_cfg1_5632x2048": g3, "read_ceiling": rc,
+        "kernels_cfg2_cfg3": kern,
         "decode": {**{k: round(v, 3) if isinstance(v, float) else v for k, v in dec.items()},
                    "bytes_per_token": bpt, "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / bpt, 1),
                    "frac_of_roofline": round(dec["tok_s"] / (HBM_PEAK_GBS * 1e9 / bpt), 4)},
