@@ -580,6 +580,45 @@ def gemm_timing(model, lin, M, epilogue, reps=20):
             "hipblaslt_fp16_tflops": round(fl / ub / 1e6, 1)}
 
 
+GEMM_SHAPES = (("llama3_8b.gate_up", 28672, 4096, 1), ("llama3_8b.qkv", 6144, 4096, 0), ("llama3_8b.o", 4096, 4096, 0),
+               ("llama3_8b.down", 4096, 14336, 0), ("tinyllama.gate_up", 11264, 2048, 1),
+               ("tinyllama.qkv", 2560, 2048, 0), ("tinyllama.down", 2048, 5632, 0))
+
+
+def gemm_leg(Kx, M=512, reps=5, eager=4, G=128):
+    """The prefill projections alone: dk_gemm_w4a16 at M prompt rows over the Llama-3-8B and TinyLlama shapes (SwiGLU
+    epilogue for gate|up), clock-warmed graph windows, beside hipBLASLt's fp16 GEMM (torch.mm) on fp16 weights of the
+    same shape; `eager` extra launches of each run outside any graph first, for the counter passes (rocprofv3 --pmc
+    over this leg)."""
+    import torch
+    from runtime.quant import quantize_pack
+    from runtime.timing import windowed_time
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(11)
+    for name, N, K, epi in GEMM_SHAPES:
+        packed, sz = quantize_pack((torch.randn(N, K, generator=g, device="cuda") * 0.02).half(), G)
+        x = torch.randn(M, K, generator=g, device="cuda").half()
+        y = torch.empty(M, N // (1 + epi), dtype=torch.half, device="cuda")
+        for _ in range(eager):
+            Kx.gemm_w4a16(packed, sz, x, y, G, epilogue=epi)
+        torch.cuda.synchronize()
+        w = windowed_time(lambda i: Kx.gemm_w4a16(packed, sz, x, y, G, epilogue=epi), 8, reps, warm_ms=100.0,
+                          window_ms=40.0)
+        w16 = torch.randn(N, K, generator=g, device="cuda").half()
+        yb = torch.empty(M, N, dtype=torch.half, device="cuda")
+        wb = windowed_time(lambda i: torch.mm(x, w16.t(), out=yb), 8, reps, warm_ms=30.0, window_ms=40.0)
+        fl = 2 * M * N * K
+        out[name] = {"M": M, "N": N, "K": K, "epilogue": epi, "us": round(w["median_us"], 2),
+                     "tflops": round(fl / w["median_us"] / 1e6, 1), "hipblaslt_fp16_us": round(wb["median_us"], 2),
+                     "hipblaslt_fp16_tflops": round(fl / wb["median_us"] / 1e6, 1),
+                     "sclk_median": w["clocks"].get("sclk_mhz", {}).get("median")}
+        log(f"gemm {name} {M}x{N}x{K}: {out[name]['us']} us ({out[name]['tflops']} TFLOP/s), hipBLASLt fp16 "
+            f"{out[name]['hipblaslt_fp16_us']} us")
+        del packed, sz, w16, yb
+        torch.cuda.empty_cache()
+    return out
+
+
 def token_quartiles(tok_us):
     """First and third quartile and the interquartile range of per-token times in us (bench/timing.py:134-138 of the
     reference reports median + IQR); empty for fewer than two tokens."""
@@ -640,13 +679,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--ctx", type=int, default=512)
     ap.add_argument("--leg", choices=("all", "gemv", "kernels", "decode", "decode8b", "attn8b", "readsweep",
-                                      "readceiling", "prefill"),
+                                      "readceiling", "prefill", "gemm"),
                     default="all",
                     help="gemv: the 4096x14336 GEMV and its calibration copies only; decode: the TinyLlama decode "
                          "step only; decode8b: the Llama-3-8B decode legs only; attn8b: the Llama-3-8B ctx-4096 "
                          "attention alone and the read probe over its K/V bytes; readsweep: the read probe from 2 "
                          "to 512 MB and its fixed-cost + bandwidth fit; readceiling: the read probe's launch-shape "
-                         "sweep at the roofline GEMV's byte count; prefill: the TinyLlama prefill leg only; "
+                         "sweep at the roofline GEMV's byte count; gemm: the prefill GEMM alone at the Llama-3-8B and "
+                         "TinyLlama projection shapes, M 512, beside hipBLASLt fp16; prefill: the TinyLlama prefill leg only; "
                          "kernels: the attention and fused-op kernels of configs 2 and 3 only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline leg")
     ap.add_argument("--attn-part", type=int, default=0, help="attn8b: split size instead of the policy's")
@@ -698,6 +738,10 @@ def main():
         log(f"read probe: time = {r['fit_fixed_us']} us + bytes / {r['fit_gbps']} GB/s; " +
             ", ".join(f"{p['bytes'] / 1e6:.0f} MB {p['us']} us ({p['frac']:.0%})" for p in r["points"]))
         print(json.dumps({"leg": "readsweep", "read_sweep": r}), flush=True)
+        return
+
+    if a.leg == "gemm":
+        print(json.dumps({"leg": "gemm", "gemm_512": gemm_leg(Kx)}), flush=True)
         return
 
     if a.leg == "readceiling":

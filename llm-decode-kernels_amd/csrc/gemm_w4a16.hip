@@ -32,13 +32,9 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
 
-// 8 weights of one packed word -> fp16((q - zero) * scale), in element order; mlo = vgpr_const(0x000F000F) (one
-// v_and_or_b32 per pair)
-__device__ __forceinline__ u32x4 dequant8(uint32_t word, uint32_t szw, uint32_t mlo) {
-  const f16x2 sz = as_f16x2(szw);
-  const f16x2 s2 = {sz.x, sz.x};
-  const f16 zb = (f16)1024.0f + sz.y;            // 1024 + zero, exact (zero is an integer in [0, 15])
-  const f16x2 z2 = {zb, zb};
+// 8 weights of one packed word -> fp16((q - zero) * scale), in element order, given s2 = (scale, scale) and z2 =
+// (1024 + zero) twice; mlo = vgpr_const(0x000F000F) (one v_and_or_b32 per pair)
+__device__ __forceinline__ u32x4 dequant8_sz(uint32_t word, f16x2 s2, f16x2 z2, uint32_t mlo) {
   const uint32_t hi = word >> 8;
   // pairs (e0, e1), (e2, e3), (e4, e5), (e6, e7): nibble i of each 16-bit half
   const uint32_t p0 = (word & mlo) | 0x64006400u;
@@ -51,6 +47,13 @@ __device__ __forceinline__ u32x4 dequant8(uint32_t word, uint32_t szw, uint32_t 
   r[2] = as_u32((as_f16x2(p2) - z2) * s2);
   r[3] = as_u32((as_f16x2(p3) - z2) * s2);
   return r;
+}
+
+// the same from the group's packed (scale, zero) pair (1024 + zero is exact: zero is an integer in [0, 15])
+__device__ __forceinline__ u32x4 dequant8(uint32_t word, uint32_t szw, uint32_t mlo) {
+  const f16x2 sz = as_f16x2(szw);
+  const f16 zb = (f16)1024.0f + sz.y;
+  return dequant8_sz(word, f16x2{sz.x, sz.x}, f16x2{zb, zb}, mlo);
 }
 
 template <int EPI>
@@ -365,6 +368,221 @@ gemm_w4a16_wide(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Register-stationary weights (K % 128 == 0, G >= 64, grids of a few hundred tiles): every wave owns 64 weight rows
+// of the tile (two 32-row MFMA tiles) and all of its BM tokens. The weights go from HBM straight into registers --
+// lane l = 32 h + r of row tile i loads words 8h .. 8h+7 of row 32 i + r in the 128-wide k chunk (two 16-byte
+// loads) -- and are dequantized there, already in the MFMA A layout: no weight passes through LDS and each is
+// dequantized once. Only the token tile X [BM x 128] is staged in LDS (rows of 256 bytes, 16-byte chunk q of row t at
+// q ^ (t & 15)), written once per chunk and read by all four waves.
+//   MFMA: v_mfma_f32_32x32x16_f16, the form that reaches this part's MFMA rate (a 16x16x32 stream tops out near
+//   three quarters of it per clock). k order: in k step s (0..7) of a chunk, lane (h, r) takes word 8h + s of its row
+//   (k 64h + 8s .. + 7) and the same eight k of its token row from LDS -- one order for both operands, so the products
+//   and their sums are those of the plain order. The accumulator of tile (i, j) leaves lane (h, r) with rows
+//   8 q + 4 h + v (q, v = 0..3) of the weight tile for token r: four consecutive outputs of one token per q.
+//   LDS traffic: per k step a wave reads BM / 32 token fragments of 1 KB for 2 BM / 32 MFMAs of 32 cycles, 8 bytes
+//   per MFMA cycle, 32 per CU cycle with four waves at the full MFMA rate, plus the stage's 16.
+// Pipeline per chunk c: compute chunk c (dequant of W(c) in registers, X(c) from LDS buffer c & 1), store X(c + 1)
+// (loaded a chunk earlier) into the other buffer, issue the loads of chunk c + 2, barrier. W, scales and X come in
+// through buffer loads (SGPR base and chunk offset, a constant VGPR offset per row), so moving to the next chunk costs
+// no vector instruction; the host checks that every offset fits 31 bits. Two workgroups share a CU (accumulators and
+// operands in the 256 architectural VGPRs of a wave).
+constexpr int kRsK = 128, kRsRows = 64, kRsThreads = 256;
+#ifndef RS_AHEAD
+#define RS_AHEAD 2
+#endif
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16 mfma32x32(h8 a, h8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* p, uint32_t bytes) {
+  // stride 0 (raw buffer), word 3 = 32-bit data format as the gfx9 family expects for untyped loads
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+template <int BM, int EPI>
+__global__ void __launch_bounds__(kRsThreads, 2)
+gemm_w4a16_rs(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int M, int N, int K, int gsh,
+              int tiles_m, int tiles) {
+  constexpr int TI = kRsRows / 32, TJ = BM / 32, KS = kRsK / 16;
+  constexpr int XL = BM * 16 / kRsThreads;  // 16-byte X loads per thread per chunk
+  __shared__ u32x4 Xs[2][BM][16];
+  const int per = gridDim.x / kXcds;
+  const int t = (int)(blockIdx.x % kXcds) * per + (int)(blockIdx.x / kXcds);
+  if (t >= tiles) return;  // uniform: the grid is rounded up to a multiple of the XCD count
+  const int m0 = (t % tiles_m) * BM, n0 = (t / tiles_m) * (4 * kRsRows);
+  const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 31, h = lane >> 5;
+  const int KW = K >> 3, NG = K >> gsh, nk = K / kRsK;
+  const __amdgpu_buffer_rsrc_t wres = buffer_of(W, (uint32_t)N * (uint32_t)KW * 4u);
+  const __amdgpu_buffer_rsrc_t sres = buffer_of(SZ, (uint32_t)N * (uint32_t)NG * 4u);
+  const __amdgpu_buffer_rsrc_t xres = buffer_of(X, (uint32_t)M * (uint32_t)K * 2u);
+  // rows past N or M re-read the last valid row (their results are never stored); the lane's scale is that of its
+  // first k, k0 + 64 h, whose group holds all 64 of its k (G >= 64)
+  uint32_t wo[TI], so[TI];
+#pragma unroll
+  for (int i = 0; i < TI; ++i) {
+    const uint32_t row = (uint32_t)min(n0 + wave * kRsRows + 32 * i + r, N - 1);
+    wo[i] = row * (uint32_t)KW * 4u + 32u * (uint32_t)h;
+    so[i] = (row * (uint32_t)NG + (uint32_t)((64 * h) >> gsh)) * 4u;
+  }
+  // X staging: chunk xq of rows xr + 16 v, stored at chunk xq ^ xr of the row (xr = (xr + 16 v) & 15)
+  const int xq = tid & 15, xr = tid >> 4;
+  uint32_t xo[XL];
+#pragma unroll
+  for (int v = 0; v < XL; ++v) xo[v] = (uint32_t)min(m0 + xr + 16 * v, M - 1) * (uint32_t)K * 2u + 16u * (uint32_t)xq;
+
+  u32x4 xv[XL], wv[2][TI][2];
+  uint32_t sv[2][TI];
+  // loads are unconditional (chunks past the end re-read the last one): a load behind a branch would make the
+  // compiler drain every outstanding load at the join
+  auto fetch = [&](int kc, int slot) {
+    const int k0 = min(kc, nk - 1) * kRsK;
+#pragma unroll
+    for (int v = 0; v < XL; ++v)
+      xv[v] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, xo[v], 2 * k0, 0));
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        wv[slot][i][u] =
+            __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, wo[i] + 16u * u, k0 >> 1, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < TI; ++i) sv[slot][i] = __builtin_amdgcn_raw_buffer_load_b32(sres, so[i], (k0 >> gsh) * 4, 0);
+  };
+  auto stage = [&](int buf) {
+#pragma unroll
+    for (int v = 0; v < XL; ++v) Xs[buf][xr + 16 * v][xq ^ xr] = xv[v];
+  };
+  f32x16 acc[TI][TJ];
+#pragma unroll
+  for (int i = 0; i < TI; ++i) {
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) acc[i][j] = f32x16{};
+  }
+  const uint32_t mlo = vgpr_const(0x000F000Fu);
+  auto compute = [&](int buf, int slot) {
+    // the chunk's weight words and scales enter here: without the pin the compiler hoists their first use above the
+    // previous chunk's barrier, where waiting for them drains the newer loads as well
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+      asm volatile("" : "+v"(wv[slot][i][0]), "+v"(wv[slot][i][1]));
+      asm volatile("" : "+v"(sv[slot][i]));
+    }
+    f16x2 s2[TI], z2[TI];
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+      const f16x2 sz = as_f16x2(sv[slot][i]);
+      const f16 zb = (f16)1024.0f + sz.y;  // 1024 + zero, exact
+      s2[i] = f16x2{sz.x, sz.x};
+      z2[i] = f16x2{zb, zb};
+    }
+    // the chunk's KS x TJ token fragments in (k step, token tile) order, each read from LDS RB fragments ahead of
+    // its MFMAs so the reads' latency hides behind the MFMAs of the ones before it
+    constexpr int NB = KS * TJ, RB = RS_AHEAD;
+    h8 b[RB + 1];
+    auto read_b = [&](int q) {
+      return __builtin_bit_cast(h8, Xs[buf][32 * (q % TJ) + r][(8 * h + q / TJ) ^ (r & 15)]);
+    };
+#pragma unroll
+    for (int q = 0; q < RB; ++q) b[q] = read_b(q);
+    h8 a[TI];
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      if (q + RB < NB) b[(q + RB) % (RB + 1)] = read_b(q + RB);
+      if (q % TJ == 0) {
+        const int s = q / TJ;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+          a[i] = __builtin_bit_cast(h8, dequant8_sz(wv[slot][i][s >> 2][s & 3], s2[i], z2[i], mlo));
+      }
+#pragma unroll
+      for (int i = 0; i < TI; ++i) acc[i][q % TJ] = mfma32x32(a[i], b[q % (RB + 1)], acc[i][q % TJ]);
+    }
+  };
+  fetch(0, 0);
+  phase_fence();
+  stage(0);
+  phase_fence();
+  fetch(1, 1);
+  phase_fence();
+  __syncthreads();
+  // one chunk: compute c, stage c + 1, fetch c + 2 into the registers chunk c (W) and c + 1 (X) held
+  auto step = [&](int kc, int p) {
+    compute(p, p);
+    stage(p ^ 1);
+    phase_fence();
+    fetch(kc + 2, p);
+    phase_fence();
+    __syncthreads();
+  };
+  // pairs of chunks in the loop, so every chunk's register slot and LDS buffer is a constant
+  int kc = 0;
+  for (; kc + 2 <= nk; kc += 2) {
+    step(kc, 0);
+    step(kc + 1, 1);
+  }
+  if (kc < nk) step(kc, 0);
+  // ---- epilogue: lane holds Y[token m0 + 32 j + r][n0 + 64 wave + 32 i + 8 q + 4 h + v] in acc[i][j][4 q + v]
+  const bool vec = (N & 3) == 0;
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int m = m0 + 32 * j + r;
+    if (m >= M) continue;
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wave * kRsRows + 32 * i + 8 * q + 4 * h;
+        if (n >= N) continue;
+        const f16 y0 = (f16)acc[i][j][4 * q], y1 = (f16)acc[i][j][4 * q + 1];
+        const f16 y2 = (f16)acc[i][j][4 * q + 2], y3 = (f16)acc[i][j][4 * q + 3];
+        if constexpr (EPI == 0) {
+          f16* dst = Y + (size_t)m * N + n;
+          if (vec && n + 3 < N) {
+            u32x2 o;
+            o[0] = as_u32(f16x2{y0, y1});
+            o[1] = as_u32(f16x2{y2, y3});
+            *reinterpret_cast<u32x2*>(dst) = o;
+          } else {
+            const f16 yy[4] = {y0, y1, y2, y3};
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              if (n + v < N) dst[v] = yy[v];
+          }
+        } else {
+          // rows (n, n + 1) and (n + 2, n + 3) are (gate, up) pairs n / 2 and n / 2 + 1 of act[M, N / 2]
+          f16* dst = Y + (size_t)m * (N >> 1) + (n >> 1);
+          const f16 a0 = silu_mul(y0, y1), a1 = silu_mul(y2, y3);
+          if (vec && n + 3 < N) {
+            *reinterpret_cast<uint32_t*>(dst) = as_u32(f16x2{a0, a1});
+          } else {
+            if (n + 1 < N) dst[0] = a0;
+            if (n + 3 < N) dst[1] = a1;
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int BM>
+void launch_rs(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int log2G,
+               int epilogue, hipStream_t st) {
+  const int tiles_m = (M + BM - 1) / BM, tiles = tiles_m * ((N + 4 * kRsRows - 1) / (4 * kRsRows));
+  const dim3 grid((tiles + kXcds - 1) / kXcds * kXcds);
+  if (epilogue == 1)
+    hipLaunchKernelGGL((gemm_w4a16_rs<BM, 1>), grid, dim3(kRsThreads), 0, st, (const uint32_t*)packed,
+                       (const uint32_t*)sz, (const f16*)x, (f16*)y, M, N, K, log2G, tiles_m, tiles);
+  else
+    hipLaunchKernelGGL((gemm_w4a16_rs<BM, 0>), grid, dim3(kRsThreads), 0, st, (const uint32_t*)packed,
+                       (const uint32_t*)sz, (const f16*)x, (f16*)y, M, N, K, log2G, tiles_m, tiles);
+}
+
 #ifndef DK_GEMM_PD
 #define DK_GEMM_PD 2
 #endif
@@ -386,15 +604,26 @@ void launch_wide(const void* packed, const void* sz, const void* x, void* y, int
 
 }  // namespace
 
-// Tile choice: the largest of 128 x 128, 128 x 64, 64 x 64 whose grid still covers the 256 CUs, then K groups
-// (KG = 2 or 4 four-wave groups per workgroup; 2 at most for 128 x 64, by LDS) while the grid leaves CUs with a single
-// workgroup; K % 64 != 0 takes the
-// 64 x 64 16x16x16 kernel above. Returns 10 * tile + KG (tile 3: 128 x 128, 2: 128 x 64, 1: 64 x 64), 0 for that one.
+// Tile choice: the register-stationary kernel (K % 128 == 0, G >= 64) with 256 weight rows x 128 tokens when that
+// gives at least 320 tiles (two workgroups per CU: 512 slots), else x 64 tokens when that gives at least 160 (returns
+// 42 and 41). Otherwise the wide kernel: the largest of 128 x 128, 128 x 64, 64 x 64 whose grid still covers the 256
+// CUs, then K groups (KG = 2 or 4 four-wave groups per workgroup; 2 at most for 128 x 64, by LDS) while the grid leaves
+// CUs with a single workgroup (returns 10 * tile + KG, tile 3: 128 x 128, 2: 128 x 64, 1: 64 x 64); K % 64 != 0 takes
+// the 64 x 64 16x16x16 kernel above (returns 0).
 #ifndef DK_GEMM_KG
 #define DK_GEMM_KG 0
 #endif
-int gemm_w4a16_tile(int M, int N, int K) {
+#ifndef DK_GEMM_RS
+#define DK_GEMM_RS 1
+#endif
+int gemm_w4a16_tile(int M, int N, int K, int log2G) {
   if (K % kWK != 0) return 0;
+  if (DK_GEMM_RS && K % kRsK == 0 && log2G >= 6 && (long long)N * K <= 0x7fffffffLL &&
+      (long long)M * K <= 0x3fffffffLL) {
+    const long long n_t = (N + 4 * kRsRows - 1) / (4 * kRsRows);
+    if (n_t * ((M + 127) / 128) >= 320) return 40 + 2;
+    if (n_t * ((M + 63) / 64) >= 160) return 40 + 1;
+  }
   const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128);
   const long long t64m = (long long)((M + 63) / 64) * ((N + 127) / 128);
   const long long t64 = (long long)((M + 63) / 64) * ((N + 63) / 64);
@@ -416,7 +645,9 @@ int gemm_w4a16_tile(int M, int N, int K) {
 
 void launch_gemm_w4a16(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int log2G,
                        int epilogue, hipStream_t st) {
-  switch (gemm_w4a16_tile(M, N, K)) {
+  switch (gemm_w4a16_tile(M, N, K, log2G)) {
+    case 42: launch_rs<128>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
+    case 41: launch_rs<64>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
     case 31: launch_wide<128, 128, 1>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
     case 21: launch_wide<128, 64, 1>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
     case 22: launch_wide<128, 64, 2>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;

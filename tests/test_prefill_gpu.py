@@ -28,14 +28,18 @@ def _weights(K, N, Kd, G, seed):
     return packed, sz
 
 
-# kernel coverage: K % 64 == 0 -> the wide kernel, tiles 128 x 128, 128 x 64, 64 x 64 and 1, 2 or 4 K groups by
-# grid size (the last three cases are wide grids at G 64 and 32, one ragged); K % 64 == 32 -> the 16x16x16 kernel;
-# N % 4 != 0 -> the element-wise epilogue stores
+# kernel coverage: K % 128 == 0, G >= 64 and at least 320 tiles of 256 weight rows x 128 tokens -> the
+# register-stationary kernel with 128-token tiles (the last four cases: G 64, 128 and 256, ragged M and N, an odd
+# chunk count), at least 160 tiles of 256 x 64 -> the same with 64-token tiles ((512, 11264) and the ragged
+# (200, 12302) at G 64); otherwise K % 64 == 0 -> the wide kernel, tiles 128 x 128, 128 x 64, 64 x 64 and 1, 2 or 4
+# K groups by grid size; K % 64 == 32 -> the 16x16x16 kernel; N % 4 != 0 -> the element-wise epilogue stores
 @pytest.mark.parametrize("M,N,Kd,G", [(1, 64, 256, 128), (7, 2560, 2048, 128), (64, 2048, 2048, 64),
                                       (100, 1000, 5632, 128), (512, 11264, 2048, 128), (33, 4096, 4096, 32),
                                       (512, 4096, 1024, 128), (70, 999, 256, 128), (40, 300, 320, 64),
                                       (300, 4100, 448, 64), (512, 8192, 192, 64), (20, 100, 96, 32),
-                                      (256, 32768, 256, 64), (512, 16384, 256, 32), (500, 16400, 192, 64)])
+                                      (500, 16400, 192, 64), (256, 65536, 256, 64), (512, 16384, 256, 32),
+                                      (400, 8000, 256, 32), (200, 12302, 640, 64),
+                                      (300, 49002, 384, 128), (130, 98304, 512, 256), (512, 28672, 1024, 128)])
 def test_gemm_matches_oracle(K, M, N, Kd, G):
     packed, sz = _weights(K, N, Kd, G, seed=M + N)
     wref = dequant_from_gpu(packed, sz, G)
@@ -46,8 +50,11 @@ def test_gemm_matches_oracle(K, M, N, Kd, G):
     assert_close(y, ref, 5e-3, f"gemm {M}x{N}x{Kd} G{G}")
 
 
-def test_gemm_one_hot_rows_exact(K):
-    N, Kd, G = 200, 512, 64
+@pytest.mark.parametrize("N", [200, 49152])
+def test_gemm_one_hot_rows_exact(K, N):
+    """Row i of X is one-hot at k_i, so row i of Y is column k_i of the dequantized weight, bit for bit (N 49152 runs
+    the register-stationary kernel, whose k order within an MFMA step is permuted)."""
+    Kd, G = 512, 64
     packed, sz = _weights(K, N, Kd, G, seed=9)
     wref = dequant_from_gpu(packed, sz, G)
     ks = [0, 1, 7, 8, 31, 32, 127, 128, 300, 511]
@@ -60,7 +67,7 @@ def test_gemm_one_hot_rows_exact(K):
 
 
 @pytest.mark.parametrize("M,I,Kd", [(16, 5632, 2048), (130, 512, 256), (1, 64, 1024), (9, 513, 320), (33, 70, 96),
-                                    (512, 8192, 256)])
+                                    (512, 8192, 256), (260, 14000, 640)])
 def test_gemm_swiglu_epilogue(K, M, I, Kd):
     from runtime.model import interleave_halves
     G = 128 if Kd % 128 == 0 else (64 if Kd % 64 == 0 else 32)
