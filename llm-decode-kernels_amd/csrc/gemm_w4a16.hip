@@ -1,22 +1,30 @@
 // W4A16 GEMM for prefill on gfx950: Y[M, N] = X[M, K] . dequant(W)[N, K]^T  (fp16 in/out, fp32 accumulation)
 //
 // The prompt's tokens go through a layer together, so the projections are GEMMs, MFMA-shaped work. The weight format
-// is the decode GEMV's (packed int32 [N, K/8], (scale, zero) fp16 [N, K/G, 2]); each weight is dequantized on its way
-// into LDS as fp16((q - zero) * scale) with one rounding -- the reference's dequantize (runtime/quant.py:93-97) bit
-// for bit: (1024 + q) - (1024 + zero) is an exact fp16 integer and its fp16 product with the fp16 scale rounds the
-// exact product once -- so every v_mfma_f32_16x16x16_f16 product is exact and the sums are fp32.
+// is the decode GEMV's (packed int32 [N, K/8], (scale, zero) fp16 [N, K/G, 2]); each weight is dequantized as
+// fp16((q - zero) * scale) with one rounding -- the reference's dequantize (runtime/quant.py:93-97) bit for bit:
+// (1024 + q) - (1024 + zero) is an exact fp16 integer and its fp16 product with the fp16 scale rounds the exact
+// product once -- so every MFMA product is exact and the sums are fp32.
 //
-// Block tile 64 x 64 of Y, four waves of 32 x 32 (2 x 2 MFMA tiles of 16 x 16), K in chunks of 32 (one 16-byte word
-// group of each weight row; G >= 32 so a chunk never straddles a group). Per chunk the 256 threads stage X [64 x 32]
-// (one 16-byte load each) and the dequantized W [64 x 32] (one packed word and its scale/zero each) in LDS rows padded
-// to 40 halves (80 B: the 16 rows a wave reads for one operand fall in distinct banks), then each wave runs 2 k-steps
-// x 4 MFMAs. The next chunk's global loads are issued before the current chunk's MFMAs (two LDS buffers, one barrier
-// per chunk).
-//   Operands (lane l = 16 g + c): A = X rows, lane l holds X[row c][k 4g..4g+3]; B = W^T, lane l holds
-//   W[col c][k 4g..4g+3]; the accumulator leaves lane l with Y[rows 4g..4g+3][col c].
-// Epilogue 0 writes Y [M, N]; epilogue 1 treats the columns as interleaved gate / up pairs (col 2i = gate_i, col
+// Three kernels, chosen by grid size (gemm_w4a16_tile at the end of this file):
+//   * register-stationary (K % 128 == 0, G >= 64, a few hundred tiles of 256 weight rows): each wave's 64 weight
+//     rows are dequantized in registers straight into the v_mfma_f32_32x32x16_f16 A layout; only the token tile
+//     passes through LDS. The fastest form, described at its definition.
+//   * wide (K % 64 == 0): weight and token tiles of 64 or 128 both staged in LDS (the weights dequantized on the
+//     way), v_mfma_f32_16x16x32_f16, optional K groups inside a workgroup for grids that do not fill the CUs.
+//   * the 64 x 64 kernel below (K % 64 == 32): v_mfma_f32_16x16x16_f16 over K chunks of 32.
+// Epilogue 0 writes Y [M, N]; epilogue 1 treats the weight rows as interleaved gate / up pairs (row 2i = gate_i, row
 // 2i + 1 = up_i, the decode runtime's layout) and writes act[M, N/2] = silu_mul(fp16(gate), fp16(up)), the swiglu
 // of the reference's composition with its rounding points.
+//
+// 64 x 64 kernel: block tile 64 x 64 of Y, four waves of 32 x 32 (2 x 2 MFMA tiles of 16 x 16), K in chunks of 32
+// (one 16-byte word group of each weight row; G >= 32 so a chunk never straddles a group). Per chunk the 256 threads
+// stage X [64 x 32] (one 16-byte load each) and the dequantized W [64 x 32] (one packed word and its scale/zero each)
+// in LDS rows padded to 40 halves (80 B: the 16 rows a wave reads for one operand fall in distinct banks), then each
+// wave runs 2 k-steps x 4 MFMAs. The next chunk's global loads are issued before the current chunk's MFMAs (two LDS
+// buffers, one barrier per chunk).
+//   Operands (lane l = 16 g + c): A = X rows, lane l holds X[row c][k 4g..4g+3]; B = W^T, lane l holds
+//   W[col c][k 4g..4g+3]; the accumulator leaves lane l with Y[rows 4g..4g+3][col c].
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -375,21 +383,26 @@ gemm_w4a16_wide(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int
 // loads) -- and are dequantized there, already in the MFMA A layout: no weight passes through LDS and each is
 // dequantized once. Only the token tile X [BM x 128] is staged in LDS (rows of 256 bytes, 16-byte chunk q of row t at
 // q ^ (t & 15)), written once per chunk and read by all four waves.
-//   MFMA: v_mfma_f32_32x32x16_f16, the form that reaches this part's MFMA rate (a 16x16x32 stream tops out near
-//   three quarters of it per clock). k order: in k step s (0..7) of a chunk, lane (h, r) takes word 8h + s of its row
+//   MFMA: v_mfma_f32_32x32x16_f16. A stream of independent 32x32x16 MFMAs runs at one per 32 clocks per SIMD (the
+//   dense fp16 rate), a stream of 16x16x32 ones at about three quarters of that, so the 32 x 32 form carries the
+//   kernel; the dequant's vector instructions issue between the MFMAs, one k step ahead of them. k order: in k step s (0..7) of a chunk, lane (h, r) takes word 8h + s of its row
 //   (k 64h + 8s .. + 7) and the same eight k of its token row from LDS -- one order for both operands, so the products
 //   and their sums are those of the plain order. The accumulator of tile (i, j) leaves lane (h, r) with rows
 //   8 q + 4 h + v (q, v = 0..3) of the weight tile for token r: four consecutive outputs of one token per q.
 //   LDS traffic: per k step a wave reads BM / 32 token fragments of 1 KB for 2 BM / 32 MFMAs of 32 cycles, 8 bytes
 //   per MFMA cycle, 32 per CU cycle with four waves at the full MFMA rate, plus the stage's 16.
-// Pipeline per chunk c: compute chunk c (dequant of W(c) in registers, X(c) from LDS buffer c & 1), store X(c + 1)
-// (loaded a chunk earlier) into the other buffer, issue the loads of chunk c + 2, barrier. W, scales and X come in
+// Pipeline per chunk c: compute chunk c (dequant of W(c) in registers, one k step ahead of the MFMAs; X(c) from LDS
+// buffer c & 1); halfway through, store the first half of X(c + 1) (loaded a chunk earlier) into the other buffer and
+// load its second half; after the MFMAs store that half, issue the loads of X(c + 2)'s first half and W(c + 2), barrier. W, scales and X come in
 // through buffer loads (SGPR base and chunk offset, a constant VGPR offset per row), so moving to the next chunk costs
 // no vector instruction; the host checks that every offset fits 31 bits. Two workgroups share a CU (accumulators and
 // operands in the 256 architectural VGPRs of a wave).
 constexpr int kRsK = 128, kRsRows = 64, kRsThreads = 256;
 #ifndef RS_AHEAD
-#define RS_AHEAD 2
+#define RS_AHEAD 3
+#endif
+#ifndef RS_XSPLIT
+#define RS_XSPLIT (KS * TJ / 2)
 #endif
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -413,50 +426,55 @@ gemm_w4a16_rs(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int M
   const int per = gridDim.x / kXcds;
   const int t = (int)(blockIdx.x % kXcds) * per + (int)(blockIdx.x / kXcds);
   if (t >= tiles) return;  // uniform: the grid is rounded up to a multiple of the XCD count
-  const int m0 = (t % tiles_m) * BM, n0 = (t / tiles_m) * (4 * kRsRows);
+  // a ragged last tile is shifted inward (the launcher requires M >= BM and N >= 256), so every row a lane loads is
+  // valid; the rows it shares with its neighbour tile are computed by both, bit for bit alike, and stored twice
+  const int m0 = min((t % tiles_m) * BM, M - BM), n0 = min((t / tiles_m) * (4 * kRsRows), N - 4 * kRsRows);
   const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 31, h = lane >> 5;
   const int KW = K >> 3, NG = K >> gsh, nk = K / kRsK;
   const __amdgpu_buffer_rsrc_t wres = buffer_of(W, (uint32_t)N * (uint32_t)KW * 4u);
   const __amdgpu_buffer_rsrc_t sres = buffer_of(SZ, (uint32_t)N * (uint32_t)NG * 4u);
   const __amdgpu_buffer_rsrc_t xres = buffer_of(X, (uint32_t)M * (uint32_t)K * 2u);
-  // rows past N or M re-read the last valid row (their results are never stored); the lane's scale is that of its
-  // first k, k0 + 64 h, whose group holds all 64 of its k (G >= 64)
-  uint32_t wo[TI], so[TI];
-#pragma unroll
-  for (int i = 0; i < TI; ++i) {
-    const uint32_t row = (uint32_t)min(n0 + wave * kRsRows + 32 * i + r, N - 1);
-    wo[i] = row * (uint32_t)KW * 4u + 32u * (uint32_t)h;
-    so[i] = (row * (uint32_t)NG + (uint32_t)((64 * h) >> gsh)) * 4u;
-  }
+  // one VGPR offset per operand; the row tile (W, scales) and row block (X) go into the SGPR offset. The lane's scale
+  // is that of its first k, k0 + 64 h, whose group holds all 64 of its k (G >= 64).
+  const uint32_t row = (uint32_t)(n0 + wave * kRsRows + r);
+  const uint32_t wo = row * (uint32_t)KW * 4u + 32u * (uint32_t)h;
+  const uint32_t so = (row * (uint32_t)NG + (uint32_t)((64 * h) >> gsh)) * 4u;
   // X staging: chunk xq of rows xr + 16 v, stored at chunk xq ^ xr of the row (xr = (xr + 16 v) & 15)
   const int xq = tid & 15, xr = tid >> 4;
-  uint32_t xo[XL];
-#pragma unroll
-  for (int v = 0; v < XL; ++v) xo[v] = (uint32_t)min(m0 + xr + 16 * v, M - 1) * (uint32_t)K * 2u + 16u * (uint32_t)xq;
+  const uint32_t xo = (uint32_t)(m0 + xr) * (uint32_t)K * 2u + 16u * (uint32_t)xq;
 
-  u32x4 xv[XL], wv[2][TI][2];
+  // with 128-token tiles X is staged in two halves of XL / 2 rows per thread, so only half a chunk of it is ever held
+  // in registers (the accumulators leave no room for more); W and the scales are held for two chunks, the one
+  // computed and the next
+  constexpr int NXH = BM >= 128 ? 2 : 1, XH = XL / NXH;
+  u32x4 xv[XH], wv[2][TI][2];
   uint32_t sv[2][TI];
   // loads are unconditional (chunks past the end re-read the last one): a load behind a branch would make the
   // compiler drain every outstanding load at the join
-  auto fetch = [&](int kc, int slot) {
+  auto fetch_x = [&](int kc, int half) {
     const int k0 = min(kc, nk - 1) * kRsK;
 #pragma unroll
-    for (int v = 0; v < XL; ++v)
-      xv[v] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, xo[v], 2 * k0, 0));
+    for (int v = 0; v < XH; ++v)
+      xv[v] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, xo, 2 * k0 + 32 * K * (v + XH * half), 0));
+  };
+  auto fetch_w = [&](int kc, int slot) {
+    const int k0 = min(kc, nk - 1) * kRsK;
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
 #pragma unroll
       for (int u = 0; u < 2; ++u)
-        wv[slot][i][u] =
-            __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, wo[i] + 16u * u, k0 >> 1, 0));
+        wv[slot][i][u] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, wo + 16u * u, (k0 >> 1) + 128 * KW * i, 0));
     }
 #pragma unroll
-    for (int i = 0; i < TI; ++i) sv[slot][i] = __builtin_amdgcn_raw_buffer_load_b32(sres, so[i], (k0 >> gsh) * 4, 0);
+    for (int i = 0; i < TI; ++i)
+      sv[slot][i] = __builtin_amdgcn_raw_buffer_load_b32(sres, so, ((k0 >> gsh) + 32 * NG * i) * 4, 0);
   };
-  auto stage = [&](int buf) {
+  auto stage = [&](int buf, int half) {
 #pragma unroll
-    for (int v = 0; v < XL; ++v) Xs[buf][xr + 16 * v][xq ^ xr] = xv[v];
+    for (int v = 0; v < XH; ++v) Xs[buf][xr + 16 * (v + XH * half)][xq ^ xr] = xv[v];
   };
   f32x16 acc[TI][TJ];
 #pragma unroll
@@ -465,7 +483,9 @@ gemm_w4a16_rs(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int M
     for (int j = 0; j < TJ; ++j) acc[i][j] = f32x16{};
   }
   const uint32_t mlo = vgpr_const(0x000F000Fu);
-  auto compute = [&](int buf, int slot) {
+  // MFMAs of one chunk; `mid` (the next chunk's first X half into LDS, its second half's loads) runs after the
+  // MFMAs of the first RS_XSPLIT fragments
+  auto compute = [&](int buf, int slot, auto&& mid) {
     // the chunk's weight words and scales enter here: without the pin the compiler hoists their first use above the
     // previous chunk's barrier, where waiting for them drains the newer loads as well
 #pragma unroll
@@ -488,35 +508,60 @@ gemm_w4a16_rs(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int M
     auto read_b = [&](int q) {
       return __builtin_bit_cast(h8, Xs[buf][32 * (q % TJ) + r][(8 * h + q / TJ) ^ (r & 15)]);
     };
+    // k step s + 1's weights are dequantized while step s's MFMAs run (two sets of A operands)
+    auto dequant = [&](int s, h8 (&a)[TI]) {
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+        a[i] = __builtin_bit_cast(h8, dequant8_sz(wv[slot][i][s >> 2][s & 3], s2[i], z2[i], mlo));
+    };
 #pragma unroll
     for (int q = 0; q < RB; ++q) b[q] = read_b(q);
-    h8 a[TI];
+    h8 a[2][TI];
+    dequant(0, a[0]);
 #pragma unroll
     for (int q = 0; q < NB; ++q) {
+      const int s = q / TJ;
+      if (q == RS_XSPLIT) mid();
       if (q + RB < NB) b[(q + RB) % (RB + 1)] = read_b(q + RB);
-      if (q % TJ == 0) {
-        const int s = q / TJ;
 #pragma unroll
-        for (int i = 0; i < TI; ++i)
-          a[i] = __builtin_bit_cast(h8, dequant8_sz(wv[slot][i][s >> 2][s & 3], s2[i], z2[i], mlo));
-      }
-#pragma unroll
-      for (int i = 0; i < TI; ++i) acc[i][q % TJ] = mfma32x32(a[i], b[q % (RB + 1)], acc[i][q % TJ]);
+      for (int i = 0; i < TI; ++i) acc[i][q % TJ] = mfma32x32(a[s & 1][i], b[q % (RB + 1)], acc[i][q % TJ]);
+      if (q % TJ == 0 && s + 1 < KS) dequant(s + 1, a[(s + 1) & 1]);
     }
   };
-  fetch(0, 0);
+  // prologue: X(0) into buffer 0, X(1)'s first half in flight, W(0) and W(1) in flight
+  fetch_x(0, 0);
+  fetch_w(0, 0);
   phase_fence();
-  stage(0);
+  stage(0, 0);
   phase_fence();
-  fetch(1, 1);
+  if constexpr (NXH == 2) {
+    fetch_x(0, 1);
+    phase_fence();
+    stage(0, 1);
+    phase_fence();
+  }
+  fetch_x(1, 0);
+  fetch_w(1, 1);
   phase_fence();
   __syncthreads();
-  // one chunk: compute c, stage c + 1, fetch c + 2 into the registers chunk c (W) and c + 1 (X) held
+  // one chunk c: MFMAs from LDS buffer c & 1 and register slot c & 1; inside them X(c + 1)'s first half goes to the
+  // other buffer and its second half is loaded; after them that half is stored, X(c + 2)'s first half and W(c + 2)
+  // are loaded (issue order = wait order: each wait leaves the newer loads in flight). With one X part (64-token
+  // tiles) all of X(c + 1) is stored after the MFMAs.
   auto step = [&](int kc, int p) {
-    compute(p, p);
-    stage(p ^ 1);
+    compute(p, p, [&] {
+      if constexpr (NXH == 2) {
+        phase_fence();
+        stage(p ^ 1, 0);
+        phase_fence();
+        fetch_x(kc + 1, 1);
+        phase_fence();
+      }
+    });
+    stage(p ^ 1, NXH - 1);
     phase_fence();
-    fetch(kc + 2, p);
+    fetch_x(kc + 2, 0);
+    fetch_w(kc + 2, p);
     phase_fence();
     __syncthreads();
   };
@@ -573,6 +618,7 @@ gemm_w4a16_rs(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int M
 template <int BM>
 void launch_rs(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int log2G,
                int epilogue, hipStream_t st) {
+  // requires M >= BM and N >= 256 (the last tile in each direction is shifted inward)
   const int tiles_m = (M + BM - 1) / BM, tiles = tiles_m * ((N + 4 * kRsRows - 1) / (4 * kRsRows));
   const dim3 grid((tiles + kXcds - 1) / kXcds * kXcds);
   if (epilogue == 1)
@@ -604,9 +650,9 @@ void launch_wide(const void* packed, const void* sz, const void* x, void* y, int
 
 }  // namespace
 
-// Tile choice: the register-stationary kernel (K % 128 == 0, G >= 64) with 256 weight rows x 128 tokens when that
-// gives at least 320 tiles (two workgroups per CU: 512 slots), else x 64 tokens when that gives at least 160 (returns
-// 42 and 41). Otherwise the wide kernel: the largest of 128 x 128, 128 x 64, 64 x 64 whose grid still covers the 256
+// Tile choice: the register-stationary kernel (K % 128 == 0, G >= 64, N >= 256) with 256 weight rows x 128 tokens
+// when M >= 128 and that gives at least 320 tiles (two workgroups per CU: 512 slots), else x 64 tokens when M >= 64
+// and that gives at least 160 (returns 42 and 41). Otherwise the wide kernel: the largest of 128 x 128, 128 x 64, 64 x 64 whose grid still covers the 256
 // CUs, then K groups (KG = 2 or 4 four-wave groups per workgroup; 2 at most for 128 x 64, by LDS) while the grid leaves
 // CUs with a single workgroup (returns 10 * tile + KG, tile 3: 128 x 128, 2: 128 x 64, 1: 64 x 64); K % 64 != 0 takes
 // the 64 x 64 16x16x16 kernel above (returns 0).
@@ -621,8 +667,8 @@ int gemm_w4a16_tile(int M, int N, int K, int log2G) {
   if (DK_GEMM_RS && K % kRsK == 0 && log2G >= 6 && (long long)N * K <= 0x7fffffffLL &&
       (long long)M * K <= 0x3fffffffLL) {
     const long long n_t = (N + 4 * kRsRows - 1) / (4 * kRsRows);
-    if (n_t * ((M + 127) / 128) >= 320) return 40 + 2;
-    if (n_t * ((M + 63) / 64) >= 160) return 40 + 1;
+    if (M >= 128 && N >= 256 && n_t * ((M + 127) / 128) >= 320) return 40 + 2;
+    if (M >= 64 && N >= 256 && n_t * ((M + 63) / 64) >= 160) return 40 + 1;
   }
   const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128);
   const long long t64m = (long long)((M + 63) / 64) * ((N + 127) / 128);
