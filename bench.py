@@ -599,22 +599,24 @@ def gemm_leg(Kx, M=512, reps=5, eager=4, G=128):
         packed, sz = quantize_pack((torch.randn(N, K, generator=g, device="cuda") * 0.02).half(), G)
         x = torch.randn(M, K, generator=g, device="cuda").half()
         y = torch.empty(M, N // (1 + epi), dtype=torch.half, device="cuda")
+        wsb = Kx.gemm_workspace_bytes(M, N, K, G, epi)     # split-K workspace, as Model.gemm passes it
+        ws = torch.empty(wsb, dtype=torch.uint8, device="cuda") if wsb else None
         for _ in range(eager):
-            Kx.gemm_w4a16(packed, sz, x, y, G, epilogue=epi)
+            Kx.gemm_w4a16(packed, sz, x, y, G, epilogue=epi, workspace=ws)
         torch.cuda.synchronize()
-        w = windowed_time(lambda i: Kx.gemm_w4a16(packed, sz, x, y, G, epilogue=epi), 8, reps, warm_ms=100.0,
-                          window_ms=40.0)
+        w = windowed_time(lambda i: Kx.gemm_w4a16(packed, sz, x, y, G, epilogue=epi, workspace=ws), 8, reps,
+                          warm_ms=100.0, window_ms=40.0)
         w16 = torch.randn(N, K, generator=g, device="cuda").half()
         yb = torch.empty(M, N, dtype=torch.half, device="cuda")
         wb = windowed_time(lambda i: torch.mm(x, w16.t(), out=yb), 8, reps, warm_ms=30.0, window_ms=40.0)
         fl = 2 * M * N * K
-        out[name] = {"M": M, "N": N, "K": K, "epilogue": epi, "us": round(w["median_us"], 2),
+        out[name] = {"M": M, "N": N, "K": K, "epilogue": epi, "splitk_workspace_bytes": wsb, "us": round(w["median_us"], 2),
                      "tflops": round(fl / w["median_us"] / 1e6, 1), "hipblaslt_fp16_us": round(wb["median_us"], 2),
                      "hipblaslt_fp16_tflops": round(fl / wb["median_us"] / 1e6, 1),
                      "sclk_median": w["clocks"].get("sclk_mhz", {}).get("median")}
         log(f"gemm {name} {M}x{N}x{K}: {out[name]['us']} us ({out[name]['tflops']} TFLOP/s), hipBLASLt fp16 "
             f"{out[name]['hipblaslt_fp16_us']} us")
-        del packed, sz, w16, yb
+        del packed, sz, w16, yb, ws
         torch.cuda.empty_cache()
     return out
 

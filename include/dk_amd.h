@@ -185,6 +185,18 @@ int dk_gemm_w4a16(const void* packed, const void* sz, const void* x, void* y, in
                   int epilogue, void* stream);
 
 /*
+ * dk_gemm_w4a16 with a caller-provided workspace for split-K: shapes whose weight rows are too few to fill the CUs
+ * (e.g. 4096 x 14336 or 4096 x 4096 at M 512) split K over S workgroups per tile, write fp32 partials [S, M, N] to
+ * the workspace and sum them in a second launch, in split order (the result does not depend on scheduling; its fp32
+ * summation order differs from the unsplit kernel's). dk_gemm_w4a16_workspace_bytes returns the bytes a shape needs
+ * (0: it does not split; epilogue 1 never splits). workspace NULL runs dk_gemm_w4a16; otherwise it must hold that
+ * many bytes, be 16-byte aligned and overlap neither x nor y. Like dk_gemm_w4a16, no counterpart in the reference.
+ */
+size_t dk_gemm_w4a16_workspace_bytes(int M, int N, int K, int group, int epilogue);
+int dk_gemm_w4a16_ws(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int group,
+                     int epilogue, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Read-bandwidth probe: `blocks` workgroups of `threads` threads read the first floor(bytes / 16) 16-byte words of buf
  * once, workgroup b the b-th of `blocks` contiguous slabs of n / blocks or n / blocks + 1 of the n words, in rounds of
  * unroll x threads words (every lane's `unroll` loads of a round in flight together). With

@@ -24,6 +24,10 @@ int fail(int code, const char* fmt, ...) {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 bool pow2(long long v) { return v > 0 && (v & (v - 1)) == 0; }
+bool ranges_overlap(const void* a, size_t na, const void* b, size_t nb) {
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return x < y + nb && y < x + na;
+}
 int ilog2(long long v) {
   int r = 0;
   while ((1LL << r) < v) ++r;
@@ -232,8 +236,8 @@ int dk_gemv_f16_rmsnorm(int R, int warps, int pf, const void* w, const void* x, 
   return launched("gemv_f16_rmsnorm");
 }
 
-int dk_gemm_w4a16(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int group,
-                  int epilogue, void* stream) {
+static int gemm_check(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int group,
+                      int epilogue) {
   if (!packed || !sz || !x || !y) return fail(DK_ERR_NULL, "gemm_w4a16: null pointer argument");
   if (M <= 0 || N <= 0 || K <= 0) return fail(DK_ERR_SHAPE, "gemm_w4a16: M, N and K must be positive");
   if (M > 65535 * 64) return fail(DK_ERR_SHAPE, "gemm_w4a16: M too large (%d)", M);
@@ -248,9 +252,41 @@ int dk_gemm_w4a16(const void* packed, const void* sz, const void* x, void* y, in
   if (!aligned16(packed) || !aligned16(x)) return fail(DK_ERR_ALIGN, "gemm_w4a16: packed and x must be 16B aligned");
   if (!aligned4(sz)) return fail(DK_ERR_ALIGN, "gemm_w4a16: sz must be 4B aligned");
   if (y == x) return fail(DK_ERR_DOMAIN, "gemm_w4a16: y must not alias x");
+  return DK_OK;
+}
+
+int dk_gemm_w4a16(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int group,
+                  int epilogue, void* stream) {
+  const int rc = gemm_check(packed, sz, x, y, M, N, K, group, epilogue);
+  if (rc != DK_OK) return rc;
   clear_error();
-  dk::launch_gemm_w4a16(packed, sz, x, y, M, N, K, ilog2(group), epilogue, (hipStream_t)stream);
+  dk::launch_gemm_w4a16(packed, sz, x, y, M, N, K, ilog2(group), epilogue, nullptr, (hipStream_t)stream);
   return launched("gemm_w4a16");
+}
+
+size_t dk_gemm_w4a16_workspace_bytes(int M, int N, int K, int group, int epilogue) {
+  if (M <= 0 || N <= 0 || K <= 0 || group < 32 || !pow2(group) || K % group != 0) return 0;
+  return dk::gemm_w4a16_workspace_bytes(M, N, K, ilog2(group), epilogue);
+}
+
+int dk_gemm_w4a16_ws(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int group,
+                     int epilogue, void* workspace, size_t workspace_bytes, void* stream) {
+  const int rc = gemm_check(packed, sz, x, y, M, N, K, group, epilogue);
+  if (rc != DK_OK) return rc;
+  const size_t need = dk::gemm_w4a16_workspace_bytes(M, N, K, ilog2(group), epilogue);
+  if (workspace != nullptr) {
+    if (workspace_bytes < need)
+      return fail(DK_ERR_SHAPE, "gemm_w4a16_ws: workspace of %zu bytes, this shape needs %zu", workspace_bytes, need);
+    if (!aligned16(workspace)) return fail(DK_ERR_ALIGN, "gemm_w4a16_ws: workspace must be 16B aligned");
+    if (need > 0 && ranges_overlap(workspace, need, y, (size_t)M * N * 2))
+      return fail(DK_ERR_DOMAIN, "gemm_w4a16_ws: workspace must not overlap y");
+    if (need > 0 && ranges_overlap(workspace, need, x, (size_t)M * K * 2))
+      return fail(DK_ERR_DOMAIN, "gemm_w4a16_ws: workspace must not overlap x");
+  }
+  clear_error();
+  dk::launch_gemm_w4a16(packed, sz, x, y, M, N, K, ilog2(group), epilogue, need > 0 ? workspace : nullptr,
+                        (hipStream_t)stream);
+  return launched("gemm_w4a16_ws");
 }
 
 int dk_bw_read(const void* buf, size_t bytes, uint32_t* sink, int sink_words, int blocks, int threads, int unroll,

@@ -416,22 +416,27 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* p, uint3
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }
 
+// EPI 2 (split-K): the grid covers tiles x `splits` work items; item (tile, s) takes the k chunks [s nk / S,
+// (s + 1) nk / S) and writes its fp32 partial sums to Y = ws [S][M][N] (float), for gemm_splitk_reduce.
 template <int BM, int EPI>
 __global__ void __launch_bounds__(kRsThreads, 2)
 gemm_w4a16_rs(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int M, int N, int K, int gsh,
-              int tiles_m, int tiles) {
+              int tiles_m, int tiles, int splits) {
   constexpr int TI = kRsRows / 32, TJ = BM / 32, KS = kRsK / 16;
   constexpr int XL = BM * 16 / kRsThreads;  // 16-byte X loads per thread per chunk
   __shared__ u32x4 Xs[2][BM][16];
   const int per = gridDim.x / kXcds;
-  const int t = (int)(blockIdx.x % kXcds) * per + (int)(blockIdx.x / kXcds);
-  if (t >= tiles) return;  // uniform: the grid is rounded up to a multiple of the XCD count
+  const int item = (int)(blockIdx.x % kXcds) * per + (int)(blockIdx.x / kXcds);
+  if (item >= tiles * splits) return;  // uniform: the grid is rounded up to a multiple of the XCD count
+  // items are split-major with the token tiles fastest, so the tiles that share a weight tile's k range share an XCD
+  const int t = item % tiles, split = item / tiles;
   // a ragged last tile is shifted inward (the launcher requires M >= BM and N >= 256), so every row a lane loads is
   // valid; the rows it shares with its neighbour tile are computed by both, bit for bit alike, and stored twice
   const int m0 = min((t % tiles_m) * BM, M - BM), n0 = min((t / tiles_m) * (4 * kRsRows), N - 4 * kRsRows);
   const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 31, h = lane >> 5;
-  const int KW = K >> 3, NG = K >> gsh, nk = K / kRsK;
+  const int KW = K >> 3, NG = K >> gsh, nk_all = K / kRsK;
+  const int c_lo = split * nk_all / splits, nk = (split + 1) * nk_all / splits - c_lo;  // this item's chunks
   const __amdgpu_buffer_rsrc_t wres = buffer_of(W, (uint32_t)N * (uint32_t)KW * 4u);
   const __amdgpu_buffer_rsrc_t sres = buffer_of(SZ, (uint32_t)N * (uint32_t)NG * 4u);
   const __amdgpu_buffer_rsrc_t xres = buffer_of(X, (uint32_t)M * (uint32_t)K * 2u);
@@ -453,14 +458,14 @@ gemm_w4a16_rs(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int M
   // loads are unconditional (chunks past the end re-read the last one): a load behind a branch would make the
   // compiler drain every outstanding load at the join
   auto fetch_x = [&](int kc, int half) {
-    const int k0 = min(kc, nk - 1) * kRsK;
+    const int k0 = (c_lo + min(kc, nk - 1)) * kRsK;
 #pragma unroll
     for (int v = 0; v < XH; ++v)
       xv[v] = __builtin_bit_cast(
           u32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, xo, 2 * k0 + 32 * K * (v + XH * half), 0));
   };
   auto fetch_w = [&](int kc, int slot) {
-    const int k0 = min(kc, nk - 1) * kRsK;
+    const int k0 = (c_lo + min(kc, nk - 1)) * kRsK;
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
 #pragma unroll
@@ -584,6 +589,12 @@ gemm_w4a16_rs(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int M
       for (int q = 0; q < 4; ++q) {
         const int n = n0 + wave * kRsRows + 32 * i + 8 * q + 4 * h;
         if (n >= N) continue;
+        if constexpr (EPI == 2) {  // fp32 partials, N % 4 == 0 (checked by the launcher)
+          float* dst = reinterpret_cast<float*>(Y) + ((size_t)split * M + m) * N + n;
+          *reinterpret_cast<float4*>(dst) =
+              float4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+          continue;
+        }
         const f16 y0 = (f16)acc[i][j][4 * q], y1 = (f16)acc[i][j][4 * q + 1];
         const f16 y2 = (f16)acc[i][j][4 * q + 2], y3 = (f16)acc[i][j][4 * q + 3];
         if constexpr (EPI == 0) {
@@ -615,18 +626,48 @@ gemm_w4a16_rs(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int M
   }
 }
 
+// Y[m][n] = fp16(sum over s of ws[s][m][n]), s in order (deterministic); four consecutive n per thread (N % 4 == 0).
+__global__ void __launch_bounds__(256)
+gemm_splitk_reduce(const float* __restrict__ ws, int splits, f16* __restrict__ Y, int MN4) {
+  const int i = blockIdx.x * 256 + (int)threadIdx.x;
+  if (i >= MN4) return;
+  const float4* p = reinterpret_cast<const float4*>(ws) + i;
+  float4 a = p[0];
+  for (int s = 1; s < splits; ++s) {
+    const float4 b = p[(size_t)s * MN4];
+    a.x += b.x;
+    a.y += b.y;
+    a.z += b.z;
+    a.w += b.w;
+  }
+  u32x2 o;
+  o[0] = as_u32(f16x2{(f16)a.x, (f16)a.y});
+  o[1] = as_u32(f16x2{(f16)a.z, (f16)a.w});
+  reinterpret_cast<u32x2*>(Y)[i] = o;
+}
+
+// requires M >= BM and N >= 256 (the last tile in each direction is shifted inward); splits > 1: epilogue 0, N % 4
+// == 0 and a workspace of splits * M * N floats (the partials), reduced by a second launch
 template <int BM>
 void launch_rs(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int log2G,
-               int epilogue, hipStream_t st) {
-  // requires M >= BM and N >= 256 (the last tile in each direction is shifted inward)
+               int epilogue, int splits, void* ws, hipStream_t st) {
   const int tiles_m = (M + BM - 1) / BM, tiles = tiles_m * ((N + 4 * kRsRows - 1) / (4 * kRsRows));
-  const dim3 grid((tiles + kXcds - 1) / kXcds * kXcds);
-  if (epilogue == 1)
-    hipLaunchKernelGGL((gemm_w4a16_rs<BM, 1>), grid, dim3(kRsThreads), 0, st, (const uint32_t*)packed,
-                       (const uint32_t*)sz, (const f16*)x, (f16*)y, M, N, K, log2G, tiles_m, tiles);
-  else
-    hipLaunchKernelGGL((gemm_w4a16_rs<BM, 0>), grid, dim3(kRsThreads), 0, st, (const uint32_t*)packed,
-                       (const uint32_t*)sz, (const f16*)x, (f16*)y, M, N, K, log2G, tiles_m, tiles);
+  const dim3 grid((tiles * splits + kXcds - 1) / kXcds * kXcds);
+  const uint32_t* P = (const uint32_t*)packed;
+  const uint32_t* S = (const uint32_t*)sz;
+  if (splits > 1) {
+    hipLaunchKernelGGL((gemm_w4a16_rs<BM, 2>), grid, dim3(kRsThreads), 0, st, P, S, (const f16*)x, (f16*)ws, M, N,
+                       K, log2G, tiles_m, tiles, splits);
+    const int mn4 = M * (N / 4);
+    hipLaunchKernelGGL(gemm_splitk_reduce, dim3((mn4 + 255) / 256), dim3(256), 0, st, (const float*)ws, splits,
+                       (f16*)y, mn4);
+  } else if (epilogue == 1) {
+    hipLaunchKernelGGL((gemm_w4a16_rs<BM, 1>), grid, dim3(kRsThreads), 0, st, P, S, (const f16*)x, (f16*)y, M, N, K,
+                       log2G, tiles_m, tiles, 1);
+  } else {
+    hipLaunchKernelGGL((gemm_w4a16_rs<BM, 0>), grid, dim3(kRsThreads), 0, st, P, S, (const f16*)x, (f16*)y, M, N, K,
+                       log2G, tiles_m, tiles, 1);
+  }
 }
 
 #ifndef DK_GEMM_PD
@@ -662,6 +703,33 @@ void launch_wide(const void* packed, const void* sz, const void* x, void* y, int
 #ifndef DK_GEMM_RS
 #define DK_GEMM_RS 1
 #endif
+// Split-K for grids the register-stationary kernel cannot fill (fewer than 160 tiles of 256 x 64): the smallest
+// power-of-two split S in 2..16 whose S x tiles reaches 384 workgroups while every split keeps at least
+// RS_SPLIT_MIN_CHUNKS of the 128-wide k chunks, and only if S x tiles reaches 192; 1 when the shape does not qualify
+// (epilogue 0, K % 128 == 0, G >= 64, M >= 64, N >= 256, N % 4 == 0, offsets within 31 bits) or already fills the
+// CUs unsplit. Short splits lose: the partials' traffic (S x M x N x 4 bytes, written and read back) and the reduce
+// launch outweigh the fuller grid (TinyLlama qkv 2560 x 2048 at S 4, 4 chunks per split: 27 against 19 us unsplit).
+#ifndef RS_SPLIT_MIN_CHUNKS
+#define RS_SPLIT_MIN_CHUNKS 16
+#endif
+int gemm_w4a16_splits(int M, int N, int K, int log2G, int epilogue) {
+  if (!DK_GEMM_RS || epilogue != 0 || K % kRsK != 0 || log2G < 6 || M < 64 || N < 256 || N % 4 != 0 ||
+      (long long)N * K > 0x7fffffffLL || (long long)M * K > 0x3fffffffLL)
+    return 1;
+  const long long t64 = (long long)((N + 4 * kRsRows - 1) / (4 * kRsRows)) * ((M + 63) / 64);
+  if (t64 >= 160) return 1;
+  const int nk = K / kRsK;
+  int s = 2;
+  while (s < 16 && t64 * s < 384 && nk / (2 * s) >= RS_SPLIT_MIN_CHUNKS) s *= 2;
+  if (nk / s < RS_SPLIT_MIN_CHUNKS || t64 * s < 192) return 1;
+  return s;
+}
+
+size_t gemm_w4a16_workspace_bytes(int M, int N, int K, int log2G, int epilogue) {
+  const int s = gemm_w4a16_splits(M, N, K, log2G, epilogue);
+  return s > 1 ? (size_t)s * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
 int gemm_w4a16_tile(int M, int N, int K, int log2G) {
   if (K % kWK != 0) return 0;
   if (DK_GEMM_RS && K % kRsK == 0 && log2G >= 6 && (long long)N * K <= 0x7fffffffLL &&
@@ -690,10 +758,14 @@ int gemm_w4a16_tile(int M, int N, int K, int log2G) {
 }
 
 void launch_gemm_w4a16(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int log2G,
-                       int epilogue, hipStream_t st) {
+                       int epilogue, void* ws, hipStream_t st) {
+  if (ws != nullptr) {
+    const int splits = gemm_w4a16_splits(M, N, K, log2G, epilogue);
+    if (splits > 1) return launch_rs<64>(packed, sz, x, y, M, N, K, log2G, 0, splits, ws, st);
+  }
   switch (gemm_w4a16_tile(M, N, K, log2G)) {
-    case 42: launch_rs<128>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
-    case 41: launch_rs<64>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
+    case 42: launch_rs<128>(packed, sz, x, y, M, N, K, log2G, epilogue, 1, nullptr, st); return;
+    case 41: launch_rs<64>(packed, sz, x, y, M, N, K, log2G, epilogue, 1, nullptr, st); return;
     case 31: launch_wide<128, 128, 1>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
     case 21: launch_wide<128, 64, 1>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
     case 22: launch_wide<128, 64, 2>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;

@@ -73,7 +73,9 @@ void launch_gemv_f16(int prologue, int R, int waves, int pf, const void* w, cons
 // W4A16 GEMM (prefill): Y[M, N] = X[M, K] . dequant(W)^T; epilogue 1 = SwiGLU of interleaved gate/up column pairs
 // (Y [M, N/2]). K % 32 == 0, group >= 32.
 void launch_gemm_w4a16(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int log2G,
-                       int epilogue, hipStream_t st);
+                       int epilogue, void* ws, hipStream_t st);
+// bytes of fp32 split-K partials launch_gemm_w4a16 uses for this shape when given a workspace (0: it does not split)
+size_t gemm_w4a16_workspace_bytes(int M, int N, int K, int log2G, int epilogue);
 
 // Read-ceiling probe (read_probe.hip): `blocks` workgroups of `threads` threads, workgroup b streaming the b-th of
 // `blocks` equal contiguous slabs in rounds of depth x threads 16-byte words; with sink_words >= blocks x W (W =

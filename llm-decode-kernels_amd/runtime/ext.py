@@ -32,6 +32,8 @@ SIGNATURES = {
     "dk_gemv_f16": ([_I, _I, _I, _P, _P, _P, _I, _I, _P], _I),
     "dk_gemv_f16_rmsnorm": ([_I, _I, _I, _P, _P, _P, _P, _F, _P, _P, _I, _I, _P], _I),
     "dk_gemm_w4a16": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _P], _I),
+    "dk_gemm_w4a16_workspace_bytes": ([_I, _I, _I, _I, _I], _Z),
+    "dk_gemm_w4a16_ws": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _Z, _P], _I),
     "dk_rope_append_rows": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
     "dk_rmsnorm_rows": ([_P, _P, _I, _P, _P, _P, _P, _I, _I, _F, _P], _I),
     "dk_attention_prefill": ([_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P], _I),
@@ -258,7 +260,13 @@ class DecodeKernels:
                    norm_w.data_ptr(), float(eps), ptr(x_out), y.data_ptr(), N, Kd, _stream(x))
 
     # prefill projections: Y = X . dequant(W)^T (epilogue 1: SwiGLU of interleaved gate/up pairs)
-    def gemm_w4a16(self, packed, sz, x, y, group, epilogue=0):
+    def gemm_workspace_bytes(self, M, N, K, group, epilogue=0):
+        """Bytes of split-K workspace dk_gemm_w4a16_ws uses for this shape (0: it does not split)."""
+        return int(self.lib.dk_gemm_w4a16_workspace_bytes(int(M), int(N), int(K), int(group), int(epilogue)))
+
+    def gemm_w4a16(self, packed, sz, x, y, group, epilogue=0, workspace=None):
+        """y = x . dequant(W)^T (epilogue 1: SwiGLU of interleaved gate/up rows); `workspace` (a CUDA tensor of at
+        least gemm_workspace_bytes bytes) lets the shapes that do not fill the CUs split K."""
         for t, n in ((packed, "packed"), (sz, "sz"), (x, "x"), (y, "y")):
             _check_cuda(t, n)
         N, K = packed.size(0), packed.size(1) * 8
@@ -270,8 +278,14 @@ class DecodeKernels:
         _check_dtype(packed, torch.int32, "packed")
         for t, n in ((sz, "sz"), (x, "x"), (y, "y")):
             _check_dtype(t, torch.float16, n)
-        self._call(self.lib.dk_gemm_w4a16, packed.data_ptr(), sz.data_ptr(), x.data_ptr(), y.data_ptr(), M, N, K,
-                   int(group), int(epilogue), _stream(x))
+        if workspace is None:
+            self._call(self.lib.dk_gemm_w4a16, packed.data_ptr(), sz.data_ptr(), x.data_ptr(), y.data_ptr(), M, N, K,
+                       int(group), int(epilogue), _stream(x))
+            return
+        _check_cuda(workspace, "workspace")
+        self._call(self.lib.dk_gemm_w4a16_ws, packed.data_ptr(), sz.data_ptr(), x.data_ptr(), y.data_ptr(), M, N, K,
+                   int(group), int(epilogue), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+                   _stream(x))
 
     # prefill: rope_append over M token rows (row m at position *pos + m)
     def rope_append_rows(self, qkv, cos_t, sin_t, pos, bt, kc, vc, n_q, n_kv):

@@ -624,9 +624,20 @@ class Model:
                 packed, sz = self._gate_up_pairs(lin)
                 self.K.gemm_w4a16(packed, sz, x, y, self.cfg.group, epilogue=1)
             else:
-                self.K.gemm_w4a16(lin.packed, lin.sz, x, y, self.cfg.group)
+                self.K.gemm_w4a16(lin.packed, lin.sz, x, y, self.cfg.group,
+                                  workspace=self._gemm_workspace(x.size(0), lin.N, lin.K))
         else:
             torch.mm(x, lin.w.t(), out=y)
+
+    def _gemm_workspace(self, M, N, K):
+        """The split-K workspace of the projections that do not fill the CUs unsplit (None where a shape does not
+        split); one buffer for the model, grown to the largest need seen."""
+        need = self.K.gemm_workspace_bytes(M, N, K, self.cfg.group)
+        if need == 0:
+            return None
+        if getattr(self, "_gws", None) is None or self._gws.numel() < need:
+            self._gws = torch.empty(need, dtype=torch.uint8, device=self.cfg.device)
+        return self._gws
 
     def _gate_up_pairs(self, lin):
         """Interleaved (gate_i, up_i) rows for the GEMM's SwiGLU epilogue: the Linear's own storage when the decode

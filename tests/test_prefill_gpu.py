@@ -50,6 +50,59 @@ def test_gemm_matches_oracle(K, M, N, Kd, G):
     assert_close(y, ref, 5e-3, f"gemm {M}x{N}x{Kd} G{G}")
 
 
+# split-K (a workspace, shapes with fewer than 160 tiles of 256 x 64 and at least 16 k chunks per split): S = 2 at
+# Llama-3 o, S = 4 at Llama-3 down, S = 4 with uneven chunk ranges (109 chunks) and ragged M and N, S = 4 at G 256
+# with M = 100 (its second token tile shifted inward)
+@pytest.mark.parametrize("M,N,Kd,G,S", [(512, 4096, 4096, 128, 2), (512, 4096, 14336, 128, 4),
+                                        (300, 4100, 13952, 64, 4), (100, 14000, 8192, 256, 4)])
+def test_gemm_splitk_matches_oracle(K, M, N, Kd, G, S):
+    assert K.gemm_workspace_bytes(M, N, Kd, G) == S * M * N * 4
+    packed, sz = _weights(K, N, Kd, G, seed=M + N + 1)
+    wref = dequant_from_gpu(packed, sz, G)
+    x = torch.randn(M, Kd, generator=gen(M * 5 + Kd)).half()
+    ref = (x.float() @ wref.float().t())
+    ws = torch.full((S * M * N * 4 + 64,), 0xFF, dtype=torch.uint8, device=DEV)   # NaN-filled: every slot is written
+    y = torch.full((M, N), 7.0, dtype=torch.half, device=DEV)
+    K.gemm_w4a16(packed, sz, x.to(DEV), y, G, workspace=ws)
+    assert_close(y, ref, 5e-3, f"split-K gemm {M}x{N}x{Kd} G{G} S{S}")
+    y2 = torch.empty_like(y)
+    K.gemm_w4a16(packed, sz, x.to(DEV), y2, G, workspace=ws)
+    assert torch.equal(y, y2)                           # deterministic: the partials are summed in split order
+    y3 = torch.empty_like(y)
+    K.gemm_w4a16(packed, sz, x.to(DEV), y3, G)          # without a workspace: the unsplit kernel, same tolerance
+    assert_close(y3, ref, 5e-3, "unsplit")
+
+
+def test_gemm_short_k_does_not_split(K):
+    """Shapes whose splits would hold fewer than 16 k chunks run unsplit even with a workspace (TinyLlama's
+    projections): no workspace is asked for, and passing one changes nothing, bit for bit."""
+    M, N, Kd, G = 512, 2560, 2048, 128
+    assert K.gemm_workspace_bytes(M, N, Kd, G) == 0
+    packed, sz = _weights(K, N, Kd, G, seed=5)
+    x = torch.randn(M, Kd, generator=gen(6)).half().to(DEV)
+    y1, y2 = (torch.empty(M, N, dtype=torch.half, device=DEV) for _ in range(2))
+    K.gemm_w4a16(packed, sz, x, y1, G)
+    K.gemm_w4a16(packed, sz, x, y2, G, workspace=torch.empty(1 << 20, dtype=torch.uint8, device=DEV))
+    assert torch.equal(y1, y2)
+
+
+def test_gemm_splitk_one_hot_rows_exact(K):
+    """One-hot rows through the split-K path: each row's single product lands in one split's partial, the others add
+    exact zeros, so row i of Y is column k_i of the dequantized weight bit for bit."""
+    M, N, Kd, G = 64, 24576, 4096, 64
+    assert K.gemm_workspace_bytes(M, N, Kd, G) == 2 * M * N * 4
+    packed, sz = _weights(K, N, Kd, G, seed=21)
+    wref = dequant_from_gpu(packed, sz, G)
+    ks = [0, 1, 127, 128, 511, 512, 1000, 1535, 2047] + [700] * (M - 9)
+    x = torch.zeros(M, Kd, dtype=torch.half)
+    for i, k in enumerate(ks):
+        x[i, k] = 1.0
+    ws = torch.empty(K.gemm_workspace_bytes(M, N, Kd, G), dtype=torch.uint8, device=DEV)
+    y = torch.empty(M, N, dtype=torch.half, device=DEV)
+    K.gemm_w4a16(packed, sz, x.to(DEV), y, G, workspace=ws)
+    assert torch.equal(y.cpu(), wref[:, ks].t().contiguous())
+
+
 @pytest.mark.parametrize("N", [200, 49152])
 def test_gemm_one_hot_rows_exact(K, N):
     """Row i of X is one-hot at k_i, so row i of Y is column k_i of the dequantized weight, bit for bit (N 49152 runs
