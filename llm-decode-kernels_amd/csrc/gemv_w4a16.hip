@@ -350,10 +350,13 @@ __device__ __forceinline__ void tile_input_finish(const GemvInput& in, const voi
       }
     }
     ss = wave_sum_all(live ? ss : 0.f);
-    if ((threadIdx.x & 63) == 0) s_ss[wave] = ss;
-    __syncthreads();
-    float tot = 0.f;
-    for (int i = 0; i < nw; ++i) tot += s_ss[gw0 + i];
+    float tot = ss;
+    if (nw > 1) {  // uniform: the row group's waves meet in LDS (a one-wave group has its total already)
+      if ((threadIdx.x & 63) == 0) s_ss[wave] = ss;
+      __syncthreads();
+      tot = 0.f;
+      for (int i = 0; i < nw; ++i) tot += s_ss[gw0 + i];
+    }
     const float r = 1.0f / sqrtf(tot / (float)K + in.eps);
     if (writer && in.x_out != nullptr && live) {
       u32x4* Xo = reinterpret_cast<u32x4*>(in.x_out);
@@ -567,7 +570,15 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
       for (int r = 0; r < T; ++r) red[wave][t * T + r] = v[r];
     }
   }
-  __syncthreads();
+  // the rows are finished by the row group's threads from LDS: across its waves a workgroup barrier; within a one-wave
+  // group the wave's own LDS writes, ordered before its reads by a wavefront-scope fence (the other row groups of the
+  // workgroup need not be waited for)
+  if (nw > 1) {
+    __syncthreads();
+  } else {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  }
   if constexpr (EPI == kOutRows) {
     if (tid < T * NT && base + tid < N) {
       float acc = 0.f;
