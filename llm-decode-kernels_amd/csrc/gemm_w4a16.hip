@@ -377,8 +377,8 @@ gemm_w4a16_wide(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Register-stationary weights (K % 128 == 0, G >= 64, grids of a few hundred tiles): every wave owns 64 weight rows
-// of the tile (two 32-row MFMA tiles) and all of its BM tokens. The weights go from HBM straight into registers --
+// Register-stationary weights (K % 128 == 0, G >= 64, grids of a few hundred tiles): every wave owns RW = 64 or 32
+// weight rows of the tile (two or one 32-row MFMA tiles) and all of its BM tokens. The weights go from HBM straight into registers --
 // lane l = 32 h + r of row tile i loads words 8h .. 8h+7 of row 32 i + r in the 128-wide k chunk (two 16-byte
 // loads) -- and are dequantized there, already in the MFMA A layout: no weight passes through LDS and each is
 // dequantized once. Only the token tile X [BM x 128] is staged in LDS (rows of 256 bytes, 16-byte chunk q of row t at
@@ -397,7 +397,7 @@ gemm_w4a16_wide(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int
 // through buffer loads (SGPR base and chunk offset, a constant VGPR offset per row), so moving to the next chunk costs
 // no vector instruction; the host checks that every offset fits 31 bits. Two workgroups share a CU (accumulators and
 // operands in the 256 architectural VGPRs of a wave).
-constexpr int kRsK = 128, kRsRows = 64, kRsThreads = 256;
+constexpr int kRsK = 128, kRsThreads = 256;
 #ifndef RS_AHEAD
 #define RS_AHEAD 3
 #endif
@@ -418,11 +418,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* p, uint3
 
 // EPI 2 (split-K): the grid covers tiles x `splits` work items; item (tile, s) takes the k chunks [s nk / S,
 // (s + 1) nk / S) and writes its fp32 partial sums to Y = ws [S][M][N] (float), for gemm_splitk_reduce.
-template <int BM, int EPI>
+template <int RW, int BM, int EPI>
 __global__ void __launch_bounds__(kRsThreads, 2)
 gemm_w4a16_rs(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int M, int N, int K, int gsh,
               int tiles_m, int tiles, int splits) {
-  constexpr int TI = kRsRows / 32, TJ = BM / 32, KS = kRsK / 16;
+  constexpr int TI = RW / 32, TJ = BM / 32, KS = kRsK / 16;
   constexpr int XL = BM * 16 / kRsThreads;  // 16-byte X loads per thread per chunk
   __shared__ u32x4 Xs[2][BM][16];
   const int per = gridDim.x / kXcds;
@@ -432,7 +432,7 @@ gemm_w4a16_rs(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int M
   const int t = item % tiles, split = item / tiles;
   // a ragged last tile is shifted inward (the launcher requires M >= BM and N >= 256), so every row a lane loads is
   // valid; the rows it shares with its neighbour tile are computed by both, bit for bit alike, and stored twice
-  const int m0 = min((t % tiles_m) * BM, M - BM), n0 = min((t / tiles_m) * (4 * kRsRows), N - 4 * kRsRows);
+  const int m0 = min((t % tiles_m) * BM, M - BM), n0 = min((t / tiles_m) * (4 * RW), N - 4 * RW);
   const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 31, h = lane >> 5;
   const int KW = K >> 3, NG = K >> gsh, nk_all = K / kRsK;
@@ -442,7 +442,7 @@ gemm_w4a16_rs(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int M
   const __amdgpu_buffer_rsrc_t xres = buffer_of(X, (uint32_t)M * (uint32_t)K * 2u);
   // one VGPR offset per operand; the row tile (W, scales) and row block (X) go into the SGPR offset. The lane's scale
   // is that of its first k, k0 + 64 h, whose group holds all 64 of its k (G >= 64).
-  const uint32_t row = (uint32_t)(n0 + wave * kRsRows + r);
+  const uint32_t row = (uint32_t)(n0 + wave * RW + r);
   const uint32_t wo = row * (uint32_t)KW * 4u + 32u * (uint32_t)h;
   const uint32_t so = (row * (uint32_t)NG + (uint32_t)((64 * h) >> gsh)) * 4u;
   // X staging: chunk xq of rows xr + 16 v, stored at chunk xq ^ xr of the row (xr = (xr + 16 v) & 15)
@@ -587,7 +587,7 @@ gemm_w4a16_rs(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int M
     for (int i = 0; i < TI; ++i) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wave * kRsRows + 32 * i + 8 * q + 4 * h;
+        const int n = n0 + wave * RW + 32 * i + 8 * q + 4 * h;
         if (n >= N) continue;
         if constexpr (EPI == 2) {  // fp32 partials, N % 4 == 0 (checked by the launcher)
           float* dst = reinterpret_cast<float*>(Y) + ((size_t)split * M + m) * N + n;
@@ -646,26 +646,26 @@ gemm_splitk_reduce(const float* __restrict__ ws, int splits, f16* __restrict__ Y
   reinterpret_cast<u32x2*>(Y)[i] = o;
 }
 
-// requires M >= BM and N >= 256 (the last tile in each direction is shifted inward); splits > 1: epilogue 0, N % 4
+// requires M >= BM and N >= 4 RW (the last tile in each direction is shifted inward); splits > 1: epilogue 0, N % 4
 // == 0 and a workspace of splits * M * N floats (the partials), reduced by a second launch
-template <int BM>
+template <int RW, int BM>
 void launch_rs(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int log2G,
                int epilogue, int splits, void* ws, hipStream_t st) {
-  const int tiles_m = (M + BM - 1) / BM, tiles = tiles_m * ((N + 4 * kRsRows - 1) / (4 * kRsRows));
+  const int tiles_m = (M + BM - 1) / BM, tiles = tiles_m * ((N + 4 * RW - 1) / (4 * RW));
   const dim3 grid((tiles * splits + kXcds - 1) / kXcds * kXcds);
   const uint32_t* P = (const uint32_t*)packed;
   const uint32_t* S = (const uint32_t*)sz;
   if (splits > 1) {
-    hipLaunchKernelGGL((gemm_w4a16_rs<BM, 2>), grid, dim3(kRsThreads), 0, st, P, S, (const f16*)x, (f16*)ws, M, N,
+    hipLaunchKernelGGL((gemm_w4a16_rs<RW, BM, 2>), grid, dim3(kRsThreads), 0, st, P, S, (const f16*)x, (f16*)ws, M, N,
                        K, log2G, tiles_m, tiles, splits);
     const int mn4 = M * (N / 4);
     hipLaunchKernelGGL(gemm_splitk_reduce, dim3((mn4 + 255) / 256), dim3(256), 0, st, (const float*)ws, splits,
                        (f16*)y, mn4);
   } else if (epilogue == 1) {
-    hipLaunchKernelGGL((gemm_w4a16_rs<BM, 1>), grid, dim3(kRsThreads), 0, st, P, S, (const f16*)x, (f16*)y, M, N, K,
+    hipLaunchKernelGGL((gemm_w4a16_rs<RW, BM, 1>), grid, dim3(kRsThreads), 0, st, P, S, (const f16*)x, (f16*)y, M, N, K,
                        log2G, tiles_m, tiles, 1);
   } else {
-    hipLaunchKernelGGL((gemm_w4a16_rs<BM, 0>), grid, dim3(kRsThreads), 0, st, P, S, (const f16*)x, (f16*)y, M, N, K,
+    hipLaunchKernelGGL((gemm_w4a16_rs<RW, BM, 0>), grid, dim3(kRsThreads), 0, st, P, S, (const f16*)x, (f16*)y, M, N, K,
                        log2G, tiles_m, tiles, 1);
   }
 }
@@ -691,9 +691,12 @@ void launch_wide(const void* packed, const void* sz, const void* x, void* y, int
 
 }  // namespace
 
-// Tile choice: the register-stationary kernel (K % 128 == 0, G >= 64, N >= 256) with 256 weight rows x 128 tokens
-// when M >= 128 and that gives at least 320 tiles (two workgroups per CU: 512 slots), else x 64 tokens when M >= 64
-// and that gives at least 160 (returns 42 and 41). Otherwise the wide kernel: the largest of 128 x 128, 128 x 64, 64 x 64 whose grid still covers the 256
+// Tile choice: the register-stationary kernel (K % 128 == 0, G >= 64) in the first of these that gives its number
+// of tiles (two workgroups per CU: 512 slots): 256 weight rows x 128 tokens, 320 tiles (returns 42); 128 x 128, 320
+// (52); 256 x 64, 160 (41); 128 x 64, 160 (51). The 128-row tiles (32 rows per wave) give the narrower shapes their
+// tiles (TinyLlama qkv 2560 x 2048 at M 512: 14.0 against 17.3 us on the wide kernel; gate|up 11264 x 2048: 37.1
+// against 40.3 at 256 x 64); below 160 they lose to the wide kernel (TinyLlama o and down: 13.8 against 11.4 and
+// 34.2 against 31.3 us at 128 tiles). Otherwise the wide kernel: the largest of 128 x 128, 128 x 64, 64 x 64 whose grid still covers the 256
 // CUs, then K groups (KG = 2 or 4 four-wave groups per workgroup; 2 at most for 128 x 64, by LDS) while the grid leaves
 // CUs with a single workgroup (returns 10 * tile + KG, tile 3: 128 x 128, 2: 128 x 64, 1: 64 x 64); K % 64 != 0 takes
 // the 64 x 64 16x16x16 kernel above (returns 0).
@@ -716,7 +719,7 @@ int gemm_w4a16_splits(int M, int N, int K, int log2G, int epilogue) {
   if (!DK_GEMM_RS || epilogue != 0 || K % kRsK != 0 || log2G < 6 || M < 64 || N < 256 || N % 4 != 0 ||
       (long long)N * K > 0x7fffffffLL || (long long)M * K > 0x3fffffffLL)
     return 1;
-  const long long t64 = (long long)((N + 4 * kRsRows - 1) / (4 * kRsRows)) * ((M + 63) / 64);
+  const long long t64 = (long long)((N + 255) / 256) * ((M + 63) / 64);
   if (t64 >= 160) return 1;
   const int nk = K / kRsK;
   int s = 2;
@@ -734,9 +737,12 @@ int gemm_w4a16_tile(int M, int N, int K, int log2G) {
   if (K % kWK != 0) return 0;
   if (DK_GEMM_RS && K % kRsK == 0 && log2G >= 6 && (long long)N * K <= 0x7fffffffLL &&
       (long long)M * K <= 0x3fffffffLL) {
-    const long long n_t = (N + 4 * kRsRows - 1) / (4 * kRsRows);
-    if (M >= 128 && N >= 256 && n_t * ((M + 127) / 128) >= 320) return 40 + 2;
-    if (M >= 64 && N >= 256 && n_t * ((M + 63) / 64) >= 160) return 40 + 1;
+    // weight tiles of 256 (64 rows per wave) and 128 (32 rows per wave), token tiles of 128 and 64
+    const long long n_t = (N + 255) / 256, n_t32 = (N + 127) / 128, tm128 = (M + 127) / 128, tm64 = (M + 63) / 64;
+    if (M >= 128 && N >= 256 && n_t * tm128 >= 320) return 42;
+    if (M >= 128 && N >= 128 && n_t32 * tm128 >= 320) return 52;
+    if (M >= 64 && N >= 256 && n_t * tm64 >= 160) return 41;
+    if (M >= 64 && N >= 128 && n_t32 * tm64 >= 160) return 51;
   }
   const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128);
   const long long t64m = (long long)((M + 63) / 64) * ((N + 127) / 128);
@@ -761,11 +767,13 @@ void launch_gemm_w4a16(const void* packed, const void* sz, const void* x, void* 
                        int epilogue, void* ws, hipStream_t st) {
   if (ws != nullptr) {
     const int splits = gemm_w4a16_splits(M, N, K, log2G, epilogue);
-    if (splits > 1) return launch_rs<64>(packed, sz, x, y, M, N, K, log2G, 0, splits, ws, st);
+    if (splits > 1) return launch_rs<64, 64>(packed, sz, x, y, M, N, K, log2G, 0, splits, ws, st);
   }
   switch (gemm_w4a16_tile(M, N, K, log2G)) {
-    case 42: launch_rs<128>(packed, sz, x, y, M, N, K, log2G, epilogue, 1, nullptr, st); return;
-    case 41: launch_rs<64>(packed, sz, x, y, M, N, K, log2G, epilogue, 1, nullptr, st); return;
+    case 42: launch_rs<64, 128>(packed, sz, x, y, M, N, K, log2G, epilogue, 1, nullptr, st); return;
+    case 41: launch_rs<64, 64>(packed, sz, x, y, M, N, K, log2G, epilogue, 1, nullptr, st); return;
+    case 52: launch_rs<32, 128>(packed, sz, x, y, M, N, K, log2G, epilogue, 1, nullptr, st); return;
+    case 51: launch_rs<32, 64>(packed, sz, x, y, M, N, K, log2G, epilogue, 1, nullptr, st); return;
     case 31: launch_wide<128, 128, 1>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
     case 21: launch_wide<128, 64, 1>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;
     case 22: launch_wide<128, 64, 2>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;

@@ -28,17 +28,21 @@ def _weights(K, N, Kd, G, seed):
     return packed, sz
 
 
-# kernel coverage: K % 128 == 0, G >= 64 and at least 320 tiles of 256 weight rows x 128 tokens -> the
-# register-stationary kernel with 128-token tiles (the last four cases: G 64, 128 and 256, ragged M and N, an odd
-# chunk count), at least 160 tiles of 256 x 64 -> the same with 64-token tiles ((512, 11264) and the ragged
-# (200, 12302) at G 64); otherwise K % 64 == 0 -> the wide kernel, tiles 128 x 128, 128 x 64, 64 x 64 and 1, 2 or 4
-# K groups by grid size; K % 64 == 32 -> the 16x16x16 kernel; N % 4 != 0 -> the element-wise epilogue stores
+# kernel coverage: K % 128 == 0 and G >= 64 -> the register-stationary kernel when a tiling has enough tiles:
+# 256 weight rows x 128 tokens (the last four cases: G 64, 128 and 256, ragged M and N, an odd chunk count),
+# 128 x 128 ((512, 11264), ragged (300, 20000), (260, 19998) with N % 4 != 0 and 3 chunks), 256 x 64 (the ragged
+# (200, 12302) at G 64), 128 x 64 ((512, 2560), ragged (130, 10002)); otherwise K % 64 == 0 -> the wide kernel, tiles
+# 128 x 128, 128 x 64, 64 x 64 and 1, 2 or 4 K groups by grid size (G 32 keeps (512, 4096, 1024) on 128 x 64 with 2
+# groups and (200, 4100, 512) on 64 x 64 with 2); K % 64 == 32 -> the 16x16x16 kernel; N % 4 != 0 -> the element-wise
+# epilogue stores
 @pytest.mark.parametrize("M,N,Kd,G", [(1, 64, 256, 128), (7, 2560, 2048, 128), (64, 2048, 2048, 64),
                                       (100, 1000, 5632, 128), (512, 11264, 2048, 128), (33, 4096, 4096, 32),
                                       (512, 4096, 1024, 128), (70, 999, 256, 128), (40, 300, 320, 64),
                                       (300, 4100, 448, 64), (512, 8192, 192, 64), (20, 100, 96, 32),
                                       (500, 16400, 192, 64), (256, 65536, 256, 64), (512, 16384, 256, 32),
-                                      (400, 8000, 256, 32), (200, 12302, 640, 64),
+                                      (400, 8000, 256, 32), (200, 12302, 640, 64), (300, 20000, 256, 64),
+                                      (260, 19998, 384, 128), (512, 2560, 2048, 128), (130, 10002, 512, 64),
+                                      (512, 4096, 1024, 32), (200, 4100, 512, 32),
                                       (300, 49002, 384, 128), (130, 98304, 512, 256), (512, 28672, 1024, 128)])
 def test_gemm_matches_oracle(K, M, N, Kd, G):
     packed, sz = _weights(K, N, Kd, G, seed=M + N)
@@ -110,7 +114,7 @@ def test_gemm_one_hot_rows_exact(K, N):
     Kd, G = 512, 64
     packed, sz = _weights(K, N, Kd, G, seed=9)
     wref = dequant_from_gpu(packed, sz, G)
-    ks = [0, 1, 7, 8, 31, 32, 127, 128, 300, 511]
+    ks = [0, 1, 7, 8, 31, 32, 127, 128, 300, 511] * 6 + [64, 65, 255, 256]   # 64 rows (the kernel's token tile)
     x = torch.zeros(len(ks), Kd, dtype=torch.half)
     for i, k in enumerate(ks):
         x[i, k] = 1.0
@@ -119,8 +123,10 @@ def test_gemm_one_hot_rows_exact(K, N):
     assert torch.equal(y.cpu(), wref[:, ks].t().contiguous())
 
 
+# register-stationary tilings of the SwiGLU epilogue: 128 x 128 at (512, 8192), 256 x 128 at (260, 14000), 256 x 64
+# at (64, 20500), 128 x 64 at (64, 10240)
 @pytest.mark.parametrize("M,I,Kd", [(16, 5632, 2048), (130, 512, 256), (1, 64, 1024), (9, 513, 320), (33, 70, 96),
-                                    (512, 8192, 256), (260, 14000, 640)])
+                                    (512, 8192, 256), (260, 14000, 640), (64, 20500, 256), (64, 10240, 256)])
 def test_gemm_swiglu_epilogue(K, M, I, Kd):
     from runtime.model import interleave_halves
     G = 128 if Kd % 128 == 0 else (64 if Kd % 64 == 0 else 32)
