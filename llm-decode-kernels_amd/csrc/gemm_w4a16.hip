@@ -706,44 +706,60 @@ void launch_wide(const void* packed, const void* sz, const void* x, void* y, int
 #ifndef DK_GEMM_RS
 #define DK_GEMM_RS 1
 #endif
-// Split-K for grids the register-stationary kernel cannot fill (fewer than 160 tiles of 256 x 64): the smallest
-// power-of-two split S in 2..16 whose S x tiles reaches 384 workgroups while every split keeps at least
-// RS_SPLIT_MIN_CHUNKS of the 128-wide k chunks, and only if S x tiles reaches 192; 1 when the shape does not qualify
-// (epilogue 0, K % 128 == 0, G >= 64, M >= 64, N >= 256, N % 4 == 0, offsets within 31 bits) or already fills the
-// CUs unsplit. Short splits lose: the partials' traffic (S x M x N x 4 bytes, written and read back) and the reduce
-// launch outweigh the fuller grid (TinyLlama qkv 2560 x 2048 at S 4, 4 chunks per split: 27 against 19 us unsplit).
-#ifndef RS_SPLIT_MIN_CHUNKS
-#define RS_SPLIT_MIN_CHUNKS 16
-#endif
-int gemm_w4a16_splits(int M, int N, int K, int log2G, int epilogue) {
+// Split-K (a workspace given, epilogue 0, K % 128 == 0, G >= 64, M >= 64, N >= 256, N % 4 == 0, offsets within 31
+// bits): taken when no unsplit register-stationary tiling has its tiles (gemm_w4a16_rs_tile) or K is long (64 chunks
+// of 128 or more: Llama-3-8B down 4096 x 14336 at M 512 takes 82 us split 4 ways against 92 unsplit on 128-row
+// tiles, while its o 4096 x 4096 takes 28.5 unsplit against 31.6 split). Over 64-token tiles of 256 weight rows, else
+// 128: the smallest power-of-two split S in 2..16 whose S x tiles reaches 384 workgroups while every split keeps at
+// least 16 of the 128-wide chunks, and only if S x tiles reaches 192. Shorter splits lose: the partials' traffic
+// (S x M x N x 4 bytes, written and read back) and the reduce launch outweigh the fuller grid (TinyLlama qkv
+// 2560 x 2048 at S 4, 4 chunks per split: 27 against 19 us). Returns S (1: no split) and the rows per wave in *rw.
+constexpr int kSplitMinChunks = 16;
+int gemm_w4a16_rs_tile(int M, int N, int K, int log2G);
+
+int gemm_w4a16_splits(int M, int N, int K, int log2G, int epilogue, int* rw) {
+  *rw = 64;
   if (!DK_GEMM_RS || epilogue != 0 || K % kRsK != 0 || log2G < 6 || M < 64 || N < 256 || N % 4 != 0 ||
       (long long)N * K > 0x7fffffffLL || (long long)M * K > 0x3fffffffLL)
     return 1;
-  const long long t64 = (long long)((N + 255) / 256) * ((M + 63) / 64);
-  if (t64 >= 160) return 1;
   const int nk = K / kRsK;
-  int s = 2;
-  while (s < 16 && t64 * s < 384 && nk / (2 * s) >= RS_SPLIT_MIN_CHUNKS) s *= 2;
-  if (nk / s < RS_SPLIT_MIN_CHUNKS || t64 * s < 192) return 1;
-  return s;
+  if (nk < 64 && gemm_w4a16_rs_tile(M, N, K, log2G) != 0) return 1;
+  const long long tm = (M + 63) / 64;
+  for (int r = 64; r >= 32; r /= 2) {
+    const long long tiles = (N + 4 * r - 1) / (4 * r) * tm;
+    int s = 2;
+    while (s < 16 && tiles * s < 384 && nk / (2 * s) >= kSplitMinChunks) s *= 2;
+    if (nk / s >= kSplitMinChunks && tiles * s >= 192) {
+      *rw = r;
+      return s;
+    }
+  }
+  return 1;
 }
 
 size_t gemm_w4a16_workspace_bytes(int M, int N, int K, int log2G, int epilogue) {
-  const int s = gemm_w4a16_splits(M, N, K, log2G, epilogue);
+  int rw;
+  const int s = gemm_w4a16_splits(M, N, K, log2G, epilogue, &rw);
   return s > 1 ? (size_t)s * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
+// the unsplit register-stationary tiling (see gemm_w4a16_tile), 0 if none has its tiles
+int gemm_w4a16_rs_tile(int M, int N, int K, int log2G) {
+  if (!DK_GEMM_RS || K % kRsK != 0 || log2G < 6 || (long long)N * K > 0x7fffffffLL || (long long)M * K > 0x3fffffffLL)
+    return 0;
+  // weight tiles of 256 (64 rows per wave) and 128 (32 rows per wave), token tiles of 128 and 64
+  const long long n_t = (N + 255) / 256, n_t32 = (N + 127) / 128, tm128 = (M + 127) / 128, tm64 = (M + 63) / 64;
+  if (M >= 128 && N >= 256 && n_t * tm128 >= 320) return 42;
+  if (M >= 128 && N >= 128 && n_t32 * tm128 >= 320) return 52;
+  if (M >= 64 && N >= 256 && n_t * tm64 >= 160) return 41;
+  if (M >= 64 && N >= 128 && n_t32 * tm64 >= 160) return 51;
+  return 0;
 }
 
 int gemm_w4a16_tile(int M, int N, int K, int log2G) {
   if (K % kWK != 0) return 0;
-  if (DK_GEMM_RS && K % kRsK == 0 && log2G >= 6 && (long long)N * K <= 0x7fffffffLL &&
-      (long long)M * K <= 0x3fffffffLL) {
-    // weight tiles of 256 (64 rows per wave) and 128 (32 rows per wave), token tiles of 128 and 64
-    const long long n_t = (N + 255) / 256, n_t32 = (N + 127) / 128, tm128 = (M + 127) / 128, tm64 = (M + 63) / 64;
-    if (M >= 128 && N >= 256 && n_t * tm128 >= 320) return 42;
-    if (M >= 128 && N >= 128 && n_t32 * tm128 >= 320) return 52;
-    if (M >= 64 && N >= 256 && n_t * tm64 >= 160) return 41;
-    if (M >= 64 && N >= 128 && n_t32 * tm64 >= 160) return 51;
-  }
+  const int rs = gemm_w4a16_rs_tile(M, N, K, log2G);
+  if (rs != 0) return rs;
   const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128);
   const long long t64m = (long long)((M + 63) / 64) * ((N + 127) / 128);
   const long long t64 = (long long)((M + 63) / 64) * ((N + 63) / 64);
@@ -766,8 +782,12 @@ int gemm_w4a16_tile(int M, int N, int K, int log2G) {
 void launch_gemm_w4a16(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int log2G,
                        int epilogue, void* ws, hipStream_t st) {
   if (ws != nullptr) {
-    const int splits = gemm_w4a16_splits(M, N, K, log2G, epilogue);
-    if (splits > 1) return launch_rs<64, 64>(packed, sz, x, y, M, N, K, log2G, 0, splits, ws, st);
+    int rw;
+    const int splits = gemm_w4a16_splits(M, N, K, log2G, epilogue, &rw);
+    if (splits > 1) {
+      if (rw == 64) return launch_rs<64, 64>(packed, sz, x, y, M, N, K, log2G, 0, splits, ws, st);
+      return launch_rs<32, 64>(packed, sz, x, y, M, N, K, log2G, 0, splits, ws, st);
+    }
   }
   switch (gemm_w4a16_tile(M, N, K, log2G)) {
     case 42: launch_rs<64, 128>(packed, sz, x, y, M, N, K, log2G, epilogue, 1, nullptr, st); return;

@@ -293,14 +293,15 @@ def test_prefill_validation(lib):
     # split-K workspace: the bytes a shape needs (fp32 partials [S, M, N]; 0 where it does not split), then every
     # workspace check ahead of a launch
     wb = lib.dk_gemm_w4a16_workspace_bytes
-    assert wb(512, 4096, 14336, 128, 0) == 4 * 512 * 4096 * 4 and wb(512, 4096, 4096, 128, 0) == 2 * 512 * 4096 * 4
-    assert wb(512, 2048, 5632, 128, 0) == 0 and wb(512, 2560, 2048, 128, 0) == 0   # splits under 16 chunks: unsplit
+    assert wb(512, 4096, 14336, 128, 0) == 4 * 512 * 4096 * 4 and wb(512, 2048, 5632, 128, 0) == 2 * 512 * 2048 * 4
+    assert wb(512, 4096, 4096, 128, 0) == 0      # an unsplit tiling fills the CUs and K is short: no split
+    assert wb(512, 2560, 2048, 128, 0) == 0 and wb(512, 2048, 2048, 128, 0) == 0   # splits under 16 chunks
     assert wb(512, 4096, 4096, 128, 1) == 0 and wb(512, 28672, 4096, 128, 0) == 0 and wb(512, 4096, 4096, 32, 0) == 0
     assert wb(32, 4096, 4096, 128, 0) == 0 and wb(512, 4096, 4100, 128, 0) == 0 and wb(0, 4096, 4096, 128, 0) == 0
-    need = wb(512, 4096, 4096, 128, 0)
+    need = wb(512, 4096, 14336, 128, 0)
     W = 0x7f0000000000
     ws = lambda **kw: _err(lib, lib.dk_gemm_w4a16_ws(*dict(dict(
-        p=A16, sz=A16, x=A16, y=B16, M=512, N=4096, K=4096, G=128, epi=0, w=W, wbytes=need), **kw).values(), None))
+        p=A16, sz=A16, x=A16, y=B16, M=512, N=4096, K=14336, G=128, epi=0, w=W, wbytes=need), **kw).values(), None))
     assert ws(wbytes=need - 1)[0] == 3 and "needs %d" % need in ws(wbytes=need - 1)[1]
     assert ws(w=W + 8)[0] == 2 and ws(w=B16 - 64)[0] == 4 and ws(w=A16)[0] == 4
     assert ws(K=240)[0] == 3 and ws(x=None)[0] == 1

@@ -54,10 +54,10 @@ def test_gemm_matches_oracle(K, M, N, Kd, G):
     assert_close(y, ref, 5e-3, f"gemm {M}x{N}x{Kd} G{G}")
 
 
-# split-K (a workspace, shapes with fewer than 160 tiles of 256 x 64 and at least 16 k chunks per split): S = 2 at
-# Llama-3 o, S = 4 at Llama-3 down, S = 4 with uneven chunk ranges (109 chunks) and ragged M and N, S = 4 at G 256
-# with M = 100 (its second token tile shifted inward)
-@pytest.mark.parametrize("M,N,Kd,G,S", [(512, 4096, 4096, 128, 2), (512, 4096, 14336, 128, 4),
+# split-K (a workspace; K long or no unsplit register-stationary tiling; at least 16 k chunks per split): S = 4 over
+# 256-row tiles at Llama-3 down, S = 2 over 128-row tiles at TinyLlama down (44 chunks), S = 4 with uneven chunk
+# ranges (109 chunks) and ragged M and N, S = 4 at G 256 with M = 100 (its second token tile shifted inward)
+@pytest.mark.parametrize("M,N,Kd,G,S", [(512, 4096, 14336, 128, 4), (512, 2048, 5632, 128, 2),
                                         (300, 4100, 13952, 64, 4), (100, 14000, 8192, 256, 4)])
 def test_gemm_splitk_matches_oracle(K, M, N, Kd, G, S):
     assert K.gemm_workspace_bytes(M, N, Kd, G) == S * M * N * 4
@@ -93,11 +93,11 @@ def test_gemm_short_k_does_not_split(K):
 def test_gemm_splitk_one_hot_rows_exact(K):
     """One-hot rows through the split-K path: each row's single product lands in one split's partial, the others add
     exact zeros, so row i of Y is column k_i of the dequantized weight bit for bit."""
-    M, N, Kd, G = 64, 24576, 4096, 64
-    assert K.gemm_workspace_bytes(M, N, Kd, G) == 2 * M * N * 4
+    M, N, Kd, G = 64, 8192, 8192, 64                 # split 4 ways over 128-row tiles
+    assert K.gemm_workspace_bytes(M, N, Kd, G) == 4 * M * N * 4
     packed, sz = _weights(K, N, Kd, G, seed=21)
     wref = dequant_from_gpu(packed, sz, G)
-    ks = [0, 1, 127, 128, 511, 512, 1000, 1535, 2047] + [700] * (M - 9)
+    ks = [0, 1, 127, 128, 511, 512, 1000, 1535, 2047, 2048, 4095, 4096, 6143, 6144, 8191] + [700] * (M - 15)
     x = torch.zeros(M, Kd, dtype=torch.half)
     for i, k in enumerate(ks):
         x[i, k] = 1.0
