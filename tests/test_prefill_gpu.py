@@ -7,6 +7,7 @@ import pytest
 import torch
 
 from helpers import DEV, assert_close, dequant_from_gpu, gen, make_cache
+from oracle import quant_ref as Q
 from oracle import ref_ops as R
 
 pytestmark = pytest.mark.gpu
@@ -52,6 +53,43 @@ def test_gemm_matches_oracle(K, M, N, Kd, G):
     y = torch.full((M, N), 7.0, dtype=torch.half, device=DEV)
     K.gemm_w4a16(packed, sz, x.to(DEV), y, G)
     assert_close(y, ref, 5e-3, f"gemm {M}x{N}x{Kd} G{G}")
+
+
+def _grid_weights(N, Kd, G, seed):
+    """Codes and zeros uniform in 0..15 and scales 2^-6 or 2^-5 per group (packed by the oracle): every dequantized
+    weight is a multiple of 2^-6, so with small-integer x every product and every partial sum of the GEMM is exact in
+    fp32 whatever the summation order, and the result is the exact product rounded once to fp16."""
+    rng = np.random.default_rng(seed)
+    q = rng.integers(0, 16, (N, Kd), dtype=np.uint8)
+    zero = rng.integers(0, 16, (N, Kd // G)).astype(np.float16)
+    scale = np.where(rng.random((N, Kd // G)) < 0.5, 2.0 ** -6, 2.0 ** -5).astype(np.float16)
+    packed = torch.from_numpy(Q.pack(q)).to(DEV)
+    sz = torch.from_numpy(Q.pack_scale_zero(scale, zero)).to(DEV)
+    return packed, sz, torch.from_numpy(Q.dequantize(q, scale, zero, G))
+
+
+# one case per kernel and tiling: the K % 64 == 32 kernel; the wide kernel at 64 x 64 with 1, 2 and 4 K groups,
+# 128 x 64 with 1 and 2, 128 x 128; the register-stationary tilings 256 x 128, 128 x 128, 256 x 64, 128 x 64; split-K
+# over 256-row and over 128-row tiles
+@pytest.mark.parametrize("M,N,Kd,G,ws", [(20, 100, 96, 32, False), (40, 300, 320, 64, False),
+                                         (200, 4100, 512, 32, False), (64, 2048, 2048, 64, False),
+                                         (400, 8000, 256, 32, False), (512, 4096, 1024, 32, False),
+                                         (512, 8192, 192, 64, False), (256, 65536, 256, 64, False),
+                                         (300, 20000, 256, 64, False), (200, 12302, 640, 64, False),
+                                         (130, 10002, 512, 64, False), (300, 4100, 13952, 64, True),
+                                         (512, 2048, 5632, 128, True)])
+def test_gemm_exact_on_integer_grid(K, M, N, Kd, G, ws):
+    """Bit-exact against the oracle where the arithmetic is exact (see _grid_weights): pins every index and every
+    term of the reduction, split-K's partials included, independently of the fp32 summation order."""
+    packed, sz, wref = _grid_weights(N, Kd, G, seed=M + N + Kd)
+    x = torch.randint(-3, 4, (M, Kd), generator=gen(M + 1)).half()
+    want = (x.float() @ wref.float().t()).half()        # exact sums (multiples of 2^-6 below 2^18), one rounding
+    y = torch.full((M, N), 7.0, dtype=torch.half, device=DEV)
+    need = K.gemm_workspace_bytes(M, N, Kd, G)
+    assert (need > 0) == ws
+    K.gemm_w4a16(packed, sz, x.to(DEV), y, G,
+                 workspace=torch.empty(need, dtype=torch.uint8, device=DEV) if ws else None)
+    assert torch.equal(y.cpu(), want)
 
 
 # split-K (a workspace; K long or no unsplit register-stationary tiling; at least 16 k chunks per split): S = 4 over
