@@ -40,28 +40,33 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f4 mfma16(h4 a, h4 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
 
-// 8 weights of one packed word -> fp16((q - zero) * scale), in element order, given s2 = (scale, scale) and z2 =
-// (1024 + zero) twice; mlo = vgpr_const(0x000F000F) (one v_and_or_b32 per pair)
-__device__ __forceinline__ u32x4 dequant8_sz(uint32_t word, f16x2 s2, f16x2 z2, uint32_t mlo) {
+// 8 weights of one packed word -> fp16((q - zero) * scale), in element order, given s2 = (scale, scale), zk = (1024 +
+// zero) twice and zs = (64 + zero) twice. Pairs (e0, e1) and (e4, e5) are nibbles 0 and 2 of each 16-bit half: OR-ed
+// into the mantissa of fp16 1024 (step 1) they give 1024 + q; pairs (e2, e3) and (e6, e7) are nibbles 1 and 3, and
+// OR-ed in place into fp16 64 (step 1/16) they give 64 + q, so one shift (by 8) serves all four pairs. Subtracting
+// 1024 + zero or 64 + zero is exact, and the product with the scale rounds the exact (q - zero) * scale once.
+// mlo = vgpr_const(0x000F000F), mhi = vgpr_const(0x00F000F0): one v_and_or_b32 per pair.
+__device__ __forceinline__ u32x4 dequant8_sz(uint32_t word, f16x2 s2, f16x2 zk, f16x2 zs, uint32_t mlo,
+                                             uint32_t mhi) {
   const uint32_t hi = word >> 8;
-  // pairs (e0, e1), (e2, e3), (e4, e5), (e6, e7): nibble i of each 16-bit half
   const uint32_t p0 = (word & mlo) | 0x64006400u;
-  const uint32_t p1 = ((word >> 4) & mlo) | 0x64006400u;
+  const uint32_t p1 = (word & mhi) | 0x54005400u;
   const uint32_t p2 = (hi & mlo) | 0x64006400u;
-  const uint32_t p3 = ((hi >> 4) & mlo) | 0x64006400u;
+  const uint32_t p3 = (hi & mhi) | 0x54005400u;
   u32x4 r;
-  r[0] = as_u32((as_f16x2(p0) - z2) * s2);
-  r[1] = as_u32((as_f16x2(p1) - z2) * s2);
-  r[2] = as_u32((as_f16x2(p2) - z2) * s2);
-  r[3] = as_u32((as_f16x2(p3) - z2) * s2);
+  r[0] = as_u32((as_f16x2(p0) - zk) * s2);
+  r[1] = as_u32((as_f16x2(p1) - zs) * s2);
+  r[2] = as_u32((as_f16x2(p2) - zk) * s2);
+  r[3] = as_u32((as_f16x2(p3) - zs) * s2);
   return r;
 }
 
-// the same from the group's packed (scale, zero) pair (1024 + zero is exact: zero is an integer in [0, 15])
-__device__ __forceinline__ u32x4 dequant8(uint32_t word, uint32_t szw, uint32_t mlo) {
+// the same from the group's packed (scale, zero) pair (1024 + zero and 64 + zero are exact: zero is an integer in
+// [0, 15])
+__device__ __forceinline__ u32x4 dequant8(uint32_t word, uint32_t szw, uint32_t mlo, uint32_t mhi) {
   const f16x2 sz = as_f16x2(szw);
-  const f16 zb = (f16)1024.0f + sz.y;
-  return dequant8_sz(word, f16x2{sz.x, sz.x}, f16x2{zb, zb}, mlo);
+  const f16 zk = (f16)1024.0f + sz.y, zs = (f16)64.0f + sz.y;
+  return dequant8_sz(word, f16x2{sz.x, sz.x}, f16x2{zk, zk}, f16x2{zs, zs}, mlo, mhi);
 }
 
 template <int EPI>
@@ -82,7 +87,7 @@ gemm_w4a16_kernel(const uint32_t* __restrict__ W, const uint32_t* __restrict__ S
   const uint32_t* wrow = W + (size_t)wr * KW + sc;
   const uint32_t* szrow = SZ + (size_t)wr * NG;
 
-  const uint32_t mlo = vgpr_const(0x000F000Fu);
+  const uint32_t mlo = vgpr_const(0x000F000Fu), mhi = vgpr_const(0x00F000F0u);
   auto fetch = [&](int k0, u32x4& xv, uint32_t& wv, uint32_t& sv) {
     xv = *reinterpret_cast<const u32x4*>(xrow + k0);
     wv = __builtin_nontemporal_load(wrow + (k0 >> 3));
@@ -90,7 +95,7 @@ gemm_w4a16_kernel(const uint32_t* __restrict__ W, const uint32_t* __restrict__ S
   };
   auto stage = [&](int buf, const u32x4& xv, uint32_t wv, uint32_t sv) {
     *reinterpret_cast<u32x4*>(&As[buf][sr][8 * sc]) = xv;
-    *reinterpret_cast<u32x4*>(&Bs[buf][sr][8 * sc]) = dequant8(wv, sv, mlo);
+    *reinterpret_cast<u32x4*>(&Bs[buf][sr][8 * sc]) = dequant8(wv, sv, mlo, mhi);
   };
 
   f4 acc[2][2];
@@ -226,7 +231,7 @@ gemm_w4a16_wide(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int
   uint32_t wv[PD][WPT], sv[PD];
   // loads are unconditional (threads past 2 BN re-read a valid row, tail fetches re-read the last chunk): loads
   // behind branches make the compiler wait for every outstanding load before a stage, which defeats the ring
-  const uint32_t mlo = vgpr_const(0x000F000Fu);
+  const uint32_t mlo = vgpr_const(0x000F000Fu), mhi = vgpr_const(0x00F000F0u);
   auto fetch = [&](int kc, int slot) {
     const int k0 = min(kc, nk - 1) * kWK;
 #pragma unroll
@@ -246,7 +251,8 @@ gemm_w4a16_wide(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int
 #pragma unroll
     for (int i = 0; i < XL; ++i) Xs[kg][buf][xr + 32 * i][lds_chunk(xr + 32 * i, xc)] = xv[slot][i];
 #pragma unroll
-    for (int w = 0; w < WPT; ++w) Ws[kg][buf][wr][lds_chunk(wr, WPT * wq + w)] = dequant8(wv[slot][w], sv[slot], mlo);
+    for (int w = 0; w < WPT; ++w)
+      Ws[kg][buf][wr][lds_chunk(wr, WPT * wq + w)] = dequant8(wv[slot][w], sv[slot], mlo, mhi);
   };
 
   f4 acc[TI][TJ];
@@ -487,7 +493,7 @@ gemm_w4a16_rs(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int M
 #pragma unroll
     for (int j = 0; j < TJ; ++j) acc[i][j] = f32x16{};
   }
-  const uint32_t mlo = vgpr_const(0x000F000Fu);
+  const uint32_t mlo = vgpr_const(0x000F000Fu), mhi = vgpr_const(0x00F000F0u);
   // MFMAs of one chunk; `mid` (the next chunk's first X half into LDS, its second half's loads) runs after the
   // MFMAs of the first RS_XSPLIT fragments
   auto compute = [&](int buf, int slot, auto&& mid) {
@@ -498,13 +504,14 @@ gemm_w4a16_rs(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int M
       asm volatile("" : "+v"(wv[slot][i][0]), "+v"(wv[slot][i][1]));
       asm volatile("" : "+v"(sv[slot][i]));
     }
-    f16x2 s2[TI], z2[TI];
+    f16x2 s2[TI], zk[TI], zs[TI];
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
       const f16x2 sz = as_f16x2(sv[slot][i]);
-      const f16 zb = (f16)1024.0f + sz.y;  // 1024 + zero, exact
+      const f16 a = (f16)1024.0f + sz.y, b = (f16)64.0f + sz.y;  // 1024 + zero and 64 + zero, exact
       s2[i] = f16x2{sz.x, sz.x};
-      z2[i] = f16x2{zb, zb};
+      zk[i] = f16x2{a, a};
+      zs[i] = f16x2{b, b};
     }
     // the chunk's KS x TJ token fragments in (k step, token tile) order, each read from LDS RB fragments ahead of
     // its MFMAs so the reads' latency hides behind the MFMAs of the ones before it
@@ -517,7 +524,7 @@ gemm_w4a16_rs(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int M
     auto dequant = [&](int s, h8 (&a)[TI]) {
 #pragma unroll
       for (int i = 0; i < TI; ++i)
-        a[i] = __builtin_bit_cast(h8, dequant8_sz(wv[slot][i][s >> 2][s & 3], s2[i], z2[i], mlo));
+        a[i] = __builtin_bit_cast(h8, dequant8_sz(wv[slot][i][s >> 2][s & 3], s2[i], zk[i], zs[i], mlo, mhi));
     };
 #pragma unroll
     for (int q = 0; q < RB; ++q) b[q] = read_b(q);
