@@ -17,6 +17,21 @@ __device__ __forceinline__ uint32_t as_u32(f16x2 h) { return __builtin_bit_cast(
 // 16-byte load that bypasses cache retention: weights and KV rows are read once per token.
 __device__ __forceinline__ u32x4 load_stream(const u32x4* p) { return __builtin_nontemporal_load(p); }
 
+// Write-through stores (agent-scope relaxed: `sc1`): the issuing XCD's L2 passes the data on to memory at once
+// instead of holding the lines dirty until the write-back at the end of the kernel. They order nothing. Used for
+// outputs of whole 128-byte lines that the next launch reads from every XCD (the attention split partials, the
+// residual written by a norm prologue): 1.3-3 us per TinyLlama token in the decode step. Not for the GEMVs' 2-byte
+// outputs, whose lines are written piecewise by several workgroups: write-through there cost 8.6 us per token.
+__device__ __forceinline__ void store_through(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+// 16 bytes at byte offset `off` of `base` (a raw buffer store with the sc1 cache policy, bit 4 of its aux operand)
+__device__ __forceinline__ void store_through16(void* base, uint32_t off, u32x4 v) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7fffffff, 0x00020000);
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 16);
+}
+
 // A constant moved into a VGPR behind an empty asm, so the optimiser treats it as a per-lane value. Used for the
 // nibble masks of the INT4 dequant: with the mask and the OR constant both literal the compiler emits v_and_b32 +
 // v_or_b32 (a gfx9 VOP3 instruction takes no literal and at most one scalar operand); with the mask in a VGPR it

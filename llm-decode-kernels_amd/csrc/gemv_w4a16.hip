@@ -359,9 +359,8 @@ __device__ __forceinline__ void tile_input_finish(const GemvInput& in, const voi
     }
     const float r = 1.0f / sqrtf(tot / (float)K + in.eps);
     if (writer && in.x_out != nullptr && live) {
-      u32x4* Xo = reinterpret_cast<u32x4*>(in.x_out);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) Xo[4 * uc + k] = xr[k];
+      for (int k = 0; k < 4; ++k) store_through16(in.x_out, (4 * uc + k) * 16, xr[k]);
     }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {

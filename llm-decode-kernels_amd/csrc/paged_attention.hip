@@ -659,13 +659,13 @@ attn_lean_kernel(const int32_t* __restrict__ pos_ptr, const int32_t* __restrict_
     if (nsplit == 1) {
       out[(size_t)head * D + d] = (f16)O;
     } else {
-      o_part[((size_t)head * max_splits + split) * D + d] = O;
+      store_through(o_part + ((size_t)head * max_splits + split) * D + d, O);
     }
   }
   if (nsplit > 1 && tid < HPG) {
     const int head = kvh * HPG + tid;
-    m_part[(size_t)head * max_splits + split] = Mh;
-    l_part[(size_t)head * max_splits + split] = Lh;
+    store_through(m_part + (size_t)head * max_splits + split, Mh);
+    store_through(l_part + (size_t)head * max_splits + split, Lh);
   }
 }
 
