@@ -749,44 +749,59 @@ void launch_attn_hpg(const AttnLaunch& a, hipStream_t st) {
 
 // ---------------------------------------------------------------------------------------------------------------
 // Prefill attention: causal attention of M prompt rows (row m at position pos + m) over the paged cache, which already
-// holds their K / V. A workgroup of four waves owns one kv head and QB = 64 / HPG consecutive rows; each wave's 16
-// MFMA columns are (row, query head) pairs, PW = 16 / HPG rows x HPG heads, so every column does work. The K / V of
-// the tokens [0, last row's position] stream through LDS in 64-token blocks (double-buffered, the next block's loads
-// in flight during the current block's MFMAs) and all four waves read them there.
+// holds their K / V. A workgroup owns one kv head and QB = 64 / HPG consecutive rows, and runs KVS groups of four
+// waves. Wave w of every group has the same 16 MFMA columns, (row, query head) pairs, PW = 16 / HPG rows x HPG heads,
+// so every column does work; group h takes the 64-token blocks b with b % KVS == h. The K / V of the tokens
+// [0, last row's position] stream through LDS in rounds of KVS blocks (double-buffered, the next rounds' loads in
+// flight in registers during the current round's MFMAs), one block per group, read there by the group's four waves.
+// With KVS = 2, two waves share each SIMD and each works through half the blocks: the launcher takes it when the grid
+// leaves CUs with one workgroup or none, where a lone wave per SIMD waits on its own per-block chain (about 430 vector
+// instructions around 48 MFMAs); with more workgroups than CUs the grid fills the SIMDs by itself (KVS = 1).
 // Per 16-token tile the math is the MFMA decode kernel's: S^T = K . Q^T (the accumulator is P's A operand as is), the
 // causal bound of each column applied to its own scores, online softmax once per block, P . V with p as fp16 hi + lo
-// parts and V operands built by byte permutes from 4 token rows. Each column's tokens are taken in the same block
-// order whatever workgroup or batch the row is in, so a row's result does not depend on how the prompt is batched.
-constexpr int kPfWaves = 4, kPfThreads = kPfWaves * kWave, kPfBlock = 64, kPfPages = 2048, kPfRing = 2;
+// parts and V operands built by byte permutes from 4 token rows. The groups' states (running max, sum, accumulator per
+// column) meet in LDS at the end and group 0 merges them in group order. Every column's tokens go to the same group in
+// the same order whatever workgroup or batch its row is in (block b to group b % KVS, from token 0), and a block
+// wholly past a column's bound changes nothing for it, so a row's result does not depend on how the prompt is
+// batched; for a given KVS. The launch's KVS depends on the grid, so the split of a prompt into launches can change it.
+constexpr int kPfGroupWaves = 4, kPfBlock = 64, kPfPages = 2048, kPfRing = 2;
+// Running maximum of a column that has seen no token yet: a finite stand-in for -infinity, so that exp(max_old -
+// max_new) and exp(score - max) never meet -inf - (-inf); exp(-1e30 - x) is 0 for every score x.
+constexpr float kPfNoMax = -1e30f;
 
 // Keeps loads where they are written (no sinking to their first use; see the K / V ring below).
 __device__ __forceinline__ void pf_fence() { asm volatile("" ::: "memory"); }
 
-template <int D, int HPG>
-__global__ void __launch_bounds__(kPfThreads)
+template <int D, int HPG, int KVS>
+__global__ void __launch_bounds__(kPfGroupWaves * kWave * KVS)
 attn_prefill_kernel(const f16* __restrict__ qkv, const int32_t* __restrict__ pos_ptr, const int32_t* __restrict__ bt,
                     int n_bt, const f16* kc, const f16* vc, int n_pages, int log2P, int n_q, int n_kv, int M,
                     int ctx_cap, float scale, f16* __restrict__ out) {
   // (kc, vc without __restrict__: the fences must order their loads)
   using S = MfmaAttnShape<D>;
   constexpr int KD = S::KD, KW = S::KW, QS = S::QS, VD = S::VD;
+  constexpr int NTH = kPfGroupWaves * kWave * KVS;       // threads
   constexpr int PW = 16 / HPG;                           // rows per wave
-  constexpr int QB = kPfWaves * PW;                      // rows per workgroup
+  constexpr int QB = kPfGroupWaves * PW;                 // rows per workgroup
   constexpr int ROW = D + 8;                             // padded LDS row: 16 rows of one K read in distinct banks
   constexpr int CH = D / 8;                              // 16-byte chunks per K / V row
-  constexpr int LPT = kPfBlock * CH / kPfThreads;        // 16-byte K (and V) loads per thread per block
-  constexpr int RPI = kPfThreads / CH;                   // token rows covered per load index
-  __shared__ __align__(16) f16 Ks[2][kPfBlock][ROW];
-  __shared__ __align__(16) f16 Vs[2][kPfBlock][ROW];
+  constexpr int SB = kPfBlock * KVS;                     // tokens per round (one block per group)
+  constexpr int LPT = SB * CH / NTH;                     // 16-byte K (and V) loads per thread per round
+  constexpr int RPI = NTH / CH;                          // token rows covered per load index
+  __shared__ __align__(16) f16 Ks[2][SB][ROW];
+  __shared__ __align__(16) f16 Vs[2][SB][ROW];
   __shared__ int s_pg[kPfPages];
 
   const int kvh = blockIdx.x, qb = blockIdx.y;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave / kPfGroupWaves, gw = wave % kPfGroupWaves;  // group, and the wave's columns within it
   const int col = lane & 15, g = lane >> 4;
   const int P = 1 << log2P;
   const int pos0 = *pos_ptr;
   // this lane's query column: prompt row m, head h; tokens t <= lim are attended
-  const int m = qb * QB + wave * PW + col / HPG;
+  const int mw = qb * QB + gw * PW;                      // the wave's first row
+  const int m = mw + col / HPG;
   const int h = kvh * HPG + col % HPG;
   const bool live = m < M;
   const int lim = live ? min(pos0 + m, ctx_cap - 1) : -1;  // the cap bounds the mask as well as the loads
@@ -795,7 +810,7 @@ attn_prefill_kernel(const f16* __restrict__ qkv, const int32_t* __restrict__ pos
   const int npg = (ctx + P - 1) >> log2P;
   const bool staged = npg <= kPfPages;  // uniform: block-table pages in LDS, else read per token from global
   if (staged)
-    for (int i = tid; i < npg; i += kPfThreads) s_pg[i] = bt[i];
+    for (int i = tid; i < npg; i += NTH) s_pg[i] = bt[i];
   u32x4 qr[KW];
   {
     const f16* qh = qkv + (size_t)(live ? m : 0) * (n_q + 2 * n_kv) * D + (size_t)h * D;
@@ -805,14 +820,14 @@ attn_prefill_kernel(const f16* __restrict__ qkv, const int32_t* __restrict__ pos
   }
   __syncthreads();  // s_pg
 
-  // K / V ring: block b's loads go into register slot b % kPfRing kPfRing blocks before the block is computed and
-  // are staged into LDS buffer b & 1 one block before. Thread: chunk tid % CH of token rows tid / CH + RPI i; tokens
-  // past ctx or without a page read page 0's row (every cache has one) and are zeroed by select.
-  const int nblk = (ctx + kPfBlock - 1) / kPfBlock;
+  // K / V ring: round r's loads go into register slot r % kPfRing kPfRing rounds before the round is computed and are
+  // staged into LDS buffer r & 1 one round before. Thread: chunk tid % CH of token rows tid / CH + RPI i of the round;
+  // tokens past ctx or without a page read page 0's row (every cache has one) and are zeroed by select.
+  const int nrnd = (ctx + SB - 1) / SB;
   u32x4 kk[kPfRing][LPT], vv[kPfRing][LPT];
   bool ok[kPfRing][LPT];
-  auto fetch = [&](int blk, int slot) {
-    const int b0 = min(blk, nblk - 1) * kPfBlock;  // past the end: a re-read of the last block, never staged
+  auto fetch = [&](int rnd, int slot) {
+    const int b0 = min(rnd, nrnd - 1) * SB;  // past the end: a re-read of the last round, never staged
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int t = b0 + tid / CH + RPI * i;
@@ -836,12 +851,14 @@ attn_prefill_kernel(const f16* __restrict__ qkv, const int32_t* __restrict__ pos
     }
   };
 
-  float mrun = -INFINITY, l = 0.f;
+  float mrun = kPfNoMax, l = 0.f;
   f4 acc[VD];
 #pragma unroll
   for (int t = 0; t < VD; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int blk, int buf) {
+  // the group's block of round rnd (tokens t0 .. t0 + 63, LDS rows r0 .. r0 + 63 of buffer buf)
+  auto compute = [&](int t0, int buf) {
+    const int r0 = grp * kPfBlock;
     // ---- scores of the block's four 16-token tiles: sc[tt][v] = score of token 16 tt + 4 g + v for column col
     f4 sc[4];
     float rmax = -INFINITY;
@@ -849,7 +866,8 @@ attn_prefill_kernel(const f16* __restrict__ qkv, const int32_t* __restrict__ pos
     for (int tt = 0; tt < 4; ++tt) {
       u32x4 kr[KW];
 #pragma unroll
-      for (int w = 0; w < KW; ++w) kr[w] = *reinterpret_cast<const u32x4*>(&Ks[buf][16 * tt + col][KD * g + 8 * w]);
+      for (int w = 0; w < KW; ++w)
+        kr[w] = *reinterpret_cast<const u32x4*>(&Ks[buf][r0 + 16 * tt + col][KD * g + 8 * w]);
       f4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int q = 0; q < QS; ++q) {
@@ -859,21 +877,21 @@ attn_prefill_kernel(const f16* __restrict__ qkv, const int32_t* __restrict__ pos
       }
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int t = blk * kPfBlock + 16 * tt + 4 * g + v;
+        const int t = t0 + 16 * tt + 4 * g + v;
         sc[tt][v] = t <= lim ? c[v] * scale : -INFINITY;
         rmax = fmaxf(rmax, sc[tt][v]);
       }
     }
-    // ---- online softmax, once per block
+    // ---- online softmax, once per block (mrun is finite, so is mn: a masked score gives exp(-inf) = 0)
     rmax = rows_max(rmax);
     const float mn = fmaxf(mrun, rmax);
-    const float alpha = (mrun == -INFINITY) ? 0.f : __expf(mrun - mn);
+    const float alpha = __expf(mrun - mn);
     float ps = 0.f;
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const float pv = (sc[tt][v] == -INFINITY) ? 0.f : __expf(sc[tt][v] - mn);
+        const float pv = __expf(sc[tt][v] - mn);
         sc[tt][v] = pv;
         ps += pv;
       }
@@ -899,7 +917,7 @@ attn_prefill_kernel(const f16* __restrict__ qkv, const int32_t* __restrict__ pos
       VRow<VD> vr[4];
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const f16* src = &Vs[buf][16 * tt + 4 * g + v][VD * col];
+        const f16* src = &Vs[buf][r0 + 16 * tt + 4 * g + v][VD * col];
         if constexpr (VD == 4) {
           const u32x2 x = *reinterpret_cast<const u32x2*>(src);
           vr[v].w[0] = x.x;
@@ -922,19 +940,20 @@ attn_prefill_kernel(const f16* __restrict__ qkv, const int32_t* __restrict__ pos
       }
     }
   };
-  // block blk (u = blk % kPfRing, a constant wherever this is called): compute from LDS buffer blk & 1, stage block
-  // blk + 1 from its slot into the other buffer (every wave finished reading it before the last barrier), refill that
-  // slot with block blk + 1 + kPfRing
-  auto step = [&](int blk, int u) {
-    compute(blk, blk & 1);
+  // round rnd (u = rnd % kPfRing, a constant wherever this is called): the group's block from LDS buffer rnd & 1, stage
+  // round rnd + 1 from its slot into the other buffer (every wave finished reading it before the last barrier), refill
+  // that slot with round rnd + 1 + kPfRing. (Branching around the compute of blocks past the wave's rows, or around the
+  // rescale when no maximum moved, measured slower: up to 1.6x at head dim 128.)
+  auto step = [&](int rnd, int u) {
+    compute((rnd * KVS + grp) * kPfBlock, rnd & 1);
     const int ns = (u + 1) % kPfRing;
-    stage((blk + 1) & 1, ns);  // past the end: a stale slot into an unread buffer
+    stage((rnd + 1) & 1, ns);  // past the end: a stale slot into an unread buffer
     pf_fence();
-    fetch(blk + 1 + kPfRing, ns);
+    fetch(rnd + 1 + kPfRing, ns);
     pf_fence();
     __syncthreads();
   };
-  if (nblk > 0) {  // uniform
+  if (nrnd > 0) {  // uniform
 #pragma unroll
     for (int u = 0; u < kPfRing; ++u) {
       fetch(u, u);
@@ -945,25 +964,66 @@ attn_prefill_kernel(const f16* __restrict__ qkv, const int32_t* __restrict__ pos
     fetch(kPfRing, 0);
     pf_fence();
     __syncthreads();
-    // whole groups of kPfRing blocks in the loop, the remainder after it (no exit between a group's blocks, which
+    // whole groups of kPfRing rounds in the loop, the remainder after it (no exit between a group's rounds, which
     // would leave a path where another slot's loads are the newest and the in-order waits drain everything)
-    int b0 = 0;
-    for (; b0 + kPfRing <= nblk; b0 += kPfRing) {
+    int r0 = 0;
+    for (; r0 + kPfRing <= nrnd; r0 += kPfRing) {
 #pragma unroll
-      for (int u = 0; u < kPfRing; ++u) step(b0 + u, u);
+      for (int u = 0; u < kPfRing; ++u) step(r0 + u, u);
     }
 #pragma unroll
     for (int u = 0; u + 1 < kPfRing; ++u)
-      if (b0 + u < nblk) step(b0 + u, u);
+      if (r0 + u < nrnd) step(r0 + u, u);
   }
-  // ---- output: acc[t][v] = O[column 4 g + v][dim VD col + t]; the column's l lives in lane 4 g + v
+  // ---- merge: groups 1 .. KVS - 1 leave max and sum per column and the accumulator per lane in LDS (over the K / V
+  // buffers, which every wave has finished reading at the last barrier); group 0 merges them in group order
+  static_assert(KVS == 1 || (2 * KVS * kPfGroupWaves * 16 + (KVS - 1) * kPfGroupWaves * kWave * 4 * VD) * 4 <=
+                                (int)sizeof(Ks), "merge scratch fits the K buffers");
+  float* s_ml = reinterpret_cast<float*>(&Ks[0][0][0]);          // [2][KVS][waves][16]: max, then sum
+  float* s_acc = s_ml + 2 * KVS * kPfGroupWaves * 16;           // [KVS - 1][waves][lanes][VD][4]
+  if constexpr (KVS > 1) {
+    if (g == 0) {
+      s_ml[(grp * kPfGroupWaves + gw) * 16 + col] = mrun;
+      s_ml[((KVS + grp) * kPfGroupWaves + gw) * 16 + col] = l;
+    }
+    if (grp > 0) {
+      f4* dst = reinterpret_cast<f4*>(s_acc) + (((grp - 1) * kPfGroupWaves + gw) * kWave + lane) * VD;
+#pragma unroll
+      for (int t = 0; t < VD; ++t) dst[t] = acc[t];
+    }
+    __syncthreads();
+    if (grp > 0) return;  // uniform per wave; no barrier follows
+  }
+  // ---- output: acc[t][v] = O[column 4 g + v][dim VD col + t]
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int cc = 4 * g + v;
-    const float lv = __shfl(l, cc, kWave);
-    const int mm = qb * QB + wave * PW + cc / HPG, hh = kvh * HPG + cc % HPG;
+    float inv;
+    if constexpr (KVS == 1) {
+      const float lv = __shfl(l, cc, kWave);  // the column's sum lives in lane 4 g + v
+      inv = lv > 0.f ? 1.0f / lv : 0.f;
+    } else {
+      float mx = kPfNoMax;
+#pragma unroll
+      for (int hh = 0; hh < KVS; ++hh) mx = fmaxf(mx, s_ml[(hh * kPfGroupWaves + gw) * 16 + cc]);
+      float wg[KVS], tot = 0.f;  // group hh's weight exp(m_hh - max) (0 for a group that saw no token)
+#pragma unroll
+      for (int hh = 0; hh < KVS; ++hh) {
+        wg[hh] = __expf(s_ml[(hh * kPfGroupWaves + gw) * 16 + cc] - mx);
+        tot = fmaf(wg[hh], s_ml[((KVS + hh) * kPfGroupWaves + gw) * 16 + cc], tot);
+      }
+      inv = tot > 0.f ? 1.0f / tot : 0.f;
+#pragma unroll
+      for (int t = 0; t < VD; ++t) {
+        float o = wg[0] * acc[t][v];
+#pragma unroll
+        for (int hh = 1; hh < KVS; ++hh)
+          o = fmaf(wg[hh], s_acc[((((hh - 1) * kPfGroupWaves + gw) * kWave + lane) * VD + t) * 4 + v], o);
+        acc[t][v] = o;
+      }
+    }
+    const int mm = mw + cc / HPG, hh = kvh * HPG + cc % HPG;
     if (mm < M) {
-      const float inv = lv > 0.f ? 1.0f / lv : 0.f;
       f16* dst = out + (size_t)mm * n_q * D + (size_t)hh * D + VD * col;
 #pragma unroll
       for (int t = 0; t < VD; ++t) dst[t] = (f16)(acc[t][v] * inv);
@@ -971,16 +1031,27 @@ attn_prefill_kernel(const f16* __restrict__ qkv, const int32_t* __restrict__ pos
   }
 }
 
+// Grids of at most this many workgroups (one round of the 256 CUs) run two wave groups per workgroup (KVS = 2).
+constexpr int kPfSplitGrid = 256;
+
 template <int D>
 void launch_prefill_hpg(const void* qkv, const int32_t* pos, const int32_t* bt, int n_bt, const void* kc,
                         const void* vc, int n_pages, int log2P, int n_q, int n_kv, int M, int max_ctx, void* out,
                         hipStream_t st) {
   const float scale = 1.0f / sqrtf((float)D);
   const int cap = (int)min((long long)max_ctx, (long long)n_bt << log2P);
+#define DK_PREFILL_KVS(H, KVS)                                                                                      \
+  hipLaunchKernelGGL((attn_prefill_kernel<D, H, KVS>), dim3(n_kv, rb), dim3(kPfGroupWaves * kWave * KVS), 0, st,  \
+                     (const f16*)qkv, pos, bt, n_bt, (const f16*)kc, (const f16*)vc, n_pages, log2P, n_q, n_kv, M, cap, \
+                     scale, (f16*)out)
 #define DK_PREFILL(H)                                                                                               \
-  hipLaunchKernelGGL((attn_prefill_kernel<D, H>), dim3(n_kv, (M + kPfWaves * (16 / H) - 1) / (kPfWaves * (16 / H))), \
-                     dim3(kPfThreads), 0, st, (const f16*)qkv, pos, bt, n_bt, (const f16*)kc, (const f16*)vc,       \
-                     n_pages, log2P, n_q, n_kv, M, cap, scale, (f16*)out)
+  {                                                                                                                 \
+    const int rb = (M + kPfGroupWaves * (16 / H) - 1) / (kPfGroupWaves * (16 / H));                                 \
+    if ((long long)n_kv * rb <= kPfSplitGrid)                                                                       \
+      DK_PREFILL_KVS(H, 2);                                                                                         \
+    else                                                                                                            \
+      DK_PREFILL_KVS(H, 1);                                                                                         \
+  }
   switch (n_q / n_kv) {
     case 1: DK_PREFILL(1); break;
     case 2: DK_PREFILL(2); break;
@@ -988,6 +1059,7 @@ void launch_prefill_hpg(const void* qkv, const int32_t* pos, const int32_t* bt, 
     default: DK_PREFILL(8); break;
   }
 #undef DK_PREFILL
+#undef DK_PREFILL_KVS
 }
 
 }  // namespace

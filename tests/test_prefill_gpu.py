@@ -274,10 +274,13 @@ def _prefill_attn(K, qkv, start, kd, vd, btd, n_q, n_kv, max_ctx):
 @pytest.mark.parametrize("D,n_q,n_kv,page,start,M", [(64, 32, 4, 16, 0, 40), (64, 32, 4, 16, 300, 17),
                                                     (128, 32, 8, 16, 0, 64), (128, 8, 8, 32, 1000, 9),
                                                     (64, 16, 8, 16, 0, 1), (64, 4, 4, 16, 4000, 96),
-                                                    (128, 16, 4, 16, 20000, 20), (64, 8, 1, 16, 70, 130)])
+                                                    (128, 16, 4, 16, 20000, 20), (64, 8, 1, 16, 70, 130),
+                                                    (64, 64, 32, 16, 0, 300), (128, 64, 32, 16, 100, 280)])
 def test_attention_prefill(K, D, n_q, n_kv, page, start, M):
     """Every row m (position start + m) against the oracle's attention over tokens [0, start + m] (2e-3; the cache
-    also holds the later rows' tokens, which must not be attended); HPG 1..8, D 64 and 128, contexts past 16K."""
+    also holds the later rows' tokens, which must not be attended); HPG 1..8, D 64 and 128, contexts past 16K; grids
+    of at most 256 workgroups (two wave groups per workgroup, each taking every other block) and, in the last two
+    cases, of more (one group)."""
     ctx_all = start + M
     kc, vc, bt = make_cache(ctx_all, n_kv, page, D=D, seed=D + M + start)
     qkv = torch.randn(M, (n_q + 2 * n_kv) * D, generator=gen(start + M)).half()
@@ -289,15 +292,19 @@ def test_attention_prefill(K, D, n_q, n_kv, page, start, M):
         assert_close(out[m].view(n_q, D), ref, 2e-3, f"row {m} vs oracle")
 
 
-def test_attention_prefill_rows_independent_of_batch(K):
+@pytest.mark.parametrize("D,n_q,n_kv,M,ks", [(64, 32, 4, 77, (1, 30, 64, 76)), (64, 64, 32, 300, (1, 20)),
+                                             (128, 64, 32, 300, (1, 20))])
+def test_attention_prefill_rows_independent_of_batch(K, D, n_q, n_kv, M, ks):
     """A row's result does not depend on which other rows share its launch: the last rows of a prompt computed alone
-    (pos advanced, qkv sliced) are bit-identical to the same rows of the whole prompt."""
-    D, n_q, n_kv, page, M = 64, 32, 4, 16, 77
-    kc, vc, bt = make_cache(M, n_kv, page, D=D, seed=11)
+    (pos advanced, qkv sliced) are bit-identical to the same rows of the whole prompt. Both launches of a case have
+    grids on the same side of 256 workgroups (first case below, the others above), which sets the wave groups per
+    workgroup and with them the order in which a row's blocks are summed."""
+    page = 16
+    kc, vc, bt = make_cache(M, n_kv, page, D=D, seed=11 + D)
     qkv = torch.randn(M, (n_q + 2 * n_kv) * D, generator=gen(12)).half()
     kd, vd, btd = kc.to(DEV), vc.to(DEV), bt.to(DEV)
     full = _prefill_attn(K, qkv, 0, kd, vd, btd, n_q, n_kv, M)
-    for k in (1, 30, 64, 76):
+    for k in ks:
         part = _prefill_attn(K, qkv[k:].contiguous(), k, kd, vd, btd, n_q, n_kv, M)
         assert torch.equal(part, full[k:]), k
 
@@ -371,7 +378,8 @@ def test_prefill_matches_oracle_and_teacher_force(K, D):
 def test_prefill_in_chunks_is_bit_exact(K):
     """Attention rows are computed independently of their batch, and for this model's shapes every chunk size takes
     the same GEMM configuration (64 x 64 tiles, four K groups; the configuration, and with it the fp32 summation order,
-    is chosen per M x N x K): a prompt prefilled in three chunks leaves the same cache and logits as one pass."""
+    is chosen per M x N x K) and the same attention grid class (at most 256 workgroups): a prompt prefilled in three
+    chunks leaves the same cache and logits as one pass."""
     m, _ = _model()
     prompt = _prompt(70, seed=2)
     m.reset(0)
