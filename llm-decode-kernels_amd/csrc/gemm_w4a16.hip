@@ -585,7 +585,67 @@ gemm_w4a16_rs(const uint32_t* W, const uint32_t* SZ, const f16* X, f16* Y, int M
   }
   if (kc < nk) step(kc, 0);
   // ---- epilogue: lane holds Y[token m0 + 32 j + r][n0 + 64 wave + 32 i + 8 q + 4 h + v] in acc[i][j][4 q + v]
-  const bool vec = (N & 3) == 0;
+  // Through LDS when the rows allow 16-byte stores (the X buffers are free: the last step ended at a barrier): a
+  // direct store of this layout puts each lane on its own token row, 32 rows per store instruction, which kept the
+  // memory pipeline busy at the kernel's end; staged, each wave writes its 32-token slices of the tile into its own
+  // quarter of the buffers (16-byte chunks XOR-swizzled by token) and stores whole row segments, 16 bytes per lane.
+  {
+    constexpr int ES = EPI == 2 ? 4 : (EPI == 1 ? 1 : 2);  // output bytes per weight row and token
+    constexpr int RB = RW * ES, CPR = RB / 16;              // a token's bytes in the wave's slice, its 16-byte chunks
+    static_assert(CPR >= 2 && 32 * CPR % 64 == 0 && 4 * 32 * RB <= (int)sizeof(Xs), "staged epilogue fits");
+    const bool co = (reinterpret_cast<uintptr_t>(Y) & 15) == 0 &&  // 16-byte aligned rows (uniform)
+                    (EPI == 2 || (EPI == 0 ? (N & 7) == 0 : (N & 15) == 0));
+    if (co) {
+      uint8_t* reg = reinterpret_cast<uint8_t*>(&Xs[0][0][0]) + wave * 32 * RB;
+      const int nw0 = n0 + wave * RW;
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        const int sw = r & (CPR - 1);
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x16& a = acc[i][j];
+            if constexpr (EPI == 2) {
+              const int c = 8 * i + 2 * q + h;
+              *reinterpret_cast<float4*>(reg + r * RB + ((c ^ sw) << 4)) =
+                  float4{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+            } else if constexpr (EPI == 1) {
+              // rows (n, n + 1), (n + 2, n + 3) are (gate, up) pairs: act columns (32 i + 8 q + 4 h) / 2 + 0, 1
+              const int c = 2 * i + (q >> 1), off = 8 * (q & 1) + 4 * h;
+              const f16 a0 = silu_mul((f16)a[4 * q], (f16)a[4 * q + 1]);
+              const f16 a1 = silu_mul((f16)a[4 * q + 2], (f16)a[4 * q + 3]);
+              *reinterpret_cast<uint32_t*>(reg + r * RB + ((c ^ sw) << 4) + off) = as_u32(f16x2{a0, a1});
+            } else {
+              const int c = 4 * i + q;
+              u32x2 o;
+              o[0] = as_u32(f16x2{(f16)a[4 * q], (f16)a[4 * q + 1]});
+              o[1] = as_u32(f16x2{(f16)a[4 * q + 2], (f16)a[4 * q + 3]});
+              *reinterpret_cast<u32x2*>(reg + r * RB + ((c ^ sw) << 4) + 8 * h) = o;
+            }
+          }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // the wave's own LDS writes, read by other lanes
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int k2 = 0; k2 < 32 * CPR / 64; ++k2) {
+          const int idx = lane + 64 * k2, t = idx / CPR, c = idx % CPR;
+          const u32x4 v = *reinterpret_cast<const u32x4*>(reg + t * RB + ((c ^ (t & (CPR - 1))) << 4));
+          const size_t m = (size_t)(m0 + 32 * j + t);
+          if constexpr (EPI == 2)
+            *reinterpret_cast<u32x4*>(reinterpret_cast<float*>(Y) + ((size_t)split * M + m) * N + nw0 + 4 * c) = v;
+          else if constexpr (EPI == 1)
+            *reinterpret_cast<u32x4*>(Y + m * (N >> 1) + (nw0 >> 1) + 8 * c) = v;
+          else
+            *reinterpret_cast<u32x4*>(Y + m * N + nw0 + 8 * c) = v;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // reads done before the next slice overwrites
+        __builtin_amdgcn_wave_barrier();
+      }
+      return;
+    }
+  }
+  const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(Y) & 7) == 0;
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
     const int m = m0 + 32 * j + r;
