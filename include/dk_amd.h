@@ -164,6 +164,18 @@ int dk_rmsnorm_rows(const void* x_in, const int64_t* rows, int n_src, const void
                     void* out, int M, int H, float eps, void* stream);
 
 /*
+ * dk_rmsnorm_rows without a gather, its delta given as the fp32 split partials dk_gemm_w4a16_ws leaves with epilogue
+ * 2: delta[r] = fp16(sum over s < splits of parts[s * part_stride + r * H + n]), summed in split order as the GEMM's
+ * own reduce launch sums them, so x_out and out are bit for bit those of dk_gemm_w4a16_ws (epilogue 0) followed by
+ * dk_rmsnorm_rows; the reduce launch is folded into this one. part_stride (floats) a multiple of 4, >= H when
+ * splits > 1 (the partials of rows [0, M) of one split are contiguous: M * H for a whole output, larger for a slice
+ * of its rows); splits 1..64; parts 16-byte aligned and overlapping neither x_out nor out; x_out may be x_in. No
+ * counterpart in the reference.
+ */
+int dk_rmsnorm_rows_parts(const void* x_in, const float* parts, int splits, long long part_stride, const void* w,
+                          void* x_out, void* out, int M, int H, float eps, void* stream);
+
+/*
  * Causal paged attention of M prompt rows (prefill): row m (position *pos + m) attends tokens [0, *pos + m] of the
  * cache, which must already hold them (dk_rope_append_rows); q is the first n_q heads of qkv row m, already rotated.
  * out [M, n_q * head_dim] fp16. Tokens at positions >= max_ctx (and past the block table) are neither read nor
@@ -190,7 +202,9 @@ int dk_gemm_w4a16(const void* packed, const void* sz, const void* x, void* y, in
  * the workspace and sum them in a second launch, in split order (the result does not depend on scheduling; its fp32
  * summation order differs from the unsplit kernel's). dk_gemm_w4a16_workspace_bytes returns the bytes a shape needs
  * (0: it does not split; epilogue 1 never splits). workspace NULL runs dk_gemm_w4a16; otherwise it must hold that
- * many bytes, be 16-byte aligned and overlap neither x nor y. Like dk_gemm_w4a16, no counterpart in the reference.
+ * many bytes, be 16-byte aligned and overlap neither x nor y. epilogue 2 (shapes that split only; y unused, may be
+ * NULL): the partials alone, left in the workspace for a reader that sums them (dk_rmsnorm_rows_parts), which saves
+ * the second launch. Like dk_gemm_w4a16, no counterpart in the reference.
  */
 size_t dk_gemm_w4a16_workspace_bytes(int M, int N, int K, int group, int epilogue);
 int dk_gemm_w4a16_ws(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int group,

@@ -271,14 +271,18 @@ size_t dk_gemm_w4a16_workspace_bytes(int M, int N, int K, int group, int epilogu
 
 int dk_gemm_w4a16_ws(const void* packed, const void* sz, const void* x, void* y, int M, int N, int K, int group,
                      int epilogue, void* workspace, size_t workspace_bytes, void* stream) {
-  const int rc = gemm_check(packed, sz, x, y, M, N, K, group, epilogue);
+  const bool parts = epilogue == 2;  // the fp32 split partials alone, left in the workspace (y unused)
+  const int rc = gemm_check(packed, sz, x, parts ? workspace : y, M, N, K, group, parts ? 0 : epilogue);
   if (rc != DK_OK) return rc;
   const size_t need = dk::gemm_w4a16_workspace_bytes(M, N, K, ilog2(group), epilogue);
+  if (parts && need == 0)
+    return fail(DK_ERR_DOMAIN, "gemm_w4a16_ws: epilogue 2 (split partials only) needs a shape that splits "
+                               "(gemm_w4a16_workspace_bytes > 0)");
   if (workspace != nullptr) {
     if (workspace_bytes < need)
       return fail(DK_ERR_SHAPE, "gemm_w4a16_ws: workspace of %zu bytes, this shape needs %zu", workspace_bytes, need);
     if (!aligned16(workspace)) return fail(DK_ERR_ALIGN, "gemm_w4a16_ws: workspace must be 16B aligned");
-    if (need > 0 && ranges_overlap(workspace, need, y, (size_t)M * N * 2))
+    if (!parts && need > 0 && ranges_overlap(workspace, need, y, (size_t)M * N * 2))
       return fail(DK_ERR_DOMAIN, "gemm_w4a16_ws: workspace must not overlap y");
     if (need > 0 && ranges_overlap(workspace, need, x, (size_t)M * K * 2))
       return fail(DK_ERR_DOMAIN, "gemm_w4a16_ws: workspace must not overlap x");
@@ -606,6 +610,27 @@ int dk_rmsnorm_rows(const void* x_in, const int64_t* rows, int n_src, const void
   clear_error();
   dk::launch_rmsnorm_rows(x_in, rows, n_src, delta, w, x_out, out, M, H, eps, (hipStream_t)stream);
   return launched("rmsnorm_rows");
+}
+
+int dk_rmsnorm_rows_parts(const void* x_in, const float* parts, int splits, long long part_stride, const void* w,
+                          void* x_out, void* out, int M, int H, float eps, void* stream) {
+  if (!x_in || !parts || !w || !x_out || !out) return fail(DK_ERR_NULL, "rmsnorm_rows_parts: null pointer argument");
+  if (M < 1 || M > (1 << 24)) return fail(DK_ERR_SHAPE, "rmsnorm_rows_parts: M must be 1..2^24, got %d", M);
+  if (H <= 0 || H % 8 != 0 || H > dk::kRowNormMaxH)
+    return fail(DK_ERR_SHAPE, "rmsnorm_rows_parts: H must be a positive multiple of 8 (<= %d), got %d",
+                dk::kRowNormMaxH, H);
+  if (splits < 1 || splits > 64) return fail(DK_ERR_SHAPE, "rmsnorm_rows_parts: splits must be 1..64, got %d", splits);
+  if (part_stride % 4 != 0 || (splits > 1 && part_stride < (long long)H))
+    return fail(DK_ERR_SHAPE, "rmsnorm_rows_parts: part_stride must be a multiple of 4 and >= H, got %lld", part_stride);
+  if (!aligned16(x_in) || !aligned16(parts) || !aligned16(w) || !aligned16(x_out) || !aligned16(out))
+    return fail(DK_ERR_ALIGN, "rmsnorm_rows_parts: x_in, parts, w, x_out and out must be 16B aligned");
+  if (out == x_in || out == x_out) return fail(DK_ERR_DOMAIN, "rmsnorm_rows_parts: out must not alias x_in or x_out");
+  const size_t pbytes = ((size_t)(splits - 1) * (size_t)part_stride + (size_t)M * H) * sizeof(float);
+  if (ranges_overlap(parts, pbytes, x_out, (size_t)M * H * 2) || ranges_overlap(parts, pbytes, out, (size_t)M * H * 2))
+    return fail(DK_ERR_DOMAIN, "rmsnorm_rows_parts: parts must not overlap x_out or out");
+  clear_error();
+  dk::launch_rmsnorm_rows_parts(x_in, parts, splits, part_stride, w, x_out, out, M, H, eps, (hipStream_t)stream);
+  return launched("rmsnorm_rows_parts");
 }
 
 int dk_attention_prefill(const void* qkv, const int32_t* pos, const int32_t* bt, int n_bt, const void* kc,

@@ -17,10 +17,14 @@ namespace {
 // row), so the weight's latency hides behind the sum and the row is never read back. One wave sum per wave, one LDS
 // exchange. x_out may be x_in itself when there is no gather: a thread writes only chunks it has already read.
 // A gathered row index outside [0, n_src) reads row 0 and poisons the row with NaN instead of reading out of bounds.
-template <int C>
+// PARTS: the delta is the split-K GEMM's fp32 partials, parts[s * pstride + r * H + n] for s < splits, rounded to fp16
+// after summing them in split order exactly as gemm_splitk_reduce does (the GEMM's reduce launch folded in here; loads
+// of up to four splits in flight together).
+template <int C, bool PARTS = false>
 __global__ void __launch_bounds__(1024)
 row_norm_kernel(const f16* x_in, const int64_t* __restrict__ rows, int n_src, const f16* __restrict__ delta,
-                const f16* __restrict__ w, f16* x_out, f16* __restrict__ out, int H, float eps) {
+                const f16* __restrict__ w, f16* x_out, f16* __restrict__ out, int H, float eps,
+                const float* __restrict__ parts, int splits, long long pstride) {
   __shared__ float part[16];
   const int r = blockIdx.x, tid = threadIdx.x, T = blockDim.x, U = H >> 3;
   const long long sr = rows != nullptr ? rows[r] : r;
@@ -31,8 +35,43 @@ row_norm_kernel(const f16* x_in, const int64_t* __restrict__ rows, int n_src, co
   u32x4 xv[C], dv[C], wv[C];
 #pragma unroll
   for (int c = 0; c < C; ++c) xv[c] = src[min(tid + c * T, U - 1)];
+  if constexpr (PARTS) {
+    const float4* pr = reinterpret_cast<const float4*>(parts + (size_t)r * H);
+    float4 lo[C], hi[C];  // running sums of the chunk's 8 values, split 0 first
+    for (int s0 = 0; s0 < splits; s0 += 4) {
+      float4 bl[C][4], bh[C][4];
 #pragma unroll
-  for (int c = 0; c < C; ++c) dv[c] = dl[min(tid + c * T, U - 1)];
+      for (int c = 0; c < C; ++c) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float4* ps = pr + (size_t)min(s0 + k, splits - 1) * (size_t)(pstride >> 2) + 2 * min(tid + c * T, U - 1);
+          bl[c][k] = ps[0];
+          bh[c][k] = ps[1];
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          if (s0 + k >= splits) continue;
+          if (s0 + k == 0) {
+            lo[c] = bl[c][k];
+            hi[c] = bh[c][k];
+          } else {
+            lo[c].x += bl[c][k].x; lo[c].y += bl[c][k].y; lo[c].z += bl[c][k].z; lo[c].w += bl[c][k].w;
+            hi[c].x += bh[c][k].x; hi[c].y += bh[c][k].y; hi[c].z += bh[c][k].z; hi[c].w += bh[c][k].w;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+      dv[c] = u32x4{as_u32(f16x2{(f16)lo[c].x, (f16)lo[c].y}), as_u32(f16x2{(f16)lo[c].z, (f16)lo[c].w}),
+                    as_u32(f16x2{(f16)hi[c].x, (f16)hi[c].y}), as_u32(f16x2{(f16)hi[c].z, (f16)hi[c].w})};
+  } else {
+#pragma unroll
+    for (int c = 0; c < C; ++c) dv[c] = dl[min(tid + c * T, U - 1)];
+  }
 #pragma unroll
   for (int c = 0; c < C; ++c) wv[c] = wc[min(tid + c * T, U - 1)];
   u32x4* xo = reinterpret_cast<u32x4*>(x_out + (size_t)r * H);
@@ -40,7 +79,7 @@ row_norm_kernel(const f16* x_in, const int64_t* __restrict__ rows, int n_src, co
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     const int u = tid + c * T;
-    if (delta != nullptr) {
+    if (PARTS || delta != nullptr) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) xv[c][k] = as_u32(as_f16x2(xv[c][k]) + as_f16x2(dv[c][k]));
     }
@@ -345,7 +384,8 @@ static void launch_row_norm(const void* x_in, const int64_t* rows, int n_src, co
   f16 *xo = (f16*)x_out, *o = (f16*)out;
   auto kernel = C == 1 ? row_norm_kernel<1> : C == 2 ? row_norm_kernel<2> : C == 4 ? row_norm_kernel<4>
                                                                             : row_norm_kernel<8>;
-  hipLaunchKernelGGL(kernel, dim3(M), dim3(T), 0, st, xi, rows, n_src, d, wn, xo, o, H, eps);
+  hipLaunchKernelGGL(kernel, dim3(M), dim3(T), 0, st, xi, rows, n_src, d, wn, xo, o, H, eps, (const float*)nullptr, 0,
+                     0LL);
 }
 
 void launch_add_rmsnorm(void* x, const void* delta, const void* w, void* out, int H, float eps, hipStream_t st) {
@@ -382,6 +422,18 @@ void launch_rope_append(void* qkv, const float* cos_t, const float* sin_t, const
 void launch_rmsnorm_rows(const void* x_in, const int64_t* rows, int n_src, const void* delta, const void* w, void* x_out,
                          void* out, int M, int H, float eps, hipStream_t st) {
   launch_row_norm(x_in, rows, n_src, delta, w, x_out, out, M, H, eps, st);
+}
+
+void launch_rmsnorm_rows_parts(const void* x_in, const float* parts, int splits, long long pstride, const void* w,
+                               void* x_out, void* out, int M, int H, float eps, hipStream_t st) {
+  const int U = H >> 3;
+  int C = 1;
+  while (C < 8 && C * 1024 < U) C *= 2;
+  const int T = min(1024, ((U + C - 1) / C + 63) / 64 * 64);
+  auto kernel = C == 1 ? row_norm_kernel<1, true> : C == 2 ? row_norm_kernel<2, true>
+                : C == 4 ? row_norm_kernel<4, true> : row_norm_kernel<8, true>;
+  hipLaunchKernelGGL(kernel, dim3(M), dim3(T), 0, st, (const f16*)x_in, nullptr, M, nullptr, (const f16*)w,
+                     (f16*)x_out, (f16*)out, H, eps, parts, splits, pstride);
 }
 
 void launch_argmax_advance(const void* logits, int V, int64_t* tok, int32_t* pos, hipStream_t st) {

@@ -725,6 +725,7 @@ void launch_rs(const void* packed, const void* sz, const void* x, void* y, int M
   if (splits > 1) {
     hipLaunchKernelGGL((gemm_w4a16_rs<RW, BM, 2>), grid, dim3(kRsThreads), 0, st, P, S, (const f16*)x, (f16*)ws, M, N,
                        K, log2G, tiles_m, tiles, splits);
+    if (epilogue == 2) return;  // the partials are the output (their reader sums them)
     const int mn4 = M * (N / 4);
     hipLaunchKernelGGL(gemm_splitk_reduce, dim3((mn4 + 255) / 256), dim3(256), 0, st, (const float*)ws, splits,
                        (f16*)y, mn4);
@@ -773,7 +774,7 @@ void launch_wide(const void* packed, const void* sz, const void* x, void* y, int
 #ifndef DK_GEMM_RS
 #define DK_GEMM_RS 1
 #endif
-// Split-K (a workspace given, epilogue 0, K % 128 == 0, G >= 64, M >= 64, N >= 256, N % 4 == 0, offsets within 31
+// Split-K (a workspace given, epilogue 0 or 2 = the partials alone, K % 128 == 0, G >= 64, M >= 64, N >= 256, N % 4 == 0, offsets within 31
 // bits): taken when no unsplit register-stationary tiling has its tiles (gemm_w4a16_rs_tile) or K is long (64 chunks
 // of 128 or more: Llama-3-8B down 4096 x 14336 at M 512 takes 82 us split 4 ways against 92 unsplit on 128-row
 // tiles, while its o 4096 x 4096 takes 28.5 unsplit against 31.6 split). Over 64-token tiles of 256 weight rows, else
@@ -786,7 +787,7 @@ int gemm_w4a16_rs_tile(int M, int N, int K, int log2G);
 
 int gemm_w4a16_splits(int M, int N, int K, int log2G, int epilogue, int* rw) {
   *rw = 64;
-  if (!DK_GEMM_RS || epilogue != 0 || K % kRsK != 0 || log2G < 6 || M < 64 || N < 256 || N % 4 != 0 ||
+  if (!DK_GEMM_RS || (epilogue != 0 && epilogue != 2) || K % kRsK != 0 || log2G < 6 || M < 64 || N < 256 || N % 4 != 0 ||
       (long long)N * K > 0x7fffffffLL || (long long)M * K > 0x3fffffffLL)
     return 1;
   const int nk = K / kRsK;
@@ -852,8 +853,8 @@ void launch_gemm_w4a16(const void* packed, const void* sz, const void* x, void* 
     int rw;
     const int splits = gemm_w4a16_splits(M, N, K, log2G, epilogue, &rw);
     if (splits > 1) {
-      if (rw == 64) return launch_rs<64, 64>(packed, sz, x, y, M, N, K, log2G, 0, splits, ws, st);
-      return launch_rs<32, 64>(packed, sz, x, y, M, N, K, log2G, 0, splits, ws, st);
+      if (rw == 64) return launch_rs<64, 64>(packed, sz, x, y, M, N, K, log2G, epilogue, splits, ws, st);
+      return launch_rs<32, 64>(packed, sz, x, y, M, N, K, log2G, epilogue, splits, ws, st);
     }
   }
   switch (gemm_w4a16_tile(M, N, K, log2G)) {

@@ -135,6 +135,9 @@ void launch_rope_append(void* qkv, const float* cos_t, const float* sin_t, const
                         int n_bt, int rows, hipStream_t st);
 void launch_rmsnorm_rows(const void* x_in, const int64_t* rows, int n_src, const void* delta, const void* w, void* x_out,
                          void* out, int M, int H, float eps, hipStream_t st);
+// the same with the delta given as split-K GEMM partials (fp32, split s of row r at parts + s * pstride + r * H)
+void launch_rmsnorm_rows_parts(const void* x_in, const float* parts, int splits, long long pstride, const void* w,
+                               void* x_out, void* out, int M, int H, float eps, hipStream_t st);
 
 void launch_argmax_advance(const void* logits, int V, int64_t* tok, int32_t* pos, hipStream_t st);
 void launch_argmax_split(const void* logits, int V, int64_t* tok, int32_t* pos, unsigned long long* work,

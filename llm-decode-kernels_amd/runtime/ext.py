@@ -35,6 +35,7 @@ SIGNATURES = {
     "dk_gemm_w4a16_workspace_bytes": ([_I, _I, _I, _I, _I], _Z),
     "dk_gemm_w4a16_ws": ([_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _Z, _P], _I),
     "dk_rope_append_rows": ([_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P], _I),
+    "dk_rmsnorm_rows_parts": ([_P, _P, _I, ctypes.c_longlong, _P, _P, _P, _I, _I, _F, _P], _I),
     "dk_rmsnorm_rows": ([_P, _P, _I, _P, _P, _P, _P, _I, _I, _F, _P], _I),
     "dk_attention_prefill": ([_P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P], _I),
     "dk_bw_read": ([_P, _Z, _P, _I, _I, _I, _I, _P], _I),
@@ -286,6 +287,39 @@ class DecodeKernels:
         self._call(self.lib.dk_gemm_w4a16_ws, packed.data_ptr(), sz.data_ptr(), x.data_ptr(), y.data_ptr(), M, N, K,
                    int(group), int(epilogue), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
                    _stream(x))
+
+    def gemm_w4a16_parts(self, packed, sz, x, group, workspace):
+        """The split-K GEMM's fp32 partials alone (no reduce launch), left in `workspace`; returns them as a [S, M, N]
+        float32 view of it. Only for shapes that split (gemm_workspace_bytes(M, N, K, group) > 0)."""
+        for t, n in ((packed, "packed"), (sz, "sz"), (x, "x"), (workspace, "workspace")):
+            _check_cuda(t, n)
+        N, K = packed.size(0), packed.size(1) * 8
+        if x.dim() != 2 or x.size(1) != K:
+            raise RuntimeError("gemm_w4a16_parts: x must be [M, K]")
+        M = x.size(0)
+        if sz.size(0) != N or sz.size(1) != K // group:
+            raise RuntimeError("gemm_w4a16_parts: sz must be [N, K/G, 2]")
+        _check_dtype(packed, torch.int32, "packed")
+        for t, n in ((sz, "sz"), (x, "x")):
+            _check_dtype(t, torch.float16, n)
+        need = self.gemm_workspace_bytes(M, N, K, group)
+        self._call(self.lib.dk_gemm_w4a16_ws, packed.data_ptr(), sz.data_ptr(), x.data_ptr(), None, M, N, K,
+                   int(group), 2, workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream(x))
+        S = need // (M * N * 4)
+        return workspace.view(torch.uint8)[:need].view(torch.float32).view(S, M, N)
+
+    # prefill: residual + RMSNorm of M rows whose delta is split-K partials [S, M, H] (a view; rows contiguous)
+    def rmsnorm_rows_parts(self, x_in, parts, w, x_out, out, eps):
+        for t, n in ((x_in, "x_in"), (w, "w"), (x_out, "x_out"), (out, "out")):
+            _check_cuda(t, n)
+            _check_dtype(t, torch.float16, n)
+        if not parts.is_cuda or parts.dtype != torch.float32 or parts.dim() != 3:
+            raise RuntimeError("rmsnorm_rows_parts: parts must be a CUDA float32 [S, M, H] view")
+        S, M, H = parts.shape
+        if parts.stride(2) != 1 or parts.stride(1) != H or out.shape != (M, H) or x_in.shape != (M, H):
+            raise RuntimeError("rmsnorm_rows_parts: parts [S, M, H] with contiguous rows; x_in, out [M, H]")
+        self._call(self.lib.dk_rmsnorm_rows_parts, x_in.data_ptr(), parts.data_ptr(), S, parts.stride(0),
+                   w.data_ptr(), x_out.data_ptr(), out.data_ptr(), M, H, float(eps), _stream(x_in))
 
     # prefill: rope_append over M token rows (row m at position *pos + m)
     def rope_append_rows(self, qkv, cos_t, sin_t, pos, bt, kc, vc, n_q, n_kv):

@@ -639,6 +639,28 @@ class Model:
             self._gws = torch.empty(need, dtype=torch.uint8, device=self.cfg.device)
         return self._gws
 
+    # prefill projections whose output only feeds the next residual + RMSNorm (o, down): where the GEMM splits K, its
+    # fp32 partials go straight to the norm, which sums them as the GEMM's reduce launch would (bit for bit the same
+    # x and normed rows, one launch fewer)
+    fold_split_reduce = True
+
+    def _proj_delta(self, lin, x_in, y):
+        """Y = X . W^T of such a projection: the split partials [S, M, N] (a view of the workspace, valid until the
+        next GEMM that splits) where the shape splits, else y itself."""
+        if lin.quant and self.fold_split_reduce:
+            ws = self._gemm_workspace(x_in.size(0), lin.N, lin.K)
+            if ws is not None:
+                return self.K.gemm_w4a16_parts(lin.packed, lin.sz, x_in, self.cfg.group, ws)
+        self.gemm(lin, x_in, y)
+        return y
+
+    def _add_norm_rows(self, x, delta, w, xn):
+        """x += delta (fp16 rows, or split partials [S, M, H]); xn = RMSNorm(x) * w, in place over the prompt rows."""
+        if delta.dtype == torch.float32:
+            self.K.rmsnorm_rows_parts(x, delta, w, x, xn, self.eps)
+        else:
+            self.K.rmsnorm_rows(x, None, delta, w, x, xn, self.eps)
+
     def _gate_up_pairs(self, lin):
         """Interleaved (gate_i, up_i) rows for the GEMM's SwiGLU epilogue: the Linear's own storage when the decode
         step already uses that layout, else a permuted copy made once."""
@@ -672,22 +694,21 @@ class Model:
             if li == 0:
                 self.K.rmsnorm_rows(self.emb, B["tok"], None, lw["ln1"], x, xn, eps)
             else:
-                self.K.rmsnorm_rows(x, None, delta, lw["ln1"], x, xn, eps)
+                self._add_norm_rows(x, delta, lw["ln1"], xn)
             self.gemm(lw["qkv"], xn, B["qkv"])
             kc, vc = self.kv[li, 0], self.kv[li, 1]
             self.K.rope_append_rows(B["qkv"], self.cos, self.sin, self.pos, self.bt, kc, vc, self.n_q, self.n_kv)
             self.K.attention_prefill(B["qkv"], self.pos, self.bt, kc, vc, self.n_q, self.n_kv, start + M, B["attn"])
-            self.gemm(lw["o"], B["attn"], B["o"])
-            self.K.rmsnorm_rows(x, None, B["o"], lw["ln2"], x, xn, eps)
+            self._add_norm_rows(x, self._proj_delta(lw["o"], B["attn"], B["o"]), lw["ln2"], xn)
             if lw["gu"].quant:
                 self.gemm(lw["gu"], xn, B["act"], epilogue=1)
             else:
                 gu = torch.mm(xn, lw["gu"].w.t())
                 B["act"].copy_(torch.nn.functional.silu(gu[:, : self.I].float()).half() * gu[:, self.I:])
-            self.gemm(lw["down"], B["act"], B["down"])
-            delta = B["down"]
+            delta = self._proj_delta(lw["down"], B["act"], B["down"])
         last = slice(M - 1, M)
-        self.K.rmsnorm_rows(x[last], None, delta[last], self.norm_f, x[last], xn[last], eps)
+        self._add_norm_rows(x[last], delta[:, last] if delta.dtype == torch.float32 else delta[last], self.norm_f,
+                            xn[last])
         self.linear(self.lm_head, xn[M - 1], self.logits)
         if M > 1:
             self.pos.add_(M - 1)

@@ -305,6 +305,15 @@ def test_prefill_validation(lib):
     assert ws(wbytes=need - 1)[0] == 3 and "needs %d" % need in ws(wbytes=need - 1)[1]
     assert ws(w=W + 8)[0] == 2 and ws(w=B16 - 64)[0] == 4 and ws(w=A16)[0] == 4
     assert ws(K=240)[0] == 3 and ws(x=None)[0] == 1
+    # epilogue 2: the split partials alone, only where the shape splits (y unused)
+    assert wb(512, 4096, 14336, 128, 2) == need
+    assert ws(epi=2, K=4096, wbytes=1 << 30)[0] == 4 and "splits" in ws(epi=2, K=4096, wbytes=1 << 30)[1]
+    assert ws(epi=2, wbytes=need - 1)[0] == 3 and ws(epi=2, w=None)[0] == 1
+    rp = lambda **kw: _err(lib, lib.dk_rmsnorm_rows_parts(*dict(dict(
+        x=A16, p=W, S=2, ps=4 * 2048, w=A16, xo=A16, out=B16, M=4, H=2048, eps=1e-5), **kw).values(), None))
+    assert rp(S=0)[0] == 3 and rp(S=65)[0] == 3 and rp(ps=2046)[0] == 3 and rp(ps=1024)[0] == 3
+    assert rp(H=2044)[0] == 3 and rp(M=0)[0] == 3 and rp(p=W + 4)[0] == 2 and rp(out=A16)[0] == 4
+    assert rp(p=None)[0] == 1 and rp(p=B16 - 4 * 2048)[0] == 4 and "overlap" in rp(p=B16 - 4 * 2048)[1]
     rr = lambda **kw: _err(lib, lib.dk_rope_append_rows(*dict(
         dict(qkv=A16, c=A16, s=A16, pos=A16, bt=A16, kc=A16, vc=A16, M=8, n_q=32, n_kv=4, D=64, page=16, max_pos=100,
              n_pages=8, n_bt=8), **kw).values(), None))

@@ -115,6 +115,40 @@ def test_gemm_splitk_matches_oracle(K, M, N, Kd, G, S):
     assert_close(y3, ref, 5e-3, "unsplit")
 
 
+# the split partials read by the next residual + RMSNorm instead of the GEMM's reduce launch: S 2 (TinyLlama down),
+# S 4 over 32-row tiles with a ragged M, S 8 (two batches of four splits in the norm's loads)
+@pytest.mark.parametrize("M,N,Kd,S", [(512, 2048, 5632, 2), (100, 4096, 14336, 4), (256, 1536, 16384, 8)])
+def test_rmsnorm_rows_parts_matches_reduce_then_norm(K, M, N, Kd, S):
+    """gemm_w4a16_parts leaves S fp32 partials whose split-order sum, rounded once, is the reduced output, and
+    rmsnorm_rows_parts over them gives x and the normed rows bit for bit as gemm_w4a16 (workspace) then rmsnorm_rows;
+    also for the last row alone (the partials of a slice of rows, strided)."""
+    G = 128
+    need = K.gemm_workspace_bytes(M, N, Kd, G)
+    assert need == S * M * N * 4
+    packed, sz = _weights(K, N, Kd, G, seed=M + S)
+    a = torch.randn(M, Kd, generator=gen(S)).half().to(DEV)
+    x0 = torch.randn(M, N, generator=gen(S + 1)).half().to(DEV)
+    w = (torch.rand(N, generator=gen(S + 2)) + 0.5).half().to(DEV)
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    y = torch.empty(M, N, dtype=torch.half, device=DEV)
+    K.gemm_w4a16(packed, sz, a, y, G, workspace=ws)
+    x1, o1 = x0.clone(), torch.empty_like(x0)
+    K.rmsnorm_rows(x1, None, y, w, x1, o1, 1e-5)
+    ws.fill_(255)
+    parts = K.gemm_w4a16_parts(packed, sz, a, G, ws)
+    assert parts.shape == (S, M, N)
+    tot = parts[0].clone()
+    for s in range(1, S):
+        tot += parts[s]
+    assert torch.equal(tot.half(), y)
+    x2, o2 = x0.clone(), torch.empty_like(x0)
+    K.rmsnorm_rows_parts(x2, parts, w, x2, o2, 1e-5)
+    assert torch.equal(x2, x1) and torch.equal(o2, o1)
+    x3, o3 = x0[-1:].clone(), torch.empty(1, N, dtype=torch.half, device=DEV)
+    K.rmsnorm_rows_parts(x3, parts[:, -1:], w, x3, o3, 1e-5)
+    assert torch.equal(x3, x1[-1:]) and torch.equal(o3, o1[-1:])
+
+
 def test_gemm_short_k_does_not_split(K):
     """Shapes whose splits would hold fewer than 16 k chunks run unsplit even with a workspace (TinyLlama's
     projections): no workspace is asked for, and passing one changes nothing, bit for bit."""
@@ -395,6 +429,28 @@ def test_prefill_in_chunks_is_bit_exact(K):
         used[:, :, int(m.bt[t // 16]), :, t % 16, :] = True
     assert torch.equal(m.kv[used], one[0][used])
     assert torch.equal(m.logits, one[1]) and int(m.tok) == one[2] and int(m.pos) == one[3] == 70
+
+
+def test_prefill_split_reduce_folded_into_norm(K):
+    """A 512-token prompt through a TinyLlama-width model, whose down projection splits K: with the split partials
+    summed by the next norm (the default) the prefill leaves the same cache, logits and token as with the GEMM's own
+    reduce launch."""
+    from runtime.model import DecodeConfig, Model
+    from runtime.synth import LlamaShape, SyntheticLlama
+    shape = LlamaShape(2048, 2, 32, 4, 5632, 1000)
+    m = Model(SyntheticLlama(shape, seed=6, device=DEV, std=0.05), shape, DecodeConfig(max_ctx=600, device=DEV))
+    m.prepare(600)
+    assert K.gemm_workspace_bytes(512, 2048, 5632, m.cfg.group) > 0   # the path under test is taken
+    prompt = _prompt(512, seed=9)
+    out = []
+    for fold in (True, False):
+        m.fold_split_reduce = fold
+        m.kv.zero_()
+        m.reset(0)
+        m.prefill(prompt)
+        torch.cuda.synchronize()
+        out.append((m.kv.clone(), m.logits.clone(), int(m.tok)))
+    assert torch.equal(out[0][0], out[1][0]) and torch.equal(out[0][1], out[1][1]) and out[0][2] == out[1][2]
 
 
 def test_prefill_gate_up_layouts_agree(K):
