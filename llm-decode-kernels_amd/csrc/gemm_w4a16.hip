@@ -3,8 +3,9 @@
 // The prompt's tokens go through a layer together, so the projections are GEMMs, MFMA-shaped work. The weight format
 // is the decode GEMV's (packed int32 [N, K/8], (scale, zero) fp16 [N, K/G, 2]); each weight is dequantized as
 // fp16((q - zero) * scale) with one rounding -- the reference's dequantize (runtime/quant.py:93-97) bit for bit:
-// (1024 + q) - (1024 + zero) is an exact fp16 integer and its fp16 product with the fp16 scale rounds the exact
-// product once -- so every MFMA product is exact and the sums are fp32.
+// (1024 + q) - (1024 + zero), or (64 + q) - (64 + zero) for the nibbles OR-ed in at mantissa bits 4-7, is an exact
+// fp16 integer and its fp16 product with the fp16 scale rounds the exact product once -- so every MFMA product is
+// exact and the sums are fp32. Epilogue 2 (split-K) writes fp32 partials instead of rows.
 //
 // Three kernels, chosen by grid size (gemm_w4a16_tile at the end of this file):
 //   * register-stationary (K % 128 == 0, G >= 64, a few hundred tiles of 256 weight rows): each wave's 64 weight
