@@ -762,10 +762,11 @@ void launch_wide(const void* packed, const void* sz, const void* x, void* y, int
 
 // Tile choice: the register-stationary kernel (K % 128 == 0, G >= 64) in the first of these that gives its number
 // of tiles (two workgroups per CU: 512 slots): 256 weight rows x 128 tokens, 320 tiles (returns 42); 128 x 128, 320
-// (52); 256 x 64, 160 (41); 128 x 64, 160 (51). The 128-row tiles (32 rows per wave) give the narrower shapes their
-// tiles (TinyLlama qkv 2560 x 2048 at M 512: 14.0 against 17.3 us on the wide kernel; gate|up 11264 x 2048: 37.1
-// against 40.3 at 256 x 64); below 160 they lose to the wide kernel (TinyLlama o and down: 13.8 against 11.4 and
-// 34.2 against 31.3 us at 128 tiles). Otherwise the wide kernel: the largest of 128 x 128, 128 x 64, 64 x 64 whose grid still covers the 256
+// (52); 128 x 64, 160 (51). The 128-row tiles (32 rows per wave) give the narrower shapes their tiles (TinyLlama qkv
+// 2560 x 2048 at M 512: 14.0 against 17.3 us on the wide kernel; gate|up 11264 x 2048: 37.1 against 40.3 at 256 x 64;
+// Llama-3-8B qkv 6144 x 4096: 40.0 against 41.4 at 256 x 64, 384 tiles against 192, which is why 256 x 64 tiles are
+// no longer among the unsplit choices: wherever they reach 160 tiles the 128 x 64 tiling reaches 320); below 160
+// they lose to the wide kernel (TinyLlama o and down: 13.8 against 11.4 and 34.2 against 31.3 us at 128 tiles). Otherwise the wide kernel: the largest of 128 x 128, 128 x 64, 64 x 64 whose grid still covers the 256
 // CUs, then K groups (KG = 2 or 4 four-wave groups per workgroup; 2 at most for 128 x 64, by LDS) while the grid leaves
 // CUs with a single workgroup (returns 10 * tile + KG, tile 3: 128 x 128, 2: 128 x 64, 1: 64 x 64); K % 64 != 0 takes
 // the 64 x 64 16x16x16 kernel above (returns 0).
@@ -820,7 +821,6 @@ int gemm_w4a16_rs_tile(int M, int N, int K, int log2G) {
   const long long n_t = (N + 255) / 256, n_t32 = (N + 127) / 128, tm128 = (M + 127) / 128, tm64 = (M + 63) / 64;
   if (M >= 128 && N >= 256 && n_t * tm128 >= 320) return 42;
   if (M >= 128 && N >= 128 && n_t32 * tm128 >= 320) return 52;
-  if (M >= 64 && N >= 256 && n_t * tm64 >= 160) return 41;
   if (M >= 64 && N >= 128 && n_t32 * tm64 >= 160) return 51;
   return 0;
 }
@@ -860,7 +860,6 @@ void launch_gemm_w4a16(const void* packed, const void* sz, const void* x, void* 
   }
   switch (gemm_w4a16_tile(M, N, K, log2G)) {
     case 42: launch_rs<64, 128>(packed, sz, x, y, M, N, K, log2G, epilogue, 1, nullptr, st); return;
-    case 41: launch_rs<64, 64>(packed, sz, x, y, M, N, K, log2G, epilogue, 1, nullptr, st); return;
     case 52: launch_rs<32, 128>(packed, sz, x, y, M, N, K, log2G, epilogue, 1, nullptr, st); return;
     case 51: launch_rs<32, 64>(packed, sz, x, y, M, N, K, log2G, epilogue, 1, nullptr, st); return;
     case 31: launch_wide<128, 128, 1>(packed, sz, x, y, M, N, K, log2G, epilogue, st); return;

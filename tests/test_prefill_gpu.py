@@ -31,8 +31,8 @@ def _weights(K, N, Kd, G, seed):
 
 # kernel coverage: K % 128 == 0 and G >= 64 -> the register-stationary kernel when a tiling has enough tiles:
 # 256 weight rows x 128 tokens (the last four cases: G 64, 128 and 256, ragged M and N, an odd chunk count),
-# 128 x 128 ((512, 11264), ragged (300, 20000), (260, 19998) with N % 4 != 0 and 3 chunks), 256 x 64 (the ragged
-# (200, 12302) at G 64), 128 x 64 ((512, 2560), ragged (130, 10002)); otherwise K % 64 == 0 -> the wide kernel, tiles
+# 128 x 128 ((512, 11264), ragged (300, 20000), (260, 19998) with N % 4 != 0 and 3 chunks), 128 x 64 ((512, 2560),
+# ragged (130, 10002), (200, 12302) at G 64); otherwise K % 64 == 0 -> the wide kernel, tiles
 # 128 x 128, 128 x 64, 64 x 64 and 1, 2 or 4 K groups by grid size (G 32 keeps (512, 4096, 1024) on 128 x 64 with 2
 # groups and (200, 4100, 512) on 64 x 64 with 2); K % 64 == 32 -> the 16x16x16 kernel; N % 4 != 0 -> the element-wise
 # epilogue stores
@@ -69,8 +69,8 @@ def _grid_weights(N, Kd, G, seed):
 
 
 # one case per kernel and tiling: the K % 64 == 32 kernel; the wide kernel at 64 x 64 with 1, 2 and 4 K groups,
-# 128 x 64 with 1 and 2, 128 x 128; the register-stationary tilings 256 x 128, 128 x 128, 256 x 64, 128 x 64; split-K
-# over 256-row and over 128-row tiles
+# 128 x 64 with 1 and 2, 128 x 128; the register-stationary tilings 256 x 128, 128 x 128, 128 x 64; split-K over
+# 256-row tiles (the 256 x 64 tiling runs split only) and over 128-row tiles
 @pytest.mark.parametrize("M,N,Kd,G,ws", [(20, 100, 96, 32, False), (40, 300, 320, 64, False),
                                          (200, 4100, 512, 32, False), (64, 2048, 2048, 64, False),
                                          (400, 8000, 256, 32, False), (512, 4096, 1024, 32, False),
@@ -195,8 +195,8 @@ def test_gemm_one_hot_rows_exact(K, N):
     assert torch.equal(y.cpu(), wref[:, ks].t().contiguous())
 
 
-# register-stationary tilings of the SwiGLU epilogue: 128 x 128 at (512, 8192), 256 x 128 at (260, 14000), 256 x 64
-# at (64, 20500), 128 x 64 at (64, 10240)
+# register-stationary tilings of the SwiGLU epilogue: 128 x 128 at (512, 8192), 256 x 128 at (260, 14000), 128 x 64
+# at (64, 20500) and (64, 10240)
 @pytest.mark.parametrize("M,I,Kd", [(16, 5632, 2048), (130, 512, 256), (1, 64, 1024), (9, 513, 320), (33, 70, 96),
                                     (512, 8192, 256), (260, 14000, 640), (64, 20500, 256), (64, 10240, 256)])
 def test_gemm_swiglu_epilogue(K, M, I, Kd):
