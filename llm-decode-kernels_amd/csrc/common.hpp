@@ -95,6 +95,73 @@ __device__ __forceinline__ float group_sum_dpp(float v) {
   if constexpr (CPL == 16) v += DK_DPP_F32(v, 0x140, 0xF);
   return v;
 }
+// Transposed reduction of n = 2^k row partials per lane over each 16-lane DPP row ("row fold"). Summing every row
+// over the wave separately costs 6 DPP steps per row; folding them together costs n - 1 DPP adds in all. Step s
+// (s = 1..4) pairs lane L with lane L ^ X_s, X = {1, 2, 7, 15} (quad_perm [1,0,3,2], quad_perm [2,3,0,1],
+// row_half_mirror, row_mirror), and merges two half-blocks of rows that differ in row bit s - 1: the lane keeps the
+// half whose bit equals its c_s and sends the other to its partner, which keeps exactly that half (c_s flips between
+// partners and no other c_t does: with L = sum c_s X_s over GF(2), c1 = b0^b2, c2 = b1^b2, c3 = b2^b3, c4 = b3 for the
+// lane bits b). After min(k, 4) such steps and plain DPP sums for the remaining steps up to 4, every lane holds the
+// sums over its 16-lane row of the rows 16 j + m(L), m(L) = sum c_s 2^(s - 1) over the merging steps, and the 16 lanes
+// of a row cover every m once. The quarters of the wave (rows of 16 lanes) are summed by the caller. Every lane must
+// be active; each partial goes through the same tree of additions whatever its row.
+struct FoldLane {
+  bool c[4];
+  int m;  // the row (mod 16) this lane holds after the merging steps of a fold over n rows
+};
+__device__ __forceinline__ FoldLane fold_lane(int lane, int n) {
+  const int b0 = lane & 1, b1 = (lane >> 1) & 1, b2 = (lane >> 2) & 1, b3 = (lane >> 3) & 1;
+  FoldLane f;
+  f.c[0] = (b0 ^ b2) != 0;
+  f.c[1] = (b1 ^ b2) != 0;
+  f.c[2] = (b2 ^ b3) != 0;
+  f.c[3] = b3 != 0;
+  f.m = 0;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) f.m |= ((1 << (s + 1)) <= n && f.c[s]) ? 1 << s : 0;
+  return f;
+}
+template <int S>  // DPP partner of step S (1..4)
+__device__ __forceinline__ float fold_dpp(float v) {
+  constexpr int ctrl = S == 1 ? 0xB1 : S == 2 ? 0x4E : S == 3 ? 0x141 : 0x140;
+  return DK_DPP_F32(v, ctrl, 0xF);
+}
+// Merging step S over the half-blocks a (row bit S - 1 clear) and b (set).
+template <int S>
+__device__ __forceinline__ float fold_merge(float a, float b, bool c) {
+  const float keep = c ? b : a, send = c ? a : b;
+  return keep + fold_dpp<S>(send);
+}
+// The merges that become possible once rows [r0, r0 + T) of a fold over N rows are in p: for each step S (ascending),
+// every block of 2^S rows that ends inside [r0, r0 + T) merges its two halves into p[block start]. All indices are
+// compile-time constants after unrolling.
+template <int S, int N, int T>
+__device__ __forceinline__ void fold_step(float (&p)[N], int r0, const FoldLane& f) {
+  if constexpr ((1 << S) <= N) {
+    constexpr int blk = 1 << S, half = blk >> 1;
+#pragma unroll
+    for (int b = 0; b < N; b += blk) {
+      const int end = b + blk - 1;
+      if (end >= r0 && end < r0 + T) p[b] = fold_merge<S>(p[b], p[b + half], f.c[S - 1]);
+    }
+  }
+}
+template <int N, int T>
+__device__ __forceinline__ void fold_rows(float (&p)[N], int r0, const FoldLane& f) {
+  fold_step<1, N, T>(p, r0, f);
+  fold_step<2, N, T>(p, r0, f);
+  fold_step<3, N, T>(p, r0, f);
+  fold_step<4, N, T>(p, r0, f);
+}
+// The plain steps after the merges of a fold over N < 16 rows: the remaining lane bits of the 16-lane row.
+template <int N>
+__device__ __forceinline__ void fold_finish(float (&p)[N]) {
+  if constexpr (N < 2) p[0] += fold_dpp<1>(p[0]);
+  if constexpr (N < 4) p[0] += fold_dpp<2>(p[0]);
+  if constexpr (N < 8) p[0] += fold_dpp<3>(p[0]);
+  if constexpr (N < 16) p[0] += fold_dpp<4>(p[0]);
+}
+
 // Same sum, broadcast to every lane (v_readlane of lane 63 into a scalar register).
 __device__ __forceinline__ float wave_sum_all(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wave_sum_lane63(v)), 63));

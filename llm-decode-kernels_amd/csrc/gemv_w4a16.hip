@@ -266,15 +266,17 @@ __device__ __forceinline__ void tile_issue(const u32x4* __restrict__ W, const ui
   for (int r = 0; r < T; ++r) s[r] = SZ[(size_t)min(row0 + r, N - 1) * NG + (uc >> gsh)];
 }
 
-template <int T>
+// The lane's partials of one tile's T rows into p[r0 .. r0 + T). Dead lanes (u >= U) hold x = 0, so their partials
+// are exactly 0 for finite scales (a non-finite scale of the last column already makes the live lane's row non-finite).
+template <int T, int N>
 __device__ __forceinline__ void tile_rows(const u32x4 (&w)[T], const uint32_t (&s)[T], const u32x4 (&xc)[4],
-                                          ColumnSums cs, NibbleMasks m, bool live, float (&v)[T]) {
+                                          ColumnSums cs, NibbleMasks m, int r0, float (&p)[N]) {
 #pragma unroll
   for (int r = 0; r < T; ++r) {
     const f16x2 sz = as_f16x2(s[r]);
-    const float c = column_row(w[r], (float)sz.y, xc, cs, m);
-    const float part = live ? (float)sz.x * c : 0.f;  // dead lanes (u >= U) contribute 0; the DPP sum runs on all lanes
-    v[r] = wave_sum_lane63(part);
+    // an fma with +0 (v_fma_mix_f32 takes the fp16 scale directly; a multiply would convert it first), equal to the
+    // product but for the sign of a zero result
+    p[r0 + r] = fmaf((float)sz.x, column_row(w[r], (float)sz.y, xc, cs, m), 0.f);
   }
 }
 
@@ -472,10 +474,21 @@ __device__ __forceinline__ void rope_rotate(f16 a16, f16 b16, float c, float s, 
   hi = (f16)(bc + as);
 }
 
-#ifndef DK_TILE_DEPTH
-#define DK_TILE_DEPTH 2
-#endif
-constexpr int kTileDepth = DK_TILE_DEPTH;  // weight tiles in flight per workgroup (the buffers of the pipeline)
+// Total of row `row` of a row group: its partials from the four quarters of each of the group's nw waves.
+template <int NR>
+__device__ __forceinline__ float row_total(const float* red, int gw0, int nw, int row) {
+  float acc = 0.f;
+  for (int i = 0; i < nw; ++i) {
+    const float* q = red + (gw0 + i) * 4 * NR + row;
+    acc += (q[0] + q[NR]) + (q[2 * NR] + q[3 * NR]);
+  }
+  return acc;
+}
+
+// Weight tiles in flight per wave (the buffers of the pipeline): 2, or 4 for walks of 8 tiles of at most 2 rows
+// (4096 x 14336 at 2-row tiles: 7.02 against 7.13 us; 3-4 tiles measured no better at shorter walks, all 8 at once
+// 7.36, and 4 tiles of 4 or 8 rows spill registers).
+constexpr int tile_depth(int t, int nt) { return nt >= 8 && t <= 2 ? 4 : nt < 2 ? nt : 2; }
 
 // Pipeline: operand loads, then the weight loads of tiles 0 and 1, then the operand (waits for the operand loads
 // only), then for each tile t: compute it from its buffer and refill that buffer with tile t + 2. Two tiles are in
@@ -496,7 +509,8 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
                 int groups, const void* op1, const void* op2, f16* __restrict__ y, const GemvInput in) {
   static_assert(EPI == kOutRows || (T * NT) % 2 == 0, "gate/up and rotation pairs need an even row tile");
   static_assert(!is_combine(PRO) || EPI == kOutRows, "the combine prologue feeds the plain epilogue");
-  __shared__ float red[16][T * NT];
+  // row partials: [wave][quarter of the wave][row] (the quarters of a row fold, summed when the rows are finished)
+  __shared__ float red[16 * 4 * T * NT];
   __shared__ float s_ss[16];
   __shared__ u32x4 xs[is_combine(PRO) ? kGemvCombineMaxWarps * 64 : 1];   // combine: x, 8 values per thread
   const int nw = (U + kWave - 1) / kWave;  // waves of one row group
@@ -522,7 +536,7 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
                  static_cast<const float*>(op2), U << 5, craw);
   else
     tile_input_load<PRO>(in, op0, op1, op2, uc, U << 5, raw);
-  constexpr int DP = NT < kTileDepth ? NT : kTileDepth;  // tiles in flight
+  constexpr int DP = tile_depth(T, NT);
   u32x4 w[DP][T];
   uint32_t sz[DP][T];
 #pragma unroll
@@ -558,15 +572,22 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
       }
     }
   }
+  constexpr int NR = T * NT;  // rows of the row group, folded over each 16-lane row as the tiles finish
+  const FoldLane fl = fold_lane(lane, NR);
+  float p[NR];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    float v[T];
-    tile_rows<T>(w[t % DP], sz[t % DP], xc, cs, m, live, v);
+    tile_rows<T, NR>(w[t % DP], sz[t % DP], xc, cs, m, t * T, p);
     if (t + DP < NT) tile_issue<T>(W, SZ, base + (t + DP) * T, N, U, NG, uc, gsh, w[t % DP], sz[t % DP]);
     __builtin_amdgcn_sched_barrier(0);
-    if (lane == 63) {
+    fold_rows<NR, T>(p, t * T, fl);
+  }
+  fold_finish<NR>(p);
+  {
+    float* rq = red + (wave * 4 + (lane >> 4)) * NR + fl.m;
+    if ((lane & 15) < (NR < 16 ? NR : 16)) {
 #pragma unroll
-      for (int r = 0; r < T; ++r) red[wave][t * T + r] = v[r];
+      for (int j = 0; j < (NR + 15) / 16; ++j) rq[16 * j] = p[16 * j];
     }
   }
   // the rows are finished by the row group's threads from LDS: across its waves a workgroup barrier; within a one-wave
@@ -580,18 +601,11 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
   }
   if constexpr (EPI == kOutRows) {
     if (tid < T * NT && base + tid < N) {
-      float acc = 0.f;
-      for (int i = 0; i < nw; ++i) acc += red[gw0 + i][tid];
-      y[base + tid] = (f16)acc;
+      y[base + tid] = (f16)row_total<NR>(red, gw0, nw, tid);
     }
   } else if constexpr (EPI == kOutRope) {
     if (tid < T * NT / 2 && 2 * rp + 1 < N) {
-      float a = 0.f, b = 0.f;
-      for (int i = 0; i < nw; ++i) {
-        a += red[gw0 + i][2 * tid];
-        b += red[gw0 + i][2 * tid + 1];
-      }
-      const f16 a16 = (f16)a, b16 = (f16)b;
+      const f16 a16 = (f16)row_total<NR>(red, gw0, nw, 2 * tid), b16 = (f16)row_total<NR>(red, gw0, nw, 2 * tid + 1);
       const int nq = in.rope.n_q, nkv = in.rope.n_kv, half = 1 << hb;
       f16 lo = a16, hi = b16;
       if (rvalid && rhead < nq + nkv) rope_rotate(a16, b16, rc, rs, lo, hi);
@@ -610,11 +624,7 @@ gemv_w4a16_tile(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, co
     }
   } else {
     if (tid < T * NT / 2 && base + 2 * tid + 1 < N) {
-      float g = 0.f, up = 0.f;
-      for (int i = 0; i < nw; ++i) {
-        g += red[gw0 + i][2 * tid];
-        up += red[gw0 + i][2 * tid + 1];
-      }
+      const float g = row_total<NR>(red, gw0, nw, 2 * tid), up = row_total<NR>(red, gw0, nw, 2 * tid + 1);
       y[(base >> 1) + tid] = silu_mul((f16)g, (f16)up);
     }
   }
