@@ -29,7 +29,8 @@
 //                               reduced through LDS: for narrow N, where whole-row waves would leave CUs idle.
 //   stage 4  gemv_w4a16_tile    the workgroup's waves cover K once with a register-resident x slice per lane and
 //                               walk 2^pf tiles of R rows, the next tile's loads in flight while the current one is
-//                               computed; x is read once per workgroup, row sums by DPP within waves, LDS across.
+//                               computed; x is read once per workgroup, row sums by a DPP fold within waves, LDS
+//                               across.
 // The compiler's scheduler, left alone, issues only two of a tile's weight loads before it starts computing (it keeps
 // register pressure low); __builtin_amdgcn_sched_barrier pins every load of a step ahead of its arithmetic.
 #include "attn_common.hpp"
@@ -254,9 +255,10 @@ gemv_w4a16_splitk(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, 
 // Stage 4: row tiles with a stationary x slice. The workgroup's waves cover K once: lane l of wave v owns column
 // u = 64 v + l (so U <= 64 * waves) and loads its 32 x values once into registers. The workgroup walks NT tiles of T
 // consecutive rows; for each tile every lane requests its column of all T rows at once (T 16-byte loads + T scale /
-// zero words), and the loads of tile t + 1 are issued before tile t is computed (double buffering, pinned by
-// scheduling barriers so the compiler cannot serialise them). Each row partial is summed over the wave with DPP and
-// the waves meet in LDS; T * NT threads finish the rows and store them.
+// zero words), and the loads of later tiles are issued before tile t is computed (2 or 4 tiles in flight, pinned by
+// scheduling barriers so the compiler cannot serialise them). The lanes' row partials are folded together over each
+// 16-lane DPP row as the tiles finish (fold_rows: T * NT - 1 merging steps for all rows, instead of a wave sum per
+// row), the wave quarters and the waves meet in LDS, and T * NT threads finish the rows and store them.
 template <int T>
 __device__ __forceinline__ void tile_issue(const u32x4* __restrict__ W, const uint32_t* __restrict__ SZ, int row0,
                                            int N, int U, int NG, int uc, int gsh, u32x4 (&w)[T], uint32_t (&s)[T]) {
