@@ -27,7 +27,6 @@ the tuning table), autotune_path, attn_policy_path, shuffle_pages, device; fused
 select the MI355X launch fusions (each one is checked against the unfused composition by the GPU tests).
 """
 import json
-import math
 from dataclasses import dataclass, field
 from pathlib import Path
 

@@ -2,7 +2,6 @@
 include/dk_amd.h declares with the signature the ctypes shim binds, and every argument-validation path of the C layer
 (kernels/bindings.cpp:18-88 TORCH_CHECKs) returns its error code and message before any HIP call. The torch-facing
 shim rejects non-CUDA tensors with the reference's message."""
-import ctypes
 import re
 
 import pytest

@@ -3,7 +3,6 @@ array instead of caller buffers (for callers that cannot allocate). Checked thro
 entry point dk_paged_attention on the same inputs -- the same kernels, so the outputs must be bit-identical -- on two
 calls in a row, the second with a smaller input (the scratch keeps the first call's partials), and against the
 oracle within the attention tolerance; sizes beyond the scratch array are rejected before any launch."""
-import ctypes
 
 import pytest
 import torch
