@@ -6,7 +6,9 @@ the reference's backend="ref" composition, runtime/model.py:216-233) with the ba
     heads, page 32, fp16 weights throughout, the attention combine as a launch instead of merged into the o
     projection, at TinyLlama widths (hidden 2048, 32 q / 4 kv heads, SwiGLU 5632) over 3 layers;
   * head_dim 128 (Llama-3-8B widths: hidden 4096, 32 q / 8 kv heads, SwiGLU 14336) with G64 and an INT4 head over
-    2 layers.
+    2 layers;
+  * long contexts (4000 and 12000 at TinyLlama widths, 8000 at head_dim 128), where the attention policy's later
+    split bands run and the combine is a launch of its own.
 
 Each case starts both decoders from the same seeded K/V cache at its context and steps 32 greedy tokens (the oracle
 runs the GPU's greedy tokens as one batch of teacher-forced steps)."""
@@ -25,7 +27,12 @@ CASES = [("G64 int4 head", TINY_W, dict(group=64, lm_head="int4"), 300),
          ("G256 fp16 head page 32", TINY_W, dict(group=256, lm_head="fp16", page=32), 700),
          ("fp16 weights", TINY_W, dict(weights="fp16"), 400),
          ("combine launch", TINY_W, dict(combine_in_o=False), 512),
-         ("D128 G64 int4 head", L3_W, dict(group=64, lm_head="int4"), 1000)]
+         ("D128 G64 int4 head", L3_W, dict(group=64, lm_head="int4"), 1000),
+         # long contexts: the attention policy's later bands (more splits than the o projection merges, so the
+         # combine runs as a launch) inside the whole step
+         ("long ctx 4000", TINY_W, {}, 4000),
+         ("long ctx 12000", TINY_W, {}, 12000),
+         ("D128 long ctx 8000", L3_W, dict(group=64, lm_head="int4"), 8000)]
 
 
 @pytest.mark.parametrize("name,widths,over,ctx", CASES, ids=[c[0] for c in CASES])
