@@ -492,9 +492,9 @@ __device__ __forceinline__ float row_total(const float* red, int gw0, int nw, in
 // 7.36, and 4 tiles of 4 or 8 rows spill registers).
 constexpr int tile_depth(int t, int nt) { return nt >= 8 && t <= 2 ? 4 : nt < 2 ? nt : 2; }
 
-// Pipeline: operand loads, then the weight loads of tiles 0 and 1, then the operand (waits for the operand loads
-// only), then for each tile t: compute it from its buffer and refill that buffer with tile t + 2. Two tiles are in
-// flight from the first instruction on.
+// Pipeline: operand loads, then the weight loads of tiles 0 .. DP - 1 (DP = tile_depth), then the operand (waits for
+// the operand loads only), then for each tile t: compute it from its buffer, refill that buffer with tile t + DP and
+// fold the tile's rows. DP tiles are in flight from the first instruction on.
 // A workgroup holds blockDim / (64 nw) independent row groups of nw = ceil(U / 64) waves each (group g takes the
 // workgroup's g-th run of T * NT rows): at small K a group is one wave, and several groups per workgroup cost fewer
 // workgroup dispatches than one single-wave workgroup per row tile.
